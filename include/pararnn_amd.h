@@ -1,0 +1,92 @@
+/* pararnn_amd — C ABI of the MI355X (gfx950) fused Newton + scan kernels.
+ *
+ * Plain pointers and sizes only.  All tensors are dense, row-major ("contiguous"
+ * in torch terms) device buffers on the current HIP device; `stream` is a
+ * hipStream_t passed as void* (NULL = the default stream).  Nothing here
+ * allocates device memory or synchronises the host: scratch space comes from
+ * the caller's `workspace` (size from the matching *_workspace_size call,
+ * 256-byte aligned), and every entry point only enqueues work on `stream`.
+ * Calls that share one workspace must not overlap in time.
+ *
+ * dtype codes: PRNN_F32 (float32) and PRNN_BF16 (bfloat16 storage).  All
+ * arithmetic is fp32; bf16 tensors are widened on load and rounded (nearest
+ * even) on store.
+ *
+ * Return codes: PRNN_OK, or an error whose message prnn_last_error() returns
+ * (thread-local).  The Python shim maps PRNN_ERR_VALUE -> ValueError,
+ * PRNN_ERR_TYPE -> TypeError, PRNN_ERR_RUNTIME -> RuntimeError, as the
+ * reference's ops raise them (kernels/newton_slstm.py:2725-2728,
+ * kernels/precision.py:40-68, kernels/newton_gru_head.py:108-117).
+ *
+ * Reference interfaces replaced (paths relative to the reference's src/pararnn):
+ *   prnn_slstm_init       -> solvers/slstm_picard.py:143-181
+ *                            slstm_zero_hidden_init / slstm_picard_init, as
+ *                            called by kernels/fused_newton.py:367-372
+ *   prnn_slstm_newton     -> kernels/custom_ops.py:486-516
+ *                            torch.library op pararnn::newton_slstm_fused
+ *   prnn_gru_head_newton  -> kernels/custom_ops.py:311-358
+ *                            torch.library op pararnn::newton_gru_head_fused
+ */
+#ifndef PARARNN_AMD_H
+#define PARARNN_AMD_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PRNN_API __attribute__((visibility("default")))
+
+enum { PRNN_F32 = 0, PRNN_BF16 = 1 };
+enum { PRNN_OK = 0, PRNN_ERR_VALUE = 1, PRNN_ERR_TYPE = 2, PRNN_ERR_RUNTIME = 3 };
+
+/* Library ABI version (bumped on any signature change). */
+PRNN_API int prnn_abi_version(void);
+/* Message of the last failing call on this thread ("" if none). */
+PRNN_API const char* prnn_last_error(void);
+
+/* ---- ParaSLSTM mix='diag' ------------------------------------------------
+ * Layouts: wx (B, T, 4d) gate blocks (i, f, z, o);  r (4, d) recurrent mix,
+ * already clamped by the caller;  h0 (B, 4, d) slots (c, n, m, h) or NULL
+ * (zeros);  states / out (B, T, 4, d) slots (c, n, m, h).
+ * wx, r, h0, states and out all have the dtype `dtype`.
+ */
+
+/* Newton initial guess: the zero-hidden frozen-gate scan followed by
+ * `picard_iters` frozen-gate passes that freeze the gates at
+ * wx + r * h_prev of the previous pass; `states` receives the last pass. */
+PRNN_API size_t prnn_slstm_init_workspace_size(int B, int T, int d, int picard_iters, int dtype);
+PRNN_API int prnn_slstm_init(const void* wx, const void* r, const void* h0, void* states, int B,
+                             int T, int d, int picard_iters, float eps, int dtype,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+/* `max_iters` Newton iterations from the guess `states` (read only);
+ * `out` receives the result.  `out` must not alias `states`.  Iterations
+ * between the first and the last keep the trajectory in fp32 inside the
+ * workspace. */
+PRNN_API size_t prnn_slstm_newton_workspace_size(int B, int T, int d, int max_iters, int dtype);
+PRNN_API int prnn_slstm_newton(const void* wx, const void* r, const void* h0, const void* states,
+                               void* out, int B, int T, int d, int max_iters, float omega,
+                               float eps, int dtype, void* workspace, size_t workspace_bytes,
+                               void* stream);
+
+/* ---- ParaGRU mix='head' --------------------------------------------------
+ * Layouts: wx (B, T, 3d) gate blocks (z, r, n);  a_z, a_r, a_n
+ * (n_heads, d_head, d_head) laid out (in, out) so y = h @ A per head;
+ * h0 (B, d) or NULL;  out (B, T, d);  d = n_heads * d_head.
+ * d_head must be 64.  The initial guess is f(h_prev0, x_t) with h_prev0 zero
+ * except h0 at t = 0; then `max_iters` Newton iterations.
+ */
+PRNN_API size_t prnn_gru_head_newton_workspace_size(int B, int T, int n_heads, int d_head,
+                                                    int max_iters, int dtype);
+PRNN_API int prnn_gru_head_newton(const void* wx, const void* a_z, const void* a_r,
+                                  const void* a_n, const void* h0, void* out, int B, int T,
+                                  int n_heads, int d_head, int max_iters, float omega, int dtype,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PARARNN_AMD_H */

@@ -1,0 +1,30 @@
+// Library-wide pieces of the C ABI: error buffer, ABI version, word clear.
+#include "prnn_host.h"
+
+namespace prnn {
+
+char* last_error_buffer() {
+  static thread_local char buf[512] = {0};
+  return buf;
+}
+
+__global__ void clear_words_kernel(int* __restrict__ p, size_t n) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+    p[i] = 0;
+}
+
+int clear_words(int* p, size_t n, hipStream_t stream) {
+  if (n == 0) return PRNN_OK;
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 1024) blocks = 1024;
+  clear_words_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(p, n);
+  PRNN_HIP(hipGetLastError());
+  return PRNN_OK;
+}
+
+}  // namespace prnn
+
+extern "C" PRNN_API int prnn_abi_version(void) { return 1; }
+
+extern "C" PRNN_API const char* prnn_last_error(void) { return prnn::last_error_buffer(); }

@@ -1,0 +1,53 @@
+// Host-side helpers shared by the C entry points: error reporting, workspace
+// carving and the status-word clear kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "pararnn_amd.h"
+
+namespace prnn {
+
+// Thread-local message of the last failing call.
+char* last_error_buffer();
+
+inline int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(last_error_buffer(), 512, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+inline int hip_fail(hipError_t e, const char* what) {
+  return fail(PRNN_ERR_RUNTIME, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define PRNN_HIP(call)                                   \
+  do {                                                   \
+    hipError_t e_ = (call);                              \
+    if (e_ != hipSuccess) return prnn::hip_fail(e_, #call); \
+  } while (0)
+
+// Bump allocator over the caller's workspace; every block 256-byte aligned.
+struct Carver {
+  char* base;
+  size_t used;
+  explicit Carver(void* p) : base(static_cast<char*>(p)), used(0) {}
+  void* take(size_t bytes) {
+    used = (used + 255) & ~static_cast<size_t>(255);
+    void* p = base ? base + used : nullptr;
+    used += bytes;
+    return p;
+  }
+};
+
+// Zero `n` 32-bit words on `stream` with a kernel (no memset node, so the
+// sequence stays replay-safe under HIP graph capture).
+int clear_words(int* p, size_t n, hipStream_t stream);
+
+}  // namespace prnn

@@ -1,0 +1,777 @@
+// ParaSLSTM mix='diag' Newton + scan kernels for gfx950 (CDNA4).
+//
+// Two single-pass chunked scans over time, both with the same tile schedule:
+//
+//   tile  = (batch b, channel block of 64, time chunk of W*L steps)
+//   lane  = one channel; wave w = L consecutive steps of the chunk
+//
+// Pass 1 walks the lane's L steps serially from register-cached inputs and
+// folds them into the lane's segment aggregate; the W wave aggregates are
+// combined through LDS into the tile aggregate; wave 0 publishes it and runs a
+// decoupled look-back over earlier chunks of the same (b, channel block) to
+// get the carry into the tile; pass 2 replays the L steps from registers with
+// the true carry and streams the outputs.  Inputs are read from HBM once and
+// outputs written once per launch.
+//
+// (1) slstm_frozen_kernel: frozen-gate pass (zero-hidden or one Picard pass).
+//     Per step  m' = max(z_f + m, z_i),  f = e^{z_f + m - m'},  i = e^{z_i - m'},
+//     n' = f n + i,  c' = f c + i tanh z_z,  h = sigmoid(z_o) c' / (n' + eps)
+//     with pre = wx (+ R * h_prev of the previous pass).  The carry (m, n, c)
+//     composes through the stabilised monoid (F, M, N, C): F = sum z_f, M the
+//     max-plus aggregate, N / C the sums scaled by e^{-M}.
+//     Reference: solvers/slstm_picard.py:51-107, 143-181.
+// (2) slstm_newton_kernel: one Newton iteration.  Per step the cell value
+//     f(H_{t-1}, x_t), the 4x4 Jacobian J_t (12 structural non-zeros) and the
+//     residual F_t = f - H_t; the scan solves delta_t = J_t delta_{t-1} + F_t
+//     on the affine monoid (A, b) -> (J A, J b + F); H_t += omega delta_t.
+//     Reference: cells/para_slstm.py:347-446, solvers/scan.py:82-100,
+//     solvers/newton/__init__.py:516-543, kernels/newton_slstm.py:886-966.
+#include "prnn_common.h"
+#include "pararnn_amd.h"
+#include "prnn_host.h"
+
+namespace prnn {
+namespace slstm {
+
+constexpr int kCB = 64;  // channels per tile (one per lane)
+
+struct TileId {
+  int b, cb, chunk, rem;
+};
+
+__device__ __forceinline__ TileId decode_tile(int tile, int B, int n_cb) {
+  const int per = B * n_cb;
+  TileId t;
+  t.chunk = tile / per;
+  t.rem = tile - t.chunk * per;
+  t.b = t.rem / n_cb;
+  t.cb = t.rem - t.b * n_cb;
+  return t;
+}
+
+__device__ __forceinline__ int take_ticket(int* counter) {
+  __shared__ int s_ticket;
+  if (threadIdx.x == 0)
+    s_ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  return s_ticket;
+}
+
+// ---------------------------------------------------------------------------
+// (1) frozen-gate pass
+// ---------------------------------------------------------------------------
+
+struct FG {
+  float F, M, N, C;
+};
+
+__device__ __forceinline__ FG fg_identity() { return FG{0.f, -INFINITY, 0.f, 0.f}; }
+
+// Aggregate of segment x followed by segment y.
+__device__ __forceinline__ FG fg_compose(FG x, FG y) {
+  if (y.M == -INFINITY) return FG{x.F + y.F, x.M, x.N, x.C};
+  if (x.M == -INFINITY) return FG{x.F + y.F, y.M, y.N, y.C};
+  const float mx = y.F + x.M;
+  const float m = fmaxf(mx, y.M);
+  const float sx = fexp(mx - m), sy = fexp(y.M - m);
+  return FG{x.F + y.F, m, x.N * sx + y.N * sy, x.C * sx + y.C * sy};
+}
+
+// Carry (m, n, c) after applying aggregate y to carry (m, n, c).
+__device__ __forceinline__ void fg_apply(const FG& y, float& m, float& n, float& c) {
+  if (y.M == -INFINITY) return;
+  const float mc = y.F + m;
+  const float mn = fmaxf(mc, y.M);
+  const float sc = fexp(mc - mn), sy = fexp(y.M - mn);
+  n = n * sc + y.N * sy;
+  c = c * sc + y.C * sy;
+  m = mn;
+}
+
+// One frozen-gate step in place on (m, n, c); returns tanh-free readout pieces.
+__device__ __forceinline__ void fg_step(float zi, float zf, float zz, float& m, float& n, float& c) {
+  const float left = zf + m;
+  const float mn = fmaxf(left, zi);
+  const float f = fexp(left - mn);
+  const float i = fexp(zi - mn);
+  const float z = ftanh(zz);
+  n = f * n + i;
+  c = f * c + i * z;
+  m = mn;
+}
+
+template <typename TX, int L, int W, bool HAS_H, bool FULL_OUT>
+__global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
+    const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
+    const TX* __restrict__ hsrc, TX* __restrict__ out_full, TX* __restrict__ out_h, int B, int T,
+    int d, int n_cb, float eps, int* __restrict__ counter, int* __restrict__ flags,
+    float* __restrict__ agg, float* __restrict__ incl, int epoch) {
+  __shared__ float s_agg[W][4][kCB];
+  __shared__ float s_carry[W][3][kCB];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int tile = take_ticket(counter);
+  const TileId id = decode_tile(tile, B, n_cb);
+  const int ch = id.cb * kCB + lane;
+  const bool live = ch < d;
+  const int chunk_len = W * L;
+  const int t0 = id.chunk * chunk_len + wave * L;
+  const size_t row4 = static_cast<size_t>(4) * d;
+
+  float r[4] = {0.f, 0.f, 0.f, 0.f};
+  if (HAS_H && live) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) r[g] = ld(rmix + g * d + ch);
+  }
+
+  // Cache the frozen pre-activations of this lane's L steps.
+  float pre[L][4];
+#pragma unroll
+  for (int s = 0; s < L; ++s) {
+    const int t = t0 + s;
+    if (live && t < T) {
+      const size_t base = (static_cast<size_t>(id.b) * T + t) * row4 + ch;
+      float hp = 0.f;
+      if (HAS_H) {
+        if (t > 0)
+          hp = ld(hsrc + (static_cast<size_t>(id.b) * T + (t - 1)) * d + ch);
+        else if (h0 != nullptr)
+          hp = ld(h0 + static_cast<size_t>(id.b) * row4 + 3 * d + ch);
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float x = ld(wx + base + g * d);
+        // wx + R * h_prev, rounded to the storage dtype after each op.
+        pre[s][g] = HAS_H ? round_to<TX>(add_rn(x, round_to<TX>(mul_rn(r[g], hp)))) : x;
+      }
+    } else {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) pre[s][g] = 0.f;
+    }
+  }
+
+  // Pass 1: segment aggregate from the empty state (m = -inf, n = c = 0).
+  FG a = fg_identity();
+#pragma unroll
+  for (int s = 0; s < L; ++s) {
+    if (t0 + s < T) {
+      a.F += pre[s][1];
+      fg_step(pre[s][0], pre[s][1], pre[s][2], a.M, a.N, a.C);
+    }
+  }
+  s_agg[wave][0][lane] = a.F;
+  s_agg[wave][1][lane] = a.M;
+  s_agg[wave][2][lane] = a.N;
+  s_agg[wave][3][lane] = a.C;
+  __syncthreads();
+
+  if (wave == 0) {
+    FG seg[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+      seg[w] = FG{s_agg[w][0][lane], s_agg[w][1][lane], s_agg[w][2][lane], s_agg[w][3][lane]};
+    FG tile_agg = seg[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) tile_agg = fg_compose(tile_agg, seg[w]);
+
+    // Carry into the tile.
+    float m = 0.f, n = 0.f, c = 0.f;
+    if (id.chunk == 0) {
+      if (h0 != nullptr && live) {
+        const TX* hb = h0 + static_cast<size_t>(id.b) * row4 + ch;
+        c = ld(hb);
+        n = ld(hb + d);
+        m = ld(hb + 2 * d);
+      }
+    } else {
+      float* ap = agg + (static_cast<size_t>(tile) * 4) * kCB + lane;
+      ap[0 * kCB] = tile_agg.F;
+      ap[1 * kCB] = tile_agg.M;
+      ap[2 * kCB] = tile_agg.N;
+      ap[3 * kCB] = tile_agg.C;
+      publish(flags + tile, epoch, kStatusAgg, lane);
+      FG acc = fg_identity();
+      int pc = id.chunk - 1;
+      while (true) {
+        const int ptile = pc * (B * n_cb) + id.rem;
+        const int st = wait_status(flags + ptile, epoch);
+        if (st == kStatusIncl) {
+          const float* ip = incl + (static_cast<size_t>(ptile) * 3) * kCB + lane;
+          m = ld_payload(ip);
+          n = ld_payload(ip + kCB);
+          c = ld_payload(ip + 2 * kCB);
+          fg_apply(acc, m, n, c);
+          break;
+        }
+        const float* pp = agg + (static_cast<size_t>(ptile) * 4) * kCB + lane;
+        const FG pa{ld_payload(pp), ld_payload(pp + kCB), ld_payload(pp + 2 * kCB),
+                    ld_payload(pp + 3 * kCB)};
+        acc = fg_compose(pa, acc);
+        --pc;
+      }
+    }
+    // Per-wave carries, then the tile's inclusive carry.
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      s_carry[w][0][lane] = m;
+      s_carry[w][1][lane] = n;
+      s_carry[w][2][lane] = c;
+      fg_apply(seg[w], m, n, c);
+    }
+    float* ip = incl + (static_cast<size_t>(tile) * 3) * kCB + lane;
+    ip[0] = m;
+    ip[kCB] = n;
+    ip[2 * kCB] = c;
+    publish(flags + tile, epoch, kStatusIncl, lane);
+  }
+  __syncthreads();
+
+  // Pass 2: replay with the true carry and stream the trajectory.
+  float m = s_carry[wave][0][lane], n = s_carry[wave][1][lane], c = s_carry[wave][2][lane];
+#pragma unroll
+  for (int s = 0; s < L; ++s) {
+    const int t = t0 + s;
+    if (live && t < T) {
+      fg_step(pre[s][0], pre[s][1], pre[s][2], m, n, c);
+      const float o = fsigmoid(pre[s][3]);
+      const float h = o * (c * frcp(n + eps));
+      if (FULL_OUT) {
+        TX* op = out_full + (static_cast<size_t>(id.b) * T + t) * row4 + ch;
+        st(op, c);
+        st(op + d, n);
+        st(op + 2 * d, m);
+        st(op + 3 * d, h);
+      } else {
+        st(out_h + (static_cast<size_t>(id.b) * T + t) * d + ch, h);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// (2) Newton iteration
+// ---------------------------------------------------------------------------
+
+// Cell value and the 12 structural non-zeros of the per-channel Jacobian
+// [out, in] over slots (c, n, m, h):
+//   c: [f, 0, cm, ch]   n: [0, f, nm, nh]   m: [0, 0, al, mh]   h: [hc, hn, hm, hh]
+struct CellJ {
+  float pc, pn, pm, ph;
+  float f, cm, ch, nm, nh, al, mh, hc, hn, hm, hh;
+};
+
+__device__ __forceinline__ CellJ cell_jac(const float prev[4], const float x[4], const float r[4],
+                                          float eps) {
+  const float c = prev[0], n = prev[1], m = prev[2], h = prev[3];
+  const float zi = add_rn(x[0], mul_rn(r[0], h));
+  const float zf = add_rn(x[1], mul_rn(r[1], h));
+  const float zz = add_rn(x[2], mul_rn(r[2], h));
+  const float zo = add_rn(x[3], mul_rn(r[3], h));
+  const float left = zf + m;
+  const float mn = fmaxf(left, zi);
+  // d max(left, z_i) / d left, ties split 0.5 / 0.5 (para_slstm.py:530-534).
+  const float al = left > zi ? 1.f : (left == zi ? 0.5f : 0.f);
+  const float i = fexp(zi - mn);
+  const float f = fexp(left - mn);
+  const float z = ftanh(zz);
+  const float nn = f * n + i;
+  const float cn = f * c + i * z;
+  const float o = fsigmoid(zo);
+  const float inv_den = frcp(nn + eps);
+  CellJ J;
+  J.pc = cn;
+  J.pn = nn;
+  J.pm = mn;
+  J.ph = o * (cn * inv_den);
+  const float be = 1.f - al;
+  const float dm_dh = al * r[1] + be * r[0];
+  const float di_dm = -i * al;
+  const float df_dm = f * be;
+  const float di_dh = i * (r[0] - dm_dh);
+  const float df_dh = f * (r[1] - dm_dh);
+  const float dz_dh = (1.f - z * z) * r[2];
+  const float do_dh = o * (1.f - o) * r[3];
+  J.f = f;
+  J.cm = df_dm * c + di_dm * z;
+  J.ch = df_dh * c + di_dh * z + i * dz_dh;
+  J.nm = df_dm * n + di_dm;
+  J.nh = df_dh * n + di_dh;
+  J.al = al;
+  J.mh = dm_dh;
+  const float inv = o * inv_den;
+  const float dn = -o * cn * inv_den * inv_den;
+  const float du = cn * inv_den;
+  J.hc = inv * f;
+  J.hn = dn * f;
+  J.hm = inv * J.cm + dn * J.nm;
+  J.hh = inv * J.ch + dn * J.nh + du * do_dh;
+  return J;
+}
+
+// v <- J v (+ add)
+__device__ __forceinline__ void jmv(const CellJ& J, float v[4]) {
+  const float c = v[0], n = v[1], m = v[2], h = v[3];
+  v[0] = J.f * c + J.cm * m + J.ch * h;
+  v[1] = J.f * n + J.nm * m + J.nh * h;
+  v[2] = J.al * m + J.mh * h;
+  v[3] = J.hc * c + J.hn * n + J.hm * m + J.hh * h;
+}
+
+// 4x4 affine element (A, b): x -> A x + b
+struct Aff {
+  float A[4][4];
+  float b[4];
+};
+
+__device__ __forceinline__ void aff_identity(Aff& a) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    a.b[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a.A[i][j] = i == j ? 1.f : 0.f;
+  }
+}
+
+// y after x: (Ay Ax, Ay bx + by)
+__device__ __forceinline__ Aff aff_compose(const Aff& x, const Aff& y) {
+  Aff o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float acc = y.b[i];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc += y.A[i][k] * x.b[k];
+    o.b[i] = acc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float s = 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) s += y.A[i][k] * x.A[k][j];
+      o.A[i][j] = s;
+    }
+  }
+  return o;
+}
+
+__device__ __forceinline__ void aff_apply(const Aff& a, float v[4]) {
+  float o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float acc = a.b[i];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc += a.A[i][k] * v[k];
+    o[i] = acc;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = o[i];
+}
+
+template <typename TX, typename TIN, typename TOUT, int L, int W>
+__global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
+    const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
+    const TIN* __restrict__ hin, TOUT* __restrict__ hout, int B, int T, int d, int n_cb,
+    float omega, float eps, int* __restrict__ counter, int* __restrict__ flags,
+    float* __restrict__ agg, float* __restrict__ incl, int epoch) {
+  __shared__ float s_agg[W][20][kCB];
+  __shared__ float s_carry[W][4][kCB];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int tile = take_ticket(counter);
+  const TileId id = decode_tile(tile, B, n_cb);
+  const int ch = id.cb * kCB + lane;
+  const bool live = ch < d;
+  const int t0 = id.chunk * (W * L) + wave * L;
+  const size_t row4 = static_cast<size_t>(4) * d;
+
+  float r[4] = {0.f, 0.f, 0.f, 0.f};
+  if (live) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) r[g] = ld(rmix + g * d + ch);
+  }
+  // Linearisation point H_{t0-1}: previous guess, h0 at t = 0, else zeros.
+  float prev0[4] = {0.f, 0.f, 0.f, 0.f};
+  if (live) {
+    if (t0 > 0 && t0 - 1 < T) {
+      const TIN* p = hin + (static_cast<size_t>(id.b) * T + (t0 - 1)) * row4 + ch;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) prev0[k] = ld(p + k * d);
+    } else if (t0 == 0 && h0 != nullptr) {
+      const TX* p = h0 + static_cast<size_t>(id.b) * row4 + ch;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) prev0[k] = ld(p + k * d);
+    }
+  }
+  float xs[L][4], hs[L][4];
+#pragma unroll
+  for (int s = 0; s < L; ++s) {
+    const int t = t0 + s;
+    if (live && t < T) {
+      const size_t base = (static_cast<size_t>(id.b) * T + t) * row4 + ch;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        xs[s][k] = ld(wx + base + k * d);
+        hs[s][k] = ld(hin + base + k * d);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) xs[s][k] = hs[s][k] = 0.f;
+    }
+  }
+
+  // Pass 1: lane segment aggregate (A, b) of the affine maps x -> J x + F.
+  Aff a;
+  aff_identity(a);
+  {
+    float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
+#pragma unroll
+    for (int s = 0; s < L; ++s) {
+      if (t0 + s < T) {
+        const CellJ J = cell_jac(prev, xs[s], r, eps);
+        const float F[4] = {J.pc - hs[s][0], J.pn - hs[s][1], J.pm - hs[s][2], J.ph - hs[s][3]};
+        jmv(J, a.b);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) a.b[k] += F[k];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float col[4] = {a.A[0][j], a.A[1][j], a.A[2][j], a.A[3][j]};
+          jmv(J, col);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) a.A[k][j] = col[k];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) prev[k] = hs[s][k];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s_agg[wave][16 + i][lane] = a.b[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s_agg[wave][4 * i + j][lane] = a.A[i][j];
+  }
+  __syncthreads();
+
+  if (wave == 0) {
+    Aff tile_agg;
+    aff_identity(tile_agg);
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      Aff sw;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sw.b[i] = s_agg[w][16 + i][lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sw.A[i][j] = s_agg[w][4 * i + j][lane];
+      }
+      tile_agg = w == 0 ? sw : aff_compose(tile_agg, sw);
+    }
+    float carry[4] = {0.f, 0.f, 0.f, 0.f};  // delta_{-1} = 0
+    if (id.chunk > 0) {
+      float* ap = agg + (static_cast<size_t>(tile) * 20) * kCB + lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ap[(16 + i) * kCB] = tile_agg.b[i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ap[(4 * i + j) * kCB] = tile_agg.A[i][j];
+      }
+      publish(flags + tile, epoch, kStatusAgg, lane);
+      // acc maps the carry out of predecessor tile pc to the carry into this tile.
+      Aff acc;
+      aff_identity(acc);
+      int pc = id.chunk - 1;
+      while (true) {
+        const int ptile = pc * (B * n_cb) + id.rem;
+        const int st = wait_status(flags + ptile, epoch);
+        if (st == kStatusIncl) {
+          const float* ip = incl + (static_cast<size_t>(ptile) * 4) * kCB + lane;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) carry[k] = ld_payload(ip + k * kCB);
+          aff_apply(acc, carry);
+          break;
+        }
+        const float* pp = agg + (static_cast<size_t>(ptile) * 20) * kCB + lane;
+        Aff pa;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pa.b[i] = ld_payload(pp + (16 + i) * kCB);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) pa.A[i][j] = ld_payload(pp + (4 * i + j) * kCB);
+        }
+        acc = aff_compose(pa, acc);
+        --pc;
+      }
+    }
+    // Carry into each wave's segment, then the tile's outgoing carry.
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) s_carry[w][k][lane] = carry[k];
+      Aff sw;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sw.b[i] = s_agg[w][16 + i][lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sw.A[i][j] = s_agg[w][4 * i + j][lane];
+      }
+      aff_apply(sw, carry);
+    }
+    float* ip = incl + (static_cast<size_t>(tile) * 4) * kCB + lane;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ip[k * kCB] = carry[k];
+    publish(flags + tile, epoch, kStatusIncl, lane);
+  }
+  __syncthreads();
+
+  // Pass 2: delta_t = J_t delta_{t-1} + F_t from the true carry; H += omega delta.
+  float dl[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) dl[k] = s_carry[wave][k][lane];
+  float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
+#pragma unroll
+  for (int s = 0; s < L; ++s) {
+    const int t = t0 + s;
+    if (live && t < T) {
+      const CellJ J = cell_jac(prev, xs[s], r, eps);
+      jmv(J, dl);
+      dl[0] += J.pc - hs[s][0];
+      dl[1] += J.pn - hs[s][1];
+      dl[2] += J.pm - hs[s][2];
+      dl[3] += J.ph - hs[s][3];
+      TOUT* op = hout + (static_cast<size_t>(id.b) * T + t) * row4 + ch;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) st(op + k * d, add_rn(hs[s][k], mul_rn(omega, dl[k])));
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) prev[k] = hs[s][k];
+  }
+}
+
+}  // namespace slstm
+}  // namespace prnn
+
+// ===========================================================================
+// Host entry points
+// ===========================================================================
+namespace prnn {
+namespace slstm {
+
+constexpr int kFrozenL = 16, kFrozenW = 4;  // frozen-gate tile: 64 ch x 64 steps
+constexpr int kNewtonL = 16, kNewtonW = 4;  // Newton tile:      64 ch x 64 steps
+constexpr int kMaxStages = 64;              // ticket counters per call
+
+struct Geo {
+  int n_cb, n_chunks, n_tiles;
+};
+
+static Geo geometry(int B, int T, int d, int chunk) {
+  Geo g;
+  g.n_cb = (d + kCB - 1) / kCB;
+  g.n_chunks = (T + chunk - 1) / chunk;
+  g.n_tiles = B * g.n_cb * g.n_chunks;
+  return g;
+}
+
+static size_t elem_size(int dtype) { return dtype == PRNN_BF16 ? 2 : 4; }
+
+static int check_dims(int B, int T, int d, int dtype) {
+  if (B < 1 || T < 1 || d < 1)
+    return fail(PRNN_ERR_VALUE, "B, T, d must be >= 1, got B=%d T=%d d=%d", B, T, d);
+  if (dtype != PRNN_F32 && dtype != PRNN_BF16)
+    return fail(PRNN_ERR_TYPE, "dtype code %d is not float32 (0) or bfloat16 (1)", dtype);
+  const long long tiles = static_cast<long long>(B) * ((d + kCB - 1) / kCB) * ((T + 63) / 64);
+  if (tiles > (1ll << 28))
+    return fail(PRNN_ERR_VALUE, "problem too large: %lld tiles", tiles);
+  return PRNN_OK;
+}
+
+struct InitWs {
+  int* counters;
+  int* flags;
+  float* agg;
+  float* incl;
+  void* hbuf[2];
+};
+
+static InitWs carve_init(void* base, int B, int T, int d, int P, int dtype, size_t* total) {
+  const Geo g = geometry(B, T, d, kFrozenL * kFrozenW);
+  Carver cv(base);
+  InitWs w;
+  w.counters = static_cast<int*>(cv.take(sizeof(int) * kMaxStages));
+  w.flags = static_cast<int*>(cv.take(sizeof(int) * g.n_tiles));
+  w.agg = static_cast<float*>(cv.take(sizeof(float) * 4 * kCB * g.n_tiles));
+  w.incl = static_cast<float*>(cv.take(sizeof(float) * 3 * kCB * g.n_tiles));
+  const size_t hb = static_cast<size_t>(B) * T * d * elem_size(dtype);
+  w.hbuf[0] = P >= 1 ? cv.take(hb) : nullptr;
+  w.hbuf[1] = P >= 2 ? cv.take(hb) : nullptr;
+  *total = cv.used;
+  return w;
+}
+
+struct NewtonWs {
+  int* counters;
+  int* flags;
+  float* agg;
+  float* incl;
+  float* work[2];
+};
+
+static NewtonWs carve_newton(void* base, int B, int T, int d, int K, size_t* total) {
+  const Geo g = geometry(B, T, d, kNewtonL * kNewtonW);
+  Carver cv(base);
+  NewtonWs w;
+  w.counters = static_cast<int*>(cv.take(sizeof(int) * kMaxStages));
+  w.flags = static_cast<int*>(cv.take(sizeof(int) * g.n_tiles));
+  w.agg = static_cast<float*>(cv.take(sizeof(float) * 20 * kCB * g.n_tiles));
+  w.incl = static_cast<float*>(cv.take(sizeof(float) * 4 * kCB * g.n_tiles));
+  const size_t wb = static_cast<size_t>(B) * T * 4 * d * sizeof(float);
+  w.work[0] = K >= 2 ? static_cast<float*>(cv.take(wb)) : nullptr;
+  w.work[1] = K >= 3 ? static_cast<float*>(cv.take(wb)) : nullptr;
+  *total = cv.used;
+  return w;
+}
+
+template <typename TX>
+static int run_init(const TX* wx, const TX* r, const TX* h0, TX* states, int B, int T, int d,
+                    int P, float eps, const InitWs& w, hipStream_t stream) {
+  const Geo g = geometry(B, T, d, kFrozenL * kFrozenW);
+  const dim3 grid(g.n_tiles), block(64 * kFrozenW);
+  int rc = clear_words(w.counters, kMaxStages + (g.n_tiles + 63) / 64 * 64, stream);
+  if (rc != PRNN_OK) return rc;
+  // Pass 0: zero-hidden scan (pre = wx).
+  if (P == 0) {
+    slstm_frozen_kernel<TX, kFrozenL, kFrozenW, false, true><<<grid, block, 0, stream>>>(
+        wx, r, h0, nullptr, states, nullptr, B, T, d, g.n_cb, eps, w.counters + 1, w.flags,
+        w.agg, w.incl, 1);
+  } else {
+    slstm_frozen_kernel<TX, kFrozenL, kFrozenW, false, false><<<grid, block, 0, stream>>>(
+        wx, r, h0, nullptr, nullptr, static_cast<TX*>(w.hbuf[0]), B, T, d, g.n_cb, eps,
+        w.counters + 1, w.flags, w.agg, w.incl, 1);
+  }
+  PRNN_HIP(hipGetLastError());
+  for (int p = 1; p <= P; ++p) {
+    const TX* src = static_cast<const TX*>(w.hbuf[(p - 1) & 1]);
+    const int epoch = p + 1;
+    if (p == P) {
+      slstm_frozen_kernel<TX, kFrozenL, kFrozenW, true, true><<<grid, block, 0, stream>>>(
+          wx, r, h0, src, states, nullptr, B, T, d, g.n_cb, eps, w.counters + epoch, w.flags,
+          w.agg, w.incl, epoch);
+    } else {
+      slstm_frozen_kernel<TX, kFrozenL, kFrozenW, true, false><<<grid, block, 0, stream>>>(
+          wx, r, h0, src, nullptr, static_cast<TX*>(w.hbuf[p & 1]), B, T, d, g.n_cb, eps,
+          w.counters + epoch, w.flags, w.agg, w.incl, epoch);
+    }
+    PRNN_HIP(hipGetLastError());
+  }
+  return PRNN_OK;
+}
+
+template <typename TX, typename TIN, typename TOUT>
+static void launch_newton(const TX* wx, const TX* r, const TX* h0, const TIN* hin, TOUT* hout,
+                          int B, int T, int d, float omega, float eps, const NewtonWs& w,
+                          int epoch, hipStream_t stream) {
+  const Geo g = geometry(B, T, d, kNewtonL * kNewtonW);
+  slstm_newton_kernel<TX, TIN, TOUT, kNewtonL, kNewtonW>
+      <<<dim3(g.n_tiles), dim3(64 * kNewtonW), 0, stream>>>(
+          wx, r, h0, hin, hout, B, T, d, g.n_cb, omega, eps, w.counters + epoch, w.flags, w.agg,
+          w.incl, epoch);
+}
+
+template <typename TX>
+static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, TX* out, int B,
+                      int T, int d, int K, float omega, float eps, const NewtonWs& w,
+                      hipStream_t stream) {
+  if (K == 0) {
+    PRNN_HIP(hipMemcpyAsync(out, guess, static_cast<size_t>(B) * T * 4 * d * sizeof(TX),
+                            hipMemcpyDeviceToDevice, stream));
+    return PRNN_OK;
+  }
+  const Geo g = geometry(B, T, d, kNewtonL * kNewtonW);
+  int rc = clear_words(w.counters, kMaxStages + (g.n_tiles + 63) / 64 * 64, stream);
+  if (rc != PRNN_OK) return rc;
+  for (int k = 1; k <= K; ++k) {
+    const bool first = k == 1, last = k == K;
+    const float* win = first ? nullptr : w.work[(k - 2) & 1];
+    float* wout = last ? nullptr : w.work[(k - 1) & 1];
+    if (first && last)
+      launch_newton<TX, TX, TX>(wx, r, h0, guess, out, B, T, d, omega, eps, w, k, stream);
+    else if (first)
+      launch_newton<TX, TX, float>(wx, r, h0, guess, wout, B, T, d, omega, eps, w, k, stream);
+    else if (last)
+      launch_newton<TX, float, TX>(wx, r, h0, win, out, B, T, d, omega, eps, w, k, stream);
+    else
+      launch_newton<TX, float, float>(wx, r, h0, win, wout, B, T, d, omega, eps, w, k, stream);
+    PRNN_HIP(hipGetLastError());
+  }
+  return PRNN_OK;
+}
+
+}  // namespace slstm
+}  // namespace prnn
+
+using namespace prnn;
+
+extern "C" PRNN_API size_t prnn_slstm_init_workspace_size(int B, int T, int d, int picard_iters,
+                                                          int dtype) {
+  if (slstm::check_dims(B, T, d, dtype) != PRNN_OK || picard_iters < 0) return 0;
+  size_t total = 0;
+  slstm::carve_init(nullptr, B, T, d, picard_iters, dtype, &total);
+  return total;
+}
+
+extern "C" PRNN_API int prnn_slstm_init(const void* wx, const void* r, const void* h0,
+                                        void* states, int B, int T, int d, int picard_iters,
+                                        float eps, int dtype, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  int rc = slstm::check_dims(B, T, d, dtype);
+  if (rc != PRNN_OK) return rc;
+  if (picard_iters < 0 || picard_iters > slstm::kMaxStages - 2)
+    return fail(PRNN_ERR_VALUE, "picard_iters must be in [0, %d], got %d",
+                slstm::kMaxStages - 2, picard_iters);
+  if (!wx || !r || !states || !workspace)
+    return fail(PRNN_ERR_VALUE, "wx, r, states and workspace must be non-null");
+  size_t need = 0;
+  const slstm::InitWs w = slstm::carve_init(workspace, B, T, d, picard_iters, dtype, &need);
+  if (workspace_bytes < need)
+    return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == PRNN_F32)
+    return slstm::run_init(static_cast<const float*>(wx), static_cast<const float*>(r),
+                           static_cast<const float*>(h0), static_cast<float*>(states), B, T, d,
+                           picard_iters, eps, w, s);
+  return slstm::run_init(static_cast<const bf16*>(wx), static_cast<const bf16*>(r),
+                         static_cast<const bf16*>(h0), static_cast<bf16*>(states), B, T, d,
+                         picard_iters, eps, w, s);
+}
+
+extern "C" PRNN_API size_t prnn_slstm_newton_workspace_size(int B, int T, int d, int max_iters,
+                                                            int dtype) {
+  if (slstm::check_dims(B, T, d, dtype) != PRNN_OK || max_iters < 0) return 0;
+  size_t total = 0;
+  slstm::carve_newton(nullptr, B, T, d, max_iters, &total);
+  return total;
+}
+
+extern "C" PRNN_API int prnn_slstm_newton(const void* wx, const void* r, const void* h0,
+                                          const void* states, void* out, int B, int T, int d,
+                                          int max_iters, float omega, float eps, int dtype,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = slstm::check_dims(B, T, d, dtype);
+  if (rc != PRNN_OK) return rc;
+  if (max_iters < 0 || max_iters > slstm::kMaxStages - 1)
+    return fail(PRNN_ERR_VALUE, "max_iters must be in [0, %d], got %d", slstm::kMaxStages - 1,
+                max_iters);
+  if (!wx || !r || !states || !out || !workspace)
+    return fail(PRNN_ERR_VALUE, "wx, r, states, out and workspace must be non-null");
+  if (out == states) return fail(PRNN_ERR_VALUE, "out must not alias states");
+  size_t need = 0;
+  const slstm::NewtonWs w = slstm::carve_newton(workspace, B, T, d, max_iters, &need);
+  if (workspace_bytes < need)
+    return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == PRNN_F32)
+    return slstm::run_newton(static_cast<const float*>(wx), static_cast<const float*>(r),
+                             static_cast<const float*>(h0), static_cast<const float*>(states),
+                             static_cast<float*>(out), B, T, d, max_iters, omega, eps, w, s);
+  return slstm::run_newton(static_cast<const bf16*>(wx), static_cast<const bf16*>(r),
+                           static_cast<const bf16*>(h0), static_cast<const bf16*>(states),
+                           static_cast<bf16*>(out), B, T, d, max_iters, omega, eps, w, s);
+}

@@ -1,0 +1,249 @@
+"""``torch.library`` custom ops over the HIP kernels (the drop-in boundary).
+
+``pararnn::newton_slstm_fused`` and ``pararnn::newton_gru_head_fused`` keep the
+names, schemas, return layouts and error types of the reference's ops
+(``kernels/custom_ops.py:311-386, 486-540``); ``pararnn::slstm_init_fused``
+is the frozen-gate / Picard guess that the reference computes in Python
+before calling its op (``kernels/fused_newton.py:358-372``).  Each op
+validates on the host, allocates its outputs and a workspace through torch's
+caching allocator, and enqueues the kernels on the current stream of the
+tensors' device through the C ABI.  All are functional (``mutates_args=()``)
+and have fake kernels for ``torch.compile``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+from torch import Tensor
+
+from pararnn_amd import _lib
+
+_DTYPES = {torch.float32: _lib.PRNN_F32, torch.bfloat16: _lib.PRNN_BF16}
+
+
+def _validate(name: str, *tensors: Tensor | None) -> int:
+    """Device/dtype rules of the reference's ``validate_cuda_tensors``
+    (kernels/precision.py:40-68): one GPU device, one dtype, float32/bfloat16."""
+    ts = [t for t in tensors if t is not None]
+    ref = ts[0]
+    for t in ts:
+        if t.device.type != "cuda":
+            raise RuntimeError(f"{name} requires a ROCm GPU tensor, got {t.device}")
+        if t.device != ref.device:
+            raise RuntimeError(f"{name}: tensors on different devices ({t.device} vs {ref.device})")
+        if t.dtype != ref.dtype:
+            raise TypeError(f"{name}: dtype mismatch {t.dtype} vs {ref.dtype}")
+    if ref.dtype not in _DTYPES:
+        raise TypeError(f"{name} supports float32/bfloat16, got {ref.dtype}")
+    return _DTYPES[ref.dtype]
+
+
+def _ptr(t: Tensor | None) -> ctypes.c_void_p | None:
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _workspace(nbytes: int, dev: torch.device) -> Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
+
+
+# ---------------------------------------------------------------------------
+# ParaSLSTM mix='diag'
+# ---------------------------------------------------------------------------
+
+
+def _slstm_shapes(wx: Tensor, r: Tensor) -> tuple[int, int, int]:
+    if wx.dim() != 3:
+        raise ValueError(f"wx must be (B, T, 4 d_h), got {tuple(wx.shape)}")
+    batch, time, four_d = wx.shape
+    d_h = r.shape[-1]
+    if r.shape != (4, d_h):
+        raise ValueError(f"r shape {tuple(r.shape)} != {(4, d_h)}")
+    if four_d != 4 * d_h:
+        raise ValueError(f"wx last dim {four_d} != 4 * d_h={4 * d_h}")
+    return batch, time, d_h
+
+
+def _slstm_h0(h0: Tensor | None, batch: int, d_h: int) -> Tensor | None:
+    if h0 is None:
+        return None
+    if h0.shape != (batch, 4, d_h):
+        raise ValueError(f"h0 shape {tuple(h0.shape)} != {(batch, 4, d_h)}")
+    return h0.contiguous()
+
+
+@torch.library.custom_op("pararnn::slstm_init_fused", mutates_args=())
+def slstm_init_fused(
+    wx: Tensor, r: Tensor, h0: Tensor | None = None, *, picard_iters: int, eps: float
+) -> Tensor:
+    """Zero-hidden frozen-gate scan plus ``picard_iters`` Picard passes on the GPU.
+
+    Same result layout and rounding points as the reference's
+    ``slstm_picard_init`` / ``slstm_zero_hidden_init`` (solvers/slstm_picard.py:143-181):
+    states ``(B, T, 4, d_h)`` in ``wx``'s dtype; between passes the trajectory
+    is held in that dtype and ``wx + R * h_prev`` is rounded after each op.
+    """
+    batch, time, d_h = _slstm_shapes(wx, r)
+    code = _validate("slstm_init_fused", wx, r, h0)
+    if picard_iters < 0:
+        raise ValueError(f"n_picard must be >= 0, got {picard_iters!r}")
+    wx = wx.contiguous()
+    r = r.contiguous()
+    h0 = _slstm_h0(h0, batch, d_h)
+    out = wx.new_empty(batch, time, 4, d_h)
+    lib = _lib.load()
+    with torch.cuda.device(wx.device):
+        nbytes = lib.prnn_slstm_init_workspace_size(batch, time, d_h, picard_iters, code)
+        ws = _workspace(nbytes, wx.device)
+        rc = lib.prnn_slstm_init(
+            _ptr(wx), _ptr(r), _ptr(h0), _ptr(out), batch, time, d_h, int(picard_iters),
+            float(eps), code, _ptr(ws), ws.numel(), _stream(wx.device),
+        )
+    _lib.check(rc, "slstm_init_fused")
+    return out
+
+
+@slstm_init_fused.register_fake
+def _(wx, r, h0=None, *, picard_iters, eps):
+    batch, time, _ = wx.shape
+    return wx.new_empty(batch, time, 4, r.shape[-1])
+
+
+@torch.library.custom_op("pararnn::newton_slstm_fused", mutates_args=())
+def newton_slstm_fused(
+    wx: Tensor,
+    r: Tensor,
+    h0: Tensor | None = None,
+    states: Tensor | None = None,
+    block_table: Tensor | None = None,
+    *,
+    max_iters: int,
+    omega: float,
+    eps: float,
+    log_coords: bool = False,
+    scan_tile: str = "assoc",
+    time_loop: bool = False,
+    window_len: int = 0,
+) -> Tensor:
+    """``max_iters`` fused Newton iterations for diag ParaSLSTM on the GPU.
+
+    Same schema as the reference op (kernels/custom_ops.py:486-516).  Work is
+    fp32 throughout; intermediate trajectories stay fp32 and the result is
+    rounded once to ``wx``'s dtype (kernels/newton_slstm.py:2780-2939).
+    ``states=None`` starts from the zero-hidden guess.
+    """
+    if log_coords:
+        raise TypeError("newton_slstm_fused: log_coords is not provided by pararnn_amd")
+    if scan_tile != "assoc":
+        raise TypeError(f"newton_slstm_fused: scan_tile={scan_tile!r} is not provided (assoc only)")
+    if time_loop or window_len:
+        raise TypeError("newton_slstm_fused: fused_time_loop is not provided by pararnn_amd")
+    if block_table is not None:
+        raise TypeError("newton_slstm_fused: block_table (paged h0) is not provided by pararnn_amd")
+    batch, time, d_h = _slstm_shapes(wx, r)
+    code = _validate("newton_slstm_fused", wx, r, h0)
+    if max_iters < 0:
+        raise ValueError(f"max_iters must be >= 0, got {max_iters!r}")
+    h0 = _slstm_h0(h0, batch, d_h)
+    if states is None:
+        states = slstm_init_fused(wx, r, h0, picard_iters=0, eps=eps)
+    else:
+        if states.shape != (batch, time, 4, d_h):
+            raise ValueError(f"states shape {tuple(states.shape)} != {(batch, time, 4, d_h)}")
+        _validate("newton_slstm_fused", wx, states)
+    wx = wx.contiguous()
+    r = r.contiguous()
+    states = states.contiguous()
+    out = wx.new_empty(batch, time, 4, d_h)
+    lib = _lib.load()
+    with torch.cuda.device(wx.device):
+        nbytes = lib.prnn_slstm_newton_workspace_size(batch, time, d_h, int(max_iters), code)
+        ws = _workspace(nbytes, wx.device)
+        rc = lib.prnn_slstm_newton(
+            _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), _ptr(out), batch, time, d_h,
+            int(max_iters), float(omega), float(eps), code, _ptr(ws), ws.numel(),
+            _stream(wx.device),
+        )
+    _lib.check(rc, "newton_slstm_fused")
+    return out
+
+
+@newton_slstm_fused.register_fake
+def _(wx, r, h0=None, states=None, block_table=None, *, max_iters, omega, eps,
+      log_coords=False, scan_tile="assoc", time_loop=False, window_len=0):
+    if states is not None:
+        return torch.empty_like(states)
+    batch, time, _ = wx.shape
+    return wx.new_empty(batch, time, 4, r.shape[-1])
+
+
+# ---------------------------------------------------------------------------
+# ParaGRU mix='head'
+# ---------------------------------------------------------------------------
+
+
+@torch.library.custom_op("pararnn::newton_gru_head_fused", mutates_args=())
+def newton_gru_head_fused(
+    wx: Tensor,
+    a_z: Tensor,
+    a_r: Tensor,
+    a_n: Tensor,
+    h0: Tensor | None = None,
+    cu_seqlens: Tensor | None = None,
+    *,
+    max_iters: int,
+    omega: float,
+) -> Tensor:
+    """Fused Alg. 1 for ``ParaGRU(mix='head')`` on the GPU (custom_ops.py:311-358).
+
+    Initial guess ``f(h_prev0, x_t)`` (zeros except ``h0`` at t = 0), then
+    ``max_iters`` Newton iterations, all in fp32; result in ``wx``'s dtype.
+    """
+    if a_z.dim() != 3 or a_z.shape[-1] != a_z.shape[-2]:
+        raise ValueError(f"a_z needs (H,d,d), got {tuple(a_z.shape)}")
+    n_heads, d_head, _ = a_z.shape
+    if a_r.shape != a_z.shape or a_n.shape != a_z.shape:
+        raise ValueError("a_z, a_r, a_n shape mismatch")
+    d_h = n_heads * d_head
+    if wx.dim() != 3 or wx.shape[-1] != 3 * d_h:
+        raise ValueError(f"wx last dim {wx.shape[-1]} != 3 * d_h={3 * d_h}")
+    if cu_seqlens is not None:
+        raise TypeError(
+            "ParaGRU(mix='head') fused Newton does not support cu_seqlens yet; "
+            "use scan_backend='eager' for ragged packs, or pad to a rectangular batch"
+        )
+    if d_head != 64:
+        raise TypeError(f"newton_gru_head_fused: pararnn_amd provides d_head=64, got {d_head}")
+    batch, time, _ = wx.shape
+    code = _validate("newton_gru_head_fused", wx, a_z, a_r, a_n, h0)
+    if h0 is not None and h0.shape != (batch, d_h):
+        raise ValueError(f"h0 shape {tuple(h0.shape)} != {(batch, d_h)}")
+    if max_iters < 0:
+        raise ValueError(f"max_iters must be >= 0, got {max_iters!r}")
+    wx = wx.contiguous()
+    a_z, a_r, a_n = a_z.contiguous(), a_r.contiguous(), a_n.contiguous()
+    h0 = None if h0 is None else h0.contiguous()
+    out = wx.new_empty(batch, time, d_h)
+    lib = _lib.load()
+    with torch.cuda.device(wx.device):
+        nbytes = lib.prnn_gru_head_newton_workspace_size(batch, time, n_heads, d_head,
+                                                         int(max_iters), code)
+        ws = _workspace(nbytes, wx.device)
+        rc = lib.prnn_gru_head_newton(
+            _ptr(wx), _ptr(a_z), _ptr(a_r), _ptr(a_n), _ptr(h0), _ptr(out), batch, time,
+            n_heads, d_head, int(max_iters), float(omega), code, _ptr(ws), ws.numel(),
+            _stream(wx.device),
+        )
+    _lib.check(rc, "newton_gru_head_fused")
+    return out
+
+
+@newton_gru_head_fused.register_fake
+def _(wx, a_z, a_r, a_n, h0=None, cu_seqlens=None, *, max_iters, omega):
+    batch, time, _ = wx.shape
+    return wx.new_empty(batch, time, int(a_z.shape[0] * a_z.shape[-1]))

@@ -1,0 +1,40 @@
+"""Sequential unroll — the numerics oracle that ``verify_agreement`` compares
+against (reference ``solvers/sequential.py:22-86``).  Plain torch ops on the
+tensors' device: one shared ``W_x`` GEMM, then ``cell.step`` over T.
+"""
+
+from __future__ import annotations
+
+import inspect
+
+import torch
+from torch import Tensor, nn
+
+
+def _zero_state(cell: nn.Module, batch: int, ref: Tensor) -> Tensor:
+    slots = getattr(cell, "state_slots", 1)
+    if slots == 1:
+        return ref.new_zeros(batch, cell.d_h)
+    return ref.new_zeros(batch, slots, cell.d_h)
+
+
+def sequential_apply(cell: nn.Module, x: Tensor, h0: Tensor | None = None, *, step=None,
+                     cu_seqlens: Tensor | None = None) -> Tensor:
+    """Unroll ``cell.step`` along time; output at t is the state after step t."""
+    if cu_seqlens is not None:
+        raise TypeError("packed cu_seqlens are not provided by pararnn_amd")
+    batch, time, _ = x.shape
+    if time < 1:
+        raise ValueError(f"sequential_apply needs time >= 1, got {time}")
+    h = h0 if h0 is not None else _zero_state(cell, batch, x)
+    fn = step or cell.step
+    wx_all = None
+    if step is None and "wx" in inspect.signature(cell.step).parameters:
+        lin = getattr(cell, "W_x", None)
+        if lin is not None:
+            wx_all = lin(x)
+    outs = []
+    for t in range(time):
+        h = fn(h, x[:, t]) if wx_all is None else fn(h, x[:, t], wx=wx_all[:, t])
+        outs.append(h)
+    return torch.stack(outs, dim=1)

@@ -1,0 +1,202 @@
+"""Write golden input/output vectors from the reference's eager CPU path.
+
+The reference ships no tests, fixtures or known-answer vectors, and the exact
+rounding of its eager path (bf16 re-rounding after every torch op, the fp32
+Blelloch summation order, the cumsum/cummax stabiliser of the frozen-gate
+scan, and the resolved Picard depth) is not fixed by any closed form.  This
+script therefore imports the reference ONCE, in the build container (never on
+the GPU box), and stores small safetensors fixtures next to itself.  The
+fixtures are data only: inputs, weights and the reference's outputs.
+
+Run:  PYTHONPATH=/root/reference/src python tests/golden/make_golden.py
+
+Reference call sites exercised (paths relative to the reference's src/pararnn):
+  solvers/newton/__init__.py:212 newton_apply   (scan_backend='eager')
+  solvers/sequential.py:22       sequential_apply
+  solvers/slstm_picard.py:160    slstm_picard_init
+  solvers/scan.py:82,103         scan_block4 / scan_dense
+  cells/para_slstm.py:241        ParaSLSTM.step_with_jacobian
+  cells/para_gru.py:344          ParaGRU.step_with_jacobian
+"""
+
+from __future__ import annotations
+
+import json
+import os
+import sys
+
+import torch
+from safetensors.torch import save_file
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _save(name: str, tensors: dict, meta: dict) -> None:
+    out = {k: v.detach().contiguous().cpu() for k, v in tensors.items()}
+    path = os.path.join(HERE, f"{name}.safetensors")
+    save_file(out, path, metadata={"meta": json.dumps(meta)})
+    size = os.path.getsize(path)
+    print(f"wrote {path} ({size / 1e6:.2f} MB)")
+
+
+def _cfg(K: int, P: int | None):
+    from pararnn import NewtonConfig
+
+    return NewtonConfig(
+        max_iters=K,
+        residual_atol=None,
+        residual_fail=None,
+        picard_iters=P,
+        picard_adapt=False,
+        scan_backend="eager",
+    )
+
+
+def slstm_case(name, *, d_in, d, B, T, K, P, dtype, seed, x_std=1.0, with_h0=False,
+               keep_wx=True):
+    from pararnn import ParaSLSTM, newton_apply, sequential_apply
+    from pararnn.solvers.slstm_picard import slstm_picard_init
+
+    torch.manual_seed(seed)
+    cell = ParaSLSTM(d_in, d, mix="diag")
+    cell = cell.to(dtype)
+    g = torch.Generator().manual_seed(seed + 1)
+    x = (torch.randn(B, T, d_in, generator=g) * x_std).to(dtype)
+    h0 = None
+    tensors = {}
+    if with_h0:
+        # A reachable state: the sequential unroll of a short random prefix.
+        xp = torch.randn(B, 16, d_in, generator=g).to(dtype)
+        with torch.no_grad():
+            h0 = sequential_apply(cell, xp)[:, -1].clone()
+        tensors["h0"] = h0
+    with torch.no_grad():
+        wx = cell.W_x(x)
+        init = slstm_picard_init(cell, wx, h0=h0, n_picard=P)
+        H = newton_apply(cell, x, _cfg(K, P), h0=h0)
+        Hs = sequential_apply(cell, x, h0)
+    tensors.update(
+        x=x,
+        W=cell.W_x.weight,
+        b=cell.W_x.bias,
+        R=cell.R,
+        wx=wx,
+        init=init,
+        newton=H,
+        sequential=Hs,
+    )
+    if not keep_wx:
+        # fp32 wx is recomputed exactly from x, W, b; dropping it keeps the file small.
+        tensors.pop("wx")
+    meta = dict(cell="ParaSLSTM", mix="diag", d_in=d_in, d=d, B=B, T=T, K=K, P=P,
+                dtype=str(dtype).replace("torch.", ""), seed=seed, x_std=x_std,
+                eps=cell.eps, max_recurrent_norm=cell.max_recurrent_norm, h0=with_h0)
+    _save(name, tensors, meta)
+
+
+def gru_head_case(name, *, d_in, n_heads, d_head, B, T, K, dtype, seed, with_h0=False):
+    from pararnn import ParaGRU, newton_apply, sequential_apply
+
+    torch.manual_seed(seed)
+    cell = ParaGRU(d_in, n_heads * d_head, mix="head", n_heads=n_heads)
+    cell = cell.to(dtype)
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(B, T, d_in, generator=g).to(dtype)
+    h0 = None
+    tensors = {}
+    if with_h0:
+        h0 = (0.5 * torch.randn(B, n_heads * d_head, generator=g)).to(dtype)
+        tensors["h0"] = h0
+    with torch.no_grad():
+        wx = cell.W_x(x)
+        H = newton_apply(cell, x, _cfg(K, None), h0=h0)
+        Hs = sequential_apply(cell, x, h0)
+    tensors.update(
+        x=x, W=cell.W_x.weight, b=cell.W_x.bias, A_z=cell.A_z, A_r=cell.A_r, A_n=cell.A_n,
+        wx=wx, newton=H, sequential=Hs,
+    )
+    meta = dict(cell="ParaGRU", mix="head", d_in=d_in, n_heads=n_heads, d_head=d_head,
+                B=B, T=T, K=K, dtype=str(dtype).replace("torch.", ""), seed=seed, h0=with_h0)
+    _save(name, tensors, meta)
+
+
+def parts_case():
+    """Single-step cell/Jacobian values and bare scans on random operands."""
+    from pararnn import ParaGRU, ParaSLSTM
+    from pararnn.solvers.scan import scan_block4, scan_dense
+    from pararnn.solvers.slstm_picard import slstm_frozen_gate_scan_eager
+
+    g = torch.Generator().manual_seed(1234)
+    torch.manual_seed(1234)
+    cell = ParaSLSTM(8, 16, mix="diag")
+    state = torch.randn(3, 5, 4, 16, generator=g)
+    state[..., 1, :] = state[..., 1, :].abs() + 0.1  # normaliser n > 0
+    wx = torch.randn(3, 5, 64, generator=g)
+    # Force exact ties of the maximum in a few places (0.5/0.5 subgradient).
+    r = cell.clipped_r().detach()
+    h = state[..., 3, :]
+    pre_f = wx[..., 16:32] + r[1] * h
+    wx[..., 0, 0, 0:4] = (pre_f[0, 0, 0:4] + state[0, 0, 2, 0:4]) - r[0, 0:4] * h[0, 0, 0:4]
+    with torch.no_grad():
+        new, jac = cell.step_with_jacobian(state, None, wx=wx)
+    jb = torch.randn(2, 37, 4, 4, 8, generator=g) * 0.6
+    rb = torch.randn(2, 37, 4, 8, generator=g)
+    db = scan_block4(jb, rb)
+    jd = torch.randn(2, 19, 6, 6, generator=g) * 0.4
+    rd = torch.randn(2, 19, 6, generator=g)
+    dd = scan_dense(jd, rd)
+    pre = torch.randn(2, 300, 4 * 8, generator=g) * 2.0
+    h0 = torch.randn(2, 4, 8, generator=g)
+    h0[:, 1] = h0[:, 1].abs()
+    fg = slstm_frozen_gate_scan_eager(pre, eps=1e-6, h0=h0)
+    fg0 = slstm_frozen_gate_scan_eager(pre, eps=1e-6, h0=None)
+    torch.manual_seed(99)
+    gcell = ParaGRU(8, 2 * 64, mix="head", n_heads=2)
+    hp = torch.randn(3, 4, 128, generator=g) * 0.5
+    gwx = torch.randn(3, 4, 3 * 128, generator=g)
+    with torch.no_grad():
+        gnew, gjac = gcell.step_with_jacobian(hp, None, wx=gwx)
+    _save(
+        "parts",
+        dict(
+            slstm_R=cell.R, slstm_state=state, slstm_wx=wx, slstm_new=new, slstm_jac=jac,
+            scan4_j=jb, scan4_r=rb, scan4_out=db, scand_j=jd, scand_r=rd, scand_out=dd,
+            fg_pre=pre, fg_h0=h0, fg_out=fg, fg_out_noh0=fg0,
+            gru_A_z=gcell.A_z, gru_A_r=gcell.A_r, gru_A_n=gcell.A_n, gru_h=hp, gru_wx=gwx,
+            gru_new=gnew, gru_jac=gjac,
+        ),
+        dict(eps=1e-6),
+    )
+
+
+def auto_picard_table():
+    from pararnn.solvers.newton.picard import slstm_auto_picard
+
+    return {str(t): slstm_auto_picard(t) for t in (1, 64, 65, 2048, 2049, 16384, 131072)}
+
+
+def main() -> int:
+    torch.set_num_threads(8)
+    parts_case()
+    # BASELINE config 1, the reference's CPU-runnable parity case.
+    slstm_case("slstm_cfg1_fp32", d_in=64, d=64, B=2, T=1024, K=2, P=3,
+               dtype=torch.float32, seed=0, keep_wx=False)
+    slstm_case("slstm_h0_fp32", d_in=24, d=32, B=2, T=200, K=3, P=1,
+               dtype=torch.float32, seed=5, with_h0=True)
+    slstm_case("slstm_bf16", d_in=64, d=64, B=2, T=512, K=2, P=3,
+               dtype=torch.bfloat16, seed=1)
+    slstm_case("slstm_long_fp32", d_in=16, d=16, B=1, T=4096, K=2, P=5,
+               dtype=torch.float32, seed=2, x_std=0.5)
+    gru_head_case("gru_head_fp32", d_in=64, n_heads=2, d_head=64, B=2, T=256, K=3,
+                  dtype=torch.float32, seed=3)
+    gru_head_case("gru_head_h0_fp32", d_in=32, n_heads=2, d_head=64, B=1, T=96, K=3,
+                  dtype=torch.float32, seed=4, with_h0=True)
+    gru_head_case("gru_head_bf16", d_in=64, n_heads=2, d_head=64, B=1, T=128, K=3,
+                  dtype=torch.bfloat16, seed=6)
+    with open(os.path.join(HERE, "auto_picard.json"), "w") as f:
+        json.dump(auto_picard_table(), f, indent=1)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

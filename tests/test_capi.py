@@ -1,0 +1,62 @@
+"""The C-ABI library loads and exports every entry point include/pararnn_amd.h
+declares, with the argument counts the ctypes binding uses.  No GPU calls."""
+
+import ctypes
+import os
+import re
+
+import pytest
+from conftest import REPO
+
+
+def _declared():
+    text = open(os.path.join(REPO, "include", "pararnn_amd.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"PRNN_API\s+[\w\s\*]+?\b(prnn_\w+)\s*\(([^)]*)\)", text):
+        args = [a for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
+        out[m.group(1)] = len(args)
+    return out
+
+
+def test_header_declares_entry_points():
+    decl = _declared()
+    for name in ("prnn_slstm_init", "prnn_slstm_newton", "prnn_gru_head_newton",
+                 "prnn_last_error", "prnn_abi_version"):
+        assert name in decl
+
+
+def test_library_exports_every_declared_symbol():
+    from pararnn_amd import _lib
+
+    if not os.path.exists(_lib.lib_path()):
+        pytest.skip("library not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(_lib.lib_path())
+    decl = _declared()
+    for name, nargs in decl.items():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, name
+        assert len(_lib.SIGNATURES[name][1]) == nargs, name
+
+
+def test_host_only_calls():
+    from pararnn_amd import _lib
+
+    if not os.path.exists(_lib.lib_path()):
+        pytest.skip("library not built")
+    lib = _lib.load()
+    assert lib.prnn_abi_version() == _lib.ABI_VERSION
+    n = lib.prnn_slstm_newton_workspace_size(1, 131072, 1024, 2, _lib.PRNN_BF16)
+    # K=2 keeps one fp32 trajectory (B*T*4*d*4 bytes) plus look-back state.
+    assert n > 131072 * 4 * 1024 * 4
+    assert lib.prnn_slstm_newton_workspace_size(0, 1, 1, 2, 0) == 0
+    assert lib.prnn_slstm_init_workspace_size(1, 10, 10, -1, 0) == 0
+    # invalid arguments fail before any device work
+    rc = lib.prnn_slstm_newton(None, None, None, None, None, 1, 1, 1, 1, 1.0, 1e-6, 0,
+                               None, 0, None)
+    assert rc == _lib.PRNN_ERR_VALUE
+    assert b"non-null" in lib.prnn_last_error()
+    rc = lib.prnn_slstm_init(None, None, None, None, 1, 1, 1, 0, 1e-6, 7, None, 0, None)
+    assert rc == _lib.PRNN_ERR_TYPE
+    with pytest.raises(TypeError):
+        _lib.check(rc, "x")
