@@ -239,3 +239,53 @@ def slstm_sequential(p: SLSTMParams, x: Tensor, h0: Tensor | None = None,
         state = slstm_step(p, state, wx[:, t])
         outs.append(state)
     return torch.stack(outs, dim=1)
+
+
+# ---- float64 evaluation of the same algorithm --------------------------------
+
+
+def frozen_gate_scan_f64(pre: Tensor, eps: float, h0: Tensor | None = None) -> Tensor:
+    """``frozen_gate_scan`` evaluated left to right in float64.
+
+    Same recurrence as the reference's frozen-gate pass (slstm_picard.py:51-107),
+    m_t = max(z_f + m_{t-1}, z_i) etc., without the fp32 cumsum: a float64
+    yardstick for how far any fp32 implementation (the reference's included)
+    is from the exact iterate.
+    """
+    q = pre.double()
+    bsz, d = q.shape[0], q.shape[-1] // 4
+    zi, zf, zz, zo = q.chunk(4, dim=-1)
+    if h0 is None:
+        c = n = m = q.new_zeros(bsz, d)
+    else:
+        g = h0.double()
+        c, n, m = g[:, C], g[:, N], g[:, M]
+    out = []
+    for t in range(q.shape[1]):
+        mn = torch.maximum(zf[:, t] + m, zi[:, t])
+        f = torch.exp(zf[:, t] + m - mn)
+        i = torch.exp(zi[:, t] - mn)
+        n = f * n + i
+        c = f * c + i * torch.tanh(zz[:, t])
+        m = mn
+        out.append(torch.stack((c, n, m, torch.sigmoid(zo[:, t]) * (c / (n + eps))), dim=-2))
+    return torch.stack(out, dim=1)
+
+
+def slstm_newton_f64(p: SLSTMParams, wx: Tensor, *, max_iters: int, picard_iters: int,
+                     omega: float = 1.0, h0: Tensor | None = None) -> Tensor:
+    """Alg. 1 at fixed K and P entirely in float64 (Picard passes included)."""
+    from oracle.scan import sequential_affine
+
+    p64 = SLSTMParams(p.W.double(), p.b.double(), p.R.double(), p.eps, p.cap)
+    wx = wx.double()
+    h0 = None if h0 is None else h0.double()
+    states = frozen_gate_scan_f64(wx, p.eps, h0)
+    for _ in range(picard_iters):
+        h_prev = prepend(states, h0)[..., H, :]
+        states = frozen_gate_scan_f64(_pre(p64, wx, h_prev), p.eps, h0)
+    init = states
+    for _ in range(max_iters):
+        pred, jac = slstm_jacobian(p64, prepend(states, h0), wx)
+        states = states + omega * sequential_affine(jac, pred - states, "block4")
+    return init, states

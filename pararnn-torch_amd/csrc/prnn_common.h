@@ -21,24 +21,24 @@ __device__ __forceinline__ float to_f32(bf16 v) {
   return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
 }
 
-// Round-to-nearest-even, NaN kept quiet (matches torch's float -> bfloat16).
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
-}
-
 template <typename T>
 __device__ __forceinline__ T from_f32(float v);
 template <>
 __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+// gfx950 converts with round-to-nearest-even in hardware (v_cvt_pk_bf16_f32).
 template <>
-__device__ __forceinline__ bf16 from_f32<bf16>(float v) { return bf16{f32_to_bf16_bits(v)}; }
+__device__ __forceinline__ bf16 from_f32<bf16>(float v) {
+  const __bf16 h = static_cast<__bf16>(v);
+  return bf16{__builtin_bit_cast(uint16_t, h)};
+}
 
 // Value after a round trip through storage type T (identity for fp32).
 template <typename T>
 __device__ __forceinline__ float round_to(float v) { return to_f32(from_f32<T>(v)); }
+template <>
+__device__ __forceinline__ float round_to<bf16>(float v) {
+  return static_cast<float>(static_cast<__bf16>(v));
+}
 
 template <typename T>
 __device__ __forceinline__ float ld(const T* p) { return to_f32(*p); }
@@ -65,36 +65,52 @@ __device__ __forceinline__ float ftanh(float x) {
 __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
 __device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
 
-// ---- decoupled look-back status words -------------------------------------
-// A status word holds (epoch << 2) | state.  The epoch is the index of the
-// launch within one solver call; the workspace is zeroed at the start of every
-// call, so a word left by an earlier launch of the same call (smaller epoch)
-// or by an earlier call (zeroed) never reads as ready.
-enum : int { kStatusAgg = 1, kStatusIncl = 2 };
+// ---- decoupled look-back ----------------------------------------------------
+// Cross-tile data moves through system-scope relaxed atomics, which the
+// compiler lowers to write-through / cache-bypassing (sc0 sc1) vector loads
+// and stores: a tile on one XCD sees another XCD's data without L2
+// write-back or invalidate, so a look-back hop costs one memory round trip.
+//
+// * Inclusive carries are "tagged words": 64-bit {float bits, tag} written
+//   and read as single atomic words.  A word whose tag equals the current
+//   epoch is valid; no separate flag or ordering is needed.
+// * Aggregates are published as plain fp32 payload, then (after the stores
+//   have completed, s_waitcnt) a status word set to the epoch.
+//
+// The epoch is the index of the launch within one solver call (>= 1).  The
+// status words and tagged words are cleared at the start of every call, so
+// nothing left by an earlier call or an earlier launch reads as valid.
 
-// Called by every lane of the publishing wave after its payload stores: the
-// release fence orders each lane's own stores, then lane 0 sets the word.
-__device__ __forceinline__ void publish(int* flag, int epoch, int state, int lane) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  if (lane == 0)
-    __hip_atomic_store(flag, (epoch << 2) | state, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void st_sys(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
-
-// Spin until the word carries this epoch; return its state.  Every tile that
-// is waited on has a smaller ticket than the waiter, so it is already resident
-// and finishes without waiting on the waiter: the spin always ends.
-__device__ __forceinline__ int wait_status(const int* flag, int epoch) {
-  int v;
-  while (true) {
-    v = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((v >> 2) == epoch) break;
-    __builtin_amdgcn_s_sleep(1);
-  }
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  return v & 3;
+__device__ __forceinline__ float ld_sys(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
+__device__ __forceinline__ void st_sys_int(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ int ld_sys_int(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void st_tagged(unsigned long long* p, float v, int tag) {
+  const unsigned long long w =
+      (static_cast<unsigned long long>(static_cast<uint32_t>(tag)) << 32) | __float_as_uint(v);
+  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+// True (and v set) when the word carries this tag.
+__device__ __forceinline__ bool ld_tagged(const unsigned long long* p, int tag, float& v) {
+  const unsigned long long w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  v = __uint_as_float(static_cast<uint32_t>(w));
+  return static_cast<int>(w >> 32) == tag;
+}
+// Wait until this lane's earlier stores have completed (vmcnt covers stores on gfx9).
+__device__ __forceinline__ void drain_stores() { __builtin_amdgcn_s_waitcnt(0); }
 
-// Payload loads after the acquire fence; plain loads are enough there.
-__device__ __forceinline__ float ld_payload(const float* p) { return *p; }
+// Publish an aggregate: call after the payload's st_sys stores.
+__device__ __forceinline__ void publish_agg(int* flag, int epoch, int lane) {
+  drain_stores();
+  if (lane == 0) st_sys_int(flag, epoch);
+}
 
 }  // namespace prnn

@@ -30,6 +30,9 @@
 #include "pararnn_amd.h"
 #include "prnn_host.h"
 
+#include <stdio.h>
+#include <stdlib.h>
+
 namespace prnn {
 namespace slstm {
 
@@ -55,6 +58,119 @@ __device__ __forceinline__ int take_ticket(int* counter) {
     s_ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   return s_ticket;
+}
+
+
+// ---------------------------------------------------------------------------
+// Windowed decoupled look-back.
+//
+// Called by every wave of a tile with chunk > 0 (it contains barriers).  Each
+// lane (channel) keeps its own position; in one round every wave w fetches
+// predecessor (position - w) for every lane -- W predecessors per memory round
+// trip -- and stages its status and payload in LDS; wave 0 then folds them in
+// nearest-first: an inclusive carry ends the walk, an aggregate is absorbed
+// and the walk continues, a predecessor with nothing published yet stops the
+// round (retried next round).  On return wave 0 holds the carry into the tile.
+//
+// Monoid policy M: NI inclusive values, NA aggregate values, Acc type with
+// identity / absorb (acc <- acc o agg of an earlier tile) / finish (carry =
+// acc applied to the inclusive value of that tile).
+// ---------------------------------------------------------------------------
+template <class M, int W>
+struct LookbackShared {
+  float pl[W][M::NA][kCB];
+  int st[W][kCB];
+  int pos[kCB];
+  int more;
+};
+
+template <class M, int W>
+__device__ __forceinline__ void windowed_lookback(const TileId& id, int B, int n_cb, int epoch,
+                                                  const int* __restrict__ flags,
+                                                  const unsigned long long* __restrict__ incl,
+                                                  const float* __restrict__ agg, int lane,
+                                                  int wave, LookbackShared<M, W>& sh,
+                                                  float carry[M::NI]) {
+  typename M::Acc acc;
+  M::identity(acc);
+  int pos = id.chunk - 1;  // wave 0: next predecessor chunk to examine
+  bool done = false;
+  const int per = B * n_cb;
+  int idle_rounds = 0;
+  while (true) {
+    if (wave == 0) sh.pos[lane] = done ? -1 : pos;
+    __syncthreads();
+    {
+      const int base = sh.pos[lane];
+      const int p = base - wave;
+      int st = 0;
+      if (base >= 0 && p >= 0) {
+        const size_t ptile = static_cast<size_t>(p) * per + id.rem;
+        const unsigned long long* ip = incl + ptile * M::NI * kCB + lane;
+        float v[M::NI];
+        bool ok = true;
+#pragma unroll
+        for (int k = 0; k < M::NI; ++k) ok = ld_tagged(ip + k * kCB, epoch, v[k]) && ok;
+        if (ok) {
+          st = 2;
+#pragma unroll
+          for (int k = 0; k < M::NI; ++k) sh.pl[wave][k][lane] = v[k];
+        } else if (ld_sys_int(flags + ptile) == epoch) {
+          st = 1;
+          const float* ap = agg + ptile * M::NA * kCB + lane;
+          float a[M::NA];
+#pragma unroll
+          for (int k = 0; k < M::NA; ++k) a[k] = ld_sys(ap + k * kCB);
+#pragma unroll
+          for (int k = 0; k < M::NA; ++k) sh.pl[wave][k][lane] = a[k];
+        }
+      }
+      sh.st[wave][lane] = st;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      bool progressed = false;
+      if (!done) {
+        bool stalled = false;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          if (!done && !stalled) {
+            const int st = sh.st[w][lane];
+            if (st == 2) {
+              float v[M::NI];
+#pragma unroll
+              for (int k = 0; k < M::NI; ++k) v[k] = sh.pl[w][k][lane];
+              M::finish(acc, v, carry);
+              done = true;
+              progressed = true;
+            } else if (st == 1) {
+              float a[M::NA];
+#pragma unroll
+              for (int k = 0; k < M::NA; ++k) a[k] = sh.pl[w][k][lane];
+              M::absorb(acc, a);
+              --pos;
+              progressed = true;
+            } else {
+              stalled = true;
+            }
+          }
+        }
+      }
+      const unsigned long long pending = __ballot(!done);
+      const unsigned long long moved = __ballot(progressed);
+      if (lane == 0) sh.more = pending != 0ull;
+      // Nothing new anywhere: back off before polling again.
+      idle_rounds = moved ? 0 : idle_rounds + 1;
+      if (pending && !moved) {
+        if (idle_rounds > 8)
+          __builtin_amdgcn_s_sleep(8);
+        else
+          __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    __syncthreads();
+    if (!sh.more) break;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -89,25 +205,48 @@ __device__ __forceinline__ void fg_apply(const FG& y, float& m, float& n, float&
 }
 
 // One frozen-gate step in place on (m, n, c); returns tanh-free readout pieces.
+// One of f, i is exactly e^0 = 1 (the larger exponent is the new stabiliser),
+// so a single exp of -|left - z_i| gives both, bit-identical to two exps.
 __device__ __forceinline__ void fg_step(float zi, float zf, float zz, float& m, float& n, float& c) {
   const float left = zf + m;
   const float mn = fmaxf(left, zi);
-  const float f = fexp(left - mn);
-  const float i = fexp(zi - mn);
+  const float e = fexp(-fabsf(left - zi));
+  const bool lf = left >= zi;
+  const float f = lf ? 1.f : e;
+  const float i = lf ? e : 1.f;
   const float z = ftanh(zz);
   n = f * n + i;
   c = f * c + i * z;
   m = mn;
 }
 
+
+struct FrozenMonoid {
+  static constexpr int NI = 3;  // carry (m, n, c)
+  static constexpr int NA = 4;  // aggregate (F, M, N, C)
+  using Acc = FG;
+  static __device__ __forceinline__ void identity(Acc& a) { a = fg_identity(); }
+  static __device__ __forceinline__ void absorb(Acc& acc, const float a[NA]) {
+    acc = fg_compose(FG{a[0], a[1], a[2], a[3]}, acc);
+  }
+  static __device__ __forceinline__ void finish(const Acc& acc, const float v[NI], float out[NI]) {
+    float m = v[0], n = v[1], c = v[2];
+    fg_apply(acc, m, n, c);
+    out[0] = m;
+    out[1] = n;
+    out[2] = c;
+  }
+};
+
 template <typename TX, int L, int W, bool HAS_H, bool FULL_OUT>
 __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
     const TX* __restrict__ hsrc, TX* __restrict__ out_full, TX* __restrict__ out_h, int B, int T,
     int d, int n_cb, float eps, int* __restrict__ counter, int* __restrict__ flags,
-    float* __restrict__ agg, float* __restrict__ incl, int epoch) {
+    float* __restrict__ agg, unsigned long long* __restrict__ incl, int epoch) {
   __shared__ float s_agg[W][4][kCB];
   __shared__ float s_carry[W][3][kCB];
+  __shared__ LookbackShared<FrozenMonoid, W> s_lb;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int tile = take_ticket(counter);
@@ -124,39 +263,36 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
     for (int g = 0; g < 4; ++g) r[g] = ld(rmix + g * d + ch);
   }
 
-  // Cache the frozen pre-activations of this lane's L steps.
-  float pre[L][4];
-#pragma unroll
-  for (int s = 0; s < L; ++s) {
-    const int t = t0 + s;
-    if (live && t < T) {
-      const size_t base = (static_cast<size_t>(id.b) * T + t) * row4 + ch;
-      float hp = 0.f;
-      if (HAS_H) {
-        if (t > 0)
-          hp = ld(hsrc + (static_cast<size_t>(id.b) * T + (t - 1)) * d + ch);
-        else if (h0 != nullptr)
-          hp = ld(h0 + static_cast<size_t>(id.b) * row4 + 3 * d + ch);
-      }
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float x = ld(wx + base + g * d);
-        // wx + R * h_prev, rounded to the storage dtype after each op.
-        pre[s][g] = HAS_H ? round_to<TX>(add_rn(x, round_to<TX>(mul_rn(r[g], hp)))) : x;
-      }
-    } else {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) pre[s][g] = 0.f;
+  // Frozen pre-activations of step t: wx (+ R * h_prev rounded like the
+  // reference's two torch ops).  Read in pass 1 and again in pass 2: the
+  // second read hits the caches, which keeps registers free for occupancy and
+  // lets a tile span many steps (fewer look-back hops).
+  auto load_pre = [&](int t, float pre[4]) {
+    const size_t base = (static_cast<size_t>(id.b) * T + t) * row4 + ch;
+    float hp = 0.f;
+    if (HAS_H) {
+      if (t > 0)
+        hp = ld(hsrc + (static_cast<size_t>(id.b) * T + (t - 1)) * d + ch);
+      else if (h0 != nullptr)
+        hp = ld(h0 + static_cast<size_t>(id.b) * row4 + 3 * d + ch);
     }
-  }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float x = ld(wx + base + g * d);
+      pre[g] = HAS_H ? round_to<TX>(add_rn(x, round_to<TX>(mul_rn(r[g], hp)))) : x;
+    }
+  };
+  const int t_end = min(t0 + L, T);
 
   // Pass 1: segment aggregate from the empty state (m = -inf, n = c = 0).
   FG a = fg_identity();
-#pragma unroll
-  for (int s = 0; s < L; ++s) {
-    if (t0 + s < T) {
-      a.F += pre[s][1];
-      fg_step(pre[s][0], pre[s][1], pre[s][2], a.M, a.N, a.C);
+  if (live) {
+#pragma unroll 8
+    for (int t = t0; t < t_end; ++t) {
+      float pre[4];
+      load_pre(t, pre);
+      a.F += pre[1];
+      fg_step(pre[0], pre[1], pre[2], a.M, a.N, a.C);
     }
   }
   s_agg[wave][0][lane] = a.F;
@@ -165,76 +301,60 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
   s_agg[wave][3][lane] = a.C;
   __syncthreads();
 
+  float carry[3] = {0.f, 0.f, 0.f};  // (m, n, c) into the tile, wave 0
   if (wave == 0) {
-    FG seg[W];
+    FG tile_agg = fg_identity();
 #pragma unroll
     for (int w = 0; w < W; ++w)
-      seg[w] = FG{s_agg[w][0][lane], s_agg[w][1][lane], s_agg[w][2][lane], s_agg[w][3][lane]};
-    FG tile_agg = seg[0];
-#pragma unroll
-    for (int w = 1; w < W; ++w) tile_agg = fg_compose(tile_agg, seg[w]);
-
-    // Carry into the tile.
-    float m = 0.f, n = 0.f, c = 0.f;
+      tile_agg = fg_compose(
+          tile_agg, FG{s_agg[w][0][lane], s_agg[w][1][lane], s_agg[w][2][lane], s_agg[w][3][lane]});
     if (id.chunk == 0) {
       if (h0 != nullptr && live) {
         const TX* hb = h0 + static_cast<size_t>(id.b) * row4 + ch;
-        c = ld(hb);
-        n = ld(hb + d);
-        m = ld(hb + 2 * d);
+        carry[2] = ld(hb);
+        carry[1] = ld(hb + d);
+        carry[0] = ld(hb + 2 * d);
       }
     } else {
       float* ap = agg + (static_cast<size_t>(tile) * 4) * kCB + lane;
-      ap[0 * kCB] = tile_agg.F;
-      ap[1 * kCB] = tile_agg.M;
-      ap[2 * kCB] = tile_agg.N;
-      ap[3 * kCB] = tile_agg.C;
-      publish(flags + tile, epoch, kStatusAgg, lane);
-      FG acc = fg_identity();
-      int pc = id.chunk - 1;
-      while (true) {
-        const int ptile = pc * (B * n_cb) + id.rem;
-        const int st = wait_status(flags + ptile, epoch);
-        if (st == kStatusIncl) {
-          const float* ip = incl + (static_cast<size_t>(ptile) * 3) * kCB + lane;
-          m = ld_payload(ip);
-          n = ld_payload(ip + kCB);
-          c = ld_payload(ip + 2 * kCB);
-          fg_apply(acc, m, n, c);
-          break;
-        }
-        const float* pp = agg + (static_cast<size_t>(ptile) * 4) * kCB + lane;
-        const FG pa{ld_payload(pp), ld_payload(pp + kCB), ld_payload(pp + 2 * kCB),
-                    ld_payload(pp + 3 * kCB)};
-        acc = fg_compose(pa, acc);
-        --pc;
-      }
+      st_sys(ap + 0 * kCB, tile_agg.F);
+      st_sys(ap + 1 * kCB, tile_agg.M);
+      st_sys(ap + 2 * kCB, tile_agg.N);
+      st_sys(ap + 3 * kCB, tile_agg.C);
+      publish_agg(flags + tile, epoch, lane);
     }
+  }
+  if (id.chunk > 0)
+    windowed_lookback<FrozenMonoid, W>(id, B, n_cb, epoch, flags, incl, agg, lane, wave, s_lb,
+                                       carry);
+  if (wave == 0) {
     // Per-wave carries, then the tile's inclusive carry.
+    float m = carry[0], n = carry[1], c = carry[2];
 #pragma unroll
     for (int w = 0; w < W; ++w) {
       s_carry[w][0][lane] = m;
       s_carry[w][1][lane] = n;
       s_carry[w][2][lane] = c;
-      fg_apply(seg[w], m, n, c);
+      fg_apply(FG{s_agg[w][0][lane], s_agg[w][1][lane], s_agg[w][2][lane], s_agg[w][3][lane]}, m,
+               n, c);
     }
-    float* ip = incl + (static_cast<size_t>(tile) * 3) * kCB + lane;
-    ip[0] = m;
-    ip[kCB] = n;
-    ip[2 * kCB] = c;
-    publish(flags + tile, epoch, kStatusIncl, lane);
+    unsigned long long* ip = incl + (static_cast<size_t>(tile) * 3) * kCB + lane;
+    st_tagged(ip, m, epoch);
+    st_tagged(ip + kCB, n, epoch);
+    st_tagged(ip + 2 * kCB, c, epoch);
   }
   __syncthreads();
 
   // Pass 2: replay with the true carry and stream the trajectory.
   float m = s_carry[wave][0][lane], n = s_carry[wave][1][lane], c = s_carry[wave][2][lane];
-#pragma unroll
-  for (int s = 0; s < L; ++s) {
-    const int t = t0 + s;
-    if (live && t < T) {
-      fg_step(pre[s][0], pre[s][1], pre[s][2], m, n, c);
-      const float o = fsigmoid(pre[s][3]);
-      const float h = o * (c * frcp(n + eps));
+  if (live) {
+#pragma unroll 8
+    for (int t = t0; t < t_end; ++t) {
+      float pre[4];
+      load_pre(t, pre);
+      fg_step(pre[0], pre[1], pre[2], m, n, c);
+      // h = sigmoid(z_o) c / (n + eps) with one reciprocal.
+      const float h = c * frcp((1.f + fexp(-pre[3])) * (n + eps));
       if (FULL_OUT) {
         TX* op = out_full + (static_cast<size_t>(id.b) * T + t) * row4 + ch;
         st(op, c);
@@ -271,8 +391,10 @@ __device__ __forceinline__ CellJ cell_jac(const float prev[4], const float x[4],
   const float mn = fmaxf(left, zi);
   // d max(left, z_i) / d left, ties split 0.5 / 0.5 (para_slstm.py:530-534).
   const float al = left > zi ? 1.f : (left == zi ? 0.5f : 0.f);
-  const float i = fexp(zi - mn);
-  const float f = fexp(left - mn);
+  const float e = fexp(-fabsf(left - zi));  // the smaller of the two gate exponents
+  const bool lf = left >= zi;
+  const float f = lf ? 1.f : e;
+  const float i = lf ? e : 1.f;
   const float z = ftanh(zz);
   const float nn = f * n + i;
   const float cn = f * c + i * z;
@@ -365,14 +487,38 @@ __device__ __forceinline__ void aff_apply(const Aff& a, float v[4]) {
   for (int i = 0; i < 4; ++i) v[i] = o[i];
 }
 
+
+struct NewtonMonoid {
+  static constexpr int NI = 4;   // carry delta (c, n, m, h)
+  static constexpr int NA = 20;  // aggregate A (16, row major) then b (4)
+  using Acc = Aff;
+  static __device__ __forceinline__ void identity(Acc& a) { aff_identity(a); }
+  static __device__ __forceinline__ void absorb(Acc& acc, const float v[NA]) {
+    Aff pa;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pa.b[i] = v[16 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pa.A[i][j] = v[4 * i + j];
+    }
+    acc = aff_compose(pa, acc);
+  }
+  static __device__ __forceinline__ void finish(const Acc& acc, const float v[NI], float out[NI]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) out[k] = v[k];
+    aff_apply(acc, out);
+  }
+};
+
 template <typename TX, typename TIN, typename TOUT, int L, int W>
 __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
     const TIN* __restrict__ hin, TOUT* __restrict__ hout, int B, int T, int d, int n_cb,
     float omega, float eps, int* __restrict__ counter, int* __restrict__ flags,
-    float* __restrict__ agg, float* __restrict__ incl, int epoch) {
+    float* __restrict__ agg, unsigned long long* __restrict__ incl, int epoch) {
   __shared__ float s_agg[W][20][kCB];
   __shared__ float s_carry[W][4][kCB];
+  __shared__ LookbackShared<NewtonMonoid, W> s_lb;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int tile = take_ticket(counter);
@@ -400,46 +546,42 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
       for (int k = 0; k < 4; ++k) prev0[k] = ld(p + k * d);
     }
   }
-  float xs[L][4], hs[L][4];
+  // Inputs of step t are read in pass 1 and again in pass 2 (the second read
+  // hits the caches); nothing is held in registers across the look-back.
+  auto load_step = [&](int t, float x[4], float hv[4]) {
+    const size_t base = (static_cast<size_t>(id.b) * T + t) * row4 + ch;
 #pragma unroll
-  for (int s = 0; s < L; ++s) {
-    const int t = t0 + s;
-    if (live && t < T) {
-      const size_t base = (static_cast<size_t>(id.b) * T + t) * row4 + ch;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        xs[s][k] = ld(wx + base + k * d);
-        hs[s][k] = ld(hin + base + k * d);
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) xs[s][k] = hs[s][k] = 0.f;
+    for (int k = 0; k < 4; ++k) {
+      x[k] = ld(wx + base + k * d);
+      hv[k] = ld(hin + base + k * d);
     }
-  }
+  };
+  const int t_end = min(t0 + L, T);
 
   // Pass 1: lane segment aggregate (A, b) of the affine maps x -> J x + F.
   Aff a;
   aff_identity(a);
-  {
+  if (live) {
     float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
+#pragma unroll 4
+    for (int t = t0; t < t_end; ++t) {
+      float x[4], hv[4];
+      load_step(t, x, hv);
+      const CellJ J = cell_jac(prev, x, r, eps);
+      jmv(J, a.b);
+      a.b[0] += J.pc - hv[0];
+      a.b[1] += J.pn - hv[1];
+      a.b[2] += J.pm - hv[2];
+      a.b[3] += J.ph - hv[3];
 #pragma unroll
-    for (int s = 0; s < L; ++s) {
-      if (t0 + s < T) {
-        const CellJ J = cell_jac(prev, xs[s], r, eps);
-        const float F[4] = {J.pc - hs[s][0], J.pn - hs[s][1], J.pm - hs[s][2], J.ph - hs[s][3]};
-        jmv(J, a.b);
+      for (int j = 0; j < 4; ++j) {
+        float col[4] = {a.A[0][j], a.A[1][j], a.A[2][j], a.A[3][j]};
+        jmv(J, col);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) a.b[k] += F[k];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float col[4] = {a.A[0][j], a.A[1][j], a.A[2][j], a.A[3][j]};
-          jmv(J, col);
-#pragma unroll
-          for (int k = 0; k < 4; ++k) a.A[k][j] = col[k];
-        }
+        for (int k = 0; k < 4; ++k) a.A[k][j] = col[k];
       }
 #pragma unroll
-      for (int k = 0; k < 4; ++k) prev[k] = hs[s][k];
+      for (int k = 0; k < 4; ++k) prev[k] = hv[k];
     }
   }
 #pragma unroll
@@ -450,7 +592,8 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
   }
   __syncthreads();
 
-  if (wave == 0) {
+  float carry[4] = {0.f, 0.f, 0.f, 0.f};  // delta into the tile (delta_{-1} = 0), wave 0
+  if (wave == 0 && id.chunk > 0) {
     Aff tile_agg;
     aff_identity(tile_agg);
 #pragma unroll
@@ -464,42 +607,19 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
       }
       tile_agg = w == 0 ? sw : aff_compose(tile_agg, sw);
     }
-    float carry[4] = {0.f, 0.f, 0.f, 0.f};  // delta_{-1} = 0
-    if (id.chunk > 0) {
-      float* ap = agg + (static_cast<size_t>(tile) * 20) * kCB + lane;
+    float* ap = agg + (static_cast<size_t>(tile) * 20) * kCB + lane;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        ap[(16 + i) * kCB] = tile_agg.b[i];
+    for (int i = 0; i < 4; ++i) {
+      st_sys(ap + (16 + i) * kCB, tile_agg.b[i]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ap[(4 * i + j) * kCB] = tile_agg.A[i][j];
-      }
-      publish(flags + tile, epoch, kStatusAgg, lane);
-      // acc maps the carry out of predecessor tile pc to the carry into this tile.
-      Aff acc;
-      aff_identity(acc);
-      int pc = id.chunk - 1;
-      while (true) {
-        const int ptile = pc * (B * n_cb) + id.rem;
-        const int st = wait_status(flags + ptile, epoch);
-        if (st == kStatusIncl) {
-          const float* ip = incl + (static_cast<size_t>(ptile) * 4) * kCB + lane;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) carry[k] = ld_payload(ip + k * kCB);
-          aff_apply(acc, carry);
-          break;
-        }
-        const float* pp = agg + (static_cast<size_t>(ptile) * 20) * kCB + lane;
-        Aff pa;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pa.b[i] = ld_payload(pp + (16 + i) * kCB);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) pa.A[i][j] = ld_payload(pp + (4 * i + j) * kCB);
-        }
-        acc = aff_compose(pa, acc);
-        --pc;
-      }
+      for (int j = 0; j < 4; ++j) st_sys(ap + (4 * i + j) * kCB, tile_agg.A[i][j]);
     }
+    publish_agg(flags + tile, epoch, lane);
+  }
+  if (id.chunk > 0)
+    windowed_lookback<NewtonMonoid, W>(id, B, n_cb, epoch, flags, incl, agg, lane, wave, s_lb,
+                                       carry);
+  if (wave == 0) {
     // Carry into each wave's segment, then the tile's outgoing carry.
 #pragma unroll
     for (int w = 0; w < W; ++w) {
@@ -514,10 +634,9 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
       }
       aff_apply(sw, carry);
     }
-    float* ip = incl + (static_cast<size_t>(tile) * 4) * kCB + lane;
+    unsigned long long* ip = incl + (static_cast<size_t>(tile) * 4) * kCB + lane;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) ip[k * kCB] = carry[k];
-    publish(flags + tile, epoch, kStatusIncl, lane);
+    for (int k = 0; k < 4; ++k) st_tagged(ip + k * kCB, carry[k], epoch);
   }
   __syncthreads();
 
@@ -525,23 +644,24 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
   float dl[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) dl[k] = s_carry[wave][k][lane];
-  float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
-#pragma unroll
-  for (int s = 0; s < L; ++s) {
-    const int t = t0 + s;
-    if (live && t < T) {
-      const CellJ J = cell_jac(prev, xs[s], r, eps);
+  if (live) {
+    float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
+#pragma unroll 4
+    for (int t = t0; t < t_end; ++t) {
+      float x[4], hv[4];
+      load_step(t, x, hv);
+      const CellJ J = cell_jac(prev, x, r, eps);
       jmv(J, dl);
-      dl[0] += J.pc - hs[s][0];
-      dl[1] += J.pn - hs[s][1];
-      dl[2] += J.pm - hs[s][2];
-      dl[3] += J.ph - hs[s][3];
+      dl[0] += J.pc - hv[0];
+      dl[1] += J.pn - hv[1];
+      dl[2] += J.pm - hv[2];
+      dl[3] += J.ph - hv[3];
       TOUT* op = hout + (static_cast<size_t>(id.b) * T + t) * row4 + ch;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) st(op + k * d, add_rn(hs[s][k], mul_rn(omega, dl[k])));
-    }
+      for (int k = 0; k < 4; ++k) st(op + k * d, add_rn(hv[k], mul_rn(omega, dl[k])));
 #pragma unroll
-    for (int k = 0; k < 4; ++k) prev[k] = hs[s][k];
+      for (int k = 0; k < 4; ++k) prev[k] = hv[k];
+    }
   }
 }
 
@@ -554,18 +674,46 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
 namespace prnn {
 namespace slstm {
 
-constexpr int kFrozenL = 16, kFrozenW = 4;  // frozen-gate tile: 64 ch x 64 steps
-constexpr int kNewtonL = 16, kNewtonW = 4;  // Newton tile:      64 ch x 64 steps
-constexpr int kMaxStages = 64;              // ticket counters per call
+constexpr int kMaxStages = 64;  // ticket counters per call
+
+// Tile shapes (L steps per lane x W waves).  Selected once per process;
+// PRNN_SLSTM_TILES="<frozen L>x<W>,<newton L>x<W>" overrides the default for
+// tuning runs (only the instantiated shapes are accepted).
+struct Shape {
+  int L, W;
+};
+static const Shape kFrozenShapes[] = {{64, 4}, {32, 8}, {128, 4}, {64, 8}};
+static const Shape kNewtonShapes[] = {{64, 4}, {32, 8}, {128, 4}, {32, 4}};
+
+struct Tiles {
+  Shape frozen, newton;
+};
+
+static Tiles tiles() {
+  static Tiles t = [] {
+    Tiles r{{64, 4}, {64, 4}};
+    if (const char* e = getenv("PRNN_SLSTM_TILES")) {
+      int fl, fw, nl, nw;
+      if (sscanf(e, "%dx%d,%dx%d", &fl, &fw, &nl, &nw) == 4) {
+        for (const Shape& s : kFrozenShapes)
+          if (s.L == fl && s.W == fw) r.frozen = s;
+        for (const Shape& s : kNewtonShapes)
+          if (s.L == nl && s.W == nw) r.newton = s;
+      }
+    }
+    return r;
+  }();
+  return t;
+}
 
 struct Geo {
   int n_cb, n_chunks, n_tiles;
 };
 
-static Geo geometry(int B, int T, int d, int chunk) {
+static Geo geometry(int B, int T, int d, Shape sh) {
   Geo g;
   g.n_cb = (d + kCB - 1) / kCB;
-  g.n_chunks = (T + chunk - 1) / chunk;
+  g.n_chunks = (T + sh.L * sh.W - 1) / (sh.L * sh.W);
   g.n_tiles = B * g.n_cb * g.n_chunks;
   return g;
 }
@@ -577,28 +725,45 @@ static int check_dims(int B, int T, int d, int dtype) {
     return fail(PRNN_ERR_VALUE, "B, T, d must be >= 1, got B=%d T=%d d=%d", B, T, d);
   if (dtype != PRNN_F32 && dtype != PRNN_BF16)
     return fail(PRNN_ERR_TYPE, "dtype code %d is not float32 (0) or bfloat16 (1)", dtype);
-  const long long tiles = static_cast<long long>(B) * ((d + kCB - 1) / kCB) * ((T + 63) / 64);
-  if (tiles > (1ll << 28))
-    return fail(PRNN_ERR_VALUE, "problem too large: %lld tiles", tiles);
+  const long long tiles = static_cast<long long>(B) * ((d + kCB - 1) / kCB) * T;
+  if (tiles > (1ll << 30))
+    return fail(PRNN_ERR_VALUE, "problem too large: B*T*ceil(d/64) = %lld", tiles);
   return PRNN_OK;
 }
 
-struct InitWs {
+// Look-back state shared by the launches of one call.  Layout:
+//   counters[kMaxStages] | status words[n_tiles] | tagged carries | aggregates
+// The first three are cleared by one kernel at the start of the call.
+struct Lookback {
   int* counters;
   int* flags;
+  unsigned long long* incl;
   float* agg;
-  float* incl;
+  size_t clear_words;
+};
+
+static Lookback carve_lookback(Carver& cv, const Geo& g, int incl_vals, int agg_vals) {
+  Lookback lb;
+  lb.counters = static_cast<int*>(cv.take(sizeof(int) * kMaxStages));
+  lb.flags = static_cast<int*>(cv.take(sizeof(int) * g.n_tiles));
+  lb.incl = static_cast<unsigned long long*>(
+      cv.take(sizeof(unsigned long long) * incl_vals * kCB * g.n_tiles));
+  const size_t end = cv.used;
+  lb.agg = static_cast<float*>(cv.take(sizeof(float) * agg_vals * kCB * g.n_tiles));
+  lb.clear_words = (end - (reinterpret_cast<char*>(lb.counters) - cv.base)) / sizeof(int);
+  return lb;
+}
+
+struct InitWs {
+  Lookback lb;
   void* hbuf[2];
 };
 
 static InitWs carve_init(void* base, int B, int T, int d, int P, int dtype, size_t* total) {
-  const Geo g = geometry(B, T, d, kFrozenL * kFrozenW);
+  const Geo g = geometry(B, T, d, tiles().frozen);
   Carver cv(base);
   InitWs w;
-  w.counters = static_cast<int*>(cv.take(sizeof(int) * kMaxStages));
-  w.flags = static_cast<int*>(cv.take(sizeof(int) * g.n_tiles));
-  w.agg = static_cast<float*>(cv.take(sizeof(float) * 4 * kCB * g.n_tiles));
-  w.incl = static_cast<float*>(cv.take(sizeof(float) * 3 * kCB * g.n_tiles));
+  w.lb = carve_lookback(cv, g, 3, 4);
   const size_t hb = static_cast<size_t>(B) * T * d * elem_size(dtype);
   w.hbuf[0] = P >= 1 ? cv.take(hb) : nullptr;
   w.hbuf[1] = P >= 2 ? cv.take(hb) : nullptr;
@@ -607,21 +772,15 @@ static InitWs carve_init(void* base, int B, int T, int d, int P, int dtype, size
 }
 
 struct NewtonWs {
-  int* counters;
-  int* flags;
-  float* agg;
-  float* incl;
+  Lookback lb;
   float* work[2];
 };
 
 static NewtonWs carve_newton(void* base, int B, int T, int d, int K, size_t* total) {
-  const Geo g = geometry(B, T, d, kNewtonL * kNewtonW);
+  const Geo g = geometry(B, T, d, tiles().newton);
   Carver cv(base);
   NewtonWs w;
-  w.counters = static_cast<int*>(cv.take(sizeof(int) * kMaxStages));
-  w.flags = static_cast<int*>(cv.take(sizeof(int) * g.n_tiles));
-  w.agg = static_cast<float*>(cv.take(sizeof(float) * 20 * kCB * g.n_tiles));
-  w.incl = static_cast<float*>(cv.take(sizeof(float) * 4 * kCB * g.n_tiles));
+  w.lb = carve_lookback(cv, g, 4, 20);
   const size_t wb = static_cast<size_t>(B) * T * 4 * d * sizeof(float);
   w.work[0] = K >= 2 ? static_cast<float*>(cv.take(wb)) : nullptr;
   w.work[1] = K >= 3 ? static_cast<float*>(cv.take(wb)) : nullptr;
@@ -629,50 +788,82 @@ static NewtonWs carve_newton(void* base, int B, int T, int d, int K, size_t* tot
   return w;
 }
 
+template <typename TX, int L, int W>
+static void launch_frozen(bool has_h, bool full_out, const TX* wx, const TX* r, const TX* h0,
+                          const TX* src, TX* out_full, TX* out_h, int B, int T, int d, float eps,
+                          const Lookback& lb, int epoch, hipStream_t stream) {
+  const Geo g = geometry(B, T, d, Shape{L, W});
+  const dim3 grid(g.n_tiles), block(64 * W);
+  int* ctr = lb.counters + epoch;
+#define PRNN_FROZEN(HH, FO)                                                                    \
+  slstm_frozen_kernel<TX, L, W, HH, FO><<<grid, block, 0, stream>>>(                           \
+      wx, r, h0, src, out_full, out_h, B, T, d, g.n_cb, eps, ctr, lb.flags, lb.agg, lb.incl, \
+      epoch)
+  if (has_h) {
+    if (full_out) PRNN_FROZEN(true, true); else PRNN_FROZEN(true, false);
+  } else {
+    if (full_out) PRNN_FROZEN(false, true); else PRNN_FROZEN(false, false);
+  }
+#undef PRNN_FROZEN
+}
+
+template <typename TX>
+static void frozen_pass(bool has_h, bool full_out, const TX* wx, const TX* r, const TX* h0,
+                        const TX* src, TX* out_full, TX* out_h, int B, int T, int d, float eps,
+                        const Lookback& lb, int epoch, hipStream_t stream) {
+  const Shape sh = tiles().frozen;
+#define PRNN_SHAPE(LL, WW)                                                                   \
+  if (sh.L == LL && sh.W == WW)                                                              \
+    return launch_frozen<TX, LL, WW>(has_h, full_out, wx, r, h0, src, out_full, out_h, B, T, \
+                                     d, eps, lb, epoch, stream);
+  PRNN_SHAPE(64, 4)
+  PRNN_SHAPE(32, 8)
+  PRNN_SHAPE(128, 4)
+  PRNN_SHAPE(64, 8)
+#undef PRNN_SHAPE
+}
+
 template <typename TX>
 static int run_init(const TX* wx, const TX* r, const TX* h0, TX* states, int B, int T, int d,
                     int P, float eps, const InitWs& w, hipStream_t stream) {
-  const Geo g = geometry(B, T, d, kFrozenL * kFrozenW);
-  const dim3 grid(g.n_tiles), block(64 * kFrozenW);
-  int rc = clear_words(w.counters, kMaxStages + (g.n_tiles + 63) / 64 * 64, stream);
+  int rc = clear_words(w.lb.counters, w.lb.clear_words, stream);
   if (rc != PRNN_OK) return rc;
-  // Pass 0: zero-hidden scan (pre = wx).
-  if (P == 0) {
-    slstm_frozen_kernel<TX, kFrozenL, kFrozenW, false, true><<<grid, block, 0, stream>>>(
-        wx, r, h0, nullptr, states, nullptr, B, T, d, g.n_cb, eps, w.counters + 1, w.flags,
-        w.agg, w.incl, 1);
-  } else {
-    slstm_frozen_kernel<TX, kFrozenL, kFrozenW, false, false><<<grid, block, 0, stream>>>(
-        wx, r, h0, nullptr, nullptr, static_cast<TX*>(w.hbuf[0]), B, T, d, g.n_cb, eps,
-        w.counters + 1, w.flags, w.agg, w.incl, 1);
-  }
-  PRNN_HIP(hipGetLastError());
-  for (int p = 1; p <= P; ++p) {
-    const TX* src = static_cast<const TX*>(w.hbuf[(p - 1) & 1]);
-    const int epoch = p + 1;
-    if (p == P) {
-      slstm_frozen_kernel<TX, kFrozenL, kFrozenW, true, true><<<grid, block, 0, stream>>>(
-          wx, r, h0, src, states, nullptr, B, T, d, g.n_cb, eps, w.counters + epoch, w.flags,
-          w.agg, w.incl, epoch);
-    } else {
-      slstm_frozen_kernel<TX, kFrozenL, kFrozenW, true, false><<<grid, block, 0, stream>>>(
-          wx, r, h0, src, nullptr, static_cast<TX*>(w.hbuf[p & 1]), B, T, d, g.n_cb, eps,
-          w.counters + epoch, w.flags, w.agg, w.incl, epoch);
-    }
+  // Pass 0: zero-hidden scan (pre = wx); passes 1..P freeze wx + R h_prev.
+  for (int p = 0; p <= P; ++p) {
+    const TX* src = p == 0 ? nullptr : static_cast<const TX*>(w.hbuf[(p - 1) & 1]);
+    const bool last = p == P;
+    TX* out_h = last ? nullptr : static_cast<TX*>(w.hbuf[p & 1]);
+    frozen_pass<TX>(p > 0, last, wx, r, h0, src, last ? states : nullptr, out_h, B, T, d, eps,
+                    w.lb, p + 1, stream);
     PRNN_HIP(hipGetLastError());
   }
   return PRNN_OK;
 }
 
+template <typename TX, typename TIN, typename TOUT, int L, int W>
+static void launch_newton_shape(const TX* wx, const TX* r, const TX* h0, const TIN* hin,
+                                TOUT* hout, int B, int T, int d, float omega, float eps,
+                                const Lookback& lb, int epoch, hipStream_t stream) {
+  const Geo g = geometry(B, T, d, Shape{L, W});
+  slstm_newton_kernel<TX, TIN, TOUT, L, W><<<dim3(g.n_tiles), dim3(64 * W), 0, stream>>>(
+      wx, r, h0, hin, hout, B, T, d, g.n_cb, omega, eps, lb.counters + epoch, lb.flags, lb.agg,
+      lb.incl, epoch);
+}
+
 template <typename TX, typename TIN, typename TOUT>
 static void launch_newton(const TX* wx, const TX* r, const TX* h0, const TIN* hin, TOUT* hout,
-                          int B, int T, int d, float omega, float eps, const NewtonWs& w,
+                          int B, int T, int d, float omega, float eps, const Lookback& lb,
                           int epoch, hipStream_t stream) {
-  const Geo g = geometry(B, T, d, kNewtonL * kNewtonW);
-  slstm_newton_kernel<TX, TIN, TOUT, kNewtonL, kNewtonW>
-      <<<dim3(g.n_tiles), dim3(64 * kNewtonW), 0, stream>>>(
-          wx, r, h0, hin, hout, B, T, d, g.n_cb, omega, eps, w.counters + epoch, w.flags, w.agg,
-          w.incl, epoch);
+  const Shape sh = tiles().newton;
+#define PRNN_SHAPE(LL, WW)                                                                     \
+  if (sh.L == LL && sh.W == WW)                                                                \
+    return launch_newton_shape<TX, TIN, TOUT, LL, WW>(wx, r, h0, hin, hout, B, T, d, omega, eps, \
+                                                      lb, epoch, stream);
+  PRNN_SHAPE(64, 4)
+  PRNN_SHAPE(32, 8)
+  PRNN_SHAPE(128, 4)
+  PRNN_SHAPE(32, 4)
+#undef PRNN_SHAPE
 }
 
 template <typename TX>
@@ -684,21 +875,20 @@ static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, 
                             hipMemcpyDeviceToDevice, stream));
     return PRNN_OK;
   }
-  const Geo g = geometry(B, T, d, kNewtonL * kNewtonW);
-  int rc = clear_words(w.counters, kMaxStages + (g.n_tiles + 63) / 64 * 64, stream);
+  int rc = clear_words(w.lb.counters, w.lb.clear_words, stream);
   if (rc != PRNN_OK) return rc;
   for (int k = 1; k <= K; ++k) {
     const bool first = k == 1, last = k == K;
     const float* win = first ? nullptr : w.work[(k - 2) & 1];
     float* wout = last ? nullptr : w.work[(k - 1) & 1];
     if (first && last)
-      launch_newton<TX, TX, TX>(wx, r, h0, guess, out, B, T, d, omega, eps, w, k, stream);
+      launch_newton<TX, TX, TX>(wx, r, h0, guess, out, B, T, d, omega, eps, w.lb, k, stream);
     else if (first)
-      launch_newton<TX, TX, float>(wx, r, h0, guess, wout, B, T, d, omega, eps, w, k, stream);
+      launch_newton<TX, TX, float>(wx, r, h0, guess, wout, B, T, d, omega, eps, w.lb, k, stream);
     else if (last)
-      launch_newton<TX, float, TX>(wx, r, h0, win, out, B, T, d, omega, eps, w, k, stream);
+      launch_newton<TX, float, TX>(wx, r, h0, win, out, B, T, d, omega, eps, w.lb, k, stream);
     else
-      launch_newton<TX, float, float>(wx, r, h0, win, wout, B, T, d, omega, eps, w, k, stream);
+      launch_newton<TX, float, float>(wx, r, h0, win, wout, B, T, d, omega, eps, w.lb, k, stream);
     PRNN_HIP(hipGetLastError());
   }
   return PRNN_OK;
