@@ -1,0 +1,221 @@
+"""Benchmark of the fused Newton + scan forward (one MI355X).
+
+Workload (the one the metric names): ParaSLSTM mix='diag',
+d=1024, B=1, T=131072, bf16, K=2 Newton iterations, P=5 Picard passes,
+x ~ N(0, 0.5) seeded, default seeded init.  A step is one solve on one batch
+with ``wx = W_x(x)`` already resident in HBM: the zero-hidden pass, P Picard
+passes and K Newton iterations (8 kernel launches plus two status clears).
+The W_x GEMM and the end-to-end ``newton_apply`` (GEMM + solve) are timed
+separately and reported as extra fields.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Prints one JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(REPO, "pararnn-torch_amd"), REPO]
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor peak
+D, B, T, K, P = 1024, 1, 131072, 2, 5
+
+
+def _events(torch):
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def _time(torch, fn, reps, warm=2):
+    """Average ms per call of fn(), HIP events on the current stream."""
+    for _ in range(warm):
+        fn()
+    s, e = _events(torch)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def _traffic_from_profile(name: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (committed summary)."""
+    path = os.path.join(REPO, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(torch, t_sample: int):
+    """The CPU oracle (the reference's eager algorithm restated) on a bounded
+    sample: the same cell and K, P at T = t_sample, all 1024 channels."""
+    import oracle as O
+    from pararnn_amd import ParaSLSTM
+
+    torch.manual_seed(0)
+    cell = ParaSLSTM(D, D).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(1)
+    x = (torch.randn(1, t_sample, D, generator=g) * 0.5).to(torch.bfloat16)
+    p = O.SLSTMParams(cell.W_x.weight.detach(), cell.W_x.bias.detach(), cell.R.detach())
+    with torch.no_grad():
+        wx = p.wx(x)
+        t0 = time.perf_counter()
+        O.slstm_newton(p, None, max_iters=K, picard_iters=P, wx=wx, work="fused")
+        dt = time.perf_counter() - t0
+    return {
+        "value": t_sample / dt,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"oracle Picard init (P={P}) + K={K} Newton, B=1, T={t_sample}, d={D}, bf16 "
+                  f"(fused-op semantics), {dt:.2f} s",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-sample", type=int, default=32768)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device copy (for rocprofv3 --pmc byte scaling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
+              f"got --gpus {args.gpus}", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if args.copy_calibration:
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda:0")  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2}))
+        return 0
+
+    from pararnn_amd import NewtonConfig, ParaSLSTM, fused_newton, newton_apply, slstm_init_fused
+
+    dev = "cuda:0"
+    torch.manual_seed(0)
+    cell = ParaSLSTM(D, D).to(dev, torch.bfloat16)
+    g = torch.Generator(device=dev).manual_seed(1)
+    x = (torch.randn(B, T, D, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    tokens = B * T
+    with torch.no_grad():
+        wx = cell.W_x(x)
+        r = cell.clipped_r()
+
+        def step():
+            return fused_newton(cell, wx, max_iters=K, omega=1.0, h0=None, picard_iters=P)
+
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        s, e = _events(torch)
+        s.record()
+        t_wall = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        e.record()
+        torch.cuda.synchronize()
+        t_wall = time.perf_counter() - t_wall
+        ms = s.elapsed_time(e) / args.steps
+
+        # Per-kernel launch durations (each call adds one ~10 us status clear,
+        # which cancels in the differences).
+        reps = max(5, args.steps // 2)
+        init = slstm_init_fused(wx, r, None, picard_iters=P, eps=cell.eps)
+        ms_init1 = _time(torch, lambda: slstm_init_fused(wx, r, None, picard_iters=1, eps=cell.eps), reps)
+        ms_initP = _time(torch, lambda: slstm_init_fused(wx, r, None, picard_iters=P, eps=cell.eps), reps)
+        ms_picard = (ms_initP - ms_init1) / (P - 1)  # one Picard pass launch (h-only output)
+        from pararnn_amd import newton_slstm_fused
+
+        ms_n1 = _time(torch, lambda: newton_slstm_fused(wx, r, None, init, max_iters=1, omega=1.0,
+                                                        eps=cell.eps), reps)
+        ms_n2 = _time(torch, lambda: newton_slstm_fused(wx, r, None, init, max_iters=2, omega=1.0,
+                                                        eps=cell.eps), reps)
+        ms_newton = ms_n2 / 2  # one Newton-iteration launch (average of the two)
+        ms_gemm = _time(torch, lambda: cell.W_x(x), reps)
+        cfg = NewtonConfig(max_iters=K, picard_iters=P, residual_atol=None, residual_fail=None,
+                           picard_adapt=False)
+        ms_e2e = _time(torch, lambda: newton_apply(cell, x, cfg), max(3, reps // 2), warm=1)
+
+    elems = B * T * D
+    s_x = 2
+    # Algorithmic bytes per element (per (b, t, channel)), SURVEY 8(d) figures.
+    picard_bytes = elems * (4 * s_x + 20)
+    newton_bytes = elems * (4 * s_x + 32)
+    step_bytes = elems * ((4 * s_x + 16) + P * (4 * s_x + 20) + K * (4 * s_x + 32))
+    ach_picard = picard_bytes / (ms_picard * 1e-3) / 1e9
+    ach_newton = newton_bytes / (ms_newton * 1e-3) / 1e9
+    out = {
+        "metric": "Newton+scan fwd tokens/sec + % HBM roofline, ParaSLSTM diag d=1024 T=131072",
+        "value": tokens / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: x ~ N(0, 0.5) seeded, default seeded ParaSLSTM init",
+        "config": {"workload": "ParaSLSTM mix='diag' fused Newton forward (init + K Newton, "
+                               "wx resident)",
+                   "d": D, "batch": B, "seq_len": T, "max_iters": K, "picard_iters": P,
+                   "storage": "bf16 wx/states, fp32 Newton work",
+                   "parallelism": "single GPU"},
+        "roofline": {
+            "kernel": "slstm_frozen_kernel (Picard pass, h-only output; 4 of the 8 launches, "
+                      "largest time share)",
+            "bound": "hbm",
+            "achieved": ach_picard,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": ach_picard / HBM_PEAK_GBS,
+            "traffic": _traffic_from_profile("slstm_frozen_picard_cfg3.md"),
+            "algorithmic_bytes_per_launch": picard_bytes,
+            "avg_launch_ms": ms_picard,
+        },
+        "roofline_newton": {
+            "kernel": "slstm_newton_kernel (one Newton iteration)",
+            "bound": "hbm",
+            "achieved": ach_newton,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": ach_newton / HBM_PEAK_GBS,
+            "traffic": _traffic_from_profile("slstm_newton_cfg3.md"),
+            "algorithmic_bytes_per_launch": newton_bytes,
+            "avg_launch_ms": ms_newton,
+        },
+        "step_algorithmic_GBps": step_bytes / (ms * 1e-3) / 1e9,
+        "step_roofline_frac": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "gemm_ms": ms_gemm,
+        "newton_apply_ms": ms_e2e,
+        "newton_apply_tokens_per_s": tokens / (ms_e2e * 1e-3),
+        "wall_s_timed_region": t_wall,
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(torch, args.cpu_sample)
+        out["gpu_over_cpu"] = out["value"] / out["cpu_baseline"]["value"]
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

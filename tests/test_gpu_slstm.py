@@ -174,11 +174,36 @@ def test_residual_gate_and_divergence_error():
                                                picard_adapt=False))
 
 
-def test_full_length_channel_slice_vs_oracle():
-    """BASELINE config 3 shape (d=1024, B=1, T=131072, bf16, K=2, P=5, x~N(0,0.5)):
-    the GPU solves all 1024 channels; channels are independent, so the CPU
-    oracle re-solves a slice of them over the full T."""
-    from pararnn_amd import ParaSLSTM, fused_newton
+def _slice_params(cell, chans, dtype):
+    d = cell.d_h
+    R_s = cell.R.detach()[:, chans.to(cell.R.device)].cpu()
+    return O.SLSTMParams(torch.zeros(4 * len(chans), 1, dtype=dtype),
+                         torch.zeros(4 * len(chans), dtype=dtype), R_s)
+
+
+def _slice_wx(wx, chans, d):
+    idx = torch.cat([chans + gi * d for gi in range(4)])
+    return wx[:, :, idx.to(wx.device)].cpu()
+
+
+def _rel_per_slot(got, ref):
+    return [((got[..., k, :] - ref[..., k, :]).abs().max() / ref[..., k, :].abs().max()).item()
+            for k in range(4)]
+
+
+CHANS = torch.tensor([0, 1, 63, 64, 511, 777, 1022, 1023])
+
+
+def test_full_length_cfg3_channel_slice_vs_oracle():
+    """BASELINE config 3 shape (d=1024, B=1, T=131072, bf16, P=5, x~N(0,0.5)).
+
+    The GPU solves all 1024 channels; channels are independent, so the CPU
+    oracle re-solves a slice of them over the full T.  At this length the
+    pinned K=2 leaves the reference algorithm's convergence basin: its second
+    Newton step overflows (the oracle's does too).  So the guess and the first
+    Newton step are compared in value, and the second by which channels
+    overflow."""
+    from pararnn_amd import ParaSLSTM, fused_newton, slstm_init_fused
 
     print("case full-length cfg3 slice", flush=True)
     torch.manual_seed(0)
@@ -188,17 +213,53 @@ def test_full_length_channel_slice_vs_oracle():
     x = (torch.randn(1, T, d, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
     with torch.no_grad():
         wx = cell.W_x(x)
+        init = slstm_init_fused(wx, cell.clipped_r(), None, picard_iters=5, eps=cell.eps)
+        k1 = fused_newton(cell, wx, max_iters=1, omega=1.0, h0=None, picard_iters=5)
+        k2 = fused_newton(cell, wx, max_iters=2, omega=1.0, h0=None, picard_iters=5)
+        cs = CHANS.to(DEV)
+        got_init = init[:, :, :, cs].float().cpu()
+        got_k1 = k1[:, :, :, cs].float().cpu()
+        got_k2 = k2[:, :, :, cs].float().cpu()
+        p = _slice_params(cell, CHANS, torch.bfloat16)
+        wx_s = _slice_wx(wx, CHANS, d)
+    ref_init = O.picard_init(p, wx_s, 5).float()
+    ref_k1 = O.slstm_newton(p, None, max_iters=1, picard_iters=5, wx=wx_s, work="fused").float()
+    ref_k2 = O.slstm_newton(p, None, max_iters=2, picard_iters=5, wx=wx_s, work="fused").float()
+    r_init, r_k1 = _rel_per_slot(got_init, ref_init), _rel_per_slot(got_k1, ref_k1)
+    print(f"cfg3 slice: init rel/slot {['%.1e' % v for v in r_init]}  "
+          f"K=1 rel/slot {['%.1e' % v for v in r_k1]}", flush=True)
+    assert max(r_init) <= 2e-2 and max(r_k1) <= 2e-2
+    fin_got = torch.isfinite(got_k2).all(dim=(0, 1, 2))
+    fin_ref = torch.isfinite(ref_k2).all(dim=(0, 1, 2))
+    print(f"cfg3 slice K=2 finite channels: gpu {fin_got.tolist()} oracle {fin_ref.tolist()}",
+          flush=True)
+    assert torch.equal(fin_got, fin_ref)
+
+
+def test_full_size_cfg2_fp32_channel_slice_converges():
+    """BASELINE config 2 shape (d=1024, B=8, T=16384) in fp32, K=2, P=5: inside
+    the basin, so the full solve is compared in value on a channel slice, and
+    its residual is checked."""
+    from pararnn_amd import ParaSLSTM, fused_newton
+
+    print("case full-size cfg2 fp32 slice", flush=True)
+    torch.manual_seed(0)
+    d, B, T = 1024, 8, 16384
+    cell = ParaSLSTM(d, d).to(DEV)
+    g = torch.Generator(device=DEV).manual_seed(1)
+    x = torch.randn(B, T, d, generator=g, device=DEV)
+    with torch.no_grad():
+        wx = cell.W_x(x)
         out = fused_newton(cell, wx, max_iters=2, omega=1.0, h0=None, picard_iters=5)
-        assert torch.isfinite(out.float()).all()
-        chans = torch.tensor([0, 1, 63, 64, 511, 777, 1022, 1023])
-        idx = torch.cat([chans + gi * d for gi in range(4)])
-        wx_s = wx[:, :, idx.to(DEV)].cpu()
-        R_s = cell.R.detach()[:, chans.to(DEV)].cpu()
-        p = O.SLSTMParams(torch.zeros(4 * len(chans), 1, dtype=torch.bfloat16),
-                          torch.zeros(4 * len(chans), dtype=torch.bfloat16), R_s)
-        ref = O.slstm_newton(p, None, max_iters=2, picard_iters=5, wx=wx_s, work="fused").float()
-        got = out[:, :, :, chans.to(DEV)].float().cpu()
-    _report("cfg3 slice", got, ref)
-    for k in range(4):
-        rel = ((got[..., k, :] - ref[..., k, :]).abs().max() / ref[..., k, :].abs().max()).item()
-        assert rel <= 2e-2, (k, rel)
+        pred = cell.step(O.slstm.prepend(out, None), None, wx=wx)
+        res = (pred - out).abs().amax(dim=(0, 1, 3)).tolist()
+        got = out[:, :, :, CHANS.to(DEV)].cpu()
+        p = _slice_params(cell, CHANS, torch.float32)
+        wx_s = _slice_wx(wx, CHANS, d)
+    print(f"cfg2 fp32 residual per slot {['%.1e' % v for v in res]}", flush=True)
+    ref = O.slstm_newton(p, None, max_iters=2, picard_iters=5, wx=wx_s)
+    d_abs = (got - ref).abs()
+    print(f"cfg2 fp32 slice max|gpu-oracle| per slot {['%.1e' % d_abs[..., k, :].max() for k in range(4)]}",
+          flush=True)
+    assert max(res) < 1e-3
+    assert torch.all(d_abs <= 1e-4 * (1 + ref.abs()))
