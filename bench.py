@@ -156,7 +156,10 @@ def main() -> int:
 
     elems = B * T * D
     s_x = 2
-    # Algorithmic bytes per element (per (b, t, channel)), SURVEY 8(d) figures.
+    # Algorithmic bytes per (b, t, channel) with s_x = bytes of the wx dtype:
+    # zero-hidden pass 4 s_x + 16 (read wx, write the state), each Picard pass
+    # 4 s_x + 20 (read wx and fp32 h_prev, write the state), each Newton
+    # iteration 4 s_x + 32 (read wx and the fp32 state, write the state).
     picard_bytes = elems * (4 * s_x + 20)
     newton_bytes = elems * (4 * s_x + 32)
     step_bytes = elems * ((4 * s_x + 16) + P * (4 * s_x + 20) + K * (4 * s_x + 32))
