@@ -1,0 +1,152 @@
+"""GPU parity of the ParaGRU(mix='head') HIP path (chunked MFMA scan) against
+the CPU oracle and the reference's golden vectors."""
+
+import ctypes
+
+import pytest
+import torch
+from conftest import load_golden
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _cfg(K):
+    from pararnn_amd import NewtonConfig
+
+    return NewtonConfig(max_iters=K, residual_atol=None, residual_fail=None)
+
+
+def _cell(t, m, dtype):
+    from pararnn_amd import ParaGRU
+
+    cell = ParaGRU(m["d_in"], m["n_heads"] * m["d_head"], mix="head", n_heads=m["n_heads"])
+    with torch.no_grad():
+        cell.W_x.weight.copy_(t["W"])
+        cell.W_x.bias.copy_(t["b"])
+        for k in ("A_z", "A_r", "A_n"):
+            getattr(cell, k).copy_(t[k])
+    return cell.to(device=DEV, dtype=dtype)
+
+
+def test_mfma_operand_layout():
+    from pararnn_amd import _lib
+
+    print("case mfma probe", flush=True)
+    lib = _lib.load()
+    fn = lib.prnn_internal_mfma_probe
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p] * 4
+    g = torch.Generator().manual_seed(0)
+    A = torch.randn(64, 64, generator=g)
+    B = torch.randn(64, 64, generator=g)
+    C = torch.empty(64, 64, device=DEV)
+    Ad, Bd = A.to(DEV), B.to(DEV)
+    assert fn(Ad.data_ptr(), Bd.data_ptr(), C.data_ptr(), torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    ref = A.bfloat16().float() @ B.bfloat16().float()
+    err = (C.cpu() - ref).abs().max().item()
+    print(f"mfma probe max err {err:.2e}", flush=True)
+    assert err < 1e-3
+
+
+@pytest.mark.parametrize("name", ["gru_head_fp32", "gru_head_h0_fp32"])
+def test_fp32_matches_reference_eager(name):
+    from pararnn_amd import newton_apply
+
+    print(f"case {name}", flush=True)
+    t, m = load_golden(name)
+    cell = _cell(t, m, torch.float32)
+    h0 = t["h0"].to(DEV) if "h0" in t else None
+    with torch.no_grad():
+        out = newton_apply(cell, t["x"].to(DEV), _cfg(m["K"]), h0=h0).cpu()
+    err = (out - t["newton"]).abs().max().item()
+    err_seq = (out - t["sequential"]).abs().max().item()
+    print(f"[{name}] max|gpu-ref| {err:.2e}  max|gpu-seq| {err_seq:.2e}", flush=True)
+    assert err <= 1e-5
+
+
+def test_bf16_matches_fused_semantics():
+    from pararnn_amd import newton_apply
+
+    print("case gru_head_bf16", flush=True)
+    t, m = load_golden("gru_head_bf16")
+    cell = _cell(t, m, torch.bfloat16)
+    p = O.GRUHeadParams(t["W"], t["b"], t["A_z"], t["A_r"], t["A_n"])
+    with torch.no_grad():
+        from pararnn_amd import fused_newton
+
+        out = fused_newton(cell, t["wx"].to(DEV), max_iters=m["K"], omega=1.0, h0=None).float().cpu()
+        out2 = newton_apply(cell, t["x"].to(DEV), _cfg(m["K"])).float().cpu()
+    ref = O.gru_head_newton(p, None, max_iters=m["K"], wx=t["wx"], work="fused").float()
+    eager = t["newton"].float()
+    rel = ((out - ref).abs().max() / ref.abs().max()).item()
+    rel_e = ((out - eager).abs().max() / eager.abs().max()).item()
+    print(f"bf16: rel vs fused semantics {rel:.2e}, rel vs reference eager bf16 {rel_e:.2e}",
+          flush=True)
+    assert rel <= 2e-2 and rel_e <= 2e-2
+    assert ((out2 - out).abs().max() / out.abs().max()).item() <= 2e-2
+
+
+@pytest.mark.parametrize("B,T,H,K,with_h0", [
+    (1, 1, 1, 1, False), (3, 70, 2, 2, True), (2, 33, 1, 0, True), (1, 200, 3, 4, False),
+])
+def test_ragged_shapes_vs_oracle(B, T, H, K, with_h0):
+    from pararnn_amd import ParaGRU, newton_apply
+
+    print(f"case ragged B={B} T={T} H={H} K={K} h0={with_h0}", flush=True)
+    torch.manual_seed(T * 7 + H)
+    cell = ParaGRU(10, 64 * H, mix="head", n_heads=H)
+    x = torch.randn(B, T, 10) * 1.5
+    h0 = torch.randn(B, 64 * H) * 0.5 if with_h0 else None
+    p = O.GRUHeadParams(cell.W_x.weight.detach(), cell.W_x.bias.detach(), cell.A_z.detach(),
+                        cell.A_r.detach(), cell.A_n.detach())
+    with torch.no_grad():
+        ref = O.gru_head_newton(p, x, max_iters=K, h0=h0)
+        out = newton_apply(cell.to(DEV), x.to(DEV), _cfg(K),
+                           h0=None if h0 is None else h0.to(DEV)).cpu()
+    err = (out - ref).abs().max().item()
+    print(f"[ragged] max|gpu-oracle| {err:.2e}", flush=True)
+    assert err <= 1e-5
+
+
+def test_verify_agreement():
+    from pararnn_amd import NewtonConfig, verify_agreement
+
+    print("case verify_agreement head", flush=True)
+    t, m = load_golden("gru_head_fp32")
+    cell = _cell(t, m, torch.float32)
+    rep = verify_agreement(cell, t["x"].to(DEV), config=NewtonConfig(max_iters=3))
+    print(f"verify_agreement: max_abs {rep.max_abs:.2e} ok={rep.ok}", flush=True)
+    assert rep.ok
+
+
+def test_full_size_cfg4_head_slice_vs_oracle():
+    """BASELINE config 4 shape (H=8, d_head=64, B=4, T=32768, fp32, K=3): the GPU
+    solves all 32 (batch, head) sequences; they are independent, so the CPU
+    oracle re-solves one of them over the full T."""
+    from pararnn_amd import ParaGRU, fused_newton
+
+    print("case full-size cfg4 slice", flush=True)
+    torch.manual_seed(0)
+    H, B, T = 8, 4, 32768
+    cell = ParaGRU(512, 512, mix="head", n_heads=H).to(DEV)
+    g = torch.Generator(device=DEV).manual_seed(1)
+    x = torch.randn(B, T, 512, generator=g, device=DEV)
+    b_s, h_s = 2, 5
+    with torch.no_grad():
+        wx = cell.W_x(x)
+        out = fused_newton(cell, wx, max_iters=3, omega=1.0, h0=None)
+        assert torch.isfinite(out).all()
+        got = out[b_s, :, 64 * h_s:64 * (h_s + 1)].cpu()
+        cols = torch.cat([torch.arange(64 * h_s, 64 * (h_s + 1)) + gi * 512 for gi in range(3)])
+        wx_s = wx[b_s:b_s + 1, :, cols.to(DEV)].cpu()
+        p = O.GRUHeadParams(torch.zeros(192, 1), torch.zeros(192),
+                            *(getattr(cell, k).detach()[h_s:h_s + 1].cpu() for k in ("A_z", "A_r", "A_n")))
+    ref = O.gru_head_newton(p, None, max_iters=3, wx=wx_s)[0]
+    err = (got - ref).abs().max().item()
+    print(f"cfg4 slice max|gpu-oracle| {err:.2e}", flush=True)
+    assert err <= 1e-5
