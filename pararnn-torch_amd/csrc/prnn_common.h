@@ -66,51 +66,29 @@ __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, 
 __device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
 
 // ---- decoupled look-back ----------------------------------------------------
-// Cross-tile data moves through system-scope relaxed atomics, which the
-// compiler lowers to write-through / cache-bypassing (sc0 sc1) vector loads
-// and stores: a tile on one XCD sees another XCD's data without L2
-// write-back or invalidate, so a look-back hop costs one memory round trip.
-//
-// * Inclusive carries are "tagged words": 64-bit {float bits, tag} written
-//   and read as single atomic words.  A word whose tag equals the current
-//   epoch is valid; no separate flag or ordering is needed.
-// * Aggregates are published as plain fp32 payload, then (after the stores
-//   have completed, s_waitcnt) a status word set to the epoch.
+// Cross-tile data moves through agent-scope relaxed atomics: the compiler
+// lowers them to vector loads / stores with the sc1 bit, which write through
+// and bypass the per-XCD L2, so a tile on one XCD sees another XCD's data at
+// the device-coherent level (the memory-side cache) without any L2 write-back
+// or invalidate.  Every published value is a "tagged word": 64-bit
+// {float bits, tag} written and read as one atomic word.  A word whose tag
+// equals the current epoch is valid, so no status flag or store ordering is
+// needed and one load both tests and fetches a value.
 //
 // The epoch is the index of the launch within one solver call (>= 1).  The
-// status words and tagged words are cleared at the start of every call, so
-// nothing left by an earlier call or an earlier launch reads as valid.
+// tagged words are cleared at the start of every call, so nothing left by an
+// earlier call or an earlier launch reads as valid.
 
-__device__ __forceinline__ void st_sys(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ float ld_sys(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ void st_sys_int(int* p, int v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ int ld_sys_int(const int* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
 __device__ __forceinline__ void st_tagged(unsigned long long* p, float v, int tag) {
   const unsigned long long w =
       (static_cast<unsigned long long>(static_cast<uint32_t>(tag)) << 32) | __float_as_uint(v);
-  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // True (and v set) when the word carries this tag.
 __device__ __forceinline__ bool ld_tagged(const unsigned long long* p, int tag, float& v) {
-  const unsigned long long w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  const unsigned long long w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   v = __uint_as_float(static_cast<uint32_t>(w));
   return static_cast<int>(w >> 32) == tag;
-}
-// Wait until this lane's earlier stores have completed (vmcnt covers stores on gfx9).
-__device__ __forceinline__ void drain_stores() { __builtin_amdgcn_s_waitcnt(0); }
-
-// Publish an aggregate: call after the payload's st_sys stores.
-__device__ __forceinline__ void publish_agg(int* flag, int epoch, int lane) {
-  drain_stores();
-  if (lane == 0) st_sys_int(flag, epoch);
 }
 
 }  // namespace prnn

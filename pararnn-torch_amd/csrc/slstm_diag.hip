@@ -76,20 +76,21 @@ __device__ __forceinline__ int take_ticket(int* counter) {
 // identity / absorb (acc <- acc o agg of an earlier tile) / finish (carry =
 // acc applied to the inclusive value of that tile).
 // ---------------------------------------------------------------------------
-template <class M, int W>
+template <class M, int NW>
 struct LookbackShared {
-  float pl[W][M::NA][kCB];
-  int st[W][kCB];
+  float pl[NW][M::NA][kCB];
+  int st[NW][kCB];
   int pos[kCB];
   int more;
 };
 
-template <class M, int W>
+// W waves, each fetching KP predecessors per round (window NW = W * KP).
+template <class M, int W, int KP>
 __device__ __forceinline__ void windowed_lookback(const TileId& id, int B, int n_cb, int epoch,
-                                                  const int* __restrict__ flags,
                                                   const unsigned long long* __restrict__ incl,
-                                                  const float* __restrict__ agg, int lane,
-                                                  int wave, LookbackShared<M, W>& sh,
+                                                  const unsigned long long* __restrict__ agg,
+                                                  int lane, int wave,
+                                                  LookbackShared<M, W * KP>& sh,
                                                   float carry[M::NI]) {
   typename M::Acc acc;
   M::identity(acc);
@@ -102,30 +103,33 @@ __device__ __forceinline__ void windowed_lookback(const TileId& id, int B, int n
     __syncthreads();
     {
       const int base = sh.pos[lane];
-      const int p = base - wave;
-      int st = 0;
-      if (base >= 0 && p >= 0) {
-        const size_t ptile = static_cast<size_t>(p) * per + id.rem;
-        const unsigned long long* ip = incl + ptile * M::NI * kCB + lane;
-        float v[M::NI];
-        bool ok = true;
 #pragma unroll
-        for (int k = 0; k < M::NI; ++k) ok = ld_tagged(ip + k * kCB, epoch, v[k]) && ok;
-        if (ok) {
-          st = 2;
+      for (int k = 0; k < KP; ++k) {
+        const int slot = wave * KP + k;
+        const int p = base - slot;
+        int st = 0;
+        if (base >= 0 && p >= 0) {
+          const size_t ptile = static_cast<size_t>(p) * per + id.rem;
+          const unsigned long long* ip = incl + ptile * M::NI * kCB + lane;
+          const unsigned long long* ap = agg + ptile * M::NA * kCB + lane;
+          float v[M::NI], a[M::NA];
+          bool ok_i = true, ok_a = true;
 #pragma unroll
-          for (int k = 0; k < M::NI; ++k) sh.pl[wave][k][lane] = v[k];
-        } else if (ld_sys_int(flags + ptile) == epoch) {
-          st = 1;
-          const float* ap = agg + ptile * M::NA * kCB + lane;
-          float a[M::NA];
+          for (int q = 0; q < M::NI; ++q) ok_i = ld_tagged(ip + q * kCB, epoch, v[q]) && ok_i;
 #pragma unroll
-          for (int k = 0; k < M::NA; ++k) a[k] = ld_sys(ap + k * kCB);
+          for (int q = 0; q < M::NA; ++q) ok_a = ld_tagged(ap + q * kCB, epoch, a[q]) && ok_a;
+          if (ok_i) {
+            st = 2;
 #pragma unroll
-          for (int k = 0; k < M::NA; ++k) sh.pl[wave][k][lane] = a[k];
+            for (int q = 0; q < M::NI; ++q) sh.pl[slot][q][lane] = v[q];
+          } else if (ok_a) {
+            st = 1;
+#pragma unroll
+            for (int q = 0; q < M::NA; ++q) sh.pl[slot][q][lane] = a[q];
+          }
         }
+        sh.st[slot][lane] = st;
       }
-      sh.st[wave][lane] = st;
     }
     __syncthreads();
     if (wave == 0) {
@@ -133,7 +137,7 @@ __device__ __forceinline__ void windowed_lookback(const TileId& id, int B, int n
       if (!done) {
         bool stalled = false;
 #pragma unroll
-        for (int w = 0; w < W; ++w) {
+        for (int w = 0; w < W * KP; ++w) {
           if (!done && !stalled) {
             const int st = sh.st[w][lane];
             if (st == 2) {
@@ -242,11 +246,12 @@ template <typename TX, int L, int W, bool HAS_H, bool FULL_OUT>
 __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
     const TX* __restrict__ hsrc, TX* __restrict__ out_full, TX* __restrict__ out_h, int B, int T,
-    int d, int n_cb, float eps, int* __restrict__ counter, int* __restrict__ flags,
-    float* __restrict__ agg, unsigned long long* __restrict__ incl, int epoch) {
+    int d, int n_cb, float eps, int* __restrict__ counter, unsigned long long* __restrict__ agg,
+    unsigned long long* __restrict__ incl, int epoch) {
+  constexpr int KP = 2;  // predecessors per wave per look-back round
   __shared__ float s_agg[W][4][kCB];
   __shared__ float s_carry[W][3][kCB];
-  __shared__ LookbackShared<FrozenMonoid, W> s_lb;
+  __shared__ LookbackShared<FrozenMonoid, W * KP> s_lb;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int tile = take_ticket(counter);
@@ -316,17 +321,16 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
         carry[0] = ld(hb + 2 * d);
       }
     } else {
-      float* ap = agg + (static_cast<size_t>(tile) * 4) * kCB + lane;
-      st_sys(ap + 0 * kCB, tile_agg.F);
-      st_sys(ap + 1 * kCB, tile_agg.M);
-      st_sys(ap + 2 * kCB, tile_agg.N);
-      st_sys(ap + 3 * kCB, tile_agg.C);
-      publish_agg(flags + tile, epoch, lane);
+      unsigned long long* ap = agg + (static_cast<size_t>(tile) * 4) * kCB + lane;
+      st_tagged(ap + 0 * kCB, tile_agg.F, epoch);
+      st_tagged(ap + 1 * kCB, tile_agg.M, epoch);
+      st_tagged(ap + 2 * kCB, tile_agg.N, epoch);
+      st_tagged(ap + 3 * kCB, tile_agg.C, epoch);
     }
   }
   if (id.chunk > 0)
-    windowed_lookback<FrozenMonoid, W>(id, B, n_cb, epoch, flags, incl, agg, lane, wave, s_lb,
-                                       carry);
+    windowed_lookback<FrozenMonoid, W, KP>(id, B, n_cb, epoch, incl, agg, lane, wave, s_lb,
+                                           carry);
   if (wave == 0) {
     // Per-wave carries, then the tile's inclusive carry.
     float m = carry[0], n = carry[1], c = carry[2];
@@ -514,11 +518,12 @@ template <typename TX, typename TIN, typename TOUT, int L, int W>
 __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
     const TIN* __restrict__ hin, TOUT* __restrict__ hout, int B, int T, int d, int n_cb,
-    float omega, float eps, int* __restrict__ counter, int* __restrict__ flags,
-    float* __restrict__ agg, unsigned long long* __restrict__ incl, int epoch) {
+    float omega, float eps, int* __restrict__ counter, unsigned long long* __restrict__ agg,
+    unsigned long long* __restrict__ incl, int epoch) {
+  constexpr int KP = 1;  // predecessors per wave per look-back round
   __shared__ float s_agg[W][20][kCB];
   __shared__ float s_carry[W][4][kCB];
-  __shared__ LookbackShared<NewtonMonoid, W> s_lb;
+  __shared__ LookbackShared<NewtonMonoid, W * KP> s_lb;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int tile = take_ticket(counter);
@@ -607,18 +612,17 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
       }
       tile_agg = w == 0 ? sw : aff_compose(tile_agg, sw);
     }
-    float* ap = agg + (static_cast<size_t>(tile) * 20) * kCB + lane;
+    unsigned long long* ap = agg + (static_cast<size_t>(tile) * 20) * kCB + lane;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      st_sys(ap + (16 + i) * kCB, tile_agg.b[i]);
+      st_tagged(ap + (16 + i) * kCB, tile_agg.b[i], epoch);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) st_sys(ap + (4 * i + j) * kCB, tile_agg.A[i][j]);
+      for (int j = 0; j < 4; ++j) st_tagged(ap + (4 * i + j) * kCB, tile_agg.A[i][j], epoch);
     }
-    publish_agg(flags + tile, epoch, lane);
   }
   if (id.chunk > 0)
-    windowed_lookback<NewtonMonoid, W>(id, B, n_cb, epoch, flags, incl, agg, lane, wave, s_lb,
-                                       carry);
+    windowed_lookback<NewtonMonoid, W, KP>(id, B, n_cb, epoch, incl, agg, lane, wave, s_lb,
+                                           carry);
   if (wave == 0) {
     // Carry into each wave's segment, then the tile's outgoing carry.
 #pragma unroll
@@ -731,26 +735,24 @@ static int check_dims(int B, int T, int d, int dtype) {
   return PRNN_OK;
 }
 
-// Look-back state shared by the launches of one call.  Layout:
-//   counters[kMaxStages] | status words[n_tiles] | tagged carries | aggregates
-// The first three are cleared by one kernel at the start of the call.
+// Look-back state shared by the launches of one call, cleared by one kernel
+// at the start of the call:
+//   counters[kMaxStages] | tagged carries | tagged aggregates
 struct Lookback {
   int* counters;
-  int* flags;
   unsigned long long* incl;
-  float* agg;
+  unsigned long long* agg;
   size_t clear_words;
 };
 
 static Lookback carve_lookback(Carver& cv, const Geo& g, int incl_vals, int agg_vals) {
   Lookback lb;
   lb.counters = static_cast<int*>(cv.take(sizeof(int) * kMaxStages));
-  lb.flags = static_cast<int*>(cv.take(sizeof(int) * g.n_tiles));
   lb.incl = static_cast<unsigned long long*>(
       cv.take(sizeof(unsigned long long) * incl_vals * kCB * g.n_tiles));
-  const size_t end = cv.used;
-  lb.agg = static_cast<float*>(cv.take(sizeof(float) * agg_vals * kCB * g.n_tiles));
-  lb.clear_words = (end - (reinterpret_cast<char*>(lb.counters) - cv.base)) / sizeof(int);
+  lb.agg = static_cast<unsigned long long*>(
+      cv.take(sizeof(unsigned long long) * agg_vals * kCB * g.n_tiles));
+  lb.clear_words = (cv.used - (reinterpret_cast<char*>(lb.counters) - cv.base)) / sizeof(int);
   return lb;
 }
 
@@ -797,8 +799,7 @@ static void launch_frozen(bool has_h, bool full_out, const TX* wx, const TX* r, 
   int* ctr = lb.counters + epoch;
 #define PRNN_FROZEN(HH, FO)                                                                    \
   slstm_frozen_kernel<TX, L, W, HH, FO><<<grid, block, 0, stream>>>(                           \
-      wx, r, h0, src, out_full, out_h, B, T, d, g.n_cb, eps, ctr, lb.flags, lb.agg, lb.incl, \
-      epoch)
+      wx, r, h0, src, out_full, out_h, B, T, d, g.n_cb, eps, ctr, lb.agg, lb.incl, epoch)
   if (has_h) {
     if (full_out) PRNN_FROZEN(true, true); else PRNN_FROZEN(true, false);
   } else {
@@ -846,7 +847,7 @@ static void launch_newton_shape(const TX* wx, const TX* r, const TX* h0, const T
                                 const Lookback& lb, int epoch, hipStream_t stream) {
   const Geo g = geometry(B, T, d, Shape{L, W});
   slstm_newton_kernel<TX, TIN, TOUT, L, W><<<dim3(g.n_tiles), dim3(64 * W), 0, stream>>>(
-      wx, r, h0, hin, hout, B, T, d, g.n_cb, omega, eps, lb.counters + epoch, lb.flags, lb.agg,
+      wx, r, h0, hin, hout, B, T, d, g.n_cb, omega, eps, lb.counters + epoch, lb.agg,
       lb.incl, epoch);
 }
 
