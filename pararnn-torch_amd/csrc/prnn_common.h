@@ -91,4 +91,53 @@ __device__ __forceinline__ bool ld_tagged(const unsigned long long* p, int tag, 
   return static_cast<int>(w >> 32) == tag;
 }
 
+// ---- buffer access ----------------------------------------------------------
+// Streams are read and written through buffer resources: the per-step offset
+// is a wave-uniform SGPR (soffset), so a step costs no 64-bit address
+// arithmetic.  A lane whose offset is kOOB is outside every resource: its
+// loads return 0 and its stores are dropped, which masks channels past d.
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+constexpr uint32_t kOOB = 0x80000000u;
+
+// Raw (stride 0) resource over `bytes` bytes from `base` (CDNA dword 3).
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
+// Raw storage bits of one element (bf16: zero-extended 16-bit word).
+__device__ __forceinline__ uint32_t ldb_bits(bf16*, rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+__device__ __forceinline__ uint32_t ldb_bits(float*, rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+__device__ __forceinline__ float bits_to_f32(bf16*, uint32_t b) { return __uint_as_float(b << 16); }
+__device__ __forceinline__ float bits_to_f32(float*, uint32_t b) { return __uint_as_float(b); }
+
+template <typename T>
+__device__ __forceinline__ float ldb(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return bits_to_f32(static_cast<T*>(nullptr), ldb_bits(static_cast<T*>(nullptr), r, voff, soff));
+}
+template <typename T>
+__device__ __forceinline__ void stb(rsrc_t r, uint32_t voff, uint32_t soff, float v);
+template <>
+__device__ __forceinline__ void stb<bf16>(rsrc_t r, uint32_t voff, uint32_t soff, float v) {
+  __builtin_amdgcn_raw_buffer_store_b16(from_f32<bf16>(v).bits, r, voff, soff, 0);
+}
+template <>
+__device__ __forceinline__ void stb<float>(rsrc_t r, uint32_t voff, uint32_t soff, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, voff, soff, 0);
+}
+
+// Two floats rounded to bf16 (RNE) and packed low | high << 16 in one
+// v_cvt_pk_bf16_f32; unpacked halves are exact floats.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2_t{lo, hi}, bf16x2_t));
+}
+__device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
 }  // namespace prnn

@@ -57,7 +57,7 @@ __device__ __forceinline__ int take_ticket(int* counter) {
   if (threadIdx.x == 0)
     s_ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
-  return s_ticket;
+  return __builtin_amdgcn_readfirstlane(s_ticket);  // wave-uniform
 }
 
 
@@ -242,6 +242,61 @@ struct FrozenMonoid {
   }
 };
 
+// Pre-activations of a tile's steps, held in registers between the two
+// passes.  In bf16 they are exact bf16 values (wx, or wx + R h_prev rounded as
+// the reference's two torch ops), packed two to a register.
+template <typename TX>
+struct PreStash;
+
+template <>
+struct PreStash<bf16> {
+  static constexpr int N = 2;  // registers per step: (z_i, z_f), (z_z, z_o)
+  template <bool HAS_H>
+  static __device__ __forceinline__ void make(const uint32_t x[4], const float r[4], float hp,
+                                              uint32_t w[N]) {
+    if (!HAS_H) {
+      w[0] = x[0] | (x[1] << 16);
+      w[1] = x[2] | (x[3] << 16);
+      return;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      // round(R h) and round(wx + round(R h)), two gates per conversion.
+      const uint32_t q = pack_bf16x2(r[2 * k] * hp, r[2 * k + 1] * hp);
+      w[k] = pack_bf16x2(__uint_as_float(x[2 * k] << 16) + lo_bf16(q),
+                         __uint_as_float(x[2 * k + 1] << 16) + hi_bf16(q));
+    }
+  }
+  static __device__ __forceinline__ void get(const uint32_t w[N], float p[4]) {
+    p[0] = lo_bf16(w[0]);
+    p[1] = hi_bf16(w[0]);
+    p[2] = lo_bf16(w[1]);
+    p[3] = hi_bf16(w[1]);
+  }
+};
+
+template <>
+struct PreStash<float> {
+  static constexpr int N = 4;
+  template <bool HAS_H>
+  static __device__ __forceinline__ void make(const uint32_t x[4], const float r[4], float hp,
+                                              uint32_t w[N]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float xv = __uint_as_float(x[g]);
+      w[g] = __float_as_uint(HAS_H ? add_rn(xv, mul_rn(r[g], hp)) : xv);
+    }
+  }
+  static __device__ __forceinline__ void get(const uint32_t w[N], float p[4]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) p[g] = __uint_as_float(w[g]);
+  }
+};
+
+// One frozen-gate pass over a tile of W waves x L steps x 64 channels.  Each
+// lane owns one channel; its L steps are read once (pass 1, which builds the
+// lane aggregate), kept in registers through the look-back, and replayed from
+// the true carry in pass 2, which writes the trajectory.
 template <typename TX, int L, int W, bool HAS_H, bool FULL_OUT>
 __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
@@ -249,55 +304,67 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
     int d, int n_cb, float eps, int* __restrict__ counter, unsigned long long* __restrict__ agg,
     unsigned long long* __restrict__ incl, int epoch) {
   constexpr int KP = 2;  // predecessors per wave per look-back round
+  using Stash = PreStash<TX>;
+  constexpr uint32_t SZ = sizeof(TX);
   __shared__ float s_agg[W][4][kCB];
   __shared__ float s_carry[W][3][kCB];
   __shared__ LookbackShared<FrozenMonoid, W * KP> s_lb;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tile = take_ticket(counter);
   const TileId id = decode_tile(tile, B, n_cb);
-  const int ch = id.cb * kCB + lane;
-  const bool live = ch < d;
-  const int chunk_len = W * L;
-  const int t0 = id.chunk * chunk_len + wave * L;
+  const int c0 = id.cb * kCB;
+  const bool live = c0 + lane < d;
+  const int t0 = id.chunk * (W * L) + wave * L;
+  const int n_steps = max(0, min(L, T - t0));
   const size_t row4 = static_cast<size_t>(4) * d;
+  const size_t first = static_cast<size_t>(id.b) * T + t0;  // first (b, t) row of the wave
+  const uint32_t voff = live ? lane * SZ : kOOB;
+  const uint32_t slot = d * SZ;  // bytes between the slots of a (b, t, 4d) row
+  // Bytes from the wave's base to the end of its last live element.
+  const uint32_t span4 = n_steps > 0 ? ((n_steps - 1) * row4 + 3 * d + (d - c0)) * SZ : 0;
+  const uint32_t span1 = n_steps > 0 ? ((n_steps - 1) * static_cast<size_t>(d) + (d - c0)) * SZ : 0;
 
   float r[4] = {0.f, 0.f, 0.f, 0.f};
+  float hp0 = 0.f;  // h_prev of the wave's first step
   if (HAS_H && live) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) r[g] = ld(rmix + g * d + ch);
+    for (int g = 0; g < 4; ++g) r[g] = ld(rmix + g * d + c0 + lane);
+    if (t0 > 0 && n_steps > 0)
+      hp0 = ld(hsrc + (first - 1) * d + c0 + lane);
+    else if (t0 == 0 && h0 != nullptr)
+      hp0 = ld(h0 + static_cast<size_t>(id.b) * row4 + 3 * d + c0 + lane);
   }
 
-  // Frozen pre-activations of step t: wx (+ R * h_prev rounded like the
-  // reference's two torch ops).  Read in pass 1 and again in pass 2: the
-  // second read hits the caches, which keeps registers free for occupancy and
-  // lets a tile span many steps (fewer look-back hops).
-  auto load_pre = [&](int t, float pre[4]) {
-    const size_t base = (static_cast<size_t>(id.b) * T + t) * row4 + ch;
-    float hp = 0.f;
-    if (HAS_H) {
-      if (t > 0)
-        hp = ld(hsrc + (static_cast<size_t>(id.b) * T + (t - 1)) * d + ch);
-      else if (h0 != nullptr)
-        hp = ld(h0 + static_cast<size_t>(id.b) * row4 + 3 * d + ch);
-    }
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const float x = ld(wx + base + g * d);
-      pre[g] = HAS_H ? round_to<TX>(add_rn(x, round_to<TX>(mul_rn(r[g], hp)))) : x;
-    }
-  };
-  const int t_end = min(t0 + L, T);
-
-  // Pass 1: segment aggregate from the empty state (m = -inf, n = c = 0).
+  // Pass 1: read the steps, stash the pre-activations, and fold the segment
+  // aggregate from the empty state (m = -inf, n = c = 0).
+  uint32_t stash[L][Stash::N];
   FG a = fg_identity();
-  if (live) {
-#pragma unroll 8
-    for (int t = t0; t < t_end; ++t) {
-      float pre[4];
-      load_pre(t, pre);
-      a.F += pre[1];
-      fg_step(pre[0], pre[1], pre[2], a.M, a.N, a.C);
+  {
+    const rsrc_t rx = make_rsrc(wx + first * row4 + c0, span4);
+    const rsrc_t rh = make_rsrc(HAS_H ? hsrc + first * d + c0 : nullptr, HAS_H ? span1 : 0);
+    auto step = [&](int s) {
+      uint32_t x[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        x[g] = ldb_bits(static_cast<TX*>(nullptr), rx, voff, s * row4 * SZ + g * slot);
+      float hp = hp0;
+      if (HAS_H && s > 0) hp = ldb<TX>(rh, voff, (s - 1) * d * SZ);
+      Stash::template make<HAS_H>(x, r, hp, stash[s]);
+      float p[4];
+      Stash::get(stash[s], p);
+      a.F += p[1];
+      fg_step(p[0], p[1], p[2], a.M, a.N, a.C);
+    };
+    // Whole segments run branch-free so the loads of many steps are in
+    // flight together; only the last segment of a sequence is guarded.
+    if (n_steps == L) {
+#pragma unroll
+      for (int s = 0; s < L; ++s) step(s);
+    } else {
+#pragma unroll
+      for (int s = 0; s < L; ++s)
+        if (s < n_steps) step(s);
     }
   }
   s_agg[wave][0][lane] = a.F;
@@ -315,7 +382,7 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
           tile_agg, FG{s_agg[w][0][lane], s_agg[w][1][lane], s_agg[w][2][lane], s_agg[w][3][lane]});
     if (id.chunk == 0) {
       if (h0 != nullptr && live) {
-        const TX* hb = h0 + static_cast<size_t>(id.b) * row4 + ch;
+        const TX* hb = h0 + static_cast<size_t>(id.b) * row4 + c0 + lane;
         carry[2] = ld(hb);
         carry[1] = ld(hb + d);
         carry[0] = ld(hb + 2 * d);
@@ -349,26 +416,34 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
   }
   __syncthreads();
 
-  // Pass 2: replay with the true carry and stream the trajectory.
+  // Pass 2: replay the stashed steps from the true carry and write the
+  // trajectory (dead lanes' stores fall outside the resources).
   float m = s_carry[wave][0][lane], n = s_carry[wave][1][lane], c = s_carry[wave][2][lane];
-  if (live) {
-#pragma unroll 8
-    for (int t = t0; t < t_end; ++t) {
-      float pre[4];
-      load_pre(t, pre);
-      fg_step(pre[0], pre[1], pre[2], m, n, c);
-      // h = sigmoid(z_o) c / (n + eps) with one reciprocal.
-      const float h = c * frcp((1.f + fexp(-pre[3])) * (n + eps));
-      if (FULL_OUT) {
-        TX* op = out_full + (static_cast<size_t>(id.b) * T + t) * row4 + ch;
-        st(op, c);
-        st(op + d, n);
-        st(op + 2 * d, m);
-        st(op + 3 * d, h);
-      } else {
-        st(out_h + (static_cast<size_t>(id.b) * T + t) * d + ch, h);
-      }
+  const rsrc_t ro = FULL_OUT ? make_rsrc(out_full + first * row4 + c0, span4)
+                             : make_rsrc(out_h + first * d + c0, span1);
+  auto replay = [&](int s) {
+    float p[4];
+    Stash::get(stash[s], p);
+    fg_step(p[0], p[1], p[2], m, n, c);
+    // h = sigmoid(z_o) c / (n + eps) with one reciprocal.
+    const float h = c * frcp((1.f + fexp(-p[3])) * (n + eps));
+    if (FULL_OUT) {
+      const uint32_t so = s * row4 * SZ;
+      stb<TX>(ro, voff, so, c);
+      stb<TX>(ro, voff, so + slot, n);
+      stb<TX>(ro, voff, so + 2 * slot, m);
+      stb<TX>(ro, voff, so + 3 * slot, h);
+    } else {
+      stb<TX>(ro, voff, s * d * SZ, h);
     }
+  };
+  if (n_steps == L) {
+#pragma unroll
+    for (int s = 0; s < L; ++s) replay(s);
+  } else {
+#pragma unroll
+    for (int s = 0; s < L; ++s)
+      if (s < n_steps) replay(s);
   }
 }
 
@@ -514,6 +589,51 @@ struct NewtonMonoid {
   }
 };
 
+// Raw storage words of a tile's steps, held in registers between the two
+// passes: bf16 values packed two to a register, fp32 values one each.
+template <typename T>
+struct RowStash;
+
+template <>
+struct RowStash<bf16> {
+  static constexpr int N = 2;
+  // Slot g of the row at byte offset soff (+ g * slot bytes, wave-uniform).
+  static __device__ __forceinline__ void load(rsrc_t rs, uint32_t voff, uint32_t soff,
+                                              uint32_t slot, uint32_t w[N]) {
+    uint32_t v[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      v[g] = __builtin_amdgcn_raw_buffer_load_b16(rs, voff, soff + g * slot, 0);
+    w[0] = v[0] | (v[1] << 16);
+    w[1] = v[2] | (v[3] << 16);
+  }
+  static __device__ __forceinline__ void get(const uint32_t w[N], float p[4]) {
+    p[0] = lo_bf16(w[0]);
+    p[1] = hi_bf16(w[0]);
+    p[2] = lo_bf16(w[1]);
+    p[3] = hi_bf16(w[1]);
+  }
+};
+
+template <>
+struct RowStash<float> {
+  static constexpr int N = 4;
+  static __device__ __forceinline__ void load(rsrc_t rs, uint32_t voff, uint32_t soff,
+                                              uint32_t slot, uint32_t w[N]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      w[g] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff + g * slot, 0);
+  }
+  static __device__ __forceinline__ void get(const uint32_t w[N], float p[4]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) p[g] = __uint_as_float(w[g]);
+  }
+};
+
+// One Newton iteration over a tile of W waves x L steps x 64 channels.  Pass 1
+// reads each step once (wx and the guess, kept in registers) and folds the
+// lane's affine aggregate x -> J x + F; pass 2 replays the steps from the true
+// carry, delta_t = J_t delta_{t-1} + F_t, and writes H + omega delta.
 template <typename TX, typename TIN, typename TOUT, int L, int W>
 __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
@@ -521,57 +641,59 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
     float omega, float eps, int* __restrict__ counter, unsigned long long* __restrict__ agg,
     unsigned long long* __restrict__ incl, int epoch) {
   constexpr int KP = 1;  // predecessors per wave per look-back round
+  using XS = RowStash<TX>;
+  using HS = RowStash<TIN>;
   __shared__ float s_agg[W][20][kCB];
   __shared__ float s_carry[W][4][kCB];
   __shared__ LookbackShared<NewtonMonoid, W * KP> s_lb;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tile = take_ticket(counter);
   const TileId id = decode_tile(tile, B, n_cb);
-  const int ch = id.cb * kCB + lane;
-  const bool live = ch < d;
+  const int c0 = id.cb * kCB;
+  const bool live = c0 + lane < d;
   const int t0 = id.chunk * (W * L) + wave * L;
+  const int n_steps = max(0, min(L, T - t0));
   const size_t row4 = static_cast<size_t>(4) * d;
+  const size_t first = static_cast<size_t>(id.b) * T + t0;
+  // Per-slot byte offsets inside a (b, t, 4d) row for each storage type, and
+  // the bytes from the wave's base to its last live element.
+  const uint32_t vx = live ? lane * sizeof(TX) : kOOB;
+  const uint32_t vi = live ? lane * sizeof(TIN) : kOOB;
+  const uint32_t vo = live ? lane * sizeof(TOUT) : kOOB;
+  const size_t span = n_steps > 0 ? (n_steps - 1) * row4 + 3 * d + (d - c0) : 0;
 
   float r[4] = {0.f, 0.f, 0.f, 0.f};
-  if (live) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) r[g] = ld(rmix + g * d + ch);
-  }
   // Linearisation point H_{t0-1}: previous guess, h0 at t = 0, else zeros.
   float prev0[4] = {0.f, 0.f, 0.f, 0.f};
   if (live) {
-    if (t0 > 0 && t0 - 1 < T) {
-      const TIN* p = hin + (static_cast<size_t>(id.b) * T + (t0 - 1)) * row4 + ch;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) r[g] = ld(rmix + g * d + c0 + lane);
+    if (t0 > 0 && n_steps > 0) {
+      const TIN* p = hin + (first - 1) * row4 + c0 + lane;
 #pragma unroll
       for (int k = 0; k < 4; ++k) prev0[k] = ld(p + k * d);
     } else if (t0 == 0 && h0 != nullptr) {
-      const TX* p = h0 + static_cast<size_t>(id.b) * row4 + ch;
+      const TX* p = h0 + static_cast<size_t>(id.b) * row4 + c0 + lane;
 #pragma unroll
       for (int k = 0; k < 4; ++k) prev0[k] = ld(p + k * d);
     }
   }
-  // Inputs of step t are read in pass 1 and again in pass 2 (the second read
-  // hits the caches); nothing is held in registers across the look-back.
-  auto load_step = [&](int t, float x[4], float hv[4]) {
-    const size_t base = (static_cast<size_t>(id.b) * T + t) * row4 + ch;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      x[k] = ld(wx + base + k * d);
-      hv[k] = ld(hin + base + k * d);
-    }
-  };
-  const int t_end = min(t0 + L, T);
 
+  uint32_t xs[L][XS::N], hs[L][HS::N];
   // Pass 1: lane segment aggregate (A, b) of the affine maps x -> J x + F.
   Aff a;
   aff_identity(a);
-  if (live) {
+  {
+    const rsrc_t rx = make_rsrc(wx + first * row4 + c0, span * sizeof(TX));
+    const rsrc_t ri = make_rsrc(hin + first * row4 + c0, span * sizeof(TIN));
     float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
-#pragma unroll 4
-    for (int t = t0; t < t_end; ++t) {
+    auto step = [&](int s) {
+      XS::load(rx, vx, s * row4 * sizeof(TX), d * sizeof(TX), xs[s]);
+      HS::load(ri, vi, s * row4 * sizeof(TIN), d * sizeof(TIN), hs[s]);
       float x[4], hv[4];
-      load_step(t, x, hv);
+      XS::get(xs[s], x);
+      HS::get(hs[s], hv);
       const CellJ J = cell_jac(prev, x, r, eps);
       jmv(J, a.b);
       a.b[0] += J.pc - hv[0];
@@ -587,6 +709,14 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
       }
 #pragma unroll
       for (int k = 0; k < 4; ++k) prev[k] = hv[k];
+    };
+    if (n_steps == L) {
+#pragma unroll
+      for (int s = 0; s < L; ++s) step(s);
+    } else {
+#pragma unroll
+      for (int s = 0; s < L; ++s)
+        if (s < n_steps) step(s);
     }
   }
 #pragma unroll
@@ -648,23 +778,33 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
   float dl[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) dl[k] = s_carry[wave][k][lane];
-  if (live) {
+  {
+    const rsrc_t ro = make_rsrc(hout + first * row4 + c0, span * sizeof(TOUT));
     float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
-#pragma unroll 4
-    for (int t = t0; t < t_end; ++t) {
+    auto replay = [&](int s) {
       float x[4], hv[4];
-      load_step(t, x, hv);
+      XS::get(xs[s], x);
+      HS::get(hs[s], hv);
       const CellJ J = cell_jac(prev, x, r, eps);
       jmv(J, dl);
       dl[0] += J.pc - hv[0];
       dl[1] += J.pn - hv[1];
       dl[2] += J.pm - hv[2];
       dl[3] += J.ph - hv[3];
-      TOUT* op = hout + (static_cast<size_t>(id.b) * T + t) * row4 + ch;
+      const uint32_t so = s * row4 * sizeof(TOUT);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) st(op + k * d, add_rn(hv[k], mul_rn(omega, dl[k])));
+      for (int k = 0; k < 4; ++k)
+        stb<TOUT>(ro, vo, so + k * d * sizeof(TOUT), add_rn(hv[k], mul_rn(omega, dl[k])));
 #pragma unroll
       for (int k = 0; k < 4; ++k) prev[k] = hv[k];
+    };
+    if (n_steps == L) {
+#pragma unroll
+      for (int s = 0; s < L; ++s) replay(s);
+    } else {
+#pragma unroll
+      for (int s = 0; s < L; ++s)
+        if (s < n_steps) replay(s);
     }
   }
 }
@@ -686,8 +826,12 @@ constexpr int kMaxStages = 64;  // ticket counters per call
 struct Shape {
   int L, W;
 };
-static const Shape kFrozenShapes[] = {{64, 4}, {32, 8}, {128, 4}, {64, 8}};
-static const Shape kNewtonShapes[] = {{64, 4}, {32, 8}, {128, 4}, {32, 4}};
+// bf16 frozen tiles stash 2 registers per step, fp32 ones 4 (one fp32 shape).
+static const Shape kFrozenShapes[] = {{64, 4}, {32, 8}, {32, 4}, {64, 2}};
+constexpr Shape kFrozenF32{32, 4};
+// Newton tiles stash wx and the guess: 4 to 6 registers per step in bf16, 8 in fp32.
+static const Shape kNewtonShapes[] = {{16, 8}, {16, 4}, {24, 4}, {32, 8}};
+constexpr Shape kNewtonF32{16, 8};
 
 struct Tiles {
   Shape frozen, newton;
@@ -695,7 +839,7 @@ struct Tiles {
 
 static Tiles tiles() {
   static Tiles t = [] {
-    Tiles r{{64, 4}, {64, 4}};
+    Tiles r{{64, 4}, {16, 8}};
     if (const char* e = getenv("PRNN_SLSTM_TILES")) {
       int fl, fw, nl, nw;
       if (sscanf(e, "%dx%d,%dx%d", &fl, &fw, &nl, &nw) == 4) {
@@ -724,9 +868,14 @@ static Geo geometry(int B, int T, int d, Shape sh) {
 
 static size_t elem_size(int dtype) { return dtype == PRNN_BF16 ? 2 : 4; }
 
+static Shape frozen_shape(int dtype) { return dtype == PRNN_BF16 ? tiles().frozen : kFrozenF32; }
+static Shape newton_shape(int dtype) { return dtype == PRNN_BF16 ? tiles().newton : kNewtonF32; }
+
 static int check_dims(int B, int T, int d, int dtype) {
   if (B < 1 || T < 1 || d < 1)
     return fail(PRNN_ERR_VALUE, "B, T, d must be >= 1, got B=%d T=%d d=%d", B, T, d);
+  // A wave addresses its steps with 32-bit buffer offsets.
+  if (d >= (1 << 20)) return fail(PRNN_ERR_VALUE, "d must be < 2^20, got %d", d);
   if (dtype != PRNN_F32 && dtype != PRNN_BF16)
     return fail(PRNN_ERR_TYPE, "dtype code %d is not float32 (0) or bfloat16 (1)", dtype);
   const long long tiles = static_cast<long long>(B) * ((d + kCB - 1) / kCB) * T;
@@ -762,7 +911,7 @@ struct InitWs {
 };
 
 static InitWs carve_init(void* base, int B, int T, int d, int P, int dtype, size_t* total) {
-  const Geo g = geometry(B, T, d, tiles().frozen);
+  const Geo g = geometry(B, T, d, frozen_shape(dtype));
   Carver cv(base);
   InitWs w;
   w.lb = carve_lookback(cv, g, 3, 4);
@@ -778,8 +927,8 @@ struct NewtonWs {
   float* work[2];
 };
 
-static NewtonWs carve_newton(void* base, int B, int T, int d, int K, size_t* total) {
-  const Geo g = geometry(B, T, d, tiles().newton);
+static NewtonWs carve_newton(void* base, int B, int T, int d, int K, int dtype, size_t* total) {
+  const Geo g = geometry(B, T, d, newton_shape(dtype));
   Carver cv(base);
   NewtonWs w;
   w.lb = carve_lookback(cv, g, 4, 20);
@@ -812,6 +961,11 @@ template <typename TX>
 static void frozen_pass(bool has_h, bool full_out, const TX* wx, const TX* r, const TX* h0,
                         const TX* src, TX* out_full, TX* out_h, int B, int T, int d, float eps,
                         const Lookback& lb, int epoch, hipStream_t stream) {
+  if constexpr (sizeof(TX) == 4) {
+    return launch_frozen<TX, kFrozenF32.L, kFrozenF32.W>(has_h, full_out, wx, r, h0, src,
+                                                         out_full, out_h, B, T, d, eps, lb,
+                                                         epoch, stream);
+  } else {
   const Shape sh = tiles().frozen;
 #define PRNN_SHAPE(LL, WW)                                                                   \
   if (sh.L == LL && sh.W == WW)                                                              \
@@ -819,9 +973,10 @@ static void frozen_pass(bool has_h, bool full_out, const TX* wx, const TX* r, co
                                      d, eps, lb, epoch, stream);
   PRNN_SHAPE(64, 4)
   PRNN_SHAPE(32, 8)
-  PRNN_SHAPE(128, 4)
-  PRNN_SHAPE(64, 8)
+  PRNN_SHAPE(32, 4)
+  PRNN_SHAPE(64, 2)
 #undef PRNN_SHAPE
+  }
 }
 
 template <typename TX>
@@ -855,16 +1010,21 @@ template <typename TX, typename TIN, typename TOUT>
 static void launch_newton(const TX* wx, const TX* r, const TX* h0, const TIN* hin, TOUT* hout,
                           int B, int T, int d, float omega, float eps, const Lookback& lb,
                           int epoch, hipStream_t stream) {
+  if constexpr (sizeof(TX) == 4) {
+    return launch_newton_shape<TX, TIN, TOUT, kNewtonF32.L, kNewtonF32.W>(
+        wx, r, h0, hin, hout, B, T, d, omega, eps, lb, epoch, stream);
+  } else {
   const Shape sh = tiles().newton;
 #define PRNN_SHAPE(LL, WW)                                                                     \
   if (sh.L == LL && sh.W == WW)                                                                \
     return launch_newton_shape<TX, TIN, TOUT, LL, WW>(wx, r, h0, hin, hout, B, T, d, omega, eps, \
                                                       lb, epoch, stream);
-  PRNN_SHAPE(64, 4)
+  PRNN_SHAPE(16, 8)
+  PRNN_SHAPE(16, 4)
+  PRNN_SHAPE(24, 4)
   PRNN_SHAPE(32, 8)
-  PRNN_SHAPE(128, 4)
-  PRNN_SHAPE(32, 4)
 #undef PRNN_SHAPE
+  }
 }
 
 template <typename TX>
@@ -937,7 +1097,7 @@ extern "C" PRNN_API size_t prnn_slstm_newton_workspace_size(int B, int T, int d,
                                                             int dtype) {
   if (slstm::check_dims(B, T, d, dtype) != PRNN_OK || max_iters < 0) return 0;
   size_t total = 0;
-  slstm::carve_newton(nullptr, B, T, d, max_iters, &total);
+  slstm::carve_newton(nullptr, B, T, d, max_iters, dtype, &total);
   return total;
 }
 
@@ -954,7 +1114,7 @@ extern "C" PRNN_API int prnn_slstm_newton(const void* wx, const void* r, const v
     return fail(PRNN_ERR_VALUE, "wx, r, states, out and workspace must be non-null");
   if (out == states) return fail(PRNN_ERR_VALUE, "out must not alias states");
   size_t need = 0;
-  const slstm::NewtonWs w = slstm::carve_newton(workspace, B, T, d, max_iters, &need);
+  const slstm::NewtonWs w = slstm::carve_newton(workspace, B, T, d, max_iters, dtype, &need);
   if (workspace_bytes < need)
     return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
   hipStream_t s = static_cast<hipStream_t>(stream);
