@@ -156,15 +156,23 @@ def main() -> int:
 
     elems = B * T * D
     s_x = 2
-    # Algorithmic bytes per (b, t, channel) with s_x = bytes of the wx dtype:
-    # zero-hidden pass 4 s_x + 16 (read wx, write the state), each Picard pass
-    # 4 s_x + 20 (read wx and fp32 h_prev, write the state), each Newton
-    # iteration 4 s_x + 32 (read wx and the fp32 state, write the state).
-    picard_bytes = elems * (4 * s_x + 20)
-    newton_bytes = elems * (4 * s_x + 32)
+    # Algorithmic bytes per (b, t, channel) with s_x = bytes of the wx dtype
+    # (the per-element figures the workload is priced with): zero-hidden pass
+    # 4 s_x + 16, each Picard pass 4 s_x + 20, each Newton iteration
+    # 4 s_x + 32 (read wx and the fp32 state, write the state).
     step_bytes = elems * ((4 * s_x + 16) + P * (4 * s_x + 20) + K * (4 * s_x + 32))
-    ach_picard = picard_bytes / (ms_picard * 1e-3) / 1e9
+    newton_bytes = elems * (4 * s_x + 32)
+    # Compulsory I/O of this build's kernels, whose formats are narrower:
+    # a Newton iteration reads wx (8 B) and a bf16 guess (8 B) or fp32 work
+    # (16 B) and writes fp32 work (16 B) or the bf16 result (8 B): 32 B either
+    # way; a Picard pass reads wx (8 B) and bf16 h_prev (2 B) and writes bf16
+    # h (2 B).
+    newton_io = elems * 32
+    picard_io = elems * 12
     ach_newton = newton_bytes / (ms_newton * 1e-3) / 1e9
+    ach_picard = picard_io / (ms_picard * 1e-3) / 1e9
+    newton_share = K * ms_newton / ms
+    picard_share = (ms_initP - ms_init1) / ms  # the P - 1 h-only Picard launches
     out = {
         "metric": "Newton+scan fwd tokens/sec + % HBM roofline, ParaSLSTM diag d=1024 T=131072",
         "value": tokens / (ms * 1e-3),
@@ -184,19 +192,8 @@ def main() -> int:
                    "storage": "bf16 wx/states, fp32 Newton work",
                    "parallelism": "single GPU"},
         "roofline": {
-            "kernel": "slstm_frozen_kernel (Picard pass, h-only output; 4 of the 8 launches, "
-                      "largest time share)",
-            "bound": "hbm",
-            "achieved": ach_picard,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": ach_picard / HBM_PEAK_GBS,
-            "traffic": _traffic_from_profile("slstm_frozen_picard_cfg3.md"),
-            "algorithmic_bytes_per_launch": picard_bytes,
-            "avg_launch_ms": ms_picard,
-        },
-        "roofline_newton": {
-            "kernel": "slstm_newton_kernel (one Newton iteration)",
+            "kernel": f"slstm_newton_kernel (one Newton iteration; {K} launches, "
+                      f"{100 * newton_share:.0f}% of the step)",
             "bound": "hbm",
             "achieved": ach_newton,
             "peak": HBM_PEAK_GBS,
@@ -205,6 +202,21 @@ def main() -> int:
             "traffic": _traffic_from_profile("slstm_newton_cfg3.md"),
             "algorithmic_bytes_per_launch": newton_bytes,
             "avg_launch_ms": ms_newton,
+            "own_io_bytes_per_launch": newton_io,
+            "own_io_frac": newton_io / (ms_newton * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        },
+        "roofline_picard": {
+            "kernel": f"slstm_frozen_kernel (Picard pass, h-only output; {P - 1} launches, "
+                      f"{100 * picard_share:.0f}% of the step)",
+            "bound": "hbm",
+            "bytes_basis": "compulsory I/O of the kernel (12 B per element)",
+            "achieved": ach_picard,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": ach_picard / HBM_PEAK_GBS,
+            "traffic": _traffic_from_profile("slstm_frozen_picard_cfg3.md"),
+            "io_bytes_per_launch": picard_io,
+            "avg_launch_ms": ms_picard,
         },
         "step_algorithmic_GBps": step_bytes / (ms * 1e-3) / 1e9,
         "step_roofline_frac": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,

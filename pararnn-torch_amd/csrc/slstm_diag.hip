@@ -830,23 +830,27 @@ struct Shape {
 static const Shape kFrozenShapes[] = {{64, 4}, {32, 8}, {32, 4}, {64, 2}};
 constexpr Shape kFrozenF32{32, 4};
 // Newton tiles stash wx and the guess: 4 to 6 registers per step in bf16, 8 in fp32.
-static const Shape kNewtonShapes[] = {{16, 8}, {16, 4}, {24, 4}, {32, 8}};
+static const Shape kNewtonShapes[] = {{32, 8}, {32, 4}, {24, 4}, {16, 8}, {64, 4}};
 constexpr Shape kNewtonF32{16, 8};
 
 struct Tiles {
-  Shape frozen, newton;
+  Shape frozen;
+  Shape newton_guess;  // Newton launches that read the bf16 guess
+  Shape newton_work;   // Newton launches that read the fp32 work trajectory
 };
 
 static Tiles tiles() {
   static Tiles t = [] {
-    Tiles r{{64, 4}, {16, 8}};
+    Tiles r{{64, 4}, {32, 4}, {24, 4}};
     if (const char* e = getenv("PRNN_SLSTM_TILES")) {
-      int fl, fw, nl, nw;
-      if (sscanf(e, "%dx%d,%dx%d", &fl, &fw, &nl, &nw) == 4) {
+      int fl, fw, gl, gw, wl, ww;
+      if (sscanf(e, "%dx%d,%dx%d,%dx%d", &fl, &fw, &gl, &gw, &wl, &ww) == 6) {
         for (const Shape& s : kFrozenShapes)
           if (s.L == fl && s.W == fw) r.frozen = s;
-        for (const Shape& s : kNewtonShapes)
-          if (s.L == nl && s.W == nw) r.newton = s;
+        for (const Shape& s : kNewtonShapes) {
+          if (s.L == gl && s.W == gw) r.newton_guess = s;
+          if (s.L == wl && s.W == ww) r.newton_work = s;
+        }
       }
     }
     return r;
@@ -869,7 +873,11 @@ static Geo geometry(int B, int T, int d, Shape sh) {
 static size_t elem_size(int dtype) { return dtype == PRNN_BF16 ? 2 : 4; }
 
 static Shape frozen_shape(int dtype) { return dtype == PRNN_BF16 ? tiles().frozen : kFrozenF32; }
-static Shape newton_shape(int dtype) { return dtype == PRNN_BF16 ? tiles().newton : kNewtonF32; }
+// Shape of a Newton launch; `work_in` when it reads the fp32 work trajectory.
+static Shape newton_shape(int dtype, bool work_in) {
+  if (dtype != PRNN_BF16) return kNewtonF32;
+  return work_in ? tiles().newton_work : tiles().newton_guess;
+}
 
 static int check_dims(int B, int T, int d, int dtype) {
   if (B < 1 || T < 1 || d < 1)
@@ -928,7 +936,11 @@ struct NewtonWs {
 };
 
 static NewtonWs carve_newton(void* base, int B, int T, int d, int K, int dtype, size_t* total) {
-  const Geo g = geometry(B, T, d, newton_shape(dtype));
+  // Launches of one call share the look-back arrays: size them for the
+  // larger tile count of the two shapes.
+  const Geo g1 = geometry(B, T, d, newton_shape(dtype, false));
+  const Geo g2 = geometry(B, T, d, newton_shape(dtype, true));
+  const Geo& g = g1.n_tiles >= g2.n_tiles ? g1 : g2;
   Carver cv(base);
   NewtonWs w;
   w.lb = carve_lookback(cv, g, 4, 20);
@@ -1014,15 +1026,16 @@ static void launch_newton(const TX* wx, const TX* r, const TX* h0, const TIN* hi
     return launch_newton_shape<TX, TIN, TOUT, kNewtonF32.L, kNewtonF32.W>(
         wx, r, h0, hin, hout, B, T, d, omega, eps, lb, epoch, stream);
   } else {
-  const Shape sh = tiles().newton;
+  const Shape sh = newton_shape(PRNN_BF16, sizeof(TIN) == 4);
 #define PRNN_SHAPE(LL, WW)                                                                     \
   if (sh.L == LL && sh.W == WW)                                                                \
     return launch_newton_shape<TX, TIN, TOUT, LL, WW>(wx, r, h0, hin, hout, B, T, d, omega, eps, \
                                                       lb, epoch, stream);
-  PRNN_SHAPE(16, 8)
-  PRNN_SHAPE(16, 4)
-  PRNN_SHAPE(24, 4)
   PRNN_SHAPE(32, 8)
+  PRNN_SHAPE(32, 4)
+  PRNN_SHAPE(24, 4)
+  PRNN_SHAPE(16, 8)
+  PRNN_SHAPE(64, 4)
 #undef PRNN_SHAPE
   }
 }
