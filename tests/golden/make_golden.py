@@ -17,6 +17,9 @@ Reference call sites exercised (paths relative to the reference's src/pararnn):
   solvers/scan.py:82,103         scan_block4 / scan_dense
   cells/para_slstm.py:241        ParaSLSTM.step_with_jacobian
   cells/para_gru.py:344          ParaGRU.step_with_jacobian
+  solvers/newton/__init__.py:91  _NewtonFixedPoint (eq. 2.6 backward, eager)
+  solvers/scan.py:166            reverse_scan_block4
+  kernels/vjp_slstm.py:173       slstm_recurrence_vjp_eager
 """
 
 from __future__ import annotations
@@ -169,6 +172,64 @@ def parts_case():
     )
 
 
+def slstm_bwd_case(name, *, d_in, d, B, T, K, P, dtype, seed, with_h0=False):
+    """Gradients of sum(g * H) through newton_apply's eq. 2.6 backward."""
+    from pararnn import ParaSLSTM, newton_apply, sequential_apply
+
+    torch.manual_seed(seed)
+    cell = ParaSLSTM(d_in, d, mix="diag").to(dtype)
+    gen = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(B, T, d_in, generator=gen).to(dtype)
+    grad = torch.randn(B, T, 4, d, generator=gen).to(dtype)
+    tensors = {}
+    h0 = None
+    if with_h0:
+        xp = torch.randn(B, 16, d_in, generator=gen).to(dtype)
+        with torch.no_grad():
+            h0 = sequential_apply(cell, xp)[:, -1].clone()
+        tensors["h0"] = h0.clone()
+        h0 = h0.requires_grad_(True)
+    xg = x.clone().requires_grad_(True)
+    H = newton_apply(cell, xg, _cfg(K, P), h0=h0)
+    (H.float() * grad.float()).sum().backward()
+    tensors.update(
+        x=x, W=cell.W_x.weight.detach(), b=cell.W_x.bias.detach(), R=cell.R.detach(),
+        grad=grad, newton=H.detach(),
+        grad_x=xg.grad, grad_W=cell.W_x.weight.grad, grad_b=cell.W_x.bias.grad,
+        grad_R=cell.R.grad,
+    )
+    if with_h0:
+        tensors["grad_h0"] = h0.grad
+    meta = dict(cell="ParaSLSTM", mix="diag", d_in=d_in, d=d, B=B, T=T, K=K, P=P,
+                dtype=str(dtype).replace("torch.", ""), seed=seed, eps=cell.eps,
+                max_recurrent_norm=cell.max_recurrent_norm, h0=with_h0,
+                loss="sum(grad.float() * H.float())")
+    _save(name, tensors, meta)
+
+
+def bwd_parts_case():
+    """The reverse 4x4 scan and the packed sLSTM cell VJP on random operands."""
+    from pararnn.kernels.vjp_slstm import slstm_recurrence_vjp_eager
+    from pararnn.solvers.scan import reverse_scan_block4
+
+    g = torch.Generator().manual_seed(4321)
+    jb = torch.randn(2, 41, 4, 4, 8, generator=g) * 0.6
+    pb = torch.randn(2, 41, 4, 8, generator=g)
+    mu = reverse_scan_block4(jb, pb)
+    state = torch.randn(2, 33, 4, 16, generator=g)
+    state[..., 1, :] = state[..., 1, :].abs() + 0.1
+    wx = torch.randn(2, 33, 64, generator=g)
+    r = torch.randn(4, 16, generator=g) * 0.3
+    vmu = torch.randn(2, 33, 4, 16, generator=g)
+    g_wx, g_r = slstm_recurrence_vjp_eager(state, wx, r, vmu, 1e-6)
+    _save(
+        "bwd_parts",
+        dict(rev4_j=jb, rev4_p=pb, rev4_mu=mu, vjp_state=state, vjp_wx=wx, vjp_r=r, vjp_mu=vmu,
+             vjp_gwx=g_wx, vjp_gr=g_r),
+        dict(eps=1e-6),
+    )
+
+
 def auto_picard_table():
     from pararnn.solvers.newton.picard import slstm_auto_picard
 
@@ -193,6 +254,11 @@ def main() -> int:
                   dtype=torch.float32, seed=4, with_h0=True)
     gru_head_case("gru_head_bf16", d_in=64, n_heads=2, d_head=64, B=1, T=128, K=3,
                   dtype=torch.bfloat16, seed=6)
+    bwd_parts_case()
+    slstm_bwd_case("slstm_bwd_fp32", d_in=24, d=32, B=2, T=256, K=3, P=3,
+                   dtype=torch.float32, seed=7, with_h0=True)
+    slstm_bwd_case("slstm_bwd_bf16", d_in=32, d=32, B=2, T=256, K=2, P=3,
+                   dtype=torch.bfloat16, seed=8)
     with open(os.path.join(HERE, "auto_picard.json"), "w") as f:
         json.dump(auto_picard_table(), f, indent=1)
     return 0

@@ -1,0 +1,87 @@
+"""The CPU oracle of the eq. 2.6 backward against the reference's golden vectors
+and against autograd through the sequential unroll (float64)."""
+
+import pytest
+import torch
+from conftest import load_golden
+
+from oracle.backward import reverse_scan_block4, slstm_backward, slstm_cell_vjp
+from oracle.scan import sequential_affine
+from oracle.slstm import SLSTMParams, slstm_newton, slstm_sequential
+
+
+def _params(t, m, dtype=None):
+    W, b, R = t["W"], t["b"], t["R"]
+    if dtype is not None:
+        W, b, R = W.to(dtype), b.to(dtype), R.to(dtype)
+    return SLSTMParams(W, b, R, eps=m["eps"], cap=m["max_recurrent_norm"])
+
+
+def test_bwd_parts_match_reference():
+    t, m = load_golden("bwd_parts")
+    mu = reverse_scan_block4(t["rev4_j"], t["rev4_p"])
+    assert torch.allclose(mu, t["rev4_mu"], rtol=0, atol=2e-6)
+    g_wx, g_r = slstm_cell_vjp(t["vjp_state"], t["vjp_wx"], t["vjp_r"], t["vjp_mu"], m["eps"])
+    assert torch.equal(g_wx, t["vjp_gwx"])
+    assert torch.allclose(g_r, t["vjp_gr"], rtol=1e-6, atol=1e-6)
+
+
+def test_reverse_scan_is_the_adjoint_recursion():
+    # mu_t = p_t + J_{t+1}^T mu_{t+1}, walked backwards in float64.
+    g = torch.Generator().manual_seed(3)
+    j = torch.randn(2, 23, 4, 4, 5, generator=g, dtype=torch.float64) * 0.5
+    p = torch.randn(2, 23, 4, 5, generator=g, dtype=torch.float64)
+    mu = reverse_scan_block4(j, p)
+    ref = torch.empty_like(p)
+    ref[:, -1] = p[:, -1]
+    for t in range(21, -1, -1):
+        ref[:, t] = p[:, t] + (j[:, t + 1] * ref[:, t + 1].unsqueeze(-2)).sum(dim=-3)
+    assert torch.allclose(mu, ref, rtol=0, atol=1e-12)
+    # and it is the transpose of the forward solve: <mu, r> = <p, delta>
+    r = torch.randn(2, 23, 4, 5, generator=g, dtype=torch.float64)
+    j_fwd = j.clone()
+    j_fwd[:, 0] = 0
+    delta = sequential_affine(j_fwd, r, "block4")
+    assert torch.allclose((mu * r).sum(), (p * delta).sum(), rtol=1e-12)
+
+
+@pytest.mark.parametrize("with_h0", [False, True])
+def test_backward_matches_autograd_through_sequential_float64(with_h0):
+    g = torch.Generator().manual_seed(11)
+    B, T, d, din = 2, 40, 8, 6
+    f64 = dict(dtype=torch.float64)
+    W = torch.randn(4 * d, din, generator=g, **f64) * 0.3
+    b = torch.randn(4 * d, generator=g, **f64) * 0.1
+    R = torch.randn(4, d, generator=g, **f64) * 0.4  # some entries beyond the 0.5 clamp
+    x = torch.randn(B, T, din, generator=g, **f64)
+    h0 = torch.randn(B, 4, d, generator=g, **f64).abs() if with_h0 else None
+    up = torch.randn(B, T, 4, d, generator=g, **f64)
+    leaves = [t.clone().requires_grad_(True) for t in (x, W, b, R)]
+    h0l = h0.clone().requires_grad_(True) if with_h0 else None
+    H = slstm_sequential(SLSTMParams(leaves[1], leaves[2], leaves[3]), leaves[0], h0=h0l)
+    grads = torch.autograd.grad((H * up).sum(), leaves + ([h0l] if with_h0 else []))
+    out = slstm_backward(SLSTMParams(W, b, R), x, H.detach(), up, h0=h0, work=torch.float64)
+    names = ["x", "W", "b", "R"] + (["h0"] if with_h0 else [])
+    for name, ref in zip(names, grads):
+        assert torch.allclose(out[name], ref, rtol=1e-10, atol=1e-10), name
+    assert (R.abs() > 0.5).any() and (out["R"][R.abs() > 0.5] == 0).all()
+
+
+@pytest.mark.parametrize("name", ["slstm_bwd_fp32", "slstm_bwd_bf16"])
+def test_backward_matches_reference(name):
+    t, m = load_golden(name)
+    dtype = getattr(torch, m["dtype"])
+    p = _params(t, m)
+    h0 = t.get("h0")
+    x = t["x"]
+    # forward: the same K, P iterate as the reference
+    H = slstm_newton(p, x, max_iters=m["K"], picard_iters=m["P"], h0=h0)
+    assert torch.equal(H, t["newton"])
+    out = slstm_backward(p, x, t["newton"], t["grad"], h0=h0)
+    for k in ["x", "W", "b", "R"] + (["h0"] if m["h0"] else []):
+        ref = t[f"grad_{k}"]
+        assert out[k].dtype == ref.dtype, k
+        scale = ref.float().abs().max().item()
+        tol = 1e-5 if dtype == torch.float32 else 0
+        err = (out[k].float() - ref.float()).abs().max().item()
+        assert err <= tol * max(1.0, scale), (k, err, scale)
