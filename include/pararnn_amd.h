@@ -26,6 +26,11 @@
  *                            torch.library op pararnn::newton_slstm_fused
  *   prnn_gru_head_newton  -> kernels/custom_ops.py:311-358
  *                            torch.library op pararnn::newton_gru_head_fused
+ *   prnn_slstm_backward   -> solvers/newton/__init__.py:765-866 (_eq26_vjp, diag
+ *                            sLSTM path): reverse_scan_block4 (solvers/scan.py:
+ *                            166-178) + slstm_recurrence_vjp (kernels/
+ *                            vjp_slstm.py:209-240) + _t0_state_vjp
+ *                            (solvers/newton/dispatch.py:406-410)
  */
 #ifndef PARARNN_AMD_H
 #define PARARNN_AMD_H
@@ -84,6 +89,22 @@ PRNN_API int prnn_gru_head_newton(const void* wx, const void* a_z, const void* a
                                   const void* a_n, const void* h0, void* out, int B, int T,
                                   int n_heads, int d_head, int max_iters, float omega, int dtype,
                                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* Eq. 2.6 backward at the solved trajectory `states` = H* (B, T, 4, d) with
+ * upstream gradient `grad` = dL/dH (B, T, 4, d):
+ *   mu_{T-1} = grad_{T-1},  mu_t = grad_t + J_{t+1}^T mu_{t+1}  (fp32),
+ * then the VJP of every step f(H*_{t-1}, wx_t) with mu_t:
+ *   g_wx (B, T, 4d), dtype `dtype`:  dL/dwx (the W_x GEMMs stay with the caller);
+ *   g_r  (4, d) fp32:                sum over (b, t) of dL/dz_g * h_{t-1}, before
+ *                                    the caller's clamp mask on R;
+ *   g_h0 (B, 4, d) fp32 or NULL:     J_0^T mu_0 (gradient of h0).
+ * h0 as in the forward (NULL = zeros).  g_r is deterministic (fixed-order sums).
+ */
+PRNN_API size_t prnn_slstm_backward_workspace_size(int B, int T, int d, int dtype);
+PRNN_API int prnn_slstm_backward(const void* wx, const void* r, const void* h0,
+                                 const void* states, const void* grad, void* g_wx, float* g_r,
+                                 float* g_h0, int B, int T, int d, float eps, int dtype,
+                                 void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

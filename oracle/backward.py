@@ -80,14 +80,17 @@ def slstm_cell_vjp(state_prev: Tensor, wx: Tensor, r: Tensor, mu: Tensor, eps: f
 
 
 def slstm_backward(p: SLSTMParams, x: Tensor, states: Tensor, grad: Tensor,
-                   h0: Tensor | None = None, work: torch.dtype = torch.float32) -> dict:
+                   h0: Tensor | None = None, work: torch.dtype = torch.float32,
+                   wx: Tensor | None = None) -> dict:
     """Gradients of ``sum(grad * H)`` for ``H = newton_apply(cell, x)`` at ``H* = states``.
 
     Returns ``x``, ``W``, ``b``, ``R`` and (when ``h0`` is given) ``h0``
     gradients plus the intermediates ``mu`` and ``g_wx``, every tensor in the
-    dtype the reference produces it in.
+    dtype the reference produces it in.  ``wx`` overrides ``W_x(x)`` (to
+    evaluate at exactly the projection a caller used).
     """
-    wx = p.wx(x)
+    if wx is None:
+        wx = p.wx(x)
     h_prev = prepend(states, h0)
     _, jac = slstm_jacobian(p, h_prev, wx)
     mu = reverse_scan_block4(jac, grad)

@@ -1,0 +1,414 @@
+// Eq. 2.6 backward of the ParaSLSTM mix='diag' Newton solve for gfx950.
+//
+// Given the solved trajectory H* and the upstream gradient g = dL/dH, the
+// adjoint mu solves the reverse recursion
+//     mu_{T-1} = g_{T-1},   mu_t = g_t + J_{t+1}^T mu_{t+1},
+// and the parameter / input gradients are the cell VJP of every step with its
+// mu.  One kernel does both: a reverse chunked scan with the same tile
+// schedule and decoupled look-back as the forward Newton kernel, with time
+// chunks taken from the end, and the cell VJP fused into its second pass.
+//
+// The carry between segments is nu_t = J_t^T mu_t (so mu_{t-1} = g_{t-1} +
+// nu_t and nu_T = 0): a segment [t0, t1) maps nu_{t1} -> nu_{t0} through the
+// affine steps nu <- J_t^T (nu + g_t), t = t1-1 ... t0, whose aggregate
+// (A, b) composes on the same 4x4 affine monoid as the forward solve.  In
+// pass 2, nu_t falls out of the VJP itself: with d_* the adjoints of the
+// step's intermediates, nu = (d_c' f, d_n' f, d_zf, sum_g r_g d_zg), and
+// nu_0 = J_0^T mu_0 is the gradient of h0.
+//
+// Outputs: g_wx = d L / d wx (B, T, 4d) in the storage dtype, the per-tile
+// partial sums of d_zg * h_{t-1} (reduced by a second kernel into
+// g_r (4, d) fp32, before the clamp mask), and g_h0 (B, 4, d) fp32.
+//
+// Reference: solvers/newton/__init__.py:91-190, 765-866 (eq. 2.6),
+// solvers/scan.py:166-178 (reverse block-4 scan), kernels/vjp_slstm.py:173-240
+// (cell VJP), solvers/newton/dispatch.py:406-410 (h0 adjoint).
+#include "slstm_scan.h"
+
+namespace prnn {
+namespace slstm {
+
+// v <- J^T v
+__device__ __forceinline__ void jtmv(const CellJ& J, float v[4]) {
+  const float c = v[0], n = v[1], m = v[2], h = v[3];
+  v[0] = J.f * c + J.hc * h;
+  v[1] = J.f * n + J.hn * h;
+  v[2] = J.cm * c + J.nm * n + J.al * m + J.hm * h;
+  v[3] = J.ch * c + J.nh * n + J.mh * m + J.hh * h;
+}
+
+// VJP of one step f(prev, x) with adjoint mu: the four pre-activation
+// adjoints dz = dL/d(z_i, z_f, z_z, z_o) (= dL/dwx) and nu = J^T mu.
+__device__ __forceinline__ void cell_vjp(const float prev[4], const float x[4], const float r[4],
+                                         float eps, const float mu[4], float dz[4],
+                                         float nu[4]) {
+  const float c = prev[0], n = prev[1], m = prev[2], h = prev[3];
+  const float zi = add_rn(x[0], mul_rn(r[0], h));
+  const float zf = add_rn(x[1], mul_rn(r[1], h));
+  const float zz = add_rn(x[2], mul_rn(r[2], h));
+  const float zo = add_rn(x[3], mul_rn(r[3], h));
+  const float left = zf + m;
+  // d max(left, z_i) / d left, ties split 0.5 / 0.5 (para_slstm.py:530-534).
+  const float al = left > zi ? 1.f : (left == zi ? 0.5f : 0.f);
+  const float e = fexp(-fabsf(left - zi));
+  const bool lf = left >= zi;
+  const float f = lf ? 1.f : e;
+  const float i = lf ? e : 1.f;
+  const float z = ftanh(zz);
+  const float nn = f * n + i;
+  const float cn = f * c + i * z;
+  const float o = fsigmoid(zo);
+  const float inv_den = frcp(nn + eps);
+  const float t1 = mu[3] * inv_den;
+  const float d_o = t1 * cn;
+  const float d_cn = mu[0] + t1 * o;
+  const float d_nn = mu[1] - t1 * o * cn * inv_den;
+  const float d_f = d_cn * c + d_nn * n;
+  const float d_i = d_cn * z + d_nn;
+  const float d_mn = mu[2] - d_i * i - d_f * f;
+  dz[0] = d_i * i + d_mn * (1.f - al);
+  dz[1] = d_f * f + d_mn * al;
+  dz[2] = d_cn * i * (1.f - z * z);
+  dz[3] = d_o * o * (1.f - o);
+  nu[0] = d_cn * f;
+  nu[1] = d_nn * f;
+  nu[2] = dz[1];
+  nu[3] = r[0] * dz[0] + r[1] * dz[1] + r[2] * dz[2] + r[3] * dz[3];
+}
+
+template <typename TX, int L, int W>
+__global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
+    const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
+    const TX* __restrict__ states, const TX* __restrict__ grad, TX* __restrict__ gwx,
+    float* __restrict__ gr_part, float* __restrict__ gh0, int B, int T, int d, int n_cb,
+    int n_chunks, float eps, int* __restrict__ counter, unsigned long long* __restrict__ agg,
+    unsigned long long* __restrict__ incl, int epoch) {
+  constexpr int KP = 1;  // predecessors per wave per look-back round
+  using RS = RowStash<TX>;
+  constexpr uint32_t SZ = sizeof(TX);
+  __shared__ float s_agg[W][20][kCB];
+  __shared__ float s_carry[W][4][kCB];
+  __shared__ LookbackShared<NewtonMonoid, W * KP> s_lb;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tile = take_ticket(counter);
+  const TileId id = decode_tile(tile, B, n_cb);  // id.chunk counts from the end of time
+  const int tc = n_chunks - 1 - id.chunk;
+  const int c0 = id.cb * kCB;
+  const bool live = c0 + lane < d;
+  const int t0 = tc * (W * L) + wave * L;
+  const int n_steps = max(0, min(L, T - t0));
+  const size_t row4 = static_cast<size_t>(4) * d;
+  const size_t first = static_cast<size_t>(id.b) * T + t0;
+  const uint32_t voff = live ? lane * SZ : kOOB;
+  const uint32_t slot = d * SZ;
+  const uint32_t span = n_steps > 0 ? ((n_steps - 1) * row4 + 3 * d + (d - c0)) * SZ : 0;
+
+  float r[4] = {0.f, 0.f, 0.f, 0.f};
+  float prev0[4] = {0.f, 0.f, 0.f, 0.f};  // H*_{t0-1}: states, h0 at t = 0, else zeros
+  if (live) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) r[g] = ld(rmix + g * d + c0 + lane);
+    if (t0 > 0 && n_steps > 0) {
+      const TX* p = states + (first - 1) * row4 + c0 + lane;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) prev0[k] = ld(p + k * d);
+    } else if (t0 == 0 && h0 != nullptr) {
+      const TX* p = h0 + static_cast<size_t>(id.b) * row4 + c0 + lane;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) prev0[k] = ld(p + k * d);
+    }
+  }
+
+  // Registers: H*_{t-1} (step s >= 1; step 0 uses prev0), wx_t and g_t.
+  uint32_t hs[L][RS::N], xs[L][RS::N], gs[L][RS::N];
+  const rsrc_t rh = make_rsrc(states + first * row4 + c0, span);
+  const rsrc_t rx = make_rsrc(wx + first * row4 + c0, span);
+  const rsrc_t rg = make_rsrc(grad + first * row4 + c0, span);
+  auto prev_of = [&](int s, float p[4]) {
+    if (s == 0) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) p[k] = prev0[k];
+    } else {
+      RS::get(hs[s], p);
+    }
+  };
+
+  // Pass 1: the segment's map nu_{t1} -> nu_{t0}, steps from the last down.
+  Aff a;
+  aff_identity(a);
+  {
+    auto step = [&](int s) {
+      const uint32_t so = s * row4 * SZ;
+      RS::load(rx, voff, so, slot, xs[s]);
+      RS::load(rg, voff, so, slot, gs[s]);
+      if (s > 0) RS::load(rh, voff, so - row4 * SZ, slot, hs[s]);
+      float prev[4], x[4], g[4];
+      prev_of(s, prev);
+      RS::get(xs[s], x);
+      RS::get(gs[s], g);
+      const CellJ J = cell_jac(prev, x, r, eps);
+      float v[4] = {a.b[0] + g[0], a.b[1] + g[1], a.b[2] + g[2], a.b[3] + g[3]};
+      jtmv(J, v);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) a.b[k] = v[k];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float col[4] = {a.A[0][j], a.A[1][j], a.A[2][j], a.A[3][j]};
+        jtmv(J, col);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) a.A[k][j] = col[k];
+      }
+    };
+    if (n_steps == L) {
+#pragma unroll
+      for (int s = L - 1; s >= 0; --s) step(s);
+    } else {
+#pragma unroll
+      for (int s = L - 1; s >= 0; --s)
+        if (s < n_steps) step(s);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s_agg[wave][16 + i][lane] = a.b[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s_agg[wave][4 * i + j][lane] = a.A[i][j];
+  }
+  __syncthreads();
+
+  auto wave_map = [&](int w, Aff& sw) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sw.b[i] = s_agg[w][16 + i][lane];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sw.A[i][j] = s_agg[w][4 * i + j][lane];
+    }
+  };
+  float carry[4] = {0.f, 0.f, 0.f, 0.f};  // nu entering the tile from later time (0 at T)
+  if (wave == 0 && id.chunk > 0) {
+    // Scan order inside the tile runs from the last wave to the first.
+    Aff tile_agg;
+    wave_map(W - 1, tile_agg);
+#pragma unroll
+    for (int w = W - 2; w >= 0; --w) {
+      Aff sw;
+      wave_map(w, sw);
+      tile_agg = aff_compose(tile_agg, sw);
+    }
+    unsigned long long* ap = agg + (static_cast<size_t>(tile) * 20) * kCB + lane;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      st_tagged(ap + (16 + i) * kCB, tile_agg.b[i], epoch);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) st_tagged(ap + (4 * i + j) * kCB, tile_agg.A[i][j], epoch);
+    }
+  }
+  if (id.chunk > 0)
+    windowed_lookback<NewtonMonoid, W, KP>(id, B, n_cb, epoch, incl, agg, lane, wave, s_lb,
+                                           carry);
+  if (wave == 0) {
+#pragma unroll
+    for (int w = W - 1; w >= 0; --w) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) s_carry[w][k][lane] = carry[k];
+      Aff sw;
+      wave_map(w, sw);
+      aff_apply(sw, carry);
+    }
+    unsigned long long* ip = incl + (static_cast<size_t>(tile) * 4) * kCB + lane;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) st_tagged(ip + k * kCB, carry[k], epoch);
+  }
+  __syncthreads();
+
+  // Pass 2: mu_t = g_t + nu_{t+1}, the cell VJP of step t, nu_t = J_t^T mu_t.
+  float nu[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) nu[k] = s_carry[wave][k][lane];
+  float gr[4] = {0.f, 0.f, 0.f, 0.f};
+  {
+    const rsrc_t ro = make_rsrc(gwx + first * row4 + c0, span);
+    auto replay = [&](int s) {
+      float prev[4], x[4], g[4], mu[4], dz[4];
+      prev_of(s, prev);
+      RS::get(xs[s], x);
+      RS::get(gs[s], g);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) mu[k] = g[k] + nu[k];
+      cell_vjp(prev, x, r, eps, mu, dz, nu);
+      const uint32_t so = s * row4 * SZ;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        stb<TX>(ro, voff, so + k * slot, dz[k]);
+        gr[k] += dz[k] * prev[3];
+      }
+    };
+    if (n_steps == L) {
+#pragma unroll
+      for (int s = L - 1; s >= 0; --s) replay(s);
+    } else {
+#pragma unroll
+      for (int s = L - 1; s >= 0; --s)
+        if (s < n_steps) replay(s);
+    }
+  }
+  if (gh0 != nullptr && t0 == 0 && live) {
+    float* p = gh0 + static_cast<size_t>(id.b) * row4 + c0 + lane;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) p[k * d] = nu[k];
+  }
+  // Tile partial of sum_t dz_g * h_{t-1}: waves through LDS (s_agg is free).
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) s_agg[wave][k][lane] = gr[k];
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) acc += s_agg[w][k][lane];
+      gr_part[(static_cast<size_t>(tile) * 4 + k) * kCB + lane] = acc;
+    }
+  }
+}
+
+// g_r[g][ch] = sum over the tiles of ch's (b, channel block) of the partials,
+// in a fixed order (deterministic).
+__global__ void slstm_gr_reduce_kernel(const float* __restrict__ gr_part, float* __restrict__ gr,
+                                       int B, int d, int n_cb, int n_chunks) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= 4 * d) return;
+  const int g = idx / d, ch = idx - g * d;
+  const int cb = ch / kCB, lane = ch - cb * kCB;
+  float acc = 0.f;
+  for (int c = 0; c < n_chunks; ++c)
+    for (int b = 0; b < B; ++b) {
+      const size_t tile = (static_cast<size_t>(c) * B + b) * n_cb + cb;
+      acc += gr_part[(tile * 4 + g) * kCB + lane];
+    }
+  gr[idx] = acc;
+}
+
+}  // namespace slstm
+}  // namespace prnn
+
+// ===========================================================================
+// Host entry points
+// ===========================================================================
+namespace prnn {
+namespace slstm {
+
+// Backward tiles stash H*_{t-1}, wx and g: 6 registers per step in bf16,
+// 12 in fp32.  PRNN_SLSTM_BWD_TILES="<L>x<W>" overrides the bf16 shape for
+// tuning runs (instantiated shapes only).
+static const Shape kBwdShapes[] = {{16, 8}, {16, 4}, {24, 4}, {32, 4}};
+constexpr Shape kBwdF32{8, 8};
+
+static Shape bwd_shape(int dtype) {
+  static Shape s = [] {
+    Shape r{16, 8};
+    if (const char* e = getenv("PRNN_SLSTM_BWD_TILES")) {
+      int l, w;
+      if (sscanf(e, "%dx%d", &l, &w) == 2)
+        for (const Shape& c : kBwdShapes)
+          if (c.L == l && c.W == w) r = c;
+    }
+    return r;
+  }();
+  return dtype == PRNN_BF16 ? s : kBwdF32;
+}
+
+struct BwdWs {
+  Lookback lb;
+  float* gr_part;
+};
+
+static BwdWs carve_bwd(void* base, int B, int T, int d, int dtype, size_t* total) {
+  const Geo g = geometry(B, T, d, bwd_shape(dtype));
+  Carver cv(base);
+  BwdWs w;
+  w.lb = carve_lookback(cv, g, 4, 20);
+  w.gr_part = static_cast<float*>(cv.take(sizeof(float) * 4 * kCB * g.n_tiles));
+  *total = cv.used;
+  return w;
+}
+
+template <typename TX, int L, int W>
+static void launch_reverse(const TX* wx, const TX* r, const TX* h0, const TX* states,
+                           const TX* grad, TX* gwx, float* gh0, int B, int T, int d, float eps,
+                           const BwdWs& w, hipStream_t stream) {
+  const Geo g = geometry(B, T, d, Shape{L, W});
+  slstm_reverse_kernel<TX, L, W><<<dim3(g.n_tiles), dim3(64 * W), 0, stream>>>(
+      wx, r, h0, states, grad, gwx, w.gr_part, gh0, B, T, d, g.n_cb, g.n_chunks, eps,
+      w.lb.counters + 1, w.lb.agg, w.lb.incl, 1);
+}
+
+template <typename TX>
+static int run_bwd(const TX* wx, const TX* r, const TX* h0, const TX* states, const TX* grad,
+                   TX* gwx, float* gr, float* gh0, int B, int T, int d, float eps,
+                   const BwdWs& w, hipStream_t stream) {
+  int rc = clear_words(w.lb.counters, w.lb.clear_words, stream);
+  if (rc != PRNN_OK) return rc;
+  Shape sh;
+  if constexpr (sizeof(TX) == 4) {
+    sh = kBwdF32;
+    launch_reverse<TX, kBwdF32.L, kBwdF32.W>(wx, r, h0, states, grad, gwx, gh0, B, T, d, eps, w,
+                                             stream);
+  } else {
+    sh = bwd_shape(PRNN_BF16);
+#define PRNN_SHAPE(LL, WW)                                                                    \
+  if (sh.L == LL && sh.W == WW)                                                               \
+    launch_reverse<TX, LL, WW>(wx, r, h0, states, grad, gwx, gh0, B, T, d, eps, w, stream);
+    PRNN_SHAPE(16, 8)
+    PRNN_SHAPE(16, 4)
+    PRNN_SHAPE(24, 4)
+    PRNN_SHAPE(32, 4)
+#undef PRNN_SHAPE
+  }
+  PRNN_HIP(hipGetLastError());
+  const Geo g = geometry(B, T, d, sh);
+  const int n = 4 * d;
+  slstm_gr_reduce_kernel<<<dim3((n + 255) / 256), dim3(256), 0, stream>>>(w.gr_part, gr, B, d,
+                                                                         g.n_cb, g.n_chunks);
+  PRNN_HIP(hipGetLastError());
+  return PRNN_OK;
+}
+
+}  // namespace slstm
+}  // namespace prnn
+
+using namespace prnn;
+
+extern "C" PRNN_API size_t prnn_slstm_backward_workspace_size(int B, int T, int d, int dtype) {
+  if (slstm::check_dims(B, T, d, dtype) != PRNN_OK) return 0;
+  size_t total = 0;
+  slstm::carve_bwd(nullptr, B, T, d, dtype, &total);
+  return total;
+}
+
+extern "C" PRNN_API int prnn_slstm_backward(const void* wx, const void* r, const void* h0,
+                                            const void* states, const void* grad, void* gwx,
+                                            float* gr, float* gh0, int B, int T, int d, float eps,
+                                            int dtype, void* workspace, size_t workspace_bytes,
+                                            void* stream) {
+  int rc = slstm::check_dims(B, T, d, dtype);
+  if (rc != PRNN_OK) return rc;
+  if (!wx || !r || !states || !grad || !gwx || !gr || !workspace)
+    return fail(PRNN_ERR_VALUE, "wx, r, states, grad, g_wx, g_r and workspace must be non-null");
+  size_t need = 0;
+  const slstm::BwdWs w = slstm::carve_bwd(workspace, B, T, d, dtype, &need);
+  if (workspace_bytes < need)
+    return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == PRNN_F32)
+    return slstm::run_bwd(static_cast<const float*>(wx), static_cast<const float*>(r),
+                          static_cast<const float*>(h0), static_cast<const float*>(states),
+                          static_cast<const float*>(grad), static_cast<float*>(gwx), gr, gh0, B,
+                          T, d, eps, w, s);
+  return slstm::run_bwd(static_cast<const bf16*>(wx), static_cast<const bf16*>(r),
+                        static_cast<const bf16*>(h0), static_cast<const bf16*>(states),
+                        static_cast<const bf16*>(grad), static_cast<bf16*>(gwx), gr, gh0, B, T, d,
+                        eps, w, s);
+}

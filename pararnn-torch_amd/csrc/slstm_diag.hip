@@ -26,156 +26,13 @@
 //     on the affine monoid (A, b) -> (J A, J b + F); H_t += omega delta_t.
 //     Reference: cells/para_slstm.py:347-446, solvers/scan.py:82-100,
 //     solvers/newton/__init__.py:516-543, kernels/newton_slstm.py:886-966.
-#include "prnn_common.h"
-#include "pararnn_amd.h"
-#include "prnn_host.h"
+#include "slstm_scan.h"
 
 #include <stdio.h>
 #include <stdlib.h>
 
 namespace prnn {
 namespace slstm {
-
-constexpr int kCB = 64;  // channels per tile (one per lane)
-
-struct TileId {
-  int b, cb, chunk, rem;
-};
-
-__device__ __forceinline__ TileId decode_tile(int tile, int B, int n_cb) {
-  const int per = B * n_cb;
-  TileId t;
-  t.chunk = tile / per;
-  t.rem = tile - t.chunk * per;
-  t.b = t.rem / n_cb;
-  t.cb = t.rem - t.b * n_cb;
-  return t;
-}
-
-__device__ __forceinline__ int take_ticket(int* counter) {
-  __shared__ int s_ticket;
-  if (threadIdx.x == 0)
-    s_ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  return __builtin_amdgcn_readfirstlane(s_ticket);  // wave-uniform
-}
-
-
-// ---------------------------------------------------------------------------
-// Windowed decoupled look-back.
-//
-// Called by every wave of a tile with chunk > 0 (it contains barriers).  Each
-// lane (channel) keeps its own position; in one round every wave w fetches
-// predecessor (position - w) for every lane -- W predecessors per memory round
-// trip -- and stages its status and payload in LDS; wave 0 then folds them in
-// nearest-first: an inclusive carry ends the walk, an aggregate is absorbed
-// and the walk continues, a predecessor with nothing published yet stops the
-// round (retried next round).  On return wave 0 holds the carry into the tile.
-//
-// Monoid policy M: NI inclusive values, NA aggregate values, Acc type with
-// identity / absorb (acc <- acc o agg of an earlier tile) / finish (carry =
-// acc applied to the inclusive value of that tile).
-// ---------------------------------------------------------------------------
-template <class M, int NW>
-struct LookbackShared {
-  float pl[NW][M::NA][kCB];
-  int st[NW][kCB];
-  int pos[kCB];
-  int more;
-};
-
-// W waves, each fetching KP predecessors per round (window NW = W * KP).
-template <class M, int W, int KP>
-__device__ __forceinline__ void windowed_lookback(const TileId& id, int B, int n_cb, int epoch,
-                                                  const unsigned long long* __restrict__ incl,
-                                                  const unsigned long long* __restrict__ agg,
-                                                  int lane, int wave,
-                                                  LookbackShared<M, W * KP>& sh,
-                                                  float carry[M::NI]) {
-  typename M::Acc acc;
-  M::identity(acc);
-  int pos = id.chunk - 1;  // wave 0: next predecessor chunk to examine
-  bool done = false;
-  const int per = B * n_cb;
-  int idle_rounds = 0;
-  while (true) {
-    if (wave == 0) sh.pos[lane] = done ? -1 : pos;
-    __syncthreads();
-    {
-      const int base = sh.pos[lane];
-#pragma unroll
-      for (int k = 0; k < KP; ++k) {
-        const int slot = wave * KP + k;
-        const int p = base - slot;
-        int st = 0;
-        if (base >= 0 && p >= 0) {
-          const size_t ptile = static_cast<size_t>(p) * per + id.rem;
-          const unsigned long long* ip = incl + ptile * M::NI * kCB + lane;
-          const unsigned long long* ap = agg + ptile * M::NA * kCB + lane;
-          float v[M::NI], a[M::NA];
-          bool ok_i = true, ok_a = true;
-#pragma unroll
-          for (int q = 0; q < M::NI; ++q) ok_i = ld_tagged(ip + q * kCB, epoch, v[q]) && ok_i;
-#pragma unroll
-          for (int q = 0; q < M::NA; ++q) ok_a = ld_tagged(ap + q * kCB, epoch, a[q]) && ok_a;
-          if (ok_i) {
-            st = 2;
-#pragma unroll
-            for (int q = 0; q < M::NI; ++q) sh.pl[slot][q][lane] = v[q];
-          } else if (ok_a) {
-            st = 1;
-#pragma unroll
-            for (int q = 0; q < M::NA; ++q) sh.pl[slot][q][lane] = a[q];
-          }
-        }
-        sh.st[slot][lane] = st;
-      }
-    }
-    __syncthreads();
-    if (wave == 0) {
-      bool progressed = false;
-      if (!done) {
-        bool stalled = false;
-#pragma unroll
-        for (int w = 0; w < W * KP; ++w) {
-          if (!done && !stalled) {
-            const int st = sh.st[w][lane];
-            if (st == 2) {
-              float v[M::NI];
-#pragma unroll
-              for (int k = 0; k < M::NI; ++k) v[k] = sh.pl[w][k][lane];
-              M::finish(acc, v, carry);
-              done = true;
-              progressed = true;
-            } else if (st == 1) {
-              float a[M::NA];
-#pragma unroll
-              for (int k = 0; k < M::NA; ++k) a[k] = sh.pl[w][k][lane];
-              M::absorb(acc, a);
-              --pos;
-              progressed = true;
-            } else {
-              stalled = true;
-            }
-          }
-        }
-      }
-      const unsigned long long pending = __ballot(!done);
-      const unsigned long long moved = __ballot(progressed);
-      if (lane == 0) sh.more = pending != 0ull;
-      // Nothing new anywhere: back off before polling again.
-      idle_rounds = moved ? 0 : idle_rounds + 1;
-      if (pending && !moved) {
-        if (idle_rounds > 8)
-          __builtin_amdgcn_s_sleep(8);
-        else
-          __builtin_amdgcn_s_sleep(2);
-      }
-    }
-    __syncthreads();
-    if (!sh.more) break;
-  }
-}
 
 // ---------------------------------------------------------------------------
 // (1) frozen-gate pass
@@ -451,185 +308,6 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
 // (2) Newton iteration
 // ---------------------------------------------------------------------------
 
-// Cell value and the 12 structural non-zeros of the per-channel Jacobian
-// [out, in] over slots (c, n, m, h):
-//   c: [f, 0, cm, ch]   n: [0, f, nm, nh]   m: [0, 0, al, mh]   h: [hc, hn, hm, hh]
-struct CellJ {
-  float pc, pn, pm, ph;
-  float f, cm, ch, nm, nh, al, mh, hc, hn, hm, hh;
-};
-
-__device__ __forceinline__ CellJ cell_jac(const float prev[4], const float x[4], const float r[4],
-                                          float eps) {
-  const float c = prev[0], n = prev[1], m = prev[2], h = prev[3];
-  const float zi = add_rn(x[0], mul_rn(r[0], h));
-  const float zf = add_rn(x[1], mul_rn(r[1], h));
-  const float zz = add_rn(x[2], mul_rn(r[2], h));
-  const float zo = add_rn(x[3], mul_rn(r[3], h));
-  const float left = zf + m;
-  const float mn = fmaxf(left, zi);
-  // d max(left, z_i) / d left, ties split 0.5 / 0.5 (para_slstm.py:530-534).
-  const float al = left > zi ? 1.f : (left == zi ? 0.5f : 0.f);
-  const float e = fexp(-fabsf(left - zi));  // the smaller of the two gate exponents
-  const bool lf = left >= zi;
-  const float f = lf ? 1.f : e;
-  const float i = lf ? e : 1.f;
-  const float z = ftanh(zz);
-  const float nn = f * n + i;
-  const float cn = f * c + i * z;
-  const float o = fsigmoid(zo);
-  const float inv_den = frcp(nn + eps);
-  CellJ J;
-  J.pc = cn;
-  J.pn = nn;
-  J.pm = mn;
-  J.ph = o * (cn * inv_den);
-  const float be = 1.f - al;
-  const float dm_dh = al * r[1] + be * r[0];
-  const float di_dm = -i * al;
-  const float df_dm = f * be;
-  const float di_dh = i * (r[0] - dm_dh);
-  const float df_dh = f * (r[1] - dm_dh);
-  const float dz_dh = (1.f - z * z) * r[2];
-  const float do_dh = o * (1.f - o) * r[3];
-  J.f = f;
-  J.cm = df_dm * c + di_dm * z;
-  J.ch = df_dh * c + di_dh * z + i * dz_dh;
-  J.nm = df_dm * n + di_dm;
-  J.nh = df_dh * n + di_dh;
-  J.al = al;
-  J.mh = dm_dh;
-  const float inv = o * inv_den;
-  const float dn = -o * cn * inv_den * inv_den;
-  const float du = cn * inv_den;
-  J.hc = inv * f;
-  J.hn = dn * f;
-  J.hm = inv * J.cm + dn * J.nm;
-  J.hh = inv * J.ch + dn * J.nh + du * do_dh;
-  return J;
-}
-
-// v <- J v (+ add)
-__device__ __forceinline__ void jmv(const CellJ& J, float v[4]) {
-  const float c = v[0], n = v[1], m = v[2], h = v[3];
-  v[0] = J.f * c + J.cm * m + J.ch * h;
-  v[1] = J.f * n + J.nm * m + J.nh * h;
-  v[2] = J.al * m + J.mh * h;
-  v[3] = J.hc * c + J.hn * n + J.hm * m + J.hh * h;
-}
-
-// 4x4 affine element (A, b): x -> A x + b
-struct Aff {
-  float A[4][4];
-  float b[4];
-};
-
-__device__ __forceinline__ void aff_identity(Aff& a) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    a.b[i] = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) a.A[i][j] = i == j ? 1.f : 0.f;
-  }
-}
-
-// y after x: (Ay Ax, Ay bx + by)
-__device__ __forceinline__ Aff aff_compose(const Aff& x, const Aff& y) {
-  Aff o;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float acc = y.b[i];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) acc += y.A[i][k] * x.b[k];
-    o.b[i] = acc;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float s = 0.f;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) s += y.A[i][k] * x.A[k][j];
-      o.A[i][j] = s;
-    }
-  }
-  return o;
-}
-
-__device__ __forceinline__ void aff_apply(const Aff& a, float v[4]) {
-  float o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float acc = a.b[i];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) acc += a.A[i][k] * v[k];
-    o[i] = acc;
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = o[i];
-}
-
-
-struct NewtonMonoid {
-  static constexpr int NI = 4;   // carry delta (c, n, m, h)
-  static constexpr int NA = 20;  // aggregate A (16, row major) then b (4)
-  using Acc = Aff;
-  static __device__ __forceinline__ void identity(Acc& a) { aff_identity(a); }
-  static __device__ __forceinline__ void absorb(Acc& acc, const float v[NA]) {
-    Aff pa;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      pa.b[i] = v[16 + i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) pa.A[i][j] = v[4 * i + j];
-    }
-    acc = aff_compose(pa, acc);
-  }
-  static __device__ __forceinline__ void finish(const Acc& acc, const float v[NI], float out[NI]) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) out[k] = v[k];
-    aff_apply(acc, out);
-  }
-};
-
-// Raw storage words of a tile's steps, held in registers between the two
-// passes: bf16 values packed two to a register, fp32 values one each.
-template <typename T>
-struct RowStash;
-
-template <>
-struct RowStash<bf16> {
-  static constexpr int N = 2;
-  // Slot g of the row at byte offset soff (+ g * slot bytes, wave-uniform).
-  static __device__ __forceinline__ void load(rsrc_t rs, uint32_t voff, uint32_t soff,
-                                              uint32_t slot, uint32_t w[N]) {
-    uint32_t v[4];
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-      v[g] = __builtin_amdgcn_raw_buffer_load_b16(rs, voff, soff + g * slot, 0);
-    w[0] = v[0] | (v[1] << 16);
-    w[1] = v[2] | (v[3] << 16);
-  }
-  static __device__ __forceinline__ void get(const uint32_t w[N], float p[4]) {
-    p[0] = lo_bf16(w[0]);
-    p[1] = hi_bf16(w[0]);
-    p[2] = lo_bf16(w[1]);
-    p[3] = hi_bf16(w[1]);
-  }
-};
-
-template <>
-struct RowStash<float> {
-  static constexpr int N = 4;
-  static __device__ __forceinline__ void load(rsrc_t rs, uint32_t voff, uint32_t soff,
-                                              uint32_t slot, uint32_t w[N]) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-      w[g] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff + g * slot, 0);
-  }
-  static __device__ __forceinline__ void get(const uint32_t w[N], float p[4]) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) p[g] = __uint_as_float(w[g]);
-  }
-};
-
 // One Newton iteration over a tile of W waves x L steps x 64 channels.  Pass 1
 // reads each step once (wx and the guess, kept in registers) and folds the
 // lane's affine aggregate x -> J x + F; pass 2 replays the steps from the true
@@ -818,14 +496,9 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
 namespace prnn {
 namespace slstm {
 
-constexpr int kMaxStages = 64;  // ticket counters per call
-
 // Tile shapes (L steps per lane x W waves).  Selected once per process;
 // PRNN_SLSTM_TILES="<frozen L>x<W>,<newton L>x<W>" overrides the default for
 // tuning runs (only the instantiated shapes are accepted).
-struct Shape {
-  int L, W;
-};
 // bf16 frozen tiles stash 2 registers per step, fp32 ones 4 (one fp32 shape).
 static const Shape kFrozenShapes[] = {{64, 4}, {32, 8}, {32, 4}, {64, 2}};
 constexpr Shape kFrozenF32{32, 4};
@@ -858,59 +531,11 @@ static Tiles tiles() {
   return t;
 }
 
-struct Geo {
-  int n_cb, n_chunks, n_tiles;
-};
-
-static Geo geometry(int B, int T, int d, Shape sh) {
-  Geo g;
-  g.n_cb = (d + kCB - 1) / kCB;
-  g.n_chunks = (T + sh.L * sh.W - 1) / (sh.L * sh.W);
-  g.n_tiles = B * g.n_cb * g.n_chunks;
-  return g;
-}
-
-static size_t elem_size(int dtype) { return dtype == PRNN_BF16 ? 2 : 4; }
-
 static Shape frozen_shape(int dtype) { return dtype == PRNN_BF16 ? tiles().frozen : kFrozenF32; }
 // Shape of a Newton launch; `work_in` when it reads the fp32 work trajectory.
 static Shape newton_shape(int dtype, bool work_in) {
   if (dtype != PRNN_BF16) return kNewtonF32;
   return work_in ? tiles().newton_work : tiles().newton_guess;
-}
-
-static int check_dims(int B, int T, int d, int dtype) {
-  if (B < 1 || T < 1 || d < 1)
-    return fail(PRNN_ERR_VALUE, "B, T, d must be >= 1, got B=%d T=%d d=%d", B, T, d);
-  // A wave addresses its steps with 32-bit buffer offsets.
-  if (d >= (1 << 20)) return fail(PRNN_ERR_VALUE, "d must be < 2^20, got %d", d);
-  if (dtype != PRNN_F32 && dtype != PRNN_BF16)
-    return fail(PRNN_ERR_TYPE, "dtype code %d is not float32 (0) or bfloat16 (1)", dtype);
-  const long long tiles = static_cast<long long>(B) * ((d + kCB - 1) / kCB) * T;
-  if (tiles > (1ll << 30))
-    return fail(PRNN_ERR_VALUE, "problem too large: B*T*ceil(d/64) = %lld", tiles);
-  return PRNN_OK;
-}
-
-// Look-back state shared by the launches of one call, cleared by one kernel
-// at the start of the call:
-//   counters[kMaxStages] | tagged carries | tagged aggregates
-struct Lookback {
-  int* counters;
-  unsigned long long* incl;
-  unsigned long long* agg;
-  size_t clear_words;
-};
-
-static Lookback carve_lookback(Carver& cv, const Geo& g, int incl_vals, int agg_vals) {
-  Lookback lb;
-  lb.counters = static_cast<int*>(cv.take(sizeof(int) * kMaxStages));
-  lb.incl = static_cast<unsigned long long*>(
-      cv.take(sizeof(unsigned long long) * incl_vals * kCB * g.n_tiles));
-  lb.agg = static_cast<unsigned long long*>(
-      cv.take(sizeof(unsigned long long) * agg_vals * kCB * g.n_tiles));
-  lb.clear_words = (cv.used - (reinterpret_cast<char*>(lb.counters) - cv.base)) / sizeof(int);
-  return lb;
 }
 
 struct InitWs {

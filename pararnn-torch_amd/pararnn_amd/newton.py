@@ -311,9 +311,138 @@ def newton_apply(
         or (h0 is not None and h0.requires_grad)
         or any(p.requires_grad for p in params)
     )
-    if needs_grad:
+    if not needs_grad:
+        return _newton_forward(cell, x, config, h0=h0, stats=stats)
+    if not isinstance(cell, ParaSLSTM):
         raise NotImplementedError(
-            "pararnn_amd provides the Newton forward only; the eq. 2.6 backward is not built "
-            "yet. Run newton_apply under torch.no_grad() / torch.inference_mode()."
+            "pararnn_amd builds the eq. 2.6 backward for ParaSLSTM(mix='diag') only; run "
+            f"{type(cell).__name__}(mix={getattr(cell, 'mix', None)!r}) under torch.no_grad()"
         )
-    return _newton_forward(cell, x, config, h0=h0, stats=stats)
+    has_h0 = h0 is not None
+    h0_leaf = h0 if has_h0 else x.new_zeros(())
+    _fwd_pack.clear()
+    _fwd_pack.update(cell=cell, config=config, stats=stats, has_h0=has_h0)
+    try:
+        return _NewtonFixedPoint.apply(x, h0_leaf, *params)
+    finally:
+        _fwd_pack.clear()
+
+
+# ---------------------------------------------------------------------------
+# Eq. 2.6 backward (newton/__init__.py:84-190, 765-918)
+# ---------------------------------------------------------------------------
+
+# Forward-thread hand-off for the duration of ``_NewtonFixedPoint.apply`` only;
+# backward reads ``ctx`` alone.  Concurrent ``newton_apply`` calls with
+# gradients are unsupported, as in the reference (newton/__init__.py:84-88).
+_fwd_pack: dict[str, object] = {}
+
+
+class _NewtonFixedPoint(torch.autograd.Function):
+    """Implicit-function backward at the solved trajectory H* (eq. 2.6).
+
+    Gradients never flow through the Newton iterations: backward solves the
+    adjoint recursion ``mu_t = dL/dH_t + J_{t+1}^T mu_{t+1}`` at ``H*`` and
+    contracts ``mu`` with the cell VJP (newton/__init__.py:91-190).
+    """
+
+    @staticmethod
+    def forward(ctx, x_in: Tensor, h0_in: Tensor, *param_tensors: Tensor) -> Tensor:
+        del param_tensors
+        cell = _fwd_pack["cell"]
+        config = _fwd_pack["config"]
+        has_h0 = bool(_fwd_pack["has_h0"])
+        h0_fwd = h0_in if has_h0 else None
+        with torch.no_grad():
+            states = _newton_forward(cell, x_in, config, h0=h0_fwd, stats=_fwd_pack["stats"])
+        ctx.cell = cell
+        ctx.has_h0 = has_h0
+        ctx.recompute = bool(config.recompute)
+        ctx.fwd_config = config
+        ctx.chunk_len = config.chunk_len
+        if ctx.recompute:
+            ctx.save_for_backward(x_in, h0_in)
+        else:
+            ctx.save_for_backward(states, x_in, h0_in)
+        return states
+
+    @staticmethod
+    def backward(ctx, grad_states: Tensor):
+        if ctx.recompute:
+            x_in, h0_in = ctx.saved_tensors
+            h0_fwd = h0_in if ctx.has_h0 else None
+            with torch.no_grad():
+                states = _newton_forward(ctx.cell, x_in, ctx.fwd_config, h0=h0_fwd, stats=None)
+        else:
+            states, x_in, h0_in = ctx.saved_tensors
+            h0_fwd = h0_in if ctx.has_h0 else None
+        with torch.no_grad():
+            if ctx.chunk_len is not None:
+                grad_x, param_grads, grad_h0 = _eq26_vjp_chunked(
+                    ctx.cell, states, x_in, grad_states, chunk_len=int(ctx.chunk_len), h0=h0_fwd
+                )
+            else:
+                grad_x, param_grads, grad_h0 = _eq26_vjp(
+                    ctx.cell, states, x_in, grad_states, h0=h0_fwd
+                )
+        if not x_in.requires_grad:
+            grad_x = None
+        if not ctx.has_h0 or not h0_in.requires_grad:
+            grad_h0 = None
+        return (grad_x, grad_h0, *param_grads)
+
+
+def _eq26_vjp(cell: nn.Module, states: Tensor, x: Tensor, partial: Tensor, *,
+              h0: Tensor | None = None):
+    """``(grad_x, per-parameter grads, grad_h0)`` for diag ParaSLSTM.
+
+    The reverse scan and the cell VJP run in one HIP op
+    (``pararnn::slstm_backward_fused``); the ``W_x`` VJP is two GEMMs and a
+    column sum as in the reference (solvers/vjp.py:109-120, 288-306).
+    """
+    if not (isinstance(cell, ParaSLSTM) and cell.mix == "diag"):
+        raise NotImplementedError(f"eq. 2.6 backward for {type(cell).__name__} is not built")
+    wx = cell.W_x(x)
+    partial = partial.to(states.dtype)
+    g_wx, g_r, g_h0 = ops.slstm_backward_fused(
+        wx, cell.clipped_r(), h0, states, partial, eps=cell.eps
+    )
+    g_r = g_r.to(cell.R.dtype)
+    if cell.max_recurrent_norm is not None:
+        g_r = g_r * (cell.R.abs() <= cell.max_recurrent_norm).to(g_r.dtype)
+    gy = g_wx.reshape(-1, g_wx.shape[-1])
+    xx = x.reshape(-1, x.shape[-1])
+    grad_x = (gy @ cell.W_x.weight).reshape(x.shape)
+    by_name = {"W_x.weight": gy.t() @ xx, "W_x.bias": gy.sum(0), "R": g_r}
+    grads = tuple(
+        by_name.get(n) if p.requires_grad else None for n, p in cell.named_parameters()
+    )
+    grad_h0 = None if h0 is None else g_h0.to(h0.dtype)
+    return grad_x, grads, grad_h0
+
+
+def _eq26_vjp_chunked(cell: nn.Module, states: Tensor, x: Tensor, partial: Tensor, *,
+                      chunk_len: int, h0: Tensor | None = None):
+    """Eq. 2.6 on the windows of ``_newton_chunked``, last window first: the
+    ``h0`` gradient of window i+1 adds to dL/dH at the last step of window i
+    (newton/__init__.py:868-918)."""
+    time = int(x.shape[1])
+    acc_x = None
+    acc = [None] * len(tuple(cell.parameters()))
+    carry = None
+    for t0 in reversed(range(0, time, int(chunk_len))):
+        t1 = min(t0 + int(chunk_len), time)
+        part = partial[:, t0:t1]
+        if carry is not None:
+            part = part.clone()
+            part[:, -1] = part[:, -1] + carry
+        h0_w = h0 if t0 == 0 else states[:, t0 - 1]
+        gx, pg, gh0 = _eq26_vjp(cell, states[:, t0:t1], x[:, t0:t1], part, h0=h0_w)
+        carry = gh0
+        if acc_x is None:
+            acc_x = x.new_zeros(x.shape)
+        acc_x[:, t0:t1] = gx
+        for i, g in enumerate(pg):
+            if g is not None:
+                acc[i] = g if acc[i] is None else acc[i] + g
+    return acc_x, tuple(acc), (None if h0 is None else carry)

@@ -182,6 +182,51 @@ def _(wx, r, h0=None, states=None, block_table=None, *, max_iters, omega, eps,
     return wx.new_empty(batch, time, 4, r.shape[-1])
 
 
+@torch.library.custom_op("pararnn::slstm_backward_fused", mutates_args=())
+def slstm_backward_fused(
+    wx: Tensor, r: Tensor, h0: Tensor | None, states: Tensor, grad: Tensor, *, eps: float
+) -> tuple[Tensor, Tensor, Tensor]:
+    """Eq. 2.6 backward of diag ParaSLSTM at ``H* = states`` on the GPU.
+
+    Returns ``(g_wx, g_r, g_h0)``: ``dL/dwx`` ``(B, T, 4 d_h)`` in ``wx``'s
+    dtype, ``g_r`` ``(4, d_h)`` fp32 (before the clamp mask on ``R``) and
+    ``g_h0 = J_0^T mu_0`` ``(B, 4, d_h)`` fp32 (zeros-input adjoint when
+    ``h0`` is None).  The reference computes the same quantities with
+    ``step_and_jacobian`` + ``reverse_scan_block4`` + ``slstm_recurrence_vjp``
+    (solvers/newton/__init__.py:765-866, kernels/vjp_slstm.py:209-240).
+    """
+    batch, time, d_h = _slstm_shapes(wx, r)
+    code = _validate("slstm_backward_fused", wx, r, h0, states, grad)
+    for name, t in (("states", states), ("grad", grad)):
+        if t.shape != (batch, time, 4, d_h):
+            raise ValueError(f"{name} shape {tuple(t.shape)} != {(batch, time, 4, d_h)}")
+    wx, r, states, grad = wx.contiguous(), r.contiguous(), states.contiguous(), grad.contiguous()
+    h0 = _slstm_h0(h0, batch, d_h)
+    g_wx = torch.empty_like(wx)
+    g_r = torch.empty(4, d_h, dtype=torch.float32, device=wx.device)
+    g_h0 = torch.zeros(batch, 4, d_h, dtype=torch.float32, device=wx.device)
+    lib = _lib.load()
+    with torch.cuda.device(wx.device):
+        nbytes = lib.prnn_slstm_backward_workspace_size(batch, time, d_h, code)
+        ws = _workspace(nbytes, wx.device)
+        rc = lib.prnn_slstm_backward(
+            _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), _ptr(grad), _ptr(g_wx), _ptr(g_r),
+            _ptr(g_h0), batch, time, d_h, float(eps), code, _ptr(ws), ws.numel(), _stream(wx.device),
+        )
+    _lib.check(rc, "slstm_backward_fused")
+    return g_wx, g_r, g_h0
+
+
+@slstm_backward_fused.register_fake
+def _(wx, r, h0, states, grad, *, eps):
+    batch, _, d_h = states.shape[0], states.shape[1], r.shape[-1]
+    return (
+        torch.empty_like(wx),
+        wx.new_empty(4, d_h, dtype=torch.float32),
+        wx.new_empty(batch, 4, d_h, dtype=torch.float32),
+    )
+
+
 # ---------------------------------------------------------------------------
 # ParaGRU mix='head'
 # ---------------------------------------------------------------------------

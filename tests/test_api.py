@@ -95,9 +95,9 @@ def test_unsupported_cells_and_knobs():
         newton_apply(ParaGRU(4, 8), torch.randn(1, 3, 4), NewtonConfig(picard_iters=2))
 
 
-def test_grad_mode_is_rejected_until_backward_exists():
+def test_grad_mode_on_cpu_input_fails_loudly():
     cell = ParaSLSTM(4, 8)
-    with pytest.raises((NotImplementedError, TypeError)):
+    with pytest.raises(TypeError, match="ROCm GPU"):
         newton_apply(cell, torch.randn(1, 5, 4))
 
 

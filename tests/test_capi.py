@@ -22,7 +22,7 @@ def _declared():
 def test_header_declares_entry_points():
     decl = _declared()
     for name in ("prnn_slstm_init", "prnn_slstm_newton", "prnn_gru_head_newton",
-                 "prnn_last_error", "prnn_abi_version"):
+                 "prnn_slstm_backward", "prnn_last_error", "prnn_abi_version"):
         assert name in decl
 
 
@@ -60,3 +60,7 @@ def test_host_only_calls():
     assert rc == _lib.PRNN_ERR_TYPE
     with pytest.raises(TypeError):
         _lib.check(rc, "x")
+    assert lib.prnn_slstm_backward_workspace_size(4, 32768, 768, _lib.PRNN_BF16) > 0
+    rc = lib.prnn_slstm_backward(None, None, None, None, None, None, None, None, 1, 1, 1, 1e-6,
+                                 0, None, 0, None)
+    assert rc == _lib.PRNN_ERR_VALUE
