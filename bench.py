@@ -6,7 +6,8 @@ x ~ N(0, 0.5) seeded, default seeded init.  A step is one solve on one batch
 with ``wx = W_x(x)`` already resident in HBM: the zero-hidden pass, P Picard
 passes and K Newton iterations (8 kernel launches plus two status clears).
 The W_x GEMM and the end-to-end ``newton_apply`` (GEMM + solve) are timed
-separately and reported as extra fields.
+separately and reported as extra fields, as is BASELINE config 5 (one
+training step: forward solve + eq. 2.6 backward, ``train_cfg5``).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 Prints one JSON line.
@@ -81,6 +82,48 @@ def cpu_baseline(torch, t_sample: int):
     }
 
 
+def train_cfg5(torch, reps: int):
+    """one training step (forward Newton solve + eq. 2.6
+    backward, W_x GEMMs included) of ParaSLSTM diag d=768, B=4, T=32768,
+    bf16, K=2, P=5, x and the upstream gradient ~ N(0, 1)."""
+    from pararnn_amd import NewtonConfig, ParaSLSTM, newton_apply, ops
+
+    b5, t5, d5 = 4, 32768, 768
+    torch.manual_seed(0)
+    cell = ParaSLSTM(d5, d5).to("cuda:0", torch.bfloat16)
+    g = torch.Generator(device="cuda:0").manual_seed(1)
+    x = torch.randn(b5, t5, d5, generator=g, device="cuda:0").to(torch.bfloat16)
+    up = torch.randn(b5, t5, 4, d5, generator=g, device="cuda:0").to(torch.bfloat16)
+    cfg = NewtonConfig(max_iters=K, picard_iters=P, residual_atol=None, residual_fail=None,
+                       picard_adapt=False)
+
+    def step():
+        cell.zero_grad(set_to_none=True)
+        xx = x.detach().requires_grad_(True)
+        newton_apply(cell, xx, cfg).backward(up)
+
+    ms = _time(torch, step, reps)
+    with torch.no_grad():
+        H = newton_apply(cell, x, cfg)
+        wx = cell.W_x(x)
+        r = cell.clipped_r()
+        ms_bwd = _time(torch, lambda: ops.slstm_backward_fused(wx, r, None, H, up, eps=cell.eps),
+                       reps)
+    elems = b5 * t5 * d5
+    # reverse-scan kernel bytes per (b, t, channel): read wx 8, H* 8, dL/dH 8,
+    # write dL/dwx 8 (bf16)
+    ach = elems * 32 / (ms_bwd * 1e-3) / 1e9
+    return {
+        "workload": "ParaSLSTM diag train step (fwd + eq. 2.6 bwd), d=768 B=4 T=32768 bf16 "
+                    "K=2 P=5",
+        "ms_per_step": ms,
+        "tokens_per_s": b5 * t5 / (ms * 1e-3),
+        "bwd_kernel_ms": ms_bwd,
+        "bwd_kernel_GBps": ach,
+        "bwd_kernel_frac": ach / HBM_PEAK_GBS,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -88,6 +131,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-sample", type=int, default=32768)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-train", action="store_true", help="skip the config 5 training step")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (for rocprofv3 --pmc byte scaling)")
     args = ap.parse_args()
@@ -225,6 +269,8 @@ def main() -> int:
         "newton_apply_tokens_per_s": tokens / (ms_e2e * 1e-3),
         "wall_s_timed_region": t_wall,
     }
+    if not args.no_train:
+        out["train_cfg5"] = train_cfg5(torch, max(3, args.steps // 4))
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(torch, args.cpu_sample)
         out["gpu_over_cpu"] = out["value"] / out["cpu_baseline"]["value"]

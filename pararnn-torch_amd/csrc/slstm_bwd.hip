@@ -303,12 +303,12 @@ namespace slstm {
 // Backward tiles stash H*_{t-1}, wx and g: 6 registers per step in bf16,
 // 12 in fp32.  PRNN_SLSTM_BWD_TILES="<L>x<W>" overrides the bf16 shape for
 // tuning runs (instantiated shapes only).
-static const Shape kBwdShapes[] = {{16, 8}, {16, 4}, {24, 4}, {32, 4}};
+static const Shape kBwdShapes[] = {{24, 4}, {16, 8}, {16, 4}, {32, 4}};
 constexpr Shape kBwdF32{8, 8};
 
 static Shape bwd_shape(int dtype) {
   static Shape s = [] {
-    Shape r{16, 8};
+    Shape r{24, 4};
     if (const char* e = getenv("PRNN_SLSTM_BWD_TILES")) {
       int l, w;
       if (sscanf(e, "%dx%d", &l, &w) == 2)

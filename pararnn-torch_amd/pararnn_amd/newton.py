@@ -202,12 +202,13 @@ def _fill_stats(cell, x, states, h0, config, *, iters, stats, history=(), known=
         log.warning("newton_residual_high max_residual=%g iters=%d", res, iters)
 
 
-def _newton_solve(cell, x, config, *, h0, stats) -> Tensor:
+def _newton_solve(cell, x, config, *, h0, stats, wx=None) -> Tensor:
     if config.chunk_len is not None:
         return _newton_chunked(cell, x, config, h0=h0, stats=stats)
     if config.fused_early_exit:
         raise TypeError("fused_early_exit is not provided by pararnn_amd")
-    wx = cell.W_x(x)
+    if wx is None:
+        wx = cell.W_x(x)
     states = fused_newton(
         cell, wx,
         max_iters=int(config.max_iters), omega=float(config.omega), h0=h0,
@@ -250,16 +251,18 @@ def _picard_retry_needed(res: float, config: NewtonConfig) -> bool:
     return fail is not None and res > fail
 
 
-def _newton_forward(cell, x, config, *, h0, stats) -> Tensor:
+def _newton_forward(cell, x, config, *, h0, stats, wx=None) -> Tensor:
+    """The solve; ``wx`` (unchunked only) reuses a projection already computed."""
     if config.chunk_len is not None:
         return _newton_chunked(cell, x, config, h0=h0, stats=stats)
     if not (config.picard_adapt and isinstance(cell, ParaSLSTM)) or torch.compiler.is_compiling():
-        return _newton_solve(cell, x, config, h0=h0, stats=stats)
+        return _newton_solve(cell, x, config, h0=h0, stats=stats, wx=wx)
     # Adaptive Picard ladder (picard.py:105-158).
     cfg = config
     while True:
         st = stats if stats is not None else NewtonStats()
-        states = _newton_solve(cell, x, replace(cfg, residual_fail=None), h0=h0, stats=st)
+        states = _newton_solve(cell, x, replace(cfg, residual_fail=None), h0=h0, stats=st,
+                               wx=wx)
         res = st.max_residual
         nxt = slstm_picard_next(int(cfg.picard_iters or 0))
         if _picard_retry_needed(res, config) and nxt is not None:
@@ -353,15 +356,23 @@ class _NewtonFixedPoint(torch.autograd.Function):
         config = _fwd_pack["config"]
         has_h0 = bool(_fwd_pack["has_h0"])
         h0_fwd = h0_in if has_h0 else None
-        with torch.no_grad():
-            states = _newton_forward(cell, x_in, config, h0=h0_fwd, stats=_fwd_pack["stats"])
         ctx.cell = cell
         ctx.has_h0 = has_h0
         ctx.recompute = bool(config.recompute)
         ctx.fwd_config = config
         ctx.chunk_len = config.chunk_len
+        with torch.no_grad():
+            # Unchunked and not recomputing: keep W_x(x) for the backward's
+            # cell VJP instead of projecting again.
+            wx = None
+            if config.chunk_len is None and not ctx.recompute:
+                wx = cell.W_x(x_in)
+            states = _newton_forward(cell, x_in, config, h0=h0_fwd, stats=_fwd_pack["stats"],
+                                     wx=wx)
         if ctx.recompute:
             ctx.save_for_backward(x_in, h0_in)
+        elif wx is not None:
+            ctx.save_for_backward(states, x_in, h0_in, wx)
         else:
             ctx.save_for_backward(states, x_in, h0_in)
         return states
@@ -374,8 +385,11 @@ class _NewtonFixedPoint(torch.autograd.Function):
             with torch.no_grad():
                 states = _newton_forward(ctx.cell, x_in, ctx.fwd_config, h0=h0_fwd, stats=None)
         else:
-            states, x_in, h0_in = ctx.saved_tensors
+            states, x_in, h0_in, *rest = ctx.saved_tensors
+            wx = rest[0] if rest else None
             h0_fwd = h0_in if ctx.has_h0 else None
+        if ctx.recompute:
+            wx = None
         with torch.no_grad():
             if ctx.chunk_len is not None:
                 grad_x, param_grads, grad_h0 = _eq26_vjp_chunked(
@@ -383,7 +397,7 @@ class _NewtonFixedPoint(torch.autograd.Function):
                 )
             else:
                 grad_x, param_grads, grad_h0 = _eq26_vjp(
-                    ctx.cell, states, x_in, grad_states, h0=h0_fwd
+                    ctx.cell, states, x_in, grad_states, h0=h0_fwd, wx=wx
                 )
         if not x_in.requires_grad:
             grad_x = None
@@ -393,7 +407,7 @@ class _NewtonFixedPoint(torch.autograd.Function):
 
 
 def _eq26_vjp(cell: nn.Module, states: Tensor, x: Tensor, partial: Tensor, *,
-              h0: Tensor | None = None):
+              h0: Tensor | None = None, wx: Tensor | None = None):
     """``(grad_x, per-parameter grads, grad_h0)`` for diag ParaSLSTM.
 
     The reverse scan and the cell VJP run in one HIP op
@@ -402,7 +416,8 @@ def _eq26_vjp(cell: nn.Module, states: Tensor, x: Tensor, partial: Tensor, *,
     """
     if not (isinstance(cell, ParaSLSTM) and cell.mix == "diag"):
         raise NotImplementedError(f"eq. 2.6 backward for {type(cell).__name__} is not built")
-    wx = cell.W_x(x)
+    if wx is None:
+        wx = cell.W_x(x)
     partial = partial.to(states.dtype)
     g_wx, g_r, g_h0 = ops.slstm_backward_fused(
         wx, cell.clipped_r(), h0, states, partial, eps=cell.eps
