@@ -43,10 +43,10 @@ __device__ __forceinline__ void cell_vjp(const float prev[4], const float x[4], 
                                          float eps, const float mu[4], float dz[4],
                                          float nu[4]) {
   const float c = prev[0], n = prev[1], m = prev[2], h = prev[3];
-  const float zi = add_rn(x[0], mul_rn(r[0], h));
-  const float zf = add_rn(x[1], mul_rn(r[1], h));
-  const float zz = add_rn(x[2], mul_rn(r[2], h));
-  const float zo = add_rn(x[3], mul_rn(r[3], h));
+  const float zi = x[0] + r[0] * h;
+  const float zf = x[1] + r[1] * h;
+  const float zz = x[2] + r[2] * h;
+  const float zo = x[3] + r[3] * h;
   const float left = zf + m;
   // d max(left, z_i) / d left, ties split 0.5 / 0.5 (para_slstm.py:530-534).
   const float al = left > zi ? 1.f : (left == zi ? 0.5f : 0.f);

@@ -463,16 +463,14 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
       float x[4], hv[4];
       XS::get(xs[s], x);
       HS::get(hs[s], hv);
-      const CellJ J = cell_jac(prev, x, r, eps);
-      jmv(J, dl);
-      dl[0] += J.pc - hv[0];
-      dl[1] += J.pn - hv[1];
-      dl[2] += J.pm - hv[2];
-      dl[3] += J.ph - hv[3];
+      float pv[4], jv[4];
+      cell_jvp(prev, x, r, eps, dl, pv, jv);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) dl[k] = jv[k] + (pv[k] - hv[k]);
       const uint32_t so = s * row4 * sizeof(TOUT);
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        stb<TOUT>(ro, vo, so + k * d * sizeof(TOUT), add_rn(hv[k], mul_rn(omega, dl[k])));
+        stb<TOUT>(ro, vo, so + k * d * sizeof(TOUT), hv[k] + omega * dl[k]);
 #pragma unroll
       for (int k = 0; k < 4; ++k) prev[k] = hv[k];
     };

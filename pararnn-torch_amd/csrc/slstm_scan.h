@@ -97,20 +97,32 @@ __device__ __forceinline__ void windowed_lookback(const TileId& id, int B, int n
           const size_t ptile = static_cast<size_t>(p) * per + id.rem;
           const unsigned long long* ip = incl + ptile * M::NI * kCB + lane;
           const unsigned long long* ap = agg + ptile * M::NA * kCB + lane;
+          // Large aggregates (the 4x4 affine monoid) are fetched only when the
+          // inclusive carry is not there yet; small ones in the same round.
+          constexpr bool kLazyAgg = M::NA > 2 * M::NI;
           float v[M::NI], a[M::NA];
           bool ok_i = true, ok_a = true;
 #pragma unroll
           for (int q = 0; q < M::NI; ++q) ok_i = ld_tagged(ip + q * kCB, epoch, v[q]) && ok_i;
+          if constexpr (!kLazyAgg) {
 #pragma unroll
-          for (int q = 0; q < M::NA; ++q) ok_a = ld_tagged(ap + q * kCB, epoch, a[q]) && ok_a;
+            for (int q = 0; q < M::NA; ++q) ok_a = ld_tagged(ap + q * kCB, epoch, a[q]) && ok_a;
+          }
           if (ok_i) {
             st = 2;
 #pragma unroll
             for (int q = 0; q < M::NI; ++q) sh.pl[slot][q][lane] = v[q];
-          } else if (ok_a) {
-            st = 1;
+          } else {
+            if constexpr (kLazyAgg) {
 #pragma unroll
-            for (int q = 0; q < M::NA; ++q) sh.pl[slot][q][lane] = a[q];
+              for (int q = 0; q < M::NA; ++q)
+                ok_a = ld_tagged(ap + q * kCB, epoch, a[q]) && ok_a;
+            }
+            if (ok_a) {
+              st = 1;
+#pragma unroll
+              for (int q = 0; q < M::NA; ++q) sh.pl[slot][q][lane] = a[q];
+            }
           }
         }
         sh.st[slot][lane] = st;
@@ -173,10 +185,10 @@ struct CellJ {
 __device__ __forceinline__ CellJ cell_jac(const float prev[4], const float x[4], const float r[4],
                                           float eps) {
   const float c = prev[0], n = prev[1], m = prev[2], h = prev[3];
-  const float zi = add_rn(x[0], mul_rn(r[0], h));
-  const float zf = add_rn(x[1], mul_rn(r[1], h));
-  const float zz = add_rn(x[2], mul_rn(r[2], h));
-  const float zo = add_rn(x[3], mul_rn(r[3], h));
+  const float zi = x[0] + r[0] * h;
+  const float zf = x[1] + r[1] * h;
+  const float zz = x[2] + r[2] * h;
+  const float zo = x[3] + r[3] * h;
   const float left = zf + m;
   const float mn = fmaxf(left, zi);
   // d max(left, z_i) / d left, ties split 0.5 / 0.5 (para_slstm.py:530-534).
@@ -218,6 +230,48 @@ __device__ __forceinline__ CellJ cell_jac(const float prev[4], const float x[4],
   J.hm = inv * J.cm + dn * J.nm;
   J.hh = inv * J.ch + dn * J.nh + du * do_dh;
   return J;
+}
+
+// Cell value p = f(prev, x) and the directional derivative jv = J v along
+// v, without forming J (a forward-mode pass through the cell, about half the
+// arithmetic of building the 12 entries and multiplying).
+__device__ __forceinline__ void cell_jvp(const float prev[4], const float x[4], const float r[4],
+                                         float eps, const float v[4], float p[4], float jv[4]) {
+  const float c = prev[0], n = prev[1], m = prev[2], h = prev[3];
+  const float zi = x[0] + r[0] * h;
+  const float zf = x[1] + r[1] * h;
+  const float zz = x[2] + r[2] * h;
+  const float zo = x[3] + r[3] * h;
+  const float left = zf + m;
+  const float mn = fmaxf(left, zi);
+  const float al = left > zi ? 1.f : (left == zi ? 0.5f : 0.f);
+  const float e = fexp(-fabsf(left - zi));
+  const bool lf = left >= zi;
+  const float f = lf ? 1.f : e;
+  const float i = lf ? e : 1.f;
+  const float z = ftanh(zz);
+  const float nn = f * n + i;
+  const float cn = f * c + i * z;
+  const float o = fsigmoid(zo);
+  const float inv_den = frcp(nn + eps);
+  const float u = cn * inv_den;
+  p[0] = cn;
+  p[1] = nn;
+  p[2] = mn;
+  p[3] = o * u;
+  // tangents: z_g' = r_g h', left' = z_f' + m', m_new' = al left' + (1 - al) z_i'
+  const float dzi = r[0] * v[3];
+  const float dleft = r[1] * v[3] + v[2];
+  const float dmn = dzi + al * (dleft - dzi);
+  const float di = i * (dzi - dmn);
+  const float df = f * (dleft - dmn);
+  const float dnn = df * n + f * v[1] + di;
+  const float dcn = df * c + f * v[0] + di * z + i * (1.f - z * z) * (r[2] * v[3]);
+  const float dso = o * (1.f - o) * (r[3] * v[3]);
+  jv[0] = dcn;
+  jv[1] = dnn;
+  jv[2] = dmn;
+  jv[3] = dso * u + o * inv_den * (dcn - u * dnn);
 }
 
 // v <- J v (+ add)
