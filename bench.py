@@ -185,7 +185,6 @@ def main() -> int:
         init = slstm_init_fused(wx, r, None, picard_iters=P, eps=cell.eps)
         ms_init1 = _time(torch, lambda: slstm_init_fused(wx, r, None, picard_iters=1, eps=cell.eps), reps)
         ms_initP = _time(torch, lambda: slstm_init_fused(wx, r, None, picard_iters=P, eps=cell.eps), reps)
-        ms_picard = (ms_initP - ms_init1) / (P - 1)  # one Picard pass launch (h-only output)
         from pararnn_amd import newton_slstm_fused
 
         ms_n1 = _time(torch, lambda: newton_slstm_fused(wx, r, None, init, max_iters=1, omega=1.0,
@@ -209,14 +208,14 @@ def main() -> int:
     # Compulsory I/O of this build's kernels, whose formats are narrower:
     # a Newton iteration reads wx (8 B) and a bf16 guess (8 B) or fp32 work
     # (16 B) and writes fp32 work (16 B) or the bf16 result (8 B): 32 B either
-    # way; a Picard pass reads wx (8 B) and bf16 h_prev (2 B) and writes bf16
-    # h (2 B).
+    # way; the fused warm start reads wx (8 B) and writes the bf16 state (8 B)
+    # once for all P + 1 frozen-gate stages.
     newton_io = elems * 32
-    picard_io = elems * 12
+    init_io = elems * 16
+    init_alg = elems * ((4 * s_x + 16) + P * (4 * s_x + 20))
     ach_newton = newton_bytes / (ms_newton * 1e-3) / 1e9
-    ach_picard = picard_io / (ms_picard * 1e-3) / 1e9
     newton_share = K * ms_newton / ms
-    picard_share = (ms_initP - ms_init1) / ms  # the P - 1 h-only Picard launches
+    init_share = ms_initP / ms
     out = {
         "metric": "Newton+scan fwd tokens/sec + % HBM roofline, ParaSLSTM diag d=1024 T=131072",
         "value": tokens / (ms * 1e-3),
@@ -249,18 +248,16 @@ def main() -> int:
             "own_io_bytes_per_launch": newton_io,
             "own_io_frac": newton_io / (ms_newton * 1e-3) / 1e9 / HBM_PEAK_GBS,
         },
-        "roofline_picard": {
-            "kernel": f"slstm_frozen_kernel (Picard pass, h-only output; {P - 1} launches, "
-                      f"{100 * picard_share:.0f}% of the step)",
-            "bound": "hbm",
-            "bytes_basis": "compulsory I/O of the kernel (12 B per element)",
-            "achieved": ach_picard,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": ach_picard / HBM_PEAK_GBS,
-            "traffic": _traffic_from_profile("slstm_frozen_picard_cfg3.md"),
-            "io_bytes_per_launch": picard_io,
-            "avg_launch_ms": ms_picard,
+        "roofline_init": {
+            "kernel": f"slstm_picard_fused_kernel (zero-hidden pass + {P} Picard passes in one "
+                      f"launch; {100 * init_share:.0f}% of the step)",
+            "bound": "valu",
+            "avg_launch_ms": ms_initP,
+            "per_stage_ms": (ms_initP - ms_init1) / (P - 1),
+            "io_bytes_per_launch": init_io,
+            "io_GBps": init_io / (ms_initP * 1e-3) / 1e9,
+            "algorithmic_bytes_per_launch": init_alg,
+            "algorithmic_GBps": init_alg / (ms_initP * 1e-3) / 1e9,
         },
         "step_algorithmic_GBps": step_bytes / (ms * 1e-3) / 1e9,
         "step_roofline_frac": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,

@@ -274,21 +274,36 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
   }
 }
 
-// g_r[g][ch] = sum over the tiles of ch's (b, channel block) of the partials,
-// in a fixed order (deterministic).
-__global__ void slstm_gr_reduce_kernel(const float* __restrict__ gr_part, float* __restrict__ gr,
-                                       int B, int d, int n_cb, int n_chunks) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= 4 * d) return;
-  const int g = idx / d, ch = idx - g * d;
-  const int cb = ch / kCB, lane = ch - cb * kCB;
+// g_r[g][ch] = sum over the tiles of ch's (b, channel block) of the partials.
+// One block per (gate, channel block): lane = channel, each of the 16 waves
+// sums a fixed quarter of the tiles (coalesced 256-byte rows), then the
+// quarters combine in LDS in a fixed order (deterministic).
+constexpr int kReduceWaves = 16;
+__global__ __launch_bounds__(64 * kReduceWaves) void slstm_gr_reduce_kernel(
+    const float* __restrict__ gr_part, float* __restrict__ gr, int B, int d, int n_cb,
+    int n_chunks) {
+  __shared__ float s_part[kReduceWaves][kCB];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = blockIdx.x / n_cb, cb = blockIdx.x - g * n_cb;
+  const int per_cb = n_chunks * B;  // tiles of this channel block
+  const int q0 = static_cast<int>(static_cast<long long>(per_cb) * wave / kReduceWaves);
+  const int q1 = static_cast<int>(static_cast<long long>(per_cb) * (wave + 1) / kReduceWaves);
   float acc = 0.f;
-  for (int c = 0; c < n_chunks; ++c)
-    for (int b = 0; b < B; ++b) {
-      const size_t tile = (static_cast<size_t>(c) * B + b) * n_cb + cb;
-      acc += gr_part[(tile * 4 + g) * kCB + lane];
-    }
-  gr[idx] = acc;
+  for (int q = q0; q < q1; ++q) {
+    // q enumerates (chunk, b) in tile order
+    const size_t tile = static_cast<size_t>(q) * n_cb + cb;
+    acc += gr_part[(tile * 4 + g) * kCB + lane];
+  }
+  s_part[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < kReduceWaves; ++w) t += s_part[w][lane];
+    const int ch = cb * kCB + lane;
+    if (ch < d) gr[g * d + ch] = t;
+  }
 }
 
 }  // namespace slstm
@@ -369,9 +384,8 @@ static int run_bwd(const TX* wx, const TX* r, const TX* h0, const TX* states, co
   }
   PRNN_HIP(hipGetLastError());
   const Geo g = geometry(B, T, d, sh);
-  const int n = 4 * d;
-  slstm_gr_reduce_kernel<<<dim3((n + 255) / 256), dim3(256), 0, stream>>>(w.gr_part, gr, B, d,
-                                                                         g.n_cb, g.n_chunks);
+  slstm_gr_reduce_kernel<<<dim3(4 * g.n_cb), dim3(64 * kReduceWaves), 0, stream>>>(
+      w.gr_part, gr, B, d, g.n_cb, g.n_chunks);
   PRNN_HIP(hipGetLastError());
   return PRNN_OK;
 }

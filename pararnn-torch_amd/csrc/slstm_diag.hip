@@ -305,6 +305,237 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// (1b) all frozen-gate passes in one launch (bf16 storage)
+// ---------------------------------------------------------------------------
+//
+// Pass p of the Picard warm start freezes the gates at wx + R * h_{p-1}[t-1]
+// (h_{p-1} the readout of pass p - 1, rounded to bf16 as the reference keeps
+// it in the tensor dtype).  Each tile runs stage p = 0 .. P over its own
+// steps with wx, the stage's pre-activations and its h trajectory held in
+// registers; only the last stage writes the state.  Stage p of a tile needs
+//  * h_{p-1} at the step before the tile: the predecessor tile publishes the
+//    h of its last step after each stage (tagged word, stage-indexed);
+//  * the stage-p carry: a decoupled look-back on stage-indexed tagged words.
+// Both only ever wait on tiles with earlier tickets (already resident or
+// done), so every wave reaches the end.
+template <int L, int W, int WPE>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) void
+slstm_picard_fused_kernel(
+    const bf16* __restrict__ wx, const bf16* __restrict__ rmix, const bf16* __restrict__ h0,
+    bf16* __restrict__ out, int B, int T, int d, int n_cb, int n_tiles, int P, float eps,
+    int* __restrict__ counter, unsigned long long* __restrict__ agg,
+    unsigned long long* __restrict__ incl, unsigned long long* __restrict__ hlast) {
+  static_assert(L % 2 == 0, "h is packed two steps to a register");
+  constexpr int KP = 2;
+  constexpr uint32_t SZ = 2;
+  __shared__ float s_agg[W][4][kCB];
+  __shared__ float s_carry[W][3][kCB];
+  __shared__ float s_hl[W][kCB];
+  __shared__ LookbackShared<FrozenMonoid, W * KP> s_lb;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tile = take_ticket(counter);
+  const TileId id = decode_tile(tile, B, n_cb);
+  const int c0 = id.cb * kCB;
+  const bool live = c0 + lane < d;
+  const int t0 = id.chunk * (W * L) + wave * L;
+  const int n_steps = max(0, min(L, T - t0));
+  const size_t row4 = static_cast<size_t>(4) * d;
+  const size_t first = static_cast<size_t>(id.b) * T + t0;
+  const uint32_t voff = live ? lane * SZ : kOOB;
+  const uint32_t slot = d * SZ;
+  const uint32_t span4 = n_steps > 0 ? ((n_steps - 1) * row4 + 3 * d + (d - c0)) * SZ : 0;
+  const size_t stage_incl = static_cast<size_t>(n_tiles) * 3 * kCB;
+  const size_t stage_agg = static_cast<size_t>(n_tiles) * 4 * kCB;
+  const size_t stage_h = static_cast<size_t>(n_tiles) * kCB;
+
+  float r[4] = {0.f, 0.f, 0.f, 0.f};
+  float h0h = 0.f;  // h_prev at t = 0 in every pass
+  float c_init[3] = {0.f, 0.f, 0.f};  // (m, n, c) carry into time 0
+  if (live) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) r[g] = ld(rmix + g * d + c0 + lane);
+    if (h0 != nullptr) {
+      const bf16* hb = h0 + static_cast<size_t>(id.b) * row4 + c0 + lane;
+      c_init[2] = ld(hb);
+      c_init[1] = ld(hb + d);
+      c_init[0] = ld(hb + 2 * d);
+      h0h = ld(hb + 3 * d);
+    }
+  }
+
+  uint32_t xw[L][2], pre[L][2], hh[L / 2];
+  {
+    const rsrc_t rx = make_rsrc(wx + first * row4 + c0, span4);
+    auto load = [&](int s) {
+      uint32_t v[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        v[g] = __builtin_amdgcn_raw_buffer_load_b16(rx, voff, s * row4 * SZ + g * slot, 0);
+      xw[s][0] = v[0] | (v[1] << 16);
+      xw[s][1] = v[2] | (v[3] << 16);
+    };
+    if (n_steps == L) {
+#pragma unroll
+      for (int s = 0; s < L; ++s) load(s);
+    } else {
+#pragma unroll
+      for (int s = 0; s < L; ++s)
+        if (s < n_steps) load(s);
+    }
+  }
+  const rsrc_t ro = make_rsrc(out + first * row4 + c0, span4);
+
+  for (int p = 0; p <= P; ++p) {
+    const int tag = p + 1;
+    // Keep wx packed across stages: without this the compiler hoists the
+    // bf16 unpacking out of the stage loop and holds 4 floats per step.
+#pragma unroll
+    for (int s = 0; s < L; ++s) asm volatile("" : "+v"(xw[s][0]), "+v"(xw[s][1]));
+    // h_{p-1} at t0 - 1.
+    float hp0 = 0.f;
+    if (p > 0) {
+      if (t0 == 0) {
+        hp0 = h0h;
+      } else if (wave > 0) {
+        hp0 = s_hl[wave - 1][lane];
+      } else {
+        const unsigned long long* hw =
+            hlast + (p - 1) * stage_h + (static_cast<size_t>(tile) - B * n_cb) * kCB + lane;
+        int spins = 0;
+        while (true) {
+          const bool ok = ld_tagged(hw, tag - 1, hp0);
+          if (__ballot(!ok) == 0ull) break;
+          if (++spins > 8)
+            __builtin_amdgcn_s_sleep(8);
+          else
+            __builtin_amdgcn_s_sleep(1);
+        }
+      }
+    }
+
+    // Pass 1: this stage's pre-activations and the segment aggregate.
+    FG a = fg_identity();
+    auto step1 = [&](int s) {
+      if (p == 0) {
+        pre[s][0] = xw[s][0];
+        pre[s][1] = xw[s][1];
+      } else {
+        const float hp =
+            s == 0 ? hp0 : ((s - 1) & 1 ? hi_bf16(hh[(s - 1) >> 1]) : lo_bf16(hh[(s - 1) >> 1]));
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          // round(R h) and round(wx + round(R h)), two gates per conversion.
+          const uint32_t q = pack_bf16x2(r[2 * k] * hp, r[2 * k + 1] * hp);
+          pre[s][k] = pack_bf16x2(lo_bf16(xw[s][k]) + lo_bf16(q), hi_bf16(xw[s][k]) + hi_bf16(q));
+        }
+      }
+      const float zi = lo_bf16(pre[s][0]), zf = hi_bf16(pre[s][0]), zz = lo_bf16(pre[s][1]);
+      a.F += zf;
+      fg_step(zi, zf, zz, a.M, a.N, a.C);
+    };
+    if (n_steps == L) {
+#pragma unroll
+      for (int s = 0; s < L; ++s) step1(s);
+    } else {
+#pragma unroll
+      for (int s = 0; s < L; ++s)
+        if (s < n_steps) step1(s);
+    }
+    s_agg[wave][0][lane] = a.F;
+    s_agg[wave][1][lane] = a.M;
+    s_agg[wave][2][lane] = a.N;
+    s_agg[wave][3][lane] = a.C;
+    // Hold pre packed through the look-back: pass 2 unpacks it again rather
+    // than the compiler keeping four floats per step alive.
+#pragma unroll
+    for (int s = 0; s < L; ++s) asm volatile("" : "+v"(pre[s][0]), "+v"(pre[s][1]));
+    __syncthreads();
+
+    unsigned long long* incl_p = incl + p * stage_incl;
+    unsigned long long* agg_p = agg + p * stage_agg;
+    float carry[3] = {0.f, 0.f, 0.f};
+    if (wave == 0) {
+      FG tile_agg = fg_identity();
+#pragma unroll
+      for (int w = 0; w < W; ++w)
+        tile_agg = fg_compose(tile_agg, FG{s_agg[w][0][lane], s_agg[w][1][lane],
+                                           s_agg[w][2][lane], s_agg[w][3][lane]});
+      if (id.chunk == 0) {
+        carry[0] = c_init[0];
+        carry[1] = c_init[1];
+        carry[2] = c_init[2];
+      } else {
+        unsigned long long* ap = agg_p + (static_cast<size_t>(tile) * 4) * kCB + lane;
+        st_tagged(ap + 0 * kCB, tile_agg.F, tag);
+        st_tagged(ap + 1 * kCB, tile_agg.M, tag);
+        st_tagged(ap + 2 * kCB, tile_agg.N, tag);
+        st_tagged(ap + 3 * kCB, tile_agg.C, tag);
+      }
+    }
+    if (id.chunk > 0)
+      windowed_lookback<FrozenMonoid, W, KP>(id, B, n_cb, tag, incl_p, agg_p, lane, wave, s_lb,
+                                             carry);
+    if (wave == 0) {
+      float m = carry[0], n = carry[1], c = carry[2];
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        s_carry[w][0][lane] = m;
+        s_carry[w][1][lane] = n;
+        s_carry[w][2][lane] = c;
+        fg_apply(FG{s_agg[w][0][lane], s_agg[w][1][lane], s_agg[w][2][lane], s_agg[w][3][lane]},
+                 m, n, c);
+      }
+      unsigned long long* ip = incl_p + (static_cast<size_t>(tile) * 3) * kCB + lane;
+      st_tagged(ip, m, tag);
+      st_tagged(ip + kCB, n, tag);
+      st_tagged(ip + 2 * kCB, c, tag);
+    }
+    __syncthreads();
+
+    // Pass 2: replay from the true carry; h (bf16) stays in registers, the
+    // last stage writes the state.
+    float m = s_carry[wave][0][lane], n = s_carry[wave][1][lane], c = s_carry[wave][2][lane];
+    float h_even = 0.f, h_last = 0.f;
+    const bool last_stage = p == P;
+    auto step2 = [&](int s) {
+      const float zi = lo_bf16(pre[s][0]), zf = hi_bf16(pre[s][0]);
+      const float zz = lo_bf16(pre[s][1]), zo = hi_bf16(pre[s][1]);
+      fg_step(zi, zf, zz, m, n, c);
+      const float h = c * frcp((1.f + fexp(-zo)) * (n + eps));
+      if (last_stage) {
+        const uint32_t so = s * row4 * SZ;
+        stb<bf16>(ro, voff, so, c);
+        stb<bf16>(ro, voff, so + slot, n);
+        stb<bf16>(ro, voff, so + 2 * slot, m);
+        stb<bf16>(ro, voff, so + 3 * slot, h);
+      } else if (s & 1) {
+        hh[s >> 1] = pack_bf16x2(h_even, h);
+        h_last = hi_bf16(hh[s >> 1]);
+      } else {
+        h_even = h;
+        hh[s >> 1] = pack_bf16x2(h, h);
+        h_last = lo_bf16(hh[s >> 1]);
+      }
+    };
+    if (n_steps == L) {
+#pragma unroll
+      for (int s = 0; s < L; ++s) step2(s);
+    } else {
+#pragma unroll
+      for (int s = 0; s < L; ++s)
+        if (s < n_steps) step2(s);
+    }
+    if (!last_stage) {
+      s_hl[wave][lane] = h_last;
+      if (wave == W - 1)
+        st_tagged(hlast + p * stage_h + static_cast<size_t>(tile) * kCB + lane, h_last, tag);
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
 // (2) Newton iteration
 // ---------------------------------------------------------------------------
 
@@ -536,19 +767,62 @@ static Shape newton_shape(int dtype, bool work_in) {
   return work_in ? tiles().newton_work : tiles().newton_guess;
 }
 
+// All Picard passes in one launch (bf16 storage); PRNN_SLSTM_PICARD_FUSED=0
+// selects one launch per pass instead (the fp32 path always does).
+static bool picard_fused(int dtype) {
+  static const bool on = [] {
+    const char* e = getenv("PRNN_SLSTM_PICARD_FUSED");
+    return !(e && atoi(e) == 0);
+  }();
+  return dtype == PRNN_BF16 && on;
+}
+
+// Shapes of the fused launch: wx, the stage's pre-activations and h stay in
+// registers (4.5 per step).  PRNN_SLSTM_PICARD_TILES="<L>x<W>" for tuning.
+static const Shape kPicardShapes[] = {{24, 4}, {16, 4}, {20, 4}, {32, 4}};
+
+static Shape picard_shape() {
+  static const Shape s = [] {
+    Shape r{24, 4};
+    if (const char* e = getenv("PRNN_SLSTM_PICARD_TILES")) {
+      int l, w;
+      if (sscanf(e, "%dx%d", &l, &w) == 2)
+        for (const Shape& c : kPicardShapes)
+          if (c.L == l && c.W == w) r = c;
+    }
+    return r;
+  }();
+  return s;
+}
+
 struct InitWs {
   Lookback lb;
   void* hbuf[2];
+  unsigned long long* hlast;  // fused launch: [P][tile][64] tagged last-step h
+  bool fused;
 };
 
 static InitWs carve_init(void* base, int B, int T, int d, int P, int dtype, size_t* total) {
-  const Geo g = geometry(B, T, d, frozen_shape(dtype));
   Carver cv(base);
   InitWs w;
-  w.lb = carve_lookback(cv, g, 3, 4);
-  const size_t hb = static_cast<size_t>(B) * T * d * elem_size(dtype);
-  w.hbuf[0] = P >= 1 ? cv.take(hb) : nullptr;
-  w.hbuf[1] = P >= 2 ? cv.take(hb) : nullptr;
+  w.fused = picard_fused(dtype);
+  w.hbuf[0] = w.hbuf[1] = nullptr;
+  w.hlast = nullptr;
+  if (w.fused) {
+    // Stage-indexed look-back words (a tile may run stages ahead of the
+    // tiles that still read its earlier stages), cleared with the counters.
+    const Geo g = geometry(B, T, d, picard_shape());
+    w.lb = carve_lookback(cv, g, 3 * (P + 1), 4 * (P + 1));
+    w.hlast = static_cast<unsigned long long*>(
+        cv.take(sizeof(unsigned long long) * static_cast<size_t>(P) * kCB * g.n_tiles));
+    w.lb.clear_words = (cv.used - (reinterpret_cast<char*>(w.lb.counters) - cv.base)) / sizeof(int);
+  } else {
+    const Geo g = geometry(B, T, d, frozen_shape(dtype));
+    w.lb = carve_lookback(cv, g, 3, 4);
+    const size_t hb = static_cast<size_t>(B) * T * d * elem_size(dtype);
+    w.hbuf[0] = P >= 1 ? cv.take(hb) : nullptr;
+    w.hbuf[1] = P >= 2 ? cv.take(hb) : nullptr;
+  }
   *total = cv.used;
   return w;
 }
@@ -619,6 +893,24 @@ static int run_init(const TX* wx, const TX* r, const TX* h0, TX* states, int B, 
                     int P, float eps, const InitWs& w, hipStream_t stream) {
   int rc = clear_words(w.lb.counters, w.lb.clear_words, stream);
   if (rc != PRNN_OK) return rc;
+  if constexpr (sizeof(TX) == 2) {
+    if (w.fused) {
+      const Shape sh = picard_shape();
+      const Geo g = geometry(B, T, d, sh);
+#define PRNN_SHAPE(LL, WW, WPE)                                                                 \
+  if (sh.L == LL && sh.W == WW)                                                                 \
+    slstm_picard_fused_kernel<LL, WW, WPE><<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>(      \
+        wx, r, h0, states, B, T, d, g.n_cb, g.n_tiles, P, eps, w.lb.counters + 1, w.lb.agg,     \
+        w.lb.incl, w.hlast);
+      PRNN_SHAPE(24, 4, 3)
+      PRNN_SHAPE(16, 4, 4)
+      PRNN_SHAPE(20, 4, 3)
+      PRNN_SHAPE(32, 4, 2)
+#undef PRNN_SHAPE
+      PRNN_HIP(hipGetLastError());
+      return PRNN_OK;
+    }
+  }
   // Pass 0: zero-hidden scan (pre = wx); passes 1..P freeze wx + R h_prev.
   for (int p = 0; p <= P; ++p) {
     const TX* src = p == 0 ? nullptr : static_cast<const TX*>(w.hbuf[(p - 1) & 1]);
