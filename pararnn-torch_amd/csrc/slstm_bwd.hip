@@ -276,8 +276,8 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
 
 // g_r[g][ch] = sum over the tiles of ch's (b, channel block) of the partials.
 // One block per (gate, channel block): lane = channel, each of the 16 waves
-// sums a fixed quarter of the tiles (coalesced 256-byte rows), then the
-// quarters combine in LDS in a fixed order (deterministic).
+// sums a fixed share of the tiles (coalesced 256-byte rows), then the
+// shares combine in LDS in a fixed order (deterministic).
 constexpr int kReduceWaves = 16;
 __global__ __launch_bounds__(64 * kReduceWaves) void slstm_gr_reduce_kernel(
     const float* __restrict__ gr_part, float* __restrict__ gr, int B, int d, int n_cb,
