@@ -6,14 +6,14 @@
 //     J = diag(1-z) + diag((n-h) z(1-z)) A_z^T
 //         + diag(z (1-n^2)) A_n^T (diag(r) + diag(h r(1-r)) A_r^T)
 // (reference cells/para_gru.py:385-412, solvers/scan.py:103-123).  Time is cut
-// into chunks of kChunk steps:
+// into chunks of kChunk steps; per Newton iteration:
 //
-//  gru_chunk_kernel   per chunk: gates of all steps, then the chunk transfer
-//                     Phi = J_last ... J_first and the zero-carry local solution
-//                     e (e <- J e + F).  Per step two 64x64x64 products on MFMA
-//                     (v_mfma_f32_16x16x32_bf16, fp32 accumulate): the
-//                     Jacobian's A_n^T D A_r^T term and J Phi; e is an fp32
-//                     mat-vec on the assembled J;
+//  gru_phi_kernel     per chunk: the chunk transfer Phi = J_last ... J_first
+//                     (gates of all steps by fp32 MFMA GEMMs, then per step
+//                     three bf16 MFMA products of the factorised J with Phi
+//                     held in registers, fp32 accumulation);
+//  gru_replay_kernel  LOCAL: per chunk, the exact fp32 recurrence from a zero
+//                     carry, giving the chunk's local solution e;
 //  gru_carry_kernel   per sequence: carry_c = Phi_c carry_{c-1} + e_c over the
 //                     chunks, serially (one 64x64 mat-vec per chunk, fp32);
 //  gru_replay_kernel  per chunk: the exact fp32 recurrence from the chunk's
@@ -22,7 +22,7 @@
 //
 // Phi is composed from bf16-rounded operands and only multiplies the carry
 // entering a chunk; e and every delta_t are fp32, so the bf16 rounding reaches
-// the result only through Phi times the carry (measured ~1e-7 at K = 3).
+// the result only through Phi times the carry.
 #include "prnn_common.h"
 #include "pararnn_amd.h"
 #include "prnn_host.h"
@@ -150,187 +150,254 @@ __global__ __launch_bounds__(64) void gru_init_kernel(const TX* __restrict__ wx,
 }
 
 // ---------------------------------------------------------------------------
-// Chunk transfer.  256 threads = 4 waves; wave w owns rows 16w..16w+15 of
-// every 64-row product.
+// Chunk transfer Phi = J_last ... J_first.  256 threads = 4 waves; wave w owns
+// columns 16w..16w+15 of Phi and keeps them in registers for the whole chunk.
+//
+// Phase A (gates of every step of the chunk) runs as fp32 MFMA GEMMs over the
+// chunk's steps: [steps x 64] h_prev times A_z, A_r, then (h_prev r) times
+// A_n, each wave producing its 16 output channels; the per-step row scalars
+// of J (d1 = 1-z, d2 = (n-h) z(1-z), d3 = z(1-n^2), r, d5 = h r(1-r)) go to
+// LDS.
+//
+// Phase B: J Phi = d1 Phi + d2 (A_z^T Phi) + d3 A_n^T (r Phi + d5 (A_r^T Phi))
+// (rows scaled by the d's), three bf16 MFMA products per step with fp32
+// accumulation and no J formed.  The contraction index of every product is
+// permuted so that the accumulator layout of Phi (lane holds rows
+// 16 rt + 4 g + v of its column, g = lane / 16) is exactly the next B
+// operand: Phi never leaves the wave's registers and the step loop has no
+// barrier.
 // ---------------------------------------------------------------------------
-struct ChunkShared {
-  float vec[kChunk][5][DH];                   // per step: h_prev, z, r, n, F
-  float h[4][DH], u[4][DH];                   // per-wave gate scratch
-  float e[2][DH];                                          // local solution e (fp32)
-  __attribute__((aligned(16))) __bf16 J[DH][kPad];         // J rows (row-major)
-  __attribute__((aligned(16))) __bf16 phiT[2][DH][kPad];   // Phi transposed ([col][row])
+constexpr int kRowPad = DH + 4;  // fp32 LDS row stride of the A-operand tiles (bank spread)
+
+// D(16x16) += A(16x4) B(4x16) in fp32: lane l holds A[l%16][l/16], B[l/16][l%16],
+// D[4(l/16)+v][l%16].
+__device__ __forceinline__ floatx4 mfma_f32(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+struct PhiShared {
+  float hp[kChunk][kRowPad];  // h_prev per step; later d5
+  float r[kChunk][kRowPad];   // r per step
+  float x[3][kChunk][DH];     // zx, rx, nx; later d1, d2, d3
 };
 
 template <typename TX>
-__global__ __launch_bounds__(256) void gru_chunk_kernel(
+__global__ __launch_bounds__(256) void gru_phi_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ a_z, const TX* __restrict__ a_r,
     const TX* __restrict__ a_n, const TX* __restrict__ h0, const float* __restrict__ hin, int B,
-    int T, int H, int n_chunks, float* __restrict__ phi_out, float* __restrict__ e_out) {
-  __shared__ ChunkShared sh;
+    int T, int H, int n_chunks, float* __restrict__ phi_out) {
+  __shared__ PhiShared sh;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = lane & 15, g = lane >> 4;
   const int d = H * DH;
   const int seq = blockIdx.x / n_chunks, c = blockIdx.x % n_chunks;
   const int b = seq / H, head = seq % H;
   const int t0 = c * kChunk;
   const int len = min(kChunk, T - t0);
-
-  // Phase A: gates, prediction and residual of every step (wave w: steps w, w+4, ...).
-  {
-    float az[DH], ar[DH], an[DH];
-    load_col(a_z, head, lane, az);
-    load_col(a_r, head, lane, ar);
-    load_col(a_n, head, lane, an);
-    for (int s = wave; s < len; s += 4) {
-      const int t = t0 + s;
-      float hp = 0.f;
-      bool zero_h = true;
-      if (t > 0) {
-        hp = hin[h_at(b, t - 1, T, d, head, lane)];
-        zero_h = false;
-      } else if (h0 != nullptr) {
-        hp = ld(h0 + static_cast<size_t>(b) * d + head * DH + lane);
-        zero_h = false;
-      }
-      sh.h[wave][lane] = hp;
-      __builtin_amdgcn_wave_barrier();
-      const Gates g = gates_step(sh.h[wave], sh.u[wave], hp, ld(wx + wx_at(b, t, T, d, 0, head, lane)),
-                                 ld(wx + wx_at(b, t, T, d, 1, head, lane)),
-                                 ld(wx + wx_at(b, t, T, d, 2, head, lane)), az, ar, an, zero_h);
-      sh.vec[s][0][lane] = hp;
-      sh.vec[s][1][lane] = g.z;
-      sh.vec[s][2][lane] = g.r;
-      sh.vec[s][3][lane] = g.n;
-      sh.vec[s][4][lane] = g.h_new - hin[h_at(b, t, T, d, head, lane)];
-      __builtin_amdgcn_wave_barrier();
-    }
-  }
-
-  // Phase B constants for this wave.
-  const int li = lane & 15, lq = lane >> 4;  // MFMA lane coordinates
-  const int row_a = 16 * wave + li;           // A-operand row
-  float anT[2][8];                            // A_n^T[row_a][k] = A_n[k][row_a]
-  bf16x8 arT[4][2];                           // B operand A_r^T[k][n] = A_r[n][k]
-  float azD[4][4], anD[4][4];                 // A_z[j][i], A_n[j][i] at D positions
   const size_t hoff = static_cast<size_t>(head) * DH * DH;
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-    for (int q = 0; q < 8; ++q) anT[ks][q] = ld(a_n + hoff + (32 * ks + 8 * lq + q) * DH + row_a);
-#pragma unroll
-  for (int tn = 0; tn < 4; ++tn)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int q = 0; q < 8; ++q)
-        arT[tn][ks][q] = static_cast<__bf16>(ld(a_r + hoff + (16 * tn + li) * DH + 32 * ks + 8 * lq + q));
-#pragma unroll
-  for (int tn = 0; tn < 4; ++tn)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int i = 16 * wave + 4 * lq + v, j = 16 * tn + li;
-      azD[tn][v] = ld(a_z + hoff + j * DH + i);
-      anD[tn][v] = ld(a_n + hoff + j * DH + i);
-    }
-  // Phi = I, e = 0.
-  for (int idx = threadIdx.x; idx < DH * DH; idx += 256) {
-    const int n = idx / DH, k = idx % DH;
-    sh.phiT[0][n][k] = static_cast<__bf16>(n == k ? 1.f : 0.f);
-  }
-  if (threadIdx.x < DH) sh.e[0][threadIdx.x] = 0.f;
-  __syncthreads();
 
-  floatx4 P[4];
-  int cur = 0;
-  for (int s = 0; s < len; ++s) {
-    const float* hp = sh.vec[s][0];
-    const float* z = sh.vec[s][1];
-    const float* r = sh.vec[s][2];
-    const float* n = sh.vec[s][3];
-    // (a) M = (A_n^T diag(d5)) A_r^T, d5 = h r (1 - r).
-    bf16x8 a[2];
+  // ---- inputs of the chunk into LDS (zero rows past the end); unrolled so
+  // every load of the chunk is in flight at once ----
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int k = 32 * ks + 8 * lq + q;
-        a[ks][q] = static_cast<__bf16>(anT[ks][q] * (hp[k] * r[k] * (1.f - r[k])));
-      }
-    floatx4 M[4];
-#pragma unroll
-    for (int tn = 0; tn < 4; ++tn) {
-      M[tn] = floatx4{0.f, 0.f, 0.f, 0.f};
-      M[tn] = mfma(a[0], arT[tn][0], M[tn]);
-      M[tn] = mfma(a[1], arT[tn][1], M[tn]);
+  for (int idx = threadIdx.x; idx < kChunk * DH; idx += 256) {
+    const int s = idx / DH, j = idx % DH;
+    const int t = t0 + s;
+    float hp = 0.f, zx = 0.f, rx = 0.f, nx = 0.f;
+    if (s < len) {
+      if (t > 0)
+        hp = hin[h_at(b, t - 1, T, d, head, j)];
+      else if (h0 != nullptr)
+        hp = ld(h0 + static_cast<size_t>(b) * d + head * DH + j);
+      zx = ld(wx + wx_at(b, t, T, d, 0, head, j));
+      rx = ld(wx + wx_at(b, t, T, d, 1, head, j));
+      nx = ld(wx + wx_at(b, t, T, d, 2, head, j));
     }
-    // (b) J = diag(d1) + diag(d2) A_z^T + diag(d3) (A_n^T diag(d4) + M) at the D
-    // positions; e' = J e + F in fp32 (row sums over the 16 lanes of a row group).
-    const float* ecur = sh.e[cur];
-    float ev[4];
+    sh.hp[s][j] = hp;
+    sh.x[0][s][j] = zx;
+    sh.x[1][s][j] = rx;
+    sh.x[2][s][j] = nx;
+  }
+
+  // ---- phase A: gates by fp32 MFMA (wave w: output channels 16w + li) ----
+  const int col = 16 * wave + li;
+  floatx4 gz[2], gr[2], gn[2];
+  {
+    // B operands: A[k][col] for k = 16 g + kk (the contraction order every
+    // lane uses for its A operand below).
+    float bz[16], br[16], bn[16];
 #pragma unroll
-    for (int tn = 0; tn < 4; ++tn) ev[tn] = ecur[16 * tn + li];
-    float esum[4];
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int i = 16 * wave + 4 * lq + v;
-      const float zi = z[i], ni = n[i];
-      const float d1 = 1.f - zi;
-      const float d2 = (ni - hp[i]) * zi * (1.f - zi);
-      const float d3 = zi * (1.f - ni * ni);
-      float part = 0.f;
-#pragma unroll
-      for (int tn = 0; tn < 4; ++tn) {
-        const int j = 16 * tn + li;
-        float Jv = d2 * azD[tn][v] + d3 * (anD[tn][v] * r[j] + M[tn][v]);
-        if (i == j) Jv += d1;
-        sh.J[i][j] = static_cast<__bf16>(Jv);
-        part += Jv * ev[tn];
-      }
-      esum[v] = part;
-    }
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) esum[v] += __shfl_xor(esum[v], m);
-    __builtin_amdgcn_wave_barrier();
-    // (c) Phi' = J Phi, rows of this wave.
-    bf16x8 aj[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) aj[ks] = *reinterpret_cast<const bf16x8*>(&sh.J[row_a][32 * ks + 8 * lq]);
-#pragma unroll
-    for (int tn = 0; tn < 4; ++tn) {
-      P[tn] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8 bp = *reinterpret_cast<const bf16x8*>(&sh.phiT[cur][16 * tn + li][32 * ks + 8 * lq]);
-        P[tn] = mfma(aj[ks], bp, P[tn]);
-      }
-    }
-    const int nxt = cur ^ 1;
-#pragma unroll
-    for (int tn = 0; tn < 4; ++tn)
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        sh.phiT[nxt][16 * tn + li][16 * wave + 4 * lq + v] = static_cast<__bf16>(P[tn][v]);
-    if (li == 0) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int i = 16 * wave + 4 * lq + v;
-        sh.e[nxt][i] = esum[v] + sh.vec[s][4][i];
-      }
+    for (int kk = 0; kk < 16; ++kk) {
+      const size_t o = hoff + static_cast<size_t>(16 * g + kk) * DH + col;
+      bz[kk] = ld(a_z + o);
+      br[kk] = ld(a_r + o);
+      bn[kk] = ld(a_n + o);
     }
     __syncthreads();
-    cur = nxt;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      gz[rt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      gr[rt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      const float* hrow = &sh.hp[16 * rt + li][16 * g];
+#pragma unroll
+      for (int kk = 0; kk < 16; kk += 4) {
+        const float4 a4 = *reinterpret_cast<const float4*>(hrow + kk);
+        const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          gz[rt] = mfma_f32(av[q], bz[kk + q], gz[rt]);
+          gr[rt] = mfma_f32(av[q], br[kk + q], gr[rt]);
+        }
+      }
+    }
+    // r at the D positions (step 16 rt + 4 g + v, channel col) -> LDS
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int s = 16 * rt + 4 * g + v;
+        gr[rt][v] = fsigmoid(gr[rt][v] + sh.x[1][s][col]);
+        gz[rt][v] = fsigmoid(gz[rt][v] + sh.x[0][s][col]);
+        sh.r[s][col] = gr[rt][v];
+      }
+    __syncthreads();
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      gn[rt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      const float* hrow = &sh.hp[16 * rt + li][16 * g];
+      const float* rrow = &sh.r[16 * rt + li][16 * g];
+#pragma unroll
+      for (int kk = 0; kk < 16; kk += 4) {
+        const float4 h4 = *reinterpret_cast<const float4*>(hrow + kk);
+        const float4 r4 = *reinterpret_cast<const float4*>(rrow + kk);
+        const float av[4] = {h4.x * r4.x, h4.y * r4.y, h4.z * r4.z, h4.w * r4.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) gn[rt] = mfma_f32(av[q], bn[kk + q], gn[rt]);
+      }
+    }
   }
-  // Output the chunk transfer (fp32 accumulators of the last step).
+  // Row scalars of J per step at (step, channel col).
+  float rs[2][4][5];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int s = 16 * rt + 4 * g + v;
+      const float z = gz[rt][v], r = gr[rt][v];
+      const float n = ftanh(gn[rt][v] + sh.x[2][s][col]);
+      const float hp = sh.hp[s][col];
+      rs[rt][v][0] = 1.f - z;
+      rs[rt][v][1] = (n - hp) * z * (1.f - z);
+      rs[rt][v][2] = z * (1.f - n * n);
+      rs[rt][v][3] = r;
+      rs[rt][v][4] = hp * r * (1.f - r);
+    }
+  __syncthreads();  // every read of hp / x / r above is done
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int s = 16 * rt + 4 * g + v;
+      sh.x[0][s][col] = rs[rt][v][0];
+      sh.x[1][s][col] = rs[rt][v][1];
+      sh.x[2][s][col] = rs[rt][v][2];
+      sh.r[s][col] = rs[rt][v][3];
+      sh.hp[s][col] = rs[rt][v][4];
+    }
+
+  // ---- phase B constants: A^T operands in bf16, contraction permuted ----
+  // Product X = A^T P for output row tile rt, step ks: lane (li, g) supplies
+  // A^T[16 rt + li][k] = A[k][16 rt + li] for the 8 k of its slots
+  // k = 16 (2 ks + q / 4) + 4 g + q % 4, q = 0..7.
+  bf16x8 atz[4][2], atr[4][2], atn[4][2];
+  auto load_at = [&](const TX* A, bf16x8 at[4][2]) {
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int k = 16 * (2 * ks + (q >> 2)) + 4 * g + (q & 3);
+          at[rt][ks][q] = static_cast<__bf16>(ld(A + hoff + static_cast<size_t>(k) * DH + 16 * rt + li));
+        }
+  };
+  // one matrix at a time (bounds the registers of the loads in flight)
+  load_at(a_z, atz);
+  __builtin_amdgcn_sched_barrier(0);
+  load_at(a_r, atr);
+  __builtin_amdgcn_sched_barrier(0);
+  load_at(a_n, atn);
+  __syncthreads();
+
+  // Phi = I on this wave's columns: lane holds Phi[16 rt + 4 g + v][col].
+  float P[4][4];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) P[rt][v] = (16 * rt + 4 * g + v == col) ? 1.f : 0.f;
+
+  // B operand of a product from D-layout values: slots of step ks are rows
+  // 16 (2 ks) + 4 g + (0..3) then 16 (2 ks + 1) + 4 g + (0..3).
+  auto to_b = [](const float X[4][4], bf16x8 out[2]) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) out[ks][q] = static_cast<__bf16>(X[2 * ks + (q >> 2)][q & 3]);
+  };
+  auto product = [](const bf16x8 at[4][2], const bf16x8 bop[2], float X[4][4]) {
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = mfma(at[rt][0], bop[0], acc);
+      acc = mfma(at[rt][1], bop[1], acc);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) X[rt][v] = acc[v];
+    }
+  };
+
+  for (int s = 0; s < len; ++s) {
+    bf16x8 bp[2];
+    to_b(P, bp);
+    float X1[4][4], X2[4][4];
+    product(atz, bp, X1);
+    product(atr, bp, X2);
+    // Row scalars are read per row tile after the products are issued (kept
+    // out of the registers that hold Phi and the A^T operands).
+    __builtin_amdgcn_sched_barrier(0);
+    // Y = r P + d5 X2;  P <- d1 P + d2 X1 (partial)
+    float Y[4][4];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      const int i = 16 * rt + 4 * g;
+      const float4 r4 = *reinterpret_cast<const float4*>(&sh.r[s][i]);
+      const float4 d5 = *reinterpret_cast<const float4*>(&sh.hp[s][i]);
+      const float4 d1 = *reinterpret_cast<const float4*>(&sh.x[0][s][i]);
+      const float4 d2 = *reinterpret_cast<const float4*>(&sh.x[1][s][i]);
+      const float rv[4] = {r4.x, r4.y, r4.z, r4.w}, d5v[4] = {d5.x, d5.y, d5.z, d5.w};
+      const float d1v[4] = {d1.x, d1.y, d1.z, d1.w}, d2v[4] = {d2.x, d2.y, d2.z, d2.w};
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        Y[rt][v] = rv[v] * P[rt][v] + d5v[v] * X2[rt][v];
+        P[rt][v] = d1v[v] * P[rt][v] + d2v[v] * X1[rt][v];
+      }
+    }
+    bf16x8 by[2];
+    to_b(Y, by);
+    float X3[4][4];
+    product(atn, by, X3);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      const float4 d3 = *reinterpret_cast<const float4*>(&sh.x[2][s][16 * rt + 4 * g]);
+      const float d3v[4] = {d3.x, d3.y, d3.z, d3.w};
+#pragma unroll
+      for (int v = 0; v < 4; ++v) P[rt][v] += d3v[v] * X3[rt][v];
+    }
+  }
   float* po = phi_out + static_cast<size_t>(blockIdx.x) * DH * DH;
-  float* eo = e_out + static_cast<size_t>(blockIdx.x) * DH;
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int i = 16 * wave + 4 * lq + v;
+  for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-    for (int tn = 0; tn < 4; ++tn) po[i * DH + 16 * tn + li] = P[tn][v];
-  }
-  if (threadIdx.x < DH) eo[threadIdx.x] = sh.e[cur][threadIdx.x];
+    for (int v = 0; v < 4; ++v) po[(16 * rt + 4 * g + v) * DH + col] = P[rt][v];
 }
 
 // ---------------------------------------------------------------------------
@@ -379,13 +446,17 @@ __global__ __launch_bounds__(256) void gru_carry_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 // Replay: the exact fp32 recurrence of one chunk from its carry.  Each wave
 // handles one chunk; lane j keeps column j of A_z, A_r, A_n in registers.
+// LOCAL: from a zero carry, writing only the chunk's final delta (the local
+// solution e of the carry scan); otherwise from the chunk's carry, writing
+// H + omega delta.  The inputs of step s + 2 are loaded while step s
+// computes (the recurrence itself is serial).
 // ---------------------------------------------------------------------------
-template <typename TX, typename TOUT>
+template <typename TX, typename TOUT, bool LOCAL>
 __global__ __launch_bounds__(256) void gru_replay_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ a_z, const TX* __restrict__ a_r,
     const TX* __restrict__ a_n, const TX* __restrict__ h0, const float* __restrict__ hin,
-    const float* __restrict__ carry_in, TOUT* __restrict__ hout, int B, int T, int H,
-    int n_chunks, float omega) {
+    const float* __restrict__ carry_in, TOUT* __restrict__ hout, float* __restrict__ e_out,
+    int B, int T, int H, int n_chunks, float omega) {
   __shared__ float s_v[4][4][DH];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int task = blockIdx.x * 4 + wave;
@@ -404,25 +475,36 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
   load_col(a_z, head, lane, az);
   load_col(a_r, head, lane, ar);
   load_col(a_n, head, lane, an);
-  float dl = carry_in[static_cast<size_t>(task) * DH + lane];
-  for (int s = 0; s < len; ++s) {
-    const int t = t0 + s;
-    float hp = 0.f;
-    bool zero_h = true;
-    if (t > 0) {
-      hp = hin[h_at(b, t - 1, T, d, head, lane)];
-      zero_h = false;
-    } else if (h0 != nullptr) {
-      hp = ld(h0 + static_cast<size_t>(b) * d + head * DH + lane);
-      zero_h = false;
+  float dl = LOCAL ? 0.f : carry_in[static_cast<size_t>(task) * DH + lane];
+
+  struct In {
+    float hp, zx, rx, nx, ht;
+  };
+  auto load_in = [&](int s) {
+    In v{0.f, 0.f, 0.f, 0.f, 0.f};
+    if (s < len) {
+      const int t = t0 + s;
+      if (t > 0)
+        v.hp = hin[h_at(b, t - 1, T, d, head, lane)];
+      else if (h0 != nullptr)
+        v.hp = ld(h0 + static_cast<size_t>(b) * d + head * DH + lane);
+      v.zx = ld(wx + wx_at(b, t, T, d, 0, head, lane));
+      v.rx = ld(wx + wx_at(b, t, T, d, 1, head, lane));
+      v.nx = ld(wx + wx_at(b, t, T, d, 2, head, lane));
+      v.ht = hin[h_at(b, t, T, d, head, lane)];
     }
+    return v;
+  };
+  In cur = load_in(0), nx1 = load_in(1);
+  for (int s = 0; s < len; ++s) {
+    const In nx2 = load_in(s + 2);
+    const int t = t0 + s;
+    const bool zero_h = t == 0 && h0 == nullptr;
+    const float hp = cur.hp;
     s_h[lane] = hp;
     s_d[lane] = dl;
     __builtin_amdgcn_wave_barrier();
-    const Gates g = gates_step(s_h, s_u, hp, ld(wx + wx_at(b, t, T, d, 0, head, lane)),
-                               ld(wx + wx_at(b, t, T, d, 1, head, lane)),
-                               ld(wx + wx_at(b, t, T, d, 2, head, lane)), az, ar, an, zero_h);
-    const float h_t = hin[h_at(b, t, T, d, head, lane)];
+    const Gates g = gates_step(s_h, s_u, hp, cur.zx, cur.rx, cur.nx, az, ar, an, zero_h);
     // J delta = (1-z) delta + d2 (delta @ A_z) + d3 ((r delta + d5 (delta @ A_r)) @ A_n)
     const float yz = vec_col(s_d, az);
     const float yr = vec_col(s_d, ar);
@@ -432,10 +514,13 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
     const float yn = vec_col(s_w, an);
     const float d2 = (g.n - hp) * g.z * (1.f - g.z);
     const float d3 = g.z * (1.f - g.n * g.n);
-    dl = (1.f - g.z) * dl + d2 * yz + d3 * yn + (g.h_new - h_t);
-    st(hout + h_at(b, t, T, d, head, lane), h_t + omega * dl);
+    dl = (1.f - g.z) * dl + d2 * yz + d3 * yn + (g.h_new - cur.ht);
+    if (!LOCAL) st(hout + h_at(b, t, T, d, head, lane), cur.ht + omega * dl);
     __builtin_amdgcn_wave_barrier();
+    cur = nx1;
+    nx1 = nx2;
   }
+  if (LOCAL) e_out[static_cast<size_t>(task) * DH + lane] = dl;
 }
 
 // ---------------------------------------------------------------------------
@@ -504,17 +589,21 @@ static int run(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX*
   const int replay_blocks = (n_seq * n_chunks + 3) / 4;
   for (int k = 1; k <= K; ++k) {
     const float* hin = w.work[(k - 1) & 1];
-    gru_chunk_kernel<TX><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
-        wx, az, ar, an, h0, hin, B, T, H, n_chunks, w.phi, w.e);
+    gru_phi_kernel<TX><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
+        wx, az, ar, an, h0, hin, B, T, H, n_chunks, w.phi);
+    PRNN_HIP(hipGetLastError());
+    gru_replay_kernel<TX, float, true><<<dim3(replay_blocks), dim3(256), 0, stream>>>(
+        wx, az, ar, an, h0, hin, nullptr, static_cast<float*>(nullptr), w.e, B, T, H, n_chunks,
+        omega);
     PRNN_HIP(hipGetLastError());
     gru_carry_kernel<<<dim3(n_seq), dim3(256), 0, stream>>>(w.phi, w.e, n_chunks, w.carry);
     PRNN_HIP(hipGetLastError());
     if (k == K) {
-      gru_replay_kernel<TX, TX><<<dim3(replay_blocks), dim3(256), 0, stream>>>(
-          wx, az, ar, an, h0, hin, w.carry, out, B, T, H, n_chunks, omega);
+      gru_replay_kernel<TX, TX, false><<<dim3(replay_blocks), dim3(256), 0, stream>>>(
+          wx, az, ar, an, h0, hin, w.carry, out, nullptr, B, T, H, n_chunks, omega);
     } else {
-      gru_replay_kernel<TX, float><<<dim3(replay_blocks), dim3(256), 0, stream>>>(
-          wx, az, ar, an, h0, hin, w.carry, w.work[k & 1], B, T, H, n_chunks, omega);
+      gru_replay_kernel<TX, float, false><<<dim3(replay_blocks), dim3(256), 0, stream>>>(
+          wx, az, ar, an, h0, hin, w.carry, w.work[k & 1], nullptr, B, T, H, n_chunks, omega);
     }
     PRNN_HIP(hipGetLastError());
   }
