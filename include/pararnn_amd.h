@@ -31,6 +31,12 @@
  *                            166-178) + slstm_recurrence_vjp (kernels/
  *                            vjp_slstm.py:209-240) + _t0_state_vjp
  *                            (solvers/newton/dispatch.py:406-410)
+ *   prnn_slstm_decode     -> kernels/decode.py:420-467, 553-597 (_slstm_decode_kernel,
+ *                            decode_step for ParaSLSTM mix='diag')
+ *   prnn_gru_decode       -> kernels/decode.py:260-334, 472-501 (_gru_decode_kernel,
+ *                            decode_step for ParaGRU mix='diag'); mix='head' replaces
+ *                            the eager cell.step the reference runs for that mix
+ *                            (cells/para_gru.py:443-467)
  */
 #ifndef PARARNN_AMD_H
 #define PARARNN_AMD_H
@@ -105,6 +111,21 @@ PRNN_API int prnn_slstm_backward(const void* wx, const void* r, const void* h0,
                                  const void* states, const void* grad, void* g_wx, float* g_r,
                                  float* g_h0, int B, int T, int d, float eps, int dtype,
                                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- T = 1 decode (serving loop) -----------------------------------------
+ * One recurrent step.  state / out: (rows, 4, d) sLSTM or (rows, d) GRU;
+ * wx: (B, 4d) / (B, 3d) for this step.  block_table: NULL (row b of state is
+ * batch b, out has state's shape) or B int32 slot ids into pool-shaped
+ * state / out (in place when out == state).  The recurrent parameters (r
+ * (4, d); GRU a_* (d) for n_heads = 0, or (n_heads, 64, 64) (in, out)) are
+ * clamped to +-cap in the kernel when has_cap.  No workspace.
+ */
+PRNN_API int prnn_slstm_decode(const void* state, const void* wx, const void* r, void* out,
+                               const int* block_table, int B, int d, float eps, float cap,
+                               int has_cap, int dtype, void* stream);
+PRNN_API int prnn_gru_decode(const void* h, const void* wx, const void* a_z, const void* a_r,
+                             const void* a_n, void* out, const int* block_table, int B, int d,
+                             int n_heads, float cap, int has_cap, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

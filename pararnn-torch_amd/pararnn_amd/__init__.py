@@ -9,6 +9,7 @@ names (``pararnn::newton_slstm_fused``, ``pararnn::newton_gru_head_fused``).
 """
 
 from pararnn_amd.cells import ParaGRU, ParaSLSTM
+from pararnn_amd.decode import can_decode_step, decode_step, decode_wx
 from pararnn_amd.config import (
     LIBRARY_NEWTON_ITERS,
     NewtonConfig,
@@ -44,6 +45,9 @@ __all__ = [
     "ParaGRU",
     "ParaSLSTM",
     "auto_newton_iters",
+    "can_decode_step",
+    "decode_step",
+    "decode_wx",
     "compile_safe_config",
     "default_agreement_atol",
     "fused_newton",

@@ -1,6 +1,7 @@
 """Sequential unroll — the numerics oracle that ``verify_agreement`` compares
 against (reference ``solvers/sequential.py:22-86``).  Plain torch ops on the
-tensors' device: one shared ``W_x`` GEMM, then ``cell.step`` over T.
+tensors' device: one shared ``W_x`` GEMM, then ``cell.step`` over T; a single
+step without autograd on the GPU goes through ``decode_step``.
 """
 
 from __future__ import annotations
@@ -33,6 +34,13 @@ def sequential_apply(cell: nn.Module, x: Tensor, h0: Tensor | None = None, *, st
         lin = getattr(cell, "W_x", None)
         if lin is not None:
             wx_all = lin(x)
+    if step is None and time == 1 and not torch.is_grad_enabled():
+        from pararnn_amd.decode import can_decode_step, decode_step
+
+        if can_decode_step(cell, x):
+            # T = 1 without autograd: the decode kernel (sequential.py:77-81)
+            wx_t = None if wx_all is None else wx_all[:, 0]
+            return decode_step(cell, h, x[:, 0], wx=wx_t).unsqueeze(1)
     outs = []
     for t in range(time):
         h = fn(h, x[:, t]) if wx_all is None else fn(h, x[:, t], wx=wx_all[:, t])

@@ -115,3 +115,23 @@ def test_ops_validate_before_launch():
     a = torch.randn(2, 64, 64)
     with pytest.raises(ValueError):
         ops.newton_gru_head_fused(torch.randn(1, 3, 100), a, a, a, max_iters=1, omega=1.0)
+
+
+def test_decode_step_host_rules():
+    # CPU tensors: the reference runs the cell's own step there
+    # (kernels/decode.py:172-179); block_table needs the GPU kernel.
+    from pararnn_amd import ParaSLSTM, can_decode_step, decode_step, decode_wx
+
+    torch.manual_seed(0)
+    cell = ParaSLSTM(6, 8)
+    state = torch.zeros(2, 4, 8)
+    x = torch.randn(2, 1, 6)
+    assert not can_decode_step(cell, x)
+    with torch.no_grad():
+        y = decode_step(cell, state, x[:, 0])
+        assert torch.allclose(y, cell.step(state, x[:, 0]))
+        assert decode_wx(cell, x).shape == (2, 32)
+        with pytest.raises(RuntimeError, match="block_table"):
+            decode_step(cell, state, x[:, 0], block_table=torch.tensor([0, 1]))
+    with pytest.raises(ValueError, match="x or wx"):
+        decode_step(cell, state)
