@@ -30,6 +30,12 @@ from torch import Tensor, nn
 
 from pararnn_amd import ops
 from pararnn_amd.cells import SLSTM_HIDDEN, ParaGRU, ParaSLSTM
+from pararnn_amd.ragged import (
+    Padding,
+    gather_h0,
+    prepend_state_ragged,
+    validate_cu_seqlens,
+)
 from pararnn_amd.config import (
     _RESIDUAL_WARN,
     LIBRARY_NEWTON_ITERS,
@@ -161,12 +167,21 @@ def fused_newton(
             wx, a_z, a_r, a_n, h0, cu_seqlens, max_iters=max_iters, omega=omega
         )
     if isinstance(cell, ParaSLSTM) and cell.mix == "diag":
+        if block_table is not None:
+            # paged h0 rows, for the guess and the iterations alike
+            h0 = gather_h0(h0, block_table, wx.shape[0], (4, int(cell.d_h)))
         if cu_seqlens is not None:
-            raise TypeError("pararnn_amd fused ParaSLSTM does not take cu_seqlens")
+            # packed sequences as a padded batch, each from its own h0
+            pad = Padding(validate_cu_seqlens(cu_seqlens, wx.shape[1]), wx.device)
+            dense = fused_newton(cell, pad.pad(wx), max_iters=max_iters, omega=omega, h0=h0,
+                                 log_coords=log_coords, picard_iters=picard_iters,
+                                 scan_tile=scan_tile, fused_time_loop=fused_time_loop,
+                                 fused_window_len=fused_window_len)
+            return pad.unpad(dense)
         r = cell.clipped_r()
         states = ops.slstm_init_fused(wx, r, h0, picard_iters=int(picard_iters), eps=cell.eps)
         return ops.newton_slstm_fused(
-            wx, r, h0, states, block_table,
+            wx, r, h0, states, None,
             max_iters=max_iters, omega=omega, eps=cell.eps, log_coords=log_coords,
             scan_tile=scan_tile, time_loop=fused_time_loop,
             window_len=0 if fused_window_len is None else int(fused_window_len),
@@ -299,21 +314,25 @@ def newton_apply(
             config,
             max_iters=auto_newton_iters(cell, x.shape[1], schedule=config.newton_iters_by_t),
         )
-    config = _resolve_backend(cell, x, config)
     if cu_seqlens is not None:
-        raise TypeError(
-            "packed cu_seqlens batches are not provided by pararnn_amd; pad to a rectangular batch"
-        )
-    if block_table is not None:
-        if config.chunk_len is not None:
-            raise ValueError("block_table cannot be combined with chunk_len")
-        raise TypeError("block_table (paged h0) is not provided by pararnn_amd")
+        _check_ragged_args(x, config)
+    config = _resolve_backend(cell, x, config)
     params = tuple(cell.parameters())
     needs_grad = torch.is_grad_enabled() and (
         x.requires_grad
         or (h0 is not None and h0.requires_grad)
         or any(p.requires_grad for p in params)
     )
+    if block_table is not None:
+        if config.chunk_len is not None:
+            raise ValueError("block_table cannot be combined with chunk_len")
+        if needs_grad:
+            raise RuntimeError("block_table newton is inference-only")
+    if cu_seqlens is not None:
+        return _newton_ragged(cell, x, config, h0=h0, stats=stats, cu_seqlens=cu_seqlens,
+                              block_table=block_table, needs_grad=needs_grad)
+    if block_table is not None:
+        h0 = gather_h0(h0, block_table, x.shape[0], _state_tail(cell))
     if not needs_grad:
         return _newton_forward(cell, x, config, h0=h0, stats=stats)
     if not isinstance(cell, ParaSLSTM):
@@ -329,6 +348,58 @@ def newton_apply(
         return _NewtonFixedPoint.apply(x, h0_leaf, *params)
     finally:
         _fwd_pack.clear()
+
+
+def _state_tail(cell: nn.Module) -> tuple[int, ...]:
+    slots = getattr(cell, "state_slots", 1)
+    return (int(cell.d_h),) if slots == 1 else (int(slots), int(cell.d_h))
+
+
+def _check_ragged_args(x: Tensor, config: NewtonConfig) -> None:
+    if x.shape[0] != 1:
+        raise ValueError(f"cu_seqlens packs x with batch=1, got batch={x.shape[0]}")
+    if config.chunk_len is not None:
+        raise ValueError("chunk_len cannot be combined with cu_seqlens")
+    if config.fused_time_loop:
+        raise ValueError("fused_time_loop cannot be combined with cu_seqlens")
+
+
+def _newton_ragged(cell, x, config, *, h0, stats, cu_seqlens, block_table, needs_grad):
+    """Packed sequences (``cu_seqlens``) as a padded batch through the same solve
+    (newton/__init__.py:327-355 for the validation).  K, P and the Picard ladder
+    are resolved on the packed stream, and the residual gate is evaluated on the
+    packed result with the ragged prepend (h0[s] at each head)."""
+    cs = validate_cu_seqlens(cu_seqlens, x.shape[1])
+    n_seq = int(cs.numel()) - 1
+    if block_table is not None:
+        h0 = gather_h0(h0, block_table, n_seq, _state_tail(cell))
+    elif h0 is not None and h0.shape[0] != n_seq:
+        raise ValueError(f"h0 batch {h0.shape[0]} != n_seq {n_seq}")
+    pad = Padding(cs, x.device)
+    xp = pad.pad(x)
+    ladder = bool(config.picard_adapt) and isinstance(cell, ParaSLSTM)
+    inner = replace(config, picard_adapt=False, residual_fail=None)
+    hist = []
+    while True:
+        if needs_grad:
+            states = pad.unpad(newton_apply(cell, xp, inner, h0=h0))
+        else:
+            states = pad.unpad(_newton_forward(cell, xp, inner, h0=h0, stats=None))
+        if stats is None and config.residual_fail is None and not ladder:
+            return states
+        with torch.no_grad():
+            pred = cell.step(prepend_state_ragged(states.detach(), h0, cs), x.detach())
+            res = float((pred - states.detach()).abs().amax())
+        hist.append(res)
+        nxt = slstm_picard_next(int(inner.picard_iters or 0)) if ladder else None
+        if ladder and nxt is not None and _picard_retry_needed(res, config):
+            log.info("picard_adapt from_p=%d to_p=%d max_residual=%g",
+                     int(inner.picard_iters or 0), nxt, res)
+            inner = replace(inner, picard_iters=nxt)
+            continue
+        _fill_stats(cell, x, states, h0, replace(config, picard_iters=inner.picard_iters),
+                    iters=int(config.max_iters), stats=stats, history=hist, known=res)
+        return states
 
 
 # ---------------------------------------------------------------------------

@@ -143,9 +143,12 @@ def newton_slstm_fused(
         raise TypeError(f"newton_slstm_fused: scan_tile={scan_tile!r} is not provided (assoc only)")
     if time_loop or window_len:
         raise TypeError("newton_slstm_fused: fused_time_loop is not provided by pararnn_amd")
-    if block_table is not None:
-        raise TypeError("newton_slstm_fused: block_table (paged h0) is not provided by pararnn_amd")
     batch, time, d_h = _slstm_shapes(wx, r)
+    if block_table is not None:
+        # paged h0: the pool rows the table names (kernels/_fused_common.py:106-139)
+        from pararnn_amd.ragged import gather_h0
+
+        h0 = gather_h0(h0, block_table, batch, (4, d_h))
     code = _validate("newton_slstm_fused", wx, r, h0)
     if max_iters < 0:
         raise ValueError(f"max_iters must be >= 0, got {max_iters!r}")
@@ -257,11 +260,26 @@ def newton_gru_head_fused(
     d_h = n_heads * d_head
     if wx.dim() != 3 or wx.shape[-1] != 3 * d_h:
         raise ValueError(f"wx last dim {wx.shape[-1]} != 3 * d_h={3 * d_h}")
+    if d_head != 64:
+        raise TypeError(f"newton_gru_head_fused: pararnn_amd provides d_head=64, got {d_head}")
     if cu_seqlens is not None:
-        raise TypeError(
-            "ParaGRU(mix='head') fused Newton does not support cu_seqlens yet; "
-            "use scan_backend='eager' for ragged packs, or pad to a rectangular batch"
-        )
+        # Packed sequences run as a padded batch, each from its own h0.
+        from pararnn_amd.ragged import Padding, validate_cu_seqlens
+
+        if wx.shape[0] != 1:
+            raise ValueError(f"cu_seqlens packs wx with batch=1, got batch={wx.shape[0]}")
+        cs = validate_cu_seqlens(cu_seqlens, wx.shape[1])
+        pad = Padding(cs, wx.device)
+        if h0 is not None and h0.shape != (pad.n_seq, d_h):
+            raise ValueError(f"h0 shape {tuple(h0.shape)} != {(pad.n_seq, d_h)}")
+        dense = _gru_head_dense(pad.pad(wx), a_z, a_r, a_n, h0, max_iters, omega)
+        return pad.unpad(dense)
+    return _gru_head_dense(wx, a_z, a_r, a_n, h0, max_iters, omega)
+
+
+def _gru_head_dense(wx, a_z, a_r, a_n, h0, max_iters, omega):
+    n_heads, d_head, _ = a_z.shape
+    d_h = n_heads * d_head
     if d_head != 64:
         raise TypeError(f"newton_gru_head_fused: pararnn_amd provides d_head=64, got {d_head}")
     batch, time, _ = wx.shape

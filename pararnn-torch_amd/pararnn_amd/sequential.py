@@ -23,7 +23,7 @@ def sequential_apply(cell: nn.Module, x: Tensor, h0: Tensor | None = None, *, st
                      cu_seqlens: Tensor | None = None) -> Tensor:
     """Unroll ``cell.step`` along time; output at t is the state after step t."""
     if cu_seqlens is not None:
-        raise TypeError("packed cu_seqlens are not provided by pararnn_amd")
+        return _sequential_ragged(cell, x, h0, step=step, cu_seqlens=cu_seqlens)
     batch, time, _ = x.shape
     if time < 1:
         raise ValueError(f"sequential_apply needs time >= 1, got {time}")
@@ -46,3 +46,20 @@ def sequential_apply(cell: nn.Module, x: Tensor, h0: Tensor | None = None, *, st
         h = fn(h, x[:, t]) if wx_all is None else fn(h, x[:, t], wx=wx_all[:, t])
         outs.append(h)
     return torch.stack(outs, dim=1)
+
+
+def _sequential_ragged(cell: nn.Module, x: Tensor, h0: Tensor | None, *, step,
+                       cu_seqlens: Tensor) -> Tensor:
+    """Packed ``(1, N, d_in)``: each sequence unrolled from ``h0[s]`` (or zeros)."""
+    from pararnn_amd.ragged import validate_cu_seqlens
+
+    if x.shape[0] != 1:
+        raise ValueError(f"cu_seqlens packs x with batch=1, got batch={x.shape[0]}")
+    cs = validate_cu_seqlens(cu_seqlens, x.shape[1]).tolist()
+    if h0 is not None and h0.shape[0] != len(cs) - 1:
+        raise ValueError(f"h0 batch {h0.shape[0]} != n_seq {len(cs) - 1}")
+    parts = []
+    for s in range(len(cs) - 1):
+        hs = None if h0 is None else h0[s:s + 1]
+        parts.append(sequential_apply(cell, x[:, cs[s]:cs[s + 1]], hs, step=step))
+    return torch.cat(parts, dim=1)

@@ -230,6 +230,41 @@ def bwd_parts_case():
     )
 
 
+def ragged_case(name, cell_kind, *, d_in, d, lengths, K, P, seed, n_heads=None):
+    """Packed sequences: newton_apply and sequential_apply with cu_seqlens and
+    per-sequence h0 (eager backend)."""
+    from pararnn import ParaGRU, ParaSLSTM, newton_apply, sequential_apply
+
+    torch.manual_seed(seed)
+    if cell_kind == "slstm":
+        cell = ParaSLSTM(d_in, d, mix="diag")
+    else:
+        cell = ParaGRU(d_in, d, mix="head", n_heads=n_heads)
+    gen = torch.Generator().manual_seed(seed + 1)
+    n = sum(lengths)
+    cs = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0).tolist()), dtype=torch.long)
+    x = torch.randn(1, n, d_in, generator=gen)
+    if cell_kind == "slstm":
+        xp = torch.randn(len(lengths), 16, d_in, generator=gen)
+        with torch.no_grad():
+            h0 = sequential_apply(cell, xp)[:, -1].clone()
+    else:
+        h0 = 0.5 * torch.randn(len(lengths), d, generator=gen)
+    with torch.no_grad():
+        H = newton_apply(cell, x, _cfg(K, P), h0=h0, cu_seqlens=cs)
+        Hs = sequential_apply(cell, x, h0, cu_seqlens=cs)
+    tensors = dict(x=x, h0=h0, cu_seqlens=cs, newton=H, sequential=Hs,
+                   W=cell.W_x.weight, b=cell.W_x.bias)
+    if cell_kind == "slstm":
+        tensors["R"] = cell.R
+    else:
+        tensors.update(A_z=cell.A_z, A_r=cell.A_r, A_n=cell.A_n)
+    meta = dict(cell=cell_kind, d_in=d_in, d=d, lengths=list(lengths), K=K, P=P, seed=seed,
+                n_heads=n_heads, eps=getattr(cell, "eps", None),
+                max_recurrent_norm=cell.max_recurrent_norm)
+    _save(name, tensors, meta)
+
+
 def auto_picard_table():
     from pararnn.solvers.newton.picard import slstm_auto_picard
 
@@ -259,6 +294,10 @@ def main() -> int:
                    dtype=torch.float32, seed=7, with_h0=True)
     slstm_bwd_case("slstm_bwd_bf16", d_in=32, d=32, B=2, T=256, K=2, P=3,
                    dtype=torch.bfloat16, seed=8)
+    ragged_case("slstm_ragged_fp32", "slstm", d_in=12, d=16, lengths=(37, 100, 64), K=2, P=3,
+                seed=11)
+    ragged_case("gru_head_ragged_fp32", "gru_head", d_in=16, d=128, lengths=(20, 45, 7), K=3,
+                P=None, seed=12, n_heads=2)
     with open(os.path.join(HERE, "auto_picard.json"), "w") as f:
         json.dump(auto_picard_table(), f, indent=1)
     return 0

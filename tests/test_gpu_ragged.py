@@ -1,0 +1,137 @@
+"""GPU parity of packed ragged batches (``cu_seqlens``) and paged ``h0``
+(``block_table``) against the reference's golden vectors and the oracle.
+Every case prints its name before running."""
+
+import pytest
+import torch
+from conftest import load_golden
+
+import oracle as O
+from oracle.ragged import slstm_newton_ragged
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _cfg(K, P=None, **kw):
+    from pararnn_amd import NewtonConfig
+
+    return NewtonConfig(max_iters=K, picard_iters=P, residual_atol=None, residual_fail=None,
+                        picard_adapt=False, **kw)
+
+
+def _slstm_cell(t, m):
+    from pararnn_amd import ParaSLSTM
+
+    cell = ParaSLSTM(m["d_in"], m["d"])
+    with torch.no_grad():
+        cell.W_x.weight.copy_(t["W"])
+        cell.W_x.bias.copy_(t["b"])
+        cell.R.copy_(t["R"])
+    return cell.to(DEV)
+
+
+def test_slstm_ragged_matches_reference():
+    from pararnn_amd import newton_apply, sequential_apply
+
+    print("case slstm ragged fp32 (lengths 37, 100, 64; h0 per sequence)", flush=True)
+    t, m = load_golden("slstm_ragged_fp32")
+    cell = _slstm_cell(t, m)
+    cs = t["cu_seqlens"]
+    with torch.no_grad():
+        H = newton_apply(cell, t["x"].to(DEV), _cfg(m["K"], m["P"]), h0=t["h0"].to(DEV),
+                         cu_seqlens=cs.to(DEV)).cpu()
+        Hs = sequential_apply(cell, t["x"].to(DEV), t["h0"].to(DEV), cu_seqlens=cs).cpu()
+    p = O.SLSTMParams(t["W"], t["b"], t["R"])
+    own = slstm_newton_ragged(p, t["x"], cs, max_iters=m["K"], picard_iters=m["P"], h0=t["h0"])
+    e_ref = ((H - t["newton"]).abs() / (1 + t["newton"].abs())).max().item()
+    e_own = ((H - own).abs() / (1 + own.abs())).max().item()
+    print(f"  rel err vs reference {e_ref:.2e}, vs per-sequence oracle {e_own:.2e}", flush=True)
+    assert e_ref <= 3e-5 and e_own <= 3e-5
+    assert (H[..., 3, :] - t["newton"][..., 3, :]).abs().max().item() <= 1e-5
+    assert torch.allclose(Hs, t["sequential"], rtol=0, atol=2e-5)
+
+
+def test_gru_head_ragged_matches_reference():
+    from pararnn_amd import ParaGRU, newton_apply, verify_agreement
+
+    print("case gru head ragged fp32 (lengths 20, 45, 7)", flush=True)
+    t, m = load_golden("gru_head_ragged_fp32")
+    cell = ParaGRU(m["d_in"], m["d"], mix="head", n_heads=m["n_heads"])
+    with torch.no_grad():
+        for k in ("A_z", "A_r", "A_n"):
+            getattr(cell, k).copy_(t[k])
+        cell.W_x.weight.copy_(t["W"])
+        cell.W_x.bias.copy_(t["b"])
+    cell = cell.to(DEV)
+    cs = t["cu_seqlens"].to(DEV)
+    with torch.no_grad():
+        H = newton_apply(cell, t["x"].to(DEV), _cfg(m["K"]), h0=t["h0"].to(DEV),
+                         cu_seqlens=cs).cpu()
+    err = (H - t["newton"]).abs().max().item()
+    print(f"  max|gpu - reference| {err:.2e}", flush=True)
+    assert err <= 1e-5
+    rep = verify_agreement(cell, t["x"].to(DEV), config=_cfg(m["K"]), h0=t["h0"].to(DEV),
+                           cu_seqlens=cs)
+    print(f"  verify_agreement max_abs {rep.max_abs:.2e}", flush=True)
+    assert rep.ok
+
+
+def test_block_table_gathers_pool_rows():
+    from pararnn_amd import NewtonConfig, ParaSLSTM, newton_apply
+
+    print("case slstm block_table (pool of 6, batch 3) bf16", flush=True)
+    torch.manual_seed(0)
+    cell = ParaSLSTM(16, 64).to(DEV, torch.bfloat16)
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(3, 300, 16, generator=g).to(DEV, torch.bfloat16)
+    pool = torch.randn(6, 4, 64, generator=g)
+    pool[:, 1] = pool[:, 1].abs() + 0.5
+    pool = pool.to(DEV, torch.bfloat16)
+    bt = torch.tensor([4, 0, 4], device=DEV)
+    cfg = NewtonConfig(max_iters=2, residual_fail=None)
+    with torch.no_grad():
+        a = newton_apply(cell, x, cfg, h0=pool, block_table=bt)
+        b = newton_apply(cell, x, cfg, h0=pool[bt.long()])
+    assert torch.equal(a, b)
+    with pytest.raises(ValueError, match="outside pool"):
+        with torch.no_grad():
+            newton_apply(cell, x, cfg, h0=pool, block_table=torch.tensor([0, 1, 9], device=DEV))
+
+
+def test_ragged_backward_equals_per_sequence_sum():
+    from pararnn_amd import ParaSLSTM, newton_apply
+
+    print("case slstm ragged backward fp32 vs per-sequence backward", flush=True)
+    torch.manual_seed(2)
+    cell = ParaSLSTM(8, 32).to(DEV)
+    g = torch.Generator().manual_seed(3)
+    lengths = [50, 13, 77]
+    cs = torch.tensor([0, 50, 63, 140], device=DEV)
+    x = torch.randn(1, 140, 8, generator=g).to(DEV)
+    up = torch.randn(1, 140, 4, 32, generator=g).to(DEV)
+    h0 = torch.randn(3, 4, 32, generator=g)
+    h0[:, 1] = h0[:, 1].abs() + 0.5
+    h0 = h0.to(DEV)
+    cfg = _cfg(3, 3)
+    xa = x.clone().requires_grad_(True)
+    ha = h0.clone().requires_grad_(True)
+    (newton_apply(cell, xa, cfg, h0=ha, cu_seqlens=cs) * up).sum().backward()
+    ga = {n: p.grad.clone() for n, p in cell.named_parameters()}
+    cell.zero_grad()
+    xb = x.clone().requires_grad_(True)
+    hb = h0.clone().requires_grad_(True)
+    off = 0
+    for s, n in enumerate(lengths):
+        out = newton_apply(cell, xb[:, off:off + n], cfg, h0=hb[s:s + 1])
+        (out * up[:, off:off + n]).sum().backward()
+        off += n
+    for name, p in cell.named_parameters():
+        e = ((ga[name] - p.grad).abs().max() / p.grad.abs().max()).item()
+        print(f"  grad {name}: rel diff {e:.2e}", flush=True)
+        assert e <= 1e-5
+    for name, a, b in (("x", xa.grad, xb.grad), ("h0", ha.grad, hb.grad)):
+        e = ((a - b).abs().max() / b.abs().max()).item()
+        print(f"  grad {name}: rel diff {e:.2e}", flush=True)
+        assert e <= 1e-5

@@ -85,3 +85,29 @@ def test_backward_matches_reference(name):
         tol = 1e-5 if dtype == torch.float32 else 0
         err = (out[k].float() - ref.float()).abs().max().item()
         assert err <= tol * max(1.0, scale), (k, err, scale)
+
+
+def test_ragged_oracle_matches_reference():
+    # Per-sequence solves = the reference's packed solve with J = 0 at heads.
+    from oracle.gru_head import GRUHeadParams
+    from oracle.ragged import (
+        gru_head_newton_ragged,
+        gru_head_sequential_ragged,
+        slstm_newton_ragged,
+        slstm_sequential_ragged,
+    )
+
+    t, m = load_golden("slstm_ragged_fp32")
+    p = SLSTMParams(t["W"], t["b"], t["R"], eps=m["eps"], cap=m["max_recurrent_norm"])
+    H = slstm_newton_ragged(p, t["x"], t["cu_seqlens"], max_iters=m["K"], picard_iters=m["P"],
+                            h0=t["h0"])
+    Hs = slstm_sequential_ragged(p, t["x"], t["cu_seqlens"], t["h0"])
+    assert torch.equal(Hs, t["sequential"])
+    err = ((H - t["newton"]).abs() / (1 + t["newton"].abs())).max().item()
+    assert err <= 2e-5, err  # segmented vs per-sequence fp32 scan order
+    t, m = load_golden("gru_head_ragged_fp32")
+    p = GRUHeadParams(t["W"], t["b"], t["A_z"], t["A_r"], t["A_n"])
+    H = gru_head_newton_ragged(p, t["x"], t["cu_seqlens"], max_iters=m["K"], h0=t["h0"])
+    Hs = gru_head_sequential_ragged(p, t["x"], t["cu_seqlens"], t["h0"])
+    assert torch.allclose(Hs, t["sequential"], rtol=0, atol=1e-6)
+    assert (H - t["newton"]).abs().max().item() <= 1e-5
