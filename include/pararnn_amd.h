@@ -31,6 +31,10 @@
  *                            166-178) + slstm_recurrence_vjp (kernels/
  *                            vjp_slstm.py:209-240) + _t0_state_vjp
  *                            (solvers/newton/dispatch.py:406-410)
+ *   prnn_gru_head_backward -> solvers/newton/__init__.py:798-817 (_eq26_vjp, head
+ *                            GRU path): reverse_factor_scan_gru_head (kernels/
+ *                            newton_gru_head.py:198-258) + gru_head_t0_vjp +
+ *                            gru_head_recurrence_vjp (kernels/vjp_gru.py:656)
  *   prnn_slstm_decode     -> kernels/decode.py:420-467, 553-597 (_slstm_decode_kernel,
  *                            decode_step for ParaSLSTM mix='diag')
  *   prnn_gru_decode       -> kernels/decode.py:260-334, 472-501 (_gru_decode_kernel,
@@ -111,6 +115,25 @@ PRNN_API int prnn_slstm_backward(const void* wx, const void* r, const void* h0,
                                  const void* states, const void* grad, void* g_wx, float* g_r,
                                  float* g_h0, int B, int T, int d, float eps, int dtype,
                                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* Eq. 2.6 backward of the head GRU at `states` = H* (B, T, d) with upstream
+ * gradient `grad` = dL/dH (B, T, d) (both in `dtype`):
+ *   mu_{T-1} = grad_{T-1},  mu_t = grad_t + J_{t+1}^T mu_{t+1}  (fp32),
+ * then the VJP of every step f(H*_{t-1}, wx_t) with mu_t:
+ *   g_wx (B, T, 3d), dtype `dtype`:  dL/dwx (the W_x GEMMs stay with the caller);
+ *   g_a  (3, n_heads, 64, 64) fp32:  dL/dA_z, dL/dA_r, dL/dA_n ((in, out) layout),
+ *                                    before the caller's clamp masks;
+ *   g_h0 (B, d) fp32 or NULL:        J_0^T mu_0, written only when h0 is non-NULL.
+ * a_* are the (clamped) matrices the forward used.  g_a is deterministic
+ * (fixed-order sums).
+ */
+PRNN_API size_t prnn_gru_head_backward_workspace_size(int B, int T, int n_heads, int d_head,
+                                                      int dtype);
+PRNN_API int prnn_gru_head_backward(const void* wx, const void* a_z, const void* a_r,
+                                    const void* a_n, const void* h0, const void* states,
+                                    const void* grad, void* g_wx, float* g_a, float* g_h0, int B,
+                                    int T, int n_heads, int d_head, int dtype, void* workspace,
+                                    size_t workspace_bytes, void* stream);
 
 /* ---- T = 1 decode (serving loop) -----------------------------------------
  * One recurrent step.  state / out: (rows, 4, d) sLSTM or (rows, d) GRU;

@@ -1,4 +1,5 @@
-"""Eq. 2.6 backward of the ParaSLSTM ``mix='diag'`` Newton solve (test infrastructure only).
+"""Eq. 2.6 backward of the ParaSLSTM ``mix='diag'`` and ParaGRU ``mix='head'`` Newton
+solves (test infrastructure only).
 
 Restates, on the CPU:
 * the implicit-function backward ``_eq26_vjp`` — reference
@@ -10,6 +11,12 @@ Restates, on the CPU:
   (``slstm_recurrence_vjp_eager``: fp32 algebra, output in ``wx``'s dtype);
 * the clip mask and the ``W_x`` VJP — ``solvers/vjp.py:103-120, 288-306``;
 * the ``h0`` adjoint — ``solvers/newton/dispatch.py:406-410``.
+
+and, for ``ParaGRU(mix='head')``, the same generic path with the dense
+per-head Jacobian (reverse dense scan ``solvers/scan.py:181-203``), the head
+cell VJP ``kernels/vjp_gru.py:141-224`` with the clip masks of
+``solvers/vjp.py:214-253``, and the factorised ``J^T mu`` of
+``kernels/gru_head_factor.py:68-112``.
 
 The adjoint recursion is ``mu_{T-1} = g_{T-1}``,
 ``mu_t = g_t + J_{t+1}^T mu_{t+1}``; ``grad h0 = J_0^T mu_0``.
@@ -110,4 +117,102 @@ def slstm_backward(p: SLSTMParams, x: Tensor, states: Tensor, grad: Tensor,
     if h0 is not None:
         # J_0^T mu_0 per channel: sum over the out index
         out["h0"] = (jac[:, 0] * mu[:, 0].unsqueeze(-2)).sum(dim=-3)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# ParaGRU mix='head'
+# ---------------------------------------------------------------------------
+
+
+def reverse_scan_dense(jac: Tensor, partial: Tensor) -> Tensor:
+    """``mu`` from per-step ``J`` ``(S, T, n, n)`` ``[out, in]`` (solvers/scan.py:181-203):
+    transpose, flip time, shift by one step, forward dense scan, flip back."""
+    from oracle.scan import scan_dense
+
+    j_t = jac.transpose(-1, -2)
+    j_rev = j_t.new_zeros(j_t.shape)
+    j_rev[:, 1:] = j_t.flip(1)[:, :-1]
+    return scan_dense(j_rev.contiguous(), partial.flip(1).contiguous()).flip(1)
+
+
+def gru_head_jt_mvp(h: Tensor, z: Tensor, r: Tensor, n: Tensor, a_z: Tensor, a_r: Tensor,
+                    a_n: Tensor, mu: Tensor) -> Tensor:
+    """``J^T mu`` at head-local gates ``(..., H, d_head)`` (kernels/gru_head_factor.py:68-112):
+    ``(1-z) mu + A_z (z' (n-h) mu) + r (A_n w_n) + A_r (r' h (A_n w_n))``,
+    ``w_n = n' z mu``; ``A v`` for ``(in, out)`` matrices contracts the out index."""
+
+    def a_times(a: Tensor, v: Tensor) -> Tensor:
+        return torch.matmul(a, v.unsqueeze(-1)).squeeze(-1)
+
+    w_z = z * (1.0 - z) * ((n - h) * mu)
+    g_u = a_times(a_n, (1.0 - n.square()) * (z * mu))
+    return (1.0 - z) * mu + a_times(a_z, w_z) + r * g_u + a_times(a_r, r * (1.0 - r) * (h * g_u))
+
+
+def gru_head_cell_vjp(h_prev: Tensor, wx: Tensor, a_z: Tensor, a_r: Tensor, a_n: Tensor,
+                      mu: Tensor, work: torch.dtype = torch.float32):
+    """``(g_wx (B, T, 3d), g_az, g_ar, g_an (H, d_head, d_head))`` of
+    ``sum mu * f(h_prev, wx)`` (kernels/vjp_gru.py:141-224, eager head VJP): algebra
+    in ``work``, outputs in ``h_prev``'s dtype."""
+    dt = h_prev.dtype
+    n_heads, d_head, _ = a_z.shape
+    lead = h_prev.shape[:-1]
+    h = h_prev.to(work).reshape(*lead, n_heads, d_head)
+    m = mu.to(work).reshape(*lead, n_heads, d_head)
+    az, ar, an = a_z.to(work), a_r.to(work), a_n.to(work)
+    zx, rx, nx = (t.reshape(*lead, n_heads, d_head) for t in wx.to(work).chunk(3, dim=-1))
+
+    def mix(v: Tensor, a: Tensor) -> Tensor:
+        return torch.matmul(v.unsqueeze(-2), a).squeeze(-2)
+
+    z = torch.sigmoid(mix(h, az) + zx)
+    r = torch.sigmoid(mix(h, ar) + rx)
+    u = h * r
+    n = torch.tanh(mix(u, an) + nx)
+    d_npre = m * z * (1.0 - n.square())
+    d_zpre = m * (n - h) * z * (1.0 - z)
+    d_u = torch.matmul(d_npre.unsqueeze(-2), an.transpose(-1, -2)).squeeze(-2)
+    d_rpre = d_u * h * r * (1.0 - r)
+    g_wx = torch.cat([t.reshape(*lead, n_heads * d_head) for t in (d_zpre, d_rpre, d_npre)], -1)
+    g_az = torch.einsum("...hi,...ho->hio", h, d_zpre)
+    g_ar = torch.einsum("...hi,...ho->hio", h, d_rpre)
+    g_an = torch.einsum("...hi,...ho->hio", u, d_npre)
+    return g_wx.to(dt), g_az.to(dt), g_ar.to(dt), g_an.to(dt)
+
+
+def gru_head_backward(p, x: Tensor, states: Tensor, grad: Tensor, h0: Tensor | None = None,
+                      work: torch.dtype = torch.float32, wx: Tensor | None = None) -> dict:
+    """Gradients of ``sum(grad * H)`` for ``H = newton_apply(ParaGRU head, x)`` at
+    ``H* = states`` (solvers/newton/__init__.py:765-866 generic path,
+    solvers/vjp.py:214-253): dense ``J`` at ``H*``, reverse dense scan per head,
+    head cell VJP, clip masks on ``A_*``, ``W_x`` VJP, ``grad h0 = J_0^T mu_0``.
+    ``p`` is an ``oracle.gru_head.GRUHeadParams``.  Keys ``x, W, b, A_z, A_r, A_n``
+    (+ ``h0``) and the intermediates ``mu``, ``g_wx``."""
+    from oracle.gru_head import _prepend, gru_head_jacobian
+
+    if wx is None:
+        wx = p.wx(x)
+    bsz, time, d = states.shape
+    hh, dh = p.n_heads, p.d_head
+    h_prev = _prepend(states, h0)
+    _, jac = gru_head_jacobian(p, h_prev, wx)  # (B, T, H, dh, dh)
+    jf = jac.permute(0, 2, 1, 3, 4).reshape(bsz * hh, time, dh, dh)
+    gf = grad.reshape(bsz, time, hh, dh).permute(0, 2, 1, 3).reshape(bsz * hh, time, dh)
+    mu_f = reverse_scan_dense(jf, gf)
+    mu = mu_f.reshape(bsz, hh, time, dh).permute(0, 2, 1, 3).reshape(bsz, time, d)
+    a_z, a_r, a_n = p.mats()
+    g_wx, g_az, g_ar, g_an = gru_head_cell_vjp(h_prev, wx, a_z, a_r, a_n, mu, work)
+    if p.cap is not None:
+        g_az = g_az * (p.A_z.abs() <= p.cap).to(g_az.dtype)
+        g_ar = g_ar * (p.A_r.abs() <= p.cap).to(g_ar.dtype)
+        g_an = g_an * (p.A_n.abs() <= p.cap).to(g_an.dtype)
+    gy = g_wx.reshape(-1, g_wx.shape[-1])
+    xx = x.reshape(-1, x.shape[-1])
+    out = {"mu": mu, "g_wx": g_wx, "x": (gy @ p.W).reshape(x.shape), "W": gy.t() @ xx,
+           "b": gy.sum(0), "A_z": g_az, "A_r": g_ar, "A_n": g_an}
+    if h0 is not None:
+        j0 = jac[:, 0]  # (B, H, out, in)
+        m0 = mu[:, 0].reshape(bsz, hh, dh)
+        out["h0"] = torch.matmul(j0.transpose(-1, -2), m0.unsqueeze(-1)).squeeze(-1).reshape(bsz, d)
     return out

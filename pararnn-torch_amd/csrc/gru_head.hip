@@ -27,6 +27,8 @@
 #include "pararnn_amd.h"
 #include "prnn_host.h"
 
+#include <algorithm>
+
 namespace prnn {
 namespace gru {
 
@@ -181,11 +183,14 @@ struct PhiShared {
   float x[3][kChunk][DH];     // zx, rx, nx; later d1, d2, d3
 };
 
-template <typename TX>
+// BWD (eq. 2.6 backward at H* = hin): Phi is stored transposed (Phi^T is the
+// reverse chunk transfer) and the fp32 gates z, r, n of every step go to
+// gates_out, laid out [task][step][gate][64] with task = seq * n_chunks + c.
+template <typename TX, typename TH, bool BWD>
 __global__ __launch_bounds__(256) void gru_phi_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ a_z, const TX* __restrict__ a_r,
-    const TX* __restrict__ a_n, const TX* __restrict__ h0, const float* __restrict__ hin, int B,
-    int T, int H, int n_chunks, float* __restrict__ phi_out) {
+    const TX* __restrict__ a_n, const TX* __restrict__ h0, const TH* __restrict__ hin, int B,
+    int T, int H, int n_chunks, float* __restrict__ phi_out, float* __restrict__ gates_out) {
   __shared__ PhiShared sh;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int li = lane & 15, g = lane >> 4;
@@ -205,7 +210,7 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
     float hp = 0.f, zx = 0.f, rx = 0.f, nx = 0.f;
     if (s < len) {
       if (t > 0)
-        hp = hin[h_at(b, t - 1, T, d, head, j)];
+        hp = ld(hin + h_at(b, t - 1, T, d, head, j));
       else if (h0 != nullptr)
         hp = ld(h0 + static_cast<size_t>(b) * d + head * DH + j);
       zx = ld(wx + wx_at(b, t, T, d, 0, head, j));
@@ -290,6 +295,12 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
       rs[rt][v][2] = z * (1.f - n * n);
       rs[rt][v][3] = r;
       rs[rt][v][4] = hp * r * (1.f - r);
+      if (BWD && s < len) {
+        float* gp = gates_out + ((static_cast<size_t>(blockIdx.x) * kChunk + s) * 3) * DH + col;
+        gp[0] = z;
+        gp[DH] = r;
+        gp[2 * DH] = n;
+      }
     }
   __syncthreads();  // every read of hp / x / r above is done
 #pragma unroll
@@ -394,16 +405,26 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
     }
   }
   float* po = phi_out + static_cast<size_t>(blockIdx.x) * DH * DH;
+  if (BWD) {
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
+    for (int rt = 0; rt < 4; ++rt)
+      *reinterpret_cast<float4*>(po + col * DH + 16 * rt + 4 * g) =
+          float4{P[rt][0], P[rt][1], P[rt][2], P[rt][3]};
+  } else {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) po[(16 * rt + 4 * g + v) * DH + col] = P[rt][v];
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) po[(16 * rt + 4 * g + v) * DH + col] = P[rt][v];
+  }
 }
 
 // ---------------------------------------------------------------------------
 // Carries over chunks: carry_0 = 0, carry_{c+1} = Phi_c carry_c + e_c.
+// REV (eq. 2.6 backward, phi holding Phi^T): chunks from the last one down,
+// carry_{n-1} = 0, carry_{c-1} = Phi_c^T carry_c + e_c.
 // 256 threads: thread (i, part) sums 16 of row i's 64 products.
 // ---------------------------------------------------------------------------
+template <bool REV>
 __global__ __launch_bounds__(256) void gru_carry_kernel(const float* __restrict__ phi,
                                                        const float* __restrict__ e, int n_chunks,
                                                        float* __restrict__ carry_in) {
@@ -419,13 +440,14 @@ __global__ __launch_bounds__(256) void gru_carry_kernel(const float* __restrict_
 #pragma unroll
     for (int q = 0; q < 4; ++q) row[q] = p[q];
   };
-  load_row(0);
+  load_row(REV ? n_chunks - 1 : 0);
   int cur = 0;
-  for (int c = 0; c < n_chunks; ++c) {
+  for (int step = 0; step < n_chunks; ++step) {
+    const int c = REV ? n_chunks - 1 - step : step;
     float4 nrow[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) nrow[q] = row[q];
-    if (c + 1 < n_chunks) load_row(c + 1);
+    if (step + 1 < n_chunks) load_row(REV ? c - 1 : c + 1);
     const float* v = s_c[cur] + 16 * part;
     float acc = 0.f;
 #pragma unroll
@@ -523,6 +545,194 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
   if (LOCAL) e_out[static_cast<size_t>(task) * DH + lane] = dl;
 }
 
+
+// ===========================================================================
+// Eq. 2.6 backward at the solved trajectory H* (reference
+// solvers/newton/__init__.py:765-866 with the head Jacobian, kernels/
+// gru_head_factor.py:68-112 for J^T mu, kernels/vjp_gru.py:141-224 for the
+// cell VJP).  With nu_t = J_t^T mu_t the adjoint recursion
+//     mu_t = g_t + J_{t+1}^T mu_{t+1}   becomes   nu_t = J_t^T (g_t + nu_{t+1}),
+// nu_T = 0, mu_t = g_t + nu_{t+1} and grad h0 = nu_0.  Over chunk c
+// (steps t0..t1-1) nu_{t0} = Phi_c^T nu_{t1} + e_c, with Phi_c the forward
+// chunk transfer J_{t1-1} ... J_{t0}: the same chunk kernel, stored
+// transposed, and the carry kernel run from the last chunk down.
+//
+//  gru_phi_kernel<BWD>   Phi_c^T and the fp32 gates z, r, n of every step;
+//  gru_rev_kernel LOCAL  per chunk, nu from a zero carry -> e_c;
+//  gru_carry_kernel<REV> nu entering each chunk from the right;
+//  gru_rev_kernel        per chunk from its carry: mu_t, the pre-activation
+//                        gradients (g_wx) and, for chunk 0, grad h0 = nu_0;
+//  gru_ga_kernel         per (split of the B T rows, gate, head): the partial
+//                        sums of the outer products X^T D by fp32 MFMA
+//                        (X = h_prev for z, r; h_prev r for n);
+//  gru_ga_reduce_kernel  fixed-order sum of the splits (deterministic).
+// ===========================================================================
+
+// Row i of a head's (in, out) matrix, i.e. A[i][o] for o = 0..63.
+template <typename TX>
+__device__ __forceinline__ void load_row(const TX* A, int head, int i, float row[DH]) {
+  const TX* p = A + static_cast<size_t>(head) * DH * DH + static_cast<size_t>(i) * DH;
+#pragma unroll
+  for (int o = 0; o < DH; ++o) row[o] = ld(p + o);
+}
+
+// Reverse walk of one chunk per wave; lane i keeps row i of A_z, A_r, A_n.
+// Per step: mu = g + nu;  d_zpre = mu (n - h) z(1-z);  d_npre = mu z (1-n^2);
+// d_u = A_n d_npre;  d_rpre = d_u h r(1-r);
+// nu <- (1-z) mu + A_z d_zpre + r d_u + A_r d_rpre.
+template <typename TX, bool LOCAL>
+__global__ __launch_bounds__(256) void gru_rev_kernel(
+    const TX* __restrict__ a_z, const TX* __restrict__ a_r, const TX* __restrict__ a_n,
+    const TX* __restrict__ h0, const TX* __restrict__ states, const TX* __restrict__ grad,
+    const float* __restrict__ gates, const float* __restrict__ carry_in, TX* __restrict__ g_wx,
+    float* __restrict__ e_out, float* __restrict__ g_h0, int B, int T, int H, int n_chunks) {
+  __shared__ float s_v[4][3][DH];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int task = blockIdx.x * 4 + wave;
+  if (task >= B * H * n_chunks) return;  // whole wave exits together
+  const int d = H * DH;
+  const int seq = task / n_chunks, c = task % n_chunks;
+  const int b = seq / H, head = seq % H;
+  const int t0 = c * kChunk;
+  const int len = min(kChunk, T - t0);
+  float* s_a = s_v[wave][0];
+  float* s_b = s_v[wave][1];
+  float* s_c = s_v[wave][2];
+  float az[DH], ar[DH], an[DH];
+  load_row(a_z, head, lane, az);
+  load_row(a_r, head, lane, ar);
+  load_row(a_n, head, lane, an);
+  float nu = LOCAL ? 0.f : carry_in[static_cast<size_t>(task) * DH + lane];
+
+  struct In {
+    float hp, g, z, r, n;
+  };
+  const float* gt = gates + static_cast<size_t>(task) * kChunk * 3 * DH + lane;
+  auto load_in = [&](int s) {
+    In v{0.f, 0.f, 0.f, 0.f, 0.f};
+    if (s >= 0) {
+      const int t = t0 + s;
+      if (t > 0)
+        v.hp = ld(states + h_at(b, t - 1, T, d, head, lane));
+      else if (h0 != nullptr)
+        v.hp = ld(h0 + static_cast<size_t>(b) * d + head * DH + lane);
+      v.g = ld(grad + h_at(b, t, T, d, head, lane));
+      v.z = gt[(s * 3) * DH];
+      v.r = gt[(s * 3 + 1) * DH];
+      v.n = gt[(s * 3 + 2) * DH];
+    }
+    return v;
+  };
+  In cur = load_in(len - 1), nx1 = load_in(len - 2);
+  for (int s = len - 1; s >= 0; --s) {
+    const In nx2 = load_in(s - 2);
+    const float mu = cur.g + nu;
+    const float zp = cur.z * (1.f - cur.z);
+    const float d_zpre = mu * (cur.n - cur.hp) * zp;
+    const float d_npre = mu * cur.z * (1.f - cur.n * cur.n);
+    s_a[lane] = d_zpre;
+    s_b[lane] = d_npre;
+    __builtin_amdgcn_wave_barrier();
+    const float t_z = vec_col(s_a, az);
+    const float d_u = vec_col(s_b, an);
+    const float d_rpre = d_u * cur.hp * cur.r * (1.f - cur.r);
+    s_c[lane] = d_rpre;
+    __builtin_amdgcn_wave_barrier();
+    const float t_r = vec_col(s_c, ar);
+    nu = (1.f - cur.z) * mu + t_z + cur.r * d_u + t_r;
+    if (!LOCAL) {
+      const int t = t0 + s;
+      st(g_wx + wx_at(b, t, T, d, 0, head, lane), d_zpre);
+      st(g_wx + wx_at(b, t, T, d, 1, head, lane), d_rpre);
+      st(g_wx + wx_at(b, t, T, d, 2, head, lane), d_npre);
+    }
+    __builtin_amdgcn_wave_barrier();
+    cur = nx1;
+    nx1 = nx2;
+  }
+  if (LOCAL)
+    e_out[static_cast<size_t>(task) * DH + lane] = nu;
+  else if (c == 0 && g_h0 != nullptr)
+    g_h0[static_cast<size_t>(b) * d + head * DH + lane] = nu;
+}
+
+// Partial sums of g_A[gate][head][i][o] = sum over rows k = (b, t) of
+// X[k][i] D[k][o] over one split of the B T rows.  4 waves; wave w owns the
+// output columns 16 w .. 16 w + 15 (four 16x16 tiles down the rows i).  Rows
+// are staged through LDS 16 at a time.
+constexpr int kGaRows = 16;
+constexpr int kGaPad = 80;  // fp32 LDS row stride (the 4 lane groups land on distinct banks)
+
+template <typename TX>
+__global__ __launch_bounds__(256) void gru_ga_kernel(
+    const TX* __restrict__ h0, const TX* __restrict__ states, const float* __restrict__ gates,
+    const TX* __restrict__ g_wx, int B, int T, int H, int n_chunks, int n_split, int rows_per,
+    float* __restrict__ part) {
+  __shared__ float sx[kGaRows][kGaPad], sy[kGaRows][kGaPad];
+  const int split = blockIdx.x % n_split;
+  const int gate = (blockIdx.x / n_split) % 3;
+  const int head = blockIdx.x / (n_split * 3);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = lane & 15, g = lane >> 4;
+  const int d = H * DH;
+  const long long n_rows = static_cast<long long>(B) * T;
+  const long long r0 = static_cast<long long>(split) * rows_per;
+  const long long r1 = min(n_rows, r0 + rows_per);
+  floatx4 acc[4];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) acc[rt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (long long k0 = r0; k0 < r1; k0 += kGaRows) {
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kGaRows * DH / 256; ++q) {
+      const int idx = threadIdx.x + 256 * q;
+      const int kr = idx / DH, j = idx % DH;
+      const long long k = k0 + kr;
+      float xv = 0.f, yv = 0.f;
+      if (k < r1) {
+        const int b = static_cast<int>(k / T), t = static_cast<int>(k % T);
+        if (t > 0)
+          xv = ld(states + h_at(b, t - 1, T, d, head, j));
+        else if (h0 != nullptr)
+          xv = ld(h0 + static_cast<size_t>(b) * d + head * DH + j);
+        if (gate == 2) {
+          const size_t task = static_cast<size_t>(b * H + head) * n_chunks + t / kChunk;
+          xv *= gates[((task * kChunk + t % kChunk) * 3 + 1) * DH + j];
+        }
+        yv = ld(g_wx + wx_at(b, t, T, d, gate, head, j));
+      }
+      sx[kr][j] = xv;
+      sy[kr][j] = yv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kGaRows / 4; ++kk) {
+      const float bv = sy[4 * kk + g][16 * wave + li];
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) acc[rt] = mfma_f32(sx[4 * kk + g][16 * rt + li], bv, acc[rt]);
+    }
+  }
+  float* po = part + static_cast<size_t>(blockIdx.x) * DH * DH;
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) po[(16 * rt + 4 * g + v) * DH + 16 * wave + li] = acc[rt][v];
+}
+
+// g_a[gate][head] = sum over splits in index order.
+__global__ __launch_bounds__(256) void gru_ga_reduce_kernel(const float* __restrict__ part,
+                                                           int H, int n_split,
+                                                           float* __restrict__ g_a) {
+  const int e = blockIdx.x * 256 + threadIdx.x;  // over 3 H 64 64
+  if (e >= 3 * H * DH * DH) return;
+  const int mat = e / (DH * DH), ij = e % (DH * DH);
+  const int gate = mat / H, head = mat % H;
+  const float* p = part + (static_cast<size_t>(head * 3 + gate) * n_split) * DH * DH + ij;
+  float acc = 0.f;
+  for (int sp = 0; sp < n_split; ++sp) acc += p[static_cast<size_t>(sp) * DH * DH];
+  g_a[e] = acc;
+}
+
 // ---------------------------------------------------------------------------
 // Test hook: C = A B for 64x64 fp32 inputs through the bf16 MFMA operand
 // layout used above (one block of 256 threads).
@@ -589,14 +799,14 @@ static int run(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX*
   const int replay_blocks = (n_seq * n_chunks + 3) / 4;
   for (int k = 1; k <= K; ++k) {
     const float* hin = w.work[(k - 1) & 1];
-    gru_phi_kernel<TX><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
-        wx, az, ar, an, h0, hin, B, T, H, n_chunks, w.phi);
+    gru_phi_kernel<TX, float, false><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
+        wx, az, ar, an, h0, hin, B, T, H, n_chunks, w.phi, nullptr);
     PRNN_HIP(hipGetLastError());
     gru_replay_kernel<TX, float, true><<<dim3(replay_blocks), dim3(256), 0, stream>>>(
         wx, az, ar, an, h0, hin, nullptr, static_cast<float*>(nullptr), w.e, B, T, H, n_chunks,
         omega);
     PRNN_HIP(hipGetLastError());
-    gru_carry_kernel<<<dim3(n_seq), dim3(256), 0, stream>>>(w.phi, w.e, n_chunks, w.carry);
+    gru_carry_kernel<false><<<dim3(n_seq), dim3(256), 0, stream>>>(w.phi, w.e, n_chunks, w.carry);
     PRNN_HIP(hipGetLastError());
     if (k == K) {
       gru_replay_kernel<TX, TX, false><<<dim3(replay_blocks), dim3(256), 0, stream>>>(
@@ -607,6 +817,70 @@ static int run(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX*
     }
     PRNN_HIP(hipGetLastError());
   }
+  return PRNN_OK;
+}
+
+// ---- backward host side ----
+struct BwdWs {
+  float* phi;
+  float* e;
+  float* carry;
+  float* gates;
+  float* part;
+  int n_split, rows_per;
+};
+
+static void ga_split(int B, int T, int H, int* n_split, int* rows_per) {
+  const long long n_rows = static_cast<long long>(B) * T;
+  const long long want = (2048 + 3 * H - 1) / (3 * H);  // ~2048 blocks in flight
+  long long ns = std::min<long long>(want, (n_rows + 63) / 64);
+  if (ns < 1) ns = 1;
+  long long rp = (n_rows + ns - 1) / ns;
+  rp = (rp + kGaRows - 1) / kGaRows * kGaRows;
+  *rows_per = static_cast<int>(rp);
+  *n_split = static_cast<int>((n_rows + rp - 1) / rp);
+}
+
+static BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
+  const int n_seq = B * H, n_chunks = (T + kChunk - 1) / kChunk;
+  Carver cv(base);
+  BwdWs w;
+  const size_t tasks = static_cast<size_t>(n_seq) * n_chunks;
+  w.phi = static_cast<float*>(cv.take(sizeof(float) * tasks * DH * DH));
+  w.e = static_cast<float*>(cv.take(sizeof(float) * tasks * DH));
+  w.carry = static_cast<float*>(cv.take(sizeof(float) * tasks * DH));
+  w.gates = static_cast<float*>(cv.take(sizeof(float) * tasks * kChunk * 3 * DH));
+  ga_split(B, T, H, &w.n_split, &w.rows_per);
+  w.part = static_cast<float*>(cv.take(sizeof(float) * static_cast<size_t>(w.n_split) * 3 * H * DH * DH));
+  *total = cv.used;
+  return w;
+}
+
+template <typename TX>
+static int run_bwd(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX* h0,
+                   const TX* states, const TX* grad, TX* g_wx, float* g_a, float* g_h0, int B,
+                   int T, int H, const BwdWs& w, hipStream_t stream) {
+  const int n_seq = B * H, n_chunks = (T + kChunk - 1) / kChunk;
+  const int rev_blocks = (n_seq * n_chunks + 3) / 4;
+  gru_phi_kernel<TX, TX, true><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
+      wx, az, ar, an, h0, states, B, T, H, n_chunks, w.phi, w.gates);
+  PRNN_HIP(hipGetLastError());
+  gru_rev_kernel<TX, true><<<dim3(rev_blocks), dim3(256), 0, stream>>>(
+      az, ar, an, h0, states, grad, w.gates, nullptr, static_cast<TX*>(nullptr), w.e, nullptr, B,
+      T, H, n_chunks);
+  PRNN_HIP(hipGetLastError());
+  gru_carry_kernel<true><<<dim3(n_seq), dim3(256), 0, stream>>>(w.phi, w.e, n_chunks, w.carry);
+  PRNN_HIP(hipGetLastError());
+  gru_rev_kernel<TX, false><<<dim3(rev_blocks), dim3(256), 0, stream>>>(
+      az, ar, an, h0, states, grad, w.gates, w.carry, g_wx, nullptr, h0 != nullptr ? g_h0 : nullptr,
+      B, T, H, n_chunks);
+  PRNN_HIP(hipGetLastError());
+  gru_ga_kernel<TX><<<dim3(w.n_split * 3 * H), dim3(256), 0, stream>>>(
+      h0, states, w.gates, g_wx, B, T, H, n_chunks, w.n_split, w.rows_per, w.part);
+  PRNN_HIP(hipGetLastError());
+  gru_ga_reduce_kernel<<<dim3((3 * H * DH * DH + 255) / 256), dim3(256), 0, stream>>>(
+      w.part, H, w.n_split, g_a);
+  PRNN_HIP(hipGetLastError());
   return PRNN_OK;
 }
 
@@ -659,6 +933,44 @@ extern "C" PRNN_API int prnn_gru_head_newton(const void* wx, const void* a_z, co
                   static_cast<const bf16*>(a_r), static_cast<const bf16*>(a_n),
                   static_cast<const bf16*>(h0), static_cast<bf16*>(out), B, T, n_heads,
                   max_iters, omega, w, s);
+}
+
+extern "C" PRNN_API size_t prnn_gru_head_backward_workspace_size(int B, int T, int n_heads,
+                                                                 int d_head, int dtype) {
+  if (gru::check(B, T, n_heads, d_head, 0, dtype) != PRNN_OK) return 0;
+  size_t total = 0;
+  gru::carve_bwd(nullptr, B, T, n_heads, &total);
+  return total;
+}
+
+extern "C" PRNN_API int prnn_gru_head_backward(const void* wx, const void* a_z, const void* a_r,
+                                               const void* a_n, const void* h0,
+                                               const void* states, const void* grad, void* g_wx,
+                                               float* g_a, float* g_h0, int B, int T,
+                                               int n_heads, int d_head, int dtype,
+                                               void* workspace, size_t workspace_bytes,
+                                               void* stream) {
+  int rc = gru::check(B, T, n_heads, d_head, 0, dtype);
+  if (rc != PRNN_OK) return rc;
+  if (!wx || !a_z || !a_r || !a_n || !states || !grad || !g_wx || !g_a || !workspace)
+    return fail(PRNN_ERR_VALUE,
+                "wx, a_z, a_r, a_n, states, grad, g_wx, g_a and workspace must be non-null");
+  size_t need = 0;
+  const gru::BwdWs w = gru::carve_bwd(workspace, B, T, n_heads, &need);
+  if (workspace_bytes < need)
+    return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == PRNN_F32)
+    return gru::run_bwd(static_cast<const float*>(wx), static_cast<const float*>(a_z),
+                        static_cast<const float*>(a_r), static_cast<const float*>(a_n),
+                        static_cast<const float*>(h0), static_cast<const float*>(states),
+                        static_cast<const float*>(grad), static_cast<float*>(g_wx), g_a, g_h0, B,
+                        T, n_heads, w, s);
+  return gru::run_bwd(static_cast<const bf16*>(wx), static_cast<const bf16*>(a_z),
+                      static_cast<const bf16*>(a_r), static_cast<const bf16*>(a_n),
+                      static_cast<const bf16*>(h0), static_cast<const bf16*>(states),
+                      static_cast<const bf16*>(grad), static_cast<bf16*>(g_wx), g_a, g_h0, B, T,
+                      n_heads, w, s);
 }
 
 // Internal test hook (not part of the public header): C = A B, 64x64 fp32

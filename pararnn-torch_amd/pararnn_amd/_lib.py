@@ -19,7 +19,7 @@ PRNN_OK = 0
 PRNN_ERR_VALUE = 1
 PRNN_ERR_TYPE = 2
 PRNN_ERR_RUNTIME = 3
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # name -> (restype, argtypes); mirrors include/pararnn_amd.h
 _P = ctypes.c_void_p
@@ -42,6 +42,11 @@ SIGNATURES: dict[str, tuple] = {
     "prnn_slstm_backward": (
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _I, _P, _S, _P],
+    ),
+    "prnn_gru_head_backward_workspace_size": (_S, [_I, _I, _I, _I, _I]),
+    "prnn_gru_head_backward": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _S, _P],
     ),
     "prnn_slstm_decode": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _F, _I, _I, _P]),
     "prnn_gru_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _I, _I, _P]),

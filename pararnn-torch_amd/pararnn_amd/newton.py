@@ -335,11 +335,6 @@ def newton_apply(
         h0 = gather_h0(h0, block_table, x.shape[0], _state_tail(cell))
     if not needs_grad:
         return _newton_forward(cell, x, config, h0=h0, stats=stats)
-    if not isinstance(cell, ParaSLSTM):
-        raise NotImplementedError(
-            "pararnn_amd builds the eq. 2.6 backward for ParaSLSTM(mix='diag') only; run "
-            f"{type(cell).__name__}(mix={getattr(cell, 'mix', None)!r}) under torch.no_grad()"
-        )
     has_h0 = h0 is not None
     h0_leaf = h0 if has_h0 else x.new_zeros(())
     _fwd_pack.clear()
@@ -479,27 +474,41 @@ class _NewtonFixedPoint(torch.autograd.Function):
 
 def _eq26_vjp(cell: nn.Module, states: Tensor, x: Tensor, partial: Tensor, *,
               h0: Tensor | None = None, wx: Tensor | None = None):
-    """``(grad_x, per-parameter grads, grad_h0)`` for diag ParaSLSTM.
+    """``(grad_x, per-parameter grads, grad_h0)`` for diag ParaSLSTM and head ParaGRU.
 
     The reverse scan and the cell VJP run in one HIP op
-    (``pararnn::slstm_backward_fused``); the ``W_x`` VJP is two GEMMs and a
-    column sum as in the reference (solvers/vjp.py:109-120, 288-306).
+    (``pararnn::slstm_backward_fused`` / ``pararnn::gru_head_backward_fused``);
+    the clamp masks and the ``W_x`` VJP (two GEMMs and a column sum) follow the
+    reference (solvers/vjp.py:103-120, 214-253, 288-306).
     """
-    if not (isinstance(cell, ParaSLSTM) and cell.mix == "diag"):
-        raise NotImplementedError(f"eq. 2.6 backward for {type(cell).__name__} is not built")
     if wx is None:
         wx = cell.W_x(x)
     partial = partial.to(states.dtype)
-    g_wx, g_r, g_h0 = ops.slstm_backward_fused(
-        wx, cell.clipped_r(), h0, states, partial, eps=cell.eps
-    )
-    g_r = g_r.to(cell.R.dtype)
-    if cell.max_recurrent_norm is not None:
-        g_r = g_r * (cell.R.abs() <= cell.max_recurrent_norm).to(g_r.dtype)
+    cap = cell.max_recurrent_norm
+    if isinstance(cell, ParaSLSTM) and cell.mix == "diag":
+        g_wx, g_r, g_h0 = ops.slstm_backward_fused(
+            wx, cell.clipped_r(), h0, states, partial, eps=cell.eps
+        )
+        g_r = g_r.to(cell.R.dtype)
+        if cap is not None:
+            g_r = g_r * (cell.R.abs() <= cap).to(g_r.dtype)
+        by_name = {"R": g_r}
+    elif isinstance(cell, ParaGRU) and cell.mix == "head":
+        a_z, a_r, a_n = cell.clipped_a_head()
+        g_wx, g_a, g_h0 = ops.gru_head_backward_fused(wx, a_z, a_r, a_n, h0, states, partial)
+        by_name = {}
+        for i, name in enumerate(("A_z", "A_r", "A_n")):
+            raw = getattr(cell, name)
+            g = g_a[i].to(raw.dtype)
+            if cap is not None:
+                g = g * (raw.abs() <= cap).to(g.dtype)
+            by_name[name] = g
+    else:
+        raise NotImplementedError(f"eq. 2.6 backward for {type(cell).__name__} is not built")
     gy = g_wx.reshape(-1, g_wx.shape[-1])
     xx = x.reshape(-1, x.shape[-1])
     grad_x = (gy @ cell.W_x.weight).reshape(x.shape)
-    by_name = {"W_x.weight": gy.t() @ xx, "W_x.bias": gy.sum(0), "R": g_r}
+    by_name.update({"W_x.weight": gy.t() @ xx, "W_x.bias": gy.sum(0)})
     grads = tuple(
         by_name.get(n) if p.requires_grad else None for n, p in cell.named_parameters()
     )

@@ -310,3 +310,63 @@ def _gru_head_dense(wx, a_z, a_r, a_n, h0, max_iters, omega):
 def _(wx, a_z, a_r, a_n, h0=None, cu_seqlens=None, *, max_iters, omega):
     batch, time, _ = wx.shape
     return wx.new_empty(batch, time, int(a_z.shape[0] * a_z.shape[-1]))
+
+
+@torch.library.custom_op("pararnn::gru_head_backward_fused", mutates_args=())
+def gru_head_backward_fused(
+    wx: Tensor, a_z: Tensor, a_r: Tensor, a_n: Tensor, h0: Tensor | None, states: Tensor,
+    grad: Tensor,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """Eq. 2.6 backward of ``ParaGRU(mix='head')`` at ``H* = states`` on the GPU.
+
+    Returns ``(g_wx, g_a, g_h0)``: ``dL/dwx`` ``(B, T, 3 d_h)`` in ``wx``'s
+    dtype, ``g_a`` ``(3, H, 64, 64)`` fp32 (``dL/dA_z, dL/dA_r, dL/dA_n`` before
+    clamp masks) and ``g_h0 = J_0^T mu_0`` ``(B, d_h)`` fp32 (zeros when ``h0`` is
+    None).  The reference computes these with ``reverse_factor_scan_gru_head``,
+    ``gru_head_t0_vjp`` and ``gru_head_recurrence_vjp``
+    (solvers/newton/__init__.py:798-817, kernels/vjp_gru.py:656).
+    """
+    if a_z.dim() != 3 or a_z.shape[-1] != a_z.shape[-2]:
+        raise ValueError(f"a_z needs (H,d,d), got {tuple(a_z.shape)}")
+    n_heads, d_head, _ = a_z.shape
+    if a_r.shape != a_z.shape or a_n.shape != a_z.shape:
+        raise ValueError("a_z, a_r, a_n shape mismatch")
+    if d_head != 64:
+        raise TypeError(f"gru_head_backward_fused: pararnn_amd provides d_head=64, got {d_head}")
+    d_h = n_heads * d_head
+    if wx.dim() != 3 or wx.shape[-1] != 3 * d_h:
+        raise ValueError(f"wx last dim {wx.shape[-1]} != 3 * d_h={3 * d_h}")
+    batch, time, _ = wx.shape
+    code = _validate("gru_head_backward_fused", wx, a_z, a_r, a_n, h0, states, grad)
+    for name, t in (("states", states), ("grad", grad)):
+        if t.shape != (batch, time, d_h):
+            raise ValueError(f"{name} shape {tuple(t.shape)} != {(batch, time, d_h)}")
+    if h0 is not None and h0.shape != (batch, d_h):
+        raise ValueError(f"h0 shape {tuple(h0.shape)} != {(batch, d_h)}")
+    wx, states, grad = wx.contiguous(), states.contiguous(), grad.contiguous()
+    a_z, a_r, a_n = a_z.contiguous(), a_r.contiguous(), a_n.contiguous()
+    h0 = None if h0 is None else h0.contiguous()
+    g_wx = torch.empty_like(wx)
+    g_a = torch.empty(3, n_heads, d_head, d_head, dtype=torch.float32, device=wx.device)
+    g_h0 = torch.zeros(batch, d_h, dtype=torch.float32, device=wx.device)
+    lib = _lib.load()
+    with torch.cuda.device(wx.device):
+        nbytes = lib.prnn_gru_head_backward_workspace_size(batch, time, n_heads, d_head, code)
+        ws = _workspace(nbytes, wx.device)
+        rc = lib.prnn_gru_head_backward(
+            _ptr(wx), _ptr(a_z), _ptr(a_r), _ptr(a_n), _ptr(h0), _ptr(states), _ptr(grad),
+            _ptr(g_wx), _ptr(g_a), _ptr(g_h0), batch, time, n_heads, d_head, code, _ptr(ws),
+            ws.numel(), _stream(wx.device),
+        )
+    _lib.check(rc, "gru_head_backward_fused")
+    return g_wx, g_a, g_h0
+
+
+@gru_head_backward_fused.register_fake
+def _(wx, a_z, a_r, a_n, h0, states, grad):
+    n_heads, d_head, _ = a_z.shape
+    return (
+        torch.empty_like(wx),
+        wx.new_empty(3, n_heads, d_head, d_head, dtype=torch.float32),
+        wx.new_empty(states.shape[0], n_heads * d_head, dtype=torch.float32),
+    )

@@ -20,6 +20,8 @@ Reference call sites exercised (paths relative to the reference's src/pararnn):
   solvers/newton/__init__.py:91  _NewtonFixedPoint (eq. 2.6 backward, eager)
   solvers/scan.py:166            reverse_scan_block4
   kernels/vjp_slstm.py:173       slstm_recurrence_vjp_eager
+  kernels/gru_head_factor.py:68  gru_head_jt_mvp
+  kernels/vjp_gru.py:141         gru_head_recurrence_vjp_eager
 """
 
 from __future__ import annotations
@@ -230,6 +232,66 @@ def bwd_parts_case():
     )
 
 
+def gru_head_bwd_case(name, *, d_in, d, n_heads, B, T, K, dtype, seed, with_h0=False):
+    """Gradients of sum(g * H) through newton_apply's eq. 2.6 backward (head GRU)."""
+    from pararnn import ParaGRU, newton_apply
+
+    torch.manual_seed(seed)
+    cell = ParaGRU(d_in, d, mix="head", n_heads=n_heads).to(dtype)
+    gen = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(B, T, d_in, generator=gen).to(dtype)
+    grad = torch.randn(B, T, d, generator=gen).to(dtype)
+    tensors = {}
+    h0 = None
+    if with_h0:
+        h0 = (0.5 * torch.randn(B, d, generator=gen)).to(dtype)
+        tensors["h0"] = h0.clone()
+        h0 = h0.requires_grad_(True)
+    xg = x.clone().requires_grad_(True)
+    H = newton_apply(cell, xg, _cfg(K, None), h0=h0)
+    (H.float() * grad.float()).sum().backward()
+    tensors.update(
+        x=x, W=cell.W_x.weight.detach(), b=cell.W_x.bias.detach(), A_z=cell.A_z.detach(),
+        A_r=cell.A_r.detach(), A_n=cell.A_n.detach(), grad=grad, newton=H.detach(),
+        grad_x=xg.grad, grad_W=cell.W_x.weight.grad, grad_b=cell.W_x.bias.grad,
+        grad_A_z=cell.A_z.grad, grad_A_r=cell.A_r.grad, grad_A_n=cell.A_n.grad,
+    )
+    if with_h0:
+        tensors["grad_h0"] = h0.grad
+    meta = dict(cell="ParaGRU", mix="head", d_in=d_in, d=d, n_heads=n_heads, B=B, T=T, K=K,
+                dtype=str(dtype).replace("torch.", ""), seed=seed,
+                max_recurrent_norm=cell.max_recurrent_norm, h0=with_h0,
+                loss="sum(grad.float() * H.float())")
+    _save(name, tensors, meta)
+
+
+def gru_head_bwd_parts_case():
+    """The factorised head J^T mu and the eager head cell VJP on random operands."""
+    from pararnn.kernels.gru_head_factor import gru_head_jt_mvp
+    from pararnn.kernels.vjp_gru import gru_head_recurrence_vjp_eager
+
+    g = torch.Generator().manual_seed(2468)
+    hh, dh = 2, 64
+    a = [torch.randn(hh, dh, dh, generator=g) * 0.2 for _ in range(3)]
+    h = torch.randn(3, 5, hh, dh, generator=g) * 0.6
+    z, r, n = (torch.rand(3, 5, hh, dh, generator=g) for _ in range(3))
+    n = 2 * n - 1
+    mu = torch.randn(3, 5, hh, dh, generator=g)
+    jt = gru_head_jt_mvp(h, z, r, n, a[0], a[1], a[2], mu)
+    hp = torch.randn(2, 9, hh * dh, generator=g) * 0.6
+    wx = torch.randn(2, 9, 3 * hh * dh, generator=g)
+    vmu = torch.randn(2, 9, hh * dh, generator=g)
+    g_wx, g_az, g_ar, g_an = gru_head_recurrence_vjp_eager(hp, wx, a[0], a[1], a[2], vmu,
+                                                           n_heads=hh, d_head=dh)
+    _save(
+        "gru_head_bwd_parts",
+        dict(a_z=a[0], a_r=a[1], a_n=a[2], jt_h=h, jt_z=z, jt_r=r, jt_n=n, jt_mu=mu, jt_out=jt,
+             vjp_h=hp, vjp_wx=wx, vjp_mu=vmu, vjp_gwx=g_wx, vjp_gaz=g_az, vjp_gar=g_ar,
+             vjp_gan=g_an),
+        dict(n_heads=hh, d_head=dh),
+    )
+
+
 def ragged_case(name, cell_kind, *, d_in, d, lengths, K, P, seed, n_heads=None):
     """Packed sequences: newton_apply and sequential_apply with cu_seqlens and
     per-sequence h0 (eager backend)."""
@@ -298,6 +360,11 @@ def main() -> int:
                 seed=11)
     ragged_case("gru_head_ragged_fp32", "gru_head", d_in=16, d=128, lengths=(20, 45, 7), K=3,
                 P=None, seed=12, n_heads=2)
+    gru_head_bwd_case("gru_head_bwd_fp32", d_in=16, d=128, n_heads=2, B=2, T=80, K=3,
+                      dtype=torch.float32, seed=31, with_h0=True)
+    gru_head_bwd_case("gru_head_bwd_bf16", d_in=16, d=128, n_heads=2, B=2, T=64, K=3,
+                      dtype=torch.bfloat16, seed=32)
+    gru_head_bwd_parts_case()
     with open(os.path.join(HERE, "auto_picard.json"), "w") as f:
         json.dump(auto_picard_table(), f, indent=1)
     return 0

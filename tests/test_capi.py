@@ -22,7 +22,8 @@ def _declared():
 def test_header_declares_entry_points():
     decl = _declared()
     for name in ("prnn_slstm_init", "prnn_slstm_newton", "prnn_gru_head_newton",
-                 "prnn_slstm_backward", "prnn_last_error", "prnn_abi_version"):
+                 "prnn_slstm_backward", "prnn_gru_head_backward", "prnn_slstm_decode",
+                 "prnn_gru_decode", "prnn_last_error", "prnn_abi_version"):
         assert name in decl
 
 
@@ -63,4 +64,9 @@ def test_host_only_calls():
     assert lib.prnn_slstm_backward_workspace_size(4, 32768, 768, _lib.PRNN_BF16) > 0
     rc = lib.prnn_slstm_backward(None, None, None, None, None, None, None, None, 1, 1, 1, 1e-6,
                                  0, None, 0, None)
+    assert rc == _lib.PRNN_ERR_VALUE
+    assert lib.prnn_gru_head_backward_workspace_size(4, 32768, 8, 64, _lib.PRNN_F32) > 0
+    assert lib.prnn_gru_head_backward_workspace_size(4, 32768, 8, 32, _lib.PRNN_F32) == 0
+    rc = lib.prnn_gru_head_backward(None, None, None, None, None, None, None, None, None, None,
+                                    1, 1, 1, 64, 0, None, 0, None)
     assert rc == _lib.PRNN_ERR_VALUE

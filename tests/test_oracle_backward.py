@@ -111,3 +111,98 @@ def test_ragged_oracle_matches_reference():
     Hs = gru_head_sequential_ragged(p, t["x"], t["cu_seqlens"], t["h0"])
     assert torch.allclose(Hs, t["sequential"], rtol=0, atol=1e-6)
     assert (H - t["newton"]).abs().max().item() <= 1e-5
+
+
+# ---------------------------------------------------------------------------
+# ParaGRU mix='head'
+# ---------------------------------------------------------------------------
+
+
+def _gru_params(t, dtype=None, cap=None):
+    from oracle.gru_head import GRUHeadParams
+
+    ts = [t[k] for k in ("W", "b", "A_z", "A_r", "A_n")]
+    if dtype is not None:
+        ts = [v.to(dtype) for v in ts]
+    return GRUHeadParams(*ts, cap=cap)
+
+
+def test_gru_head_bwd_parts_match_reference():
+    from oracle.backward import gru_head_cell_vjp, gru_head_jt_mvp
+
+    t, _ = load_golden("gru_head_bwd_parts")
+    jt = gru_head_jt_mvp(t["jt_h"], t["jt_z"], t["jt_r"], t["jt_n"], t["a_z"], t["a_r"],
+                         t["a_n"], t["jt_mu"])
+    assert torch.allclose(jt, t["jt_out"], rtol=1e-5, atol=1e-5)
+    g = gru_head_cell_vjp(t["vjp_h"], t["vjp_wx"], t["a_z"], t["a_r"], t["a_n"], t["vjp_mu"])
+    for mine, key in zip(g, ("vjp_gwx", "vjp_gaz", "vjp_gar", "vjp_gan")):
+        assert torch.allclose(mine, t[key], rtol=1e-5, atol=1e-5), key
+
+
+def test_gru_head_jt_mvp_is_dense_jacobian_transpose():
+    # The factorised J^T mu equals the dense [out, in] Jacobian's transpose times mu.
+    from oracle.backward import gru_head_jt_mvp
+    from oracle.gru_head import GRUHeadParams, _acts, gru_head_jacobian
+
+    g = torch.Generator().manual_seed(5)
+    f64 = dict(dtype=torch.float64)
+    hh, dh, d = 2, 8, 16
+    p = GRUHeadParams(torch.zeros(3 * d, 1, **f64), torch.zeros(3 * d, **f64),
+                      *(torch.randn(hh, dh, dh, generator=g, **f64) * 0.4 for _ in range(3)))
+    h = torch.randn(3, d, generator=g, **f64)
+    wx = torch.randn(3, 3 * d, generator=g, **f64)
+    mu = torch.randn(3, hh, dh, generator=g, **f64)
+    _, jac = gru_head_jacobian(p, h, wx)
+    a = _acts(p, h, wx)
+    got = gru_head_jt_mvp(a["h"], a["z"], a["r"], a["n"], p.A_z, p.A_r, p.A_n, mu)
+    want = torch.matmul(jac.transpose(-1, -2), mu.unsqueeze(-1)).squeeze(-1)
+    assert torch.allclose(got, want, rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("cap", [None, 0.15])
+def test_gru_head_backward_matches_autograd_float64(cap):
+    from oracle.backward import gru_head_backward
+    from oracle.gru_head import GRUHeadParams, gru_head_sequential
+
+    g = torch.Generator().manual_seed(17)
+    f64 = dict(dtype=torch.float64)
+    B, T, hh, dh, din = 2, 30, 2, 8, 5
+    d = hh * dh
+    W = torch.randn(3 * d, din, generator=g, **f64) * 0.4
+    b = torch.randn(3 * d, generator=g, **f64) * 0.1
+    A = [torch.randn(hh, dh, dh, generator=g, **f64) * 0.3 for _ in range(3)]
+    x = torch.randn(B, T, din, generator=g, **f64)
+    h0 = torch.randn(B, d, generator=g, **f64) * 0.5
+    up = torch.randn(B, T, d, generator=g, **f64)
+    leaves = [t.clone().requires_grad_(True) for t in (x, W, b, *A, h0)]
+    H = gru_head_sequential(GRUHeadParams(*leaves[1:6], cap=cap), leaves[0], h0=leaves[6])
+    grads = torch.autograd.grad((H * up).sum(), leaves)
+    out = gru_head_backward(GRUHeadParams(W, b, *A, cap=cap), x, H.detach(), up, h0=h0,
+                            work=torch.float64)
+    for name, ref in zip(["x", "W", "b", "A_z", "A_r", "A_n", "h0"], grads):
+        assert torch.allclose(out[name], ref, rtol=1e-10, atol=1e-10), name
+    if cap is not None:
+        assert (A[0].abs() > cap).any() and (out["A_z"][A[0].abs() > cap] == 0).all()
+
+
+@pytest.mark.parametrize("name", ["gru_head_bwd_fp32", "gru_head_bwd_bf16"])
+def test_gru_head_backward_matches_reference(name):
+    from oracle.backward import gru_head_backward
+    from oracle.gru_head import gru_head_newton
+
+    t, m = load_golden(name)
+    p = _gru_params(t)
+    h0 = t.get("h0")
+    H = gru_head_newton(p, t["x"], max_iters=m["K"], h0=h0)
+    fp32 = m["dtype"] == "float32"
+    if fp32:
+        assert (H - t["newton"]).abs().max().item() <= 1e-6
+    else:
+        assert torch.equal(H, t["newton"])
+    out = gru_head_backward(p, t["x"], t["newton"], t["grad"], h0=h0)
+    for k in ["x", "W", "b", "A_z", "A_r", "A_n"] + (["h0"] if m["h0"] else []):
+        ref = t[f"grad_{k}"]
+        assert out[k].dtype == ref.dtype, k
+        scale = max(1.0, ref.float().abs().max().item())
+        err = (out[k].float() - ref.float()).abs().max().item()
+        assert err <= (1e-5 if fp32 else 2e-2) * scale, (k, err, scale)
