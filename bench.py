@@ -6,8 +6,9 @@ x ~ N(0, 0.5) seeded, default seeded init.  A step is one solve on one batch
 with ``wx = W_x(x)`` already resident in HBM: the zero-hidden pass, P Picard
 passes and K Newton iterations (8 kernel launches plus two status clears).
 The W_x GEMM and the end-to-end ``newton_apply`` (GEMM + solve) are timed
-separately and reported as extra fields, as is BASELINE config 5 (one
-training step: forward solve + eq. 2.6 backward, ``train_cfg5``).
+separately and reported as extra fields, as are BASELINE config 5 (one
+training step: forward solve + eq. 2.6 backward, ``train_cfg5``) and config 4
+(head GRU forward, backward and training step, ``head_cfg4``).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 Prints one JSON line.
@@ -124,6 +125,48 @@ def train_cfg5(torch, reps: int):
     }
 
 
+def head_cfg4(torch, reps: int):
+    """ParaGRU mix='head', H=8, d_head=64 (d=512), B=4,
+    T=32768, K=3, x ~ N(0, 1): the forward solve in fp32 and bf16, the eq. 2.6
+    backward op and one fp32 training step (forward + backward, W_x GEMMs
+    included); plus the reference's published head-GRU shape (B=1, T=4096,
+    K=3, fp32)."""
+    from pararnn_amd import NewtonConfig, ParaGRU, newton_apply, ops
+
+    out = {"workload": "ParaGRU head H=8 d_head=64 d=512 B=4 T=32768 K=3"}
+    cfg = NewtonConfig(max_iters=3, residual_atol=None, residual_fail=None)
+    for b4, t4, tag in ((4, 32768, "cfg4"), (1, 4096, "ref_shape_b1_t4096")):
+        torch.manual_seed(0)
+        cell = ParaGRU(512, 512, mix="head", n_heads=8).to("cuda:0")
+        g = torch.Generator(device="cuda:0").manual_seed(1)
+        x = torch.randn(b4, t4, 512, generator=g, device="cuda:0")
+        up = torch.randn(b4, t4, 512, generator=g, device="cuda:0")
+        res = {}
+        with torch.no_grad():
+            res["fwd_fp32_ms"] = _time(torch, lambda: newton_apply(cell, x, cfg), reps)
+            H = newton_apply(cell, x, cfg)
+            wx = cell.W_x(x)
+            a = cell.clipped_a_head()
+            res["bwd_op_fp32_ms"] = _time(
+                torch, lambda: ops.gru_head_backward_fused(wx, *a, None, H, up), reps)
+
+        def step():
+            cell.zero_grad(set_to_none=True)
+            xx = x.detach().requires_grad_(True)
+            newton_apply(cell, xx, cfg).backward(up)
+
+        res["train_step_fp32_ms"] = _time(torch, step, reps)
+        res["train_tokens_per_s"] = b4 * t4 / (res["train_step_fp32_ms"] * 1e-3)
+        if tag == "cfg4":
+            cb, xb = cell.to(torch.bfloat16), x.to(torch.bfloat16)
+            with torch.no_grad():
+                res["fwd_bf16_ms"] = _time(torch, lambda: newton_apply(cb, xb, cfg), reps)
+            res["fwd_fp32_tokens_per_s"] = b4 * t4 / (res["fwd_fp32_ms"] * 1e-3)
+            res["fwd_bf16_tokens_per_s"] = b4 * t4 / (res["fwd_bf16_ms"] * 1e-3)
+        out[tag] = res
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -132,6 +175,7 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=32768)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-train", action="store_true", help="skip the config 5 training step")
+    ap.add_argument("--no-head", action="store_true", help="skip the config 4 head-GRU lines")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (for rocprofv3 --pmc byte scaling)")
     args = ap.parse_args()
@@ -268,6 +312,8 @@ def main() -> int:
     }
     if not args.no_train:
         out["train_cfg5"] = train_cfg5(torch, max(3, args.steps // 4))
+    if not args.no_head:
+        out["head_cfg4"] = head_cfg4(torch, 3)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(torch, args.cpu_sample)
         out["gpu_over_cpu"] = out["value"] / out["cpu_baseline"]["value"]

@@ -9,9 +9,10 @@
 // into chunks of kChunk steps; per Newton iteration:
 //
 //  gru_phi_kernel     per chunk: the chunk transfer Phi = J_last ... J_first
-//                     (gates of all steps by fp32 MFMA GEMMs, then per step
-//                     three bf16 MFMA products of the factorised J with Phi
-//                     held in registers, fp32 accumulation);
+//                     (gates of all steps by fp32 MFMA GEMMs, kept in HBM for
+//                     the replays, then per step three bf16 MFMA products of
+//                     the factorised J with Phi held in registers, fp32
+//                     accumulation);
 //  gru_replay_kernel  LOCAL: per chunk, the exact fp32 recurrence from a zero
 //                     carry, giving the chunk's local solution e;
 //  gru_carry_kernel   per sequence: carry_c = Phi_c carry_{c-1} + e_c over the
@@ -183,10 +184,12 @@ struct PhiShared {
   float x[3][kChunk][DH];     // zx, rx, nx; later d1, d2, d3
 };
 
-// BWD (eq. 2.6 backward at H* = hin): Phi is stored transposed (Phi^T is the
-// reverse chunk transfer) and the fp32 gates z, r, n of every step go to
-// gates_out, laid out [task][step][gate][64] with task = seq * n_chunks + c.
-template <typename TX, typename TH, bool BWD>
+// The fp32 gates z, r, n of every step go to gates_out, laid out
+// [task][step][gate][64] with task = seq * n_chunks + c (the replays read
+// them instead of recomputing three mat-vecs per step).  TRANS (eq. 2.6
+// backward at H* = hin): Phi is stored transposed, Phi^T being the reverse
+// chunk transfer.
+template <typename TX, typename TH, bool TRANS>
 __global__ __launch_bounds__(256) void gru_phi_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ a_z, const TX* __restrict__ a_r,
     const TX* __restrict__ a_n, const TX* __restrict__ h0, const TH* __restrict__ hin, int B,
@@ -295,7 +298,7 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
       rs[rt][v][2] = z * (1.f - n * n);
       rs[rt][v][3] = r;
       rs[rt][v][4] = hp * r * (1.f - r);
-      if (BWD && s < len) {
+      if (s < len) {
         float* gp = gates_out + ((static_cast<size_t>(blockIdx.x) * kChunk + s) * 3) * DH + col;
         gp[0] = z;
         gp[DH] = r;
@@ -405,7 +408,7 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
     }
   }
   float* po = phi_out + static_cast<size_t>(blockIdx.x) * DH * DH;
-  if (BWD) {
+  if (TRANS) {
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
       *reinterpret_cast<float4*>(po + col * DH + 16 * rt + 4 * g) =
@@ -428,46 +431,66 @@ template <bool REV>
 __global__ __launch_bounds__(256) void gru_carry_kernel(const float* __restrict__ phi,
                                                        const float* __restrict__ e, int n_chunks,
                                                        float* __restrict__ carry_in) {
+  // The chain is serial over chunks, so each step's cost is the latency of
+  // its 16 KB of Phi and its e: both are fetched kDepth chunks ahead into a
+  // register ring.
+  constexpr int kDepth = 4;
   __shared__ float s_c[2][DH];
   const int seq = blockIdx.x;
   const int i = threadIdx.x >> 2, part = threadIdx.x & 3;
   if (threadIdx.x < DH) s_c[0][threadIdx.x] = 0.f;
   __syncthreads();
   const float* P = phi + static_cast<size_t>(seq) * n_chunks * DH * DH;
-  float4 row[4];
-  auto load_row = [&](int c) {
-    const float4* p = reinterpret_cast<const float4*>(P + (static_cast<size_t>(c) * DH + i) * DH + 16 * part);
+  const float* E = e + static_cast<size_t>(seq) * n_chunks * DH;
+  auto chunk_of = [&](int step) { return REV ? n_chunks - 1 - step : step; };
+  float4 ring[kDepth][4];
+  float ering[kDepth];
+  auto fetch = [&](int step, int slot) {
+    if (step < n_chunks) {
+      const int c = chunk_of(step);
+      const float4* p =
+          reinterpret_cast<const float4*>(P + (static_cast<size_t>(c) * DH + i) * DH + 16 * part);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) row[q] = p[q];
-  };
-  load_row(REV ? n_chunks - 1 : 0);
-  int cur = 0;
-  for (int step = 0; step < n_chunks; ++step) {
-    const int c = REV ? n_chunks - 1 - step : step;
-    float4 nrow[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) nrow[q] = row[q];
-    if (step + 1 < n_chunks) load_row(REV ? c - 1 : c + 1);
-    const float* v = s_c[cur] + 16 * part;
-    float acc = 0.f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      acc += nrow[q].x * v[4 * q] + nrow[q].y * v[4 * q + 1] + nrow[q].z * v[4 * q + 2] +
-             nrow[q].w * v[4 * q + 3];
-    acc += __shfl_xor(acc, 1);
-    acc += __shfl_xor(acc, 2);
-    if (part == 0) {
-      carry_in[(static_cast<size_t>(seq) * n_chunks + c) * DH + i] = s_c[cur][i];
-      s_c[cur ^ 1][i] = acc + e[(static_cast<size_t>(seq) * n_chunks + c) * DH + i];
+      for (int q = 0; q < 4; ++q) ring[slot][q] = p[q];
+      ering[slot] = E[static_cast<size_t>(c) * DH + i];
     }
-    __syncthreads();
-    cur ^= 1;
+  };
+#pragma unroll
+  for (int k = 0; k < kDepth; ++k) fetch(k, k);
+  int cur = 0;
+  for (int step0 = 0; step0 < n_chunks; step0 += kDepth) {
+#pragma unroll
+    for (int k = 0; k < kDepth; ++k) {
+      const int step = step0 + k;
+      if (step >= n_chunks) break;
+      const int c = chunk_of(step);
+      float4 row[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) row[q] = ring[k][q];
+      const float ev = ering[k];
+      fetch(step + kDepth, k);
+      const float* v = s_c[cur] + 16 * part;
+      float acc = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        acc += row[q].x * v[4 * q] + row[q].y * v[4 * q + 1] + row[q].z * v[4 * q + 2] +
+               row[q].w * v[4 * q + 3];
+      acc += __shfl_xor(acc, 1);
+      acc += __shfl_xor(acc, 2);
+      if (part == 0) {
+        carry_in[(static_cast<size_t>(seq) * n_chunks + c) * DH + i] = s_c[cur][i];
+        s_c[cur ^ 1][i] = acc + ev;
+      }
+      __syncthreads();
+      cur ^= 1;
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
 // Replay: the exact fp32 recurrence of one chunk from its carry.  Each wave
-// handles one chunk; lane j keeps column j of A_z, A_r, A_n in registers.
+// handles one chunk; lane j keeps column j of A_z, A_r, A_n in registers and
+// reads the step's gates (written by the chunk kernel from the same guess).
 // LOCAL: from a zero carry, writing only the chunk's final delta (the local
 // solution e of the carry scan); otherwise from the chunk's carry, writing
 // H + omega delta.  The inputs of step s + 2 are loaded while step s
@@ -475,11 +498,11 @@ __global__ __launch_bounds__(256) void gru_carry_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 template <typename TX, typename TOUT, bool LOCAL>
 __global__ __launch_bounds__(256) void gru_replay_kernel(
-    const TX* __restrict__ wx, const TX* __restrict__ a_z, const TX* __restrict__ a_r,
-    const TX* __restrict__ a_n, const TX* __restrict__ h0, const float* __restrict__ hin,
+    const TX* __restrict__ a_z, const TX* __restrict__ a_r, const TX* __restrict__ a_n,
+    const TX* __restrict__ h0, const float* __restrict__ hin, const float* __restrict__ gates,
     const float* __restrict__ carry_in, TOUT* __restrict__ hout, float* __restrict__ e_out,
     int B, int T, int H, int n_chunks, float omega) {
-  __shared__ float s_v[4][4][DH];
+  __shared__ float s_v[4][2][DH];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int task = blockIdx.x * 4 + wave;
   const int n_seq = B * H;
@@ -489,10 +512,8 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
   const int b = seq / H, head = seq % H;
   const int t0 = c * kChunk;
   const int len = min(kChunk, T - t0);
-  float* s_h = s_v[wave][0];
-  float* s_u = s_v[wave][1];
-  float* s_d = s_v[wave][2];
-  float* s_w = s_v[wave][3];
+  float* s_d = s_v[wave][0];
+  float* s_w = s_v[wave][1];
   float az[DH], ar[DH], an[DH];
   load_col(a_z, head, lane, az);
   load_col(a_r, head, lane, ar);
@@ -500,8 +521,9 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
   float dl = LOCAL ? 0.f : carry_in[static_cast<size_t>(task) * DH + lane];
 
   struct In {
-    float hp, zx, rx, nx, ht;
+    float hp, z, r, n, ht;
   };
+  const float* gt = gates + static_cast<size_t>(task) * kChunk * 3 * DH + lane;
   auto load_in = [&](int s) {
     In v{0.f, 0.f, 0.f, 0.f, 0.f};
     if (s < len) {
@@ -510,9 +532,9 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
         v.hp = hin[h_at(b, t - 1, T, d, head, lane)];
       else if (h0 != nullptr)
         v.hp = ld(h0 + static_cast<size_t>(b) * d + head * DH + lane);
-      v.zx = ld(wx + wx_at(b, t, T, d, 0, head, lane));
-      v.rx = ld(wx + wx_at(b, t, T, d, 1, head, lane));
-      v.nx = ld(wx + wx_at(b, t, T, d, 2, head, lane));
+      v.z = gt[(s * 3) * DH];
+      v.r = gt[(s * 3 + 1) * DH];
+      v.n = gt[(s * 3 + 2) * DH];
       v.ht = hin[h_at(b, t, T, d, head, lane)];
     }
     return v;
@@ -521,22 +543,20 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
   for (int s = 0; s < len; ++s) {
     const In nx2 = load_in(s + 2);
     const int t = t0 + s;
-    const bool zero_h = t == 0 && h0 == nullptr;
     const float hp = cur.hp;
-    s_h[lane] = hp;
     s_d[lane] = dl;
     __builtin_amdgcn_wave_barrier();
-    const Gates g = gates_step(s_h, s_u, hp, cur.zx, cur.rx, cur.nx, az, ar, an, zero_h);
     // J delta = (1-z) delta + d2 (delta @ A_z) + d3 ((r delta + d5 (delta @ A_r)) @ A_n)
     const float yz = vec_col(s_d, az);
     const float yr = vec_col(s_d, ar);
-    const float d5 = hp * g.r * (1.f - g.r);
-    s_w[lane] = g.r * dl + d5 * yr;
+    const float d5 = hp * cur.r * (1.f - cur.r);
+    s_w[lane] = cur.r * dl + d5 * yr;
     __builtin_amdgcn_wave_barrier();
     const float yn = vec_col(s_w, an);
-    const float d2 = (g.n - hp) * g.z * (1.f - g.z);
-    const float d3 = g.z * (1.f - g.n * g.n);
-    dl = (1.f - g.z) * dl + d2 * yz + d3 * yn + (g.h_new - cur.ht);
+    const float d2 = (cur.n - hp) * cur.z * (1.f - cur.z);
+    const float d3 = cur.z * (1.f - cur.n * cur.n);
+    const float h_new = lerp_t(hp, cur.n, cur.z);
+    dl = (1.f - cur.z) * dl + d2 * yz + d3 * yn + (h_new - cur.ht);
     if (!LOCAL) st(hout + h_at(b, t, T, d, head, lane), cur.ht + omega * dl);
     __builtin_amdgcn_wave_barrier();
     cur = nx1;
@@ -544,7 +564,6 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
   }
   if (LOCAL) e_out[static_cast<size_t>(task) * DH + lane] = dl;
 }
-
 
 // ===========================================================================
 // Eq. 2.6 backward at the solved trajectory H* (reference
@@ -765,6 +784,7 @@ struct Ws {
   float* phi;
   float* e;
   float* carry;
+  float* gates;
   float* work[2];
 };
 
@@ -775,6 +795,8 @@ static Ws carve(void* base, int B, int T, int H, int K, size_t* total) {
   w.phi = static_cast<float*>(cv.take(sizeof(float) * static_cast<size_t>(n_seq) * n_chunks * DH * DH));
   w.e = static_cast<float*>(cv.take(sizeof(float) * static_cast<size_t>(n_seq) * n_chunks * DH));
   w.carry = static_cast<float*>(cv.take(sizeof(float) * static_cast<size_t>(n_seq) * n_chunks * DH));
+  w.gates = static_cast<float*>(
+      cv.take(sizeof(float) * static_cast<size_t>(n_seq) * n_chunks * kChunk * 3 * DH));
   const size_t hb = sizeof(float) * static_cast<size_t>(B) * T * H * DH;
   w.work[0] = K >= 1 ? static_cast<float*>(cv.take(hb)) : nullptr;
   w.work[1] = K >= 2 ? static_cast<float*>(cv.take(hb)) : nullptr;
@@ -800,20 +822,21 @@ static int run(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX*
   for (int k = 1; k <= K; ++k) {
     const float* hin = w.work[(k - 1) & 1];
     gru_phi_kernel<TX, float, false><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
-        wx, az, ar, an, h0, hin, B, T, H, n_chunks, w.phi, nullptr);
+        wx, az, ar, an, h0, hin, B, T, H, n_chunks, w.phi, w.gates);
     PRNN_HIP(hipGetLastError());
     gru_replay_kernel<TX, float, true><<<dim3(replay_blocks), dim3(256), 0, stream>>>(
-        wx, az, ar, an, h0, hin, nullptr, static_cast<float*>(nullptr), w.e, B, T, H, n_chunks,
-        omega);
+        az, ar, an, h0, hin, w.gates, nullptr, static_cast<float*>(nullptr), w.e, B, T, H,
+        n_chunks, omega);
     PRNN_HIP(hipGetLastError());
     gru_carry_kernel<false><<<dim3(n_seq), dim3(256), 0, stream>>>(w.phi, w.e, n_chunks, w.carry);
     PRNN_HIP(hipGetLastError());
     if (k == K) {
       gru_replay_kernel<TX, TX, false><<<dim3(replay_blocks), dim3(256), 0, stream>>>(
-          wx, az, ar, an, h0, hin, w.carry, out, nullptr, B, T, H, n_chunks, omega);
+          az, ar, an, h0, hin, w.gates, w.carry, out, nullptr, B, T, H, n_chunks, omega);
     } else {
       gru_replay_kernel<TX, float, false><<<dim3(replay_blocks), dim3(256), 0, stream>>>(
-          wx, az, ar, an, h0, hin, w.carry, w.work[k & 1], nullptr, B, T, H, n_chunks, omega);
+          az, ar, an, h0, hin, w.gates, w.carry, w.work[k & 1], nullptr, B, T, H, n_chunks,
+          omega);
     }
     PRNN_HIP(hipGetLastError());
   }
