@@ -176,6 +176,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-train", action="store_true", help="skip the config 5 training step")
     ap.add_argument("--no-head", action="store_true", help="skip the config 4 head-GRU lines")
+    ap.add_argument("--head-only", action="store_true",
+                    help="only the config 4 head-GRU lines (for profiling that path)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (for rocprofv3 --pmc byte scaling)")
     args = ap.parse_args()
@@ -193,6 +195,10 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2}))
+        return 0
+
+    if args.head_only:
+        print(json.dumps({"head_cfg4": head_cfg4(torch, 3)}), flush=True)
         return 0
 
     from pararnn_amd import NewtonConfig, ParaSLSTM, fused_newton, newton_apply, slstm_init_fused
