@@ -241,7 +241,7 @@ def main() -> int:
                                                         eps=cell.eps), reps)
         ms_n2 = _time(torch, lambda: newton_slstm_fused(wx, r, None, init, max_iters=2, omega=1.0,
                                                         eps=cell.eps), reps)
-        ms_newton = ms_n2 / 2  # one Newton-iteration launch (average of the two)
+        ms_newton = ms_n2  # the K = 2 Newton iterations: one fused launch
         ms_gemm = _time(torch, lambda: cell.W_x(x), reps)
         cfg = NewtonConfig(max_iters=K, picard_iters=P, residual_atol=None, residual_fail=None,
                            picard_adapt=False)
@@ -255,16 +255,17 @@ def main() -> int:
     # 4 s_x + 32 (read wx and the fp32 state, write the state).
     step_bytes = elems * ((4 * s_x + 16) + P * (4 * s_x + 20) + K * (4 * s_x + 32))
     newton_bytes = elems * (4 * s_x + 32)
-    # Compulsory I/O of this build's kernels, whose formats are narrower:
-    # a Newton iteration reads wx (8 B) and a bf16 guess (8 B) or fp32 work
-    # (16 B) and writes fp32 work (16 B) or the bf16 result (8 B): 32 B either
-    # way; the fused warm start reads wx (8 B) and writes the bf16 state (8 B)
-    # once for all P + 1 frozen-gate stages.
-    newton_io = elems * 32
+    # Compulsory I/O of this build's kernels, whose formats are narrower: the
+    # fused Newton launch reads wx (8 B) and the bf16 guess (8 B) and writes
+    # the bf16 result (8 B) once for all K iterations (the fp32 iterate stays
+    # in registers); the fused warm start reads wx (8 B) and writes the bf16
+    # state (8 B) once for all P + 1 frozen-gate stages.
+    newton_io = elems * 24
+    newton_bytes = K * newton_bytes  # algorithmic bytes of the K iterations in the launch
     init_io = elems * 16
     init_alg = elems * ((4 * s_x + 16) + P * (4 * s_x + 20))
     ach_newton = newton_bytes / (ms_newton * 1e-3) / 1e9
-    newton_share = K * ms_newton / ms
+    newton_share = ms_newton / ms
     init_share = ms_initP / ms
     out = {
         "metric": "Newton+scan fwd tokens/sec + % HBM roofline, ParaSLSTM diag d=1024 T=131072",
@@ -285,7 +286,7 @@ def main() -> int:
                    "storage": "bf16 wx/states, fp32 Newton work",
                    "parallelism": "single GPU"},
         "roofline": {
-            "kernel": f"slstm_newton_kernel (one Newton iteration; {K} launches, "
+            "kernel": f"slstm_newton_fused_kernel ({K} Newton iterations in one launch, "
                       f"{100 * newton_share:.0f}% of the step)",
             "bound": "hbm",
             "achieved": ach_newton,

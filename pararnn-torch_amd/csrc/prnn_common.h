@@ -108,9 +108,17 @@ using rsrc_t = __amdgpu_buffer_rsrc_t;
 constexpr uint32_t kOOB = 0x80000000u;
 
 // Raw (stride 0) resource over `bytes` bytes from `base` (CDNA dword 3).
+// Callers pass wave-uniform values; readfirstlane keeps the descriptor in
+// SGPRs even where the compiler has copied a uniform operand into a VGPR
+// (otherwise every buffer access through it becomes a readfirstlane loop).
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
-                                           static_cast<int>(bytes), 0x00020000);
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+  void* p = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, static_cast<short>(0),
+                                           static_cast<int>(__builtin_amdgcn_readfirstlane(bytes)),
+                                           0x00020000);
 }
 
 // Raw storage bits of one element (bf16: zero-extended 16-bit word).

@@ -716,6 +716,276 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// (2b) all K Newton iterations in one launch
+// ---------------------------------------------------------------------------
+//
+// Each tile runs iterations k = 1 .. K over its own steps with wx and the fp32
+// iterate H^(k-1) held in registers; only the last iteration writes the state.
+// Iteration k of a tile needs
+//  * H^(k-1) at the step before the tile: the predecessor tile publishes the
+//    4 slots of its last step after each iteration (tagged words,
+//    iteration-indexed); waves of one tile hand it over through LDS;
+//  * the iteration-k carry: a decoupled look-back on iteration-indexed words.
+// Both only ever wait on tiles with earlier tickets, so every wave reaches the
+// end.  The arithmetic is that of K separate launches exchanging the fp32
+// iterate through memory.
+template <typename TX, int L, int W>
+__global__ __launch_bounds__(64 * W) void slstm_newton_fused_kernel(
+    const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
+    const TX* __restrict__ guess, TX* __restrict__ out, int B, int T, int d, int n_cb,
+    int n_tiles, int K, float omega, float eps, int* __restrict__ counter,
+    unsigned long long* __restrict__ agg, unsigned long long* __restrict__ incl,
+    unsigned long long* __restrict__ hlast) {
+  constexpr int KP = 1;
+  using XS = RowStash<TX>;
+  __shared__ float s_agg[W][20][kCB];
+  __shared__ float s_carry[W][4][kCB];
+  __shared__ float s_hl[W][4][kCB];
+  __shared__ LookbackShared<NewtonMonoid, W * KP> s_lb;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tile = take_ticket(counter);
+  const TileId id = decode_tile(tile, B, n_cb);
+  const int c0 = id.cb * kCB;
+  const bool live = c0 + lane < d;
+  const int t0 = id.chunk * (W * L) + wave * L;
+  const int n_steps = max(0, min(L, T - t0));
+  const size_t row4 = static_cast<size_t>(4) * d;
+  const size_t first = static_cast<size_t>(id.b) * T + t0;
+  const uint32_t vx = live ? lane * sizeof(TX) : kOOB;
+  const size_t span = n_steps > 0 ? (n_steps - 1) * row4 + 3 * d + (d - c0) : 0;
+  const size_t stage_incl = static_cast<size_t>(n_tiles) * 4 * kCB;
+  const size_t stage_agg = static_cast<size_t>(n_tiles) * 20 * kCB;
+  const size_t stage_h = static_cast<size_t>(n_tiles) * 4 * kCB;
+
+  float r[4] = {0.f, 0.f, 0.f, 0.f};
+  float h0v[4] = {0.f, 0.f, 0.f, 0.f};   // linearisation point at t = 0, every iteration
+  float prevg[4] = {0.f, 0.f, 0.f, 0.f};  // the guess at t0 - 1 (iteration 1)
+  if (live) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) r[g] = ld(rmix + g * d + c0 + lane);
+    if (h0 != nullptr) {
+      const TX* p = h0 + static_cast<size_t>(id.b) * row4 + c0 + lane;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) h0v[k] = ld(p + k * d);
+    }
+    if (t0 > 0 && n_steps > 0) {
+      const TX* p = guess + (first - 1) * row4 + c0 + lane;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) prevg[k] = ld(p + k * d);
+    }
+  }
+  if (t0 == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) prevg[k] = h0v[k];
+  }
+
+  uint32_t xs[L][XS::N];
+  float hf[L][4];
+  {
+    const rsrc_t rx = make_rsrc(wx + first * row4 + c0, span * sizeof(TX));
+    const rsrc_t rg = make_rsrc(guess + first * row4 + c0, span * sizeof(TX));
+    auto load = [&](int s) {
+      uint32_t gw[XS::N];
+      XS::load(rx, vx, s * row4 * sizeof(TX), d * sizeof(TX), xs[s]);
+      XS::load(rg, vx, s * row4 * sizeof(TX), d * sizeof(TX), gw);
+      XS::get(gw, hf[s]);
+    };
+    if (n_steps == L) {
+#pragma unroll
+      for (int s = 0; s < L; ++s) load(s);
+    } else {
+#pragma unroll
+      for (int s = 0; s < L; ++s)
+        if (s < n_steps) load(s);
+    }
+  }
+  const rsrc_t ro = make_rsrc(out + first * row4 + c0, span * sizeof(TX));
+
+  for (int k = 0; k < K; ++k) {
+    const int tag = k + 1;
+    // Keep wx packed across iterations (otherwise the unpacking is hoisted out
+    // of the loop and holds 4 floats per step).
+#pragma unroll
+    for (int s = 0; s < L; ++s)
+#pragma unroll
+      for (int q = 0; q < XS::N; ++q) asm volatile("" : "+v"(xs[s][q]));
+    // Linearisation point H^(k-1)_{t0-1}.
+    float prev0[4];
+    if (k == 0 || t0 == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) prev0[j] = prevg[j];
+      if (k > 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) prev0[j] = h0v[j];
+      }
+    } else if (wave > 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) prev0[j] = s_hl[wave - 1][j][lane];
+    } else {
+      const unsigned long long* hw =
+          hlast + (k - 1) * stage_h + (static_cast<size_t>(tile) - B * n_cb) * 4 * kCB + lane;
+      int spins = 0;
+      while (true) {
+        bool ok = true;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ok = ld_tagged(hw + j * kCB, tag - 1, prev0[j]) && ok;
+        if (__ballot(!ok) == 0ull) break;
+        if (++spins > 8)
+          __builtin_amdgcn_s_sleep(8);
+        else
+          __builtin_amdgcn_s_sleep(1);
+      }
+    }
+
+    // Pass 1: lane segment aggregate (A, b) of the affine maps x -> J x + F.
+    Aff a;
+    aff_identity(a);
+    {
+      float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
+      auto step = [&](int s) {
+        float x[4];
+        XS::get(xs[s], x);
+        const CellJ J = cell_jac(prev, x, r, eps);
+        jmv(J, a.b);
+        a.b[0] += J.pc - hf[s][0];
+        a.b[1] += J.pn - hf[s][1];
+        a.b[2] += J.pm - hf[s][2];
+        a.b[3] += J.ph - hf[s][3];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float col[4] = {a.A[0][j], a.A[1][j], a.A[2][j], a.A[3][j]};
+          jmv(J, col);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) a.A[i][j] = col[i];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) prev[j] = hf[s][j];
+      };
+      if (n_steps == L) {
+#pragma unroll
+        for (int s = 0; s < L; ++s) step(s);
+      } else {
+#pragma unroll
+        for (int s = 0; s < L; ++s)
+          if (s < n_steps) step(s);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s_agg[wave][16 + i][lane] = a.b[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s_agg[wave][4 * i + j][lane] = a.A[i][j];
+    }
+    // Hold wx packed through the look-back: pass 2 unpacks it again.
+#pragma unroll
+    for (int s = 0; s < L; ++s)
+#pragma unroll
+      for (int q = 0; q < XS::N; ++q) asm volatile("" : "+v"(xs[s][q]));
+    __syncthreads();
+
+    unsigned long long* incl_k = incl + k * stage_incl;
+    unsigned long long* agg_k = agg + k * stage_agg;
+    float carry[4] = {0.f, 0.f, 0.f, 0.f};
+    if (wave == 0 && id.chunk > 0) {
+      Aff tile_agg;
+      aff_identity(tile_agg);
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        Aff sw;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sw.b[i] = s_agg[w][16 + i][lane];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sw.A[i][j] = s_agg[w][4 * i + j][lane];
+        }
+        tile_agg = w == 0 ? sw : aff_compose(tile_agg, sw);
+      }
+      unsigned long long* ap = agg_k + (static_cast<size_t>(tile) * 20) * kCB + lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        st_tagged(ap + (16 + i) * kCB, tile_agg.b[i], tag);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) st_tagged(ap + (4 * i + j) * kCB, tile_agg.A[i][j], tag);
+      }
+    }
+    if (id.chunk > 0)
+      windowed_lookback<NewtonMonoid, W, KP>(id, B, n_cb, tag, incl_k, agg_k, lane, wave, s_lb,
+                                             carry);
+    if (wave == 0) {
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s_carry[w][j][lane] = carry[j];
+        Aff sw;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sw.b[i] = s_agg[w][16 + i][lane];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sw.A[i][j] = s_agg[w][4 * i + j][lane];
+        }
+        aff_apply(sw, carry);
+      }
+      unsigned long long* ip = incl_k + (static_cast<size_t>(tile) * 4) * kCB + lane;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) st_tagged(ip + j * kCB, carry[j], tag);
+    }
+    __syncthreads();
+
+    // Pass 2: delta_t = J_t delta_{t-1} + F_t from the true carry; the new
+    // iterate H + omega delta stays in registers (written by the last one).
+    const bool last_iter = k == K - 1;
+    float dl[4], hl[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dl[j] = s_carry[wave][j][lane];
+    {
+      float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
+      auto replay = [&](int s) {
+        float x[4], hv[4];
+        XS::get(xs[s], x);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hv[j] = hf[s][j];
+        float pv[4], jv[4];
+        cell_jvp(prev, x, r, eps, dl, pv, jv);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          dl[j] = jv[j] + (pv[j] - hv[j]);
+          hl[j] = hv[j] + omega * dl[j];
+          prev[j] = hv[j];
+        }
+        if (last_iter) {
+          const uint32_t so = s * row4 * sizeof(TX);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) stb<TX>(ro, vx, so + j * d * sizeof(TX), hl[j]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) hf[s][j] = hl[j];
+        }
+      };
+      if (n_steps == L) {
+#pragma unroll
+        for (int s = 0; s < L; ++s) replay(s);
+      } else {
+#pragma unroll
+        for (int s = 0; s < L; ++s)
+          if (s < n_steps) replay(s);
+      }
+    }
+    if (!last_iter) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s_hl[wave][j][lane] = hl[j];
+      if (wave == W - 1) {
+        unsigned long long* hw = hlast + k * stage_h + static_cast<size_t>(tile) * 4 * kCB + lane;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) st_tagged(hw + j * kCB, hl[j], tag);
+      }
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace slstm
 }  // namespace prnn
 
@@ -827,19 +1097,67 @@ static InitWs carve_init(void* base, int B, int T, int d, int P, int dtype, size
   return w;
 }
 
+// K >= 2 Newton iterations in one launch (the fp32 iterate stays in
+// registers); a single iteration keeps its own launch, which holds the guess
+// packed and runs at higher occupancy.  PRNN_SLSTM_NEWTON_FUSED=0 selects one
+// launch per iteration throughout.
+static bool newton_fused(int K) {
+  static const bool on = [] {
+    const char* e = getenv("PRNN_SLSTM_NEWTON_FUSED");
+    return !(e && atoi(e) == 0);
+  }();
+  return on && K >= 2;
+}
+
+// Shapes of the fused launch: wx (2 registers per step in bf16, 4 in fp32)
+// and the fp32 iterate (4) stay in registers.
+// PRNN_SLSTM_NEWTON_FUSED_TILES="<L>x<W>" for tuning (bf16).
+static const Shape kNewtonFusedShapes[] = {{20, 4}, {16, 4}, {24, 4}, {16, 8}};
+constexpr Shape kNewtonFusedF32{16, 4};
+
+static Shape newton_fused_shape(int dtype) {
+  static const Shape s = [] {
+    Shape r{20, 4};
+    if (const char* e = getenv("PRNN_SLSTM_NEWTON_FUSED_TILES")) {
+      int l, w;
+      if (sscanf(e, "%dx%d", &l, &w) == 2)
+        for (const Shape& c : kNewtonFusedShapes)
+          if (c.L == l && c.W == w) r = c;
+    }
+    return r;
+  }();
+  return dtype == PRNN_BF16 ? s : kNewtonFusedF32;
+}
+
 struct NewtonWs {
   Lookback lb;
   float* work[2];
+  unsigned long long* hlast;  // fused launch: [K-1][tile][4][64] tagged last-step state
+  bool fused;
 };
 
 static NewtonWs carve_newton(void* base, int B, int T, int d, int K, int dtype, size_t* total) {
+  Carver cv(base);
+  NewtonWs w;
+  w.fused = newton_fused(K);
+  w.work[0] = w.work[1] = nullptr;
+  w.hlast = nullptr;
+  if (w.fused) {
+    // Iteration-indexed look-back words (a tile may run iterations ahead of
+    // the tiles that still read its earlier ones), cleared with the counters.
+    const Geo g = geometry(B, T, d, newton_fused_shape(dtype));
+    w.lb = carve_lookback(cv, g, 4 * K, 20 * K);
+    w.hlast = static_cast<unsigned long long*>(
+        cv.take(sizeof(unsigned long long) * static_cast<size_t>(K - 1) * 4 * kCB * g.n_tiles));
+    w.lb.clear_words = (cv.used - (reinterpret_cast<char*>(w.lb.counters) - cv.base)) / sizeof(int);
+    *total = cv.used;
+    return w;
+  }
   // Launches of one call share the look-back arrays: size them for the
   // larger tile count of the two shapes.
   const Geo g1 = geometry(B, T, d, newton_shape(dtype, false));
   const Geo g2 = geometry(B, T, d, newton_shape(dtype, true));
   const Geo& g = g1.n_tiles >= g2.n_tiles ? g1 : g2;
-  Carver cv(base);
-  NewtonWs w;
   w.lb = carve_lookback(cv, g, 4, 20);
   const size_t wb = static_cast<size_t>(B) * T * 4 * d * sizeof(float);
   w.work[0] = K >= 2 ? static_cast<float*>(cv.take(wb)) : nullptr;
@@ -966,6 +1284,26 @@ static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, 
   }
   int rc = clear_words(w.lb.counters, w.lb.clear_words, stream);
   if (rc != PRNN_OK) return rc;
+  if (w.fused) {
+    const Shape sh = newton_fused_shape(sizeof(TX) == 2 ? PRNN_BF16 : PRNN_F32);
+    const Geo g = geometry(B, T, d, sh);
+#define PRNN_SHAPE(LL, WW)                                                                      \
+  if (sh.L == LL && sh.W == WW)                                                                 \
+    slstm_newton_fused_kernel<TX, LL, WW><<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>(       \
+        wx, r, h0, guess, out, B, T, d, g.n_cb, g.n_tiles, K, omega, eps, w.lb.counters + 1,    \
+        w.lb.agg, w.lb.incl, w.hlast);
+    if constexpr (sizeof(TX) == 4) {
+      PRNN_SHAPE(16, 4)
+    } else {
+      PRNN_SHAPE(20, 4)
+      PRNN_SHAPE(16, 4)
+      PRNN_SHAPE(24, 4)
+      PRNN_SHAPE(16, 8)
+    }
+#undef PRNN_SHAPE
+    PRNN_HIP(hipGetLastError());
+    return PRNN_OK;
+  }
   for (int k = 1; k <= K; ++k) {
     const bool first = k == 1, last = k == K;
     const float* win = first ? nullptr : w.work[(k - 2) & 1];
