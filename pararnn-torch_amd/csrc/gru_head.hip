@@ -39,6 +39,7 @@ constexpr int kPad = 72;    // bf16 row stride of the LDS operand tiles (16-byte
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // D(16x16) += A(16x32) B(32x16).  Lane l holds A[l%16][8(l/16)+q],
 // B[8(l/16)+q][l%16] (q = 0..7) and D[4(l/16)+v][l%16] (v = 0..3).
@@ -178,11 +179,18 @@ __device__ __forceinline__ floatx4 mfma_f32(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-struct PhiShared {
-  float hp[kChunk][kRowPad];  // h_prev per step; later d5
+struct PhiInputs {
+  float hp[kChunk][kRowPad];  // h_prev per step
   float r[kChunk][kRowPad];   // r per step
-  float x[3][kChunk][DH];     // zx, rx, nx; later d1, d2, d3
+  float x[3][kChunk][DH];     // zx, rx, nx
 };
+// Phase A reads the inputs; phase B reads the row scalars of J per step,
+// [step][d1, d2, d3, r, d5][row], one base address per step for all of them.
+union __attribute__((aligned(16))) PhiShared {
+  PhiInputs in;
+  float rs[kChunk][5][DH];
+};
+static_assert(sizeof(float) * kChunk * 5 * DH <= sizeof(PhiInputs), "row scalars alias the inputs");
 
 // The fp32 gates z, r, n of every step go to gates_out, laid out
 // [task][step][gate][64] with task = seq * n_chunks + c (the replays read
@@ -220,10 +228,10 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
       rx = ld(wx + wx_at(b, t, T, d, 1, head, j));
       nx = ld(wx + wx_at(b, t, T, d, 2, head, j));
     }
-    sh.hp[s][j] = hp;
-    sh.x[0][s][j] = zx;
-    sh.x[1][s][j] = rx;
-    sh.x[2][s][j] = nx;
+    sh.in.hp[s][j] = hp;
+    sh.in.x[0][s][j] = zx;
+    sh.in.x[1][s][j] = rx;
+    sh.in.x[2][s][j] = nx;
   }
 
   // ---- phase A: gates by fp32 MFMA (wave w: output channels 16w + li) ----
@@ -245,7 +253,7 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
     for (int rt = 0; rt < 2; ++rt) {
       gz[rt] = floatx4{0.f, 0.f, 0.f, 0.f};
       gr[rt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      const float* hrow = &sh.hp[16 * rt + li][16 * g];
+      const float* hrow = &sh.in.hp[16 * rt + li][16 * g];
 #pragma unroll
       for (int kk = 0; kk < 16; kk += 4) {
         const float4 a4 = *reinterpret_cast<const float4*>(hrow + kk);
@@ -263,16 +271,16 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int s = 16 * rt + 4 * g + v;
-        gr[rt][v] = fsigmoid(gr[rt][v] + sh.x[1][s][col]);
-        gz[rt][v] = fsigmoid(gz[rt][v] + sh.x[0][s][col]);
-        sh.r[s][col] = gr[rt][v];
+        gr[rt][v] = fsigmoid(gr[rt][v] + sh.in.x[1][s][col]);
+        gz[rt][v] = fsigmoid(gz[rt][v] + sh.in.x[0][s][col]);
+        sh.in.r[s][col] = gr[rt][v];
       }
     __syncthreads();
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       gn[rt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      const float* hrow = &sh.hp[16 * rt + li][16 * g];
-      const float* rrow = &sh.r[16 * rt + li][16 * g];
+      const float* hrow = &sh.in.hp[16 * rt + li][16 * g];
+      const float* rrow = &sh.in.r[16 * rt + li][16 * g];
 #pragma unroll
       for (int kk = 0; kk < 16; kk += 4) {
         const float4 h4 = *reinterpret_cast<const float4*>(hrow + kk);
@@ -291,8 +299,8 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
     for (int v = 0; v < 4; ++v) {
       const int s = 16 * rt + 4 * g + v;
       const float z = gz[rt][v], r = gr[rt][v];
-      const float n = ftanh(gn[rt][v] + sh.x[2][s][col]);
-      const float hp = sh.hp[s][col];
+      const float n = ftanh(gn[rt][v] + sh.in.x[2][s][col]);
+      const float hp = sh.in.hp[s][col];
       rs[rt][v][0] = 1.f - z;
       rs[rt][v][1] = (n - hp) * z * (1.f - z);
       rs[rt][v][2] = z * (1.f - n * n);
@@ -311,11 +319,8 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int s = 16 * rt + 4 * g + v;
-      sh.x[0][s][col] = rs[rt][v][0];
-      sh.x[1][s][col] = rs[rt][v][1];
-      sh.x[2][s][col] = rs[rt][v][2];
-      sh.r[s][col] = rs[rt][v][3];
-      sh.hp[s][col] = rs[rt][v][4];
+#pragma unroll
+      for (int q = 0; q < 5; ++q) sh.rs[s][q][col] = rs[rt][v][q];
     }
 
   // ---- phase B constants: A^T operands in bf16, contraction permuted ----
@@ -353,9 +358,13 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
   // 16 (2 ks) + 4 g + (0..3) then 16 (2 ks + 1) + 4 g + (0..3).
   auto to_b = [](const float X[4][4], bf16x8 out[2]) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int q = 0; q < 8; ++q) out[ks][q] = static_cast<__bf16>(X[2 * ks + (q >> 2)][q & 3]);
+    for (int ks = 0; ks < 2; ++ks) {
+      const u32x4 w = {pack_bf16x2(X[2 * ks][0], X[2 * ks][1]),
+                       pack_bf16x2(X[2 * ks][2], X[2 * ks][3]),
+                       pack_bf16x2(X[2 * ks + 1][0], X[2 * ks + 1][1]),
+                       pack_bf16x2(X[2 * ks + 1][2], X[2 * ks + 1][3])};
+      out[ks] = __builtin_bit_cast(bf16x8, w);
+    }
   };
   auto product = [](const bf16x8 at[4][2], const bf16x8 bop[2], float X[4][4]) {
 #pragma unroll
@@ -369,42 +378,38 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
   };
 
   for (int s = 0; s < len; ++s) {
+    const float* rsc = &sh.rs[s][0][4 * g];
     bf16x8 bp[2];
     to_b(P, bp);
-    float X1[4][4], X2[4][4];
-    product(atz, bp, X1);
-    product(atr, bp, X2);
-    // Row scalars are read per row tile after the products are issued (kept
-    // out of the registers that hold Phi and the A^T operands).
+    // Y = r P + d5 (A_r^T P), the operand of the A_n product.
+    float X[4][4];
+    product(atr, bp, X);
     __builtin_amdgcn_sched_barrier(0);
-    // Y = r P + d5 X2;  P <- d1 P + d2 X1 (partial)
     float Y[4][4];
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
-      const int i = 16 * rt + 4 * g;
-      const float4 r4 = *reinterpret_cast<const float4*>(&sh.r[s][i]);
-      const float4 d5 = *reinterpret_cast<const float4*>(&sh.hp[s][i]);
-      const float4 d1 = *reinterpret_cast<const float4*>(&sh.x[0][s][i]);
-      const float4 d2 = *reinterpret_cast<const float4*>(&sh.x[1][s][i]);
+      const float4 r4 = *reinterpret_cast<const float4*>(rsc + 3 * DH + 16 * rt);
+      const float4 d5 = *reinterpret_cast<const float4*>(rsc + 4 * DH + 16 * rt);
       const float rv[4] = {r4.x, r4.y, r4.z, r4.w}, d5v[4] = {d5.x, d5.y, d5.z, d5.w};
-      const float d1v[4] = {d1.x, d1.y, d1.z, d1.w}, d2v[4] = {d2.x, d2.y, d2.z, d2.w};
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        Y[rt][v] = rv[v] * P[rt][v] + d5v[v] * X2[rt][v];
-        P[rt][v] = d1v[v] * P[rt][v] + d2v[v] * X1[rt][v];
-      }
+      for (int v = 0; v < 4; ++v) Y[rt][v] = rv[v] * P[rt][v] + d5v[v] * X[rt][v];
     }
     bf16x8 by[2];
     to_b(Y, by);
-    float X3[4][4];
+    // A_z^T P and A_n^T Y issued together; P <- d1 P + d2 (A_z^T P) + d3 (A_n^T Y).
+    float X1[4][4], X3[4][4];
+    product(atz, bp, X1);
     product(atn, by, X3);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
-      const float4 d3 = *reinterpret_cast<const float4*>(&sh.x[2][s][16 * rt + 4 * g]);
+      const float4 d1 = *reinterpret_cast<const float4*>(rsc + 0 * DH + 16 * rt);
+      const float4 d2 = *reinterpret_cast<const float4*>(rsc + 1 * DH + 16 * rt);
+      const float4 d3 = *reinterpret_cast<const float4*>(rsc + 2 * DH + 16 * rt);
+      const float d1v[4] = {d1.x, d1.y, d1.z, d1.w}, d2v[4] = {d2.x, d2.y, d2.z, d2.w};
       const float d3v[4] = {d3.x, d3.y, d3.z, d3.w};
 #pragma unroll
-      for (int v = 0; v < 4; ++v) P[rt][v] += d3v[v] * X3[rt][v];
+      for (int v = 0; v < 4; ++v) P[rt][v] = d1v[v] * P[rt][v] + d2v[v] * X1[rt][v] + d3v[v] * X3[rt][v];
     }
   }
   float* po = phi_out + static_cast<size_t>(blockIdx.x) * DH * DH;

@@ -3,7 +3,9 @@
 The library is a plain C-ABI shared object (declarations in
 ``include/pararnn_amd.h``); it is loaded with ctypes by ``pararnn_amd._lib``.
 Building needs only ROCm's hipcc, no GPU.  Every HIP source is compiled with
-packed-fp32 instructions disabled (``-packed-fp32-ops``).
+packed-fp32 instructions disabled (``-packed-fp32-ops``) and with MFMA results
+in ordinary VGPRs (``-amdgpu-mfma-vgpr-form``: no accumulator-register reads in
+the MFMA step loops).
 """
 
 from __future__ import annotations
@@ -42,6 +44,7 @@ def _flags() -> list[str]:
         "-std=c++17",
         "-fPIC",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-mllvm", "-amdgpu-mfma-vgpr-form=1",
         f"-I{INCLUDE}",
         f"-I{CSRC}",
     ]
