@@ -187,3 +187,54 @@ def test_full_length_linearity_and_one_head_slice():
     e_a = max(_rel(a_a[i, 0], ref[k]) for i, k in enumerate(("A_z", "A_r", "A_n")))
     print(f"  head 0 vs oracle: g_wx {e_wx:.2e} g_a {e_a:.2e}", flush=True)
     assert e_wx <= 1e-4 and e_a <= 1e-4
+
+
+def test_recompute_chunk_len_and_packed_sequences():
+    """The other autograd routes of newton_apply: recompute (bit-equal), chunk_len
+    windows and packed cu_seqlens (equal to per-sequence solves)."""
+    from pararnn_amd import NewtonConfig, ParaGRU, newton_apply
+
+    print("case head GRU grads: recompute, chunk_len, cu_seqlens", flush=True)
+    torch.manual_seed(6)
+    cell = ParaGRU(12, 128, mix="head", n_heads=2).to(DEV)
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(2, 150, 12, generator=g).to(DEV)
+    h0 = (torch.randn(2, 128, generator=g) * 0.5).to(DEV)
+    up = torch.randn(2, 150, 128, generator=g).to(DEV)
+
+    def grads(cfg, **kw):
+        cell.zero_grad()
+        xx = x.clone().requires_grad_(True)
+        hh = h0.clone().requires_grad_(True)
+        (newton_apply(cell, xx, cfg, h0=hh, **kw) * up).sum().backward()
+        return [xx.grad, hh.grad] + [p.grad.clone() for p in cell.parameters()]
+
+    base = NewtonConfig(max_iters=8, residual_atol=None, residual_fail=None)
+    ref = grads(base)
+    rec = grads(NewtonConfig(max_iters=8, residual_atol=None, residual_fail=None, recompute=True))
+    for a, b in zip(ref, rec):
+        assert torch.equal(a, b)
+    chk = grads(NewtonConfig(max_iters=8, residual_atol=None, residual_fail=None, chunk_len=64))
+    for a, b in zip(ref, chk):
+        e = _rel(b.cpu(), a.cpu())
+        assert e <= 1e-4, e
+    # packed: two sequences of the batch laid end to end
+    cell.zero_grad()
+    xp = torch.cat([x[0], x[1, :90]], 0).unsqueeze(0).clone().requires_grad_(True)
+    hp = h0.clone().requires_grad_(True)
+    upp = torch.cat([up[0], up[1, :90]], 0).unsqueeze(0)
+    cs = torch.tensor([0, 150, 240], device=DEV)
+    (newton_apply(cell, xp, base, h0=hp, cu_seqlens=cs) * upp).sum().backward()
+    packed = [p.grad.clone() for p in cell.parameters()]
+    cell.zero_grad()
+    xs = [x[0:1].clone().requires_grad_(True), x[1:2, :90].clone().requires_grad_(True)]
+    hs = h0.clone().requires_grad_(True)
+    for i, xi in enumerate(xs):
+        (newton_apply(cell, xi, base, h0=hs[i:i + 1]) * up[i:i + 1, :xi.shape[1]]).sum().backward()
+    for a, b in zip(packed, [p.grad for p in cell.parameters()]):
+        e = _rel(a.cpu(), b.cpu())
+        print(f"  packed vs per-sequence param grad: {e:.2e}", flush=True)
+        assert e <= 1e-5
+    assert _rel(xp.grad[0, :150].cpu(), xs[0].grad[0].cpu()) <= 1e-5
+    assert _rel(xp.grad[0, 150:].cpu(), xs[1].grad[0].cpu()) <= 1e-5
+    assert _rel(hp.grad.cpu(), hs.grad.cpu()) <= 1e-5
