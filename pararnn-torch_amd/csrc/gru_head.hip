@@ -586,9 +586,9 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
 //  gru_carry_kernel<REV> nu entering each chunk from the right;
 //  gru_rev_kernel        per chunk from its carry: mu_t, the pre-activation
 //                        gradients (g_wx) and, for chunk 0, grad h0 = nu_0;
-//  gru_ga_kernel         per (split of the B T rows, gate, head): the partial
-//                        sums of the outer products X^T D by fp32 MFMA
-//                        (X = h_prev for z, r; h_prev r for n);
+//  gru_ga_kernel         per (split of the B T rows, head): the partial sums
+//                        of the outer products X^T D of all three gates by
+//                        fp32 MFMA (X = h_prev for z, r; h_prev r for n);
 //  gru_ga_reduce_kernel  fixed-order sum of the splits (deterministic).
 // ===========================================================================
 
@@ -681,9 +681,11 @@ __global__ __launch_bounds__(256) void gru_rev_kernel(
 }
 
 // Partial sums of g_A[gate][head][i][o] = sum over rows k = (b, t) of
-// X[k][i] D[k][o] over one split of the B T rows.  4 waves; wave w owns the
-// output columns 16 w .. 16 w + 15 (four 16x16 tiles down the rows i).  Rows
-// are staged through LDS 16 at a time.
+// X_g[k][i] D_g[k][o] over one split of the B T rows, all three gates in one
+// block (X = h_prev for z and r, h_prev r for n; D the gate's pre-activation
+// gradients), so h_prev and r are read once.  4 waves; wave w owns the output
+// columns 16 w .. 16 w + 15 of each gate (four 16x16 tiles down the rows i).
+// Rows are staged through LDS 16 at a time.
 constexpr int kGaRows = 16;
 constexpr int kGaPad = 80;  // fp32 LDS row stride (the 4 lane groups land on distinct banks)
 
@@ -692,19 +694,20 @@ __global__ __launch_bounds__(256) void gru_ga_kernel(
     const TX* __restrict__ h0, const TX* __restrict__ states, const float* __restrict__ gates,
     const TX* __restrict__ g_wx, int B, int T, int H, int n_chunks, int n_split, int rows_per,
     float* __restrict__ part) {
-  __shared__ float sx[kGaRows][kGaPad], sy[kGaRows][kGaPad];
+  __shared__ float sx[2][kGaRows][kGaPad], sy[3][kGaRows][kGaPad];
   const int split = blockIdx.x % n_split;
-  const int gate = (blockIdx.x / n_split) % 3;
-  const int head = blockIdx.x / (n_split * 3);
+  const int head = blockIdx.x / n_split;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int li = lane & 15, g = lane >> 4;
   const int d = H * DH;
   const long long n_rows = static_cast<long long>(B) * T;
   const long long r0 = static_cast<long long>(split) * rows_per;
   const long long r1 = min(n_rows, r0 + rows_per);
-  floatx4 acc[4];
+  floatx4 acc[3][4];
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt) acc[rt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < 3; ++q)
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) acc[q][rt] = floatx4{0.f, 0.f, 0.f, 0.f};
   for (long long k0 = r0; k0 < r1; k0 += kGaRows) {
     __syncthreads();
 #pragma unroll
@@ -712,35 +715,47 @@ __global__ __launch_bounds__(256) void gru_ga_kernel(
       const int idx = threadIdx.x + 256 * q;
       const int kr = idx / DH, j = idx % DH;
       const long long k = k0 + kr;
-      float xv = 0.f, yv = 0.f;
+      float hv = 0.f, rv = 0.f, y0 = 0.f, y1 = 0.f, y2 = 0.f;
       if (k < r1) {
         const int b = static_cast<int>(k / T), t = static_cast<int>(k % T);
         if (t > 0)
-          xv = ld(states + h_at(b, t - 1, T, d, head, j));
+          hv = ld(states + h_at(b, t - 1, T, d, head, j));
         else if (h0 != nullptr)
-          xv = ld(h0 + static_cast<size_t>(b) * d + head * DH + j);
-        if (gate == 2) {
-          const size_t task = static_cast<size_t>(b * H + head) * n_chunks + t / kChunk;
-          xv *= gates[((task * kChunk + t % kChunk) * 3 + 1) * DH + j];
-        }
-        yv = ld(g_wx + wx_at(b, t, T, d, gate, head, j));
+          hv = ld(h0 + static_cast<size_t>(b) * d + head * DH + j);
+        const size_t task = static_cast<size_t>(b * H + head) * n_chunks + t / kChunk;
+        rv = gates[((task * kChunk + t % kChunk) * 3 + 1) * DH + j];
+        y0 = ld(g_wx + wx_at(b, t, T, d, 0, head, j));
+        y1 = ld(g_wx + wx_at(b, t, T, d, 1, head, j));
+        y2 = ld(g_wx + wx_at(b, t, T, d, 2, head, j));
       }
-      sx[kr][j] = xv;
-      sy[kr][j] = yv;
+      sx[0][kr][j] = hv;
+      sx[1][kr][j] = hv * rv;
+      sy[0][kr][j] = y0;
+      sy[1][kr][j] = y1;
+      sy[2][kr][j] = y2;
     }
     __syncthreads();
 #pragma unroll
     for (int kk = 0; kk < kGaRows / 4; ++kk) {
-      const float bv = sy[4 * kk + g][16 * wave + li];
+      const float* xh = &sx[0][4 * kk + g][li];
+      const float* xu = &sx[1][4 * kk + g][li];
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt) acc[rt] = mfma_f32(sx[4 * kk + g][16 * rt + li], bv, acc[rt]);
+      for (int q = 0; q < 3; ++q) {
+        const float bv = sy[q][4 * kk + g][16 * wave + li];
+        const float* xa = q == 2 ? xu : xh;
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) acc[q][rt] = mfma_f32(xa[16 * rt], bv, acc[q][rt]);
+      }
     }
   }
-  float* po = part + static_cast<size_t>(blockIdx.x) * DH * DH;
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
+  for (int q = 0; q < 3; ++q) {
+    float* po = part + (static_cast<size_t>(head * 3 + q) * n_split + split) * DH * DH;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) po[(16 * rt + 4 * g + v) * DH + 16 * wave + li] = acc[rt][v];
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) po[(16 * rt + 4 * g + v) * DH + 16 * wave + li] = acc[q][rt][v];
+  }
 }
 
 // g_a[gate][head] = sum over splits in index order.
@@ -860,7 +875,7 @@ struct BwdWs {
 
 static void ga_split(int B, int T, int H, int* n_split, int* rows_per) {
   const long long n_rows = static_cast<long long>(B) * T;
-  const long long want = (2048 + 3 * H - 1) / (3 * H);  // ~2048 blocks in flight
+  const long long want = (2048 + H - 1) / H;  // ~2048 blocks in flight
   long long ns = std::min<long long>(want, (n_rows + 63) / 64);
   if (ns < 1) ns = 1;
   long long rp = (n_rows + ns - 1) / ns;
@@ -903,7 +918,7 @@ static int run_bwd(const TX* wx, const TX* az, const TX* ar, const TX* an, const
       az, ar, an, h0, states, grad, w.gates, w.carry, g_wx, nullptr, h0 != nullptr ? g_h0 : nullptr,
       B, T, H, n_chunks);
   PRNN_HIP(hipGetLastError());
-  gru_ga_kernel<TX><<<dim3(w.n_split * 3 * H), dim3(256), 0, stream>>>(
+  gru_ga_kernel<TX><<<dim3(w.n_split * H), dim3(256), 0, stream>>>(
       h0, states, w.gates, g_wx, B, T, H, n_chunks, w.n_split, w.rows_per, w.part);
   PRNN_HIP(hipGetLastError());
   gru_ga_reduce_kernel<<<dim3((3 * H * DH * DH + 255) / 256), dim3(256), 0, stream>>>(
