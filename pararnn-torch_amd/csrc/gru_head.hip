@@ -35,6 +35,7 @@ namespace gru {
 
 constexpr int DH = 64;      // head width handled by these kernels
 constexpr int kChunk = 32;  // time steps per chunk
+constexpr int kCarryParts = 16;  // threads per row of the carry mat-vec
 constexpr int kPad = 72;    // bf16 row stride of the LDS operand tiles (16-byte aligned rows)
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -426,69 +427,87 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
   }
 }
 
+// Inclusive sum over each row of 16 lanes by DPP row shifts (VALU latency, no
+// LDS round trips); lane 15 of the row ends with the row's total.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dpp_f<0x111>(v);  // row_shr:1
+  v += dpp_f<0x112>(v);  // row_shr:2
+  v += dpp_f<0x114>(v);  // row_shr:4
+  v += dpp_f<0x118>(v);  // row_shr:8
+  return v;
+}
+
 // ---------------------------------------------------------------------------
 // Carries over chunks: carry_0 = 0, carry_{c+1} = Phi_c carry_c + e_c.
 // REV (eq. 2.6 backward, phi holding Phi^T): chunks from the last one down,
 // carry_{n-1} = 0, carry_{c-1} = Phi_c^T carry_c + e_c.
-// 256 threads: thread (i, part) sums 16 of row i's 64 products.
+// 64 kCarryParts threads: thread (i, part) sums 64 / kCarryParts of row i's
+// products.
 // ---------------------------------------------------------------------------
 template <bool REV>
-__global__ __launch_bounds__(256) void gru_carry_kernel(const float* __restrict__ phi,
-                                                       const float* __restrict__ e, int n_chunks,
-                                                       float* __restrict__ carry_in) {
-  // The chain is serial over chunks, so each step's cost is the latency of
-  // its 16 KB of Phi and its e: both are fetched kDepth chunks ahead into a
-  // register ring.
-  constexpr int kDepth = 4;
+__global__ __launch_bounds__(64 * kCarryParts) void gru_carry_kernel(
+    const float* __restrict__ phi, const float* __restrict__ e, int n_chunks,
+    float* __restrict__ carry_in) {
+  // The chain is serial over chunks, so each step costs the latency of its
+  // 16 KB of Phi and its e.  Thread (i, part) holds 4 entries of row i; the
+  // chunks are fetched a block of kB ahead into one of two register blocks
+  // (written out by hand, no dynamic register indexing) while the other block
+  // is walked, and a block's carries are stored after its kB steps.
+  static_assert(DH / kCarryParts == 4, "one float4 of a Phi row per thread");
+  constexpr int kB = 8;
   __shared__ float s_c[2][DH];
   const int seq = blockIdx.x;
-  const int i = threadIdx.x >> 2, part = threadIdx.x & 3;
+  const int i = threadIdx.x / kCarryParts, part = threadIdx.x % kCarryParts;
   if (threadIdx.x < DH) s_c[0][threadIdx.x] = 0.f;
   __syncthreads();
   const float* P = phi + static_cast<size_t>(seq) * n_chunks * DH * DH;
   const float* E = e + static_cast<size_t>(seq) * n_chunks * DH;
-  auto chunk_of = [&](int step) { return REV ? n_chunks - 1 - step : step; };
-  float4 ring[kDepth][4];
-  float ering[kDepth];
-  auto fetch = [&](int step, int slot) {
-    if (step < n_chunks) {
-      const int c = chunk_of(step);
-      const float4* p =
-          reinterpret_cast<const float4*>(P + (static_cast<size_t>(c) * DH + i) * DH + 16 * part);
+  // Steps past the last chunk re-read the last chunk (no branch around the
+  // loads) and write nothing.
+  auto chunk_of = [&](int step) {
+    const int k = min(step, n_chunks - 1);
+    return REV ? n_chunks - 1 - k : k;
+  };
+  auto fetch = [&](int step0, float4 rows[kB], float ev[kB]) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) ring[slot][q] = p[q];
-      ering[slot] = E[static_cast<size_t>(c) * DH + i];
+    for (int k = 0; k < kB; ++k) {
+      const int c = chunk_of(step0 + k);
+      rows[k] = *reinterpret_cast<const float4*>(P + (static_cast<size_t>(c) * DH + i) * DH + 4 * part);
+      ev[k] = E[static_cast<size_t>(c) * DH + i];
     }
   };
-#pragma unroll
-  for (int k = 0; k < kDepth; ++k) fetch(k, k);
   int cur = 0;
-  for (int step0 = 0; step0 < n_chunks; step0 += kDepth) {
+  auto walk = [&](int step0, const float4 rows[kB], const float ev[kB]) {
+    float out[kB];
 #pragma unroll
-    for (int k = 0; k < kDepth; ++k) {
-      const int step = step0 + k;
-      if (step >= n_chunks) break;
-      const int c = chunk_of(step);
-      float4 row[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) row[q] = ring[k][q];
-      const float ev = ering[k];
-      fetch(step + kDepth, k);
-      const float* v = s_c[cur] + 16 * part;
-      float acc = 0.f;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        acc += row[q].x * v[4 * q] + row[q].y * v[4 * q + 1] + row[q].z * v[4 * q + 2] +
-               row[q].w * v[4 * q + 3];
-      acc += __shfl_xor(acc, 1);
-      acc += __shfl_xor(acc, 2);
-      if (part == 0) {
-        carry_in[(static_cast<size_t>(seq) * n_chunks + c) * DH + i] = s_c[cur][i];
-        s_c[cur ^ 1][i] = acc + ev;
-      }
+    for (int k = 0; k < kB; ++k) {
+      const float4 v = *reinterpret_cast<const float4*>(s_c[cur] + 4 * part);
+      float acc = rows[k].x * v.x + rows[k].y * v.y + rows[k].z * v.z + rows[k].w * v.w;
+      acc = row_sum16(acc);  // the 16 threads of row i are one DPP row; lane 15 holds the sum
+      out[k] = s_c[cur][i];
+      if (part == kCarryParts - 1) s_c[cur ^ 1][i] = acc + ev[k];
       __syncthreads();
       cur ^= 1;
     }
+    if (part == kCarryParts - 1) {
+#pragma unroll
+      for (int k = 0; k < kB; ++k)
+        if (step0 + k < n_chunks)
+          carry_in[(static_cast<size_t>(seq) * n_chunks + chunk_of(step0 + k)) * DH + i] = out[k];
+    }
+  };
+  float4 ra[kB], rb[kB];
+  float ea[kB], eb[kB];
+  fetch(0, ra, ea);
+  for (int step0 = 0; step0 < n_chunks; step0 += 2 * kB) {
+    fetch(step0 + kB, rb, eb);
+    walk(step0, ra, ea);
+    fetch(step0 + 2 * kB, ra, ea);
+    walk(step0 + kB, rb, eb);
   }
 }
 
@@ -848,7 +867,7 @@ static int run(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX*
         az, ar, an, h0, hin, w.gates, nullptr, static_cast<float*>(nullptr), w.e, B, T, H,
         n_chunks, omega);
     PRNN_HIP(hipGetLastError());
-    gru_carry_kernel<false><<<dim3(n_seq), dim3(256), 0, stream>>>(w.phi, w.e, n_chunks, w.carry);
+    gru_carry_kernel<false><<<dim3(n_seq), dim3(64 * kCarryParts), 0, stream>>>(w.phi, w.e, n_chunks, w.carry);
     PRNN_HIP(hipGetLastError());
     if (k == K) {
       gru_replay_kernel<TX, TX, false><<<dim3(replay_blocks), dim3(256), 0, stream>>>(
@@ -912,7 +931,7 @@ static int run_bwd(const TX* wx, const TX* az, const TX* ar, const TX* an, const
       az, ar, an, h0, states, grad, w.gates, nullptr, static_cast<TX*>(nullptr), w.e, nullptr, B,
       T, H, n_chunks);
   PRNN_HIP(hipGetLastError());
-  gru_carry_kernel<true><<<dim3(n_seq), dim3(256), 0, stream>>>(w.phi, w.e, n_chunks, w.carry);
+  gru_carry_kernel<true><<<dim3(n_seq), dim3(64 * kCarryParts), 0, stream>>>(w.phi, w.e, n_chunks, w.carry);
   PRNN_HIP(hipGetLastError());
   gru_rev_kernel<TX, false><<<dim3(rev_blocks), dim3(256), 0, stream>>>(
       az, ar, an, h0, states, grad, w.gates, w.carry, g_wx, nullptr, h0 != nullptr ? g_h0 : nullptr,
