@@ -804,7 +804,10 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_fused_kernel(
   }
   const rsrc_t ro = make_rsrc(out + first * row4 + c0, span * sizeof(TX));
 
-  for (int k = 0; k < K; ++k) {
+  // Iterations 1 .. K-1 keep the new iterate in registers; the last one,
+  // compiled separately, writes it (no per-step branch on the iteration).
+  auto iterate = [&](const int k, auto last_c) {
+    constexpr bool last_iter = decltype(last_c)::value;
     const int tag = k + 1;
     // Keep wx packed across iterations (otherwise the unpacking is hoisted out
     // of the loop and holds 4 floats per step).
@@ -936,7 +939,6 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_fused_kernel(
 
     // Pass 2: delta_t = J_t delta_{t-1} + F_t from the true carry; the new
     // iterate H + omega delta stays in registers (written by the last one).
-    const bool last_iter = k == K - 1;
     float dl[4], hl[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) dl[j] = s_carry[wave][j][lane];
@@ -955,7 +957,7 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_fused_kernel(
           hl[j] = hv[j] + omega * dl[j];
           prev[j] = hv[j];
         }
-        if (last_iter) {
+        if constexpr (last_iter) {
           const uint32_t so = s * row4 * sizeof(TX);
 #pragma unroll
           for (int j = 0; j < 4; ++j) stb<TX>(ro, vx, so + j * d * sizeof(TX), hl[j]);
@@ -973,7 +975,7 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_fused_kernel(
           if (s < n_steps) replay(s);
       }
     }
-    if (!last_iter) {
+    if constexpr (!last_iter) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) s_hl[wave][j][lane] = hl[j];
       if (wave == W - 1) {
@@ -983,7 +985,9 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_fused_kernel(
       }
     }
     __syncthreads();
-  }
+  };
+  for (int k = 0; k < K - 1; ++k) iterate(k, std::false_type{});
+  iterate(K - 1, std::true_type{});
 }
 
 }  // namespace slstm
