@@ -512,81 +512,107 @@ __global__ __launch_bounds__(64 * kCarryParts) void gru_carry_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Replay: the exact fp32 recurrence of one chunk from its carry.  Each wave
-// handles one chunk; lane j keeps column j of A_z, A_r, A_n in registers and
-// reads the step's gates (written by the chunk kernel from the same guess).
-// LOCAL: from a zero carry, writing only the chunk's final delta (the local
-// solution e of the carry scan); otherwise from the chunk's carry, writing
-// H + omega delta.  The inputs of step s + 2 are loaded while step s
-// computes (the recurrence itself is serial).
+// Replay: the exact fp32 recurrence of a chunk from its carry.  Each wave
+// walks kPair consecutive chunks of one sequence side by side (the two serial
+// chains hide each other's latency); lane j keeps column j of A_z, A_r, A_n
+// in registers, shared by the chunks, and reads the step's gates (written by
+// the chunk kernel from the same guess).  LOCAL: from a zero carry, writing
+// only each chunk's final delta (the local solution e of the carry scan);
+// otherwise from the chunk's carry, writing H + omega delta.
 // ---------------------------------------------------------------------------
+constexpr int kPair = 2;
+
 template <typename TX, typename TOUT, bool LOCAL>
 __global__ __launch_bounds__(256) void gru_replay_kernel(
     const TX* __restrict__ a_z, const TX* __restrict__ a_r, const TX* __restrict__ a_n,
     const TX* __restrict__ h0, const float* __restrict__ hin, const float* __restrict__ gates,
     const float* __restrict__ carry_in, TOUT* __restrict__ hout, float* __restrict__ e_out,
     int B, int T, int H, int n_chunks, float omega) {
-  __shared__ float s_v[4][2][DH];
+  __shared__ float s_v[4][kPair][2][DH];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n_pairs = (n_chunks + kPair - 1) / kPair;
   const int task = blockIdx.x * 4 + wave;
   const int n_seq = B * H;
-  if (task >= n_seq * n_chunks) return;  // whole wave exits together
+  if (task >= n_seq * n_pairs) return;  // whole wave exits together
   const int d = H * DH;
-  const int seq = task / n_chunks, c = task % n_chunks;
+  const int seq = task / n_pairs, c0 = (task % n_pairs) * kPair;
   const int b = seq / H, head = seq % H;
-  const int t0 = c * kChunk;
-  const int len = min(kChunk, T - t0);
-  float* s_d = s_v[wave][0];
-  float* s_w = s_v[wave][1];
   float az[DH], ar[DH], an[DH];
   load_col(a_z, head, lane, az);
   load_col(a_r, head, lane, ar);
   load_col(a_n, head, lane, an);
-  float dl = LOCAL ? 0.f : carry_in[static_cast<size_t>(task) * DH + lane];
 
   struct In {
     float hp, z, r, n, ht;
   };
-  const float* gt = gates + static_cast<size_t>(task) * kChunk * 3 * DH + lane;
-  auto load_in = [&](int s) {
+  int t0[kPair], len[kPair];
+  float dl[kPair];
+  const float* gt[kPair];
+#pragma unroll
+  for (int k = 0; k < kPair; ++k) {
+    const int c = c0 + k;
+    const bool valid = c < n_chunks;
+    t0[k] = c * kChunk;
+    len[k] = valid ? min(kChunk, T - t0[k]) : 0;
+    const size_t id = static_cast<size_t>(seq) * n_chunks + (valid ? c : c0);
+    dl[k] = (LOCAL || !valid) ? 0.f : carry_in[id * DH + lane];
+    gt[k] = gates + id * kChunk * 3 * DH + lane;
+  }
+  auto load_in = [&](int k, int s) {
     In v{0.f, 0.f, 0.f, 0.f, 0.f};
-    if (s < len) {
-      const int t = t0 + s;
+    if (s < len[k]) {
+      const int t = t0[k] + s;
       if (t > 0)
         v.hp = hin[h_at(b, t - 1, T, d, head, lane)];
       else if (h0 != nullptr)
         v.hp = ld(h0 + static_cast<size_t>(b) * d + head * DH + lane);
-      v.z = gt[(s * 3) * DH];
-      v.r = gt[(s * 3 + 1) * DH];
-      v.n = gt[(s * 3 + 2) * DH];
+      v.z = gt[k][(s * 3) * DH];
+      v.r = gt[k][(s * 3 + 1) * DH];
+      v.n = gt[k][(s * 3 + 2) * DH];
       v.ht = hin[h_at(b, t, T, d, head, lane)];
     }
     return v;
   };
-  In cur = load_in(0), nx1 = load_in(1);
-  for (int s = 0; s < len; ++s) {
-    const In nx2 = load_in(s + 2);
-    const int t = t0 + s;
-    const float hp = cur.hp;
-    s_d[lane] = dl;
-    __builtin_amdgcn_wave_barrier();
+  // Chunk 0 of the pair is the longest (only a sequence's last chunk is short).
+  for (int s = 0; s < len[0]; ++s) {
+    In cur[kPair];
+#pragma unroll
+    for (int k = 0; k < kPair; ++k) cur[k] = load_in(k, s);
     // J delta = (1-z) delta + d2 (delta @ A_z) + d3 ((r delta + d5 (delta @ A_r)) @ A_n)
-    const float yz = vec_col(s_d, az);
-    const float yr = vec_col(s_d, ar);
-    const float d5 = hp * cur.r * (1.f - cur.r);
-    s_w[lane] = cur.r * dl + d5 * yr;
+#pragma unroll
+    for (int k = 0; k < kPair; ++k) s_v[wave][k][0][lane] = dl[k];
     __builtin_amdgcn_wave_barrier();
-    const float yn = vec_col(s_w, an);
-    const float d2 = (cur.n - hp) * cur.z * (1.f - cur.z);
-    const float d3 = cur.z * (1.f - cur.n * cur.n);
-    const float h_new = lerp_t(hp, cur.n, cur.z);
-    dl = (1.f - cur.z) * dl + d2 * yz + d3 * yn + (h_new - cur.ht);
-    if (!LOCAL) st(hout + h_at(b, t, T, d, head, lane), cur.ht + omega * dl);
+    float yz[kPair], yr[kPair], yn[kPair];
+#pragma unroll
+    for (int k = 0; k < kPair; ++k) {
+      yz[k] = vec_col(s_v[wave][k][0], az);
+      yr[k] = vec_col(s_v[wave][k][0], ar);
+    }
+#pragma unroll
+    for (int k = 0; k < kPair; ++k) {
+      const float d5 = cur[k].hp * cur[k].r * (1.f - cur[k].r);
+      s_v[wave][k][1][lane] = cur[k].r * dl[k] + d5 * yr[k];
+    }
     __builtin_amdgcn_wave_barrier();
-    cur = nx1;
-    nx1 = nx2;
+#pragma unroll
+    for (int k = 0; k < kPair; ++k) yn[k] = vec_col(s_v[wave][k][1], an);
+#pragma unroll
+    for (int k = 0; k < kPair; ++k) {
+      const In& v = cur[k];
+      const float d2 = (v.n - v.hp) * v.z * (1.f - v.z);
+      const float d3 = v.z * (1.f - v.n * v.n);
+      const float h_new = lerp_t(v.hp, v.n, v.z);
+      dl[k] = (1.f - v.z) * dl[k] + d2 * yz[k] + d3 * yn[k] + (h_new - v.ht);
+      if (!LOCAL && s < len[k])
+        st(hout + h_at(b, t0[k] + s, T, d, head, lane), v.ht + omega * dl[k]);
+    }
+    __builtin_amdgcn_wave_barrier();
   }
-  if (LOCAL) e_out[static_cast<size_t>(task) * DH + lane] = dl;
+  if (LOCAL) {
+#pragma unroll
+    for (int k = 0; k < kPair; ++k)
+      if (len[k] > 0) e_out[(static_cast<size_t>(seq) * n_chunks + c0 + k) * DH + lane] = dl[k];
+  }
 }
 
 // ===========================================================================
@@ -857,7 +883,7 @@ static int run(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX*
   gru_init_kernel<TX, float><<<dim3(n_seq * n_blk64), dim3(64), 0, stream>>>(wx, az, ar, an, h0,
                                                                             w.work[0], B, T, H);
   PRNN_HIP(hipGetLastError());
-  const int replay_blocks = (n_seq * n_chunks + 3) / 4;
+  const int replay_blocks = (n_seq * ((n_chunks + kPair - 1) / kPair) + 3) / 4;
   for (int k = 1; k <= K; ++k) {
     const float* hin = w.work[(k - 1) & 1];
     gru_phi_kernel<TX, float, false><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
