@@ -24,6 +24,7 @@ from pararnn_amd.newton import (
     slstm_auto_picard,
     slstm_picard_next,
 )
+from pararnn_amd.layers import ParaRNN
 from pararnn_amd.ops import newton_gru_head_fused, newton_slstm_fused, slstm_init_fused
 from pararnn_amd.sequential import sequential_apply
 from pararnn_amd.verify import (
@@ -43,6 +44,7 @@ __all__ = [
     "NewtonDivergenceError",
     "NewtonStats",
     "ParaGRU",
+    "ParaRNN",
     "ParaSLSTM",
     "auto_newton_iters",
     "can_decode_step",

@@ -22,6 +22,7 @@ Reference call sites exercised (paths relative to the reference's src/pararnn):
   kernels/vjp_slstm.py:173       slstm_recurrence_vjp_eager
   kernels/gru_head_factor.py:68  gru_head_jt_mvp
   kernels/vjp_gru.py:141         gru_head_recurrence_vjp_eager
+  layers/para_rnn.py:27          ParaRNN (train: Newton, eval: sequential)
 """
 
 from __future__ import annotations
@@ -292,6 +293,33 @@ def gru_head_bwd_parts_case():
     )
 
 
+def para_rnn_case(name, cell_kind, *, d_in, d, layers, B, T, K, P, seed, n_heads=None):
+    """A stacked ParaRNN: Newton forward in train(), sequential in eval(), with the
+    state_dict so a model can be loaded by parameter name."""
+    from pararnn import NewtonConfig, ParaGRU, ParaRNN, ParaSLSTM
+
+    torch.manual_seed(seed)
+    if cell_kind == "slstm":
+        cell = ParaSLSTM(d_in, d, mix="diag")
+    else:
+        cell = ParaGRU(d_in, d, mix="head", n_heads=n_heads)
+    cfg = NewtonConfig(max_iters=K, residual_atol=None, residual_fail=None, picard_iters=P,
+                       picard_adapt=False, scan_backend="eager")
+    model = ParaRNN(cell, num_layers=layers, config=cfg, return_hidden=True)
+    gen = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(B, T, d_in, generator=gen)
+    with torch.no_grad():
+        model.train()
+        y_newton, last_newton = model(x)
+        model.eval()
+        y_seq, last_seq = model(x)
+    tensors = {f"sd.{k}": v for k, v in model.state_dict().items()}
+    tensors.update(x=x, y_newton=y_newton, last_newton=last_newton, y_seq=y_seq, last_seq=last_seq)
+    meta = dict(cell=cell_kind, d_in=d_in, d=d, layers=layers, B=B, T=T, K=K, P=P, seed=seed,
+                n_heads=n_heads)
+    _save(name, tensors, meta)
+
+
 def ragged_case(name, cell_kind, *, d_in, d, lengths, K, P, seed, n_heads=None):
     """Packed sequences: newton_apply and sequential_apply with cu_seqlens and
     per-sequence h0 (eager backend)."""
@@ -365,6 +393,10 @@ def main() -> int:
     gru_head_bwd_case("gru_head_bwd_bf16", d_in=16, d=128, n_heads=2, B=2, T=64, K=3,
                       dtype=torch.bfloat16, seed=32)
     gru_head_bwd_parts_case()
+    para_rnn_case("para_rnn_slstm_fp32", "slstm", d_in=12, d=32, layers=2, B=2, T=60, K=3, P=3,
+                  seed=41)
+    para_rnn_case("para_rnn_gru_head_fp32", "gru_head", d_in=12, d=128, layers=2, B=2, T=50, K=3,
+                  P=None, seed=42, n_heads=2)
     with open(os.path.join(HERE, "auto_picard.json"), "w") as f:
         json.dump(auto_picard_table(), f, indent=1)
     return 0
