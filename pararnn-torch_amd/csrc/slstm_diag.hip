@@ -731,8 +731,9 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
 // Both only ever wait on tiles with earlier tickets, so every wave reaches the
 // end.  The arithmetic is that of K separate launches exchanging the fp32
 // iterate through memory.
-template <typename TX, int L, int W>
-__global__ __launch_bounds__(64 * W) void slstm_newton_fused_kernel(
+template <typename TX, int L, int W, int WPE>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) void
+slstm_newton_fused_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
     const TX* __restrict__ guess, TX* __restrict__ out, int B, int T, int d, int n_cb,
     int n_tiles, int K, float omega, float eps, int* __restrict__ counter,
@@ -1291,18 +1292,18 @@ static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, 
   if (w.fused) {
     const Shape sh = newton_fused_shape(sizeof(TX) == 2 ? PRNN_BF16 : PRNN_F32);
     const Geo g = geometry(B, T, d, sh);
-#define PRNN_SHAPE(LL, WW)                                                                      \
+#define PRNN_SHAPE(LL, WW, WPE)                                                                 \
   if (sh.L == LL && sh.W == WW)                                                                 \
-    slstm_newton_fused_kernel<TX, LL, WW><<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>(       \
+    slstm_newton_fused_kernel<TX, LL, WW, WPE><<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>(  \
         wx, r, h0, guess, out, B, T, d, g.n_cb, g.n_tiles, K, omega, eps, w.lb.counters + 1,    \
         w.lb.agg, w.lb.incl, w.hlast);
     if constexpr (sizeof(TX) == 4) {
-      PRNN_SHAPE(16, 4)
+      PRNN_SHAPE(16, 4, 2)
     } else {
-      PRNN_SHAPE(20, 4)
-      PRNN_SHAPE(16, 4)
-      PRNN_SHAPE(24, 4)
-      PRNN_SHAPE(16, 8)
+      PRNN_SHAPE(20, 4, 2)
+      PRNN_SHAPE(16, 4, 2)
+      PRNN_SHAPE(24, 4, 1)
+      PRNN_SHAPE(16, 8, 2)
     }
 #undef PRNN_SHAPE
     PRNN_HIP(hipGetLastError());
