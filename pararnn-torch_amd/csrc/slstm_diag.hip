@@ -31,6 +31,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 namespace prnn {
 namespace slstm {
 
@@ -739,7 +741,7 @@ slstm_newton_fused_kernel(
     int n_tiles, int K, float omega, float eps, int* __restrict__ counter,
     unsigned long long* __restrict__ agg, unsigned long long* __restrict__ incl,
     unsigned long long* __restrict__ hlast) {
-  constexpr int KP = 1;
+  constexpr int KP = 1;  // predecessors per wave per look-back round
   using XS = RowStash<TX>;
   __shared__ float s_agg[W][20][kCB];
   __shared__ float s_carry[W][4][kCB];
@@ -1302,7 +1304,7 @@ static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, 
     } else {
       PRNN_SHAPE(20, 4, 2)
       PRNN_SHAPE(16, 4, 2)
-      PRNN_SHAPE(24, 4, 1)
+      PRNN_SHAPE(24, 4, 2)
       PRNN_SHAPE(16, 8, 2)
     }
 #undef PRNN_SHAPE
