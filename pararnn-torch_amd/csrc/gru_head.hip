@@ -627,7 +627,7 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
 // transposed, and the carry kernel run from the last chunk down.
 //
 //  gru_phi_kernel<BWD>   Phi_c^T and the fp32 gates z, r, n of every step;
-//  gru_rev_kernel LOCAL  per chunk, nu from a zero carry -> e_c;
+//  gru_rev_local_kernel  per chunk, nu from a zero carry -> e_c;
 //  gru_carry_kernel<REV> nu entering each chunk from the right;
 //  gru_rev_kernel        per chunk from its carry: mu_t, the pre-activation
 //                        gradients (g_wx) and, for chunk 0, grad h0 = nu_0;
@@ -645,16 +645,17 @@ __device__ __forceinline__ void load_row(const TX* A, int head, int i, float row
   for (int o = 0; o < DH; ++o) row[o] = ld(p + o);
 }
 
-// Reverse walk of one chunk per wave; lane i keeps row i of A_z, A_r, A_n.
+// Reverse walk of one chunk per wave from its carry; lane i keeps row i of
+// A_z, A_r, A_n.
 // Per step: mu = g + nu;  d_zpre = mu (n - h) z(1-z);  d_npre = mu z (1-n^2);
 // d_u = A_n d_npre;  d_rpre = d_u h r(1-r);
 // nu <- (1-z) mu + A_z d_zpre + r d_u + A_r d_rpre.
-template <typename TX, bool LOCAL>
+template <typename TX>
 __global__ __launch_bounds__(256) void gru_rev_kernel(
     const TX* __restrict__ a_z, const TX* __restrict__ a_r, const TX* __restrict__ a_n,
     const TX* __restrict__ h0, const TX* __restrict__ states, const TX* __restrict__ grad,
     const float* __restrict__ gates, const float* __restrict__ carry_in, TX* __restrict__ g_wx,
-    float* __restrict__ e_out, float* __restrict__ g_h0, int B, int T, int H, int n_chunks) {
+    float* __restrict__ g_h0, int B, int T, int H, int n_chunks) {
   __shared__ float s_v[4][3][DH];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int task = blockIdx.x * 4 + wave;
@@ -671,7 +672,7 @@ __global__ __launch_bounds__(256) void gru_rev_kernel(
   load_row(a_z, head, lane, az);
   load_row(a_r, head, lane, ar);
   load_row(a_n, head, lane, an);
-  float nu = LOCAL ? 0.f : carry_in[static_cast<size_t>(task) * DH + lane];
+  float nu = carry_in[static_cast<size_t>(task) * DH + lane];
 
   struct In {
     float hp, g, z, r, n;
@@ -709,7 +710,7 @@ __global__ __launch_bounds__(256) void gru_rev_kernel(
     __builtin_amdgcn_wave_barrier();
     const float t_r = vec_col(s_c, ar);
     nu = (1.f - cur.z) * mu + t_z + cur.r * d_u + t_r;
-    if (!LOCAL) {
+    {
       const int t = t0 + s;
       st(g_wx + wx_at(b, t, T, d, 0, head, lane), d_zpre);
       st(g_wx + wx_at(b, t, T, d, 1, head, lane), d_rpre);
@@ -719,10 +720,99 @@ __global__ __launch_bounds__(256) void gru_rev_kernel(
     cur = nx1;
     nx1 = nx2;
   }
-  if (LOCAL)
-    e_out[static_cast<size_t>(task) * DH + lane] = nu;
-  else if (c == 0 && g_h0 != nullptr)
+  if (c == 0 && g_h0 != nullptr)
     g_h0[static_cast<size_t>(b) * d + head * DH + lane] = nu;
+}
+
+// Local reverse walk: nu from a zero carry over each chunk, two consecutive
+// chunks of a sequence per wave side by side (lane i keeps row i of A_z, A_r,
+// A_n); the chunk's final nu is its local solution e.
+template <typename TX>
+__global__ __launch_bounds__(256) void gru_rev_local_kernel(
+    const TX* __restrict__ a_z, const TX* __restrict__ a_r, const TX* __restrict__ a_n,
+    const TX* __restrict__ h0, const TX* __restrict__ states, const TX* __restrict__ grad,
+    const float* __restrict__ gates, float* __restrict__ e_out, int B, int T, int H,
+    int n_chunks) {
+  constexpr int NP = kPair;
+  __shared__ float s_v[4][NP][3][DH];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n_pairs = (n_chunks + NP - 1) / NP;
+  const int task = blockIdx.x * 4 + wave;
+  if (task >= B * H * n_pairs) return;  // whole wave exits together
+  const int d = H * DH;
+  const int seq = task / n_pairs, c0 = (task % n_pairs) * NP;
+  const int b = seq / H, head = seq % H;
+  float az[DH], ar[DH], an[DH];
+  load_row(a_z, head, lane, az);
+  load_row(a_r, head, lane, ar);
+  load_row(a_n, head, lane, an);
+
+  struct In {
+    float hp, g, z, r, n;
+  };
+  int t0[NP], len[NP];
+  float nu[NP];
+  const float* gt[NP];
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {
+    const int c = c0 + k;
+    const bool valid = c < n_chunks;
+    t0[k] = c * kChunk;
+    len[k] = valid ? min(kChunk, T - t0[k]) : 0;
+    const size_t id = static_cast<size_t>(seq) * n_chunks + (valid ? c : c0);
+    nu[k] = 0.f;
+    gt[k] = gates + id * kChunk * 3 * DH + lane;
+  }
+  // Steps past a chunk's end read zeros, and a zero step leaves nu unchanged.
+  auto load_in = [&](int k, int s) {
+    In v{0.f, 0.f, 0.f, 0.f, 0.f};
+    if (s < len[k]) {
+      const int t = t0[k] + s;
+      if (t > 0)
+        v.hp = ld(states + h_at(b, t - 1, T, d, head, lane));
+      else if (h0 != nullptr)
+        v.hp = ld(h0 + static_cast<size_t>(b) * d + head * DH + lane);
+      v.g = ld(grad + h_at(b, t, T, d, head, lane));
+      v.z = gt[k][(s * 3) * DH];
+      v.r = gt[k][(s * 3 + 1) * DH];
+      v.n = gt[k][(s * 3 + 2) * DH];
+    }
+    return v;
+  };
+  // Chunk 0 of the pair is the longest (only a sequence's last chunk is short).
+  for (int s = len[0] - 1; s >= 0; --s) {
+    In cur[NP];
+#pragma unroll
+    for (int k = 0; k < NP; ++k) cur[k] = load_in(k, s);
+    float mu[NP], d_zpre[NP], d_npre[NP], d_u[NP], t_z[NP], d_rpre[NP];
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+      const In& v = cur[k];
+      mu[k] = v.g + nu[k];
+      d_zpre[k] = mu[k] * (v.n - v.hp) * (v.z * (1.f - v.z));
+      d_npre[k] = mu[k] * v.z * (1.f - v.n * v.n);
+      s_v[wave][k][0][lane] = d_zpre[k];
+      s_v[wave][k][1][lane] = d_npre[k];
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+      t_z[k] = vec_col(s_v[wave][k][0], az);
+      d_u[k] = vec_col(s_v[wave][k][1], an);
+      d_rpre[k] = d_u[k] * cur[k].hp * cur[k].r * (1.f - cur[k].r);
+      s_v[wave][k][2][lane] = d_rpre[k];
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+      const float t_r = vec_col(s_v[wave][k][2], ar);
+      nu[k] = (1.f - cur[k].z) * mu[k] + t_z[k] + cur[k].r * d_u[k] + t_r;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+#pragma unroll
+  for (int k = 0; k < NP; ++k)
+    if (len[k] > 0) e_out[(static_cast<size_t>(seq) * n_chunks + c0 + k) * DH + lane] = nu[k];
 }
 
 // Partial sums of g_A[gate][head][i][o] = sum over rows k = (b, t) of
@@ -949,18 +1039,18 @@ static int run_bwd(const TX* wx, const TX* az, const TX* ar, const TX* an, const
                    const TX* states, const TX* grad, TX* g_wx, float* g_a, float* g_h0, int B,
                    int T, int H, const BwdWs& w, hipStream_t stream) {
   const int n_seq = B * H, n_chunks = (T + kChunk - 1) / kChunk;
+  const int rev_blocks_local = (n_seq * ((n_chunks + kPair - 1) / kPair) + 3) / 4;
   const int rev_blocks = (n_seq * n_chunks + 3) / 4;
   gru_phi_kernel<TX, TX, true><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
       wx, az, ar, an, h0, states, B, T, H, n_chunks, w.phi, w.gates);
   PRNN_HIP(hipGetLastError());
-  gru_rev_kernel<TX, true><<<dim3(rev_blocks), dim3(256), 0, stream>>>(
-      az, ar, an, h0, states, grad, w.gates, nullptr, static_cast<TX*>(nullptr), w.e, nullptr, B,
-      T, H, n_chunks);
+  gru_rev_local_kernel<TX><<<dim3(rev_blocks_local), dim3(256), 0, stream>>>(
+      az, ar, an, h0, states, grad, w.gates, w.e, B, T, H, n_chunks);
   PRNN_HIP(hipGetLastError());
   gru_carry_kernel<true><<<dim3(n_seq), dim3(64 * kCarryParts), 0, stream>>>(w.phi, w.e, n_chunks, w.carry);
   PRNN_HIP(hipGetLastError());
-  gru_rev_kernel<TX, false><<<dim3(rev_blocks), dim3(256), 0, stream>>>(
-      az, ar, an, h0, states, grad, w.gates, w.carry, g_wx, nullptr, h0 != nullptr ? g_h0 : nullptr,
+  gru_rev_kernel<TX><<<dim3(rev_blocks), dim3(256), 0, stream>>>(
+      az, ar, an, h0, states, grad, w.gates, w.carry, g_wx, h0 != nullptr ? g_h0 : nullptr,
       B, T, H, n_chunks);
   PRNN_HIP(hipGetLastError());
   gru_ga_kernel<TX><<<dim3(w.n_split * H), dim3(256), 0, stream>>>(
