@@ -15,8 +15,10 @@
 //                     accumulation);
 //  gru_replay_kernel  LOCAL: per chunk, the exact fp32 recurrence from a zero
 //                     carry, giving the chunk's local solution e;
-//  gru_carry_kernel   per sequence: carry_c = Phi_c carry_{c-1} + e_c over the
-//                     chunks, serially (one 64x64 mat-vec per chunk, fp32);
+//  carry scan         carry_{c+1} = Phi_c carry_c + e_c over the chunks, fp32:
+//                     group transfers (gru_group_kernel, fp32 MFMA) in
+//                     parallel, a serial walk over the groups, then every
+//                     group re-walked from its carry (gru_carry_kernel);
 //  gru_replay_kernel  per chunk: the exact fp32 recurrence from the chunk's
 //                     carry with the factorised J v (three 64-wide mat-vecs),
 //                     then H += omega delta.
@@ -442,6 +444,96 @@ __device__ __forceinline__ float row_sum16(float v) {
 }
 
 // ---------------------------------------------------------------------------
+// Group transfers for the two-level carry scan.  Block (seq, g) composes the
+// matrices of walk steps [g group, (g + 1) group) (chunks ascending, or
+// descending for REV):  Psi = S_last ... S_first  (S the stored chunk matrix,
+// Phi or Phi^T) as fp32 MFMA products, and the group's carry-out from a zero
+// carry,  ell <- S ell + e  (from the same LDS tile, 4 lanes per row).
+// 4 waves; wave w owns the output columns 16 w .. 16 w + 15 of each product.
+// ---------------------------------------------------------------------------
+constexpr int kGroup = 16;    // chunks per group of the two-level carry scan
+constexpr int kSPad = DH + 4;  // LDS row stride of S (A operand, bank spread)
+constexpr int kMPad = DH + 16;  // LDS row stride of M (B operand, bank spread)
+
+template <bool REV>
+__global__ __launch_bounds__(256) void gru_group_kernel(const float* __restrict__ phi,
+                                                       const float* __restrict__ e, int n_chunks,
+                                                       float* __restrict__ psi,
+                                                       float* __restrict__ ell) {
+  __shared__ float sS[DH][kSPad];
+  __shared__ float sM[DH][kMPad];
+  __shared__ float sL[2][DH];
+  const int n_groups = (n_chunks + kGroup - 1) / kGroup;
+  const int seq = blockIdx.x / n_groups, grp = blockIdx.x % n_groups;
+  const int w_begin = grp * kGroup, w_end = min(n_chunks, w_begin + kGroup);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = lane & 15, g = lane >> 4;
+  const float* P = phi + static_cast<size_t>(seq) * n_chunks * DH * DH;
+  const float* E = e + static_cast<size_t>(seq) * n_chunks * DH;
+  auto chunk_of = [&](int w) { return REV ? n_chunks - 1 - w : w; };
+  // thread t stages elements 4 t .. 4 t + 3 of rows r = (t / 16) + 16 q
+  const int r0 = threadIdx.x / 16, c4 = 4 * (threadIdx.x % 16);
+  float4 nxt[4];
+  auto fetch = [&](int w) {
+    const float* src = P + static_cast<size_t>(chunk_of(min(w, w_end - 1))) * DH * DH;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) nxt[q] = *reinterpret_cast<const float4*>(src + (r0 + 16 * q) * DH + c4);
+  };
+  auto stage = [&](float (*dst)[kSPad]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) *reinterpret_cast<float4*>(&dst[r0 + 16 * q][c4]) = nxt[q];
+  };
+  // M = S_first, ell = e_first
+  fetch(w_begin);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) *reinterpret_cast<float4*>(&sM[r0 + 16 * q][c4]) = nxt[q];
+  if (threadIdx.x < DH) sL[0][threadIdx.x] = E[static_cast<size_t>(chunk_of(w_begin)) * DH + threadIdx.x];
+  int cur = 0;
+  floatx4 acc[4];
+  for (int w = w_begin + 1; w < w_end; ++w) {
+    fetch(w);
+    __syncthreads();  // the previous product's reads of sS / sM are done
+    stage(sS);
+    __syncthreads();
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) acc[rt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < DH / 4; ++ks) {
+      const float b = sM[4 * ks + g][16 * wave + li];
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) acc[rt] = mfma_f32(sS[16 * rt + li][4 * ks + g], b, acc[rt]);
+    }
+    {
+      // ell <- S ell + e: row 16 wave + lane / 4, quarter lane % 4 of its terms
+      const int row = 16 * wave + (lane >> 2), q0 = 16 * (lane & 3);
+      float v = 0.f;
+#pragma unroll
+      for (int k = 0; k < 16; k += 4) {
+        const float4 s4 = *reinterpret_cast<const float4*>(&sS[row][q0 + k]);
+        const float4 l4 = *reinterpret_cast<const float4*>(&sL[cur][q0 + k]);
+        v += s4.x * l4.x + s4.y * l4.y + s4.z * l4.z + s4.w * l4.w;
+      }
+      v += dpp_f<0xB1>(v);  // quad_perm [1,0,3,2]
+      v += dpp_f<0x4E>(v);  // quad_perm [2,3,0,1]
+      if ((lane & 3) == 0) sL[cur ^ 1][row] = v + E[static_cast<size_t>(chunk_of(w)) * DH + row];
+    }
+    cur ^= 1;
+    __syncthreads();  // every read of sM is done
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sM[16 * rt + 4 * g + v][16 * wave + li] = acc[rt][v];
+  }
+  __syncthreads();
+  float* out = psi + static_cast<size_t>(blockIdx.x) * DH * DH;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    *reinterpret_cast<float4*>(out + (r0 + 16 * q) * DH + c4) =
+        *reinterpret_cast<const float4*>(&sM[r0 + 16 * q][c4]);
+  if (threadIdx.x < DH) ell[static_cast<size_t>(blockIdx.x) * DH + threadIdx.x] = sL[cur][threadIdx.x];
+}
+
+// ---------------------------------------------------------------------------
 // Carries over chunks: carry_0 = 0, carry_{c+1} = Phi_c carry_c + e_c.
 // REV (eq. 2.6 backward, phi holding Phi^T): chunks from the last one down,
 // carry_{n-1} = 0, carry_{c-1} = Phi_c^T carry_c + e_c.
@@ -450,26 +542,32 @@ __device__ __forceinline__ float row_sum16(float v) {
 // ---------------------------------------------------------------------------
 template <bool REV>
 __global__ __launch_bounds__(64 * kCarryParts) void gru_carry_kernel(
-    const float* __restrict__ phi, const float* __restrict__ e, int n_chunks,
-    float* __restrict__ carry_in) {
+    const float* __restrict__ phi, const float* __restrict__ e, int n_chunks, int group,
+    const float* __restrict__ init, float* __restrict__ carry_in) {
   // The chain is serial over chunks, so each step costs the latency of its
   // 16 KB of Phi and its e.  Thread (i, part) holds 4 entries of row i; the
   // chunks are fetched a block of kB ahead into one of two register blocks
   // (written out by hand, no dynamic register indexing) while the other block
   // is walked, and a block's carries are stored after its kB steps.
+  // Block (seq, g) walks steps [g group, (g + 1) group) of the walk order
+  // (chunks ascending, or descending for REV) from init[seq, g] (zeros when
+  // init is NULL).
   static_assert(DH / kCarryParts == 4, "one float4 of a Phi row per thread");
   constexpr int kB = 8;
   __shared__ float s_c[2][DH];
-  const int seq = blockIdx.x;
+  const int n_groups = (n_chunks + group - 1) / group;
+  const int seq = blockIdx.x / n_groups, grp = blockIdx.x % n_groups;
+  const int w_begin = grp * group, w_end = min(n_chunks, w_begin + group);
   const int i = threadIdx.x / kCarryParts, part = threadIdx.x % kCarryParts;
-  if (threadIdx.x < DH) s_c[0][threadIdx.x] = 0.f;
+  if (threadIdx.x < DH)
+    s_c[0][threadIdx.x] = init != nullptr ? init[static_cast<size_t>(blockIdx.x) * DH + threadIdx.x] : 0.f;
   __syncthreads();
   const float* P = phi + static_cast<size_t>(seq) * n_chunks * DH * DH;
   const float* E = e + static_cast<size_t>(seq) * n_chunks * DH;
-  // Steps past the last chunk re-read the last chunk (no branch around the
+  // Steps past the group's end re-read its last chunk (no branch around the
   // loads) and write nothing.
   auto chunk_of = [&](int step) {
-    const int k = min(step, n_chunks - 1);
+    const int k = min(step, w_end - 1);
     return REV ? n_chunks - 1 - k : k;
   };
   auto fetch = [&](int step0, float4 rows[kB], float ev[kB]) {
@@ -496,14 +594,14 @@ __global__ __launch_bounds__(64 * kCarryParts) void gru_carry_kernel(
     if (part == kCarryParts - 1) {
 #pragma unroll
       for (int k = 0; k < kB; ++k)
-        if (step0 + k < n_chunks)
+        if (step0 + k < w_end)
           carry_in[(static_cast<size_t>(seq) * n_chunks + chunk_of(step0 + k)) * DH + i] = out[k];
     }
   };
   float4 ra[kB], rb[kB];
   float ea[kB], eb[kB];
-  fetch(0, ra, ea);
-  for (int step0 = 0; step0 < n_chunks; step0 += 2 * kB) {
+  fetch(w_begin, ra, ea);
+  for (int step0 = w_begin; step0 < w_end; step0 += 2 * kB) {
     fetch(step0 + kB, rb, eb);
     walk(step0, ra, ea);
     fetch(step0 + 2 * kB, ra, ea);
@@ -935,12 +1033,52 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(const float* A, const f
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+// Two-level carry scan: group transfers Psi, group carry-outs ell and the
+// carries entering each group.
+struct CarryWs {
+  float* psi;
+  float* ell;
+  float* cg;
+};
+
+static CarryWs carve_carry(Carver& cv, int n_seq, int n_chunks) {
+  const size_t ng = static_cast<size_t>(n_seq) * ((n_chunks + kGroup - 1) / kGroup);
+  CarryWs c;
+  c.psi = static_cast<float*>(cv.take(sizeof(float) * ng * DH * DH));
+  c.ell = static_cast<float*>(cv.take(sizeof(float) * ng * DH));
+  c.cg = static_cast<float*>(cv.take(sizeof(float) * ng * DH));
+  return c;
+}
+
+// carry[c] = the carry entering chunk c of every sequence, from the stored
+// chunk matrices (Phi, or Phi^T walked from the last chunk down for REV) and
+// the local solutions e.  More than one group: group transfers in parallel,
+// a serial walk over the groups, then every group re-walked from its carry.
+template <bool REV>
+static void carry_scan(const float* phi, const float* e, float* carry, int n_seq, int n_chunks,
+                       const CarryWs& c, hipStream_t stream) {
+  const int n_groups = (n_chunks + kGroup - 1) / kGroup;
+  const dim3 walk_block(64 * kCarryParts);
+  if (n_groups <= 1) {
+    gru_carry_kernel<REV><<<dim3(n_seq), walk_block, 0, stream>>>(phi, e, n_chunks, n_chunks,
+                                                                  nullptr, carry);
+    return;
+  }
+  gru_group_kernel<REV><<<dim3(n_seq * n_groups), dim3(256), 0, stream>>>(phi, e, n_chunks, c.psi,
+                                                                         c.ell);
+  gru_carry_kernel<false><<<dim3(n_seq), walk_block, 0, stream>>>(c.psi, c.ell, n_groups,
+                                                                  n_groups, nullptr, c.cg);
+  gru_carry_kernel<REV><<<dim3(n_seq * n_groups), walk_block, 0, stream>>>(phi, e, n_chunks,
+                                                                           kGroup, c.cg, carry);
+}
+
 struct Ws {
   float* phi;
   float* e;
   float* carry;
   float* gates;
   float* work[2];
+  CarryWs cs;
 };
 
 static Ws carve(void* base, int B, int T, int H, int K, size_t* total) {
@@ -952,6 +1090,7 @@ static Ws carve(void* base, int B, int T, int H, int K, size_t* total) {
   w.carry = static_cast<float*>(cv.take(sizeof(float) * static_cast<size_t>(n_seq) * n_chunks * DH));
   w.gates = static_cast<float*>(
       cv.take(sizeof(float) * static_cast<size_t>(n_seq) * n_chunks * kChunk * 3 * DH));
+  w.cs = carve_carry(cv, n_seq, n_chunks);
   const size_t hb = sizeof(float) * static_cast<size_t>(B) * T * H * DH;
   w.work[0] = K >= 1 ? static_cast<float*>(cv.take(hb)) : nullptr;
   w.work[1] = K >= 2 ? static_cast<float*>(cv.take(hb)) : nullptr;
@@ -983,7 +1122,7 @@ static int run(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX*
         az, ar, an, h0, hin, w.gates, nullptr, static_cast<float*>(nullptr), w.e, B, T, H,
         n_chunks, omega);
     PRNN_HIP(hipGetLastError());
-    gru_carry_kernel<false><<<dim3(n_seq), dim3(64 * kCarryParts), 0, stream>>>(w.phi, w.e, n_chunks, w.carry);
+    carry_scan<false>(w.phi, w.e, w.carry, n_seq, n_chunks, w.cs, stream);
     PRNN_HIP(hipGetLastError());
     if (k == K) {
       gru_replay_kernel<TX, TX, false><<<dim3(replay_blocks), dim3(256), 0, stream>>>(
@@ -1006,6 +1145,7 @@ struct BwdWs {
   float* gates;
   float* part;
   int n_split, rows_per;
+  CarryWs cs;
 };
 
 static void ga_split(int B, int T, int H, int* n_split, int* rows_per) {
@@ -1030,6 +1170,7 @@ static BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   w.gates = static_cast<float*>(cv.take(sizeof(float) * tasks * kChunk * 3 * DH));
   ga_split(B, T, H, &w.n_split, &w.rows_per);
   w.part = static_cast<float*>(cv.take(sizeof(float) * static_cast<size_t>(w.n_split) * 3 * H * DH * DH));
+  w.cs = carve_carry(cv, n_seq, n_chunks);
   *total = cv.used;
   return w;
 }
@@ -1047,7 +1188,7 @@ static int run_bwd(const TX* wx, const TX* az, const TX* ar, const TX* an, const
   gru_rev_local_kernel<TX><<<dim3(rev_blocks_local), dim3(256), 0, stream>>>(
       az, ar, an, h0, states, grad, w.gates, w.e, B, T, H, n_chunks);
   PRNN_HIP(hipGetLastError());
-  gru_carry_kernel<true><<<dim3(n_seq), dim3(64 * kCarryParts), 0, stream>>>(w.phi, w.e, n_chunks, w.carry);
+  carry_scan<true>(w.phi, w.e, w.carry, n_seq, n_chunks, w.cs, stream);
   PRNN_HIP(hipGetLastError());
   gru_rev_kernel<TX><<<dim3(rev_blocks), dim3(256), 0, stream>>>(
       az, ar, an, h0, states, grad, w.gates, w.carry, g_wx, h0 != nullptr ? g_h0 : nullptr,
