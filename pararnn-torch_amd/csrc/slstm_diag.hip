@@ -388,7 +388,11 @@ slstm_picard_fused_kernel(
   }
   const rsrc_t ro = make_rsrc(out + first * row4 + c0, span4);
 
-  for (int p = 0; p <= P; ++p) {
+  // Stage P, which writes the state, is compiled separately from the others
+  // (no per-step branch between storing the state and keeping h).
+  auto stage = [&](const int p, auto last_c) __attribute__((always_inline)) {
+    constexpr bool last_stage = decltype(last_c)::value;
+    const bool first_stage = p == 0;
     const int tag = p + 1;
     // Keep wx packed across stages: without this the compiler hoists the
     // bf16 unpacking out of the stage loop and holds 4 floats per step.
@@ -396,7 +400,7 @@ slstm_picard_fused_kernel(
     for (int s = 0; s < L; ++s) asm volatile("" : "+v"(xw[s][0]), "+v"(xw[s][1]));
     // h_{p-1} at t0 - 1.
     float hp0 = 0.f;
-    if (p > 0) {
+    if (!first_stage) {
       if (t0 == 0) {
         hp0 = h0h;
       } else if (wave > 0) {
@@ -419,7 +423,7 @@ slstm_picard_fused_kernel(
     // Pass 1: this stage's pre-activations and the segment aggregate.
     FG a = fg_identity();
     auto step1 = [&](int s) {
-      if (p == 0) {
+      if (first_stage) {
         pre[s][0] = xw[s][0];
         pre[s][1] = xw[s][1];
       } else {
@@ -499,13 +503,12 @@ slstm_picard_fused_kernel(
     // last stage writes the state.
     float m = s_carry[wave][0][lane], n = s_carry[wave][1][lane], c = s_carry[wave][2][lane];
     float h_even = 0.f, h_last = 0.f;
-    const bool last_stage = p == P;
     auto step2 = [&](int s) {
       const float zi = lo_bf16(pre[s][0]), zf = hi_bf16(pre[s][0]);
       const float zz = lo_bf16(pre[s][1]), zo = hi_bf16(pre[s][1]);
       fg_step(zi, zf, zz, m, n, c);
       const float h = c * frcp((1.f + fexp(-zo)) * (n + eps));
-      if (last_stage) {
+      if constexpr (last_stage) {
         const uint32_t so = s * row4 * SZ;
         stb<bf16>(ro, voff, so, c);
         stb<bf16>(ro, voff, so + slot, n);
@@ -528,13 +531,15 @@ slstm_picard_fused_kernel(
       for (int s = 0; s < L; ++s)
         if (s < n_steps) step2(s);
     }
-    if (!last_stage) {
+    if constexpr (!last_stage) {
       s_hl[wave][lane] = h_last;
       if (wave == W - 1)
         st_tagged(hlast + p * stage_h + static_cast<size_t>(tile) * kCB + lane, h_last, tag);
     }
     __syncthreads();
-  }
+  };
+  for (int p = 0; p < P; ++p) stage(p, std::false_type{});
+  stage(P, std::true_type{});
 }
 
 // ---------------------------------------------------------------------------
@@ -809,7 +814,7 @@ slstm_newton_fused_kernel(
 
   // Iterations 1 .. K-1 keep the new iterate in registers; the last one,
   // compiled separately, writes it (no per-step branch on the iteration).
-  auto iterate = [&](const int k, auto last_c) {
+  auto iterate = [&](const int k, auto last_c) __attribute__((always_inline)) {
     constexpr bool last_iter = decltype(last_c)::value;
     const int tag = k + 1;
     // Keep wx packed across iterations (otherwise the unpacking is hoisted out
