@@ -117,6 +117,7 @@ def test_bf16_matches_fused_semantics():
 
 @pytest.mark.parametrize("B,T,d,K,P", [
     (1, 1, 1, 1, 0), (1, 70, 5, 0, 2), (3, 129, 70, 3, 1), (2, 64, 64, 1, 0), (1, 1000, 130, 4, 3),
+    (2, 1, 3, 2, 1), (2, 45, 70, 2, 5),
 ])
 def test_ragged_shapes_vs_oracle(B, T, d, K, P):
     from pararnn_amd import newton_apply
@@ -272,3 +273,25 @@ def test_full_size_cfg2_fp32_channel_slice_converges():
           flush=True)
     assert max(res) < 1e-3
     assert torch.all(d_abs <= 1e-4 * (1 + ref.abs()))
+
+
+@pytest.mark.parametrize("B,T,d,K,P", [(2, 1, 3, 2, 1), (3, 200, 70, 2, 3), (1, 777, 130, 3, 5)])
+def test_bf16_ragged_shapes_vs_fused_semantics(B, T, d, K, P):
+    """bf16 storage through the single-launch K >= 2 path at partial tiles, d not
+    a multiple of 64 and T = 1, against the oracle's fused-op semantics."""
+    from pararnn_amd import ParaSLSTM, newton_apply
+
+    print(f"case bf16 ragged B={B} T={T} d={d} K={K} P={P}", flush=True)
+    torch.manual_seed(B * 1000 + T + d + 7)
+    cell = ParaSLSTM(7, d).to(torch.bfloat16)
+    x = torch.randn(B, T, 7).to(torch.bfloat16)
+    h0 = torch.randn(B, 4, d) * 0.5
+    h0[:, 1] = h0[:, 1].abs() + 0.5
+    h0 = h0.to(torch.bfloat16)
+    p = O.SLSTMParams(cell.W_x.weight.detach(), cell.W_x.bias.detach(), cell.R.detach())
+    with torch.no_grad():
+        ref = O.slstm_newton(p, x, max_iters=K, picard_iters=P, h0=h0, work="fused")
+        out = newton_apply(cell.to(DEV), x.to(DEV), _cfg(K, P), h0=h0.to(DEV)).cpu()
+    err = ((out.float() - ref.float()).norm() / ref.float().norm()).item()
+    print(f"  norm-rel vs fused semantics {err:.2e}", flush=True)
+    assert err <= 2e-2
