@@ -6,9 +6,10 @@ x ~ N(0, 0.5) seeded, default seeded init.  A step is one solve on one batch
 with ``wx = W_x(x)`` already resident in HBM: the zero-hidden pass, P Picard
 passes and K Newton iterations (8 kernel launches plus two status clears).
 The W_x GEMM and the end-to-end ``newton_apply`` (GEMM + solve) are timed
-separately and reported as extra fields, as are BASELINE config 5 (one
-training step: forward solve + eq. 2.6 backward, ``train_cfg5``) and config 4
-(head GRU forward, backward and training step, ``head_cfg4``).
+separately and reported as extra fields, as are BASELINE config 2 (the same
+step at B=8, T=16384, ``slstm_cfg2``), config 5 (one training step: forward
+solve + eq. 2.6 backward, ``train_cfg5``) and config 4 (head GRU forward,
+backward and training step, ``head_cfg4``).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 Prints one JSON line.
@@ -122,6 +123,36 @@ def train_cfg5(torch, reps: int):
         "bwd_kernel_ms": ms_bwd,
         "bwd_kernel_GBps": ach,
         "bwd_kernel_frac": ach / HBM_PEAK_GBS,
+    }
+
+
+def slstm_cfg2(torch, reps: int):
+    """ParaSLSTM diag d=1024, B=8, T=16384, bf16, K=2, P=5,
+    x ~ N(0, 1): the same step as the metric (warm start + Newton on resident
+    wx) and end-to-end newton_apply (GEMM included)."""
+    from pararnn_amd import NewtonConfig, ParaSLSTM, fused_newton, newton_apply
+
+    b2, t2 = 8, 16384
+    torch.manual_seed(0)
+    cell = ParaSLSTM(D, D).to("cuda:0", torch.bfloat16)
+    g = torch.Generator(device="cuda:0").manual_seed(1)
+    x = torch.randn(b2, t2, D, generator=g, device="cuda:0").to(torch.bfloat16)
+    cfg = NewtonConfig(max_iters=K, picard_iters=P, residual_atol=None, residual_fail=None,
+                       picard_adapt=False)
+    with torch.no_grad():
+        wx = cell.W_x(x)
+        ms = _time(torch, lambda: fused_newton(cell, wx, max_iters=K, omega=1.0, h0=None,
+                                               picard_iters=P), reps)
+        ms_e2e = _time(torch, lambda: newton_apply(cell, x, cfg), reps)
+    tokens = b2 * t2
+    step_bytes = tokens * D * ((4 * 2 + 16) + P * (4 * 2 + 20) + K * (4 * 2 + 32))
+    return {
+        "workload": "ParaSLSTM diag d=1024 B=8 T=16384 bf16 K=2 P=5, wx resident",
+        "ms_per_step": ms,
+        "tokens_per_s": tokens / (ms * 1e-3),
+        "step_roofline_frac": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "newton_apply_ms": ms_e2e,
+        "newton_apply_tokens_per_s": tokens / (ms_e2e * 1e-3),
     }
 
 
@@ -317,6 +348,7 @@ def main() -> int:
         "newton_apply_tokens_per_s": tokens / (ms_e2e * 1e-3),
         "wall_s_timed_region": t_wall,
     }
+    out["slstm_cfg2"] = slstm_cfg2(torch, max(3, args.steps // 4))
     if not args.no_train:
         out["train_cfg5"] = train_cfg5(torch, max(3, args.steps // 4))
     if not args.no_head:
