@@ -508,12 +508,27 @@ def _eq26_vjp(cell: nn.Module, states: Tensor, x: Tensor, partial: Tensor, *,
     gy = g_wx.reshape(-1, g_wx.shape[-1])
     xx = x.reshape(-1, x.shape[-1])
     grad_x = (gy @ cell.W_x.weight).reshape(x.shape)
-    by_name.update({"W_x.weight": gy.t() @ xx, "W_x.bias": gy.sum(0)})
+    by_name.update({"W_x.weight": _weight_grad(gy, xx), "W_x.bias": gy.sum(0)})
     grads = tuple(
         by_name.get(n) if p.requires_grad else None for n, p in cell.named_parameters()
     )
     grad_h0 = None if h0 is None else g_h0.to(h0.dtype)
     return grad_x, grads, grad_h0
+
+
+def _weight_grad(gy: Tensor, xx: Tensor) -> Tensor:
+    """``gy^T xx`` over the B*T rows (the W_x gradient).  A single GEMM with a
+    K = B*T reduction leaves too few output tiles to fill the GPU, so long
+    reductions run as a batched GEMM over row blocks with fp32 partials, summed
+    and rounded once."""
+    n = int(gy.shape[0])
+    if gy.is_cuda and gy.dtype in (torch.bfloat16, torch.float16) and n >= 65536:
+        split = next((k for k in (16, 8, 4) if n % k == 0 and n // k >= 4096), 1)
+        if split > 1:
+            part = torch.bmm(gy.view(split, n // split, -1).transpose(1, 2),
+                             xx.view(split, n // split, -1), out_dtype=torch.float32)
+            return part.sum(0).to(gy.dtype)
+    return gy.t() @ xx
 
 
 def _eq26_vjp_chunked(cell: nn.Module, states: Tensor, x: Tensor, partial: Tensor, *,
