@@ -61,6 +61,19 @@ PRNN_API int prnn_abi_version(void);
 /* Message of the last failing call on this thread ("" if none). */
 PRNN_API const char* prnn_last_error(void);
 
+/* Deterministic mode, process-wide (off by default).  When on, every sLSTM
+ * look-back scan (warm start, Newton, backward) produces bit-identical
+ * results from run to run: a tile's carry is always the serial chain of
+ * published tile aggregates, however the tiles were scheduled.  Off, carries
+ * can differ in the last bits between runs (the walk may compose a different
+ * set of predecessors).  The head GRU path is deterministic either way.
+ * Replaces the reference's reliance on torch.use_deterministic_algorithms
+ * (pararnn/determinism.py:41-45, checked at determinism.py:77-113): the
+ * Python layer sets this from torch.are_deterministic_algorithms_enabled()
+ * before each launch. */
+PRNN_API void prnn_set_deterministic(int on);
+PRNN_API int prnn_deterministic(void);
+
 /* ---- ParaSLSTM mix='diag' ------------------------------------------------
  * Layouts: wx (B, T, 4d) gate blocks (i, f, z, o);  r (4, d) recurrent mix,
  * already clamped by the caller;  h0 (B, 4, d) slots (c, n, m, h) or NULL

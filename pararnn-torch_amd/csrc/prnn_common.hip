@@ -1,4 +1,7 @@
-// Library-wide pieces of the C ABI: error buffer, ABI version, word clear.
+// Library-wide pieces of the C ABI: error buffer, ABI version, word clear,
+// deterministic mode.
+#include <atomic>
+
 #include "prnn_host.h"
 
 namespace prnn {
@@ -14,6 +17,12 @@ __global__ void clear_words_kernel(int* __restrict__ p, size_t n) {
     p[i] = 0;
 }
 
+namespace {
+std::atomic<int> g_deterministic{0};
+}
+
+int deterministic() { return g_deterministic.load(std::memory_order_relaxed); }
+
 int clear_words(int* p, size_t n, hipStream_t stream) {
   if (n == 0) return PRNN_OK;
   size_t blocks = (n + 255) / 256;
@@ -25,6 +34,12 @@ int clear_words(int* p, size_t n, hipStream_t stream) {
 
 }  // namespace prnn
 
-extern "C" PRNN_API int prnn_abi_version(void) { return 4; }
+extern "C" PRNN_API int prnn_abi_version(void) { return 5; }
 
 extern "C" PRNN_API const char* prnn_last_error(void) { return prnn::last_error_buffer(); }
+
+extern "C" PRNN_API void prnn_set_deterministic(int on) {
+  prnn::g_deterministic.store(on ? 1 : 0, std::memory_order_relaxed);
+}
+
+extern "C" PRNN_API int prnn_deterministic(void) { return prnn::deterministic(); }

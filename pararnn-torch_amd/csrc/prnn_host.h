@@ -46,6 +46,9 @@ struct Carver {
   }
 };
 
+// Process-wide deterministic look-back switch (prnn_set_deterministic).
+int deterministic();
+
 // Zero `n` 32-bit words on `stream` with a kernel (no memset node, so the
 // sequence stays replay-safe under HIP graph capture).
 int clear_words(int* p, size_t n, hipStream_t stream);

@@ -76,7 +76,7 @@ __device__ __forceinline__ void cell_vjp(const float prev[4], const float x[4], 
   nu[3] = r[0] * dz[0] + r[1] * dz[1] + r[2] * dz[2] + r[3] * dz[3];
 }
 
-template <typename TX, int L, int W>
+template <typename TX, int L, int W, bool DET>
 __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
     const TX* __restrict__ states, const TX* __restrict__ grad, TX* __restrict__ gwx,
@@ -88,6 +88,7 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
   constexpr uint32_t SZ = sizeof(TX);
   __shared__ float s_agg[W][20][kCB];
   __shared__ float s_carry[W][4][kCB];
+  __shared__ float s_tagg[20][kCB];  // the published tile aggregate (wave 0's lanes)
   __shared__ LookbackShared<NewtonMonoid, W * KP> s_lb;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -199,15 +200,21 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
     unsigned long long* ap = agg + (static_cast<size_t>(tile) * 20) * kCB + lane;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      if (DET) s_tagg[16 + i][lane] = tile_agg.b[i];
       st_tagged(ap + (16 + i) * kCB, tile_agg.b[i], epoch);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) st_tagged(ap + (4 * i + j) * kCB, tile_agg.A[i][j], epoch);
+      for (int j = 0; j < 4; ++j) {
+        if (DET) s_tagg[4 * i + j][lane] = tile_agg.A[i][j];
+        st_tagged(ap + (4 * i + j) * kCB, tile_agg.A[i][j], epoch);
+      }
     }
   }
   if (id.chunk > 0)
-    windowed_lookback<NewtonMonoid, W, KP>(id, B, n_cb, epoch, incl, agg, lane, wave, s_lb,
-                                           carry);
+    windowed_lookback<NewtonMonoid, W, KP, DET>(
+          id, B, n_cb, epoch, incl, agg, lane, wave, s_lb, carry);
   if (wave == 0) {
+    // Per-wave carries; the outgoing carry is the published aggregate applied
+    // to the carry in, as a successor's walk would compute it.
 #pragma unroll
     for (int w = W - 1; w >= 0; --w) {
 #pragma unroll
@@ -215,6 +222,14 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
       Aff sw;
       wave_map(w, sw);
       aff_apply(sw, carry);
+    }
+    if (DET && id.chunk > 0) {
+      float a[20];
+#pragma unroll
+      for (int k = 0; k < 20; ++k) a[k] = s_tagg[k][lane];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) carry[k] = s_carry[W - 1][k][lane];
+      NewtonMonoid::apply(a, carry);
     }
     unsigned long long* ip = incl + (static_cast<size_t>(tile) * 4) * kCB + lane;
 #pragma unroll
@@ -317,13 +332,15 @@ namespace slstm {
 
 // Backward tiles stash H*_{t-1}, wx and g: 6 registers per step in bf16,
 // 12 in fp32.  PRNN_SLSTM_BWD_TILES="<L>x<W>" overrides the bf16 shape for
-// tuning runs (instantiated shapes only).
+// tuning runs (instantiated shapes only); deterministic mode always runs the
+// default shape.
 static const Shape kBwdShapes[] = {{24, 4}, {16, 8}, {16, 4}, {32, 4}};
+constexpr Shape kBwdDefault{24, 4};
 constexpr Shape kBwdF32{8, 8};
 
 static Shape bwd_shape(int dtype) {
   static Shape s = [] {
-    Shape r{24, 4};
+    Shape r = kBwdDefault;
     if (const char* e = getenv("PRNN_SLSTM_BWD_TILES")) {
       int l, w;
       if (sscanf(e, "%dx%d", &l, &w) == 2)
@@ -332,7 +349,8 @@ static Shape bwd_shape(int dtype) {
     }
     return r;
   }();
-  return dtype == PRNN_BF16 ? s : kBwdF32;
+  if (dtype != PRNN_BF16) return kBwdF32;
+  return deterministic() ? kBwdDefault : s;
 }
 
 struct BwdWs {
@@ -350,12 +368,12 @@ static BwdWs carve_bwd(void* base, int B, int T, int d, int dtype, size_t* total
   return w;
 }
 
-template <typename TX, int L, int W>
+template <typename TX, int L, int W, bool DET>
 static void launch_reverse(const TX* wx, const TX* r, const TX* h0, const TX* states,
                            const TX* grad, TX* gwx, float* gh0, int B, int T, int d, float eps,
                            const BwdWs& w, hipStream_t stream) {
   const Geo g = geometry(B, T, d, Shape{L, W});
-  slstm_reverse_kernel<TX, L, W><<<dim3(g.n_tiles), dim3(64 * W), 0, stream>>>(
+  slstm_reverse_kernel<TX, L, W, DET><<<dim3(g.n_tiles), dim3(64 * W), 0, stream>>>(
       wx, r, h0, states, grad, gwx, w.gr_part, gh0, B, T, d, g.n_cb, g.n_chunks, eps,
       w.lb.counters + 1, w.lb.agg, w.lb.incl, 1);
 }
@@ -368,20 +386,25 @@ static int run_bwd(const TX* wx, const TX* r, const TX* h0, const TX* states, co
   if (rc != PRNN_OK) return rc;
   Shape sh;
   if constexpr (sizeof(TX) == 4) {
+#define PRNN_LAUNCH(LL, WW, DD) \
+  launch_reverse<TX, LL, WW, DD>(wx, r, h0, states, grad, gwx, gh0, B, T, d, eps, w, stream)
     sh = kBwdF32;
-    launch_reverse<TX, kBwdF32.L, kBwdF32.W>(wx, r, h0, states, grad, gwx, gh0, B, T, d, eps, w,
-                                             stream);
+    if (deterministic())
+      PRNN_LAUNCH(kBwdF32.L, kBwdF32.W, true);
+    else
+      PRNN_LAUNCH(kBwdF32.L, kBwdF32.W, false);
   } else {
     sh = bwd_shape(PRNN_BF16);
-#define PRNN_SHAPE(LL, WW)                                                                    \
-  if (sh.L == LL && sh.W == WW)                                                               \
-    launch_reverse<TX, LL, WW>(wx, r, h0, states, grad, gwx, gh0, B, T, d, eps, w, stream);
+#define PRNN_SHAPE(LL, WW) \
+  else if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, false);
+    if (deterministic()) PRNN_LAUNCH(kBwdDefault.L, kBwdDefault.W, true);
     PRNN_SHAPE(16, 8)
     PRNN_SHAPE(16, 4)
     PRNN_SHAPE(24, 4)
     PRNN_SHAPE(32, 4)
 #undef PRNN_SHAPE
   }
+#undef PRNN_LAUNCH
   PRNN_HIP(hipGetLastError());
   const Geo g = geometry(B, T, d, sh);
   slstm_gr_reduce_kernel<<<dim3(4 * g.n_cb), dim3(64 * kReduceWaves), 0, stream>>>(

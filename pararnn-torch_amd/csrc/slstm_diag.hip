@@ -99,6 +99,9 @@ struct FrozenMonoid {
     out[1] = n;
     out[2] = c;
   }
+  static __device__ __forceinline__ void apply(const float a[NA], float v[NI]) {
+    fg_apply(FG{a[0], a[1], a[2], a[3]}, v[0], v[1], v[2]);
+  }
 };
 
 // Pre-activations of a tile's steps, held in registers between the two
@@ -156,7 +159,7 @@ struct PreStash<float> {
 // lane owns one channel; its L steps are read once (pass 1, which builds the
 // lane aggregate), kept in registers through the look-back, and replayed from
 // the true carry in pass 2, which writes the trajectory.
-template <typename TX, int L, int W, bool HAS_H, bool FULL_OUT>
+template <typename TX, int L, int W, bool HAS_H, bool FULL_OUT, bool DET>
 __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
     const TX* __restrict__ hsrc, TX* __restrict__ out_full, TX* __restrict__ out_h, int B, int T,
@@ -233,8 +236,8 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
   __syncthreads();
 
   float carry[3] = {0.f, 0.f, 0.f};  // (m, n, c) into the tile, wave 0
+  FG tile_agg = fg_identity();
   if (wave == 0) {
-    FG tile_agg = fg_identity();
 #pragma unroll
     for (int w = 0; w < W; ++w)
       tile_agg = fg_compose(
@@ -255,10 +258,11 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
     }
   }
   if (id.chunk > 0)
-    windowed_lookback<FrozenMonoid, W, KP>(id, B, n_cb, epoch, incl, agg, lane, wave, s_lb,
-                                           carry);
+    windowed_lookback<FrozenMonoid, W, KP, DET>(
+          id, B, n_cb, epoch, incl, agg, lane, wave, s_lb, carry);
   if (wave == 0) {
-    // Per-wave carries, then the tile's inclusive carry.
+    // Per-wave carries, then the tile's inclusive carry: the published
+    // aggregate applied to the carry in (what a successor's walk computes).
     float m = carry[0], n = carry[1], c = carry[2];
 #pragma unroll
     for (int w = 0; w < W; ++w) {
@@ -267,6 +271,12 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
       s_carry[w][2][lane] = c;
       fg_apply(FG{s_agg[w][0][lane], s_agg[w][1][lane], s_agg[w][2][lane], s_agg[w][3][lane]}, m,
                n, c);
+    }
+    if (DET && id.chunk > 0) {
+      m = carry[0];
+      n = carry[1];
+      c = carry[2];
+      fg_apply(tile_agg, m, n, c);
     }
     unsigned long long* ip = incl + (static_cast<size_t>(tile) * 3) * kCB + lane;
     st_tagged(ip, m, epoch);
@@ -320,7 +330,7 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
 //  * the stage-p carry: a decoupled look-back on stage-indexed tagged words.
 // Both only ever wait on tiles with earlier tickets (already resident or
 // done), so every wave reaches the end.
-template <int L, int W, int WPE>
+template <int L, int W, int WPE, bool DET>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) void
 slstm_picard_fused_kernel(
     const bf16* __restrict__ wx, const bf16* __restrict__ rmix, const bf16* __restrict__ h0,
@@ -333,6 +343,7 @@ slstm_picard_fused_kernel(
   __shared__ float s_agg[W][4][kCB];
   __shared__ float s_carry[W][3][kCB];
   __shared__ float s_hl[W][kCB];
+  __shared__ float s_tagg[4][kCB];  // the published tile aggregate (wave 0's lanes)
   __shared__ LookbackShared<FrozenMonoid, W * KP> s_lb;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -477,11 +488,17 @@ slstm_picard_fused_kernel(
         st_tagged(ap + 1 * kCB, tile_agg.M, tag);
         st_tagged(ap + 2 * kCB, tile_agg.N, tag);
         st_tagged(ap + 3 * kCB, tile_agg.C, tag);
+        if (DET) {
+          s_tagg[0][lane] = tile_agg.F;
+          s_tagg[1][lane] = tile_agg.M;
+          s_tagg[2][lane] = tile_agg.N;
+          s_tagg[3][lane] = tile_agg.C;
+        }
       }
     }
     if (id.chunk > 0)
-      windowed_lookback<FrozenMonoid, W, KP>(id, B, n_cb, tag, incl_p, agg_p, lane, wave, s_lb,
-                                             carry);
+      windowed_lookback<FrozenMonoid, W, KP, DET>(
+          id, B, n_cb, tag, incl_p, agg_p, lane, wave, s_lb, carry);
     if (wave == 0) {
       float m = carry[0], n = carry[1], c = carry[2];
 #pragma unroll
@@ -491,6 +508,12 @@ slstm_picard_fused_kernel(
         s_carry[w][2][lane] = c;
         fg_apply(FG{s_agg[w][0][lane], s_agg[w][1][lane], s_agg[w][2][lane], s_agg[w][3][lane]},
                  m, n, c);
+      }
+      if (DET && id.chunk > 0) {
+        m = carry[0];
+        n = carry[1];
+        c = carry[2];
+        fg_apply(FG{s_tagg[0][lane], s_tagg[1][lane], s_tagg[2][lane], s_tagg[3][lane]}, m, n, c);
       }
       unsigned long long* ip = incl_p + (static_cast<size_t>(tile) * 3) * kCB + lane;
       st_tagged(ip, m, tag);
@@ -550,7 +573,7 @@ slstm_picard_fused_kernel(
 // reads each step once (wx and the guess, kept in registers) and folds the
 // lane's affine aggregate x -> J x + F; pass 2 replays the steps from the true
 // carry, delta_t = J_t delta_{t-1} + F_t, and writes H + omega delta.
-template <typename TX, typename TIN, typename TOUT, int L, int W>
+template <typename TX, typename TIN, typename TOUT, int L, int W, bool DET>
 __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
     const TIN* __restrict__ hin, TOUT* __restrict__ hout, int B, int T, int d, int n_cb,
@@ -561,6 +584,7 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
   using HS = RowStash<TIN>;
   __shared__ float s_agg[W][20][kCB];
   __shared__ float s_carry[W][4][kCB];
+  __shared__ float s_tagg[20][kCB];  // the published tile aggregate (wave 0's lanes)
   __shared__ LookbackShared<NewtonMonoid, W * KP> s_lb;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -661,16 +685,22 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
     unsigned long long* ap = agg + (static_cast<size_t>(tile) * 20) * kCB + lane;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      if (DET) s_tagg[16 + i][lane] = tile_agg.b[i];
       st_tagged(ap + (16 + i) * kCB, tile_agg.b[i], epoch);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) st_tagged(ap + (4 * i + j) * kCB, tile_agg.A[i][j], epoch);
+      for (int j = 0; j < 4; ++j) {
+        if (DET) s_tagg[4 * i + j][lane] = tile_agg.A[i][j];
+        st_tagged(ap + (4 * i + j) * kCB, tile_agg.A[i][j], epoch);
+      }
     }
   }
   if (id.chunk > 0)
-    windowed_lookback<NewtonMonoid, W, KP>(id, B, n_cb, epoch, incl, agg, lane, wave, s_lb,
-                                           carry);
+    windowed_lookback<NewtonMonoid, W, KP, DET>(
+          id, B, n_cb, epoch, incl, agg, lane, wave, s_lb, carry);
   if (wave == 0) {
-    // Carry into each wave's segment, then the tile's outgoing carry.
+    // Carry into each wave's segment, then the tile's outgoing carry (the
+    // published aggregate applied to the carry in, as a successor's walk
+    // would compute it).
 #pragma unroll
     for (int w = 0; w < W; ++w) {
 #pragma unroll
@@ -683,6 +713,14 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
         for (int j = 0; j < 4; ++j) sw.A[i][j] = s_agg[w][4 * i + j][lane];
       }
       aff_apply(sw, carry);
+    }
+    if (DET && id.chunk > 0) {
+      float a[20];
+#pragma unroll
+      for (int k = 0; k < 20; ++k) a[k] = s_tagg[k][lane];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) carry[k] = s_carry[0][k][lane];
+      NewtonMonoid::apply(a, carry);
     }
     unsigned long long* ip = incl + (static_cast<size_t>(tile) * 4) * kCB + lane;
 #pragma unroll
@@ -738,7 +776,7 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
 // Both only ever wait on tiles with earlier tickets, so every wave reaches the
 // end.  The arithmetic is that of K separate launches exchanging the fp32
 // iterate through memory.
-template <typename TX, int L, int W, int WPE>
+template <typename TX, int L, int W, int WPE, bool DET>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) void
 slstm_newton_fused_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
@@ -750,6 +788,7 @@ slstm_newton_fused_kernel(
   using XS = RowStash<TX>;
   __shared__ float s_agg[W][20][kCB];
   __shared__ float s_carry[W][4][kCB];
+  __shared__ float s_tagg[20][kCB];  // the published tile aggregate (wave 0's lanes)
   __shared__ float s_hl[W][4][kCB];
   __shared__ LookbackShared<NewtonMonoid, W * KP> s_lb;
   const int lane = threadIdx.x & 63;
@@ -917,15 +956,21 @@ slstm_newton_fused_kernel(
       unsigned long long* ap = agg_k + (static_cast<size_t>(tile) * 20) * kCB + lane;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
+        if (DET) s_tagg[16 + i][lane] = tile_agg.b[i];
         st_tagged(ap + (16 + i) * kCB, tile_agg.b[i], tag);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) st_tagged(ap + (4 * i + j) * kCB, tile_agg.A[i][j], tag);
+        for (int j = 0; j < 4; ++j) {
+          if (DET) s_tagg[4 * i + j][lane] = tile_agg.A[i][j];
+          st_tagged(ap + (4 * i + j) * kCB, tile_agg.A[i][j], tag);
+        }
       }
     }
     if (id.chunk > 0)
-      windowed_lookback<NewtonMonoid, W, KP>(id, B, n_cb, tag, incl_k, agg_k, lane, wave, s_lb,
-                                             carry);
+      windowed_lookback<NewtonMonoid, W, KP, DET>(
+          id, B, n_cb, tag, incl_k, agg_k, lane, wave, s_lb, carry);
     if (wave == 0) {
+      // Per-wave carries; the outgoing carry is the published aggregate
+      // applied to the carry in, as a successor's walk would compute it.
 #pragma unroll
       for (int w = 0; w < W; ++w) {
 #pragma unroll
@@ -938,6 +983,14 @@ slstm_newton_fused_kernel(
           for (int j = 0; j < 4; ++j) sw.A[i][j] = s_agg[w][4 * i + j][lane];
         }
         aff_apply(sw, carry);
+      }
+      if (DET && id.chunk > 0) {
+        float a[20];
+#pragma unroll
+        for (int k = 0; k < 20; ++k) a[k] = s_tagg[k][lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) carry[j] = s_carry[0][j][lane];
+        NewtonMonoid::apply(a, carry);
       }
       unsigned long long* ip = incl_k + (static_cast<size_t>(tile) * 4) * kCB + lane;
 #pragma unroll
@@ -1009,12 +1062,16 @@ namespace slstm {
 
 // Tile shapes (L steps per lane x W waves).  Selected once per process;
 // PRNN_SLSTM_TILES="<frozen L>x<W>,<newton L>x<W>" overrides the default for
-// tuning runs (only the instantiated shapes are accepted).
+// tuning runs (only the instantiated shapes are accepted).  Deterministic mode
+// always runs the default shapes (the only ones instantiated for it).
 // bf16 frozen tiles stash 2 registers per step, fp32 ones 4 (one fp32 shape).
 static const Shape kFrozenShapes[] = {{64, 4}, {32, 8}, {32, 4}, {64, 2}};
+constexpr Shape kFrozenDefault{64, 4};
 constexpr Shape kFrozenF32{32, 4};
 // Newton tiles stash wx and the guess: 4 to 6 registers per step in bf16, 8 in fp32.
 static const Shape kNewtonShapes[] = {{32, 8}, {32, 4}, {24, 4}, {16, 8}, {64, 4}};
+constexpr Shape kNewtonGuessDefault{32, 4};
+constexpr Shape kNewtonWorkDefault{24, 4};
 constexpr Shape kNewtonF32{16, 8};
 
 struct Tiles {
@@ -1025,7 +1082,7 @@ struct Tiles {
 
 static Tiles tiles() {
   static Tiles t = [] {
-    Tiles r{{64, 4}, {32, 4}, {24, 4}};
+    Tiles r{kFrozenDefault, kNewtonGuessDefault, kNewtonWorkDefault};
     if (const char* e = getenv("PRNN_SLSTM_TILES")) {
       int fl, fw, gl, gw, wl, ww;
       if (sscanf(e, "%dx%d,%dx%d,%dx%d", &fl, &fw, &gl, &gw, &wl, &ww) == 6) {
@@ -1042,10 +1099,14 @@ static Tiles tiles() {
   return t;
 }
 
-static Shape frozen_shape(int dtype) { return dtype == PRNN_BF16 ? tiles().frozen : kFrozenF32; }
+static Shape frozen_shape(int dtype) {
+  if (dtype != PRNN_BF16) return kFrozenF32;
+  return deterministic() ? kFrozenDefault : tiles().frozen;
+}
 // Shape of a Newton launch; `work_in` when it reads the fp32 work trajectory.
 static Shape newton_shape(int dtype, bool work_in) {
   if (dtype != PRNN_BF16) return kNewtonF32;
+  if (deterministic()) return work_in ? kNewtonWorkDefault : kNewtonGuessDefault;
   return work_in ? tiles().newton_work : tiles().newton_guess;
 }
 
@@ -1062,10 +1123,11 @@ static bool picard_fused(int dtype) {
 // Shapes of the fused launch: wx, the stage's pre-activations and h stay in
 // registers (4.5 per step).  PRNN_SLSTM_PICARD_TILES="<L>x<W>" for tuning.
 static const Shape kPicardShapes[] = {{24, 4}, {16, 4}, {20, 4}, {32, 4}};
+constexpr Shape kPicardDefault{24, 4};
 
 static Shape picard_shape() {
   static const Shape s = [] {
-    Shape r{24, 4};
+    Shape r = kPicardDefault;
     if (const char* e = getenv("PRNN_SLSTM_PICARD_TILES")) {
       int l, w;
       if (sscanf(e, "%dx%d", &l, &w) == 2)
@@ -1074,7 +1136,7 @@ static Shape picard_shape() {
     }
     return r;
   }();
-  return s;
+  return deterministic() ? kPicardDefault : s;
 }
 
 struct InitWs {
@@ -1125,11 +1187,12 @@ static bool newton_fused(int K) {
 // and the fp32 iterate (4) stay in registers.
 // PRNN_SLSTM_NEWTON_FUSED_TILES="<L>x<W>" for tuning (bf16).
 static const Shape kNewtonFusedShapes[] = {{20, 4}, {16, 4}, {24, 4}, {16, 8}};
+constexpr Shape kNewtonFusedDefault{20, 4};
 constexpr Shape kNewtonFusedF32{16, 4};
 
 static Shape newton_fused_shape(int dtype) {
   static const Shape s = [] {
-    Shape r{20, 4};
+    Shape r = kNewtonFusedDefault;
     if (const char* e = getenv("PRNN_SLSTM_NEWTON_FUSED_TILES")) {
       int l, w;
       if (sscanf(e, "%dx%d", &l, &w) == 2)
@@ -1138,7 +1201,8 @@ static Shape newton_fused_shape(int dtype) {
     }
     return r;
   }();
-  return dtype == PRNN_BF16 ? s : kNewtonFusedF32;
+  if (dtype != PRNN_BF16) return kNewtonFusedF32;
+  return deterministic() ? kNewtonFusedDefault : s;
 }
 
 struct NewtonWs {
@@ -1178,7 +1242,7 @@ static NewtonWs carve_newton(void* base, int B, int T, int d, int K, int dtype, 
   return w;
 }
 
-template <typename TX, int L, int W>
+template <typename TX, int L, int W, bool DET>
 static void launch_frozen(bool has_h, bool full_out, const TX* wx, const TX* r, const TX* h0,
                           const TX* src, TX* out_full, TX* out_h, int B, int T, int d, float eps,
                           const Lookback& lb, int epoch, hipStream_t stream) {
@@ -1186,7 +1250,7 @@ static void launch_frozen(bool has_h, bool full_out, const TX* wx, const TX* r, 
   const dim3 grid(g.n_tiles), block(64 * W);
   int* ctr = lb.counters + epoch;
 #define PRNN_FROZEN(HH, FO)                                                                    \
-  slstm_frozen_kernel<TX, L, W, HH, FO><<<grid, block, 0, stream>>>(                           \
+  slstm_frozen_kernel<TX, L, W, HH, FO, DET><<<grid, block, 0, stream>>>(                      \
       wx, r, h0, src, out_full, out_h, B, T, d, g.n_cb, eps, ctr, lb.agg, lb.incl, epoch)
   if (has_h) {
     if (full_out) PRNN_FROZEN(true, true); else PRNN_FROZEN(true, false);
@@ -1200,22 +1264,24 @@ template <typename TX>
 static void frozen_pass(bool has_h, bool full_out, const TX* wx, const TX* r, const TX* h0,
                         const TX* src, TX* out_full, TX* out_h, int B, int T, int d, float eps,
                         const Lookback& lb, int epoch, hipStream_t stream) {
+#define PRNN_LAUNCH(LL, WW, DD)                                                              \
+  return launch_frozen<TX, LL, WW, DD>(has_h, full_out, wx, r, h0, src, out_full, out_h, B, T, \
+                                       d, eps, lb, epoch, stream)
   if constexpr (sizeof(TX) == 4) {
-    return launch_frozen<TX, kFrozenF32.L, kFrozenF32.W>(has_h, full_out, wx, r, h0, src,
-                                                         out_full, out_h, B, T, d, eps, lb,
-                                                         epoch, stream);
+    if (deterministic()) PRNN_LAUNCH(kFrozenF32.L, kFrozenF32.W, true);
+    PRNN_LAUNCH(kFrozenF32.L, kFrozenF32.W, false);
   } else {
-  const Shape sh = tiles().frozen;
-#define PRNN_SHAPE(LL, WW)                                                                   \
-  if (sh.L == LL && sh.W == WW)                                                              \
-    return launch_frozen<TX, LL, WW>(has_h, full_out, wx, r, h0, src, out_full, out_h, B, T, \
-                                     d, eps, lb, epoch, stream);
+  if (deterministic()) PRNN_LAUNCH(kFrozenDefault.L, kFrozenDefault.W, true);
+  const Shape sh = frozen_shape(PRNN_BF16);
+#define PRNN_SHAPE(LL, WW) \
+  if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, false);
   PRNN_SHAPE(64, 4)
   PRNN_SHAPE(32, 8)
   PRNN_SHAPE(32, 4)
   PRNN_SHAPE(64, 2)
 #undef PRNN_SHAPE
   }
+#undef PRNN_LAUNCH
 }
 
 template <typename TX>
@@ -1227,16 +1293,20 @@ static int run_init(const TX* wx, const TX* r, const TX* h0, TX* states, int B, 
     if (w.fused) {
       const Shape sh = picard_shape();
       const Geo g = geometry(B, T, d, sh);
-#define PRNN_SHAPE(LL, WW, WPE)                                                                 \
-  if (sh.L == LL && sh.W == WW)                                                                 \
-    slstm_picard_fused_kernel<LL, WW, WPE><<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>(      \
-        wx, r, h0, states, B, T, d, g.n_cb, g.n_tiles, P, eps, w.lb.counters + 1, w.lb.agg,     \
-        w.lb.incl, w.hlast);
+#define PRNN_LAUNCH(LL, WW, WPE, DD)                                                            \
+  slstm_picard_fused_kernel<LL, WW, WPE, DD><<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>(    \
+      wx, r, h0, states, B, T, d, g.n_cb, g.n_tiles, P, eps, w.lb.counters + 1, w.lb.agg,       \
+      w.lb.incl, w.hlast)
+#define PRNN_SHAPE(LL, WW, WPE) \
+  else if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, WPE, false);
+      static_assert(kPicardDefault.L == 24 && kPicardDefault.W == 4, "default Picard shape");
+      if (deterministic()) PRNN_LAUNCH(24, 4, 3, true);
       PRNN_SHAPE(24, 4, 3)
       PRNN_SHAPE(16, 4, 4)
       PRNN_SHAPE(20, 4, 3)
       PRNN_SHAPE(32, 4, 2)
 #undef PRNN_SHAPE
+#undef PRNN_LAUNCH
       PRNN_HIP(hipGetLastError());
       return PRNN_OK;
     }
@@ -1253,12 +1323,12 @@ static int run_init(const TX* wx, const TX* r, const TX* h0, TX* states, int B, 
   return PRNN_OK;
 }
 
-template <typename TX, typename TIN, typename TOUT, int L, int W>
+template <typename TX, typename TIN, typename TOUT, int L, int W, bool DET>
 static void launch_newton_shape(const TX* wx, const TX* r, const TX* h0, const TIN* hin,
                                 TOUT* hout, int B, int T, int d, float omega, float eps,
                                 const Lookback& lb, int epoch, hipStream_t stream) {
   const Geo g = geometry(B, T, d, Shape{L, W});
-  slstm_newton_kernel<TX, TIN, TOUT, L, W><<<dim3(g.n_tiles), dim3(64 * W), 0, stream>>>(
+  slstm_newton_kernel<TX, TIN, TOUT, L, W, DET><<<dim3(g.n_tiles), dim3(64 * W), 0, stream>>>(
       wx, r, h0, hin, hout, B, T, d, g.n_cb, omega, eps, lb.counters + epoch, lb.agg,
       lb.incl, epoch);
 }
@@ -1267,15 +1337,20 @@ template <typename TX, typename TIN, typename TOUT>
 static void launch_newton(const TX* wx, const TX* r, const TX* h0, const TIN* hin, TOUT* hout,
                           int B, int T, int d, float omega, float eps, const Lookback& lb,
                           int epoch, hipStream_t stream) {
+#define PRNN_LAUNCH(LL, WW, DD)                                                          \
+  return launch_newton_shape<TX, TIN, TOUT, LL, WW, DD>(wx, r, h0, hin, hout, B, T, d, omega, \
+                                                        eps, lb, epoch, stream)
   if constexpr (sizeof(TX) == 4) {
-    return launch_newton_shape<TX, TIN, TOUT, kNewtonF32.L, kNewtonF32.W>(
-        wx, r, h0, hin, hout, B, T, d, omega, eps, lb, epoch, stream);
+    if (deterministic()) PRNN_LAUNCH(kNewtonF32.L, kNewtonF32.W, true);
+    PRNN_LAUNCH(kNewtonF32.L, kNewtonF32.W, false);
   } else {
+  if (deterministic()) {
+    constexpr Shape dd = sizeof(TIN) == 4 ? kNewtonWorkDefault : kNewtonGuessDefault;
+    PRNN_LAUNCH(dd.L, dd.W, true);
+  }
   const Shape sh = newton_shape(PRNN_BF16, sizeof(TIN) == 4);
-#define PRNN_SHAPE(LL, WW)                                                                     \
-  if (sh.L == LL && sh.W == WW)                                                                \
-    return launch_newton_shape<TX, TIN, TOUT, LL, WW>(wx, r, h0, hin, hout, B, T, d, omega, eps, \
-                                                      lb, epoch, stream);
+#define PRNN_SHAPE(LL, WW) \
+  if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, false);
   PRNN_SHAPE(32, 8)
   PRNN_SHAPE(32, 4)
   PRNN_SHAPE(24, 4)
@@ -1283,6 +1358,7 @@ static void launch_newton(const TX* wx, const TX* r, const TX* h0, const TIN* hi
   PRNN_SHAPE(64, 4)
 #undef PRNN_SHAPE
   }
+#undef PRNN_LAUNCH
 }
 
 template <typename TX>
@@ -1299,20 +1375,26 @@ static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, 
   if (w.fused) {
     const Shape sh = newton_fused_shape(sizeof(TX) == 2 ? PRNN_BF16 : PRNN_F32);
     const Geo g = geometry(B, T, d, sh);
-#define PRNN_SHAPE(LL, WW, WPE)                                                                 \
-  if (sh.L == LL && sh.W == WW)                                                                 \
-    slstm_newton_fused_kernel<TX, LL, WW, WPE><<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>(  \
-        wx, r, h0, guess, out, B, T, d, g.n_cb, g.n_tiles, K, omega, eps, w.lb.counters + 1,    \
-        w.lb.agg, w.lb.incl, w.hlast);
+#define PRNN_LAUNCH(LL, WW, WPE, DD)                                                             \
+  slstm_newton_fused_kernel<TX, LL, WW, WPE, DD><<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>( \
+      wx, r, h0, guess, out, B, T, d, g.n_cb, g.n_tiles, K, omega, eps, w.lb.counters + 1,       \
+      w.lb.agg, w.lb.incl, w.hlast)
+#define PRNN_SHAPE(LL, WW, WPE) \
+  else if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, WPE, false);
+    static_assert(kNewtonFusedF32.L == 16 && kNewtonFusedF32.W == 4, "fp32 fused shape");
+    static_assert(kNewtonFusedDefault.L == 20 && kNewtonFusedDefault.W == 4, "default shape");
     if constexpr (sizeof(TX) == 4) {
+      if (deterministic()) PRNN_LAUNCH(16, 4, 2, true);
       PRNN_SHAPE(16, 4, 2)
     } else {
+      if (deterministic()) PRNN_LAUNCH(20, 4, 2, true);
       PRNN_SHAPE(20, 4, 2)
       PRNN_SHAPE(16, 4, 2)
       PRNN_SHAPE(24, 4, 2)
       PRNN_SHAPE(16, 8, 2)
     }
 #undef PRNN_SHAPE
+#undef PRNN_LAUNCH
     PRNN_HIP(hipGetLastError());
     return PRNN_OK;
   }

@@ -59,7 +59,20 @@ __device__ __forceinline__ int take_ticket(int* counter) {
 //
 // Monoid policy M: NI inclusive values, NA aggregate values, Acc type with
 // identity / absorb (acc <- acc o agg of an earlier tile) / finish (carry =
-// acc applied to the inclusive value of that tile).
+// acc applied to the inclusive value of that tile), and apply (one published
+// aggregate applied to a carry vector).
+//
+// Deterministic mode (DET): which predecessors a walk composes depends on
+// timing, and composing aggregates in a different grouping rounds
+// differently.  With det set, a walk only ends on an inclusive carry inside
+// the window whose nearer predecessors have all published their aggregates,
+// and applies those aggregates to it one at a time, oldest first.  Every tile
+// publishes its inclusive carry as M::apply(its published aggregate, its
+// carry), so by induction every carry equals the serial chain
+// carry_i = apply(agg_{i-1}, carry_{i-1}) bit for bit, whichever predecessor a
+// walk happened to stop at.  The price is that the walk never reaches past
+// the window: a tile waits until one of its W * KP nearest predecessors holds
+// its inclusive carry.
 // ---------------------------------------------------------------------------
 template <class M, int NW>
 struct LookbackShared {
@@ -70,7 +83,7 @@ struct LookbackShared {
 };
 
 // W waves, each fetching KP predecessors per round (window NW = W * KP).
-template <class M, int W, int KP>
+template <class M, int W, int KP, bool DET>
 __device__ __forceinline__ void windowed_lookback(const TileId& id, int B, int n_cb, int epoch,
                                                   const unsigned long long* __restrict__ incl,
                                                   const unsigned long long* __restrict__ agg,
@@ -131,7 +144,41 @@ __device__ __forceinline__ void windowed_lookback(const TileId& id, int B, int n
     __syncthreads();
     if (wave == 0) {
       bool progressed = false;
-      if (!done) {
+      if constexpr (DET) {
+        if (!done) {
+          // Nearest inclusive carry with no unpublished predecessor before it.
+          int s = -1;
+          bool gap = false;
+#pragma unroll
+          for (int w = 0; w < W * KP; ++w) {
+            const int st = sh.st[w][lane];
+            if (s < 0 && !gap) {
+              if (st == 2)
+                s = w;
+              else if (st == 0)
+                gap = true;
+            }
+          }
+          if (s >= 0) {
+            float v[M::NI];
+#pragma unroll
+            for (int k = 0; k < M::NI; ++k) v[k] = sh.pl[s][k][lane];
+#pragma unroll
+            for (int w = W * KP - 2; w >= 0; --w) {
+              if (w < s) {
+                float a[M::NA];
+#pragma unroll
+                for (int k = 0; k < M::NA; ++k) a[k] = sh.pl[w][k][lane];
+                M::apply(a, v);
+              }
+            }
+#pragma unroll
+            for (int k = 0; k < M::NI; ++k) carry[k] = v[k];
+            done = true;
+            progressed = true;
+          }
+        }
+      } else if (!done) {
         bool stalled = false;
 #pragma unroll
         for (int w = 0; w < W * KP; ++w) {
@@ -318,6 +365,18 @@ __device__ __forceinline__ Aff aff_compose(const Aff& x, const Aff& y) {
   return o;
 }
 
+// Aggregate words: A row major (16), then b (4).
+__device__ __forceinline__ Aff aff_load(const float a[20]) {
+  Aff o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o.b[i] = a[16 + i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.A[i][j] = a[4 * i + j];
+  }
+  return o;
+}
+
 __device__ __forceinline__ void aff_apply(const Aff& a, float v[4]) {
   float o[4];
 #pragma unroll
@@ -351,6 +410,9 @@ struct NewtonMonoid {
 #pragma unroll
     for (int k = 0; k < 4; ++k) out[k] = v[k];
     aff_apply(acc, out);
+  }
+  static __device__ __forceinline__ void apply(const float a[NA], float v[NI]) {
+    aff_apply(aff_load(a), v);
   }
 };
 

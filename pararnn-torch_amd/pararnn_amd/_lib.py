@@ -19,7 +19,7 @@ PRNN_OK = 0
 PRNN_ERR_VALUE = 1
 PRNN_ERR_TYPE = 2
 PRNN_ERR_RUNTIME = 3
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # name -> (restype, argtypes); mirrors include/pararnn_amd.h
 _P = ctypes.c_void_p
@@ -29,6 +29,8 @@ _S = ctypes.c_size_t
 SIGNATURES: dict[str, tuple] = {
     "prnn_abi_version": (_I, []),
     "prnn_last_error": (ctypes.c_char_p, []),
+    "prnn_set_deterministic": (None, [_I]),
+    "prnn_deterministic": (_I, []),
     "prnn_slstm_init_workspace_size": (_S, [_I, _I, _I, _I, _I]),
     "prnn_slstm_init": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _P, _S, _P]),
     "prnn_slstm_newton_workspace_size": (_S, [_I, _I, _I, _I, _I]),
@@ -87,6 +89,17 @@ def load() -> ctypes.CDLL:
             raise RuntimeError(f"{path}: ABI version {ver}, expected {ABI_VERSION}; rebuild it")
         _handle = handle
         return handle
+
+
+def sync_deterministic(handle: ctypes.CDLL) -> None:
+    """Mirror ``torch.are_deterministic_algorithms_enabled()`` into the
+    library's deterministic look-back switch (the reference keys its own
+    determinism checks on the same torch flag, pararnn/determinism.py:41-45)."""
+    import torch
+
+    on = int(bool(torch.are_deterministic_algorithms_enabled()))
+    if handle.prnn_deterministic() != on:
+        handle.prnn_set_deterministic(on)
 
 
 def check(rc: int, what: str) -> None:

@@ -28,7 +28,7 @@ from dataclasses import replace
 import torch
 from torch import Tensor, nn
 
-from pararnn_amd import ops
+from pararnn_amd import determinism, ops
 from pararnn_amd.cells import SLSTM_HIDDEN, ParaGRU, ParaSLSTM
 from pararnn_amd.ragged import (
     Padding,
@@ -486,9 +486,12 @@ def _eq26_vjp(cell: nn.Module, states: Tensor, x: Tensor, partial: Tensor, *,
     partial = partial.to(states.dtype)
     cap = cell.max_recurrent_norm
     if isinstance(cell, ParaSLSTM) and cell.mix == "diag":
-        g_wx, g_r, g_h0 = ops.slstm_backward_fused(
-            wx, cell.clipped_r(), h0, states, partial, eps=cell.eps
-        )
+        r_mix = cell.clipped_r()
+        g_wx, g_r, g_h0 = ops.slstm_backward_fused(wx, r_mix, h0, states, partial, eps=cell.eps)
+        determinism.maybe_check_fused_vjp_once(
+            (g_r,),
+            lambda: (ops.slstm_backward_fused(wx, r_mix, h0, states, partial, eps=cell.eps)[1],),
+            cell_name=type(cell).__name__, shape=states.shape)
         g_r = g_r.to(cell.R.dtype)
         if cap is not None:
             g_r = g_r * (cell.R.abs() <= cap).to(g_r.dtype)
@@ -496,6 +499,10 @@ def _eq26_vjp(cell: nn.Module, states: Tensor, x: Tensor, partial: Tensor, *,
     elif isinstance(cell, ParaGRU) and cell.mix == "head":
         a_z, a_r, a_n = cell.clipped_a_head()
         g_wx, g_a, g_h0 = ops.gru_head_backward_fused(wx, a_z, a_r, a_n, h0, states, partial)
+        determinism.maybe_check_fused_vjp_once(
+            (g_a,),
+            lambda: (ops.gru_head_backward_fused(wx, a_z, a_r, a_n, h0, states, partial)[1],),
+            cell_name=type(cell).__name__, shape=states.shape)
         by_name = {}
         for i, name in enumerate(("A_z", "A_r", "A_n")):
             raw = getattr(cell, name)

@@ -97,6 +97,7 @@ def slstm_init_fused(
     h0 = _slstm_h0(h0, batch, d_h)
     out = wx.new_empty(batch, time, 4, d_h)
     lib = _lib.load()
+    _lib.sync_deterministic(lib)
     with torch.cuda.device(wx.device):
         nbytes = lib.prnn_slstm_init_workspace_size(batch, time, d_h, picard_iters, code)
         ws = _workspace(nbytes, wx.device)
@@ -164,6 +165,7 @@ def newton_slstm_fused(
     states = states.contiguous()
     out = wx.new_empty(batch, time, 4, d_h)
     lib = _lib.load()
+    _lib.sync_deterministic(lib)
     with torch.cuda.device(wx.device):
         nbytes = lib.prnn_slstm_newton_workspace_size(batch, time, d_h, int(max_iters), code)
         ws = _workspace(nbytes, wx.device)
@@ -209,6 +211,7 @@ def slstm_backward_fused(
     g_r = torch.empty(4, d_h, dtype=torch.float32, device=wx.device)
     g_h0 = torch.zeros(batch, 4, d_h, dtype=torch.float32, device=wx.device)
     lib = _lib.load()
+    _lib.sync_deterministic(lib)
     with torch.cuda.device(wx.device):
         nbytes = lib.prnn_slstm_backward_workspace_size(batch, time, d_h, code)
         ws = _workspace(nbytes, wx.device)

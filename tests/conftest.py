@@ -36,3 +36,17 @@ def gpu_available() -> bool:
     import torch
 
     return torch.cuda.is_available()
+
+
+@pytest.fixture(params=[False, True], ids=["lookback_default", "lookback_deterministic"])
+def lookback_mode(request):
+    """Run a test with torch's deterministic-algorithms flag off and on: on,
+    the sLSTM look-back scans take their deterministic walk, which must meet
+    the same parity bar."""
+    import torch
+
+    prev = torch.are_deterministic_algorithms_enabled()
+    prev_warn = torch.is_deterministic_algorithms_warn_only_enabled()
+    torch.use_deterministic_algorithms(request.param, warn_only=True)
+    yield request.param
+    torch.use_deterministic_algorithms(prev, warn_only=prev_warn)

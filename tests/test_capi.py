@@ -23,7 +23,8 @@ def test_header_declares_entry_points():
     decl = _declared()
     for name in ("prnn_slstm_init", "prnn_slstm_newton", "prnn_gru_head_newton",
                  "prnn_slstm_backward", "prnn_gru_head_backward", "prnn_slstm_decode",
-                 "prnn_gru_decode", "prnn_last_error", "prnn_abi_version"):
+                 "prnn_gru_decode", "prnn_last_error", "prnn_abi_version",
+                 "prnn_set_deterministic", "prnn_deterministic"):
         assert name in decl
 
 
@@ -47,6 +48,10 @@ def test_host_only_calls():
         pytest.skip("library not built")
     lib = _lib.load()
     assert lib.prnn_abi_version() == _lib.ABI_VERSION
+    lib.prnn_set_deterministic(1)
+    assert lib.prnn_deterministic() == 1
+    lib.prnn_set_deterministic(0)
+    assert lib.prnn_deterministic() == 0
     n = lib.prnn_slstm_newton_workspace_size(1, 131072, 1024, 2, _lib.PRNN_BF16)
     # K >= 2 runs in one launch: look-back words per iteration, no fp32
     # trajectory in memory; more iterations need more words.

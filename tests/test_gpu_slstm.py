@@ -10,7 +10,7 @@ from conftest import load_golden
 import oracle as O
 from oracle.slstm import slstm_newton_f64
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("lookback_mode")]
 
 DEV = "cuda:0"
 

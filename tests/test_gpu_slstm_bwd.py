@@ -9,7 +9,7 @@ from conftest import load_golden
 import oracle as O
 from oracle.backward import slstm_backward
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("lookback_mode")]
 
 DEV = "cuda:0"
 
