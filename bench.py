@@ -49,6 +49,30 @@ def _time(torch, fn, reps, warm=2):
     return s.elapsed_time(e) / reps
 
 
+def _time_kernel(torch, fn, reps, warm=2):
+    """Average ms of the library's main kernel(s) per call of fn(): the HIP
+    event pair the library records on the launch stream right around them
+    (after the per-call status-word clear; prnn_set_kernel_timing)."""
+    from pararnn_amd import _lib
+
+    lib = _lib.load()
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    lib.prnn_set_kernel_timing(1)
+    try:
+        total = 0.0
+        for _ in range(reps):
+            fn()
+            ms = lib.prnn_last_kernel_ms()
+            if ms <= 0:
+                raise RuntimeError("kernel timing returned no measurement")
+            total += ms
+    finally:
+        lib.prnn_set_kernel_timing(0)
+    return total / reps
+
+
 def _traffic_from_profile(name: str):
     """HBM bytes per launch measured with rocprofv3 --pmc (committed summary)."""
     path = os.path.join(REPO, "profiles", name)
@@ -260,19 +284,22 @@ def main() -> int:
         t_wall = time.perf_counter() - t_wall
         ms = s.elapsed_time(e) / args.steps
 
-        # Per-kernel launch durations (each call adds one ~10 us status clear,
-        # which cancels in the differences).
+        # Per-op durations (status-word clear, workspace allocation and the
+        # kernel launch, as a caller sees them).
         reps = max(5, args.steps // 2)
         init = slstm_init_fused(wx, r, None, picard_iters=P, eps=cell.eps)
-        ms_init1 = _time(torch, lambda: slstm_init_fused(wx, r, None, picard_iters=1, eps=cell.eps), reps)
         ms_initP = _time(torch, lambda: slstm_init_fused(wx, r, None, picard_iters=P, eps=cell.eps), reps)
         from pararnn_amd import newton_slstm_fused
 
-        ms_n1 = _time(torch, lambda: newton_slstm_fused(wx, r, None, init, max_iters=1, omega=1.0,
-                                                        eps=cell.eps), reps)
         ms_n2 = _time(torch, lambda: newton_slstm_fused(wx, r, None, init, max_iters=2, omega=1.0,
                                                         eps=cell.eps), reps)
-        ms_newton = ms_n2  # the K = 2 Newton iterations: one fused launch
+        # The kernels alone (HIP events around the launch, on its stream).
+        ms_initP_k = _time_kernel(torch, lambda: slstm_init_fused(wx, r, None, picard_iters=P,
+                                                                  eps=cell.eps), reps)
+        ms_init1_k = _time_kernel(torch, lambda: slstm_init_fused(wx, r, None, picard_iters=1,
+                                                                  eps=cell.eps), reps)
+        ms_newton = _time_kernel(torch, lambda: newton_slstm_fused(
+            wx, r, None, init, max_iters=2, omega=1.0, eps=cell.eps), reps)
         ms_gemm = _time(torch, lambda: cell.W_x(x), reps)
         cfg = NewtonConfig(max_iters=K, picard_iters=P, residual_atol=None, residual_fail=None,
                            picard_adapt=False)
@@ -296,7 +323,7 @@ def main() -> int:
     init_io = elems * 16
     init_alg = elems * ((4 * s_x + 16) + P * (4 * s_x + 20))
     ach_newton = newton_bytes / (ms_newton * 1e-3) / 1e9
-    newton_share = ms_newton / ms
+    newton_share = ms_n2 / ms
     init_share = ms_initP / ms
     out = {
         "metric": "Newton+scan fwd tokens/sec + % HBM roofline, ParaSLSTM diag d=1024 T=131072",
@@ -327,6 +354,7 @@ def main() -> int:
             "traffic": _traffic_from_profile("slstm_newton_cfg3.md"),
             "algorithmic_bytes_per_launch": newton_bytes,
             "avg_launch_ms": ms_newton,
+            "avg_op_ms": ms_n2,
             "own_io_bytes_per_launch": newton_io,
             "own_io_frac": newton_io / (ms_newton * 1e-3) / 1e9 / HBM_PEAK_GBS,
         },
@@ -334,12 +362,13 @@ def main() -> int:
             "kernel": f"slstm_picard_fused_kernel (zero-hidden pass + {P} Picard passes in one "
                       f"launch; {100 * init_share:.0f}% of the step)",
             "bound": "valu",
-            "avg_launch_ms": ms_initP,
-            "per_stage_ms": (ms_initP - ms_init1) / (P - 1),
+            "avg_launch_ms": ms_initP_k,
+            "avg_op_ms": ms_initP,
+            "per_stage_ms": (ms_initP_k - ms_init1_k) / (P - 1),
             "io_bytes_per_launch": init_io,
-            "io_GBps": init_io / (ms_initP * 1e-3) / 1e9,
+            "io_GBps": init_io / (ms_initP_k * 1e-3) / 1e9,
             "algorithmic_bytes_per_launch": init_alg,
-            "algorithmic_GBps": init_alg / (ms_initP * 1e-3) / 1e9,
+            "algorithmic_GBps": init_alg / (ms_initP_k * 1e-3) / 1e9,
         },
         "step_algorithmic_GBps": step_bytes / (ms * 1e-3) / 1e9,
         "step_roofline_frac": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,

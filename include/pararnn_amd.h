@@ -74,6 +74,15 @@ PRNN_API const char* prnn_last_error(void);
 PRNN_API void prnn_set_deterministic(int on);
 PRNN_API int prnn_deterministic(void);
 
+/* Kernel timing, process-wide (off by default; no counterpart in the
+ * reference, for benchmarks).  When on, the sLSTM entry points record a HIP
+ * event pair on their stream around their main kernel(s) -- after the status
+ * word clear: the warm start launch(es), the Newton launch(es), the reverse
+ * scan -- and prnn_last_kernel_ms waits for the last pair and returns its
+ * elapsed milliseconds (-1 if none).  Not for use under graph capture. */
+PRNN_API void prnn_set_kernel_timing(int on);
+PRNN_API float prnn_last_kernel_ms(void);
+
 /* ---- ParaSLSTM mix='diag' ------------------------------------------------
  * Layouts: wx (B, T, 4d) gate blocks (i, f, z, o);  r (4, d) recurrent mix,
  * already clamped by the caller;  h0 (B, 4, d) slots (c, n, m, h) or NULL

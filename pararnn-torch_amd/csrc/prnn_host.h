@@ -49,6 +49,12 @@ struct Carver {
 // Process-wide deterministic look-back switch (prnn_set_deterministic).
 int deterministic();
 
+// Optional timing of an entry point's main kernel(s) (prnn_set_kernel_timing):
+// when on, HIP events are recorded on the caller's stream right before and
+// right after them; prnn_last_kernel_ms reads the last pair.
+void timing_begin(hipStream_t stream);
+void timing_end(hipStream_t stream);
+
 // Zero `n` 32-bit words on `stream` with a kernel (no memset node, so the
 // sequence stays replay-safe under HIP graph capture).
 int clear_words(int* p, size_t n, hipStream_t stream);

@@ -384,6 +384,7 @@ static int run_bwd(const TX* wx, const TX* r, const TX* h0, const TX* states, co
                    const BwdWs& w, hipStream_t stream) {
   int rc = clear_words(w.lb.counters, w.lb.clear_words, stream);
   if (rc != PRNN_OK) return rc;
+  timing_begin(stream);
   Shape sh;
   if constexpr (sizeof(TX) == 4) {
 #define PRNN_LAUNCH(LL, WW, DD) \
@@ -405,6 +406,7 @@ static int run_bwd(const TX* wx, const TX* r, const TX* h0, const TX* states, co
 #undef PRNN_SHAPE
   }
 #undef PRNN_LAUNCH
+  timing_end(stream);
   PRNN_HIP(hipGetLastError());
   const Geo g = geometry(B, T, d, sh);
   slstm_gr_reduce_kernel<<<dim3(4 * g.n_cb), dim3(64 * kReduceWaves), 0, stream>>>(

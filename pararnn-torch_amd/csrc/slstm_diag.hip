@@ -1300,6 +1300,7 @@ static int run_init(const TX* wx, const TX* r, const TX* h0, TX* states, int B, 
 #define PRNN_SHAPE(LL, WW, WPE) \
   else if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, WPE, false);
       static_assert(kPicardDefault.L == 24 && kPicardDefault.W == 4, "default Picard shape");
+      timing_begin(stream);
       if (deterministic()) PRNN_LAUNCH(24, 4, 3, true);
       PRNN_SHAPE(24, 4, 3)
       PRNN_SHAPE(16, 4, 4)
@@ -1307,11 +1308,13 @@ static int run_init(const TX* wx, const TX* r, const TX* h0, TX* states, int B, 
       PRNN_SHAPE(32, 4, 2)
 #undef PRNN_SHAPE
 #undef PRNN_LAUNCH
+      timing_end(stream);
       PRNN_HIP(hipGetLastError());
       return PRNN_OK;
     }
   }
   // Pass 0: zero-hidden scan (pre = wx); passes 1..P freeze wx + R h_prev.
+  timing_begin(stream);
   for (int p = 0; p <= P; ++p) {
     const TX* src = p == 0 ? nullptr : static_cast<const TX*>(w.hbuf[(p - 1) & 1]);
     const bool last = p == P;
@@ -1320,6 +1323,7 @@ static int run_init(const TX* wx, const TX* r, const TX* h0, TX* states, int B, 
                     w.lb, p + 1, stream);
     PRNN_HIP(hipGetLastError());
   }
+  timing_end(stream);
   return PRNN_OK;
 }
 
@@ -1383,6 +1387,7 @@ static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, 
   else if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, WPE, false);
     static_assert(kNewtonFusedF32.L == 16 && kNewtonFusedF32.W == 4, "fp32 fused shape");
     static_assert(kNewtonFusedDefault.L == 20 && kNewtonFusedDefault.W == 4, "default shape");
+    timing_begin(stream);
     if constexpr (sizeof(TX) == 4) {
       if (deterministic()) PRNN_LAUNCH(16, 4, 2, true);
       PRNN_SHAPE(16, 4, 2)
@@ -1395,9 +1400,11 @@ static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, 
     }
 #undef PRNN_SHAPE
 #undef PRNN_LAUNCH
+    timing_end(stream);
     PRNN_HIP(hipGetLastError());
     return PRNN_OK;
   }
+  timing_begin(stream);
   for (int k = 1; k <= K; ++k) {
     const bool first = k == 1, last = k == K;
     const float* win = first ? nullptr : w.work[(k - 2) & 1];
@@ -1412,6 +1419,7 @@ static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, 
       launch_newton<TX, float, float>(wx, r, h0, win, wout, B, T, d, omega, eps, w.lb, k, stream);
     PRNN_HIP(hipGetLastError());
   }
+  timing_end(stream);
   return PRNN_OK;
 }
 

@@ -31,6 +31,8 @@ SIGNATURES: dict[str, tuple] = {
     "prnn_last_error": (ctypes.c_char_p, []),
     "prnn_set_deterministic": (None, [_I]),
     "prnn_deterministic": (_I, []),
+    "prnn_set_kernel_timing": (None, [_I]),
+    "prnn_last_kernel_ms": (ctypes.c_float, []),
     "prnn_slstm_init_workspace_size": (_S, [_I, _I, _I, _I, _I]),
     "prnn_slstm_init": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _P, _S, _P]),
     "prnn_slstm_newton_workspace_size": (_S, [_I, _I, _I, _I, _I]),

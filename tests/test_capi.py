@@ -24,7 +24,8 @@ def test_header_declares_entry_points():
     for name in ("prnn_slstm_init", "prnn_slstm_newton", "prnn_gru_head_newton",
                  "prnn_slstm_backward", "prnn_gru_head_backward", "prnn_slstm_decode",
                  "prnn_gru_decode", "prnn_last_error", "prnn_abi_version",
-                 "prnn_set_deterministic", "prnn_deterministic"):
+                 "prnn_set_deterministic", "prnn_deterministic", "prnn_set_kernel_timing",
+                 "prnn_last_kernel_ms"):
         assert name in decl
 
 
@@ -52,6 +53,7 @@ def test_host_only_calls():
     assert lib.prnn_deterministic() == 1
     lib.prnn_set_deterministic(0)
     assert lib.prnn_deterministic() == 0
+    assert lib.prnn_last_kernel_ms() == -1.0  # nothing timed yet
     n = lib.prnn_slstm_newton_workspace_size(1, 131072, 1024, 2, _lib.PRNN_BF16)
     # K >= 2 runs in one launch: look-back words per iteration, no fp32
     # trajectory in memory; more iterations need more words.
