@@ -138,6 +138,37 @@ PRNN_API int prnn_slstm_backward(const void* wx, const void* r, const void* h0,
                                  float* g_h0, int B, int T, int d, float eps, int dtype,
                                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* Tagged-workspace variants of the three sLSTM calls (no counterpart in the
+ * reference; for callers that keep one workspace across calls).  The sLSTM
+ * look-back exchanges {value, tag} words through the workspace; a word is
+ * valid when its tag is one of the call's.  With tag_base = 0 (what the plain
+ * calls do) every such word is cleared first -- a write of the whole
+ * look-back area (~0.6 GB at B=1, T=131072, d=1024, K=2: ~80 us).  With
+ * tag_base > 0 only the 64 ticket counters are cleared and the call's tags
+ * are tag_base + 1 .. tag_base + PRNN_TAG_SPAN.  The caller then guarantees
+ * that every word of the workspace is either zero or was written by an
+ * earlier call with a smaller tag_base (the workspace was zero-filled once
+ * and only these calls have written it since; advance tag_base by at least
+ * PRNN_TAG_SPAN per call; re-zero it before tag_base would pass
+ * PRNN_TAG_BASE_MAX).  Not for HIP graph capture: a replay would repeat the
+ * captured tags. */
+#define PRNN_TAG_SPAN 64
+#define PRNN_TAG_BASE_MAX (1 << 30)
+PRNN_API int prnn_slstm_init_ex(const void* wx, const void* r, const void* h0, void* states,
+                                int B, int T, int d, int picard_iters, float eps, int dtype,
+                                void* workspace, size_t workspace_bytes, int tag_base,
+                                void* stream);
+PRNN_API int prnn_slstm_newton_ex(const void* wx, const void* r, const void* h0,
+                                  const void* states, void* out, int B, int T, int d,
+                                  int max_iters, float omega, float eps, int dtype,
+                                  void* workspace, size_t workspace_bytes, int tag_base,
+                                  void* stream);
+PRNN_API int prnn_slstm_backward_ex(const void* wx, const void* r, const void* h0,
+                                    const void* states, const void* grad, void* g_wx,
+                                    float* g_r, float* g_h0, int B, int T, int d, float eps,
+                                    int dtype, void* workspace, size_t workspace_bytes,
+                                    int tag_base, void* stream);
+
 /* Eq. 2.6 backward of the head GRU at `states` = H* (B, T, d) with upstream
  * gradient `grad` = dL/dH (B, T, d) (both in `dtype`):
  *   mu_{T-1} = grad_{T-1},  mu_t = grad_t + J_{t+1}^T mu_{t+1}  (fp32),

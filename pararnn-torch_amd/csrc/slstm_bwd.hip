@@ -375,14 +375,14 @@ static void launch_reverse(const TX* wx, const TX* r, const TX* h0, const TX* st
   const Geo g = geometry(B, T, d, Shape{L, W});
   slstm_reverse_kernel<TX, L, W, DET><<<dim3(g.n_tiles), dim3(64 * W), 0, stream>>>(
       wx, r, h0, states, grad, gwx, w.gr_part, gh0, B, T, d, g.n_cb, g.n_chunks, eps,
-      w.lb.counters + 1, w.lb.agg, w.lb.incl, 1);
+      w.lb.counters + 1, w.lb.agg, w.lb.incl, w.lb.tag_base + 1);
 }
 
 template <typename TX>
 static int run_bwd(const TX* wx, const TX* r, const TX* h0, const TX* states, const TX* grad,
                    TX* gwx, float* gr, float* gh0, int B, int T, int d, float eps,
                    const BwdWs& w, hipStream_t stream) {
-  int rc = clear_words(w.lb.counters, w.lb.clear_words, stream);
+  int rc = clear_status(w.lb, stream);
   if (rc != PRNN_OK) return rc;
   timing_begin(stream);
   Shape sh;
@@ -427,19 +427,23 @@ extern "C" PRNN_API size_t prnn_slstm_backward_workspace_size(int B, int T, int 
   return total;
 }
 
-extern "C" PRNN_API int prnn_slstm_backward(const void* wx, const void* r, const void* h0,
-                                            const void* states, const void* grad, void* gwx,
-                                            float* gr, float* gh0, int B, int T, int d, float eps,
-                                            int dtype, void* workspace, size_t workspace_bytes,
-                                            void* stream) {
+extern "C" PRNN_API int prnn_slstm_backward_ex(const void* wx, const void* r, const void* h0,
+                                               const void* states, const void* grad, void* gwx,
+                                               float* gr, float* gh0, int B, int T, int d,
+                                               float eps, int dtype, void* workspace,
+                                               size_t workspace_bytes, int tag_base,
+                                               void* stream) {
   int rc = slstm::check_dims(B, T, d, dtype);
+  if (rc != PRNN_OK) return rc;
+  rc = slstm::check_tag_base(tag_base);
   if (rc != PRNN_OK) return rc;
   if (!wx || !r || !states || !grad || !gwx || !gr || !workspace)
     return fail(PRNN_ERR_VALUE, "wx, r, states, grad, g_wx, g_r and workspace must be non-null");
   size_t need = 0;
-  const slstm::BwdWs w = slstm::carve_bwd(workspace, B, T, d, dtype, &need);
+  slstm::BwdWs w = slstm::carve_bwd(workspace, B, T, d, dtype, &need);
   if (workspace_bytes < need)
     return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  w.lb.tag_base = tag_base;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == PRNN_F32)
     return slstm::run_bwd(static_cast<const float*>(wx), static_cast<const float*>(r),
@@ -450,4 +454,13 @@ extern "C" PRNN_API int prnn_slstm_backward(const void* wx, const void* r, const
                         static_cast<const bf16*>(h0), static_cast<const bf16*>(states),
                         static_cast<const bf16*>(grad), static_cast<bf16*>(gwx), gr, gh0, B, T, d,
                         eps, w, s);
+}
+
+extern "C" PRNN_API int prnn_slstm_backward(const void* wx, const void* r, const void* h0,
+                                            const void* states, const void* grad, void* gwx,
+                                            float* gr, float* gh0, int B, int T, int d, float eps,
+                                            int dtype, void* workspace, size_t workspace_bytes,
+                                            void* stream) {
+  return prnn_slstm_backward_ex(wx, r, h0, states, grad, gwx, gr, gh0, B, T, d, eps, dtype,
+                                workspace, workspace_bytes, 0, stream);
 }

@@ -336,7 +336,7 @@ slstm_picard_fused_kernel(
     const bf16* __restrict__ wx, const bf16* __restrict__ rmix, const bf16* __restrict__ h0,
     bf16* __restrict__ out, int B, int T, int d, int n_cb, int n_tiles, int P, float eps,
     int* __restrict__ counter, unsigned long long* __restrict__ agg,
-    unsigned long long* __restrict__ incl, unsigned long long* __restrict__ hlast) {
+    unsigned long long* __restrict__ incl, unsigned long long* __restrict__ hlast, int tag_base) {
   static_assert(L % 2 == 0, "h is packed two steps to a register");
   constexpr int KP = 2;
   constexpr uint32_t SZ = 2;
@@ -404,7 +404,7 @@ slstm_picard_fused_kernel(
   auto stage = [&](const int p, auto last_c) __attribute__((always_inline)) {
     constexpr bool last_stage = decltype(last_c)::value;
     const bool first_stage = p == 0;
-    const int tag = p + 1;
+    const int tag = tag_base + p + 1;
     // Keep wx packed across stages: without this the compiler hoists the
     // bf16 unpacking out of the stage loop and holds 4 floats per step.
 #pragma unroll
@@ -783,7 +783,7 @@ slstm_newton_fused_kernel(
     const TX* __restrict__ guess, TX* __restrict__ out, int B, int T, int d, int n_cb,
     int n_tiles, int K, float omega, float eps, int* __restrict__ counter,
     unsigned long long* __restrict__ agg, unsigned long long* __restrict__ incl,
-    unsigned long long* __restrict__ hlast) {
+    unsigned long long* __restrict__ hlast, int tag_base) {
   constexpr int KP = 1;  // predecessors per wave per look-back round
   using XS = RowStash<TX>;
   __shared__ float s_agg[W][20][kCB];
@@ -855,7 +855,7 @@ slstm_newton_fused_kernel(
   // compiled separately, writes it (no per-step branch on the iteration).
   auto iterate = [&](const int k, auto last_c) __attribute__((always_inline)) {
     constexpr bool last_iter = decltype(last_c)::value;
-    const int tag = k + 1;
+    const int tag = tag_base + k + 1;
     // Keep wx packed across iterations (otherwise the unpacking is hoisted out
     // of the loop and holds 4 floats per step).
 #pragma unroll
@@ -1251,7 +1251,8 @@ static void launch_frozen(bool has_h, bool full_out, const TX* wx, const TX* r, 
   int* ctr = lb.counters + epoch;
 #define PRNN_FROZEN(HH, FO)                                                                    \
   slstm_frozen_kernel<TX, L, W, HH, FO, DET><<<grid, block, 0, stream>>>(                      \
-      wx, r, h0, src, out_full, out_h, B, T, d, g.n_cb, eps, ctr, lb.agg, lb.incl, epoch)
+      wx, r, h0, src, out_full, out_h, B, T, d, g.n_cb, eps, ctr, lb.agg, lb.incl,             \
+      lb.tag_base + epoch)
   if (has_h) {
     if (full_out) PRNN_FROZEN(true, true); else PRNN_FROZEN(true, false);
   } else {
@@ -1287,7 +1288,7 @@ static void frozen_pass(bool has_h, bool full_out, const TX* wx, const TX* r, co
 template <typename TX>
 static int run_init(const TX* wx, const TX* r, const TX* h0, TX* states, int B, int T, int d,
                     int P, float eps, const InitWs& w, hipStream_t stream) {
-  int rc = clear_words(w.lb.counters, w.lb.clear_words, stream);
+  int rc = clear_status(w.lb, stream);
   if (rc != PRNN_OK) return rc;
   if constexpr (sizeof(TX) == 2) {
     if (w.fused) {
@@ -1296,7 +1297,7 @@ static int run_init(const TX* wx, const TX* r, const TX* h0, TX* states, int B, 
 #define PRNN_LAUNCH(LL, WW, WPE, DD)                                                            \
   slstm_picard_fused_kernel<LL, WW, WPE, DD><<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>(    \
       wx, r, h0, states, B, T, d, g.n_cb, g.n_tiles, P, eps, w.lb.counters + 1, w.lb.agg,       \
-      w.lb.incl, w.hlast)
+      w.lb.incl, w.hlast, w.lb.tag_base)
 #define PRNN_SHAPE(LL, WW, WPE) \
   else if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, WPE, false);
       static_assert(kPicardDefault.L == 24 && kPicardDefault.W == 4, "default Picard shape");
@@ -1334,7 +1335,7 @@ static void launch_newton_shape(const TX* wx, const TX* r, const TX* h0, const T
   const Geo g = geometry(B, T, d, Shape{L, W});
   slstm_newton_kernel<TX, TIN, TOUT, L, W, DET><<<dim3(g.n_tiles), dim3(64 * W), 0, stream>>>(
       wx, r, h0, hin, hout, B, T, d, g.n_cb, omega, eps, lb.counters + epoch, lb.agg,
-      lb.incl, epoch);
+      lb.incl, lb.tag_base + epoch);
 }
 
 template <typename TX, typename TIN, typename TOUT>
@@ -1374,7 +1375,7 @@ static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, 
                             hipMemcpyDeviceToDevice, stream));
     return PRNN_OK;
   }
-  int rc = clear_words(w.lb.counters, w.lb.clear_words, stream);
+  int rc = clear_status(w.lb, stream);
   if (rc != PRNN_OK) return rc;
   if (w.fused) {
     const Shape sh = newton_fused_shape(sizeof(TX) == 2 ? PRNN_BF16 : PRNN_F32);
@@ -1382,7 +1383,7 @@ static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, 
 #define PRNN_LAUNCH(LL, WW, WPE, DD)                                                             \
   slstm_newton_fused_kernel<TX, LL, WW, WPE, DD><<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>( \
       wx, r, h0, guess, out, B, T, d, g.n_cb, g.n_tiles, K, omega, eps, w.lb.counters + 1,       \
-      w.lb.agg, w.lb.incl, w.hlast)
+      w.lb.agg, w.lb.incl, w.hlast, w.lb.tag_base)
 #define PRNN_SHAPE(LL, WW, WPE) \
   else if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, WPE, false);
     static_assert(kNewtonFusedF32.L == 16 && kNewtonFusedF32.W == 4, "fp32 fused shape");
@@ -1436,11 +1437,13 @@ extern "C" PRNN_API size_t prnn_slstm_init_workspace_size(int B, int T, int d, i
   return total;
 }
 
-extern "C" PRNN_API int prnn_slstm_init(const void* wx, const void* r, const void* h0,
-                                        void* states, int B, int T, int d, int picard_iters,
-                                        float eps, int dtype, void* workspace,
-                                        size_t workspace_bytes, void* stream) {
+extern "C" PRNN_API int prnn_slstm_init_ex(const void* wx, const void* r, const void* h0,
+                                           void* states, int B, int T, int d, int picard_iters,
+                                           float eps, int dtype, void* workspace,
+                                           size_t workspace_bytes, int tag_base, void* stream) {
   int rc = slstm::check_dims(B, T, d, dtype);
+  if (rc != PRNN_OK) return rc;
+  rc = slstm::check_tag_base(tag_base);
   if (rc != PRNN_OK) return rc;
   if (picard_iters < 0 || picard_iters > slstm::kMaxStages - 2)
     return fail(PRNN_ERR_VALUE, "picard_iters must be in [0, %d], got %d",
@@ -1448,9 +1451,10 @@ extern "C" PRNN_API int prnn_slstm_init(const void* wx, const void* r, const voi
   if (!wx || !r || !states || !workspace)
     return fail(PRNN_ERR_VALUE, "wx, r, states and workspace must be non-null");
   size_t need = 0;
-  const slstm::InitWs w = slstm::carve_init(workspace, B, T, d, picard_iters, dtype, &need);
+  slstm::InitWs w = slstm::carve_init(workspace, B, T, d, picard_iters, dtype, &need);
   if (workspace_bytes < need)
     return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  w.lb.tag_base = tag_base;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == PRNN_F32)
     return slstm::run_init(static_cast<const float*>(wx), static_cast<const float*>(r),
@@ -1461,6 +1465,14 @@ extern "C" PRNN_API int prnn_slstm_init(const void* wx, const void* r, const voi
                          picard_iters, eps, w, s);
 }
 
+extern "C" PRNN_API int prnn_slstm_init(const void* wx, const void* r, const void* h0,
+                                        void* states, int B, int T, int d, int picard_iters,
+                                        float eps, int dtype, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  return prnn_slstm_init_ex(wx, r, h0, states, B, T, d, picard_iters, eps, dtype, workspace,
+                            workspace_bytes, 0, stream);
+}
+
 extern "C" PRNN_API size_t prnn_slstm_newton_workspace_size(int B, int T, int d, int max_iters,
                                                             int dtype) {
   if (slstm::check_dims(B, T, d, dtype) != PRNN_OK || max_iters < 0) return 0;
@@ -1469,11 +1481,14 @@ extern "C" PRNN_API size_t prnn_slstm_newton_workspace_size(int B, int T, int d,
   return total;
 }
 
-extern "C" PRNN_API int prnn_slstm_newton(const void* wx, const void* r, const void* h0,
-                                          const void* states, void* out, int B, int T, int d,
-                                          int max_iters, float omega, float eps, int dtype,
-                                          void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" PRNN_API int prnn_slstm_newton_ex(const void* wx, const void* r, const void* h0,
+                                             const void* states, void* out, int B, int T, int d,
+                                             int max_iters, float omega, float eps, int dtype,
+                                             void* workspace, size_t workspace_bytes,
+                                             int tag_base, void* stream) {
   int rc = slstm::check_dims(B, T, d, dtype);
+  if (rc != PRNN_OK) return rc;
+  rc = slstm::check_tag_base(tag_base);
   if (rc != PRNN_OK) return rc;
   if (max_iters < 0 || max_iters > slstm::kMaxStages - 1)
     return fail(PRNN_ERR_VALUE, "max_iters must be in [0, %d], got %d", slstm::kMaxStages - 1,
@@ -1482,9 +1497,10 @@ extern "C" PRNN_API int prnn_slstm_newton(const void* wx, const void* r, const v
     return fail(PRNN_ERR_VALUE, "wx, r, states, out and workspace must be non-null");
   if (out == states) return fail(PRNN_ERR_VALUE, "out must not alias states");
   size_t need = 0;
-  const slstm::NewtonWs w = slstm::carve_newton(workspace, B, T, d, max_iters, dtype, &need);
+  slstm::NewtonWs w = slstm::carve_newton(workspace, B, T, d, max_iters, dtype, &need);
   if (workspace_bytes < need)
     return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  w.lb.tag_base = tag_base;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == PRNN_F32)
     return slstm::run_newton(static_cast<const float*>(wx), static_cast<const float*>(r),
@@ -1493,4 +1509,12 @@ extern "C" PRNN_API int prnn_slstm_newton(const void* wx, const void* r, const v
   return slstm::run_newton(static_cast<const bf16*>(wx), static_cast<const bf16*>(r),
                            static_cast<const bf16*>(h0), static_cast<const bf16*>(states),
                            static_cast<bf16*>(out), B, T, d, max_iters, omega, eps, w, s);
+}
+
+extern "C" PRNN_API int prnn_slstm_newton(const void* wx, const void* r, const void* h0,
+                                          const void* states, void* out, int B, int T, int d,
+                                          int max_iters, float omega, float eps, int dtype,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+  return prnn_slstm_newton_ex(wx, r, h0, states, out, B, T, d, max_iters, omega, eps, dtype,
+                              workspace, workspace_bytes, 0, stream);
 }

@@ -463,7 +463,7 @@ struct RowStash<float> {
 namespace prnn {
 namespace slstm {
 
-constexpr int kMaxStages = 64;  // ticket counters per call
+constexpr int kMaxStages = PRNN_TAG_SPAN;  // ticket counters (and tags) per call
 
 // Tile shape: L steps per lane x W waves.
 struct Shape {
@@ -505,7 +505,24 @@ struct Lookback {
   unsigned long long* incl;
   unsigned long long* agg;
   size_t clear_words;
+  // 0: clear every status word before the call; > 0: the caller vouches that
+  // every word holds a tag below tag_base + 1 (zero-filled, or written by an
+  // earlier call with a smaller base), so only the ticket counters are
+  // cleared and this call's tags start at tag_base + 1.
+  int tag_base = 0;
 };
+
+static int check_tag_base(int tag_base) {
+  if (tag_base < 0 || tag_base > PRNN_TAG_BASE_MAX)
+    return fail(PRNN_ERR_VALUE, "tag_base must be in [0, %d], got %d", PRNN_TAG_BASE_MAX,
+                tag_base);
+  return PRNN_OK;
+}
+
+// Zero what the call's look-back needs zeroed (see Lookback::tag_base).
+static int clear_status(const Lookback& lb, hipStream_t stream) {
+  return clear_words(lb.counters, lb.tag_base > 0 ? kMaxStages : lb.clear_words, stream);
+}
 
 static Lookback carve_lookback(Carver& cv, const Geo& g, int incl_vals, int agg_vals) {
   Lookback lb;

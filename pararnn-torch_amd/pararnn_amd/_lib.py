@@ -19,7 +19,7 @@ PRNN_OK = 0
 PRNN_ERR_VALUE = 1
 PRNN_ERR_TYPE = 2
 PRNN_ERR_RUNTIME = 3
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # name -> (restype, argtypes); mirrors include/pararnn_amd.h
 _P = ctypes.c_void_p
@@ -46,6 +46,13 @@ SIGNATURES: dict[str, tuple] = {
     "prnn_slstm_backward": (
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _I, _P, _S, _P],
+    ),
+    "prnn_slstm_init_ex": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _P, _S, _I, _P]),
+    "prnn_slstm_newton_ex": (
+        _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _I, _P, _S, _I, _P]),
+    "prnn_slstm_backward_ex": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _I, _P, _S, _I, _P],
     ),
     "prnn_gru_head_backward_workspace_size": (_S, [_I, _I, _I, _I, _I]),
     "prnn_gru_head_backward": (

@@ -14,6 +14,8 @@ and have fake kernels for ``torch.compile``.
 from __future__ import annotations
 
 import ctypes
+import os
+import threading
 
 import torch
 from torch import Tensor
@@ -50,6 +52,44 @@ def _stream(dev: torch.device) -> ctypes.c_void_p:
 
 def _workspace(nbytes: int, dev: torch.device) -> Tensor:
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
+
+
+# Tagged sLSTM workspaces: one zero-filled buffer per (device, stream), kept
+# across calls, with a growing tag base, so a call skips clearing its
+# look-back words (prnn_slstm_*_ex).  Only the library writes these buffers;
+# calls on one stream run in order.  Graph capture takes a fresh, cleared
+# workspace per call (a replay would repeat captured tags).
+_TAG_SPAN = 64           # PRNN_TAG_SPAN
+_TAG_BASE_MAX = 1 << 30  # PRNN_TAG_BASE_MAX
+_tagged_lock = threading.Lock()
+_tagged: dict[tuple[int, int], list] = {}
+
+
+def _tagged_enabled() -> bool:
+    return os.environ.get("PARARNN_AMD_TAGGED_WS", "1") != "0"
+
+
+def _slstm_workspace(nbytes: int, dev: torch.device) -> tuple[Tensor, int]:
+    """``(workspace, tag_base)`` for an sLSTM call on the current stream."""
+    if not _tagged_enabled() or torch.cuda.is_current_stream_capturing():
+        return _workspace(nbytes, dev), 0
+    stream = torch.cuda.current_stream(dev)
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), stream.cuda_stream)
+    with _tagged_lock:
+        ent = _tagged.get(key)
+        if ent is None or ent[0].numel() < nbytes or ent[1] + _TAG_SPAN > _TAG_BASE_MAX:
+            # Zero-filled on this stream, ahead of the call that uses it.
+            ent = [torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=dev), 1]
+            _tagged[key] = ent
+        base = ent[1]
+        ent[1] += _TAG_SPAN
+        return ent[0], base
+
+
+def release_workspaces() -> None:
+    """Drop the cached sLSTM workspaces (they are re-created on demand)."""
+    with _tagged_lock:
+        _tagged.clear()
 
 
 # ---------------------------------------------------------------------------
@@ -100,10 +140,10 @@ def slstm_init_fused(
     _lib.sync_deterministic(lib)
     with torch.cuda.device(wx.device):
         nbytes = lib.prnn_slstm_init_workspace_size(batch, time, d_h, picard_iters, code)
-        ws = _workspace(nbytes, wx.device)
-        rc = lib.prnn_slstm_init(
+        ws, tag = _slstm_workspace(nbytes, wx.device)
+        rc = lib.prnn_slstm_init_ex(
             _ptr(wx), _ptr(r), _ptr(h0), _ptr(out), batch, time, d_h, int(picard_iters),
-            float(eps), code, _ptr(ws), ws.numel(), _stream(wx.device),
+            float(eps), code, _ptr(ws), ws.numel(), tag, _stream(wx.device),
         )
     _lib.check(rc, "slstm_init_fused")
     return out
@@ -168,10 +208,10 @@ def newton_slstm_fused(
     _lib.sync_deterministic(lib)
     with torch.cuda.device(wx.device):
         nbytes = lib.prnn_slstm_newton_workspace_size(batch, time, d_h, int(max_iters), code)
-        ws = _workspace(nbytes, wx.device)
-        rc = lib.prnn_slstm_newton(
+        ws, tag = _slstm_workspace(nbytes, wx.device)
+        rc = lib.prnn_slstm_newton_ex(
             _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), _ptr(out), batch, time, d_h,
-            int(max_iters), float(omega), float(eps), code, _ptr(ws), ws.numel(),
+            int(max_iters), float(omega), float(eps), code, _ptr(ws), ws.numel(), tag,
             _stream(wx.device),
         )
     _lib.check(rc, "newton_slstm_fused")
@@ -214,10 +254,11 @@ def slstm_backward_fused(
     _lib.sync_deterministic(lib)
     with torch.cuda.device(wx.device):
         nbytes = lib.prnn_slstm_backward_workspace_size(batch, time, d_h, code)
-        ws = _workspace(nbytes, wx.device)
-        rc = lib.prnn_slstm_backward(
+        ws, tag = _slstm_workspace(nbytes, wx.device)
+        rc = lib.prnn_slstm_backward_ex(
             _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), _ptr(grad), _ptr(g_wx), _ptr(g_r),
-            _ptr(g_h0), batch, time, d_h, float(eps), code, _ptr(ws), ws.numel(), _stream(wx.device),
+            _ptr(g_h0), batch, time, d_h, float(eps), code, _ptr(ws), ws.numel(), tag,
+            _stream(wx.device),
         )
     _lib.check(rc, "slstm_backward_fused")
     return g_wx, g_r, g_h0

@@ -25,7 +25,8 @@ def test_header_declares_entry_points():
                  "prnn_slstm_backward", "prnn_gru_head_backward", "prnn_slstm_decode",
                  "prnn_gru_decode", "prnn_last_error", "prnn_abi_version",
                  "prnn_set_deterministic", "prnn_deterministic", "prnn_set_kernel_timing",
-                 "prnn_last_kernel_ms"):
+                 "prnn_last_kernel_ms", "prnn_slstm_init_ex", "prnn_slstm_newton_ex",
+                 "prnn_slstm_backward_ex"):
         assert name in decl
 
 
@@ -79,3 +80,12 @@ def test_host_only_calls():
     rc = lib.prnn_gru_head_backward(None, None, None, None, None, None, None, None, None, None,
                                     1, 1, 1, 64, 0, None, 0, None)
     assert rc == _lib.PRNN_ERR_VALUE
+    rc = lib.prnn_slstm_newton_ex(None, None, None, None, None, 1, 1, 1, 1, 1.0, 1e-6, 0,
+                                  None, 0, -1, None)
+    assert rc == _lib.PRNN_ERR_VALUE and b"tag_base" in lib.prnn_last_error()
+    rc = lib.prnn_slstm_init_ex(None, None, None, None, 1, 1, 1, 0, 1e-6, 0, None, 0,
+                                (1 << 30) + 1, None)
+    assert rc == _lib.PRNN_ERR_VALUE and b"tag_base" in lib.prnn_last_error()
+    rc = lib.prnn_slstm_backward_ex(None, None, None, None, None, None, None, None, 1, 1, 1,
+                                    1e-6, 0, None, 0, 5, None)
+    assert rc == _lib.PRNN_ERR_VALUE and b"non-null" in lib.prnn_last_error()

@@ -166,3 +166,51 @@ def test_gru_head_bitmatch_default_mode():
     eq = _bitequal(a, b)
     print(f"  bit-equal: {eq}", flush=True)
     assert all(eq.values()), eq
+
+
+def test_tagged_workspace_matches_cleared(monkeypatch):
+    """The cached, tag-based sLSTM workspace gives bit-identical results to a
+    fresh, cleared workspace per call (deterministic mode makes both exact),
+    over a sequence of calls whose shapes grow and shrink, across a forced
+    re-zero at the tag limit."""
+    from pararnn_amd import ops
+
+    prev = torch.are_deterministic_algorithms_enabled()
+    torch.use_deterministic_algorithms(True, warn_only=True)
+    try:
+        shapes = [(1, 4096, 256), (2, 8192, 128), (1, 2048, 512), (2, 8192, 128), (1, 4096, 256)]
+        g = torch.Generator().manual_seed(5)
+        cases = []
+        for B, T, d in shapes:
+            wx = (0.5 * torch.randn(B, T, 4 * d, generator=g)).to(DEV, torch.bfloat16)
+            r = (0.3 * torch.rand(4, d, generator=g) - 0.15).to(DEV, torch.bfloat16)
+            grad = torch.randn(B, T, 4, d, generator=g).to(DEV, torch.bfloat16)
+            cases.append((wx, r, grad))
+
+        def run_all():
+            outs = []
+            for wx, r, grad in cases:
+                guess = ops.slstm_init_fused(wx, r, None, picard_iters=5, eps=1e-6)
+                H = ops.newton_slstm_fused(wx, r, None, guess, max_iters=2, omega=1.0, eps=1e-6)
+                g_wx, g_r, _ = ops.slstm_backward_fused(wx, r, None, H, grad, eps=1e-6)
+                outs.append((guess, H, g_wx, g_r))
+            torch.cuda.synchronize()
+            return outs
+
+        print("case tagged workspace vs cleared workspace (5 shapes x 3 ops)", flush=True)
+        monkeypatch.setenv("PARARNN_AMD_TAGGED_WS", "0")
+        ref = run_all()
+        monkeypatch.setenv("PARARNN_AMD_TAGGED_WS", "1")
+        ops.release_workspaces()
+        got = run_all()
+        got2 = run_all()  # the cached buffer, tags well past the first pass
+        monkeypatch.setattr(ops, "_TAG_BASE_MAX", 64 * 7)  # forces re-zeroed buffers
+        got3 = run_all()
+        for a, b, c, e in zip(ref, got, got2, got3):
+            for x, y, z, w in zip(a, b, c, e):
+                assert torch.equal(x.view(torch.uint8), y.view(torch.uint8))
+                assert torch.equal(x.view(torch.uint8), z.view(torch.uint8))
+                assert torch.equal(x.view(torch.uint8), w.view(torch.uint8))
+    finally:
+        torch.use_deterministic_algorithms(prev)
+        ops.release_workspaces()
