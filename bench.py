@@ -73,6 +73,26 @@ def _time_kernel(torch, fn, reps, warm=2):
     return total / reps
 
 
+def _literal_config(torch, cell, x):
+    """One newton_apply with the literal NewtonConfig(max_iters=2): the resolved
+    Picard passes, iterations, residual and whether the gate raised."""
+    from pararnn_amd import NewtonConfig, NewtonDivergenceError, NewtonStats, newton_apply
+
+    st = NewtonStats()
+    s, e = _events(torch)
+    s.record()
+    raised = None
+    try:
+        newton_apply(cell, x, NewtonConfig(max_iters=2), stats=st)
+    except NewtonDivergenceError as err:
+        raised = f"NewtonDivergenceError: {str(err)[:160]}"
+    e.record()
+    torch.cuda.synchronize()
+    return {"config": "NewtonConfig(max_iters=2)", "ms_one_run": s.elapsed_time(e),
+            "picard_iters": st.picard_iters, "iters": st.iters,
+            "max_residual": st.max_residual, "scan_backend": st.scan_backend, "raised": raised}
+
+
 def _traffic_from_profile(name: str):
     """HBM bytes per launch measured with rocprofv3 --pmc (committed summary)."""
     path = os.path.join(REPO, "profiles", name)
@@ -135,6 +155,7 @@ def train_cfg5(torch, reps: int):
         r = cell.clipped_r()
         ms_bwd = _time(torch, lambda: ops.slstm_backward_fused(wx, r, None, H, up, eps=cell.eps),
                        reps)
+        literal = _literal_config(torch, cell, x)
     elems = b5 * t5 * d5
     # reverse-scan kernel bytes per (b, t, channel): read wx 8, H* 8, dL/dH 8,
     # write dL/dwx 8 (bf16)
@@ -147,6 +168,7 @@ def train_cfg5(torch, reps: int):
         "bwd_kernel_ms": ms_bwd,
         "bwd_kernel_GBps": ach,
         "bwd_kernel_frac": ach / HBM_PEAK_GBS,
+        "literal_config": literal,
     }
 
 
@@ -168,6 +190,7 @@ def slstm_cfg2(torch, reps: int):
         ms = _time(torch, lambda: fused_newton(cell, wx, max_iters=K, omega=1.0, h0=None,
                                                picard_iters=P), reps)
         ms_e2e = _time(torch, lambda: newton_apply(cell, x, cfg), reps)
+        literal = _literal_config(torch, cell, x)
     tokens = b2 * t2
     step_bytes = tokens * D * ((4 * 2 + 16) + P * (4 * 2 + 20) + K * (4 * 2 + 32))
     return {
@@ -177,6 +200,7 @@ def slstm_cfg2(torch, reps: int):
         "step_roofline_frac": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "newton_apply_ms": ms_e2e,
         "newton_apply_tokens_per_s": tokens / (ms_e2e * 1e-3),
+        "literal_config": literal,
     }
 
 
@@ -204,6 +228,8 @@ def head_cfg4(torch, reps: int):
             a = cell.clipped_a_head()
             res["bwd_op_fp32_ms"] = _time(
                 torch, lambda: ops.gru_head_backward_fused(wx, *a, None, H, up), reps)
+            if tag == "cfg4":
+                res["literal_config"] = _literal_config(torch, cell, x)
 
         def step():
             cell.zero_grad(set_to_none=True)
@@ -304,6 +330,13 @@ def main() -> int:
         cfg = NewtonConfig(max_iters=K, picard_iters=P, residual_atol=None, residual_fail=None,
                            picard_adapt=False)
         ms_e2e = _time(torch, lambda: newton_apply(cell, x, cfg), max(3, reps // 2), warm=1)
+        # The same with the residual gate on (one extra cell pass and its
+        # reduction), and the literal NewtonConfig(max_iters=2) once: what the
+        # default auto-P, Picard adapt and the residual gate resolve to.
+        cfg_gate = NewtonConfig(max_iters=K, picard_iters=P, residual_atol=1e-5,
+                                residual_fail=None, picard_adapt=False)
+        ms_gate = _time(torch, lambda: newton_apply(cell, x, cfg_gate), max(3, reps // 2), warm=1)
+        literal = _literal_config(torch, cell, x)
 
     elems = B * T * D
     s_x = 2
@@ -375,6 +408,8 @@ def main() -> int:
         "gemm_ms": ms_gemm,
         "newton_apply_ms": ms_e2e,
         "newton_apply_tokens_per_s": tokens / (ms_e2e * 1e-3),
+        "newton_apply_gate_ms": ms_gate,
+        "literal_config": literal,
         "wall_s_timed_region": t_wall,
     }
     out["slstm_cfg2"] = slstm_cfg2(torch, max(3, args.steps // 4))
