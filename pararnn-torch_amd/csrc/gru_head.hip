@@ -713,6 +713,184 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Replay on the matrix cores.  The chunks of one sequence share A_z, A_r,
+// A_n, so a step of 16 chunks side by side is three 64x64 by 64x16 fp32
+// products: wave w of a block takes chunks c = 16 (4 grp + w) + n, lane
+// (n, g) = (l % 16, l / 16) holding rows 16 T + 4 g + v (T, v = 0..3) of
+// chunk n's delta, which is the fp32 MFMA accumulator layout.  With the
+// contraction index permuted (MFMA (Tc, v) contracts over rows
+// 16 Tc + 4 g + v), that accumulator is directly the B operand of the next
+// product, so delta never leaves the registers; the matching A operands,
+// A[16 Tc + 4 (l / 16) + v][16 To + l % 16], are staged once per block in
+// LDS.  Same recurrence, gates and outputs as gru_replay_kernel; the
+// 64-term sums are accumulated in the MFMA's order (fp32 products and sums).
+// A chunk past the end of the sequence is a zero column: columns of an
+// MFMA product do not mix.
+// ---------------------------------------------------------------------------
+constexpr int kRCols = 16;  // chunks per wave (the MFMA N dimension)
+#ifndef PRNN_RM_WPE
+#define PRNN_RM_WPE 1
+#endif
+#ifndef PRNN_RM_LDS
+#define PRNN_RM_LDS 0
+#endif
+
+template <typename T>
+__device__ __forceinline__ void st4(T* p, floatx4 v) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<floatx4*>(p) = v;
+  } else {
+    uint2 w;
+    w.x = pack_bf16x2(v[0], v[1]);
+    w.y = pack_bf16x2(v[2], v[3]);
+    *reinterpret_cast<uint2*>(p) = w;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ floatx4 ld4(const T* p) {
+  if constexpr (sizeof(T) == 4) {
+    return *reinterpret_cast<const floatx4*>(p);
+  } else {
+    const uint2 w = *reinterpret_cast<const uint2*>(p);
+    return floatx4{lo_bf16(w.x), hi_bf16(w.x), lo_bf16(w.y), hi_bf16(w.y)};
+  }
+}
+
+template <typename TX, typename TOUT, bool LOCAL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PRNN_RM_WPE))) void gru_replay_mfma_kernel(
+    const TX* __restrict__ a_z, const TX* __restrict__ a_r, const TX* __restrict__ a_n,
+    const TX* __restrict__ h0, const float* __restrict__ hin, const float* __restrict__ gates,
+    const float* __restrict__ carry_in, TOUT* __restrict__ hout, float* __restrict__ e_out,
+    int B, int T, int H, int n_chunks, float omega) {
+  // [matrix][output tile][contraction tile][lane] -> the 4 A operands v = 0..3
+  __shared__ floatx4 sA[3][4][4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n_grp = (n_chunks + 4 * kRCols - 1) / (4 * kRCols);
+  const int seq = blockIdx.x / n_grp, grp = blockIdx.x % n_grp;
+  const int b = seq / H, head = seq % H;
+  const int d = H * DH;
+  for (int e = threadIdx.x; e < 3 * 4 * 4 * 64; e += 256) {
+    const int l = e & 63, tc = (e >> 6) & 3, to = (e >> 8) & 3, m = e >> 10;
+    const TX* A = (m == 0 ? a_z : m == 1 ? a_r : a_n) + static_cast<size_t>(head) * DH * DH;
+    floatx4 v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = ld(A + (16 * tc + 4 * (l >> 4) + q) * DH + 16 * to + (l & 15));
+    sA[m][to][tc][l] = v;
+  }
+  __syncthreads();
+  const int c_first = (grp * 4 + wave) * kRCols;
+  if (c_first >= n_chunks) return;  // whole wave exits together (no barrier follows)
+  const int n = lane & 15, g = lane >> 4;
+  const int c = c_first + n;
+  const bool valid = c < n_chunks;
+  const int t0 = c * kChunk;
+  const int len = valid ? min(kChunk, T - t0) : 0;
+  const size_t id = static_cast<size_t>(seq) * n_chunks + (valid ? c : c_first);
+  const float* gt = gates + id * kChunk * 3 * DH + 4 * g;
+  floatx4 dl[4];
+#pragma unroll
+  for (int to = 0; to < 4; ++to) {
+    dl[to] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (!LOCAL && valid) dl[to] = *reinterpret_cast<const floatx4*>(carry_in + id * DH + 16 * to + 4 * g);
+  }
+  const int steps = min(kChunk, T - c_first * kChunk);  // the wave's longest chunk
+  struct In {
+    floatx4 hp[4], ht[4], gz[4], gr[4], gn[4];
+  };
+  // Step s's inputs (zeros past the chunk's end); loaded one step ahead.  h at
+  // t - 1 is the previous step's h at t except at the chunk's first step.
+  auto load_in = [&](int s, In& v, const floatx4* h_prev) {
+    const bool act = s < len;
+    const int t = t0 + s;
+#pragma unroll
+    for (int to = 0; to < 4; ++to) {
+      const floatx4 zero{0.f, 0.f, 0.f, 0.f};
+      v.hp[to] = v.ht[to] = v.gz[to] = v.gr[to] = v.gn[to] = zero;
+      if (act) {
+        const int j = 16 * to + 4 * g;
+        if (h_prev != nullptr)
+          v.hp[to] = h_prev[to];
+        else if (t > 0)
+          v.hp[to] = *reinterpret_cast<const floatx4*>(hin + h_at(b, t - 1, T, d, head, j));
+        else if (h0 != nullptr)
+          v.hp[to] = ld4(h0 + static_cast<size_t>(b) * d + head * DH + j);
+        v.ht[to] = *reinterpret_cast<const floatx4*>(hin + h_at(b, t, T, d, head, j));
+        v.gz[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3) * DH + 16 * to);
+        v.gr[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3 + 1) * DH + 16 * to);
+        v.gn[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3 + 2) * DH + 16 * to);
+      }
+    }
+  };
+  In nx;
+  load_in(0, nx, nullptr);
+  for (int s = 0; s < steps; ++s) {
+    const bool act = s < len;
+    const int t = t0 + s;
+    const In cur = nx;
+    if (s + 1 < steps) load_in(s + 1, nx, cur.ht);
+    const floatx4 *hp = cur.hp, *ht = cur.ht, *gz = cur.gz, *gr = cur.gr, *gn = cur.gn;
+#if PRNN_RM_LDS
+    asm volatile("" ::: "memory");  // A operands are re-read from LDS every step
+#endif
+    // J delta = (1-z) delta + d2 (delta @ A_z) + d3 ((r delta + d5 (delta @ A_r)) @ A_n)
+    floatx4 yz[4], yr[4], yn[4], vv[4];
+#pragma unroll
+    for (int to = 0; to < 4; ++to) yz[to] = yr[to] = yn[to] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int tc = 0; tc < 4; ++tc) {
+#pragma unroll
+      for (int to = 0; to < 4; ++to) {
+        const floatx4 az = sA[0][to][tc][lane], ar = sA[1][to][tc][lane];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          yz[to] = mfma_f32(az[v], dl[tc][v], yz[to]);
+          yr[to] = mfma_f32(ar[v], dl[tc][v], yr[to]);
+        }
+      }
+    }
+#pragma unroll
+    for (int to = 0; to < 4; ++to)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float r = gr[to][v];
+        const float d5 = hp[to][v] * r * (1.f - r);
+        vv[to][v] = r * dl[to][v] + d5 * yr[to][v];
+      }
+#pragma unroll
+    for (int tc = 0; tc < 4; ++tc) {
+#pragma unroll
+      for (int to = 0; to < 4; ++to) {
+        const floatx4 an = sA[2][to][tc][lane];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) yn[to] = mfma_f32(an[v], vv[tc][v], yn[to]);
+      }
+    }
+    if (act) {
+#pragma unroll
+      for (int to = 0; to < 4; ++to) {
+        floatx4 o;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float z = gz[to][v], nv = gn[to][v], h = hp[to][v];
+          const float d2 = (nv - h) * z * (1.f - z);
+          const float d3 = z * (1.f - nv * nv);
+          const float h_new = lerp_t(h, nv, z);
+          dl[to][v] = (1.f - z) * dl[to][v] + d2 * yz[to][v] + d3 * yn[to][v] + (h_new - ht[to][v]);
+          o[v] = ht[to][v] + omega * dl[to][v];
+        }
+        if (!LOCAL) st4(hout + h_at(b, t, T, d, head, 16 * to + 4 * g), o);
+      }
+    }
+  }
+  if (LOCAL && valid) {
+#pragma unroll
+    for (int to = 0; to < 4; ++to)
+      *reinterpret_cast<floatx4*>(e_out + id * DH + 16 * to + 4 * g) = dl[to];
+  }
+}
+
 // ===========================================================================
 // Eq. 2.6 backward at the solved trajectory H* (reference
 // solvers/newton/__init__.py:765-866 with the head Jacobian, kernels/
@@ -913,6 +1091,152 @@ __global__ __launch_bounds__(256) void gru_rev_local_kernel(
     if (len[k] > 0) e_out[(static_cast<size_t>(seq) * n_chunks + c0 + k) * DH + lane] = nu[k];
 }
 
+// Reverse walks on the matrix cores: 16 chunks of a sequence per wave, as in
+// gru_replay_mfma_kernel, with the products A_z D_z, A_n D_n and A_r D_r (rows
+// of the untransposed matrices: A operand A[16 To + l % 16][16 Tc + 4 (l / 16)
+// + v]).  Columns step from the chunk's end down; a chunk shorter than the
+// wave's longest reads zeros on the steps past its end, which leave nu
+// unchanged.  LOCAL: nu from zero, writing each chunk's final nu (e);
+// otherwise from the chunk's carry, writing the pre-activation gradients
+// g_wx and, for chunk 0, grad h0 = nu_0.
+template <typename TX, bool LOCAL>
+__global__ __launch_bounds__(256) void gru_rev_mfma_kernel(
+    const TX* __restrict__ a_z, const TX* __restrict__ a_r, const TX* __restrict__ a_n,
+    const TX* __restrict__ h0, const TX* __restrict__ states, const TX* __restrict__ grad,
+    const float* __restrict__ gates, const float* __restrict__ carry_in, TX* __restrict__ g_wx,
+    float* __restrict__ g_h0, float* __restrict__ e_out, int B, int T, int H, int n_chunks) {
+  __shared__ floatx4 sA[3][4][4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n_grp = (n_chunks + 4 * kRCols - 1) / (4 * kRCols);
+  const int seq = blockIdx.x / n_grp, grp = blockIdx.x % n_grp;
+  const int b = seq / H, head = seq % H;
+  const int d = H * DH;
+  for (int e = threadIdx.x; e < 3 * 4 * 4 * 64; e += 256) {
+    const int l = e & 63, tc = (e >> 6) & 3, to = (e >> 8) & 3, m = e >> 10;
+    const TX* A = (m == 0 ? a_z : m == 1 ? a_r : a_n) + static_cast<size_t>(head) * DH * DH;
+    floatx4 v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = ld(A + (16 * to + (l & 15)) * DH + 16 * tc + 4 * (l >> 4) + q);
+    sA[m][to][tc][l] = v;
+  }
+  __syncthreads();
+  const int c_first = (grp * 4 + wave) * kRCols;
+  if (c_first >= n_chunks) return;  // whole wave exits together (no barrier follows)
+  const int n = lane & 15, g = lane >> 4;
+  const int c = c_first + n;
+  const bool valid = c < n_chunks;
+  const int t0 = c * kChunk;
+  const int len = valid ? min(kChunk, T - t0) : 0;
+  const size_t id = static_cast<size_t>(seq) * n_chunks + (valid ? c : c_first);
+  const float* gt = gates + id * kChunk * 3 * DH + 4 * g;
+  floatx4 nu[4];
+#pragma unroll
+  for (int to = 0; to < 4; ++to) {
+    nu[to] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (!LOCAL && valid) nu[to] = *reinterpret_cast<const floatx4*>(carry_in + id * DH + 16 * to + 4 * g);
+  }
+  const int steps = min(kChunk, T - c_first * kChunk);  // the wave's longest chunk
+  struct In {
+    floatx4 hp[4], gr_[4], z[4], r[4], nn[4];
+  };
+  auto load_in = [&](int s, In& v) {
+    const bool act = s >= 0 && s < len;
+    const int t = t0 + s;
+#pragma unroll
+    for (int to = 0; to < 4; ++to) {
+      const floatx4 zero{0.f, 0.f, 0.f, 0.f};
+      v.hp[to] = v.gr_[to] = v.z[to] = v.r[to] = v.nn[to] = zero;
+      if (act) {
+        const int j = 16 * to + 4 * g;
+        if (t > 0)
+          v.hp[to] = ld4(states + h_at(b, t - 1, T, d, head, j));
+        else if (h0 != nullptr)
+          v.hp[to] = ld4(h0 + static_cast<size_t>(b) * d + head * DH + j);
+        v.gr_[to] = ld4(grad + h_at(b, t, T, d, head, j));
+        v.z[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3) * DH + 16 * to);
+        v.r[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3 + 1) * DH + 16 * to);
+        v.nn[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3 + 2) * DH + 16 * to);
+      }
+    }
+  };
+  In nx;
+  load_in(steps - 1, nx);
+  for (int s = steps - 1; s >= 0; --s) {
+    const bool act = s < len;
+    const int t = t0 + s;
+    const In cur = nx;
+    if (s > 0) load_in(s - 1, nx);
+    // mu = g + nu;  d_zpre = mu (n - h) z(1-z);  d_npre = mu z (1-n^2)
+    floatx4 mu[4], dz[4], dn[4], dr[4], tz[4], du[4], tr[4];
+#pragma unroll
+    for (int to = 0; to < 4; ++to)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float z = cur.z[to][v], nv = cur.nn[to][v];
+        mu[to][v] = cur.gr_[to][v] + nu[to][v];
+        dz[to][v] = mu[to][v] * (nv - cur.hp[to][v]) * (z * (1.f - z));
+        dn[to][v] = mu[to][v] * z * (1.f - nv * nv);
+      }
+#pragma unroll
+    for (int to = 0; to < 4; ++to) tz[to] = du[to] = tr[to] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int tc = 0; tc < 4; ++tc) {
+#pragma unroll
+      for (int to = 0; to < 4; ++to) {
+        const floatx4 az = sA[0][to][tc][lane], an = sA[2][to][tc][lane];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          tz[to] = mfma_f32(az[v], dz[tc][v], tz[to]);
+          du[to] = mfma_f32(an[v], dn[tc][v], du[to]);
+        }
+      }
+    }
+    // d_rpre = d_u h r(1-r)
+#pragma unroll
+    for (int to = 0; to < 4; ++to)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float r = cur.r[to][v];
+        dr[to][v] = du[to][v] * cur.hp[to][v] * r * (1.f - r);
+      }
+#pragma unroll
+    for (int tc = 0; tc < 4; ++tc) {
+#pragma unroll
+      for (int to = 0; to < 4; ++to) {
+        const floatx4 ar = sA[1][to][tc][lane];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) tr[to] = mfma_f32(ar[v], dr[tc][v], tr[to]);
+      }
+    }
+    // nu <- (1-z) mu + A_z d_zpre + r d_u + A_r d_rpre
+#pragma unroll
+    for (int to = 0; to < 4; ++to)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        nu[to][v] = (1.f - cur.z[to][v]) * mu[to][v] + tz[to][v] + cur.r[to][v] * du[to][v] +
+                    tr[to][v];
+    if (!LOCAL && act) {
+#pragma unroll
+      for (int to = 0; to < 4; ++to) {
+        const int j = 16 * to + 4 * g;
+        st4(g_wx + wx_at(b, t, T, d, 0, head, j), dz[to]);
+        st4(g_wx + wx_at(b, t, T, d, 1, head, j), dr[to]);
+        st4(g_wx + wx_at(b, t, T, d, 2, head, j), dn[to]);
+      }
+    }
+  }
+  if (valid) {
+#pragma unroll
+    for (int to = 0; to < 4; ++to) {
+      const int j = 16 * to + 4 * g;
+      if (LOCAL)
+        *reinterpret_cast<floatx4*>(e_out + id * DH + j) = nu[to];
+      else if (c == 0 && g_h0 != nullptr)
+        *reinterpret_cast<floatx4*>(g_h0 + static_cast<size_t>(b) * d + head * DH + j) = nu[to];
+    }
+  }
+}
+
 // Partial sums of g_A[gate][head][i][o] = sum over rows k = (b, t) of
 // X_g[k][i] D_g[k][o] over one split of the B T rows, all three gates in one
 // block (X = h_prev for z and r, h_prev r for n; D the gate's pre-activation
@@ -1098,6 +1422,35 @@ static Ws carve(void* base, int B, int T, int H, int K, size_t* total) {
   return w;
 }
 
+// Forward replays on the matrix cores (gru_replay_mfma_kernel) when there are
+// enough 16-chunk groups to give every SIMD work; otherwise (short or few
+// sequences) the per-lane mat-vec kernel, whose waves take 2 chunks each.
+// PRNN_GRU_REPLAY_MFMA=1 / 0 forces one or the other (read per call); the
+// backward's reverse walks choose the same way (PRNN_GRU_REV_MFMA).
+constexpr int kReplayMfmaMinWaves = 512;
+
+static bool walks_mfma(const char* env, int n_seq, int n_chunks) {
+  if (const char* e = getenv(env)) return atoi(e) != 0;
+  return n_seq * ((n_chunks + kRCols - 1) / kRCols) >= kReplayMfmaMinWaves;
+}
+
+template <typename TX, typename TOUT, bool LOCAL>
+static void launch_replay(const TX* az, const TX* ar, const TX* an, const TX* h0,
+                          const float* hin, const float* gates, const float* carry, TOUT* out,
+                          float* e, int B, int T, int H, int n_chunks, float omega,
+                          hipStream_t stream) {
+  const int n_seq = B * H;
+  if (walks_mfma("PRNN_GRU_REPLAY_MFMA", n_seq, n_chunks)) {
+    const int n_grp = (n_chunks + 4 * kRCols - 1) / (4 * kRCols);
+    gru_replay_mfma_kernel<TX, TOUT, LOCAL><<<dim3(n_seq * n_grp), dim3(256), 0, stream>>>(
+        az, ar, an, h0, hin, gates, carry, out, e, B, T, H, n_chunks, omega);
+  } else {
+    const int blocks = (n_seq * ((n_chunks + kPair - 1) / kPair) + 3) / 4;
+    gru_replay_kernel<TX, TOUT, LOCAL><<<dim3(blocks), dim3(256), 0, stream>>>(
+        az, ar, an, h0, hin, gates, carry, out, e, B, T, H, n_chunks, omega);
+  }
+}
+
 template <typename TX>
 static int run(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX* h0, TX* out,
                int B, int T, int H, int K, float omega, const Ws& w, hipStream_t stream) {
@@ -1112,26 +1465,23 @@ static int run(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX*
   gru_init_kernel<TX, float><<<dim3(n_seq * n_blk64), dim3(64), 0, stream>>>(wx, az, ar, an, h0,
                                                                             w.work[0], B, T, H);
   PRNN_HIP(hipGetLastError());
-  const int replay_blocks = (n_seq * ((n_chunks + kPair - 1) / kPair) + 3) / 4;
   for (int k = 1; k <= K; ++k) {
     const float* hin = w.work[(k - 1) & 1];
     gru_phi_kernel<TX, float, false><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
         wx, az, ar, an, h0, hin, B, T, H, n_chunks, w.phi, w.gates);
     PRNN_HIP(hipGetLastError());
-    gru_replay_kernel<TX, float, true><<<dim3(replay_blocks), dim3(256), 0, stream>>>(
-        az, ar, an, h0, hin, w.gates, nullptr, static_cast<float*>(nullptr), w.e, B, T, H,
-        n_chunks, omega);
+    launch_replay<TX, float, true>(az, ar, an, h0, hin, w.gates, nullptr,
+                                   static_cast<float*>(nullptr), w.e, B, T, H, n_chunks, omega,
+                                   stream);
     PRNN_HIP(hipGetLastError());
     carry_scan<false>(w.phi, w.e, w.carry, n_seq, n_chunks, w.cs, stream);
     PRNN_HIP(hipGetLastError());
-    if (k == K) {
-      gru_replay_kernel<TX, TX, false><<<dim3(replay_blocks), dim3(256), 0, stream>>>(
-          az, ar, an, h0, hin, w.gates, w.carry, out, nullptr, B, T, H, n_chunks, omega);
-    } else {
-      gru_replay_kernel<TX, float, false><<<dim3(replay_blocks), dim3(256), 0, stream>>>(
-          az, ar, an, h0, hin, w.gates, w.carry, w.work[k & 1], nullptr, B, T, H, n_chunks,
-          omega);
-    }
+    if (k == K)
+      launch_replay<TX, TX, false>(az, ar, an, h0, hin, w.gates, w.carry, out, nullptr, B, T, H,
+                                   n_chunks, omega, stream);
+    else
+      launch_replay<TX, float, false>(az, ar, an, h0, hin, w.gates, w.carry, w.work[k & 1],
+                                      nullptr, B, T, H, n_chunks, omega, stream);
     PRNN_HIP(hipGetLastError());
   }
   return PRNN_OK;
@@ -1182,17 +1532,29 @@ static int run_bwd(const TX* wx, const TX* az, const TX* ar, const TX* an, const
   const int n_seq = B * H, n_chunks = (T + kChunk - 1) / kChunk;
   const int rev_blocks_local = (n_seq * ((n_chunks + kPair - 1) / kPair) + 3) / 4;
   const int rev_blocks = (n_seq * n_chunks + 3) / 4;
+  const bool mfma_walks = walks_mfma("PRNN_GRU_REV_MFMA", n_seq, n_chunks);
+  const int mfma_blocks = n_seq * ((n_chunks + 4 * kRCols - 1) / (4 * kRCols));
   gru_phi_kernel<TX, TX, true><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
       wx, az, ar, an, h0, states, B, T, H, n_chunks, w.phi, w.gates);
   PRNN_HIP(hipGetLastError());
-  gru_rev_local_kernel<TX><<<dim3(rev_blocks_local), dim3(256), 0, stream>>>(
-      az, ar, an, h0, states, grad, w.gates, w.e, B, T, H, n_chunks);
+  if (mfma_walks)
+    gru_rev_mfma_kernel<TX, true><<<dim3(mfma_blocks), dim3(256), 0, stream>>>(
+        az, ar, an, h0, states, grad, w.gates, nullptr, nullptr, nullptr, w.e, B, T, H,
+        n_chunks);
+  else
+    gru_rev_local_kernel<TX><<<dim3(rev_blocks_local), dim3(256), 0, stream>>>(
+        az, ar, an, h0, states, grad, w.gates, w.e, B, T, H, n_chunks);
   PRNN_HIP(hipGetLastError());
   carry_scan<true>(w.phi, w.e, w.carry, n_seq, n_chunks, w.cs, stream);
   PRNN_HIP(hipGetLastError());
-  gru_rev_kernel<TX><<<dim3(rev_blocks), dim3(256), 0, stream>>>(
-      az, ar, an, h0, states, grad, w.gates, w.carry, g_wx, h0 != nullptr ? g_h0 : nullptr,
-      B, T, H, n_chunks);
+  if (mfma_walks)
+    gru_rev_mfma_kernel<TX, false><<<dim3(mfma_blocks), dim3(256), 0, stream>>>(
+        az, ar, an, h0, states, grad, w.gates, w.carry, g_wx, h0 != nullptr ? g_h0 : nullptr,
+        nullptr, B, T, H, n_chunks);
+  else
+    gru_rev_kernel<TX><<<dim3(rev_blocks), dim3(256), 0, stream>>>(
+        az, ar, an, h0, states, grad, w.gates, w.carry, g_wx, h0 != nullptr ? g_h0 : nullptr,
+        B, T, H, n_chunks);
   PRNN_HIP(hipGetLastError());
   gru_ga_kernel<TX><<<dim3(w.n_split * H), dim3(256), 0, stream>>>(
       h0, states, w.gates, g_wx, B, T, H, n_chunks, w.n_split, w.rows_per, w.part);

@@ -529,12 +529,14 @@ def _weight_grad(gy: Tensor, xx: Tensor) -> Tensor:
     reductions run as a batched GEMM over row blocks with fp32 partials, summed
     and rounded once."""
     n = int(gy.shape[0])
-    if gy.is_cuda and gy.dtype in (torch.bfloat16, torch.float16) and n >= 65536:
-        split = next((k for k in (16, 8, 4) if n % k == 0 and n // k >= 4096), 1)
+    if gy.is_cuda and n >= 65536 and gy.dtype in (torch.bfloat16, torch.float16, torch.float32):
+        split = next((k for k in (32, 16, 8, 4) if n % k == 0 and n // k >= 4096), 1)
         if split > 1:
-            part = torch.bmm(gy.view(split, n // split, -1).transpose(1, 2),
-                             xx.view(split, n // split, -1), out_dtype=torch.float32)
-            return part.sum(0).to(gy.dtype)
+            a = gy.view(split, n // split, -1).transpose(1, 2)
+            b = xx.view(split, n // split, -1)
+            if gy.dtype == torch.float32:
+                return torch.bmm(a, b).sum(0)
+            return torch.bmm(a, b, out_dtype=torch.float32).sum(0).to(gy.dtype)
     return gy.t() @ xx
 
 

@@ -20,6 +20,13 @@ def _cfg(K):
     return NewtonConfig(max_iters=K, residual_atol=None, residual_fail=None)
 
 
+@pytest.fixture(params=["vec", "mfma"])
+def replay_kernel(request, monkeypatch):
+    """Run with each forward replay kernel (per-lane mat-vecs / matrix cores)."""
+    monkeypatch.setenv("PRNN_GRU_REPLAY_MFMA", "1" if request.param == "mfma" else "0")
+    return request.param
+
+
 def _cell(t, m, dtype):
     from pararnn_amd import ParaGRU
 
@@ -54,7 +61,7 @@ def test_mfma_operand_layout():
 
 
 @pytest.mark.parametrize("name", ["gru_head_fp32", "gru_head_h0_fp32"])
-def test_fp32_matches_reference_eager(name):
+def test_fp32_matches_reference_eager(name, replay_kernel):
     from pararnn_amd import newton_apply
 
     print(f"case {name}", flush=True)
@@ -69,7 +76,7 @@ def test_fp32_matches_reference_eager(name):
     assert err <= 1e-5
 
 
-def test_bf16_matches_fused_semantics():
+def test_bf16_matches_fused_semantics(replay_kernel):
     from pararnn_amd import newton_apply
 
     print("case gru_head_bf16", flush=True)
@@ -93,11 +100,12 @@ def test_bf16_matches_fused_semantics():
 
 @pytest.mark.parametrize("B,T,H,K,with_h0", [
     (1, 1, 1, 1, False), (3, 70, 2, 2, True), (2, 33, 1, 0, True), (1, 200, 3, 4, False),
+    (2, 1000, 2, 2, True), (1, 1700, 1, 3, False),
 ])
-def test_ragged_shapes_vs_oracle(B, T, H, K, with_h0):
+def test_ragged_shapes_vs_oracle(B, T, H, K, with_h0, replay_kernel):
     from pararnn_amd import ParaGRU, newton_apply
 
-    print(f"case ragged B={B} T={T} H={H} K={K} h0={with_h0}", flush=True)
+    print(f"case ragged B={B} T={T} H={H} K={K} h0={with_h0} replay={replay_kernel}", flush=True)
     torch.manual_seed(T * 7 + H)
     cell = ParaGRU(10, 64 * H, mix="head", n_heads=H)
     x = torch.randn(B, T, 10) * 1.5

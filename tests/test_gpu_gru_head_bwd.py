@@ -52,7 +52,7 @@ def _rel(a, b):
     return ((a.float() - b.float()).abs().max() / b.float().abs().max().clamp_min(1e-30)).item()
 
 
-def test_op_at_reference_trajectory_fp32():
+def test_op_at_reference_trajectory_fp32(walk_kernel):
     print("case gru_head_bwd_fp32 op at reference H*", flush=True)
     t, m = load_golden("gru_head_bwd_fp32")
     p = _params(t)
@@ -84,7 +84,7 @@ def test_autograd_matches_reference_grads_fp32():
         assert e <= 1e-4, k
 
 
-def test_op_at_reference_trajectory_bf16():
+def test_op_at_reference_trajectory_bf16(walk_kernel):
     print("case gru_head_bwd_bf16 op at reference H*", flush=True)
     t, m = load_golden("gru_head_bwd_bf16")
     p = _params(t)
@@ -106,10 +106,19 @@ def test_op_at_reference_trajectory_bf16():
     assert e <= 3e-2
 
 
+@pytest.fixture(params=["vec", "mfma"])
+def walk_kernel(request, monkeypatch):
+    """Run with each reverse-walk kernel (per-lane mat-vecs / matrix cores)."""
+    monkeypatch.setenv("PRNN_GRU_REV_MFMA", "1" if request.param == "mfma" else "0")
+    return request.param
+
+
 @pytest.mark.parametrize("B,T,H,with_h0", [(1, 1, 1, True), (2, 33, 1, False),
-                                           (2, 1000, 4, True), (1, 4096, 2, True)])
-def test_op_vs_oracle_float64(B, T, H, with_h0):
-    print(f"case op vs float64 oracle B={B} T={T} H={H} h0={with_h0}", flush=True)
+                                           (2, 1000, 4, True), (1, 4096, 2, True),
+                                           (1, 1700, 1, True)])
+def test_op_vs_oracle_float64(B, T, H, with_h0, walk_kernel):
+    print(f"case op vs float64 oracle B={B} T={T} H={H} h0={with_h0} walks={walk_kernel}",
+          flush=True)
     g = torch.Generator().manual_seed(B * 7 + T + H)
     d, din = 64 * H, 24
     p = GRUHeadParams(torch.randn(3 * d, din, generator=g) * 0.2, torch.randn(3 * d, generator=g) * 0.1,
