@@ -21,8 +21,10 @@ backends this build does not provide ('eager', 'triton',
 
 from __future__ import annotations
 
+import contextlib
 import logging
 import math
+from collections.abc import Iterator
 from dataclasses import replace
 
 import torch
@@ -328,21 +330,35 @@ def newton_apply(
             raise ValueError("block_table cannot be combined with chunk_len")
         if needs_grad:
             raise RuntimeError("block_table newton is inference-only")
-    if cu_seqlens is not None:
-        return _newton_ragged(cell, x, config, h0=h0, stats=stats, cu_seqlens=cu_seqlens,
-                              block_table=block_table, needs_grad=needs_grad)
-    if block_table is not None:
-        h0 = gather_h0(h0, block_table, x.shape[0], _state_tail(cell))
-    if not needs_grad:
-        return _newton_forward(cell, x, config, h0=h0, stats=stats)
-    has_h0 = h0 is not None
-    h0_leaf = h0 if has_h0 else x.new_zeros(())
-    _fwd_pack.clear()
-    _fwd_pack.update(cell=cell, config=config, stats=stats, has_h0=has_h0)
-    try:
-        return _NewtonFixedPoint.apply(x, h0_leaf, *params)
-    finally:
+    with _newton_precision_region(x.device):
+        if cu_seqlens is not None:
+            return _newton_ragged(cell, x, config, h0=h0, stats=stats, cu_seqlens=cu_seqlens,
+                                  block_table=block_table, needs_grad=needs_grad)
+        if block_table is not None:
+            h0 = gather_h0(h0, block_table, x.shape[0], _state_tail(cell))
+        if not needs_grad:
+            return _newton_forward(cell, x, config, h0=h0, stats=stats)
+        has_h0 = h0 is not None
+        h0_leaf = h0 if has_h0 else x.new_zeros(())
         _fwd_pack.clear()
+        _fwd_pack.update(cell=cell, config=config, stats=stats, has_h0=has_h0)
+        try:
+            return _NewtonFixedPoint.apply(x, h0_leaf, *params)
+        finally:
+            _fwd_pack.clear()
+
+
+@contextlib.contextmanager
+def _newton_precision_region(device: torch.device) -> Iterator[None]:
+    """Keep the solve and the eq. 2.6 backward in the tensors' dtype under an
+    outer ``autocast`` (newton/__init__.py:193-209): AMP would round ``W_x(x)``
+    while the states stay in the module dtype.  Callers that want bf16 Newton
+    put the module and ``x`` in bf16."""
+    if device.type in ("cuda", "cpu") and torch.is_autocast_enabled(device.type):
+        with torch.autocast(device_type=device.type, enabled=False):
+            yield
+        return
+    yield
 
 
 def _state_tail(cell: nn.Module) -> tuple[int, ...]:
@@ -445,6 +461,11 @@ class _NewtonFixedPoint(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_states: Tensor):
+        with _newton_precision_region(grad_states.device):
+            return _NewtonFixedPoint._backward(ctx, grad_states)
+
+    @staticmethod
+    def _backward(ctx, grad_states: Tensor):
         if ctx.recompute:
             x_in, h0_in = ctx.saved_tensors
             h0_fwd = h0_in if ctx.has_h0 else None
