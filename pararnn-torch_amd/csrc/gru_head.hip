@@ -114,25 +114,72 @@ __device__ __forceinline__ Gates gates_step(float* s_h, float* s_u, float hp_j, 
   return g;
 }
 
+// 4 consecutive values of storage type T as floats / from floats (bf16: RNE).
+template <typename T>
+__device__ __forceinline__ void st4(T* p, floatx4 v) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<floatx4*>(p) = v;
+  } else {
+    uint2 w;
+    w.x = pack_bf16x2(v[0], v[1]);
+    w.y = pack_bf16x2(v[2], v[3]);
+    *reinterpret_cast<uint2*>(p) = w;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ floatx4 ld4(const T* p) {
+  if constexpr (sizeof(T) == 4) {
+    return *reinterpret_cast<const floatx4*>(p);
+  } else {
+    const uint2 w = *reinterpret_cast<const uint2*>(p);
+    return floatx4{lo_bf16(w.x), hi_bf16(w.x), lo_bf16(w.y), hi_bf16(w.y)};
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Initial guess: H_t = f(h_prev0_t, x_t), h_prev0 = 0 except h0 at t = 0
-// (reference solvers/newton/__init__.py:925-940).  One wave per (sequence,
-// block of 64 steps); only t = 0 with h0 needs the mat-vecs.
+// (reference solvers/newton/__init__.py:925-940).  With h_prev = 0 the step is
+// elementwise: gru_init_elem_kernel, 4 channels per thread; only t = 0 with
+// h0 needs the mat-vecs (gru_init_kernel, one wave per sequence and block of
+// `steps` steps).
 // ---------------------------------------------------------------------------
+template <typename TX, typename TOUT>
+__global__ __launch_bounds__(256) void gru_init_elem_kernel(const TX* __restrict__ wx,
+                                                            const TX* __restrict__ h0,
+                                                            TOUT* __restrict__ out, int B, int T,
+                                                            int d) {
+  const int q4 = d / 4;
+  const size_t n = static_cast<size_t>(B) * T * q4;
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const size_t bt = i / q4;
+    const int c = static_cast<int>(i % q4) * 4;
+    if (h0 != nullptr && bt % T == 0) continue;  // t = 0 with h0: gru_init_kernel
+    const TX* row = wx + bt * 3 * d + c;
+    const floatx4 zx = ld4(row), nx = ld4(row + 2 * static_cast<size_t>(d));
+    floatx4 h;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) h[v] = lerp_t(0.f, ftanh(nx[v]), fsigmoid(zx[v]));
+    st4(out + bt * d + c, h);
+  }
+}
+
+
 template <typename TX, typename TOUT>
 __global__ __launch_bounds__(64) void gru_init_kernel(const TX* __restrict__ wx,
                                                      const TX* __restrict__ a_z,
                                                      const TX* __restrict__ a_r,
                                                      const TX* __restrict__ a_n,
                                                      const TX* __restrict__ h0,
-                                                     TOUT* __restrict__ out, int B, int T, int H) {
+                                                     TOUT* __restrict__ out, int B, int T, int H,
+                                                     int steps, int n_blk) {
   __shared__ float s_h[DH], s_u[DH];
   const int j = threadIdx.x;
   const int d = H * DH;
-  const int n_blk = (T + 63) / 64;
   const int seq = blockIdx.x / n_blk, blk = blockIdx.x % n_blk;
   const int b = seq / H, head = seq % H;
-  const int t0 = blk * 64, t1 = min(T, t0 + 64);
+  const int t0 = blk * steps, t1 = min(T, t0 + steps);
   for (int t = t0; t < t1; ++t) {
     const float zx = ld(wx + wx_at(b, t, T, d, 0, head, j));
     const float rx = ld(wx + wx_at(b, t, T, d, 1, head, j));
@@ -735,28 +782,6 @@ constexpr int kRCols = 16;  // chunks per wave (the MFMA N dimension)
 #ifndef PRNN_RM_LDS
 #define PRNN_RM_LDS 0
 #endif
-
-template <typename T>
-__device__ __forceinline__ void st4(T* p, floatx4 v) {
-  if constexpr (sizeof(T) == 4) {
-    *reinterpret_cast<floatx4*>(p) = v;
-  } else {
-    uint2 w;
-    w.x = pack_bf16x2(v[0], v[1]);
-    w.y = pack_bf16x2(v[2], v[3]);
-    *reinterpret_cast<uint2*>(p) = w;
-  }
-}
-
-template <typename T>
-__device__ __forceinline__ floatx4 ld4(const T* p) {
-  if constexpr (sizeof(T) == 4) {
-    return *reinterpret_cast<const floatx4*>(p);
-  } else {
-    const uint2 w = *reinterpret_cast<const uint2*>(p);
-    return floatx4{lo_bf16(w.x), hi_bf16(w.x), lo_bf16(w.y), hi_bf16(w.y)};
-  }
-}
 
 template <typename TX, typename TOUT, bool LOCAL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PRNN_RM_WPE))) void gru_replay_mfma_kernel(
@@ -1451,19 +1476,30 @@ static void launch_replay(const TX* az, const TX* ar, const TX* an, const TX* h0
   }
 }
 
+// The initial guess into `out`: every step elementwise, then the t = 0 rows
+// from h0 (one step per sequence) when h0 is given.
+template <typename TX, typename TOUT>
+static void launch_init(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX* h0,
+                        TOUT* out, int B, int T, int H, hipStream_t stream) {
+  const int d = H * DH;
+  const size_t n = static_cast<size_t>(B) * T * (d / 4);
+  const unsigned blocks = static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 8192));
+  gru_init_elem_kernel<TX, TOUT><<<dim3(blocks), dim3(256), 0, stream>>>(wx, h0, out, B, T, d);
+  if (h0 != nullptr)  // one block of one step per sequence: t = 0 only
+    gru_init_kernel<TX, TOUT><<<dim3(B * H), dim3(64), 0, stream>>>(wx, az, ar, an, h0, out, B,
+                                                                     T, H, 1, 1);
+}
+
 template <typename TX>
 static int run(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX* h0, TX* out,
                int B, int T, int H, int K, float omega, const Ws& w, hipStream_t stream) {
   const int n_seq = B * H, n_chunks = (T + kChunk - 1) / kChunk;
-  const int n_blk64 = (T + 63) / 64;
   if (K == 0) {
-    gru_init_kernel<TX, TX><<<dim3(n_seq * n_blk64), dim3(64), 0, stream>>>(wx, az, ar, an, h0, out,
-                                                                            B, T, H);
+    launch_init<TX, TX>(wx, az, ar, an, h0, out, B, T, H, stream);
     PRNN_HIP(hipGetLastError());
     return PRNN_OK;
   }
-  gru_init_kernel<TX, float><<<dim3(n_seq * n_blk64), dim3(64), 0, stream>>>(wx, az, ar, an, h0,
-                                                                            w.work[0], B, T, H);
+  launch_init<TX, float>(wx, az, ar, an, h0, w.work[0], B, T, H, stream);
   PRNN_HIP(hipGetLastError());
   for (int k = 1; k <= K; ++k) {
     const float* hin = w.work[(k - 1) & 1];
