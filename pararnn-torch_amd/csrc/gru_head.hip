@@ -537,11 +537,14 @@ __global__ __launch_bounds__(256) void gru_group_kernel(const float* __restrict_
   if (threadIdx.x < DH) sL[0][threadIdx.x] = E[static_cast<size_t>(chunk_of(w_begin)) * DH + threadIdx.x];
   int cur = 0;
   floatx4 acc[4];
+  // The next chunk's matrix is fetched one product ahead (its loads are in
+  // flight during the current product).
+  if (w_begin + 1 < w_end) fetch(w_begin + 1);
   for (int w = w_begin + 1; w < w_end; ++w) {
-    fetch(w);
     __syncthreads();  // the previous product's reads of sS / sM are done
     stage(sS);
     __syncthreads();
+    fetch(w + 1);  // clamped to the group's last chunk past the end
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) acc[rt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
