@@ -866,16 +866,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PRNN_RM_WPE
     floatx4 yz[4], yr[4], yn[4], vv[4];
 #pragma unroll
     for (int to = 0; to < 4; ++to) yz[to] = yr[to] = yn[to] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // Eight independent accumulators between dependent MFMAs.
 #pragma unroll
     for (int tc = 0; tc < 4; ++tc) {
+      floatx4 az[4], ar[4];
 #pragma unroll
       for (int to = 0; to < 4; ++to) {
-        const floatx4 az = sA[0][to][tc][lane], ar = sA[1][to][tc][lane];
+        az[to] = sA[0][to][tc][lane];
+        ar[to] = sA[1][to][tc][lane];
+      }
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          yz[to] = mfma_f32(az[v], dl[tc][v], yz[to]);
-          yr[to] = mfma_f32(ar[v], dl[tc][v], yr[to]);
+      for (int v = 0; v < 4; ++v) {
+#pragma unroll
+        for (int to = 0; to < 4; ++to) {
+          yz[to] = mfma_f32(az[to][v], dl[tc][v], yz[to]);
+          yr[to] = mfma_f32(ar[to][v], dl[tc][v], yr[to]);
         }
+        __builtin_amdgcn_sched_barrier(0);  // keep the rounds interleaved
       }
     }
 #pragma unroll
@@ -888,11 +895,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PRNN_RM_WPE
       }
 #pragma unroll
     for (int tc = 0; tc < 4; ++tc) {
+      floatx4 an[4];
 #pragma unroll
-      for (int to = 0; to < 4; ++to) {
-        const floatx4 an = sA[2][to][tc][lane];
+      for (int to = 0; to < 4; ++to) an[to] = sA[2][to][tc][lane];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) yn[to] = mfma_f32(an[v], vv[tc][v], yn[to]);
+      for (int v = 0; v < 4; ++v) {
+#pragma unroll
+        for (int to = 0; to < 4; ++to) yn[to] = mfma_f32(an[to][v], vv[tc][v], yn[to]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     if (act) {
@@ -1209,14 +1219,20 @@ __global__ __launch_bounds__(256) void gru_rev_mfma_kernel(
     for (int to = 0; to < 4; ++to) tz[to] = du[to] = tr[to] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int tc = 0; tc < 4; ++tc) {
+      floatx4 az[4], an[4];
 #pragma unroll
       for (int to = 0; to < 4; ++to) {
-        const floatx4 az = sA[0][to][tc][lane], an = sA[2][to][tc][lane];
+        az[to] = sA[0][to][tc][lane];
+        an[to] = sA[2][to][tc][lane];
+      }
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          tz[to] = mfma_f32(az[v], dz[tc][v], tz[to]);
-          du[to] = mfma_f32(an[v], dn[tc][v], du[to]);
+      for (int v = 0; v < 4; ++v) {
+#pragma unroll
+        for (int to = 0; to < 4; ++to) {
+          tz[to] = mfma_f32(az[to][v], dz[tc][v], tz[to]);
+          du[to] = mfma_f32(an[to][v], dn[tc][v], du[to]);
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     // d_rpre = d_u h r(1-r)
@@ -1229,11 +1245,14 @@ __global__ __launch_bounds__(256) void gru_rev_mfma_kernel(
       }
 #pragma unroll
     for (int tc = 0; tc < 4; ++tc) {
+      floatx4 ar[4];
 #pragma unroll
-      for (int to = 0; to < 4; ++to) {
-        const floatx4 ar = sA[1][to][tc][lane];
+      for (int to = 0; to < 4; ++to) ar[to] = sA[1][to][tc][lane];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) tr[to] = mfma_f32(ar[v], dr[tc][v], tr[to]);
+      for (int v = 0; v < 4; ++v) {
+#pragma unroll
+        for (int to = 0; to < 4; ++to) tr[to] = mfma_f32(ar[to][v], dr[tc][v], tr[to]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     // nu <- (1-z) mu + A_z d_zpre + r d_u + A_r d_rpre
@@ -1411,7 +1430,11 @@ static void carry_scan(const float* phi, const float* e, float* carry, int n_seq
                        const CarryWs& c, hipStream_t stream) {
   const int n_groups = (n_chunks + kGroup - 1) / kGroup;
   const dim3 walk_block(64 * kCarryParts);
-  if (n_groups <= 1) {
+  static const bool single = [] {
+    const char* e = getenv("PRNN_GRU_CARRY_SINGLE");
+    return e && atoi(e) != 0;
+  }();
+  if (n_groups <= 1 || single) {
     gru_carry_kernel<REV><<<dim3(n_seq), walk_block, 0, stream>>>(phi, e, n_chunks, n_chunks,
                                                                   nullptr, carry);
     return;
