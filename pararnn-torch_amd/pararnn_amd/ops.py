@@ -13,6 +13,7 @@ and have fake kernels for ``torch.compile``.
 
 from __future__ import annotations
 
+import collections
 import ctypes
 import os
 import threading
@@ -61,8 +62,9 @@ def _workspace(nbytes: int, dev: torch.device) -> Tensor:
 # workspace per call (a replay would repeat captured tags).
 _TAG_SPAN = 64           # PRNN_TAG_SPAN
 _TAG_BASE_MAX = 1 << 30  # PRNN_TAG_BASE_MAX
+_TAGGED_MAX = 4          # cached buffers (least recently used dropped first)
 _tagged_lock = threading.Lock()
-_tagged: dict[tuple[int, int], list] = {}
+_tagged: collections.OrderedDict[tuple[int, int], list] = collections.OrderedDict()
 
 
 def _tagged_enabled() -> bool:
@@ -81,6 +83,9 @@ def _slstm_workspace(nbytes: int, dev: torch.device) -> tuple[Tensor, int]:
             # Zero-filled on this stream, ahead of the call that uses it.
             ent = [torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=dev), 1]
             _tagged[key] = ent
+        _tagged.move_to_end(key)
+        while len(_tagged) > _TAGGED_MAX:
+            _tagged.popitem(last=False)  # the stream-ordered allocator frees it safely
         base = ent[1]
         ent[1] += _TAG_SPAN
         return ent[0], base

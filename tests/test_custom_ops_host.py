@@ -75,3 +75,36 @@ def test_precision_region_disables_autocast():
             y = torch.nn.functional.linear(torch.randn(3, 4), torch.randn(5, 4))
             assert y.dtype == torch.float32
         assert torch.is_autocast_enabled("cpu")
+
+
+def test_tagged_workspace_cache_is_bounded(monkeypatch):
+    """One zero-filled buffer per (device, stream), at most a few kept, tag
+    bases 64 apart and growing; no GPU needed (buffers made on the CPU)."""
+    from pararnn_amd import ops
+
+    made = []
+    real_zeros = torch.zeros
+
+    def fake_zeros(n, dtype, device):
+        made.append(n)
+        return real_zeros(n, dtype=dtype)
+
+    class _S:
+        def __init__(self, h):
+            self.cuda_stream = h
+
+    monkeypatch.setattr(ops.torch, "zeros", fake_zeros)
+    monkeypatch.setattr(ops.torch.cuda, "is_current_stream_capturing", lambda: False)
+    ops.release_workspaces()
+    dev = torch.device("cuda", 0)
+    bases = []
+    for h in range(10):
+        monkeypatch.setattr(ops.torch.cuda, "current_stream", lambda d, h=h: _S(1000 + h))
+        ws, base = ops._slstm_workspace(1024, dev)
+        ws2, base2 = ops._slstm_workspace(512, dev)  # same stream: same buffer, next base
+        assert ws2 is ws and base2 == base + ops._TAG_SPAN
+        bases.append(base)
+    assert len(ops._tagged) == ops._TAGGED_MAX
+    assert all(b == 1 for b in bases) and len(made) == 10
+    ops.release_workspaces()
+    assert not ops._tagged
