@@ -779,15 +779,9 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
 // MFMA product do not mix.
 // ---------------------------------------------------------------------------
 constexpr int kRCols = 16;  // chunks per wave (the MFMA N dimension)
-#ifndef PRNN_RM_WPE
-#define PRNN_RM_WPE 1
-#endif
-#ifndef PRNN_RM_LDS
-#define PRNN_RM_LDS 0
-#endif
 
 template <typename TX, typename TOUT, bool LOCAL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PRNN_RM_WPE))) void gru_replay_mfma_kernel(
+__global__ __launch_bounds__(256) void gru_replay_mfma_kernel(
     const TX* __restrict__ a_z, const TX* __restrict__ a_r, const TX* __restrict__ a_n,
     const TX* __restrict__ h0, const float* __restrict__ hin, const float* __restrict__ gates,
     const float* __restrict__ carry_in, TOUT* __restrict__ hout, float* __restrict__ e_out,
@@ -859,9 +853,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PRNN_RM_WPE
     const In cur = nx;
     if (s + 1 < steps) load_in(s + 1, nx, cur.ht);
     const floatx4 *hp = cur.hp, *ht = cur.ht, *gz = cur.gz, *gr = cur.gr, *gn = cur.gn;
-#if PRNN_RM_LDS
-    asm volatile("" ::: "memory");  // A operands are re-read from LDS every step
-#endif
     // J delta = (1-z) delta + d2 (delta @ A_z) + d3 ((r delta + d5 (delta @ A_r)) @ A_n)
     floatx4 yz[4], yr[4], yn[4], vv[4];
 #pragma unroll
