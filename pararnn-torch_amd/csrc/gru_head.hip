@@ -247,11 +247,43 @@ static_assert(sizeof(float) * kChunk * 5 * DH <= sizeof(PhiInputs), "row scalars
 // them instead of recomputing three mat-vecs per step).  TRANS (eq. 2.6
 // backward at H* = hin): Phi is stored transposed, Phi^T being the reverse
 // chunk transfer.
+// The bf16 A^T operands of the chunk kernel's products, in its permuted
+// contraction order, packed once per call (they are the same for every chunk
+// of a head): out[head][matrix z, r, n][rt][ks][lane] = the 8 values lane
+// (li, g) supplies, A[k][16 rt + li] for k = 16 (2 ks + q / 4) + 4 g + q % 4.
+template <typename TX>
+__global__ __launch_bounds__(64) void gru_pack_at_kernel(const TX* __restrict__ a_z,
+                                                         const TX* __restrict__ a_r,
+                                                         const TX* __restrict__ a_n,
+                                                         u32x4* __restrict__ out) {
+  const int head = blockIdx.x, lane = threadIdx.x;
+  const int li = lane & 15, g = lane >> 4;
+  const size_t hoff = static_cast<size_t>(head) * DH * DH;
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+    const TX* A = (m == 0 ? a_z : m == 1 ? a_r : a_n) + hoff;
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        bf16x8 v;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int k = 16 * (2 * ks + (q >> 2)) + 4 * g + (q & 3);
+          v[q] = static_cast<__bf16>(ld(A + static_cast<size_t>(k) * DH + 16 * rt + li));
+        }
+        out[((static_cast<size_t>(head) * 3 + m) * 4 + rt) * 2 * 64 + ks * 64 + lane] =
+            __builtin_bit_cast(u32x4, v);
+      }
+  }
+}
+
 template <typename TX, typename TH, bool TRANS>
 __global__ __launch_bounds__(256) void gru_phi_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ a_z, const TX* __restrict__ a_r,
     const TX* __restrict__ a_n, const TX* __restrict__ h0, const TH* __restrict__ hin, int B,
-    int T, int H, int n_chunks, float* __restrict__ phi_out, float* __restrict__ gates_out) {
+    int T, int H, int n_chunks, float* __restrict__ phi_out, float* __restrict__ gates_out,
+    const u32x4* __restrict__ at_packed) {
   __shared__ PhiShared sh;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int li = lane & 15, g = lane >> 4;
@@ -378,23 +410,18 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
   // A^T[16 rt + li][k] = A[k][16 rt + li] for the 8 k of its slots
   // k = 16 (2 ks + q / 4) + 4 g + q % 4, q = 0..7.
   bf16x8 atz[4][2], atr[4][2], atn[4][2];
-  auto load_at = [&](const TX* A, bf16x8 at[4][2]) {
+  {
+    // Packed once per call by gru_pack_at_kernel: [head][matrix][rt][ks][lane].
+    const u32x4* pk = at_packed + static_cast<size_t>(head) * 3 * 4 * 2 * 64 + lane;
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int k = 16 * (2 * ks + (q >> 2)) + 4 * g + (q & 3);
-          at[rt][ks][q] = static_cast<__bf16>(ld(A + hoff + static_cast<size_t>(k) * DH + 16 * rt + li));
-        }
-  };
-  // one matrix at a time (bounds the registers of the loads in flight)
-  load_at(a_z, atz);
-  __builtin_amdgcn_sched_barrier(0);
-  load_at(a_r, atr);
-  __builtin_amdgcn_sched_barrier(0);
-  load_at(a_n, atn);
+      for (int ks = 0; ks < 2; ++ks) {
+        atz[rt][ks] = __builtin_bit_cast(bf16x8, pk[((0 * 4 + rt) * 2 + ks) * 64]);
+        atr[rt][ks] = __builtin_bit_cast(bf16x8, pk[((1 * 4 + rt) * 2 + ks) * 64]);
+        atn[rt][ks] = __builtin_bit_cast(bf16x8, pk[((2 * 4 + rt) * 2 + ks) * 64]);
+      }
+  }
   __syncthreads();
 
   // Phi = I on this wave's columns: lane holds Phi[16 rt + 4 g + v][col].
@@ -1444,8 +1471,13 @@ struct Ws {
   float* carry;
   float* gates;
   float* work[2];
+  u32x4* at;  // packed bf16 A^T operands of the chunk kernel
   CarryWs cs;
 };
+
+static u32x4* carve_at(Carver& cv, int H) {
+  return static_cast<u32x4*>(cv.take(sizeof(u32x4) * static_cast<size_t>(H) * 3 * 4 * 2 * 64));
+}
 
 static Ws carve(void* base, int B, int T, int H, int K, size_t* total) {
   const int n_seq = B * H, n_chunks = (T + kChunk - 1) / kChunk;
@@ -1457,6 +1489,7 @@ static Ws carve(void* base, int B, int T, int H, int K, size_t* total) {
   w.gates = static_cast<float*>(
       cv.take(sizeof(float) * static_cast<size_t>(n_seq) * n_chunks * kChunk * 3 * DH));
   w.cs = carve_carry(cv, n_seq, n_chunks);
+  w.at = carve_at(cv, H);
   const size_t hb = sizeof(float) * static_cast<size_t>(B) * T * H * DH;
   w.work[0] = K >= 1 ? static_cast<float*>(cv.take(hb)) : nullptr;
   w.work[1] = K >= 2 ? static_cast<float*>(cv.take(hb)) : nullptr;
@@ -1517,11 +1550,12 @@ static int run(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX*
     return PRNN_OK;
   }
   launch_init<TX, float>(wx, az, ar, an, h0, w.work[0], B, T, H, stream);
+  gru_pack_at_kernel<TX><<<dim3(H), dim3(64), 0, stream>>>(az, ar, an, w.at);
   PRNN_HIP(hipGetLastError());
   for (int k = 1; k <= K; ++k) {
     const float* hin = w.work[(k - 1) & 1];
     gru_phi_kernel<TX, float, false><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
-        wx, az, ar, an, h0, hin, B, T, H, n_chunks, w.phi, w.gates);
+        wx, az, ar, an, h0, hin, B, T, H, n_chunks, w.phi, w.gates, w.at);
     PRNN_HIP(hipGetLastError());
     launch_replay<TX, float, true>(az, ar, an, h0, hin, w.gates, nullptr,
                                    static_cast<float*>(nullptr), w.e, B, T, H, n_chunks, omega,
@@ -1548,6 +1582,7 @@ struct BwdWs {
   float* gates;
   float* part;
   int n_split, rows_per;
+  u32x4* at;
   CarryWs cs;
 };
 
@@ -1574,6 +1609,7 @@ static BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   ga_split(B, T, H, &w.n_split, &w.rows_per);
   w.part = static_cast<float*>(cv.take(sizeof(float) * static_cast<size_t>(w.n_split) * 3 * H * DH * DH));
   w.cs = carve_carry(cv, n_seq, n_chunks);
+  w.at = carve_at(cv, H);
   *total = cv.used;
   return w;
 }
@@ -1587,8 +1623,9 @@ static int run_bwd(const TX* wx, const TX* az, const TX* ar, const TX* an, const
   const int rev_blocks = (n_seq * n_chunks + 3) / 4;
   const bool mfma_walks = walks_mfma("PRNN_GRU_REV_MFMA", n_seq, n_chunks);
   const int mfma_blocks = n_seq * ((n_chunks + 4 * kRCols - 1) / (4 * kRCols));
+  gru_pack_at_kernel<TX><<<dim3(H), dim3(64), 0, stream>>>(az, ar, an, w.at);
   gru_phi_kernel<TX, TX, true><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
-      wx, az, ar, an, h0, states, B, T, H, n_chunks, w.phi, w.gates);
+      wx, az, ar, an, h0, states, B, T, H, n_chunks, w.phi, w.gates, w.at);
   PRNN_HIP(hipGetLastError());
   if (mfma_walks)
     gru_rev_mfma_kernel<TX, true><<<dim3(mfma_blocks), dim3(256), 0, stream>>>(
