@@ -251,14 +251,30 @@ static_assert(sizeof(float) * kChunk * 5 * DH <= sizeof(PhiInputs), "row scalars
 // contraction order, packed once per call (they are the same for every chunk
 // of a head): out[head][matrix z, r, n][rt][ks][lane] = the 8 values lane
 // (li, g) supplies, A[k][16 rt + li] for k = 16 (2 ks + q / 4) + 4 g + q % 4.
+// Also the fp32 B operands of its gate GEMMs: out_b[head][wave][matrix][kk / 4]
+// [lane] = A[16 g + kk][16 wave + li] for kk = 4 (kk / 4) .. + 3.
 template <typename TX>
 __global__ __launch_bounds__(64) void gru_pack_at_kernel(const TX* __restrict__ a_z,
                                                          const TX* __restrict__ a_r,
                                                          const TX* __restrict__ a_n,
-                                                         u32x4* __restrict__ out) {
+                                                         u32x4* __restrict__ out,
+                                                         floatx4* __restrict__ out_b) {
   const int head = blockIdx.x, lane = threadIdx.x;
   const int li = lane & 15, g = lane >> 4;
   const size_t hoff = static_cast<size_t>(head) * DH * DH;
+  for (int w = 0; w < 4; ++w)
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+      const TX* A = (m == 0 ? a_z : m == 1 ? a_r : a_n) + hoff;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        floatx4 v;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          v[u] = ld(A + static_cast<size_t>(16 * g + 4 * q + u) * DH + 16 * w + li);
+        out_b[((static_cast<size_t>(head) * 4 + w) * 3 + m) * 4 * 64 + q * 64 + lane] = v;
+      }
+    }
 #pragma unroll
   for (int m = 0; m < 3; ++m) {
     const TX* A = (m == 0 ? a_z : m == 1 ? a_r : a_n) + hoff;
@@ -283,7 +299,7 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ a_z, const TX* __restrict__ a_r,
     const TX* __restrict__ a_n, const TX* __restrict__ h0, const TH* __restrict__ hin, int B,
     int T, int H, int n_chunks, float* __restrict__ phi_out, float* __restrict__ gates_out,
-    const u32x4* __restrict__ at_packed) {
+    const u32x4* __restrict__ at_packed, const floatx4* __restrict__ b_packed) {
   __shared__ PhiShared sh;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int li = lane & 15, g = lane >> 4;
@@ -322,13 +338,20 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
   {
     // B operands: A[k][col] for k = 16 g + kk (the contraction order every
     // lane uses for its A operand below).
+    // Packed once per call by gru_pack_at_kernel: [head][wave][matrix][kk / 4][lane].
     float bz[16], br[16], bn[16];
+    {
+      const floatx4* pb = b_packed + (static_cast<size_t>(head) * 4 + wave) * 3 * 4 * 64 + lane;
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
-      const size_t o = hoff + static_cast<size_t>(16 * g + kk) * DH + col;
-      bz[kk] = ld(a_z + o);
-      br[kk] = ld(a_r + o);
-      bn[kk] = ld(a_n + o);
+      for (int q = 0; q < 4; ++q) {
+        const floatx4 z4 = pb[(0 * 4 + q) * 64], r4 = pb[(1 * 4 + q) * 64], n4 = pb[(2 * 4 + q) * 64];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          bz[4 * q + v] = z4[v];
+          br[4 * q + v] = r4[v];
+          bn[4 * q + v] = n4[v];
+        }
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -1471,12 +1494,16 @@ struct Ws {
   float* carry;
   float* gates;
   float* work[2];
-  u32x4* at;  // packed bf16 A^T operands of the chunk kernel
+  u32x4* at;     // packed bf16 A^T operands of the chunk kernel
+  floatx4* atb;  // packed fp32 B operands of its gate GEMMs
   CarryWs cs;
 };
 
 static u32x4* carve_at(Carver& cv, int H) {
   return static_cast<u32x4*>(cv.take(sizeof(u32x4) * static_cast<size_t>(H) * 3 * 4 * 2 * 64));
+}
+static floatx4* carve_atb(Carver& cv, int H) {
+  return static_cast<floatx4*>(cv.take(sizeof(floatx4) * static_cast<size_t>(H) * 4 * 3 * 4 * 64));
 }
 
 static Ws carve(void* base, int B, int T, int H, int K, size_t* total) {
@@ -1490,6 +1517,7 @@ static Ws carve(void* base, int B, int T, int H, int K, size_t* total) {
       cv.take(sizeof(float) * static_cast<size_t>(n_seq) * n_chunks * kChunk * 3 * DH));
   w.cs = carve_carry(cv, n_seq, n_chunks);
   w.at = carve_at(cv, H);
+  w.atb = carve_atb(cv, H);
   const size_t hb = sizeof(float) * static_cast<size_t>(B) * T * H * DH;
   w.work[0] = K >= 1 ? static_cast<float*>(cv.take(hb)) : nullptr;
   w.work[1] = K >= 2 ? static_cast<float*>(cv.take(hb)) : nullptr;
@@ -1550,12 +1578,12 @@ static int run(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX*
     return PRNN_OK;
   }
   launch_init<TX, float>(wx, az, ar, an, h0, w.work[0], B, T, H, stream);
-  gru_pack_at_kernel<TX><<<dim3(H), dim3(64), 0, stream>>>(az, ar, an, w.at);
+  gru_pack_at_kernel<TX><<<dim3(H), dim3(64), 0, stream>>>(az, ar, an, w.at, w.atb);
   PRNN_HIP(hipGetLastError());
   for (int k = 1; k <= K; ++k) {
     const float* hin = w.work[(k - 1) & 1];
     gru_phi_kernel<TX, float, false><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
-        wx, az, ar, an, h0, hin, B, T, H, n_chunks, w.phi, w.gates, w.at);
+        wx, az, ar, an, h0, hin, B, T, H, n_chunks, w.phi, w.gates, w.at, w.atb);
     PRNN_HIP(hipGetLastError());
     launch_replay<TX, float, true>(az, ar, an, h0, hin, w.gates, nullptr,
                                    static_cast<float*>(nullptr), w.e, B, T, H, n_chunks, omega,
@@ -1583,6 +1611,7 @@ struct BwdWs {
   float* part;
   int n_split, rows_per;
   u32x4* at;
+  floatx4* atb;
   CarryWs cs;
 };
 
@@ -1610,6 +1639,7 @@ static BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   w.part = static_cast<float*>(cv.take(sizeof(float) * static_cast<size_t>(w.n_split) * 3 * H * DH * DH));
   w.cs = carve_carry(cv, n_seq, n_chunks);
   w.at = carve_at(cv, H);
+  w.atb = carve_atb(cv, H);
   *total = cv.used;
   return w;
 }
@@ -1623,9 +1653,9 @@ static int run_bwd(const TX* wx, const TX* az, const TX* ar, const TX* an, const
   const int rev_blocks = (n_seq * n_chunks + 3) / 4;
   const bool mfma_walks = walks_mfma("PRNN_GRU_REV_MFMA", n_seq, n_chunks);
   const int mfma_blocks = n_seq * ((n_chunks + 4 * kRCols - 1) / (4 * kRCols));
-  gru_pack_at_kernel<TX><<<dim3(H), dim3(64), 0, stream>>>(az, ar, an, w.at);
+  gru_pack_at_kernel<TX><<<dim3(H), dim3(64), 0, stream>>>(az, ar, an, w.at, w.atb);
   gru_phi_kernel<TX, TX, true><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
-      wx, az, ar, an, h0, states, B, T, H, n_chunks, w.phi, w.gates, w.at);
+      wx, az, ar, an, h0, states, B, T, H, n_chunks, w.phi, w.gates, w.at, w.atb);
   PRNN_HIP(hipGetLastError());
   if (mfma_walks)
     gru_rev_mfma_kernel<TX, true><<<dim3(mfma_blocks), dim3(256), 0, stream>>>(
