@@ -313,23 +313,23 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
   // ---- inputs of the chunk into LDS (zero rows past the end); unrolled so
   // every load of the chunk is in flight at once ----
 #pragma unroll
-  for (int idx = threadIdx.x; idx < kChunk * DH; idx += 256) {
-    const int s = idx / DH, j = idx % DH;
+  for (int idx = threadIdx.x; idx < kChunk * DH / 4; idx += 256) {
+    const int s = idx / (DH / 4), j = 4 * (idx % (DH / 4));
     const int t = t0 + s;
-    float hp = 0.f, zx = 0.f, rx = 0.f, nx = 0.f;
+    floatx4 hp = {0.f, 0.f, 0.f, 0.f}, zx = hp, rx = hp, nx = hp;
     if (s < len) {
       if (t > 0)
-        hp = ld(hin + h_at(b, t - 1, T, d, head, j));
+        hp = ld4(hin + h_at(b, t - 1, T, d, head, j));
       else if (h0 != nullptr)
-        hp = ld(h0 + static_cast<size_t>(b) * d + head * DH + j);
-      zx = ld(wx + wx_at(b, t, T, d, 0, head, j));
-      rx = ld(wx + wx_at(b, t, T, d, 1, head, j));
-      nx = ld(wx + wx_at(b, t, T, d, 2, head, j));
+        hp = ld4(h0 + static_cast<size_t>(b) * d + head * DH + j);
+      zx = ld4(wx + wx_at(b, t, T, d, 0, head, j));
+      rx = ld4(wx + wx_at(b, t, T, d, 1, head, j));
+      nx = ld4(wx + wx_at(b, t, T, d, 2, head, j));
     }
-    sh.in.hp[s][j] = hp;
-    sh.in.x[0][s][j] = zx;
-    sh.in.x[1][s][j] = rx;
-    sh.in.x[2][s][j] = nx;
+    *reinterpret_cast<floatx4*>(&sh.in.hp[s][j]) = hp;
+    *reinterpret_cast<floatx4*>(&sh.in.x[0][s][j]) = zx;
+    *reinterpret_cast<floatx4*>(&sh.in.x[1][s][j]) = rx;
+    *reinterpret_cast<floatx4*>(&sh.in.x[2][s][j]) = nx;
   }
 
   // ---- phase A: gates by fp32 MFMA (wave w: output channels 16w + li) ----
