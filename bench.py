@@ -244,6 +244,14 @@ def head_cfg4(torch, reps: int):
                 res["fwd_bf16_ms"] = _time(torch, lambda: newton_apply(cb, xb, cfg), reps)
             res["fwd_fp32_tokens_per_s"] = b4 * t4 / (res["fwd_fp32_ms"] * 1e-3)
             res["fwd_bf16_tokens_per_s"] = b4 * t4 / (res["fwd_bf16_ms"] * 1e-3)
+            # Algorithmic MFMA work of a matrix-composing scan: form J_t and
+            # compose once per step, 4 d^3 flop per (b, head, step, iteration).
+            flop = 4.0 * 3 * b4 * 8 * t4 * 64 ** 3
+            ach = flop / (res["fwd_fp32_ms"] * 1e-3) / 1e12
+            res["roofline"] = {"bound": "mfma", "algorithmic_flop": flop, "achieved": ach,
+                               "unit": "TFLOP/s", "peak_bf16_dense": 2500.0,
+                               "frac_bf16": ach / 2500.0, "peak_fp32_mfma": 157.3,
+                               "frac_fp32": ach / 157.3}
         out[tag] = res
     return out
 
