@@ -1353,33 +1353,44 @@ __global__ __launch_bounds__(256) void gru_ga_kernel(
   for (int q = 0; q < 3; ++q)
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) acc[q][rt] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (long long k0 = r0; k0 < r1; k0 += kGaRows) {
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < kGaRows * DH / 256; ++q) {
-      const int idx = threadIdx.x + 256 * q;
-      const int kr = idx / DH, j = idx % DH;
-      const long long k = k0 + kr;
-      float hv = 0.f, rv = 0.f, y0 = 0.f, y1 = 0.f, y2 = 0.f;
-      if (k < r1) {
-        const int b = static_cast<int>(k / T), t = static_cast<int>(k % T);
-        if (t > 0)
-          hv = ld(states + h_at(b, t - 1, T, d, head, j));
-        else if (h0 != nullptr)
-          hv = ld(h0 + static_cast<size_t>(b) * d + head * DH + j);
-        const size_t task = static_cast<size_t>(b * H + head) * n_chunks + t / kChunk;
-        rv = gates[((task * kChunk + t % kChunk) * 3 + 1) * DH + j];
-        y0 = ld(g_wx + wx_at(b, t, T, d, 0, head, j));
-        y1 = ld(g_wx + wx_at(b, t, T, d, 1, head, j));
-        y2 = ld(g_wx + wx_at(b, t, T, d, 2, head, j));
-      }
-      sx[0][kr][j] = hv;
-      sx[1][kr][j] = hv * rv;
-      sy[0][kr][j] = y0;
-      sy[1][kr][j] = y1;
-      sy[2][kr][j] = y2;
+  // Thread t stages channels 4 (t % 16) .. + 3 of row t / 16 of each block
+  // of 16 rows, one 128-bit load per array; the next block is loaded while
+  // the current one's products run.
+  static_assert(kGaRows * DH == 4 * 256, "one float4 per thread and array");
+  const int sr = threadIdx.x / 16, sj = 4 * (threadIdx.x % 16);
+  struct Stage {
+    floatx4 hv, hr, y0, y1, y2;
+  };
+  auto load_rows = [&](long long k0, Stage& st) {
+    const floatx4 zero{0.f, 0.f, 0.f, 0.f};
+    st.hv = st.hr = st.y0 = st.y1 = st.y2 = zero;
+    const long long k = k0 + sr;
+    if (k < r1) {
+      const int b = static_cast<int>(k / T), t = static_cast<int>(k % T);
+      if (t > 0)
+        st.hv = ld4(states + h_at(b, t - 1, T, d, head, sj));
+      else if (h0 != nullptr)
+        st.hv = ld4(h0 + static_cast<size_t>(b) * d + head * DH + sj);
+      const size_t task = static_cast<size_t>(b * H + head) * n_chunks + t / kChunk;
+      const floatx4 rv =
+          *reinterpret_cast<const floatx4*>(gates + ((task * kChunk + t % kChunk) * 3 + 1) * DH + sj);
+      st.hr = st.hv * rv;
+      st.y0 = ld4(g_wx + wx_at(b, t, T, d, 0, head, sj));
+      st.y1 = ld4(g_wx + wx_at(b, t, T, d, 1, head, sj));
+      st.y2 = ld4(g_wx + wx_at(b, t, T, d, 2, head, sj));
     }
+  };
+  Stage nx;
+  load_rows(r0, nx);
+  for (long long k0 = r0; k0 < r1; k0 += kGaRows) {
+    __syncthreads();  // the previous block's products are done with sx / sy
+    *reinterpret_cast<floatx4*>(&sx[0][sr][sj]) = nx.hv;
+    *reinterpret_cast<floatx4*>(&sx[1][sr][sj]) = nx.hr;
+    *reinterpret_cast<floatx4*>(&sy[0][sr][sj]) = nx.y0;
+    *reinterpret_cast<floatx4*>(&sy[1][sr][sj]) = nx.y1;
+    *reinterpret_cast<floatx4*>(&sy[2][sr][sj]) = nx.y2;
     __syncthreads();
+    if (k0 + kGaRows < r1) load_rows(k0 + kGaRows, nx);
 #pragma unroll
     for (int kk = 0; kk < kGaRows / 4; ++kk) {
       const float* xh = &sx[0][4 * kk + g][li];
