@@ -551,7 +551,7 @@ def _weight_grad(gy: Tensor, xx: Tensor) -> Tensor:
     and rounded once."""
     n = int(gy.shape[0])
     if gy.is_cuda and n >= 65536 and gy.dtype in (torch.bfloat16, torch.float16, torch.float32):
-        split = next((k for k in (32, 16, 8, 4) if n % k == 0 and n // k >= 4096), 1)
+        split = next((k for k in (16, 8, 4) if n % k == 0 and n // k >= 4096), 1)
         if split > 1:
             a = gy.view(split, n // split, -1).transpose(1, 2)
             b = xx.view(split, n // split, -1)
