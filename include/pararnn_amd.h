@@ -163,11 +163,15 @@ PRNN_API int prnn_slstm_newton_ex(const void* wx, const void* r, const void* h0,
                                   int max_iters, float omega, float eps, int dtype,
                                   void* workspace, size_t workspace_bytes, int tag_base,
                                   void* stream);
+/* prnn_slstm_backward_ex also returns, when g_b is not NULL, the W_x bias
+ * gradient g_b (4, d) fp32: the sum over (b, t) of dL/dwx (of the fp32 values
+ * that g_wx rounds), reduced in a fixed order with g_r -- one pass less than
+ * summing g_wx afterwards. */
 PRNN_API int prnn_slstm_backward_ex(const void* wx, const void* r, const void* h0,
                                     const void* states, const void* grad, void* g_wx,
-                                    float* g_r, float* g_h0, int B, int T, int d, float eps,
-                                    int dtype, void* workspace, size_t workspace_bytes,
-                                    int tag_base, void* stream);
+                                    float* g_r, float* g_h0, float* g_b, int B, int T, int d,
+                                    float eps, int dtype, void* workspace,
+                                    size_t workspace_bytes, int tag_base, void* stream);
 
 /* Eq. 2.6 backward of the head GRU at `states` = H* (B, T, d) with upstream
  * gradient `grad` = dL/dH (B, T, d) (both in `dtype`):

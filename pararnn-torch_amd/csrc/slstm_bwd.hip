@@ -76,6 +76,9 @@ __device__ __forceinline__ void cell_vjp(const float prev[4], const float x[4], 
   nu[3] = r[0] * dz[0] + r[1] * dz[1] + r[2] * dz[2] + r[3] * dz[3];
 }
 
+// Per-tile gradient partials: sum_t dz_g h_{t-1} (R) then sum_t dz_g (bias), g = 0..3.
+constexpr int kPartials = 8;
+
 template <typename TX, int L, int W, bool DET>
 __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
@@ -242,6 +245,7 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
 #pragma unroll
   for (int k = 0; k < 4; ++k) nu[k] = s_carry[wave][k][lane];
   float gr[4] = {0.f, 0.f, 0.f, 0.f};
+  float gb[4] = {0.f, 0.f, 0.f, 0.f};  // sum_t dz_g: the W_x bias gradient
   {
     const rsrc_t ro = make_rsrc(gwx + first * row4 + c0, span);
     auto replay = [&](int s) {
@@ -257,6 +261,7 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
       for (int k = 0; k < 4; ++k) {
         stb<TX>(ro, voff, so + k * slot, dz[k]);
         gr[k] += dz[k] * prev[3];
+        gb[k] += dz[k];
       }
     };
     if (n_steps == L) {
@@ -273,18 +278,22 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
 #pragma unroll
     for (int k = 0; k < 4; ++k) p[k * d] = nu[k];
   }
-  // Tile partial of sum_t dz_g * h_{t-1}: waves through LDS (s_agg is free).
+  // Tile partials of sum_t dz_g * h_{t-1} (R) and sum_t dz_g (bias): waves
+  // through LDS (s_agg is free).
   __syncthreads();
 #pragma unroll
-  for (int k = 0; k < 4; ++k) s_agg[wave][k][lane] = gr[k];
+  for (int k = 0; k < 4; ++k) {
+    s_agg[wave][k][lane] = gr[k];
+    s_agg[wave][4 + k][lane] = gb[k];
+  }
   __syncthreads();
   if (wave == 0) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < 8; ++k) {
       float acc = 0.f;
 #pragma unroll
       for (int w = 0; w < W; ++w) acc += s_agg[w][k][lane];
-      gr_part[(static_cast<size_t>(tile) * 4 + k) * kCB + lane] = acc;
+      gr_part[(static_cast<size_t>(tile) * kPartials + k) * kCB + lane] = acc;
     }
   }
 }
@@ -295,8 +304,8 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
 // shares combine in LDS in a fixed order (deterministic).
 constexpr int kReduceWaves = 16;
 __global__ __launch_bounds__(64 * kReduceWaves) void slstm_gr_reduce_kernel(
-    const float* __restrict__ gr_part, float* __restrict__ gr, int B, int d, int n_cb,
-    int n_chunks) {
+    const float* __restrict__ gr_part, float* __restrict__ gr, float* __restrict__ gb, int B,
+    int d, int n_cb, int n_chunks) {
   __shared__ float s_part[kReduceWaves][kCB];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -308,7 +317,7 @@ __global__ __launch_bounds__(64 * kReduceWaves) void slstm_gr_reduce_kernel(
   for (int q = q0; q < q1; ++q) {
     // q enumerates (chunk, b) in tile order
     const size_t tile = static_cast<size_t>(q) * n_cb + cb;
-    acc += gr_part[(tile * 4 + g) * kCB + lane];
+    acc += gr_part[(tile * kPartials + g) * kCB + lane];
   }
   s_part[wave][lane] = acc;
   __syncthreads();
@@ -317,7 +326,12 @@ __global__ __launch_bounds__(64 * kReduceWaves) void slstm_gr_reduce_kernel(
 #pragma unroll
     for (int w = 0; w < kReduceWaves; ++w) t += s_part[w][lane];
     const int ch = cb * kCB + lane;
-    if (ch < d) gr[g * d + ch] = t;
+    if (ch < d) {
+      if (g < 4)
+        gr[g * d + ch] = t;
+      else
+        gb[(g - 4) * d + ch] = t;
+    }
   }
 }
 
@@ -363,7 +377,7 @@ static BwdWs carve_bwd(void* base, int B, int T, int d, int dtype, size_t* total
   Carver cv(base);
   BwdWs w;
   w.lb = carve_lookback(cv, g, 4, 20);
-  w.gr_part = static_cast<float*>(cv.take(sizeof(float) * 4 * kCB * g.n_tiles));
+  w.gr_part = static_cast<float*>(cv.take(sizeof(float) * kPartials * kCB * g.n_tiles));
   *total = cv.used;
   return w;
 }
@@ -380,7 +394,7 @@ static void launch_reverse(const TX* wx, const TX* r, const TX* h0, const TX* st
 
 template <typename TX>
 static int run_bwd(const TX* wx, const TX* r, const TX* h0, const TX* states, const TX* grad,
-                   TX* gwx, float* gr, float* gh0, int B, int T, int d, float eps,
+                   TX* gwx, float* gr, float* gh0, float* gb, int B, int T, int d, float eps,
                    const BwdWs& w, hipStream_t stream) {
   int rc = clear_status(w.lb, stream);
   if (rc != PRNN_OK) return rc;
@@ -409,8 +423,9 @@ static int run_bwd(const TX* wx, const TX* r, const TX* h0, const TX* states, co
   timing_end(stream);
   PRNN_HIP(hipGetLastError());
   const Geo g = geometry(B, T, d, sh);
-  slstm_gr_reduce_kernel<<<dim3(4 * g.n_cb), dim3(64 * kReduceWaves), 0, stream>>>(
-      w.gr_part, gr, B, d, g.n_cb, g.n_chunks);
+  // g_r, and g_b when asked for (blocks 4 n_cb .. 8 n_cb)
+  slstm_gr_reduce_kernel<<<dim3((gb != nullptr ? 8 : 4) * g.n_cb), dim3(64 * kReduceWaves), 0,
+                           stream>>>(w.gr_part, gr, gb, B, d, g.n_cb, g.n_chunks);
   PRNN_HIP(hipGetLastError());
   return PRNN_OK;
 }
@@ -429,7 +444,8 @@ extern "C" PRNN_API size_t prnn_slstm_backward_workspace_size(int B, int T, int 
 
 extern "C" PRNN_API int prnn_slstm_backward_ex(const void* wx, const void* r, const void* h0,
                                                const void* states, const void* grad, void* gwx,
-                                               float* gr, float* gh0, int B, int T, int d,
+                                               float* gr, float* gh0, float* gb, int B, int T,
+                                               int d,
                                                float eps, int dtype, void* workspace,
                                                size_t workspace_bytes, int tag_base,
                                                void* stream) {
@@ -448,12 +464,12 @@ extern "C" PRNN_API int prnn_slstm_backward_ex(const void* wx, const void* r, co
   if (dtype == PRNN_F32)
     return slstm::run_bwd(static_cast<const float*>(wx), static_cast<const float*>(r),
                           static_cast<const float*>(h0), static_cast<const float*>(states),
-                          static_cast<const float*>(grad), static_cast<float*>(gwx), gr, gh0, B,
-                          T, d, eps, w, s);
+                          static_cast<const float*>(grad), static_cast<float*>(gwx), gr, gh0, gb,
+                          B, T, d, eps, w, s);
   return slstm::run_bwd(static_cast<const bf16*>(wx), static_cast<const bf16*>(r),
                         static_cast<const bf16*>(h0), static_cast<const bf16*>(states),
-                        static_cast<const bf16*>(grad), static_cast<bf16*>(gwx), gr, gh0, B, T, d,
-                        eps, w, s);
+                        static_cast<const bf16*>(grad), static_cast<bf16*>(gwx), gr, gh0, gb, B, T,
+                        d, eps, w, s);
 }
 
 extern "C" PRNN_API int prnn_slstm_backward(const void* wx, const void* r, const void* h0,
@@ -461,6 +477,6 @@ extern "C" PRNN_API int prnn_slstm_backward(const void* wx, const void* r, const
                                             float* gr, float* gh0, int B, int T, int d, float eps,
                                             int dtype, void* workspace, size_t workspace_bytes,
                                             void* stream) {
-  return prnn_slstm_backward_ex(wx, r, h0, states, grad, gwx, gr, gh0, B, T, d, eps, dtype,
+  return prnn_slstm_backward_ex(wx, r, h0, states, grad, gwx, gr, gh0, nullptr, B, T, d, eps, dtype,
                                 workspace, workspace_bytes, 0, stream);
 }

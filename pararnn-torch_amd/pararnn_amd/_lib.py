@@ -19,7 +19,7 @@ PRNN_OK = 0
 PRNN_ERR_VALUE = 1
 PRNN_ERR_TYPE = 2
 PRNN_ERR_RUNTIME = 3
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # name -> (restype, argtypes); mirrors include/pararnn_amd.h
 _P = ctypes.c_void_p
@@ -52,7 +52,7 @@ SIGNATURES: dict[str, tuple] = {
         _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _I, _P, _S, _I, _P]),
     "prnn_slstm_backward_ex": (
         _I,
-        [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _I, _P, _S, _I, _P],
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _I, _P, _S, _I, _P],
     ),
     "prnn_gru_head_backward_workspace_size": (_S, [_I, _I, _I, _I, _I]),
     "prnn_gru_head_backward": (

@@ -508,7 +508,8 @@ def _eq26_vjp(cell: nn.Module, states: Tensor, x: Tensor, partial: Tensor, *,
     cap = cell.max_recurrent_norm
     if isinstance(cell, ParaSLSTM) and cell.mix == "diag":
         r_mix = cell.clipped_r()
-        g_wx, g_r, g_h0 = ops.slstm_backward_fused(wx, r_mix, h0, states, partial, eps=cell.eps)
+        g_wx, g_r, g_h0, g_b = ops.slstm_backward_fused(wx, r_mix, h0, states, partial,
+                                                       eps=cell.eps)
         determinism.maybe_check_fused_vjp_once(
             (g_r,),
             lambda: (ops.slstm_backward_fused(wx, r_mix, h0, states, partial, eps=cell.eps)[1],),
@@ -516,7 +517,7 @@ def _eq26_vjp(cell: nn.Module, states: Tensor, x: Tensor, partial: Tensor, *,
         g_r = g_r.to(cell.R.dtype)
         if cap is not None:
             g_r = g_r * (cell.R.abs() <= cap).to(g_r.dtype)
-        by_name = {"R": g_r}
+        by_name = {"R": g_r, "W_x.bias": g_b.reshape(-1).to(cell.W_x.bias.dtype)}
     elif isinstance(cell, ParaGRU) and cell.mix == "head":
         a_z, a_r, a_n = cell.clipped_a_head()
         g_wx, g_a, g_h0 = ops.gru_head_backward_fused(wx, a_z, a_r, a_n, h0, states, partial)
@@ -536,7 +537,9 @@ def _eq26_vjp(cell: nn.Module, states: Tensor, x: Tensor, partial: Tensor, *,
     gy = g_wx.reshape(-1, g_wx.shape[-1])
     xx = x.reshape(-1, x.shape[-1])
     grad_x = (gy @ cell.W_x.weight).reshape(x.shape)
-    by_name.update({"W_x.weight": _weight_grad(gy, xx), "W_x.bias": gy.sum(0)})
+    if "W_x.bias" not in by_name:
+        by_name["W_x.bias"] = gy.sum(0)
+    by_name["W_x.weight"] = _weight_grad(gy, xx)
     grads = tuple(
         by_name.get(n) if p.requires_grad else None for n, p in cell.named_parameters()
     )

@@ -235,13 +235,14 @@ def _(wx, r, h0=None, states=None, block_table=None, *, max_iters, omega, eps,
 @torch.library.custom_op("pararnn::slstm_backward_fused", mutates_args=())
 def slstm_backward_fused(
     wx: Tensor, r: Tensor, h0: Tensor | None, states: Tensor, grad: Tensor, *, eps: float
-) -> tuple[Tensor, Tensor, Tensor]:
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Eq. 2.6 backward of diag ParaSLSTM at ``H* = states`` on the GPU.
 
-    Returns ``(g_wx, g_r, g_h0)``: ``dL/dwx`` ``(B, T, 4 d_h)`` in ``wx``'s
-    dtype, ``g_r`` ``(4, d_h)`` fp32 (before the clamp mask on ``R``) and
-    ``g_h0 = J_0^T mu_0`` ``(B, 4, d_h)`` fp32 (zeros-input adjoint when
-    ``h0`` is None).  The reference computes the same quantities with
+    Returns ``(g_wx, g_r, g_h0, g_b)``: ``dL/dwx`` ``(B, T, 4 d_h)`` in
+    ``wx``'s dtype, ``g_r`` ``(4, d_h)`` fp32 (before the clamp mask on ``R``),
+    ``g_h0 = J_0^T mu_0`` ``(B, 4, d_h)`` fp32 (zeros-input adjoint when ``h0``
+    is None) and ``g_b = sum_{b,t} dL/dwx`` ``(4, d_h)`` fp32 (the ``W_x`` bias
+    gradient, summed in the same pass).  The reference computes the same quantities with
     ``step_and_jacobian`` + ``reverse_scan_block4`` + ``slstm_recurrence_vjp``
     (solvers/newton/__init__.py:765-866, kernels/vjp_slstm.py:209-240).
     """
@@ -255,6 +256,7 @@ def slstm_backward_fused(
     g_wx = torch.empty_like(wx)
     g_r = torch.empty(4, d_h, dtype=torch.float32, device=wx.device)
     g_h0 = torch.zeros(batch, 4, d_h, dtype=torch.float32, device=wx.device)
+    g_b = torch.empty(4, d_h, dtype=torch.float32, device=wx.device)
     lib = _lib.load()
     _lib.sync_deterministic(lib)
     with torch.cuda.device(wx.device):
@@ -262,11 +264,11 @@ def slstm_backward_fused(
         ws, tag = _slstm_workspace(nbytes, wx.device)
         rc = lib.prnn_slstm_backward_ex(
             _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), _ptr(grad), _ptr(g_wx), _ptr(g_r),
-            _ptr(g_h0), batch, time, d_h, float(eps), code, _ptr(ws), ws.numel(), tag,
+            _ptr(g_h0), _ptr(g_b), batch, time, d_h, float(eps), code, _ptr(ws), ws.numel(), tag,
             _stream(wx.device),
         )
     _lib.check(rc, "slstm_backward_fused")
-    return g_wx, g_r, g_h0
+    return g_wx, g_r, g_h0, g_b
 
 
 @slstm_backward_fused.register_fake
@@ -276,6 +278,7 @@ def _(wx, r, h0, states, grad, *, eps):
         torch.empty_like(wx),
         wx.new_empty(4, d_h, dtype=torch.float32),
         wx.new_empty(batch, 4, d_h, dtype=torch.float32),
+        wx.new_empty(4, d_h, dtype=torch.float32),
     )
 
 

@@ -86,6 +86,6 @@ def test_host_only_calls():
     rc = lib.prnn_slstm_init_ex(None, None, None, None, 1, 1, 1, 0, 1e-6, 0, None, 0,
                                 (1 << 30) + 1, None)
     assert rc == _lib.PRNN_ERR_VALUE and b"tag_base" in lib.prnn_last_error()
-    rc = lib.prnn_slstm_backward_ex(None, None, None, None, None, None, None, None, 1, 1, 1,
+    rc = lib.prnn_slstm_backward_ex(None, None, None, None, None, None, None, None, None, 1, 1, 1,
                                     1e-6, 0, None, 0, 5, None)
     assert rc == _lib.PRNN_ERR_VALUE and b"non-null" in lib.prnn_last_error()

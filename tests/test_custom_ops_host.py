@@ -42,7 +42,9 @@ def test_slstm_fake_kernels(dtype):
         out0 = torch.ops.pararnn.newton_slstm_fused(wx, r, None, None, None, max_iters=2,
                                                     omega=1.0, eps=1e-6)
         assert out0.shape == (B, T, 4, d)
-        g_wx, g_r, g_h0 = torch.ops.pararnn.slstm_backward_fused(wx, r, h0, out, out, eps=1e-6)
+        g_wx, g_r, g_h0, g_b = torch.ops.pararnn.slstm_backward_fused(wx, r, h0, out, out,
+                                                                      eps=1e-6)
+        assert g_b.shape == (4, d) and g_b.dtype == torch.float32
         assert g_wx.shape == wx.shape and g_wx.dtype == dtype
         assert g_r.shape == (4, d) and g_r.dtype == torch.float32
         assert g_h0.shape == (B, 4, d) and g_h0.dtype == torch.float32

@@ -140,9 +140,9 @@ def test_slstm_ops_deterministic_repeat(deterministic):
     for _ in range(4):
         guess = ops.slstm_init_fused(wx, r, None, picard_iters=5, eps=1e-6)
         H = ops.newton_slstm_fused(wx, r, None, guess, max_iters=2, omega=1.0, eps=1e-6)
-        g_wx, g_r, g_h0 = ops.slstm_backward_fused(wx, r, None, H, grad, eps=1e-6)
+        g_wx, g_r, g_h0, g_b = ops.slstm_backward_fused(wx, r, None, H, grad, eps=1e-6)
         torch.cuda.synchronize()
-        outs.append({"guess": guess, "H": H, "g_wx": g_wx, "g_r": g_r})
+        outs.append({"guess": guess, "H": H, "g_wx": g_wx, "g_r": g_r, "g_b": g_b})
     for o in outs[1:]:
         eq = _bitequal(outs[0], o)
         assert all(eq.values()), eq
@@ -192,7 +192,7 @@ def test_tagged_workspace_matches_cleared(monkeypatch):
             for wx, r, grad in cases:
                 guess = ops.slstm_init_fused(wx, r, None, picard_iters=5, eps=1e-6)
                 H = ops.newton_slstm_fused(wx, r, None, guess, max_iters=2, omega=1.0, eps=1e-6)
-                g_wx, g_r, _ = ops.slstm_backward_fused(wx, r, None, H, grad, eps=1e-6)
+                g_wx, g_r, _, _ = ops.slstm_backward_fused(wx, r, None, H, grad, eps=1e-6)
                 outs.append((guess, H, g_wx, g_r))
             torch.cuda.synchronize()
             return outs

@@ -68,13 +68,15 @@ def _op_vs_exact(t, m, dtype, tag, tol_wx, tol_r, tol_h0):
     p = O.SLSTMParams(t["W"], t["b"], t["R"])
     wx = p.wx(x)
     ex = _exact(t, x, states, grad, h0, wx)
-    g_wx, g_r, g_h0 = _op(wx.to(DEV), p.r().to(DEV), None if h0 is None else h0.to(DEV),
-                          states.to(DEV), grad.to(DEV), m["eps"])
+    g_wx, g_r, g_h0, g_b = _op(wx.to(DEV), p.r().to(DEV), None if h0 is None else h0.to(DEV),
+                               states.to(DEV), grad.to(DEV), m["eps"])
     torch.cuda.synchronize()
     e_wx = _rel(g_wx, ex["g_wx"])
     e_r = _rel(g_r, _exact_r_unmasked(t, x, states, grad, h0, wx))
-    print(f"[{tag}] op vs float64: g_wx rel {e_wx:.2e}, g_r rel {e_r:.2e}", flush=True)
-    assert e_wx <= tol_wx and e_r <= tol_r
+    e_b = _rel(g_b.reshape(-1), ex["b"])
+    print(f"[{tag}] op vs float64: g_wx rel {e_wx:.2e}, g_r rel {e_r:.2e}, g_b rel {e_b:.2e}",
+          flush=True)
+    assert e_wx <= tol_wx and e_r <= tol_r and e_b <= tol_r
     if h0 is not None:
         e_h0 = _rel(g_h0, ex["h0"])
         print(f"[{tag}] g_h0 rel {e_h0:.2e}", flush=True)
@@ -177,10 +179,12 @@ def test_op_ragged_shapes_fp32(B, T, d, with_h0):
     t = {"W": W, "b": b, "R": R}
     ex = _exact(t, x, states, grad, h0)
     ex_r = _exact_r_unmasked(t, x, states, grad, h0)
-    g_wx, g_r, g_h0 = _op(p.wx(x).to(DEV), p.r().to(DEV), None if h0 is None else h0.to(DEV),
-                          states.to(DEV), grad.to(DEV), 1e-6)
-    e = (_rel(g_wx, ex["g_wx"]), _rel(g_r, ex_r), _rel(g_h0, ex["h0"]) if with_h0 else 0.0)
-    print(f"  rel err g_wx {e[0]:.2e} g_r {e[1]:.2e} g_h0 {e[2]:.2e}", flush=True)
+    g_wx, g_r, g_h0, g_b = _op(p.wx(x).to(DEV), p.r().to(DEV),
+                               None if h0 is None else h0.to(DEV), states.to(DEV),
+                               grad.to(DEV), 1e-6)
+    e = (_rel(g_wx, ex["g_wx"]), _rel(g_r, ex_r), _rel(g_h0, ex["h0"]) if with_h0 else 0.0,
+         _rel(g_b.reshape(-1), ex["b"]))
+    print(f"  rel err g_wx {e[0]:.2e} g_r {e[1]:.2e} g_h0 {e[2]:.2e} g_b {e[3]:.2e}", flush=True)
     assert max(e) <= 5e-5
 
 
@@ -201,7 +205,7 @@ def test_long_sequence_bf16_cfg5_slice():
     t = {"W": W.float(), "b": b.float(), "R": R.float()}
     wx = p.wx(x)
     ex = _exact(t, x.float(), states.float(), grad.float(), None, wx)
-    g_wx, g_r, _ = _op(wx.to(DEV), p.r().to(DEV), None, states.to(DEV), grad.to(DEV), 1e-6)
+    g_wx, g_r, _, _ = _op(wx.to(DEV), p.r().to(DEV), None, states.to(DEV), grad.to(DEV), 1e-6)
     e_wx = _rel(g_wx, ex["g_wx"])
     nrel = ((g_wx.float().cpu().double() - ex["g_wx"]).norm() / ex["g_wx"].norm()).item()
     e_r = _rel(g_r, _exact_r_unmasked(t, x.float(), states.float(), grad.float(), None, wx))
