@@ -86,7 +86,9 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
     float* __restrict__ gr_part, float* __restrict__ gh0, int B, int T, int d, int n_cb,
     int n_chunks, float eps, int* __restrict__ counter, unsigned long long* __restrict__ agg,
     unsigned long long* __restrict__ incl, int epoch) {
-  constexpr int KP = 1;  // predecessors per wave per look-back round
+  // predecessors per wave per look-back round (the deterministic walk, which
+  // must find an inclusive carry inside its window, looks twice as far)
+  constexpr int KP = DET ? 2 : 1;
   using RS = RowStash<TX>;
   constexpr uint32_t SZ = sizeof(TX);
   __shared__ float s_agg[W][20][kCB];

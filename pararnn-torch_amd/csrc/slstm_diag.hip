@@ -579,7 +579,9 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
     const TIN* __restrict__ hin, TOUT* __restrict__ hout, int B, int T, int d, int n_cb,
     float omega, float eps, int* __restrict__ counter, unsigned long long* __restrict__ agg,
     unsigned long long* __restrict__ incl, int epoch) {
-  constexpr int KP = 1;  // predecessors per wave per look-back round
+  // predecessors per wave per look-back round (the deterministic walk, which
+  // must find an inclusive carry inside its window, looks twice as far)
+  constexpr int KP = DET ? 2 : 1;
   using XS = RowStash<TX>;
   using HS = RowStash<TIN>;
   __shared__ float s_agg[W][20][kCB];
@@ -784,7 +786,9 @@ slstm_newton_fused_kernel(
     int n_tiles, int K, float omega, float eps, int* __restrict__ counter,
     unsigned long long* __restrict__ agg, unsigned long long* __restrict__ incl,
     unsigned long long* __restrict__ hlast, int tag_base) {
-  constexpr int KP = 1;  // predecessors per wave per look-back round
+  // predecessors per wave per look-back round (the deterministic walk, which
+  // must find an inclusive carry inside its window, looks twice as far)
+  constexpr int KP = DET ? 2 : 1;
   using XS = RowStash<TX>;
   __shared__ float s_agg[W][20][kCB];
   __shared__ float s_carry[W][4][kCB];
