@@ -37,7 +37,6 @@ namespace gru {
 
 constexpr int DH = 64;      // head width handled by these kernels
 constexpr int kChunk = 32;  // time steps per chunk
-constexpr int kCarryParts = 16;  // threads per row of the carry mat-vec
 constexpr int kPad = 72;    // bf16 row stride of the LDS operand tiles (16-byte aligned rows)
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -637,28 +636,41 @@ __global__ __launch_bounds__(256) void gru_group_kernel(const float* __restrict_
 // Carries over chunks: carry_0 = 0, carry_{c+1} = Phi_c carry_c + e_c.
 // REV (eq. 2.6 backward, phi holding Phi^T): chunks from the last one down,
 // carry_{n-1} = 0, carry_{c-1} = Phi_c^T carry_c + e_c.
-// 64 kCarryParts threads: thread (i, part) sums 64 / kCarryParts of row i's
-// products.
+// 64 PARTS threads: thread (i, part) sums 64 / PARTS of row i's products
+// (PARTS = 16 for a single long chain per block, more loads in flight;
+// PARTS = 4 for many short chains, a 4-wave barrier per step).
 // ---------------------------------------------------------------------------
-template <bool REV>
-__global__ __launch_bounds__(64 * kCarryParts) void gru_carry_kernel(
+template <int PARTS>
+__device__ __forceinline__ float parts_sum(float v) {
+  if constexpr (PARTS == 16) {
+    return row_sum16(v);  // the 16 threads of a row are one DPP row; lane 15 holds the sum
+  } else {
+    static_assert(PARTS == 4, "4 or 16 threads per row");
+    v += dpp_f<0xB1>(v);  // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);  // quad_perm [2,3,0,1]: every lane of the quad holds the sum
+    return v;
+  }
+}
+
+template <bool REV, int PARTS>
+__global__ __launch_bounds__(64 * PARTS) void gru_carry_kernel(
     const float* __restrict__ phi, const float* __restrict__ e, int n_chunks, int group,
     const float* __restrict__ init, float* __restrict__ carry_in) {
   // The chain is serial over chunks, so each step costs the latency of its
-  // 16 KB of Phi and its e.  Thread (i, part) holds 4 entries of row i; the
+  // 16 KB of Phi and its e.  Thread (i, part) holds NQ float4 of row i; the
   // chunks are fetched a block of kB ahead into one of two register blocks
   // (written out by hand, no dynamic register indexing) while the other block
   // is walked, and a block's carries are stored after its kB steps.
   // Block (seq, g) walks steps [g group, (g + 1) group) of the walk order
   // (chunks ascending, or descending for REV) from init[seq, g] (zeros when
   // init is NULL).
-  static_assert(DH / kCarryParts == 4, "one float4 of a Phi row per thread");
-  constexpr int kB = 8;
+  constexpr int NQ = DH / PARTS / 4;  // float4 per thread and row
+  constexpr int kB = PARTS == 16 ? 8 : 4;
   __shared__ float s_c[2][DH];
   const int n_groups = (n_chunks + group - 1) / group;
   const int seq = blockIdx.x / n_groups, grp = blockIdx.x % n_groups;
   const int w_begin = grp * group, w_end = min(n_chunks, w_begin + group);
-  const int i = threadIdx.x / kCarryParts, part = threadIdx.x % kCarryParts;
+  const int i = threadIdx.x / PARTS, part = threadIdx.x % PARTS;
   if (threadIdx.x < DH)
     s_c[0][threadIdx.x] = init != nullptr ? init[static_cast<size_t>(blockIdx.x) * DH + threadIdx.x] : 0.f;
   __syncthreads();
@@ -670,35 +682,41 @@ __global__ __launch_bounds__(64 * kCarryParts) void gru_carry_kernel(
     const int k = min(step, w_end - 1);
     return REV ? n_chunks - 1 - k : k;
   };
-  auto fetch = [&](int step0, float4 rows[kB], float ev[kB]) {
+  auto fetch = [&](int step0, float4 rows[kB][NQ], float ev[kB]) {
 #pragma unroll
     for (int k = 0; k < kB; ++k) {
       const int c = chunk_of(step0 + k);
-      rows[k] = *reinterpret_cast<const float4*>(P + (static_cast<size_t>(c) * DH + i) * DH + 4 * part);
+      const float* row = P + (static_cast<size_t>(c) * DH + i) * DH + 4 * NQ * part;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) rows[k][q] = *reinterpret_cast<const float4*>(row + 4 * q);
       ev[k] = E[static_cast<size_t>(c) * DH + i];
     }
   };
   int cur = 0;
-  auto walk = [&](int step0, const float4 rows[kB], const float ev[kB]) {
+  auto walk = [&](int step0, const float4 rows[kB][NQ], const float ev[kB]) {
     float out[kB];
 #pragma unroll
     for (int k = 0; k < kB; ++k) {
-      const float4 v = *reinterpret_cast<const float4*>(s_c[cur] + 4 * part);
-      float acc = rows[k].x * v.x + rows[k].y * v.y + rows[k].z * v.z + rows[k].w * v.w;
-      acc = row_sum16(acc);  // the 16 threads of row i are one DPP row; lane 15 holds the sum
+      float acc = 0.f;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const float4 v = *reinterpret_cast<const float4*>(s_c[cur] + 4 * NQ * part + 4 * q);
+        acc += rows[k][q].x * v.x + rows[k][q].y * v.y + rows[k][q].z * v.z + rows[k][q].w * v.w;
+      }
+      acc = parts_sum<PARTS>(acc);
       out[k] = s_c[cur][i];
-      if (part == kCarryParts - 1) s_c[cur ^ 1][i] = acc + ev[k];
+      if (part == PARTS - 1) s_c[cur ^ 1][i] = acc + ev[k];
       __syncthreads();
       cur ^= 1;
     }
-    if (part == kCarryParts - 1) {
+    if (part == PARTS - 1) {
 #pragma unroll
       for (int k = 0; k < kB; ++k)
         if (step0 + k < w_end)
           carry_in[(static_cast<size_t>(seq) * n_chunks + chunk_of(step0 + k)) * DH + i] = out[k];
     }
   };
-  float4 ra[kB], rb[kB];
+  float4 ra[kB][NQ], rb[kB][NQ];
   float ea[kB], eb[kB];
   fetch(w_begin, ra, ea);
   for (int step0 = w_begin; step0 < w_end; step0 += 2 * kB) {
@@ -1481,21 +1499,21 @@ template <bool REV>
 static void carry_scan(const float* phi, const float* e, float* carry, int n_seq, int n_chunks,
                        const CarryWs& c, hipStream_t stream) {
   const int n_groups = (n_chunks + kGroup - 1) / kGroup;
-  const dim3 walk_block(64 * kCarryParts);
+  const dim3 walk_block(64 * 16), rewalk_block(64 * 4);
   static const bool single = [] {
     const char* e = getenv("PRNN_GRU_CARRY_SINGLE");
     return e && atoi(e) != 0;
   }();
   if (n_groups <= 1 || single) {
-    gru_carry_kernel<REV><<<dim3(n_seq), walk_block, 0, stream>>>(phi, e, n_chunks, n_chunks,
+    gru_carry_kernel<REV, 16><<<dim3(n_seq), walk_block, 0, stream>>>(phi, e, n_chunks, n_chunks,
                                                                   nullptr, carry);
     return;
   }
   gru_group_kernel<REV><<<dim3(n_seq * n_groups), dim3(256), 0, stream>>>(phi, e, n_chunks, c.psi,
                                                                          c.ell);
-  gru_carry_kernel<false><<<dim3(n_seq), walk_block, 0, stream>>>(c.psi, c.ell, n_groups,
+  gru_carry_kernel<false, 16><<<dim3(n_seq), walk_block, 0, stream>>>(c.psi, c.ell, n_groups,
                                                                   n_groups, nullptr, c.cg);
-  gru_carry_kernel<REV><<<dim3(n_seq * n_groups), walk_block, 0, stream>>>(phi, e, n_chunks,
+  gru_carry_kernel<REV, 4><<<dim3(n_seq * n_groups), rewalk_block, 0, stream>>>(phi, e, n_chunks,
                                                                            kGroup, c.cg, carry);
 }
 
