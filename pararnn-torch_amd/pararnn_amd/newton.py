@@ -33,7 +33,7 @@ from torch import Tensor, nn
 from pararnn_amd import determinism, ops
 from pararnn_amd.cells import SLSTM_HIDDEN, ParaGRU, ParaSLSTM
 from pararnn_amd.ragged import (
-    Padding,
+    RaggedPlan,
     gather_h0,
     prepend_state_ragged,
     validate_cu_seqlens,
@@ -174,12 +174,11 @@ def fused_newton(
             h0 = gather_h0(h0, block_table, wx.shape[0], (4, int(cell.d_h)))
         if cu_seqlens is not None:
             # packed sequences as a padded batch, each from its own h0
-            pad = Padding(validate_cu_seqlens(cu_seqlens, wx.shape[1]), wx.device)
-            dense = fused_newton(cell, pad.pad(wx), max_iters=max_iters, omega=omega, h0=h0,
-                                 log_coords=log_coords, picard_iters=picard_iters,
-                                 scan_tile=scan_tile, fused_time_loop=fused_time_loop,
-                                 fused_window_len=fused_window_len)
-            return pad.unpad(dense)
+            plan = RaggedPlan(validate_cu_seqlens(cu_seqlens, wx.shape[1]), wx.device)
+            return plan.run(wx, h0, lambda w, h: fused_newton(
+                cell, w, max_iters=max_iters, omega=omega, h0=h,
+                log_coords=log_coords, picard_iters=picard_iters, scan_tile=scan_tile,
+                fused_time_loop=fused_time_loop, fused_window_len=fused_window_len))
         r = cell.clipped_r()
         states = ops.slstm_init_fused(wx, r, h0, picard_iters=int(picard_iters), eps=cell.eps)
         return ops.newton_slstm_fused(
@@ -386,16 +385,16 @@ def _newton_ragged(cell, x, config, *, h0, stats, cu_seqlens, block_table, needs
         h0 = gather_h0(h0, block_table, n_seq, _state_tail(cell))
     elif h0 is not None and h0.shape[0] != n_seq:
         raise ValueError(f"h0 batch {h0.shape[0]} != n_seq {n_seq}")
-    pad = Padding(cs, x.device)
-    xp = pad.pad(x)
+    plan = RaggedPlan(cs, x.device)
     ladder = bool(config.picard_adapt) and isinstance(cell, ParaSLSTM)
     inner = replace(config, picard_adapt=False, residual_fail=None)
     hist = []
     while True:
         if needs_grad:
-            states = pad.unpad(newton_apply(cell, xp, inner, h0=h0))
+            states = plan.run(x, h0, lambda xp, h: newton_apply(cell, xp, inner, h0=h))
         else:
-            states = pad.unpad(_newton_forward(cell, xp, inner, h0=h0, stats=None))
+            states = plan.run(x, h0, lambda xp, h: _newton_forward(cell, xp, inner, h0=h,
+                                                                  stats=None))
         if stats is None and config.residual_fail is None and not ladder:
             return states
         with torch.no_grad():

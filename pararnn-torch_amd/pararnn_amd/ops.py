@@ -316,16 +316,16 @@ def newton_gru_head_fused(
         raise TypeError(f"newton_gru_head_fused: pararnn_amd provides d_head=64, got {d_head}")
     if cu_seqlens is not None:
         # Packed sequences run as a padded batch, each from its own h0.
-        from pararnn_amd.ragged import Padding, validate_cu_seqlens
+        from pararnn_amd.ragged import RaggedPlan, validate_cu_seqlens
 
         if wx.shape[0] != 1:
             raise ValueError(f"cu_seqlens packs wx with batch=1, got batch={wx.shape[0]}")
         cs = validate_cu_seqlens(cu_seqlens, wx.shape[1])
-        pad = Padding(cs, wx.device)
-        if h0 is not None and h0.shape != (pad.n_seq, d_h):
-            raise ValueError(f"h0 shape {tuple(h0.shape)} != {(pad.n_seq, d_h)}")
-        dense = _gru_head_dense(pad.pad(wx), a_z, a_r, a_n, h0, max_iters, omega)
-        return pad.unpad(dense)
+        plan = RaggedPlan(cs, wx.device)
+        if h0 is not None and h0.shape != (plan.n_seq, d_h):
+            raise ValueError(f"h0 shape {tuple(h0.shape)} != {(plan.n_seq, d_h)}")
+        return plan.run(wx, h0, lambda w, h: _gru_head_dense(w, a_z, a_r, a_n, h, max_iters,
+                                                              omega))
     return _gru_head_dense(wx, a_z, a_r, a_n, h0, max_iters, omega)
 
 

@@ -135,3 +135,72 @@ def test_ragged_backward_equals_per_sequence_sum():
         e = ((a - b).abs().max() / b.abs().max()).item()
         print(f"  grad {name}: rel diff {e:.2e}", flush=True)
         assert e <= 1e-5
+
+
+def _uneven(d_x, extra=(), seed=5):
+    """Lengths that make three length groups (one rectangle would pad the
+    short sequences ~40x)."""
+    from pararnn_amd.ragged import RaggedPlan
+
+    lengths = [2500, 31, 900, 700, 12, 60]
+    cs = torch.tensor([0] + lengths).cumsum(0)
+    assert RaggedPlan(cs, torch.device("cpu")).n_groups == 3
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(1, int(cs[-1]), d_x, generator=g)
+    return lengths, cs, x, [torch.randn(len(lengths), *e, generator=g) for e in extra]
+
+
+def test_slstm_ragged_length_groups(monkeypatch):
+    """Uneven lengths run as several padded groups: forward against the
+    per-sequence oracle, forward and every gradient against the single
+    padded rectangle (PARARNN_AMD_RAGGED_GROUPS=0)."""
+    from pararnn_amd import ParaSLSTM, newton_apply
+
+    print("case slstm ragged length groups fp32 (3 groups, lengths 12..2500)", flush=True)
+    torch.manual_seed(4)
+    cell = ParaSLSTM(8, 32).to(DEV)
+    lengths, cs, x, (h0,) = _uneven(8, extra=((4, 32),))
+    h0[:, 1] = h0[:, 1].abs() + 0.5
+    up = torch.randn(1, x.shape[1], 4, 32, generator=torch.Generator().manual_seed(6))
+    cfg = _cfg(3, 3)
+    x, h0, up, csd = x.to(DEV), h0.to(DEV), up.to(DEV), cs.to(DEV)
+
+    def run():
+        cell.zero_grad(set_to_none=True)
+        xx, hh = x.clone().requires_grad_(True), h0.clone().requires_grad_(True)
+        H = newton_apply(cell, xx, cfg, h0=hh, cu_seqlens=csd)
+        (H * up).sum().backward()
+        out = {"H": H.detach(), "x": xx.grad, "h0": hh.grad}
+        out.update({n: p.grad.clone() for n, p in cell.named_parameters()})
+        return out
+
+    grouped = run()
+    monkeypatch.setenv("PARARNN_AMD_RAGGED_GROUPS", "0")
+    single = run()
+    for k in grouped:
+        e = ((grouped[k] - single[k]).abs().max() / single[k].abs().max()).item()
+        print(f"  {k}: grouped vs single rel diff {e:.2e}", flush=True)
+        assert e <= 1e-5, k
+    p = O.SLSTMParams(cell.W_x.weight.detach().cpu(), cell.W_x.bias.detach().cpu(),
+                      cell.R.detach().cpu())
+    own = slstm_newton_ragged(p, x.cpu(), cs, max_iters=3, picard_iters=3, h0=h0.cpu())
+    e_own = ((grouped["H"].cpu() - own).abs() / (1 + own.abs())).max().item()
+    print(f"  rel err vs per-sequence oracle {e_own:.2e}", flush=True)
+    assert e_own <= 3e-5
+
+
+def test_gru_head_ragged_length_groups(monkeypatch):
+    from pararnn_amd import ParaGRU, newton_apply
+
+    print("case gru head ragged length groups fp32 (3 groups, lengths 12..2500)", flush=True)
+    torch.manual_seed(7)
+    cell = ParaGRU(16, 128, mix="head", n_heads=2).to(DEV)
+    lengths, cs, x, (h0,) = _uneven(16, extra=((128,),))
+    x, h0, csd = x.to(DEV), (0.3 * h0).to(DEV), cs.to(DEV)
+    with torch.no_grad():
+        a = newton_apply(cell, x, _cfg(3), h0=h0, cu_seqlens=csd)
+        monkeypatch.setenv("PARARNN_AMD_RAGGED_GROUPS", "0")
+        b = newton_apply(cell, x, _cfg(3), h0=h0, cu_seqlens=csd)
+    err = (a - b).abs().max().item()
+    print(f"  max|grouped - single| {err:.2e}", flush=True)
+    assert err <= 1e-5

@@ -3,7 +3,14 @@
 import pytest
 import torch
 
-from pararnn_amd.ragged import Padding, gather_h0, prepend_state_ragged, validate_cu_seqlens
+from pararnn_amd.ragged import (
+    Padding,
+    RaggedPlan,
+    gather_h0,
+    length_groups,
+    prepend_state_ragged,
+    validate_cu_seqlens,
+)
 
 
 @pytest.mark.parametrize("cs,time,msg", [
@@ -65,3 +72,46 @@ def test_newton_apply_ragged_rejects_batched_x():
         newton_apply(cell, x, NewtonConfig(), cu_seqlens=torch.tensor([0, 6]))
     with pytest.raises(ValueError, match="chunk_len"):
         newton_apply(cell, x[:1], NewtonConfig(chunk_len=2), cu_seqlens=torch.tensor([0, 6]))
+
+
+def test_length_groups_bound_padding():
+    g = torch.Generator().manual_seed(0)
+    lengths = [int(v) for v in torch.randint(1, 5000, (200,), generator=g)] + [100000, 3]
+    groups = length_groups(lengths)
+    assert sorted(i for grp in groups for i in grp) == list(range(len(lengths)))
+    for grp in groups:
+        top = max(lengths[i] for i in grp)
+        assert all(top <= max(2 * lengths[i], lengths[i] + 256) for i in grp)
+    # one rectangle would cost 202 * 100000 steps; the groups stay near 2 N
+    padded = sum(len(grp) * max(lengths[i] for i in grp) for grp in groups)
+    assert padded <= 2 * sum(lengths) + 256 * len(lengths)
+    assert len(groups) <= 12
+    # near-uniform lengths stay one rectangle
+    assert len(length_groups([4096, 4000, 3000, 2100])) == 1
+
+
+def _solve_marker(padded, h0):
+    """A stand-in solve: every step of row s gets its input plus h0[s]; the
+    padded rectangle must be (S_g, T_g, ...) with the group's own h0 rows."""
+    assert h0 is None or h0.shape[0] == padded.shape[0]
+    return padded if h0 is None else padded + h0[:, None]
+
+
+@pytest.mark.parametrize("lengths", [[3, 1, 5], [700, 5, 2, 1300, 40, 9000, 3]])
+def test_ragged_plan_packed_order(lengths, monkeypatch):
+    cs = torch.tensor([0] + lengths).cumsum(0)
+    n = int(cs[-1])
+    packed = torch.randn(1, n, 3, requires_grad=True)
+    h0 = torch.randn(len(lengths), 3)
+    want = packed.detach() + h0.repeat_interleave(torch.tensor(lengths), 0)[None]
+    plan = RaggedPlan(cs, torch.device("cpu"))
+    assert plan.n_groups == (1 if max(lengths) < 600 else 3)
+    assert plan.padded_steps <= 2 * n + 256 * len(lengths)
+    out = plan.run(packed, h0, _solve_marker)
+    assert torch.equal(out, want)
+    out.mul(torch.arange(n, dtype=torch.float32)[None, :, None]).sum().backward()
+    assert torch.equal(packed.grad[0, :, 0], torch.arange(n, dtype=torch.float32))
+    monkeypatch.setenv("PARARNN_AMD_RAGGED_GROUPS", "0")
+    single = RaggedPlan(cs, torch.device("cpu"))
+    assert single.n_groups == 1 and single.padded_steps == len(lengths) * max(lengths)
+    assert torch.equal(single.run(packed.detach(), h0, _solve_marker), want)
