@@ -204,6 +204,71 @@ def slstm_cfg2(torch, reps: int):
     }
 
 
+def ragged_decode(torch, reps: int):
+    """The packed-ragged and T=1 rows beside the metric (not bench lines of
+    their own): ParaSLSTM diag d=1024 bf16, K=2, P=5.
+    - ragged: one sequence of 65536 steps and 63 of 1024 packed into
+      (1, N, d), newton_apply end to end (GEMM included), with the length
+      groups and as one padded rectangle (PARARNN_AMD_RAGGED_GROUPS=0);
+    - decode: one step for 64 rows from a resident state and wx, eager and
+      replayed from a captured HIP graph."""
+    import os
+
+    from pararnn_amd import NewtonConfig, ParaSLSTM, decode_step, newton_apply
+
+    dev = "cuda:0"
+    torch.manual_seed(0)
+    cell = ParaSLSTM(D, D).to(dev, torch.bfloat16)
+    lengths = [65536] + [1024] * 63
+    cs = torch.tensor([0] + lengths).cumsum(0).to(dev)
+    n = int(cs[-1])
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn(1, n, D, generator=g, device=dev).to(torch.bfloat16)
+    cfg = NewtonConfig(max_iters=K, picard_iters=P, residual_atol=None, residual_fail=None,
+                       picard_adapt=False)
+    prev = os.environ.get("PARARNN_AMD_RAGGED_GROUPS")
+    res = {}
+    try:
+        with torch.no_grad():
+            for mode, key in (("1", "grouped"), ("0", "one_rectangle")):
+                os.environ["PARARNN_AMD_RAGGED_GROUPS"] = mode
+                ms = _time(torch, lambda: newton_apply(cell, x, cfg, cu_seqlens=cs),
+                           reps if mode == "1" else 2, warm=1)
+                res[key] = {"ms": ms, "tokens_per_s": n / (ms * 1e-3)}
+    finally:
+        if prev is None:
+            os.environ.pop("PARARNN_AMD_RAGGED_GROUPS", None)
+        else:
+            os.environ["PARARNN_AMD_RAGGED_GROUPS"] = prev
+    ragged = {"workload": f"ParaSLSTM diag d=1024 bf16 K=2 P=5, cu_seqlens 1x65536 + 63x1024 "
+                          f"(N={n}), newton_apply", **res}
+
+    rows = 64
+    state = torch.randn(rows, 4, D, generator=g, device=dev).to(torch.bfloat16)
+    state[:, 1] = state[:, 1].abs() + 0.5
+    wx = torch.randn(rows, 4 * D, generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(state)
+    with torch.no_grad():
+        eager = _time(torch, lambda: decode_step(cell, state, wx=wx, out=out), 50)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            decode_step(cell, state, wx=wx, out=out)
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(16):
+                decode_step(cell, state, wx=wx, out=out)
+        graph.replay()
+        torch.cuda.synchronize()
+        replay = _time(torch, graph.replay, 20) / 16
+    decode = {"workload": "ParaSLSTM diag d=1024 bf16, decode_step of 64 rows, state and wx "
+                          "resident",
+              "eager_us_per_step": eager * 1e3, "graph_us_per_step": replay * 1e3,
+              "graph_tokens_per_s": rows / (replay * 1e-3)}
+    return ragged, decode
+
+
 def head_cfg4(torch, reps: int):
     """ParaGRU mix='head', H=8, d_head=64 (d=512), B=4,
     T=32768, K=3, x ~ N(0, 1): the forward solve in fp32 and bf16, the eq. 2.6
@@ -265,6 +330,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-train", action="store_true", help="skip the config 5 training step")
     ap.add_argument("--no-head", action="store_true", help="skip the config 4 head-GRU lines")
+    ap.add_argument("--no-ragged", action="store_true",
+                    help="skip the ragged cu_seqlens and T=1 decode lines")
     ap.add_argument("--head-only", action="store_true",
                     help="only the config 4 head-GRU lines (for profiling that path)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -425,6 +492,8 @@ def main() -> int:
         out["train_cfg5"] = train_cfg5(torch, max(3, args.steps // 4))
     if not args.no_head:
         out["head_cfg4"] = head_cfg4(torch, 3)
+    if not args.no_ragged:
+        out["ragged"], out["decode_t1"] = ragged_decode(torch, 5)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(torch, args.cpu_sample)
         out["gpu_over_cpu"] = out["value"] / out["cpu_baseline"]["value"]
