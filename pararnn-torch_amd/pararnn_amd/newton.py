@@ -170,8 +170,10 @@ def fused_newton(
         )
     if isinstance(cell, ParaSLSTM) and cell.mix == "diag":
         if block_table is not None:
-            # paged h0 rows, for the guess and the iterations alike
-            h0 = gather_h0(h0, block_table, wx.shape[0], (4, int(cell.d_h)))
+            # paged h0 rows (one per sequence when packed), for the guess and
+            # the iterations alike
+            rows = wx.shape[0] if cu_seqlens is None else int(cu_seqlens.numel()) - 1
+            h0 = gather_h0(h0, block_table, rows, (4, int(cell.d_h)))
         if cu_seqlens is not None:
             # packed sequences as a padded batch, each from its own h0
             plan = RaggedPlan(validate_cu_seqlens(cu_seqlens, wx.shape[1]), wx.device)

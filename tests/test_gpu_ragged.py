@@ -204,3 +204,33 @@ def test_gru_head_ragged_length_groups(monkeypatch):
     err = (a - b).abs().max().item()
     print(f"  max|grouped - single| {err:.2e}", flush=True)
     assert err <= 1e-5
+
+
+def test_fused_newton_cu_seqlens_with_block_table():
+    """Packed sequences with a paged h0: packed sequence s reads pool row
+    block_table[s] (kernels/_fused_common.py:56, newton_cfc.py:357), the same
+    result as the gathered dense h0."""
+    from pararnn_amd import ParaSLSTM, fused_newton
+
+    print("case slstm fused_newton cu_seqlens + block_table (6 sequences, pool of 8)", flush=True)
+    torch.manual_seed(8)
+    cell = ParaSLSTM(8, 32).to(DEV)
+    g = torch.Generator().manual_seed(9)
+    lengths, cs, x, (pool,) = _uneven(8, extra=((4, 32),))
+    pool = torch.randn(len(lengths) + 2, 4, 32, generator=g)
+    pool[:, 1] = pool[:, 1].abs() + 0.5
+    pool, csd = pool.to(DEV), cs.to(DEV)
+    bt = torch.tensor([6, 0, 3, 3, 7, 1], device=DEV)
+    with torch.no_grad():
+        wx = cell.W_x(x.to(DEV))
+        a = fused_newton(cell, wx, max_iters=2, omega=1.0, h0=pool, picard_iters=3,
+                         cu_seqlens=csd, block_table=bt)
+        b = fused_newton(cell, wx, max_iters=2, omega=1.0, h0=pool[bt], picard_iters=3,
+                         cu_seqlens=csd)
+    err = ((a - b).abs().max() / b.abs().max()).item()
+    print(f"  rel diff paged vs gathered h0 {err:.2e}", flush=True)
+    assert err <= 1e-6
+    with pytest.raises(ValueError, match="block_table B=2"):
+        with torch.no_grad():
+            fused_newton(cell, wx, max_iters=2, omega=1.0, h0=pool, cu_seqlens=csd,
+                         block_table=bt[:2])
