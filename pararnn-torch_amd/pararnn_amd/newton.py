@@ -163,7 +163,7 @@ def fused_newton(
         if fused_time_loop:
             raise TypeError("fused_time_loop is ParaSLSTM only")
         if block_table is not None:
-            raise TypeError("block_table fused Newton is mix='diag' ParaGRU only")
+            raise TypeError("block_table fused Newton supports ParaSLSTM mix='diag' only")
         a_z, a_r, a_n = cell.clipped_a_head()
         return ops.newton_gru_head_fused(
             wx, a_z, a_r, a_n, h0, cu_seqlens, max_iters=max_iters, omega=omega
