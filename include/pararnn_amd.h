@@ -173,6 +173,22 @@ PRNN_API int prnn_slstm_backward_ex(const void* wx, const void* r, const void* h
                                     float eps, int dtype, void* workspace,
                                     size_t workspace_bytes, int tag_base, void* stream);
 
+/* Allocation-free variant of prnn_slstm_newton.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * workspace is a library-owned device array of
+ * prnn_slstm_newton_noalloc_max_bytes() bytes (64 MiB) per GPU, held until the
+ * process ends; shapes whose prnn_slstm_newton_workspace_size exceeds it are
+ * rejected with PRNN_ERR_VALUE.  The call allocates nothing and clears what
+ * it reads of the array first (a fill kernel on `stream`).  All calls on one
+ * GPU share that GPU's array: calls that overlap in time on one GPU (two
+ * streams, two host threads) race and give wrong results. */
+PRNN_API size_t prnn_slstm_newton_noalloc_max_bytes(void);
+PRNN_API int prnn_slstm_newton_noalloc(const void* wx, const void* r, const void* h0,
+                                       const void* states, void* out, int B, int T, int d,
+                                       int max_iters, float omega, float eps, int dtype,
+                                       void* stream);
+
 /* Eq. 2.6 backward of the head GRU at `states` = H* (B, T, d) with upstream
  * gradient `grad` = dL/dH (B, T, d) (both in `dtype`):
  *   mu_{T-1} = grad_{T-1},  mu_t = grad_t + J_{t+1}^T mu_{t+1}  (fp32),

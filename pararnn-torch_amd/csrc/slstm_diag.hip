@@ -31,6 +31,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <mutex>
 #include <type_traits>
 
 namespace prnn {
@@ -1521,4 +1522,70 @@ extern "C" PRNN_API int prnn_slstm_newton(const void* wx, const void* r, const v
                                           void* workspace, size_t workspace_bytes, void* stream) {
   return prnn_slstm_newton_ex(wx, r, h0, states, out, B, T, d, max_iters, omega, eps, dtype,
                               workspace, workspace_bytes, 0, stream);
+}
+
+// ---- allocation-free Newton entry point ------------------------------------
+// For callers that cannot allocate device memory (code under HIP graph
+// capture, serving loops, harnesses that forbid hipMalloc): the workspace is a
+// file-scope device array instead of a caller buffer.  Each GPU holds its own
+// copy for the life of the process.  Host code never passes the array's name
+// to a kernel (on the host that name is only a stand-in): the device address
+// of each GPU's copy is looked up once per device with hipGetSymbolAddress
+// and used from then on.
+namespace {
+
+constexpr size_t kScratchBytes = size_t(64) << 20;  // 64 MiB per GPU
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_current_device(void** out) {
+  int dev = 0;
+  PRNN_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(PRNN_ERR_RUNTIME, "device %d is beyond the %d devices supported", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(PRNN_ERR_RUNTIME, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PRNN_OK;
+}
+
+}  // namespace
+
+extern "C" PRNN_API size_t prnn_slstm_newton_noalloc_max_bytes(void) { return kScratchBytes; }
+
+extern "C" PRNN_API int prnn_slstm_newton_noalloc(const void* wx, const void* r, const void* h0,
+                                                  const void* states, void* out, int B, int T,
+                                                  int d, int max_iters, float omega, float eps,
+                                                  int dtype, void* stream) {
+  int rc = slstm::check_dims(B, T, d, dtype);
+  if (rc != PRNN_OK) return rc;
+  if (max_iters < 0 || max_iters > slstm::kMaxStages - 1)
+    return fail(PRNN_ERR_VALUE, "max_iters must be in [0, %d], got %d", slstm::kMaxStages - 1,
+                max_iters);
+  const size_t need = prnn_slstm_newton_workspace_size(B, T, d, max_iters, dtype);
+  if (need > kScratchBytes)
+    return fail(PRNN_ERR_VALUE,
+                "prnn_slstm_newton_noalloc: B=%d T=%d d=%d K=%d needs %zu bytes of scratch, "
+                "above the %zu-byte maximum (use prnn_slstm_newton with a workspace)",
+                B, T, d, max_iters, need, kScratchBytes);
+  void* ws = nullptr;
+  rc = scratch_for_current_device(&ws);
+  if (rc != PRNN_OK) return rc;
+  // tag_base 0: every look-back word the call reads is cleared first by a
+  // fill kernel on `stream`, so whatever an earlier call left in the array
+  // does not matter.
+  return prnn_slstm_newton_ex(wx, r, h0, states, out, B, T, d, max_iters, omega, eps, dtype, ws,
+                              kScratchBytes, 0, stream);
 }
