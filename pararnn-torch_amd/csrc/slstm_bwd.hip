@@ -30,11 +30,14 @@ namespace slstm {
 
 // v <- J^T v
 __device__ __forceinline__ void jtmv(const CellJ& J, float v[4]) {
-  const float c = v[0], n = v[1], m = v[2], h = v[3];
-  v[0] = J.f * c + J.hc * h;
-  v[1] = J.f * n + J.hn * h;
-  v[2] = J.cm * c + J.nm * n + J.al * m + J.hm * h;
-  v[3] = J.ch * c + J.nh * n + J.mh * m + J.hh * h;
+  // with the factorised h row, J^T v = J_cn^T w + (0, 0, al m, mh m + g h)
+  // where w = (c + inv h, n + dn h) feeds the c and n rows
+  const float m = v[2], h = v[3];
+  const float wc = v[0] + J.inv * h, wn = v[1] + J.dn * h;
+  v[0] = J.f * wc;
+  v[1] = J.f * wn;
+  v[2] = J.cm * wc + J.nm * wn + J.al * m;
+  v[3] = J.ch * wc + J.nh * wn + J.mh * m + J.g * h;
 }
 
 // VJP of one step f(prev, x) with adjoint mu: the four pre-activation
@@ -54,7 +57,7 @@ __device__ __forceinline__ void cell_vjp(const float prev[4], const float x[4], 
   const bool lf = left >= zi;
   const float f = lf ? 1.f : e;
   const float i = lf ? e : 1.f;
-  const float z = ftanh(zz);
+  const float z = ftanh5(zz);
   const float nn = f * n + i;
   const float cn = f * c + i * z;
   const float o = fsigmoid(zo);

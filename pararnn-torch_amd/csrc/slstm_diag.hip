@@ -638,11 +638,8 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
       XS::get(xs[s], x);
       HS::get(hs[s], hv);
       const CellJ J = cell_jac(prev, x, r, eps);
-      jmv(J, a.b);
-      a.b[0] += J.pc - hv[0];
-      a.b[1] += J.pn - hv[1];
-      a.b[2] += J.pm - hv[2];
-      a.b[3] += J.ph - hv[3];
+      const float F[4] = {J.pc - hv[0], J.pn - hv[1], J.pm - hv[2], J.ph - hv[3]};
+      jmv_affine(J, F, a.b);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float col[4] = {a.A[0][j], a.A[1][j], a.A[2][j], a.A[3][j]};
@@ -904,11 +901,9 @@ slstm_newton_fused_kernel(
         float x[4];
         XS::get(xs[s], x);
         const CellJ J = cell_jac(prev, x, r, eps);
-        jmv(J, a.b);
-        a.b[0] += J.pc - hf[s][0];
-        a.b[1] += J.pn - hf[s][1];
-        a.b[2] += J.pm - hf[s][2];
-        a.b[3] += J.ph - hf[s][3];
+        const float F[4] = {J.pc - hf[s][0], J.pn - hf[s][1], J.pm - hf[s][2],
+                            J.ph - hf[s][3]};
+        jmv_affine(J, F, a.b);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           float col[4] = {a.A[0][j], a.A[1][j], a.A[2][j], a.A[3][j]};

@@ -221,12 +221,17 @@ __device__ __forceinline__ void windowed_lookback(const TileId& id, int B, int n
   }
 }
 
-// Cell value and the 12 structural non-zeros of the per-channel Jacobian
-// [out, in] over slots (c, n, m, h):
-//   c: [f, 0, cm, ch]   n: [0, f, nm, nh]   m: [0, 0, al, mh]   h: [hc, hn, hm, hh]
+// Cell value and the per-channel Jacobian [out, in] over slots (c, n, m, h):
+//   c: [f, 0, cm, ch]   n: [0, f, nm, nh]   m: [0, 0, al, mh]
+//   h: inv * (c row) + dn * (n row) + [0, 0, 0, g]
+// The h row is kept factorised: h' = o c' / (n' + eps), so its derivative is
+// inv = o / den times that of c', plus dn = -o c' / den^2 times that of n',
+// plus g = (c' / den) do/dh through the output gate.  Applied to a vector
+// that costs 3 operations for the h row instead of 4, and the four dense h
+// entries are never formed.
 struct CellJ {
   float pc, pn, pm, ph;
-  float f, cm, ch, nm, nh, al, mh, hc, hn, hm, hh;
+  float f, cm, ch, nm, nh, al, mh, inv, dn, g;
 };
 
 __device__ __forceinline__ CellJ cell_jac(const float prev[4], const float x[4], const float r[4],
@@ -244,7 +249,7 @@ __device__ __forceinline__ CellJ cell_jac(const float prev[4], const float x[4],
   const bool lf = left >= zi;
   const float f = lf ? 1.f : e;
   const float i = lf ? e : 1.f;
-  const float z = ftanh(zz);
+  const float z = ftanh5(zz);
   const float nn = f * n + i;
   const float cn = f * c + i * z;
   const float o = fsigmoid(zo);
@@ -254,28 +259,24 @@ __device__ __forceinline__ CellJ cell_jac(const float prev[4], const float x[4],
   J.pn = nn;
   J.pm = mn;
   J.ph = o * (cn * inv_den);
-  const float be = 1.f - al;
-  const float dm_dh = al * r[1] + be * r[0];
-  const float di_dm = -i * al;
-  const float df_dm = f * be;
-  const float di_dh = i * (r[0] - dm_dh);
-  const float df_dh = f * (r[1] - dm_dh);
-  const float dz_dh = (1.f - z * z) * r[2];
+  // With d = r_f - r_i and the gate split a1 = f (1 - al), a2 = i al (al =
+  // d m'/d left), the m- and h-derivatives of the c and n rows share their
+  // factors: cm = a1 c - a2 z, nm = a1 n - a2, ch = d cm + i (1 - z^2) r_z,
+  // nh = d nm, and mh = r_i + al d.
+  const float a1 = f * (1.f - al);
+  const float a2 = i * al;
+  const float dr = r[1] - r[0];
   const float do_dh = o * (1.f - o) * r[3];
   J.f = f;
-  J.cm = df_dm * c + di_dm * z;
-  J.ch = df_dh * c + di_dh * z + i * dz_dh;
-  J.nm = df_dm * n + di_dm;
-  J.nh = df_dh * n + di_dh;
   J.al = al;
-  J.mh = dm_dh;
-  const float inv = o * inv_den;
-  const float dn = -o * cn * inv_den * inv_den;
-  const float du = cn * inv_den;
-  J.hc = inv * f;
-  J.hn = dn * f;
-  J.hm = inv * J.cm + dn * J.nm;
-  J.hh = inv * J.ch + dn * J.nh + du * do_dh;
+  J.cm = a1 * c - a2 * z;
+  J.nm = a1 * n - a2;
+  J.ch = dr * J.cm + i * ((1.f - z * z) * r[2]);
+  J.nh = dr * J.nm;
+  J.mh = r[0] + al * dr;
+  J.inv = o * inv_den;
+  J.dn = -J.inv * (cn * inv_den);
+  J.g = (cn * inv_den) * do_dh;
   return J;
 }
 
@@ -296,7 +297,7 @@ __device__ __forceinline__ void cell_jvp(const float prev[4], const float x[4], 
   const bool lf = left >= zi;
   const float f = lf ? 1.f : e;
   const float i = lf ? e : 1.f;
-  const float z = ftanh(zz);
+  const float z = ftanh5(zz);
   const float nn = f * n + i;
   const float cn = f * c + i * z;
   const float o = fsigmoid(zo);
@@ -306,14 +307,15 @@ __device__ __forceinline__ void cell_jvp(const float prev[4], const float x[4], 
   p[1] = nn;
   p[2] = mn;
   p[3] = o * u;
-  // tangents: z_g' = r_g h', left' = z_f' + m', m_new' = al left' + (1 - al) z_i'
-  const float dzi = r[0] * v[3];
-  const float dleft = r[1] * v[3] + v[2];
-  const float dmn = dzi + al * (dleft - dzi);
-  const float di = i * (dzi - dmn);
-  const float df = f * (dleft - dmn);
-  const float dnn = df * n + f * v[1] + di;
-  const float dcn = df * c + f * v[0] + di * z + i * (1.f - z * z) * (r[2] * v[3]);
+  // tangents: z_g' = r_g h', left' = z_f' + m', m_new' = al left' + (1 - al) z_i';
+  // with q = left' - z_i' = m' + (r_f - r_i) h', the gate tangents are
+  // f' = f (1 - al) q and i' = -i al q.
+  const float q = v[2] + (r[1] - r[0]) * v[3];
+  const float dmn = r[0] * v[3] + al * q;
+  const float a1 = f * (1.f - al);
+  const float a2 = i * al;
+  const float dnn = f * v[1] + q * (a1 * n - a2);
+  const float dcn = f * v[0] + q * (a1 * c - a2 * z) + i * (1.f - z * z) * (r[2] * v[3]);
   const float dso = o * (1.f - o) * (r[3] * v[3]);
   jv[0] = dcn;
   jv[1] = dnn;
@@ -321,13 +323,24 @@ __device__ __forceinline__ void cell_jvp(const float prev[4], const float x[4], 
   jv[3] = dso * u + o * inv_den * (dcn - u * dnn);
 }
 
-// v <- J v (+ add)
+// v <- J v
 __device__ __forceinline__ void jmv(const CellJ& J, float v[4]) {
   const float c = v[0], n = v[1], m = v[2], h = v[3];
   v[0] = J.f * c + J.cm * m + J.ch * h;
   v[1] = J.f * n + J.nm * m + J.nh * h;
   v[2] = J.al * m + J.mh * h;
-  v[3] = J.hc * c + J.hn * n + J.hm * m + J.hh * h;
+  v[3] = J.inv * v[0] + J.dn * v[1] + J.g * h;
+}
+
+// v <- J v + F: the affine step of the Newton scan.
+__device__ __forceinline__ void jmv_affine(const CellJ& J, const float F[4], float v[4]) {
+  const float c = v[0], n = v[1], m = v[2], h = v[3];
+  const float tc = J.f * c + J.cm * m + J.ch * h;
+  const float tn = J.f * n + J.nm * m + J.nh * h;
+  v[0] = tc + F[0];
+  v[1] = tn + F[1];
+  v[2] = J.al * m + J.mh * h + F[2];
+  v[3] = J.inv * tc + J.dn * tn + J.g * h + F[3];
 }
 
 // 4x4 affine element (A, b): x -> A x + b
