@@ -20,6 +20,7 @@ from torch import Tensor, nn
 
 from pararnn_amd import _lib
 from pararnn_amd.cells import ParaGRU, ParaSLSTM
+from pararnn_amd.head_blocks import HeadBlocks
 from pararnn_amd.ops import _ptr, _stream, _validate
 
 
@@ -30,8 +31,16 @@ def can_decode_step(cell: nn.Module, ref: Tensor) -> bool:
     if isinstance(cell, ParaSLSTM):
         return cell.mix == "diag"
     if isinstance(cell, ParaGRU):
-        return cell.mix == "diag" or (cell.mix == "head" and cell.d_head == 64)
+        return cell.mix == "diag" or (cell.mix == "head" and _head_blocks_in_place(cell))
     return False
+
+
+def _head_blocks_in_place(cell: ParaGRU) -> bool:
+    """Heads that tile 64-channel blocks exactly (d_head = 64, or a divisor of
+    64 with whole blocks of heads): the kernel then reads and writes the state
+    in place, merged heads being block-diagonal 64 x 64 matrices."""
+    d_head = int(cell.d_head)
+    return d_head <= 64 and 64 % d_head == 0 and int(cell.n_heads) % (64 // d_head) == 0
 
 
 def _squeeze_time(t: Tensor, name: str) -> Tensor:
@@ -142,8 +151,9 @@ def decode_step(cell: nn.Module, state: Tensor, x: Tensor | None = None, *,
         a = (cell.a_z, cell.a_r, cell.a_n)
         heads = 0
     else:
-        a = (cell.A_z, cell.A_r, cell.A_n)
-        heads = int(cell.n_heads)
+        hb = HeadBlocks(int(cell.n_heads), int(cell.d_head), state.device)
+        a = tuple(hb.matrices(t) for t in (cell.A_z, cell.A_r, cell.A_n))
+        heads = hb.n_blocks
     if wx.shape[-1] != 3 * d:
         raise ValueError(f"ParaGRU wx last dim {wx.shape[-1]} != 3 * d_h={3 * d}")
     code = _validate("decode_gru", state, wx, *a, out)

@@ -83,14 +83,14 @@ def _fusable(cell: nn.Module, x: Tensor) -> bool:
     if isinstance(cell, ParaSLSTM):
         return cell.mix == "diag"
     if isinstance(cell, ParaGRU):
-        return cell.mix == "head" and cell.d_head == 64
+        return cell.mix == "head" and cell.d_head <= 64
     return False
 
 
 def _fused_error(cell: nn.Module, x: Tensor) -> str:
     return (
         "scan_backend='fused' in pararnn_amd needs ParaSLSTM(mix='diag') or "
-        "ParaGRU(mix='head', d_head=64) on a ROCm GPU in float32/bfloat16 "
+        "ParaGRU(mix='head', d_head <= 64) on a ROCm GPU in float32/bfloat16 "
         f"(got {type(cell).__name__}(mix={getattr(cell, 'mix', None)!r}) "
         f"{x.dtype} on {x.device})"
     )

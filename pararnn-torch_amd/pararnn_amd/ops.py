@@ -22,6 +22,7 @@ import torch
 from torch import Tensor
 
 from pararnn_amd import _lib
+from pararnn_amd.head_blocks import HeadBlocks
 
 _DTYPES = {torch.float32: _lib.PRNN_F32, torch.bfloat16: _lib.PRNN_BF16}
 
@@ -312,8 +313,8 @@ def newton_gru_head_fused(
     d_h = n_heads * d_head
     if wx.dim() != 3 or wx.shape[-1] != 3 * d_h:
         raise ValueError(f"wx last dim {wx.shape[-1]} != 3 * d_h={3 * d_h}")
-    if d_head != 64:
-        raise TypeError(f"newton_gru_head_fused: pararnn_amd provides d_head=64, got {d_head}")
+    if d_head > 64:
+        raise TypeError(f"newton_gru_head_fused: pararnn_amd provides d_head <= 64, got {d_head}")
     if cu_seqlens is not None:
         # Packed sequences run as a padded batch, each from its own h0.
         from pararnn_amd.ragged import RaggedPlan, validate_cu_seqlens
@@ -332,30 +333,30 @@ def newton_gru_head_fused(
 def _gru_head_dense(wx, a_z, a_r, a_n, h0, max_iters, omega):
     n_heads, d_head, _ = a_z.shape
     d_h = n_heads * d_head
-    if d_head != 64:
-        raise TypeError(f"newton_gru_head_fused: pararnn_amd provides d_head=64, got {d_head}")
     batch, time, _ = wx.shape
     code = _validate("newton_gru_head_fused", wx, a_z, a_r, a_n, h0)
     if h0 is not None and h0.shape != (batch, d_h):
         raise ValueError(f"h0 shape {tuple(h0.shape)} != {(batch, d_h)}")
     if max_iters < 0:
         raise ValueError(f"max_iters must be >= 0, got {max_iters!r}")
-    wx = wx.contiguous()
-    a_z, a_r, a_n = a_z.contiguous(), a_r.contiguous(), a_n.contiguous()
-    h0 = None if h0 is None else h0.contiguous()
-    out = wx.new_empty(batch, time, d_h)
+    # heads narrower than 64 run as block-diagonal 64 x 64 blocks
+    hb = HeadBlocks(n_heads, d_head, wx.device)
+    wx = hb.to_blocks(wx, 3).contiguous()
+    a_z, a_r, a_n = (hb.matrices(a) for a in (a_z, a_r, a_n))
+    h0 = None if h0 is None else hb.to_blocks(h0).contiguous()
+    out = wx.new_empty(batch, time, hb.d_pad)
     lib = _lib.load()
     with torch.cuda.device(wx.device):
-        nbytes = lib.prnn_gru_head_newton_workspace_size(batch, time, n_heads, d_head,
+        nbytes = lib.prnn_gru_head_newton_workspace_size(batch, time, hb.n_blocks, 64,
                                                          int(max_iters), code)
         ws = _workspace(nbytes, wx.device)
         rc = lib.prnn_gru_head_newton(
             _ptr(wx), _ptr(a_z), _ptr(a_r), _ptr(a_n), _ptr(h0), _ptr(out), batch, time,
-            n_heads, d_head, int(max_iters), float(omega), code, _ptr(ws), ws.numel(),
+            hb.n_blocks, 64, int(max_iters), float(omega), code, _ptr(ws), ws.numel(),
             _stream(wx.device),
         )
     _lib.check(rc, "newton_gru_head_fused")
-    return out
+    return hb.from_blocks(out)
 
 
 @newton_gru_head_fused.register_fake
@@ -372,7 +373,7 @@ def gru_head_backward_fused(
     """Eq. 2.6 backward of ``ParaGRU(mix='head')`` at ``H* = states`` on the GPU.
 
     Returns ``(g_wx, g_a, g_h0)``: ``dL/dwx`` ``(B, T, 3 d_h)`` in ``wx``'s
-    dtype, ``g_a`` ``(3, H, 64, 64)`` fp32 (``dL/dA_z, dL/dA_r, dL/dA_n`` before
+    dtype, ``g_a`` ``(3, H, d_head, d_head)`` fp32 (``dL/dA_z, dL/dA_r, dL/dA_n`` before
     clamp masks) and ``g_h0 = J_0^T mu_0`` ``(B, d_h)`` fp32 (zeros when ``h0`` is
     None).  The reference computes these with ``reverse_factor_scan_gru_head``,
     ``gru_head_t0_vjp`` and ``gru_head_recurrence_vjp``
@@ -383,8 +384,8 @@ def gru_head_backward_fused(
     n_heads, d_head, _ = a_z.shape
     if a_r.shape != a_z.shape or a_n.shape != a_z.shape:
         raise ValueError("a_z, a_r, a_n shape mismatch")
-    if d_head != 64:
-        raise TypeError(f"gru_head_backward_fused: pararnn_amd provides d_head=64, got {d_head}")
+    if d_head > 64:
+        raise TypeError(f"gru_head_backward_fused: pararnn_amd provides d_head <= 64, got {d_head}")
     d_h = n_heads * d_head
     if wx.dim() != 3 or wx.shape[-1] != 3 * d_h:
         raise ValueError(f"wx last dim {wx.shape[-1]} != 3 * d_h={3 * d_h}")
@@ -395,23 +396,27 @@ def gru_head_backward_fused(
             raise ValueError(f"{name} shape {tuple(t.shape)} != {(batch, time, d_h)}")
     if h0 is not None and h0.shape != (batch, d_h):
         raise ValueError(f"h0 shape {tuple(h0.shape)} != {(batch, d_h)}")
-    wx, states, grad = wx.contiguous(), states.contiguous(), grad.contiguous()
-    a_z, a_r, a_n = a_z.contiguous(), a_r.contiguous(), a_n.contiguous()
-    h0 = None if h0 is None else h0.contiguous()
+    # heads narrower than 64 run as block-diagonal 64 x 64 blocks
+    hb = HeadBlocks(n_heads, d_head, wx.device)
+    wx = hb.to_blocks(wx, 3).contiguous()
+    states = hb.to_blocks(states).contiguous()
+    grad = hb.to_blocks(grad).contiguous()
+    a_z, a_r, a_n = (hb.matrices(a) for a in (a_z, a_r, a_n))
+    h0 = None if h0 is None else hb.to_blocks(h0).contiguous()
     g_wx = torch.empty_like(wx)
-    g_a = torch.empty(3, n_heads, d_head, d_head, dtype=torch.float32, device=wx.device)
-    g_h0 = torch.zeros(batch, d_h, dtype=torch.float32, device=wx.device)
+    g_a = torch.empty(3, hb.n_blocks, 64, 64, dtype=torch.float32, device=wx.device)
+    g_h0 = torch.zeros(batch, hb.d_pad, dtype=torch.float32, device=wx.device)
     lib = _lib.load()
     with torch.cuda.device(wx.device):
-        nbytes = lib.prnn_gru_head_backward_workspace_size(batch, time, n_heads, d_head, code)
+        nbytes = lib.prnn_gru_head_backward_workspace_size(batch, time, hb.n_blocks, 64, code)
         ws = _workspace(nbytes, wx.device)
         rc = lib.prnn_gru_head_backward(
             _ptr(wx), _ptr(a_z), _ptr(a_r), _ptr(a_n), _ptr(h0), _ptr(states), _ptr(grad),
-            _ptr(g_wx), _ptr(g_a), _ptr(g_h0), batch, time, n_heads, d_head, code, _ptr(ws),
+            _ptr(g_wx), _ptr(g_a), _ptr(g_h0), batch, time, hb.n_blocks, 64, code, _ptr(ws),
             ws.numel(), _stream(wx.device),
         )
     _lib.check(rc, "gru_head_backward_fused")
-    return g_wx, g_a, g_h0
+    return hb.from_blocks(g_wx, 3), hb.head_grads(g_a), hb.from_blocks(g_h0)
 
 
 @gru_head_backward_fused.register_fake
