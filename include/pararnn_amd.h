@@ -74,6 +74,18 @@ PRNN_API const char* prnn_last_error(void);
 PRNN_API void prnn_set_deterministic(int on);
 PRNN_API int prnn_deterministic(void);
 
+/* Bounded waits (no counterpart in the reference).  The sLSTM scans wait on
+ * words their predecessor tiles publish; publication order guarantees that
+ * they arrive, so a wait that polls more than `rounds` times (process-wide;
+ * <= 0 restores the default, 4194304, seconds of polling) means a broken
+ * invariant such as a foreign or stale workspace.  The waiting wave then
+ * gives up: it takes NaN for the missing value (so the output shows it),
+ * sets the call's status word and runs on, so every kernel still ends.
+ * prnn_slstm_lookback_status copies that word (1 = a wait gave up, 0 = none)
+ * from an sLSTM call's workspace to *status, synchronising `stream`. */
+PRNN_API void prnn_set_spin_limit(int rounds);
+PRNN_API int prnn_slstm_lookback_status(const void* workspace, int* status, void* stream);
+
 /* Kernel timing, process-wide (off by default; no counterpart in the
  * reference, for benchmarks).  When on, the sLSTM entry points record a HIP
  * event pair on their stream around their main kernel(s) -- after the status

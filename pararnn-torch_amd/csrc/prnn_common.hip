@@ -25,6 +25,12 @@ std::atomic<int> g_deterministic{0};
 int deterministic() { return g_deterministic.load(std::memory_order_relaxed); }
 
 namespace {
+std::atomic<int> g_spin_limit{kSpinLimitDefault};
+}
+
+int spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
+
+namespace {
 std::atomic<int> g_timing{0};
 std::mutex g_timing_mu;
 hipEvent_t g_ev[2] = {nullptr, nullptr};
@@ -68,6 +74,11 @@ extern "C" PRNN_API void prnn_set_deterministic(int on) {
 }
 
 extern "C" PRNN_API int prnn_deterministic(void) { return prnn::deterministic(); }
+
+extern "C" PRNN_API void prnn_set_spin_limit(int rounds) {
+  prnn::g_spin_limit.store(rounds > 0 ? rounds : prnn::kSpinLimitDefault,
+                           std::memory_order_relaxed);
+}
 
 extern "C" PRNN_API void prnn_set_kernel_timing(int on) {
   prnn::g_timing.store(on ? 1 : 0, std::memory_order_relaxed);

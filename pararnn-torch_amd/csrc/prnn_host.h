@@ -49,6 +49,11 @@ struct Carver {
 // Process-wide deterministic look-back switch (prnn_set_deterministic).
 int deterministic();
 
+// Polling rounds a look-back or hand-off wait may spend before it gives up
+// (prnn_set_spin_limit; default kSpinLimitDefault).
+constexpr int kSpinLimitDefault = 1 << 22;
+int spin_limit();
+
 // Optional timing of an entry point's main kernel(s) (prnn_set_kernel_timing):
 // when on, HIP events are recorded on the caller's stream right before and
 // right after them; prnn_last_kernel_ms reads the last pair.

@@ -88,7 +88,7 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
     const TX* __restrict__ states, const TX* __restrict__ grad, TX* __restrict__ gwx,
     float* __restrict__ gr_part, float* __restrict__ gh0, int B, int T, int d, int n_cb,
     int n_chunks, float eps, int* __restrict__ counter, unsigned long long* __restrict__ agg,
-    unsigned long long* __restrict__ incl, int epoch) {
+    unsigned long long* __restrict__ incl, int epoch, Spin spin) {
   // predecessors per wave per look-back round (the deterministic walk, which
   // must find an inclusive carry inside its window, looks twice as far)
   constexpr int KP = DET ? 2 : 1;
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
   }
   if (id.chunk > 0)
     windowed_lookback<NewtonMonoid, W, KP, DET>(
-          id, B, n_cb, epoch, incl, agg, lane, wave, s_lb, carry);
+          id, B, n_cb, epoch, incl, agg, lane, wave, s_lb, carry, spin);
   if (wave == 0) {
     // Per-wave carries; the outgoing carry is the published aggregate applied
     // to the carry in, as a successor's walk would compute it.
@@ -394,7 +394,7 @@ static void launch_reverse(const TX* wx, const TX* r, const TX* h0, const TX* st
   const Geo g = geometry(B, T, d, Shape{L, W});
   slstm_reverse_kernel<TX, L, W, DET><<<dim3(g.n_tiles), dim3(64 * W), 0, stream>>>(
       wx, r, h0, states, grad, gwx, w.gr_part, gh0, B, T, d, g.n_cb, g.n_chunks, eps,
-      w.lb.counters + 1, w.lb.agg, w.lb.incl, w.lb.tag_base + 1);
+      w.lb.counters + 1, w.lb.agg, w.lb.incl, w.lb.tag_base + 1, w.lb.spin());
 }
 
 template <typename TX>

@@ -165,7 +165,7 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
     const TX* __restrict__ hsrc, TX* __restrict__ out_full, TX* __restrict__ out_h, int B, int T,
     int d, int n_cb, float eps, int* __restrict__ counter, unsigned long long* __restrict__ agg,
-    unsigned long long* __restrict__ incl, int epoch) {
+    unsigned long long* __restrict__ incl, int epoch, Spin spin) {
   constexpr int KP = 2;  // predecessors per wave per look-back round
   using Stash = PreStash<TX>;
   constexpr uint32_t SZ = sizeof(TX);
@@ -260,7 +260,7 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
   }
   if (id.chunk > 0)
     windowed_lookback<FrozenMonoid, W, KP, DET>(
-          id, B, n_cb, epoch, incl, agg, lane, wave, s_lb, carry);
+          id, B, n_cb, epoch, incl, agg, lane, wave, s_lb, carry, spin);
   if (wave == 0) {
     // Per-wave carries, then the tile's inclusive carry: the published
     // aggregate applied to the carry in (what a successor's walk computes).
@@ -337,7 +337,8 @@ slstm_picard_fused_kernel(
     const bf16* __restrict__ wx, const bf16* __restrict__ rmix, const bf16* __restrict__ h0,
     bf16* __restrict__ out, int B, int T, int d, int n_cb, int n_tiles, int P, float eps,
     int* __restrict__ counter, unsigned long long* __restrict__ agg,
-    unsigned long long* __restrict__ incl, unsigned long long* __restrict__ hlast, int tag_base) {
+    unsigned long long* __restrict__ incl, unsigned long long* __restrict__ hlast, int tag_base,
+    Spin spin) {
   static_assert(L % 2 == 0, "h is packed two steps to a register");
   constexpr int KP = 2;
   constexpr uint32_t SZ = 2;
@@ -421,14 +422,22 @@ slstm_picard_fused_kernel(
         const unsigned long long* hw =
             hlast + (p - 1) * stage_h + (static_cast<size_t>(tile) - B * n_cb) * kCB + lane;
         int spins = 0;
+        bool gave_up = false;
         while (true) {
           const bool ok = ld_tagged(hw, tag - 1, hp0);
           if (__ballot(!ok) == 0ull) break;
-          if (++spins > 8)
+          if (++spins > 8) {
+            if (spins > spin.limit) {  // give up (see Spin)
+              spin_give_up(spin);
+              gave_up = true;
+              break;
+            }
             __builtin_amdgcn_s_sleep(8);
-          else
+          } else {
             __builtin_amdgcn_s_sleep(1);
+          }
         }
+        if (gave_up) hp0 = __builtin_nanf("");
       }
     }
 
@@ -499,7 +508,7 @@ slstm_picard_fused_kernel(
     }
     if (id.chunk > 0)
       windowed_lookback<FrozenMonoid, W, KP, DET>(
-          id, B, n_cb, tag, incl_p, agg_p, lane, wave, s_lb, carry);
+          id, B, n_cb, tag, incl_p, agg_p, lane, wave, s_lb, carry, spin);
     if (wave == 0) {
       float m = carry[0], n = carry[1], c = carry[2];
 #pragma unroll
@@ -579,7 +588,7 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
     const TIN* __restrict__ hin, TOUT* __restrict__ hout, int B, int T, int d, int n_cb,
     float omega, float eps, int* __restrict__ counter, unsigned long long* __restrict__ agg,
-    unsigned long long* __restrict__ incl, int epoch) {
+    unsigned long long* __restrict__ incl, int epoch, Spin spin) {
   // predecessors per wave per look-back round (the deterministic walk, which
   // must find an inclusive carry inside its window, looks twice as far)
   constexpr int KP = DET ? 2 : 1;
@@ -696,7 +705,7 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
   }
   if (id.chunk > 0)
     windowed_lookback<NewtonMonoid, W, KP, DET>(
-          id, B, n_cb, epoch, incl, agg, lane, wave, s_lb, carry);
+          id, B, n_cb, epoch, incl, agg, lane, wave, s_lb, carry, spin);
   if (wave == 0) {
     // Carry into each wave's segment, then the tile's outgoing carry (the
     // published aggregate applied to the carry in, as a successor's walk
@@ -783,7 +792,7 @@ slstm_newton_fused_kernel(
     const TX* __restrict__ guess, TX* __restrict__ out, int B, int T, int d, int n_cb,
     int n_tiles, int K, float omega, float eps, int* __restrict__ counter,
     unsigned long long* __restrict__ agg, unsigned long long* __restrict__ incl,
-    unsigned long long* __restrict__ hlast, int tag_base) {
+    unsigned long long* __restrict__ hlast, int tag_base, Spin spin) {
   // predecessors per wave per look-back round (the deterministic walk, which
   // must find an inclusive carry inside its window, looks twice as far)
   constexpr int KP = DET ? 2 : 1;
@@ -880,15 +889,26 @@ slstm_newton_fused_kernel(
       const unsigned long long* hw =
           hlast + (k - 1) * stage_h + (static_cast<size_t>(tile) - B * n_cb) * 4 * kCB + lane;
       int spins = 0;
+      bool gave_up = false;
       while (true) {
         bool ok = true;
 #pragma unroll
         for (int j = 0; j < 4; ++j) ok = ld_tagged(hw + j * kCB, tag - 1, prev0[j]) && ok;
         if (__ballot(!ok) == 0ull) break;
-        if (++spins > 8)
+        if (++spins > 8) {
+          if (spins > spin.limit) {  // give up (see Spin)
+            spin_give_up(spin);
+            gave_up = true;
+            break;
+          }
           __builtin_amdgcn_s_sleep(8);
-        else
+        } else {
           __builtin_amdgcn_s_sleep(1);
+        }
+      }
+      if (gave_up) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) prev0[j] = __builtin_nanf("");
       }
     }
 
@@ -967,7 +987,7 @@ slstm_newton_fused_kernel(
     }
     if (id.chunk > 0)
       windowed_lookback<NewtonMonoid, W, KP, DET>(
-          id, B, n_cb, tag, incl_k, agg_k, lane, wave, s_lb, carry);
+          id, B, n_cb, tag, incl_k, agg_k, lane, wave, s_lb, carry, spin);
     if (wave == 0) {
       // Per-wave carries; the outgoing carry is the published aggregate
       // applied to the carry in, as a successor's walk would compute it.
@@ -1252,7 +1272,7 @@ static void launch_frozen(bool has_h, bool full_out, const TX* wx, const TX* r, 
 #define PRNN_FROZEN(HH, FO)                                                                    \
   slstm_frozen_kernel<TX, L, W, HH, FO, DET><<<grid, block, 0, stream>>>(                      \
       wx, r, h0, src, out_full, out_h, B, T, d, g.n_cb, eps, ctr, lb.agg, lb.incl,             \
-      lb.tag_base + epoch)
+      lb.tag_base + epoch, lb.spin())
   if (has_h) {
     if (full_out) PRNN_FROZEN(true, true); else PRNN_FROZEN(true, false);
   } else {
@@ -1297,7 +1317,7 @@ static int run_init(const TX* wx, const TX* r, const TX* h0, TX* states, int B, 
 #define PRNN_LAUNCH(LL, WW, WPE, DD)                                                            \
   slstm_picard_fused_kernel<LL, WW, WPE, DD><<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>(    \
       wx, r, h0, states, B, T, d, g.n_cb, g.n_tiles, P, eps, w.lb.counters + 1, w.lb.agg,       \
-      w.lb.incl, w.hlast, w.lb.tag_base)
+      w.lb.incl, w.hlast, w.lb.tag_base, w.lb.spin())
 #define PRNN_SHAPE(LL, WW, WPE) \
   else if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, WPE, false);
       static_assert(kPicardDefault.L == 24 && kPicardDefault.W == 4, "default Picard shape");
@@ -1335,7 +1355,7 @@ static void launch_newton_shape(const TX* wx, const TX* r, const TX* h0, const T
   const Geo g = geometry(B, T, d, Shape{L, W});
   slstm_newton_kernel<TX, TIN, TOUT, L, W, DET><<<dim3(g.n_tiles), dim3(64 * W), 0, stream>>>(
       wx, r, h0, hin, hout, B, T, d, g.n_cb, omega, eps, lb.counters + epoch, lb.agg,
-      lb.incl, lb.tag_base + epoch);
+      lb.incl, lb.tag_base + epoch, lb.spin());
 }
 
 template <typename TX, typename TIN, typename TOUT>
@@ -1370,20 +1390,20 @@ template <typename TX>
 static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, TX* out, int B,
                       int T, int d, int K, float omega, float eps, const NewtonWs& w,
                       hipStream_t stream) {
+  int rc = clear_status(w.lb, stream);
+  if (rc != PRNN_OK) return rc;
   if (K == 0) {
     PRNN_HIP(hipMemcpyAsync(out, guess, static_cast<size_t>(B) * T * 4 * d * sizeof(TX),
                             hipMemcpyDeviceToDevice, stream));
     return PRNN_OK;
   }
-  int rc = clear_status(w.lb, stream);
-  if (rc != PRNN_OK) return rc;
   if (w.fused) {
     const Shape sh = newton_fused_shape(sizeof(TX) == 2 ? PRNN_BF16 : PRNN_F32);
     const Geo g = geometry(B, T, d, sh);
 #define PRNN_LAUNCH(LL, WW, WPE, DD)                                                             \
   slstm_newton_fused_kernel<TX, LL, WW, WPE, DD><<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>( \
       wx, r, h0, guess, out, B, T, d, g.n_cb, g.n_tiles, K, omega, eps, w.lb.counters + 1,       \
-      w.lb.agg, w.lb.incl, w.hlast, w.lb.tag_base)
+      w.lb.agg, w.lb.incl, w.hlast, w.lb.tag_base, w.lb.spin())
 #define PRNN_SHAPE(LL, WW, WPE) \
   else if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, WPE, false);
     static_assert(kNewtonFusedF32.L == 16 && kNewtonFusedF32.W == 4, "fp32 fused shape");
@@ -1517,6 +1537,17 @@ extern "C" PRNN_API int prnn_slstm_newton(const void* wx, const void* r, const v
                                           void* workspace, size_t workspace_bytes, void* stream) {
   return prnn_slstm_newton_ex(wx, r, h0, states, out, B, T, d, max_iters, omega, eps, dtype,
                               workspace, workspace_bytes, 0, stream);
+}
+
+extern "C" PRNN_API int prnn_slstm_lookback_status(const void* workspace, int* status,
+                                                   void* stream) {
+  if (!workspace || !status) return fail(PRNN_ERR_VALUE, "workspace and status must be non-null");
+  // The ticket counters lead every sLSTM workspace; the status word follows them.
+  const int* word = static_cast<const int*>(workspace) + slstm::kMaxStages;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  PRNN_HIP(hipMemcpyAsync(status, word, sizeof(int), hipMemcpyDeviceToHost, s));
+  PRNN_HIP(hipStreamSynchronize(s));
+  return PRNN_OK;
 }
 
 // ---- allocation-free Newton entry point ------------------------------------

@@ -74,6 +74,22 @@ __device__ __forceinline__ int take_ticket(int* counter) {
 // the window: a tile waits until one of its W * KP nearest predecessors holds
 // its inclusive carry.
 // ---------------------------------------------------------------------------
+// Bound on the waits of one launch: a wave that has polled `limit` rounds
+// without its predecessors' words arriving gives up -- it ORs 1 into *status
+// (a word of the call's workspace, read by prnn_slstm_lookback_status), takes
+// NaN for what it waited for, and carries on, so every wave still reaches the
+// end of the kernel and the output shows the failure.  Publication order
+// guarantees progress, so this only fires on a broken invariant (a stale or
+// foreign workspace, a tag mismatch) or an artificially small limit.
+struct Spin {
+  int* status;
+  int limit;
+};
+
+__device__ __forceinline__ void spin_give_up(const Spin& spin) {
+  __hip_atomic_fetch_or(spin.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <class M, int NW>
 struct LookbackShared {
   float pl[NW][M::NA][kCB];
@@ -89,13 +105,14 @@ __device__ __forceinline__ void windowed_lookback(const TileId& id, int B, int n
                                                   const unsigned long long* __restrict__ agg,
                                                   int lane, int wave,
                                                   LookbackShared<M, W * KP>& sh,
-                                                  float carry[M::NI]) {
+                                                  float carry[M::NI], const Spin& spin) {
   typename M::Acc acc;
   M::identity(acc);
   int pos = id.chunk - 1;  // wave 0: next predecessor chunk to examine
   bool done = false;
   const int per = B * n_cb;
   int idle_rounds = 0;
+  int rounds = 0;
   while (true) {
     if (wave == 0) sh.pos[lane] = done ? -1 : pos;
     __syncthreads();
@@ -203,6 +220,13 @@ __device__ __forceinline__ void windowed_lookback(const TileId& id, int B, int n
             }
           }
         }
+      }
+      if (++rounds > spin.limit && !done) {
+        // give up (see Spin): NaN carry, and report it
+#pragma unroll
+        for (int k = 0; k < M::NI; ++k) carry[k] = __builtin_nanf("");
+        done = true;
+        spin_give_up(spin);
       }
       const unsigned long long pending = __ballot(!done);
       const unsigned long long moved = __ballot(progressed);
@@ -514,7 +538,7 @@ static int check_dims(int B, int T, int d, int dtype) {
 // at the start of the call:
 //   counters[kMaxStages] | tagged carries | tagged aggregates
 struct Lookback {
-  int* counters;
+  int* counters;  // kMaxStages ticket counters, then the give-up status word
   unsigned long long* incl;
   unsigned long long* agg;
   size_t clear_words;
@@ -523,6 +547,7 @@ struct Lookback {
   // earlier call with a smaller base), so only the ticket counters are
   // cleared and this call's tags start at tag_base + 1.
   int tag_base = 0;
+  Spin spin() const { return Spin{counters + kMaxStages, spin_limit()}; }
 };
 
 static int check_tag_base(int tag_base) {
@@ -534,12 +559,12 @@ static int check_tag_base(int tag_base) {
 
 // Zero what the call's look-back needs zeroed (see Lookback::tag_base).
 static int clear_status(const Lookback& lb, hipStream_t stream) {
-  return clear_words(lb.counters, lb.tag_base > 0 ? kMaxStages : lb.clear_words, stream);
+  return clear_words(lb.counters, lb.tag_base > 0 ? kMaxStages + 1 : lb.clear_words, stream);
 }
 
 static Lookback carve_lookback(Carver& cv, const Geo& g, int incl_vals, int agg_vals) {
   Lookback lb;
-  lb.counters = static_cast<int*>(cv.take(sizeof(int) * kMaxStages));
+  lb.counters = static_cast<int*>(cv.take(sizeof(int) * (kMaxStages + 1)));
   lb.incl = static_cast<unsigned long long*>(
       cv.take(sizeof(unsigned long long) * incl_vals * kCB * g.n_tiles));
   lb.agg = static_cast<unsigned long long*>(

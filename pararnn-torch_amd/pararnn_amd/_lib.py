@@ -32,6 +32,8 @@ SIGNATURES: dict[str, tuple] = {
     "prnn_set_deterministic": (None, [_I]),
     "prnn_deterministic": (_I, []),
     "prnn_set_kernel_timing": (None, [_I]),
+    "prnn_set_spin_limit": (None, [_I]),
+    "prnn_slstm_lookback_status": (_I, [_P, ctypes.POINTER(ctypes.c_int), _P]),
     "prnn_last_kernel_ms": (ctypes.c_float, []),
     "prnn_slstm_init_workspace_size": (_S, [_I, _I, _I, _I, _I]),
     "prnn_slstm_init": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _P, _S, _P]),

@@ -92,6 +92,23 @@ def _slstm_workspace(nbytes: int, dev: torch.device) -> tuple[Tensor, int]:
         return ent[0], base
 
 
+def _check_lookback(ws: Tensor, what: str) -> None:
+    """With ``PARARNN_AMD_CHECK_STATUS=1``: wait for the call and raise
+    ``RuntimeError`` if one of its look-back or hand-off waits gave up
+    (``prnn_slstm_lookback_status``; the affected outputs are NaN)."""
+    if os.environ.get("PARARNN_AMD_CHECK_STATUS", "0") == "0":
+        return
+    if torch.cuda.is_current_stream_capturing():
+        return
+    st = ctypes.c_int(0)
+    lib = _lib.load()
+    _lib.check(lib.prnn_slstm_lookback_status(_ptr(ws), ctypes.byref(st), _stream(ws.device)),
+               what)
+    if st.value:
+        raise RuntimeError(f"{what}: a look-back wait gave up (status {st.value}); the output "
+                           f"holds NaN where it did")
+
+
 def release_workspaces() -> None:
     """Drop the cached sLSTM workspaces (they are re-created on demand)."""
     with _tagged_lock:
@@ -152,6 +169,7 @@ def slstm_init_fused(
             float(eps), code, _ptr(ws), ws.numel(), tag, _stream(wx.device),
         )
     _lib.check(rc, "slstm_init_fused")
+    _check_lookback(ws, "slstm_init_fused")
     return out
 
 
@@ -221,6 +239,7 @@ def newton_slstm_fused(
             _stream(wx.device),
         )
     _lib.check(rc, "newton_slstm_fused")
+    _check_lookback(ws, "newton_slstm_fused")
     return out
 
 
@@ -269,6 +288,7 @@ def slstm_backward_fused(
             _stream(wx.device),
         )
     _lib.check(rc, "slstm_backward_fused")
+    _check_lookback(ws, "slstm_backward_fused")
     return g_wx, g_r, g_h0, g_b
 
 
