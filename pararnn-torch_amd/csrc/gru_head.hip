@@ -1446,30 +1446,6 @@ __global__ __launch_bounds__(256) void gru_ga_reduce_kernel(const float* __restr
   g_a[e] = acc;
 }
 
-// ---------------------------------------------------------------------------
-// Test hook: C = A B for 64x64 fp32 inputs through the bf16 MFMA operand
-// layout used above (one block of 256 threads).
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void mfma_probe_kernel(const float* A, const float* Bm, float* C) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int li = lane & 15, lq = lane >> 4;
-#pragma unroll
-  for (int tn = 0; tn < 4; ++tn) {
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      bf16x8 a, bb;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        a[q] = static_cast<__bf16>(A[(16 * wave + li) * DH + 32 * ks + 8 * lq + q]);
-        bb[q] = static_cast<__bf16>(Bm[(32 * ks + 8 * lq + q) * DH + 16 * tn + li]);
-      }
-      acc = mfma(a, bb, acc);
-    }
-#pragma unroll
-    for (int v = 0; v < 4; ++v) C[(16 * wave + 4 * lq + v) * DH + 16 * tn + li] = acc[v];
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Host side
@@ -1803,11 +1779,3 @@ extern "C" PRNN_API int prnn_gru_head_backward(const void* wx, const void* a_z, 
                       n_heads, w, s);
 }
 
-// Internal test hook (not part of the public header): C = A B, 64x64 fp32
-// row-major, through the bf16 MFMA operand layout of the chunk kernel.
-extern "C" PRNN_API int prnn_internal_mfma_probe(const float* A, const float* Bm, float* C,
-                                                 void* stream) {
-  gru::mfma_probe_kernel<<<dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(A, Bm, C);
-  PRNN_HIP(hipGetLastError());
-  return PRNN_OK;
-}

@@ -1,8 +1,6 @@
 """GPU parity of the ParaGRU(mix='head') HIP path (chunked MFMA scan) against
 the CPU oracle and the reference's golden vectors."""
 
-import ctypes
-
 import pytest
 import torch
 from conftest import load_golden
@@ -37,27 +35,6 @@ def _cell(t, m, dtype):
         for k in ("A_z", "A_r", "A_n"):
             getattr(cell, k).copy_(t[k])
     return cell.to(device=DEV, dtype=dtype)
-
-
-def test_mfma_operand_layout():
-    from pararnn_amd import _lib
-
-    print("case mfma probe", flush=True)
-    lib = _lib.load()
-    fn = lib.prnn_internal_mfma_probe
-    fn.restype = ctypes.c_int
-    fn.argtypes = [ctypes.c_void_p] * 4
-    g = torch.Generator().manual_seed(0)
-    A = torch.randn(64, 64, generator=g)
-    B = torch.randn(64, 64, generator=g)
-    C = torch.empty(64, 64, device=DEV)
-    Ad, Bd = A.to(DEV), B.to(DEV)
-    assert fn(Ad.data_ptr(), Bd.data_ptr(), C.data_ptr(), torch.cuda.current_stream().cuda_stream) == 0
-    torch.cuda.synchronize()
-    ref = A.bfloat16().float() @ B.bfloat16().float()
-    err = (C.cpu() - ref).abs().max().item()
-    print(f"mfma probe max err {err:.2e}", flush=True)
-    assert err < 1e-3
 
 
 @pytest.mark.parametrize("name", ["gru_head_fp32", "gru_head_h0_fp32"])
