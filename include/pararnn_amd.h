@@ -120,6 +120,19 @@ PRNN_API int prnn_slstm_newton(const void* wx, const void* r, const void* h0, co
                                float eps, int dtype, void* workspace, size_t workspace_bytes,
                                void* stream);
 
+/* One Newton iteration with an fp32 result, for the host-checked early exit
+ * (replaces the per-iteration body of kernels/newton_slstm.py:2780-2922 that
+ * NewtonConfig.fused_early_exit runs, solvers/newton/__init__.py:696-762):
+ * `in` is the current iterate, fp32 when in_f32 != 0 (the fp32 work iterate
+ * of earlier steps) or else in `dtype` (the guess); `out` receives
+ * in + omega * delta in fp32, exactly what the K-iteration call keeps
+ * between its iterations.  Workspace: prnn_slstm_newton_workspace_size with
+ * max_iters = 1; tag_base as for prnn_slstm_newton_ex. */
+PRNN_API int prnn_slstm_newton_step(const void* wx, const void* r, const void* h0,
+                                    const void* in, int in_f32, float* out, int B, int T, int d,
+                                    float omega, float eps, int dtype, void* workspace,
+                                    size_t workspace_bytes, int tag_base, void* stream);
+
 /* ---- ParaGRU mix='head' --------------------------------------------------
  * Layouts: wx (B, T, 3d) gate blocks (z, r, n);  a_z, a_r, a_n
  * (n_heads, d_head, d_head) laid out (in, out) so y = h @ A per head;

@@ -1539,6 +1539,46 @@ extern "C" PRNN_API int prnn_slstm_newton(const void* wx, const void* r, const v
                               workspace, workspace_bytes, 0, stream);
 }
 
+extern "C" PRNN_API int prnn_slstm_newton_step(const void* wx, const void* r, const void* h0,
+                                               const void* in, int in_f32, float* out, int B,
+                                               int T, int d, float omega, float eps, int dtype,
+                                               void* workspace, size_t workspace_bytes,
+                                               int tag_base, void* stream) {
+  int rc = slstm::check_dims(B, T, d, dtype);
+  if (rc != PRNN_OK) return rc;
+  rc = slstm::check_tag_base(tag_base);
+  if (rc != PRNN_OK) return rc;
+  if (!wx || !r || !in || !out || !workspace)
+    return fail(PRNN_ERR_VALUE, "wx, r, in, out and workspace must be non-null");
+  if (static_cast<const void*>(out) == in) return fail(PRNN_ERR_VALUE, "out must not alias in");
+  size_t need = 0;
+  slstm::NewtonWs w = slstm::carve_newton(workspace, B, T, d, 1, dtype, &need);
+  if (workspace_bytes < need)
+    return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  w.lb.tag_base = tag_base;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = slstm::clear_status(w.lb, s);
+  if (rc != PRNN_OK) return rc;
+  timing_begin(s);
+  if (dtype == PRNN_F32) {
+    slstm::launch_newton<float, float, float>(
+        static_cast<const float*>(wx), static_cast<const float*>(r),
+        static_cast<const float*>(h0), static_cast<const float*>(in), out, B, T, d, omega, eps,
+        w.lb, 1, s);
+  } else if (in_f32) {
+    slstm::launch_newton<bf16, float, float>(
+        static_cast<const bf16*>(wx), static_cast<const bf16*>(r), static_cast<const bf16*>(h0),
+        static_cast<const float*>(in), out, B, T, d, omega, eps, w.lb, 1, s);
+  } else {
+    slstm::launch_newton<bf16, bf16, float>(
+        static_cast<const bf16*>(wx), static_cast<const bf16*>(r), static_cast<const bf16*>(h0),
+        static_cast<const bf16*>(in), out, B, T, d, omega, eps, w.lb, 1, s);
+  }
+  timing_end(s);
+  PRNN_HIP(hipGetLastError());
+  return PRNN_OK;
+}
+
 extern "C" PRNN_API int prnn_slstm_lookback_status(const void* workspace, int* status,
                                                    void* stream) {
   if (!workspace || !status) return fail(PRNN_ERR_VALUE, "workspace and status must be non-null");

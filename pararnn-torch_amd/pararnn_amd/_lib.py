@@ -64,6 +64,8 @@ SIGNATURES: dict[str, tuple] = {
     "prnn_slstm_newton_noalloc_max_bytes": (_S, []),
     "prnn_slstm_newton_noalloc": (
         _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _I, _P]),
+    "prnn_slstm_newton_step": (
+        _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _F, _F, _I, _P, _S, _I, _P]),
     "prnn_slstm_decode": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _F, _I, _I, _P]),
     "prnn_gru_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _I, _I, _P]),
 }

@@ -223,10 +223,13 @@ def _fill_stats(cell, x, states, h0, config, *, iters, stats, history=(), known=
 def _newton_solve(cell, x, config, *, h0, stats, wx=None) -> Tensor:
     if config.chunk_len is not None:
         return _newton_chunked(cell, x, config, h0=h0, stats=stats)
-    if config.fused_early_exit:
-        raise TypeError("fused_early_exit is not provided by pararnn_amd")
     if wx is None:
         wx = cell.W_x(x)
+    if config.fused_early_exit and not torch.compiler.is_compiling():
+        states, iters, history = _fused_early_exit(cell, wx, config, h0=h0)
+        _fill_stats(cell, x, states, h0, config, iters=iters, stats=stats, history=history,
+                    known=history[-1] if history else float("nan"))
+        return states
     states = fused_newton(
         cell, wx,
         max_iters=int(config.max_iters), omega=float(config.omega), h0=h0,
@@ -237,6 +240,32 @@ def _newton_solve(cell, x, config, *, h0, stats, wx=None) -> Tensor:
     if not torch.compiler.is_compiling():
         _fill_stats(cell, x, states, h0, config, iters=int(config.max_iters), stats=stats)
     return states
+
+
+def _fused_early_exit(cell, wx, config, *, h0) -> tuple[Tensor, int, list[float]]:
+    """``NewtonConfig.fused_early_exit`` (newton/__init__.py:696-762, the early-exit
+    branch of kernels/newton_slstm.py:2892-2922): the fused iterations one at a
+    time on the fp32 work iterate; after each, the host reads max|F| of the
+    iterate rounded to ``wx``'s dtype and stops below ``residual_atol``.
+    Returns ``(states, iterations run, residual history)``.  ParaSLSTM
+    mix='diag' only, as in the reference."""
+    if not (isinstance(cell, ParaSLSTM) and cell.mix == "diag"):
+        raise TypeError("fused_early_exit is mix='diag' only; ParaGRU(mix='head') uses fixed K")
+    atol = float(config.residual_atol)
+    r = cell.clipped_r()
+    P = int(config.picard_iters or 0)
+    work = ops.slstm_init_fused(wx, r, h0, picard_iters=P, eps=cell.eps)
+    history: list[float] = []
+    states = work
+    for it in range(int(config.max_iters)):
+        work = ops.slstm_newton_step(wx, r, h0, work, omega=float(config.omega), eps=cell.eps)
+        states = work.to(wx.dtype)
+        pred = cell.step(_prepend(states, h0), None, wx=wx)
+        res = float((pred - states).abs().amax())
+        history.append(res)
+        if res < atol:
+            return states, it + 1, history
+    return states, int(config.max_iters), history
 
 
 def _newton_chunked(cell, x, config, *, h0, stats) -> Tensor:
@@ -389,7 +418,9 @@ def _newton_ragged(cell, x, config, *, h0, stats, cu_seqlens, block_table, needs
         raise ValueError(f"h0 batch {h0.shape[0]} != n_seq {n_seq}")
     plan = RaggedPlan(cs, x.device)
     ladder = bool(config.picard_adapt) and isinstance(cell, ParaSLSTM)
-    inner = replace(config, picard_adapt=False, residual_fail=None)
+    # The length groups run the full K: an early exit decided per group would
+    # not be the packed stream's (fused_early_exit is ignored with cu_seqlens).
+    inner = replace(config, picard_adapt=False, residual_fail=None, fused_early_exit=False)
     hist = []
     while True:
         if needs_grad:

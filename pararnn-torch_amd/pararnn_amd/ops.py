@@ -243,6 +243,38 @@ def newton_slstm_fused(
     return out
 
 
+def slstm_newton_step(wx: Tensor, r: Tensor, h0: Tensor | None, states: Tensor, *,
+                      omega: float, eps: float) -> Tensor:
+    """One Newton iteration from ``states`` (``wx``'s dtype, or fp32 work)
+    with an fp32 result: the per-iteration body of the fused op, for the
+    host-checked early exit (``NewtonConfig.fused_early_exit``; reference
+    kernels/newton_slstm.py:2780-2922).  Not a registered op: the early exit
+    synchronises with the host after every iteration."""
+    batch, time, d_h = _slstm_shapes(wx, r)
+    code = _validate("slstm_newton_step", wx, r, h0)
+    h0 = _slstm_h0(h0, batch, d_h)
+    if states.shape != (batch, time, 4, d_h):
+        raise ValueError(f"states shape {tuple(states.shape)} != {(batch, time, 4, d_h)}")
+    in_f32 = states.dtype == torch.float32
+    if not in_f32 and states.dtype != wx.dtype:
+        raise TypeError(f"slstm_newton_step: states dtype {states.dtype} is neither fp32 nor "
+                        f"wx's {wx.dtype}")
+    wx, r, states = wx.contiguous(), r.contiguous(), states.contiguous()
+    out = torch.empty(batch, time, 4, d_h, dtype=torch.float32, device=wx.device)
+    lib = _lib.load()
+    _lib.sync_deterministic(lib)
+    with torch.cuda.device(wx.device):
+        nbytes = lib.prnn_slstm_newton_workspace_size(batch, time, d_h, 1, code)
+        ws, tag = _slstm_workspace(nbytes, wx.device)
+        rc = lib.prnn_slstm_newton_step(
+            _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), int(in_f32), _ptr(out), batch, time,
+            d_h, float(omega), float(eps), code, _ptr(ws), ws.numel(), tag, _stream(wx.device),
+        )
+    _lib.check(rc, "slstm_newton_step")
+    _check_lookback(ws, "slstm_newton_step")
+    return out
+
+
 @newton_slstm_fused.register_fake
 def _(wx, r, h0=None, states=None, block_table=None, *, max_iters, omega, eps,
       log_coords=False, scan_tile="assoc", time_loop=False, window_len=0):
