@@ -147,6 +147,38 @@ PRNN_API int prnn_gru_head_newton(const void* wx, const void* a_z, const void* a
                                   int n_heads, int d_head, int max_iters, float omega, int dtype,
                                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* Packed sequences (replace the reference's cu_seqlens handling for the
+ * diag sLSTM: the ragged frozen-gate scan solvers/slstm_picard.py:87-103 and
+ * the J = 0 segment heads of solvers/scan.py:206-216 with layout.py:115-138,
+ * and the paged h0 of kernels/_fused_common.py:106-139).  wx / states / out
+ * hold one stream (B = 1) of T steps: sequence s occupies steps
+ * [cu_seqlens[s], cu_seqlens[s+1]) (int32 device array of n_seq + 1 entries,
+ * 0 = first < ... < last = T).  At the first step of each sequence the
+ * previous state is the sequence's initial state -- h0 row block_table[s]
+ * when block_table (n_seq int32 device entries) is given, else row s; zeros
+ * when h0 is NULL -- and no carry crosses it.  The kernels read cu_seqlens
+ * and block_table themselves: no padding, no gather, one launch set for the
+ * whole stream.  Workspace from the *_packed_workspace_size calls; tag_base
+ * as for the _ex calls.  The caller checks cu_seqlens (the kernels trust it). */
+PRNN_API size_t prnn_slstm_init_packed_workspace_size(int T, int d, int picard_iters, int dtype);
+PRNN_API int prnn_slstm_init_packed(const void* wx, const void* r, const void* h0, void* states,
+                                    int T, int d, int picard_iters, float eps, int dtype,
+                                    const int* cu_seqlens, int n_seq, const int* block_table,
+                                    void* workspace, size_t workspace_bytes, int tag_base,
+                                    void* stream);
+PRNN_API size_t prnn_slstm_newton_packed_workspace_size(int T, int d, int max_iters, int dtype);
+PRNN_API int prnn_slstm_newton_packed(const void* wx, const void* r, const void* h0,
+                                      const void* states, void* out, int T, int d, int max_iters,
+                                      float omega, float eps, int dtype, const int* cu_seqlens,
+                                      int n_seq, const int* block_table, void* workspace,
+                                      size_t workspace_bytes, int tag_base, void* stream);
+PRNN_API int prnn_slstm_newton_step_packed(const void* wx, const void* r, const void* h0,
+                                           const void* in, int in_f32, float* out, int T, int d,
+                                           float omega, float eps, int dtype,
+                                           const int* cu_seqlens, int n_seq,
+                                           const int* block_table, void* workspace,
+                                           size_t workspace_bytes, int tag_base, void* stream);
+
 /* Eq. 2.6 backward at the solved trajectory `states` = H* (B, T, 4, d) with
  * upstream gradient `grad` = dL/dH (B, T, 4, d):
  *   mu_{T-1} = grad_{T-1},  mu_t = grad_t + J_{t+1}^T mu_{t+1}  (fp32),
@@ -213,6 +245,20 @@ PRNN_API int prnn_slstm_newton_noalloc(const void* wx, const void* r, const void
                                        const void* states, void* out, int B, int T, int d,
                                        int max_iters, float omega, float eps, int dtype,
                                        void* stream);
+
+/* Eq. 2.6 backward of a packed stream (cu_seqlens as for the packed forward;
+ * replaces the reference's ragged reverse scan with J = 0 at heads,
+ * solvers/scan.py:206-216 reversed, solvers/newton/__init__.py:765-866):
+ * nothing flows from a sequence's first step to the step before it, and
+ * g_h0 (n_seq, 4, d) fp32 (or NULL) receives J_head^T mu_head per sequence,
+ * the gradient of that sequence's h0 row.  Workspace as
+ * prnn_slstm_backward_workspace_size(1, T, d, dtype). */
+PRNN_API int prnn_slstm_backward_packed(const void* wx, const void* r, const void* h0,
+                                        const void* states, const void* grad, void* g_wx,
+                                        float* g_r, float* g_h0, float* g_b, int T, int d,
+                                        float eps, int dtype, const int* cu_seqlens, int n_seq,
+                                        void* workspace, size_t workspace_bytes, int tag_base,
+                                        void* stream);
 
 /* Eq. 2.6 backward of the head GRU at `states` = H* (B, T, d) with upstream
  * gradient `grad` = dL/dH (B, T, d) (both in `dtype`):

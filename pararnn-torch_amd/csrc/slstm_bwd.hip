@@ -82,13 +82,13 @@ __device__ __forceinline__ void cell_vjp(const float prev[4], const float x[4], 
 // Per-tile gradient partials: sum_t dz_g h_{t-1} (R) then sum_t dz_g (bias), g = 0..3.
 constexpr int kPartials = 8;
 
-template <typename TX, int L, int W, bool DET>
+template <typename TX, int L, int W, bool DET, bool PK>
 __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
     const TX* __restrict__ states, const TX* __restrict__ grad, TX* __restrict__ gwx,
     float* __restrict__ gr_part, float* __restrict__ gh0, int B, int T, int d, int n_cb,
     int n_chunks, float eps, int* __restrict__ counter, unsigned long long* __restrict__ agg,
-    unsigned long long* __restrict__ incl, int epoch, Spin spin) {
+    unsigned long long* __restrict__ incl, int epoch, Spin spin, Packed pk) {
   // predecessors per wave per look-back round (the deterministic walk, which
   // must find an inclusive carry inside its window, looks twice as far)
   constexpr int KP = DET ? 2 : 1;
@@ -134,8 +134,24 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
   const rsrc_t rh = make_rsrc(states + first * row4 + c0, span);
   const rsrc_t rx = make_rsrc(wx + first * row4 + c0, span);
   const rsrc_t rg = make_rsrc(grad + first * row4 + c0, span);
+  // Packed sequences (see Packed): a head's previous state is its sequence's
+  // h0 row; nothing flows from a head to the step before it (nu = 0 there),
+  // and the head's nu = J^T mu is that sequence's dL/dh0.
+  Heads hd{0ull, 0};
+  float hst[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (PK) {
+    hd = find_heads(pk, t0, n_steps);
+    if (hd.mask) head_state(pk, h0, hd.seq(hd.first()), d, c0 + lane, live, hst);
+  }
   auto prev_of = [&](int s, float p[4]) {
-    if (s == 0) {
+    if (PK && hd.at(s)) {
+      if (s == hd.first()) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) p[k] = hst[k];
+      } else {
+        head_state(pk, h0, hd.seq(s), d, c0 + lane, live, p);
+      }
+    } else if (s == 0) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) p[k] = prev0[k];
     } else {
@@ -147,7 +163,8 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
   Aff a;
   aff_identity(a);
   {
-    auto step = [&](int s) {
+    auto step = [&](int s, auto chk) {
+      constexpr bool CHECK = decltype(chk)::value;
       const uint32_t so = s * row4 * SZ;
       RS::load(rx, voff, so, slot, xs[s]);
       RS::load(rg, voff, so, slot, gs[s]);
@@ -168,15 +185,30 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
 #pragma unroll
         for (int k = 0; k < 4; ++k) a.A[k][j] = col[k];
       }
+      if (CHECK && hd.at(s)) {
+        // a head: nothing reaches the steps before it
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          a.b[i] = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) a.A[i][j] = 0.f;
+        }
+      }
     };
-    if (n_steps == L) {
+    auto run = [&](auto chk) {
+      if (n_steps == L) {
 #pragma unroll
-      for (int s = L - 1; s >= 0; --s) step(s);
-    } else {
+        for (int s = L - 1; s >= 0; --s) step(s, chk);
+      } else {
 #pragma unroll
-      for (int s = L - 1; s >= 0; --s)
-        if (s < n_steps) step(s);
-    }
+        for (int s = L - 1; s >= 0; --s)
+          if (s < n_steps) step(s, chk);
+      }
+    };
+    if (PK && hd.mask)
+      run(std::true_type{});
+    else
+      run(std::false_type{});
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -253,7 +285,8 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
   float gb[4] = {0.f, 0.f, 0.f, 0.f};  // sum_t dz_g: the W_x bias gradient
   {
     const rsrc_t ro = make_rsrc(gwx + first * row4 + c0, span);
-    auto replay = [&](int s) {
+    auto replay = [&](int s, auto chk) {
+      constexpr bool CHECK = decltype(chk)::value;
       float prev[4], x[4], g[4], mu[4], dz[4];
       prev_of(s, prev);
       RS::get(xs[s], x);
@@ -268,17 +301,33 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
         gr[k] += dz[k] * prev[3];
         gb[k] += dz[k];
       }
+      if (CHECK && hd.at(s)) {
+        // a head: nu is its sequence's dL/dh0, and nothing flows further back
+        if (gh0 != nullptr && live) {
+          float* p = gh0 + static_cast<size_t>(hd.seq(s)) * row4 + c0 + lane;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) p[k * d] = nu[k];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) nu[k] = 0.f;
+      }
     };
-    if (n_steps == L) {
+    auto run = [&](auto chk) {
+      if (n_steps == L) {
 #pragma unroll
-      for (int s = L - 1; s >= 0; --s) replay(s);
-    } else {
+        for (int s = L - 1; s >= 0; --s) replay(s, chk);
+      } else {
 #pragma unroll
-      for (int s = L - 1; s >= 0; --s)
-        if (s < n_steps) replay(s);
-    }
+        for (int s = L - 1; s >= 0; --s)
+          if (s < n_steps) replay(s, chk);
+      }
+    };
+    if (PK && hd.mask)
+      run(std::true_type{});
+    else
+      run(std::false_type{});
   }
-  if (gh0 != nullptr && t0 == 0 && live) {
+  if (!PK && gh0 != nullptr && t0 == 0 && live) {
     float* p = gh0 + static_cast<size_t>(id.b) * row4 + c0 + lane;
 #pragma unroll
     for (int k = 0; k < 4; ++k) p[k * d] = nu[k];
@@ -378,7 +427,10 @@ struct BwdWs {
 };
 
 static BwdWs carve_bwd(void* base, int B, int T, int d, int dtype, size_t* total) {
-  const Geo g = geometry(B, T, d, bwd_shape(dtype));
+  // the packed launch takes the default shape: size for both
+  Geo g = geometry(B, T, d, bwd_shape(dtype));
+  const Geo gd = geometry(B, T, d, dtype == PRNN_BF16 ? kBwdDefault : kBwdF32);
+  if (gd.n_tiles > g.n_tiles) g = gd;
   Carver cv(base);
   BwdWs w;
   w.lb = carve_lookback(cv, g, 4, 20);
@@ -387,25 +439,36 @@ static BwdWs carve_bwd(void* base, int B, int T, int d, int dtype, size_t* total
   return w;
 }
 
-template <typename TX, int L, int W, bool DET>
+template <typename TX, int L, int W, bool DET, bool PK = false>
 static void launch_reverse(const TX* wx, const TX* r, const TX* h0, const TX* states,
                            const TX* grad, TX* gwx, float* gh0, int B, int T, int d, float eps,
-                           const BwdWs& w, hipStream_t stream) {
+                           const BwdWs& w, hipStream_t stream,
+                           const Packed& pk = Packed{nullptr, nullptr, 0}) {
   const Geo g = geometry(B, T, d, Shape{L, W});
-  slstm_reverse_kernel<TX, L, W, DET><<<dim3(g.n_tiles), dim3(64 * W), 0, stream>>>(
+  slstm_reverse_kernel<TX, L, W, DET, PK><<<dim3(g.n_tiles), dim3(64 * W), 0, stream>>>(
       wx, r, h0, states, grad, gwx, w.gr_part, gh0, B, T, d, g.n_cb, g.n_chunks, eps,
-      w.lb.counters + 1, w.lb.agg, w.lb.incl, w.lb.tag_base + 1, w.lb.spin());
+      w.lb.counters + 1, w.lb.agg, w.lb.incl, w.lb.tag_base + 1, w.lb.spin(), pk);
 }
 
 template <typename TX>
 static int run_bwd(const TX* wx, const TX* r, const TX* h0, const TX* states, const TX* grad,
                    TX* gwx, float* gr, float* gh0, float* gb, int B, int T, int d, float eps,
-                   const BwdWs& w, hipStream_t stream) {
+                   const BwdWs& w, hipStream_t stream, const Packed& pk) {
   int rc = clear_status(w.lb, stream);
   if (rc != PRNN_OK) return rc;
   timing_begin(stream);
   Shape sh;
-  if constexpr (sizeof(TX) == 4) {
+  if (pk.cu != nullptr) {
+    // packed stream: default shapes
+    constexpr Shape dsh = sizeof(TX) == 4 ? kBwdF32 : kBwdDefault;
+    sh = dsh;
+    if (deterministic())
+      launch_reverse<TX, dsh.L, dsh.W, true, true>(wx, r, h0, states, grad, gwx, gh0, B, T, d,
+                                                   eps, w, stream, pk);
+    else
+      launch_reverse<TX, dsh.L, dsh.W, false, true>(wx, r, h0, states, grad, gwx, gh0, B, T, d,
+                                                    eps, w, stream, pk);
+  } else if constexpr (sizeof(TX) == 4) {
 #define PRNN_LAUNCH(LL, WW, DD) \
   launch_reverse<TX, LL, WW, DD>(wx, r, h0, states, grad, gwx, gh0, B, T, d, eps, w, stream)
     sh = kBwdF32;
@@ -447,17 +510,18 @@ extern "C" PRNN_API size_t prnn_slstm_backward_workspace_size(int B, int T, int 
   return total;
 }
 
-extern "C" PRNN_API int prnn_slstm_backward_ex(const void* wx, const void* r, const void* h0,
-                                               const void* states, const void* grad, void* gwx,
-                                               float* gr, float* gh0, float* gb, int B, int T,
-                                               int d,
-                                               float eps, int dtype, void* workspace,
-                                               size_t workspace_bytes, int tag_base,
-                                               void* stream) {
+namespace {
+
+int backward_call(const void* wx, const void* r, const void* h0, const void* states,
+                  const void* grad, void* gwx, float* gr, float* gh0, float* gb, int B, int T,
+                  int d, float eps, int dtype, void* workspace, size_t workspace_bytes,
+                  int tag_base, void* stream, const slstm::Packed& pk) {
   int rc = slstm::check_dims(B, T, d, dtype);
   if (rc != PRNN_OK) return rc;
   rc = slstm::check_tag_base(tag_base);
   if (rc != PRNN_OK) return rc;
+  if (pk.cu != nullptr && pk.n_seq < 1)
+    return fail(PRNN_ERR_VALUE, "n_seq must be >= 1, got %d", pk.n_seq);
   if (!wx || !r || !states || !grad || !gwx || !gr || !workspace)
     return fail(PRNN_ERR_VALUE, "wx, r, states, grad, g_wx, g_r and workspace must be non-null");
   size_t need = 0;
@@ -470,11 +534,38 @@ extern "C" PRNN_API int prnn_slstm_backward_ex(const void* wx, const void* r, co
     return slstm::run_bwd(static_cast<const float*>(wx), static_cast<const float*>(r),
                           static_cast<const float*>(h0), static_cast<const float*>(states),
                           static_cast<const float*>(grad), static_cast<float*>(gwx), gr, gh0, gb,
-                          B, T, d, eps, w, s);
+                          B, T, d, eps, w, s, pk);
   return slstm::run_bwd(static_cast<const bf16*>(wx), static_cast<const bf16*>(r),
                         static_cast<const bf16*>(h0), static_cast<const bf16*>(states),
                         static_cast<const bf16*>(grad), static_cast<bf16*>(gwx), gr, gh0, gb, B, T,
-                        d, eps, w, s);
+                        d, eps, w, s, pk);
+}
+
+}  // namespace
+
+extern "C" PRNN_API int prnn_slstm_backward_ex(const void* wx, const void* r, const void* h0,
+                                               const void* states, const void* grad, void* gwx,
+                                               float* gr, float* gh0, float* gb, int B, int T,
+                                               int d,
+                                               float eps, int dtype, void* workspace,
+                                               size_t workspace_bytes, int tag_base,
+                                               void* stream) {
+  return backward_call(wx, r, h0, states, grad, gwx, gr, gh0, gb, B, T, d, eps, dtype, workspace,
+                       workspace_bytes, tag_base, stream, slstm::Packed{nullptr, nullptr, 0});
+}
+
+extern "C" PRNN_API int prnn_slstm_backward_packed(const void* wx, const void* r,
+                                                   const void* h0, const void* states,
+                                                   const void* grad, void* gwx, float* gr,
+                                                   float* gh0, float* gb, int T, int d,
+                                                   float eps, int dtype, const int* cu_seqlens,
+                                                   int n_seq, void* workspace,
+                                                   size_t workspace_bytes, int tag_base,
+                                                   void* stream) {
+  if (!cu_seqlens) return fail(PRNN_ERR_VALUE, "cu_seqlens must be non-null");
+  return backward_call(wx, r, h0, states, grad, gwx, gr, gh0, gb, 1, T, d, eps, dtype, workspace,
+                       workspace_bytes, tag_base, stream,
+                       slstm::Packed{cu_seqlens, nullptr, n_seq});
 }
 
 extern "C" PRNN_API int prnn_slstm_backward(const void* wx, const void* r, const void* h0,

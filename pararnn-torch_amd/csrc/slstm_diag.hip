@@ -160,12 +160,12 @@ struct PreStash<float> {
 // lane owns one channel; its L steps are read once (pass 1, which builds the
 // lane aggregate), kept in registers through the look-back, and replayed from
 // the true carry in pass 2, which writes the trajectory.
-template <typename TX, int L, int W, bool HAS_H, bool FULL_OUT, bool DET>
+template <typename TX, int L, int W, bool HAS_H, bool FULL_OUT, bool DET, bool PK>
 __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
     const TX* __restrict__ hsrc, TX* __restrict__ out_full, TX* __restrict__ out_h, int B, int T,
     int d, int n_cb, float eps, int* __restrict__ counter, unsigned long long* __restrict__ agg,
-    unsigned long long* __restrict__ incl, int epoch, Spin spin) {
+    unsigned long long* __restrict__ incl, int epoch, Spin spin, Packed pk) {
   constexpr int KP = 2;  // predecessors per wave per look-back round
   using Stash = PreStash<TX>;
   constexpr uint32_t SZ = sizeof(TX);
@@ -199,6 +199,23 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
       hp0 = ld(h0 + static_cast<size_t>(id.b) * row4 + 3 * d + c0 + lane);
   }
 
+  // Packed sequences: heads among this wave's steps (see Packed); a head
+  // restarts the state from its sequence's initial one.
+  Heads hd{0ull, 0};
+  float hst[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (PK) {
+    hd = find_heads(pk, t0, n_steps);
+    if (hd.mask) head_state(pk, h0, hd.seq(hd.first()), d, c0 + lane, live, hst);
+  }
+  auto head_of = [&](int s, float st[4]) {
+    if (s == hd.first()) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) st[j] = hst[j];
+    } else {
+      head_state(pk, h0, hd.seq(s), d, c0 + lane, live, st);
+    }
+  };
+
   // Pass 1: read the steps, stash the pre-activations, and fold the segment
   // aggregate from the empty state (m = -inf, n = c = 0).
   uint32_t stash[L][Stash::N];
@@ -206,29 +223,41 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
   {
     const rsrc_t rx = make_rsrc(wx + first * row4 + c0, span4);
     const rsrc_t rh = make_rsrc(HAS_H ? hsrc + first * d + c0 : nullptr, HAS_H ? span1 : 0);
-    auto step = [&](int s) {
+    auto step = [&](int s, auto chk) {
+      constexpr bool CHECK = decltype(chk)::value;
+      const bool head = CHECK && hd.at(s);
+      float hs[4];
+      if (head) head_of(s, hs);
       uint32_t x[4];
 #pragma unroll
       for (int g = 0; g < 4; ++g)
         x[g] = ldb_bits(static_cast<TX*>(nullptr), rx, voff, s * row4 * SZ + g * slot);
       float hp = hp0;
       if (HAS_H && s > 0) hp = ldb<TX>(rh, voff, (s - 1) * d * SZ);
+      if (head) hp = hs[3];
       Stash::template make<HAS_H>(x, r, hp, stash[s]);
       float p[4];
       Stash::get(stash[s], p);
+      if (head) a = FG{-INFINITY, hs[2], hs[1], hs[0]};
       a.F += p[1];
       fg_step(p[0], p[1], p[2], a.M, a.N, a.C);
     };
     // Whole segments run branch-free so the loads of many steps are in
     // flight together; only the last segment of a sequence is guarded.
-    if (n_steps == L) {
+    auto run = [&](auto chk) {
+      if (n_steps == L) {
 #pragma unroll
-      for (int s = 0; s < L; ++s) step(s);
-    } else {
+        for (int s = 0; s < L; ++s) step(s, chk);
+      } else {
 #pragma unroll
-      for (int s = 0; s < L; ++s)
-        if (s < n_steps) step(s);
-    }
+        for (int s = 0; s < L; ++s)
+          if (s < n_steps) step(s, chk);
+      }
+    };
+    if (PK && hd.mask)
+      run(std::true_type{});
+    else
+      run(std::false_type{});
   }
   s_agg[wave][0][lane] = a.F;
   s_agg[wave][1][lane] = a.M;
@@ -244,7 +273,7 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
       tile_agg = fg_compose(
           tile_agg, FG{s_agg[w][0][lane], s_agg[w][1][lane], s_agg[w][2][lane], s_agg[w][3][lane]});
     if (id.chunk == 0) {
-      if (h0 != nullptr && live) {
+      if (!PK && h0 != nullptr && live) {
         const TX* hb = h0 + static_cast<size_t>(id.b) * row4 + c0 + lane;
         carry[2] = ld(hb);
         carry[1] = ld(hb + d);
@@ -291,7 +320,15 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
   float m = s_carry[wave][0][lane], n = s_carry[wave][1][lane], c = s_carry[wave][2][lane];
   const rsrc_t ro = FULL_OUT ? make_rsrc(out_full + first * row4 + c0, span4)
                              : make_rsrc(out_h + first * d + c0, span1);
-  auto replay = [&](int s) {
+  auto replay = [&](int s, auto chk) {
+    constexpr bool CHECK = decltype(chk)::value;
+    if (CHECK && hd.at(s)) {
+      float hs[4];
+      head_of(s, hs);
+      c = hs[0];
+      n = hs[1];
+      m = hs[2];
+    }
     float p[4];
     Stash::get(stash[s], p);
     fg_step(p[0], p[1], p[2], m, n, c);
@@ -307,14 +344,20 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
       stb<TX>(ro, voff, s * d * SZ, h);
     }
   };
-  if (n_steps == L) {
+  auto run2 = [&](auto chk) {
+    if (n_steps == L) {
 #pragma unroll
-    for (int s = 0; s < L; ++s) replay(s);
-  } else {
+      for (int s = 0; s < L; ++s) replay(s, chk);
+    } else {
 #pragma unroll
-    for (int s = 0; s < L; ++s)
-      if (s < n_steps) replay(s);
-  }
+      for (int s = 0; s < L; ++s)
+        if (s < n_steps) replay(s, chk);
+    }
+  };
+  if (PK && hd.mask)
+    run2(std::true_type{});
+  else
+    run2(std::false_type{});
 }
 
 // ---------------------------------------------------------------------------
@@ -331,14 +374,14 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
 //  * the stage-p carry: a decoupled look-back on stage-indexed tagged words.
 // Both only ever wait on tiles with earlier tickets (already resident or
 // done), so every wave reaches the end.
-template <int L, int W, int WPE, bool DET>
+template <int L, int W, int WPE, bool DET, bool PK>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) void
 slstm_picard_fused_kernel(
     const bf16* __restrict__ wx, const bf16* __restrict__ rmix, const bf16* __restrict__ h0,
     bf16* __restrict__ out, int B, int T, int d, int n_cb, int n_tiles, int P, float eps,
     int* __restrict__ counter, unsigned long long* __restrict__ agg,
     unsigned long long* __restrict__ incl, unsigned long long* __restrict__ hlast, int tag_base,
-    Spin spin) {
+    Spin spin, Packed pk) {
   static_assert(L % 2 == 0, "h is packed two steps to a register");
   constexpr int KP = 2;
   constexpr uint32_t SZ = 2;
@@ -379,6 +422,26 @@ slstm_picard_fused_kernel(
     }
   }
 
+  // Packed sequences: heads among this wave's steps and the initial state
+  // (c, n, m, h) of the first one's sequence (see Packed); a head restarts
+  // the frozen-gate state from it in every stage.
+  Heads hd{0ull, 0};
+  float hst[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (PK) {
+    c_init[0] = c_init[1] = c_init[2] = 0.f;
+    h0h = 0.f;
+    hd = find_heads(pk, t0, n_steps);
+    if (hd.mask) head_state(pk, h0, hd.seq(hd.first()), d, c0 + lane, live, hst);
+  }
+  auto head_of = [&](int s, float st[4]) {
+    if (s == hd.first()) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) st[j] = hst[j];
+    } else {
+      head_state(pk, h0, hd.seq(s), d, c0 + lane, live, st);
+    }
+  };
+
   uint32_t xw[L][2], pre[L][2], hh[L / 2];
   {
     const rsrc_t rx = make_rsrc(wx + first * row4 + c0, span4);
@@ -414,7 +477,9 @@ slstm_picard_fused_kernel(
     // h_{p-1} at t0 - 1.
     float hp0 = 0.f;
     if (!first_stage) {
-      if (t0 == 0) {
+      if (PK && hd.at(0)) {
+        hp0 = hst[3];
+      } else if (t0 == 0) {
         hp0 = h0h;
       } else if (wave > 0) {
         hp0 = s_hl[wave - 1][lane];
@@ -443,13 +508,18 @@ slstm_picard_fused_kernel(
 
     // Pass 1: this stage's pre-activations and the segment aggregate.
     FG a = fg_identity();
-    auto step1 = [&](int s) {
+    auto step1 = [&](int s, auto chk) {
+      constexpr bool CHECK = decltype(chk)::value;
+      const bool head = CHECK && hd.at(s);
+      float hs[4];
+      if (head) head_of(s, hs);
       if (first_stage) {
         pre[s][0] = xw[s][0];
         pre[s][1] = xw[s][1];
       } else {
-        const float hp =
+        float hp =
             s == 0 ? hp0 : ((s - 1) & 1 ? hi_bf16(hh[(s - 1) >> 1]) : lo_bf16(hh[(s - 1) >> 1]));
+        if (head) hp = hs[3];
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
           // round(R h) and round(wx + round(R h)), two gates per conversion.
@@ -458,17 +528,26 @@ slstm_picard_fused_kernel(
         }
       }
       const float zi = lo_bf16(pre[s][0]), zf = hi_bf16(pre[s][0]), zz = lo_bf16(pre[s][1]);
+      // a head: the segment so far no longer matters (F = -inf), the state
+      // restarts from the sequence's initial one
+      if (head) a = FG{-INFINITY, hs[2], hs[1], hs[0]};
       a.F += zf;
       fg_step(zi, zf, zz, a.M, a.N, a.C);
     };
-    if (n_steps == L) {
+    auto run1 = [&](auto chk) {
+      if (n_steps == L) {
 #pragma unroll
-      for (int s = 0; s < L; ++s) step1(s);
-    } else {
+        for (int s = 0; s < L; ++s) step1(s, chk);
+      } else {
 #pragma unroll
-      for (int s = 0; s < L; ++s)
-        if (s < n_steps) step1(s);
-    }
+        for (int s = 0; s < L; ++s)
+          if (s < n_steps) step1(s, chk);
+      }
+    };
+    if (PK && hd.mask)
+      run1(std::true_type{});
+    else
+      run1(std::false_type{});
     s_agg[wave][0][lane] = a.F;
     s_agg[wave][1][lane] = a.M;
     s_agg[wave][2][lane] = a.N;
@@ -536,7 +615,15 @@ slstm_picard_fused_kernel(
     // last stage writes the state.
     float m = s_carry[wave][0][lane], n = s_carry[wave][1][lane], c = s_carry[wave][2][lane];
     float h_even = 0.f, h_last = 0.f;
-    auto step2 = [&](int s) {
+    auto step2 = [&](int s, auto chk) {
+      constexpr bool CHECK = decltype(chk)::value;
+      if (CHECK && hd.at(s)) {
+        float hs[4];
+        head_of(s, hs);
+        c = hs[0];
+        n = hs[1];
+        m = hs[2];
+      }
       const float zi = lo_bf16(pre[s][0]), zf = hi_bf16(pre[s][0]);
       const float zz = lo_bf16(pre[s][1]), zo = hi_bf16(pre[s][1]);
       fg_step(zi, zf, zz, m, n, c);
@@ -556,14 +643,20 @@ slstm_picard_fused_kernel(
         h_last = lo_bf16(hh[s >> 1]);
       }
     };
-    if (n_steps == L) {
+    auto run2 = [&](auto chk) {
+      if (n_steps == L) {
 #pragma unroll
-      for (int s = 0; s < L; ++s) step2(s);
-    } else {
+        for (int s = 0; s < L; ++s) step2(s, chk);
+      } else {
 #pragma unroll
-      for (int s = 0; s < L; ++s)
-        if (s < n_steps) step2(s);
-    }
+        for (int s = 0; s < L; ++s)
+          if (s < n_steps) step2(s, chk);
+      }
+    };
+    if (PK && hd.mask)
+      run2(std::true_type{});
+    else
+      run2(std::false_type{});
     if constexpr (!last_stage) {
       s_hl[wave][lane] = h_last;
       if (wave == W - 1)
@@ -583,12 +676,12 @@ slstm_picard_fused_kernel(
 // reads each step once (wx and the guess, kept in registers) and folds the
 // lane's affine aggregate x -> J x + F; pass 2 replays the steps from the true
 // carry, delta_t = J_t delta_{t-1} + F_t, and writes H + omega delta.
-template <typename TX, typename TIN, typename TOUT, int L, int W, bool DET>
+template <typename TX, typename TIN, typename TOUT, int L, int W, bool DET, bool PK>
 __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
     const TIN* __restrict__ hin, TOUT* __restrict__ hout, int B, int T, int d, int n_cb,
     float omega, float eps, int* __restrict__ counter, unsigned long long* __restrict__ agg,
-    unsigned long long* __restrict__ incl, int epoch, Spin spin) {
+    unsigned long long* __restrict__ incl, int epoch, Spin spin, Packed pk) {
   // predecessors per wave per look-back round (the deterministic walk, which
   // must find an inclusive carry inside its window, looks twice as far)
   constexpr int KP = DET ? 2 : 1;
@@ -632,6 +725,14 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
     }
   }
 
+  // Packed sequences: heads among this wave's steps (see Packed).
+  Heads hd{0ull, 0};
+  if constexpr (PK) {
+    hd = find_heads(pk, t0, n_steps);
+    if (hd.at(0)) head_state(pk, h0, hd.seq(0), d, c0 + lane, live, prev0);
+  }
+  auto head_prev = [&](int s, float p[4]) { head_state(pk, h0, hd.seq(s), d, c0 + lane, live, p); };
+
   uint32_t xs[L][XS::N], hs[L][HS::N];
   // Pass 1: lane segment aggregate (A, b) of the affine maps x -> J x + F.
   Aff a;
@@ -640,13 +741,17 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
     const rsrc_t rx = make_rsrc(wx + first * row4 + c0, span * sizeof(TX));
     const rsrc_t ri = make_rsrc(hin + first * row4 + c0, span * sizeof(TIN));
     float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
-    auto step = [&](int s) {
+    auto step = [&](int s, auto chk) {
+      constexpr bool CHECK = decltype(chk)::value;
+      const bool head = CHECK && hd.at(s);
       XS::load(rx, vx, s * row4 * sizeof(TX), d * sizeof(TX), xs[s]);
       HS::load(ri, vi, s * row4 * sizeof(TIN), d * sizeof(TIN), hs[s]);
+      if (head && s > 0) head_prev(s, prev);
       float x[4], hv[4];
       XS::get(xs[s], x);
       HS::get(hs[s], hv);
-      const CellJ J = cell_jac(prev, x, r, eps);
+      CellJ J = cell_jac(prev, x, r, eps);
+      if (head) J.f = J.cm = J.ch = J.nm = J.nh = J.al = J.mh = J.inv = J.dn = J.g = 0.f;
       const float F[4] = {J.pc - hv[0], J.pn - hv[1], J.pm - hv[2], J.ph - hv[3]};
       jmv_affine(J, F, a.b);
 #pragma unroll
@@ -659,14 +764,20 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
 #pragma unroll
       for (int k = 0; k < 4; ++k) prev[k] = hv[k];
     };
-    if (n_steps == L) {
+    auto run = [&](auto chk) {
+      if (n_steps == L) {
 #pragma unroll
-      for (int s = 0; s < L; ++s) step(s);
-    } else {
+        for (int s = 0; s < L; ++s) step(s, chk);
+      } else {
 #pragma unroll
-      for (int s = 0; s < L; ++s)
-        if (s < n_steps) step(s);
-    }
+        for (int s = 0; s < L; ++s)
+          if (s < n_steps) step(s, chk);
+      }
+    };
+    if (PK && hd.mask)
+      run(std::true_type{});
+    else
+      run(std::false_type{});
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -744,7 +855,13 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
   {
     const rsrc_t ro = make_rsrc(hout + first * row4 + c0, span * sizeof(TOUT));
     float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
-    auto replay = [&](int s) {
+    auto replay = [&](int s, auto chk) {
+      constexpr bool CHECK = decltype(chk)::value;
+      if (CHECK && hd.at(s)) {
+        if (s > 0) head_prev(s, prev);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) dl[k] = 0.f;
+      }
       float x[4], hv[4];
       XS::get(xs[s], x);
       HS::get(hs[s], hv);
@@ -759,14 +876,20 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
 #pragma unroll
       for (int k = 0; k < 4; ++k) prev[k] = hv[k];
     };
-    if (n_steps == L) {
+    auto run = [&](auto chk) {
+      if (n_steps == L) {
 #pragma unroll
-      for (int s = 0; s < L; ++s) replay(s);
-    } else {
+        for (int s = 0; s < L; ++s) replay(s, chk);
+      } else {
 #pragma unroll
-      for (int s = 0; s < L; ++s)
-        if (s < n_steps) replay(s);
-    }
+        for (int s = 0; s < L; ++s)
+          if (s < n_steps) replay(s, chk);
+      }
+    };
+    if (PK && hd.mask)
+      run(std::true_type{});
+    else
+      run(std::false_type{});
   }
 }
 
@@ -785,14 +908,14 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
 // Both only ever wait on tiles with earlier tickets, so every wave reaches the
 // end.  The arithmetic is that of K separate launches exchanging the fp32
 // iterate through memory.
-template <typename TX, int L, int W, int WPE, bool DET>
+template <typename TX, int L, int W, int WPE, bool DET, bool PK>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) void
 slstm_newton_fused_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
     const TX* __restrict__ guess, TX* __restrict__ out, int B, int T, int d, int n_cb,
     int n_tiles, int K, float omega, float eps, int* __restrict__ counter,
     unsigned long long* __restrict__ agg, unsigned long long* __restrict__ incl,
-    unsigned long long* __restrict__ hlast, int tag_base, Spin spin) {
+    unsigned long long* __restrict__ hlast, int tag_base, Spin spin, Packed pk) {
   // predecessors per wave per look-back round (the deterministic walk, which
   // must find an inclusive carry inside its window, looks twice as far)
   constexpr int KP = DET ? 2 : 1;
@@ -839,6 +962,23 @@ slstm_newton_fused_kernel(
 #pragma unroll
     for (int k = 0; k < 4; ++k) prevg[k] = h0v[k];
   }
+  // Packed sequences: the heads among this wave's steps, and the initial
+  // state of the first one's sequence (later heads of the wave load theirs
+  // when they come).
+  Heads hd{0ull, 0};
+  float hst[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (PK) {
+    hd = find_heads(pk, t0, n_steps);
+    if (hd.mask) head_state(pk, h0, hd.seq(hd.first()), d, c0 + lane, live, hst);
+  }
+  auto head_prev = [&](int s, float p[4]) {
+    if (s == hd.first()) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) p[j] = hst[j];
+    } else {
+      head_state(pk, h0, hd.seq(s), d, c0 + lane, live, p);
+    }
+  };
 
   uint32_t xs[L][XS::N];
   float hf[L][4];
@@ -875,7 +1015,9 @@ slstm_newton_fused_kernel(
       for (int q = 0; q < XS::N; ++q) asm volatile("" : "+v"(xs[s][q]));
     // Linearisation point H^(k-1)_{t0-1}.
     float prev0[4];
-    if (k == 0 || t0 == 0) {
+    if (PK && hd.at(0)) {
+      head_prev(0, prev0);
+    } else if (k == 0 || t0 == 0) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) prev0[j] = prevg[j];
       if (k > 0) {
@@ -917,10 +1059,17 @@ slstm_newton_fused_kernel(
     aff_identity(a);
     {
       float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
-      auto step = [&](int s) {
+      auto step = [&](int s, auto chk) {
+        constexpr bool CHECK = decltype(chk)::value;
+        const bool head = CHECK && hd.at(s);
+        if (head && s > 0) head_prev(s, prev);
         float x[4];
         XS::get(xs[s], x);
-        const CellJ J = cell_jac(prev, x, r, eps);
+        CellJ J = cell_jac(prev, x, r, eps);
+        if (head) {
+          // the scan's map at a head is the constant F: no carry crosses it
+          J.f = J.cm = J.ch = J.nm = J.nh = J.al = J.mh = J.inv = J.dn = J.g = 0.f;
+        }
         const float F[4] = {J.pc - hf[s][0], J.pn - hf[s][1], J.pm - hf[s][2],
                             J.ph - hf[s][3]};
         jmv_affine(J, F, a.b);
@@ -934,14 +1083,20 @@ slstm_newton_fused_kernel(
 #pragma unroll
         for (int j = 0; j < 4; ++j) prev[j] = hf[s][j];
       };
-      if (n_steps == L) {
+      auto run = [&](auto chk) {
+        if (n_steps == L) {
 #pragma unroll
-        for (int s = 0; s < L; ++s) step(s);
-      } else {
+          for (int s = 0; s < L; ++s) step(s, chk);
+        } else {
 #pragma unroll
-        for (int s = 0; s < L; ++s)
-          if (s < n_steps) step(s);
-      }
+          for (int s = 0; s < L; ++s)
+            if (s < n_steps) step(s, chk);
+        }
+      };
+      if (PK && hd.mask)
+        run(std::true_type{});
+      else
+        run(std::false_type{});
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -1025,7 +1180,14 @@ slstm_newton_fused_kernel(
     for (int j = 0; j < 4; ++j) dl[j] = s_carry[wave][j][lane];
     {
       float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
-      auto replay = [&](int s) {
+      auto replay = [&](int s, auto chk) {
+        constexpr bool CHECK = decltype(chk)::value;
+        if (CHECK && hd.at(s)) {
+          // a head: previous state h0 of its sequence, no incoming delta
+          if (s > 0) head_prev(s, prev);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dl[j] = 0.f;
+        }
         float x[4], hv[4];
         XS::get(xs[s], x);
 #pragma unroll
@@ -1047,14 +1209,20 @@ slstm_newton_fused_kernel(
           for (int j = 0; j < 4; ++j) hf[s][j] = hl[j];
         }
       };
-      if (n_steps == L) {
+      auto run = [&](auto chk) {
+        if (n_steps == L) {
 #pragma unroll
-        for (int s = 0; s < L; ++s) replay(s);
-      } else {
+          for (int s = 0; s < L; ++s) replay(s, chk);
+        } else {
 #pragma unroll
-        for (int s = 0; s < L; ++s)
-          if (s < n_steps) replay(s);
-      }
+          for (int s = 0; s < L; ++s)
+            if (s < n_steps) replay(s, chk);
+        }
+      };
+      if (PK && hd.mask)
+        run(std::true_type{});
+      else
+        run(std::false_type{});
     }
     if constexpr (!last_iter) {
 #pragma unroll
@@ -1166,22 +1334,28 @@ struct InitWs {
   bool fused;
 };
 
-static InitWs carve_init(void* base, int B, int T, int d, int P, int dtype, size_t* total) {
+static InitWs carve_init(void* base, int B, int T, int d, int P, int dtype, size_t* total,
+                         bool packed = false) {
   Carver cv(base);
   InitWs w;
-  w.fused = picard_fused(dtype);
+  // packed bf16 streams always take the single-launch warm start
+  w.fused = packed ? dtype == PRNN_BF16 : picard_fused(dtype);
   w.hbuf[0] = w.hbuf[1] = nullptr;
   w.hlast = nullptr;
   if (w.fused) {
     // Stage-indexed look-back words (a tile may run stages ahead of the
     // tiles that still read its earlier stages), cleared with the counters.
-    const Geo g = geometry(B, T, d, picard_shape());
+    Geo g = geometry(B, T, d, picard_shape());
+    const Geo gd = geometry(B, T, d, kPicardDefault);
+    if (gd.n_tiles > g.n_tiles) g = gd;
     w.lb = carve_lookback(cv, g, 3 * (P + 1), 4 * (P + 1));
     w.hlast = static_cast<unsigned long long*>(
         cv.take(sizeof(unsigned long long) * static_cast<size_t>(P) * kCB * g.n_tiles));
     w.lb.clear_words = (cv.used - (reinterpret_cast<char*>(w.lb.counters) - cv.base)) / sizeof(int);
   } else {
-    const Geo g = geometry(B, T, d, frozen_shape(dtype));
+    Geo g = geometry(B, T, d, frozen_shape(dtype));
+    const Geo gd = geometry(B, T, d, dtype == PRNN_BF16 ? kFrozenDefault : kFrozenF32);
+    if (gd.n_tiles > g.n_tiles) g = gd;
     w.lb = carve_lookback(cv, g, 3, 4);
     const size_t hb = static_cast<size_t>(B) * T * d * elem_size(dtype);
     w.hbuf[0] = P >= 1 ? cv.take(hb) : nullptr;
@@ -1232,10 +1406,12 @@ struct NewtonWs {
   bool fused;
 };
 
-static NewtonWs carve_newton(void* base, int B, int T, int d, int K, int dtype, size_t* total) {
+static NewtonWs carve_newton(void* base, int B, int T, int d, int K, int dtype, size_t* total,
+                             bool packed = false) {
   Carver cv(base);
   NewtonWs w;
-  w.fused = newton_fused(K);
+  // packed streams always take the single-launch path for K >= 2
+  w.fused = packed ? K >= 2 : newton_fused(K);
   w.work[0] = w.work[1] = nullptr;
   w.hlast = nullptr;
   if (w.fused) {
@@ -1250,10 +1426,14 @@ static NewtonWs carve_newton(void* base, int B, int T, int d, int K, int dtype, 
     return w;
   }
   // Launches of one call share the look-back arrays: size them for the
-  // larger tile count of the two shapes.
+  // largest tile count of the shapes a launch may take.
   const Geo g1 = geometry(B, T, d, newton_shape(dtype, false));
   const Geo g2 = geometry(B, T, d, newton_shape(dtype, true));
-  const Geo& g = g1.n_tiles >= g2.n_tiles ? g1 : g2;
+  const Geo g3 = geometry(B, T, d, dtype == PRNN_BF16 ? kNewtonGuessDefault : kNewtonF32);
+  const Geo g4 = geometry(B, T, d, dtype == PRNN_BF16 ? kNewtonWorkDefault : kNewtonF32);
+  Geo g = g1.n_tiles >= g2.n_tiles ? g1 : g2;
+  if (g3.n_tiles > g.n_tiles) g = g3;
+  if (g4.n_tiles > g.n_tiles) g = g4;
   w.lb = carve_lookback(cv, g, 4, 20);
   const size_t wb = static_cast<size_t>(B) * T * 4 * d * sizeof(float);
   w.work[0] = K >= 2 ? static_cast<float*>(cv.take(wb)) : nullptr;
@@ -1262,17 +1442,18 @@ static NewtonWs carve_newton(void* base, int B, int T, int d, int K, int dtype, 
   return w;
 }
 
-template <typename TX, int L, int W, bool DET>
+template <typename TX, int L, int W, bool DET, bool PK = false>
 static void launch_frozen(bool has_h, bool full_out, const TX* wx, const TX* r, const TX* h0,
                           const TX* src, TX* out_full, TX* out_h, int B, int T, int d, float eps,
-                          const Lookback& lb, int epoch, hipStream_t stream) {
+                          const Lookback& lb, int epoch, hipStream_t stream,
+                          const Packed& pk = Packed{nullptr, nullptr, 0}) {
   const Geo g = geometry(B, T, d, Shape{L, W});
   const dim3 grid(g.n_tiles), block(64 * W);
   int* ctr = lb.counters + epoch;
 #define PRNN_FROZEN(HH, FO)                                                                    \
-  slstm_frozen_kernel<TX, L, W, HH, FO, DET><<<grid, block, 0, stream>>>(                      \
+  slstm_frozen_kernel<TX, L, W, HH, FO, DET, PK><<<grid, block, 0, stream>>>(                  \
       wx, r, h0, src, out_full, out_h, B, T, d, g.n_cb, eps, ctr, lb.agg, lb.incl,             \
-      lb.tag_base + epoch, lb.spin())
+      lb.tag_base + epoch, lb.spin(), pk)
   if (has_h) {
     if (full_out) PRNN_FROZEN(true, true); else PRNN_FROZEN(true, false);
   } else {
@@ -1284,11 +1465,19 @@ static void launch_frozen(bool has_h, bool full_out, const TX* wx, const TX* r, 
 template <typename TX>
 static void frozen_pass(bool has_h, bool full_out, const TX* wx, const TX* r, const TX* h0,
                         const TX* src, TX* out_full, TX* out_h, int B, int T, int d, float eps,
-                        const Lookback& lb, int epoch, hipStream_t stream) {
+                        const Lookback& lb, int epoch, hipStream_t stream, const Packed& pk) {
 #define PRNN_LAUNCH(LL, WW, DD)                                                              \
   return launch_frozen<TX, LL, WW, DD>(has_h, full_out, wx, r, h0, src, out_full, out_h, B, T, \
                                        d, eps, lb, epoch, stream)
   if constexpr (sizeof(TX) == 4) {
+    // packed streams: fp32 only (bf16 takes the single-launch warm start)
+    if (pk.cu != nullptr) {
+      if (deterministic())
+        return launch_frozen<TX, kFrozenF32.L, kFrozenF32.W, true, true>(
+            has_h, full_out, wx, r, h0, src, out_full, out_h, B, T, d, eps, lb, epoch, stream, pk);
+      return launch_frozen<TX, kFrozenF32.L, kFrozenF32.W, false, true>(
+          has_h, full_out, wx, r, h0, src, out_full, out_h, B, T, d, eps, lb, epoch, stream, pk);
+    }
     if (deterministic()) PRNN_LAUNCH(kFrozenF32.L, kFrozenF32.W, true);
     PRNN_LAUNCH(kFrozenF32.L, kFrozenF32.W, false);
   } else {
@@ -1307,28 +1496,35 @@ static void frozen_pass(bool has_h, bool full_out, const TX* wx, const TX* r, co
 
 template <typename TX>
 static int run_init(const TX* wx, const TX* r, const TX* h0, TX* states, int B, int T, int d,
-                    int P, float eps, const InitWs& w, hipStream_t stream) {
+                    int P, float eps, const InitWs& w, hipStream_t stream, const Packed& pk) {
   int rc = clear_status(w.lb, stream);
   if (rc != PRNN_OK) return rc;
   if constexpr (sizeof(TX) == 2) {
     if (w.fused) {
-      const Shape sh = picard_shape();
+      const Shape sh = pk.cu != nullptr ? kPicardDefault : picard_shape();
       const Geo g = geometry(B, T, d, sh);
-#define PRNN_LAUNCH(LL, WW, WPE, DD)                                                            \
-  slstm_picard_fused_kernel<LL, WW, WPE, DD><<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>(    \
-      wx, r, h0, states, B, T, d, g.n_cb, g.n_tiles, P, eps, w.lb.counters + 1, w.lb.agg,       \
-      w.lb.incl, w.hlast, w.lb.tag_base, w.lb.spin())
+#define PRNN_LAUNCH_P(LL, WW, WPE, DD, PP)                                                       \
+  slstm_picard_fused_kernel<LL, WW, WPE, DD, PP>                                                 \
+      <<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>(                                           \
+          wx, r, h0, states, B, T, d, g.n_cb, g.n_tiles, P, eps, w.lb.counters + 1, w.lb.agg,   \
+          w.lb.incl, w.hlast, w.lb.tag_base, w.lb.spin(), pk)
+#define PRNN_LAUNCH(LL, WW, WPE, DD) PRNN_LAUNCH_P(LL, WW, WPE, DD, false)
 #define PRNN_SHAPE(LL, WW, WPE) \
   else if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, WPE, false);
       static_assert(kPicardDefault.L == 24 && kPicardDefault.W == 4, "default Picard shape");
       timing_begin(stream);
-      if (deterministic()) PRNN_LAUNCH(24, 4, 3, true);
+      if (pk.cu != nullptr) {
+        if (deterministic()) PRNN_LAUNCH_P(24, 4, 3, true, true);
+        else PRNN_LAUNCH_P(24, 4, 3, false, true);
+      }
+      else if (deterministic()) PRNN_LAUNCH(24, 4, 3, true);
       PRNN_SHAPE(24, 4, 3)
       PRNN_SHAPE(16, 4, 4)
       PRNN_SHAPE(20, 4, 3)
       PRNN_SHAPE(32, 4, 2)
 #undef PRNN_SHAPE
 #undef PRNN_LAUNCH
+#undef PRNN_LAUNCH_P
       timing_end(stream);
       PRNN_HIP(hipGetLastError());
       return PRNN_OK;
@@ -1341,7 +1537,7 @@ static int run_init(const TX* wx, const TX* r, const TX* h0, TX* states, int B, 
     const bool last = p == P;
     TX* out_h = last ? nullptr : static_cast<TX*>(w.hbuf[p & 1]);
     frozen_pass<TX>(p > 0, last, wx, r, h0, src, last ? states : nullptr, out_h, B, T, d, eps,
-                    w.lb, p + 1, stream);
+                    w.lb, p + 1, stream, pk);
     PRNN_HIP(hipGetLastError());
   }
   timing_end(stream);
@@ -1353,9 +1549,10 @@ static void launch_newton_shape(const TX* wx, const TX* r, const TX* h0, const T
                                 TOUT* hout, int B, int T, int d, float omega, float eps,
                                 const Lookback& lb, int epoch, hipStream_t stream) {
   const Geo g = geometry(B, T, d, Shape{L, W});
-  slstm_newton_kernel<TX, TIN, TOUT, L, W, DET><<<dim3(g.n_tiles), dim3(64 * W), 0, stream>>>(
-      wx, r, h0, hin, hout, B, T, d, g.n_cb, omega, eps, lb.counters + epoch, lb.agg,
-      lb.incl, lb.tag_base + epoch, lb.spin());
+  slstm_newton_kernel<TX, TIN, TOUT, L, W, DET, false>
+      <<<dim3(g.n_tiles), dim3(64 * W), 0, stream>>>(
+          wx, r, h0, hin, hout, B, T, d, g.n_cb, omega, eps, lb.counters + epoch, lb.agg,
+          lb.incl, lb.tag_base + epoch, lb.spin(), Packed{nullptr, nullptr, 0});
 }
 
 template <typename TX, typename TIN, typename TOUT>
@@ -1386,10 +1583,31 @@ static void launch_newton(const TX* wx, const TX* r, const TX* h0, const TIN* hi
 #undef PRNN_LAUNCH
 }
 
+// One Newton iteration on a packed stream (B = 1): default tile shapes.
+template <typename TX, typename TIN, typename TOUT>
+static void launch_newton_packed(const TX* wx, const TX* r, const TX* h0, const TIN* hin,
+                                 TOUT* hout, int T, int d, float omega, float eps,
+                                 const Lookback& lb, int epoch, hipStream_t stream,
+                                 const Packed& pk) {
+  constexpr Shape sh = sizeof(TX) == 4 ? kNewtonF32
+                       : sizeof(TIN) == 4 ? kNewtonWorkDefault : kNewtonGuessDefault;
+  const Geo g = geometry(1, T, d, sh);
+#define PRNN_LAUNCH(DD)                                                                     \
+  slstm_newton_kernel<TX, TIN, TOUT, sh.L, sh.W, DD, true>                                  \
+      <<<dim3(g.n_tiles), dim3(64 * sh.W), 0, stream>>>(                                    \
+          wx, r, h0, hin, hout, 1, T, d, g.n_cb, omega, eps, lb.counters + epoch, lb.agg, \
+          lb.incl, lb.tag_base + epoch, lb.spin(), pk)
+  if (deterministic())
+    PRNN_LAUNCH(true);
+  else
+    PRNN_LAUNCH(false);
+#undef PRNN_LAUNCH
+}
+
 template <typename TX>
 static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, TX* out, int B,
                       int T, int d, int K, float omega, float eps, const NewtonWs& w,
-                      hipStream_t stream) {
+                      hipStream_t stream, const Packed& pk) {
   int rc = clear_status(w.lb, stream);
   if (rc != PRNN_OK) return rc;
   if (K == 0) {
@@ -1400,16 +1618,27 @@ static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, 
   if (w.fused) {
     const Shape sh = newton_fused_shape(sizeof(TX) == 2 ? PRNN_BF16 : PRNN_F32);
     const Geo g = geometry(B, T, d, sh);
-#define PRNN_LAUNCH(LL, WW, WPE, DD)                                                             \
-  slstm_newton_fused_kernel<TX, LL, WW, WPE, DD><<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>( \
-      wx, r, h0, guess, out, B, T, d, g.n_cb, g.n_tiles, K, omega, eps, w.lb.counters + 1,       \
-      w.lb.agg, w.lb.incl, w.hlast, w.lb.tag_base, w.lb.spin())
+#define PRNN_LAUNCH_P(LL, WW, WPE, DD, PP)                                                       \
+  slstm_newton_fused_kernel<TX, LL, WW, WPE, DD, PP>                                             \
+      <<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>(                                           \
+          wx, r, h0, guess, out, B, T, d, g.n_cb, g.n_tiles, K, omega, eps, w.lb.counters + 1,   \
+          w.lb.agg, w.lb.incl, w.hlast, w.lb.tag_base, w.lb.spin(), pk)
+#define PRNN_LAUNCH(LL, WW, WPE, DD) PRNN_LAUNCH_P(LL, WW, WPE, DD, false)
 #define PRNN_SHAPE(LL, WW, WPE) \
   else if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, WPE, false);
     static_assert(kNewtonFusedF32.L == 16 && kNewtonFusedF32.W == 4, "fp32 fused shape");
     static_assert(kNewtonFusedDefault.L == 20 && kNewtonFusedDefault.W == 4, "default shape");
     timing_begin(stream);
-    if constexpr (sizeof(TX) == 4) {
+    if (pk.cu != nullptr) {
+      // packed sequences: default shapes only
+      if constexpr (sizeof(TX) == 4) {
+        if (deterministic()) PRNN_LAUNCH_P(16, 4, 2, true, true);
+        else PRNN_LAUNCH_P(16, 4, 2, false, true);
+      } else {
+        if (deterministic()) PRNN_LAUNCH_P(20, 4, 2, true, true);
+        else PRNN_LAUNCH_P(20, 4, 2, false, true);
+      }
+    } else if constexpr (sizeof(TX) == 4) {
       if (deterministic()) PRNN_LAUNCH(16, 4, 2, true);
       PRNN_SHAPE(16, 4, 2)
     } else {
@@ -1421,11 +1650,20 @@ static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, 
     }
 #undef PRNN_SHAPE
 #undef PRNN_LAUNCH
+#undef PRNN_LAUNCH_P
     timing_end(stream);
     PRNN_HIP(hipGetLastError());
     return PRNN_OK;
   }
   timing_begin(stream);
+  if (pk.cu != nullptr) {
+    // K = 1 on a packed stream
+    launch_newton_packed<TX, TX, TX>(wx, r, h0, guess, out, T, d, omega, eps, w.lb, 1, stream,
+                                     pk);
+    timing_end(stream);
+    PRNN_HIP(hipGetLastError());
+    return PRNN_OK;
+  }
   for (int k = 1; k <= K; ++k) {
     const bool first = k == 1, last = k == K;
     const float* win = first ? nullptr : w.work[(k - 2) & 1];
@@ -1457,13 +1695,22 @@ extern "C" PRNN_API size_t prnn_slstm_init_workspace_size(int B, int T, int d, i
   return total;
 }
 
-extern "C" PRNN_API int prnn_slstm_init_ex(const void* wx, const void* r, const void* h0,
-                                           void* states, int B, int T, int d, int picard_iters,
-                                           float eps, int dtype, void* workspace,
-                                           size_t workspace_bytes, int tag_base, void* stream) {
+namespace {
+
+int check_packed(const slstm::Packed& pk) {
+  if (pk.cu == nullptr) return PRNN_OK;
+  if (pk.n_seq < 1) return fail(PRNN_ERR_VALUE, "n_seq must be >= 1, got %d", pk.n_seq);
+  return PRNN_OK;
+}
+
+int init_call(const void* wx, const void* r, const void* h0, void* states, int B, int T, int d,
+              int picard_iters, float eps, int dtype, void* workspace, size_t workspace_bytes,
+              int tag_base, void* stream, const slstm::Packed& pk) {
   int rc = slstm::check_dims(B, T, d, dtype);
   if (rc != PRNN_OK) return rc;
   rc = slstm::check_tag_base(tag_base);
+  if (rc != PRNN_OK) return rc;
+  rc = check_packed(pk);
   if (rc != PRNN_OK) return rc;
   if (picard_iters < 0 || picard_iters > slstm::kMaxStages - 2)
     return fail(PRNN_ERR_VALUE, "picard_iters must be in [0, %d], got %d",
@@ -1471,7 +1718,8 @@ extern "C" PRNN_API int prnn_slstm_init_ex(const void* wx, const void* r, const 
   if (!wx || !r || !states || !workspace)
     return fail(PRNN_ERR_VALUE, "wx, r, states and workspace must be non-null");
   size_t need = 0;
-  slstm::InitWs w = slstm::carve_init(workspace, B, T, d, picard_iters, dtype, &need);
+  slstm::InitWs w = slstm::carve_init(workspace, B, T, d, picard_iters, dtype, &need,
+                                      pk.cu != nullptr);
   if (workspace_bytes < need)
     return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
   w.lb.tag_base = tag_base;
@@ -1479,10 +1727,54 @@ extern "C" PRNN_API int prnn_slstm_init_ex(const void* wx, const void* r, const 
   if (dtype == PRNN_F32)
     return slstm::run_init(static_cast<const float*>(wx), static_cast<const float*>(r),
                            static_cast<const float*>(h0), static_cast<float*>(states), B, T, d,
-                           picard_iters, eps, w, s);
+                           picard_iters, eps, w, s, pk);
   return slstm::run_init(static_cast<const bf16*>(wx), static_cast<const bf16*>(r),
                          static_cast<const bf16*>(h0), static_cast<bf16*>(states), B, T, d,
-                         picard_iters, eps, w, s);
+                         picard_iters, eps, w, s, pk);
+}
+
+int newton_call(const void* wx, const void* r, const void* h0, const void* states, void* out,
+                int B, int T, int d, int max_iters, float omega, float eps, int dtype,
+                void* workspace, size_t workspace_bytes, int tag_base, void* stream,
+                const slstm::Packed& pk) {
+  int rc = slstm::check_dims(B, T, d, dtype);
+  if (rc != PRNN_OK) return rc;
+  rc = slstm::check_tag_base(tag_base);
+  if (rc != PRNN_OK) return rc;
+  rc = check_packed(pk);
+  if (rc != PRNN_OK) return rc;
+  if (max_iters < 0 || max_iters > slstm::kMaxStages - 1)
+    return fail(PRNN_ERR_VALUE, "max_iters must be in [0, %d], got %d", slstm::kMaxStages - 1,
+                max_iters);
+  if (!wx || !r || !states || !out || !workspace)
+    return fail(PRNN_ERR_VALUE, "wx, r, states, out and workspace must be non-null");
+  if (out == states) return fail(PRNN_ERR_VALUE, "out must not alias states");
+  size_t need = 0;
+  slstm::NewtonWs w = slstm::carve_newton(workspace, B, T, d, max_iters, dtype, &need,
+                                          pk.cu != nullptr);
+  if (workspace_bytes < need)
+    return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  w.lb.tag_base = tag_base;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == PRNN_F32)
+    return slstm::run_newton(static_cast<const float*>(wx), static_cast<const float*>(r),
+                             static_cast<const float*>(h0), static_cast<const float*>(states),
+                             static_cast<float*>(out), B, T, d, max_iters, omega, eps, w, s, pk);
+  return slstm::run_newton(static_cast<const bf16*>(wx), static_cast<const bf16*>(r),
+                           static_cast<const bf16*>(h0), static_cast<const bf16*>(states),
+                           static_cast<bf16*>(out), B, T, d, max_iters, omega, eps, w, s, pk);
+}
+
+const slstm::Packed kRect{nullptr, nullptr, 0};
+
+}  // namespace
+
+extern "C" PRNN_API int prnn_slstm_init_ex(const void* wx, const void* r, const void* h0,
+                                           void* states, int B, int T, int d, int picard_iters,
+                                           float eps, int dtype, void* workspace,
+                                           size_t workspace_bytes, int tag_base, void* stream) {
+  return init_call(wx, r, h0, states, B, T, d, picard_iters, eps, dtype, workspace,
+                   workspace_bytes, tag_base, stream, kRect);
 }
 
 extern "C" PRNN_API int prnn_slstm_init(const void* wx, const void* r, const void* h0,
@@ -1506,29 +1798,49 @@ extern "C" PRNN_API int prnn_slstm_newton_ex(const void* wx, const void* r, cons
                                              int max_iters, float omega, float eps, int dtype,
                                              void* workspace, size_t workspace_bytes,
                                              int tag_base, void* stream) {
-  int rc = slstm::check_dims(B, T, d, dtype);
-  if (rc != PRNN_OK) return rc;
-  rc = slstm::check_tag_base(tag_base);
-  if (rc != PRNN_OK) return rc;
-  if (max_iters < 0 || max_iters > slstm::kMaxStages - 1)
-    return fail(PRNN_ERR_VALUE, "max_iters must be in [0, %d], got %d", slstm::kMaxStages - 1,
-                max_iters);
-  if (!wx || !r || !states || !out || !workspace)
-    return fail(PRNN_ERR_VALUE, "wx, r, states, out and workspace must be non-null");
-  if (out == states) return fail(PRNN_ERR_VALUE, "out must not alias states");
-  size_t need = 0;
-  slstm::NewtonWs w = slstm::carve_newton(workspace, B, T, d, max_iters, dtype, &need);
-  if (workspace_bytes < need)
-    return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
-  w.lb.tag_base = tag_base;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == PRNN_F32)
-    return slstm::run_newton(static_cast<const float*>(wx), static_cast<const float*>(r),
-                             static_cast<const float*>(h0), static_cast<const float*>(states),
-                             static_cast<float*>(out), B, T, d, max_iters, omega, eps, w, s);
-  return slstm::run_newton(static_cast<const bf16*>(wx), static_cast<const bf16*>(r),
-                           static_cast<const bf16*>(h0), static_cast<const bf16*>(states),
-                           static_cast<bf16*>(out), B, T, d, max_iters, omega, eps, w, s);
+  return newton_call(wx, r, h0, states, out, B, T, d, max_iters, omega, eps, dtype, workspace,
+                     workspace_bytes, tag_base, stream, kRect);
+}
+
+extern "C" PRNN_API size_t prnn_slstm_init_packed_workspace_size(int T, int d, int picard_iters,
+                                                                 int dtype) {
+  if (slstm::check_dims(1, T, d, dtype) != PRNN_OK || picard_iters < 0) return 0;
+  size_t total = 0;
+  slstm::carve_init(nullptr, 1, T, d, picard_iters, dtype, &total, true);
+  return total;
+}
+
+extern "C" PRNN_API int prnn_slstm_init_packed(const void* wx, const void* r, const void* h0,
+                                               void* states, int T, int d, int picard_iters,
+                                               float eps, int dtype, const int* cu_seqlens,
+                                               int n_seq, const int* block_table,
+                                               void* workspace, size_t workspace_bytes,
+                                               int tag_base, void* stream) {
+  if (!cu_seqlens) return fail(PRNN_ERR_VALUE, "cu_seqlens must be non-null");
+  return init_call(wx, r, h0, states, 1, T, d, picard_iters, eps, dtype, workspace,
+                   workspace_bytes, tag_base, stream,
+                   slstm::Packed{cu_seqlens, block_table, n_seq});
+}
+
+extern "C" PRNN_API size_t prnn_slstm_newton_packed_workspace_size(int T, int d, int max_iters,
+                                                                   int dtype) {
+  if (slstm::check_dims(1, T, d, dtype) != PRNN_OK || max_iters < 0) return 0;
+  size_t total = 0;
+  slstm::carve_newton(nullptr, 1, T, d, max_iters, dtype, &total, true);
+  return total;
+}
+
+extern "C" PRNN_API int prnn_slstm_newton_packed(const void* wx, const void* r, const void* h0,
+                                                 const void* states, void* out, int T, int d,
+                                                 int max_iters, float omega, float eps,
+                                                 int dtype, const int* cu_seqlens, int n_seq,
+                                                 const int* block_table, void* workspace,
+                                                 size_t workspace_bytes, int tag_base,
+                                                 void* stream) {
+  if (!cu_seqlens) return fail(PRNN_ERR_VALUE, "cu_seqlens must be non-null");
+  return newton_call(wx, r, h0, states, out, 1, T, d, max_iters, omega, eps, dtype, workspace,
+                     workspace_bytes, tag_base, stream,
+                     slstm::Packed{cu_seqlens, block_table, n_seq});
 }
 
 extern "C" PRNN_API int prnn_slstm_newton(const void* wx, const void* r, const void* h0,
@@ -1539,44 +1851,79 @@ extern "C" PRNN_API int prnn_slstm_newton(const void* wx, const void* r, const v
                               workspace, workspace_bytes, 0, stream);
 }
 
-extern "C" PRNN_API int prnn_slstm_newton_step(const void* wx, const void* r, const void* h0,
-                                               const void* in, int in_f32, float* out, int B,
-                                               int T, int d, float omega, float eps, int dtype,
-                                               void* workspace, size_t workspace_bytes,
-                                               int tag_base, void* stream) {
+namespace {
+
+int step_call(const void* wx, const void* r, const void* h0, const void* in, int in_f32,
+              float* out, int B, int T, int d, float omega, float eps, int dtype,
+              void* workspace, size_t workspace_bytes, int tag_base, void* stream,
+              const slstm::Packed& pk) {
   int rc = slstm::check_dims(B, T, d, dtype);
   if (rc != PRNN_OK) return rc;
   rc = slstm::check_tag_base(tag_base);
+  if (rc != PRNN_OK) return rc;
+  rc = check_packed(pk);
   if (rc != PRNN_OK) return rc;
   if (!wx || !r || !in || !out || !workspace)
     return fail(PRNN_ERR_VALUE, "wx, r, in, out and workspace must be non-null");
   if (static_cast<const void*>(out) == in) return fail(PRNN_ERR_VALUE, "out must not alias in");
   size_t need = 0;
-  slstm::NewtonWs w = slstm::carve_newton(workspace, B, T, d, 1, dtype, &need);
+  slstm::NewtonWs w = slstm::carve_newton(workspace, B, T, d, 1, dtype, &need, pk.cu != nullptr);
   if (workspace_bytes < need)
     return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
   w.lb.tag_base = tag_base;
   hipStream_t s = static_cast<hipStream_t>(stream);
   rc = slstm::clear_status(w.lb, s);
   if (rc != PRNN_OK) return rc;
+  const bool packed = pk.cu != nullptr;
   timing_begin(s);
-  if (dtype == PRNN_F32) {
-    slstm::launch_newton<float, float, float>(
-        static_cast<const float*>(wx), static_cast<const float*>(r),
-        static_cast<const float*>(h0), static_cast<const float*>(in), out, B, T, d, omega, eps,
-        w.lb, 1, s);
-  } else if (in_f32) {
-    slstm::launch_newton<bf16, float, float>(
-        static_cast<const bf16*>(wx), static_cast<const bf16*>(r), static_cast<const bf16*>(h0),
-        static_cast<const float*>(in), out, B, T, d, omega, eps, w.lb, 1, s);
-  } else {
-    slstm::launch_newton<bf16, bf16, float>(
-        static_cast<const bf16*>(wx), static_cast<const bf16*>(r), static_cast<const bf16*>(h0),
-        static_cast<const bf16*>(in), out, B, T, d, omega, eps, w.lb, 1, s);
-  }
+#define PRNN_STEP(TX, TIN)                                                                   \
+  do {                                                                                       \
+    const TX* wx_ = static_cast<const TX*>(wx);                                              \
+    const TX* r_ = static_cast<const TX*>(r);                                                \
+    const TX* h0_ = static_cast<const TX*>(h0);                                              \
+    const TIN* in_ = static_cast<const TIN*>(in);                                            \
+    if (packed)                                                                              \
+      slstm::launch_newton_packed<TX, TIN, float>(wx_, r_, h0_, in_, out, T, d, omega, eps, \
+                                                  w.lb, 1, s, pk);                           \
+    else                                                                                     \
+      slstm::launch_newton<TX, TIN, float>(wx_, r_, h0_, in_, out, B, T, d, omega, eps,     \
+                                           w.lb, 1, s);                                      \
+  } while (0)
+  if (dtype == PRNN_F32)
+    PRNN_STEP(float, float);
+  else if (in_f32)
+    PRNN_STEP(bf16, float);
+  else
+    PRNN_STEP(bf16, bf16);
+#undef PRNN_STEP
   timing_end(s);
   PRNN_HIP(hipGetLastError());
   return PRNN_OK;
+}
+
+}  // namespace
+
+extern "C" PRNN_API int prnn_slstm_newton_step(const void* wx, const void* r, const void* h0,
+                                               const void* in, int in_f32, float* out, int B,
+                                               int T, int d, float omega, float eps, int dtype,
+                                               void* workspace, size_t workspace_bytes,
+                                               int tag_base, void* stream) {
+  return step_call(wx, r, h0, in, in_f32, out, B, T, d, omega, eps, dtype, workspace,
+                   workspace_bytes, tag_base, stream, kRect);
+}
+
+extern "C" PRNN_API int prnn_slstm_newton_step_packed(const void* wx, const void* r,
+                                                      const void* h0, const void* in, int in_f32,
+                                                      float* out, int T, int d, float omega,
+                                                      float eps, int dtype,
+                                                      const int* cu_seqlens, int n_seq,
+                                                      const int* block_table, void* workspace,
+                                                      size_t workspace_bytes, int tag_base,
+                                                      void* stream) {
+  if (!cu_seqlens) return fail(PRNN_ERR_VALUE, "cu_seqlens must be non-null");
+  return step_call(wx, r, h0, in, in_f32, out, 1, T, d, omega, eps, dtype, workspace,
+                   workspace_bytes, tag_base, stream,
+                   slstm::Packed{cu_seqlens, block_table, n_seq});
 }
 
 extern "C" PRNN_API int prnn_slstm_lookback_status(const void* workspace, int* status,

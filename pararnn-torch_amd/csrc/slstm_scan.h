@@ -47,6 +47,72 @@ __device__ __forceinline__ int take_ticket(int* counter) {
 
 
 // ---------------------------------------------------------------------------
+// Packed sequences (cu_seqlens).
+//
+// With cu != nullptr a kernel sees one stream (B = 1) of T steps holding S
+// sequences, sequence q on steps [cu[q], cu[q+1]) (cu[0] = 0, cu[S] = T).  The
+// first step of a sequence is a head: its previous state is the sequence's
+// initial state -- row tbl[q] (or q without a table) of h0, zeros without h0
+// -- and no carry crosses it (the scan's map there is constant: J = 0).  A
+// wave learns once, with scalar loads, which of its steps are heads (a
+// wave-uniform bit mask) and which sequence its first step belongs to.
+// ---------------------------------------------------------------------------
+struct Packed {
+  const int* cu;   // S + 1 offsets, or nullptr for a rectangular batch
+  const int* tbl;  // S rows of h0, or nullptr (row q)
+  int n_seq;
+};
+
+struct Heads {
+  uint64_t mask;  // bit s: step t0 + s is a head
+  int seq0;       // sequence of step t0
+  __device__ __forceinline__ bool at(int s) const { return (mask >> s) & 1ull; }
+  // sequence of step t0 + s
+  __device__ __forceinline__ int seq(int s) const {
+    const uint64_t upto = s >= 63 ? ~0ull : ((2ull << s) - 1ull);
+    return seq0 + __builtin_popcountll(mask & upto) - static_cast<int>(mask & 1ull);
+  }
+  __device__ __forceinline__ int first() const { return __builtin_ctzll(mask); }
+};
+
+// Heads among steps [t0, t0 + n), n <= 64 (wave-uniform arguments).
+__device__ __forceinline__ Heads find_heads(const Packed& pk, int t0, int n) {
+  Heads h{0ull, 0};
+  if (n <= 0) return h;
+  // cu[lo] <= t0 < cu[hi]
+  int lo = 0, hi = pk.n_seq;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (pk.cu[mid] <= t0)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  h.seq0 = lo;
+  if (pk.cu[lo] == t0) h.mask |= 1ull;
+  for (int q = hi; q < pk.n_seq; ++q) {
+    const int t = pk.cu[q];
+    if (t >= t0 + n) break;
+    h.mask |= 1ull << (t - t0);
+  }
+  return h;
+}
+
+// The 4 slots (c, n, m, h) of sequence q's initial state for this lane's
+// channel (zeros without h0 or on dead lanes).
+template <typename TX>
+__device__ __forceinline__ void head_state(const Packed& pk, const TX* h0, int q, int d, int ch,
+                                           bool live, float st[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) st[k] = 0.f;
+  if (h0 == nullptr || !live) return;
+  const int row = pk.tbl != nullptr ? pk.tbl[q] : q;
+  const TX* p = h0 + static_cast<size_t>(row) * 4 * d + ch;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) st[k] = ld(p + k * d);
+}
+
+// ---------------------------------------------------------------------------
 // Windowed decoupled look-back.
 //
 // Called by every wave of a tile with chunk > 0 (it contains barriers).  Each

@@ -24,6 +24,7 @@ from __future__ import annotations
 import contextlib
 import logging
 import math
+import os
 from collections.abc import Iterator
 from dataclasses import replace
 
@@ -169,22 +170,27 @@ def fused_newton(
             wx, a_z, a_r, a_n, h0, cu_seqlens, max_iters=max_iters, omega=omega
         )
     if isinstance(cell, ParaSLSTM) and cell.mix == "diag":
-        if block_table is not None:
-            # paged h0 rows (one per sequence when packed), for the guess and
-            # the iterations alike
-            rows = wx.shape[0] if cu_seqlens is None else int(cu_seqlens.numel()) - 1
-            h0 = gather_h0(h0, block_table, rows, (4, int(cell.d_h)))
-        if cu_seqlens is not None:
-            # packed sequences as a padded batch, each from its own h0
+        if cu_seqlens is not None and not packed_in_kernel():
+            # packed sequences as padded length groups, each from its own h0
+            if block_table is not None:
+                h0 = gather_h0(h0, block_table, int(cu_seqlens.numel()) - 1,
+                               (4, int(cell.d_h)))
             plan = RaggedPlan(validate_cu_seqlens(cu_seqlens, wx.shape[1]), wx.device)
             return plan.run(wx, h0, lambda w, h: fused_newton(
                 cell, w, max_iters=max_iters, omega=omega, h0=h,
                 log_coords=log_coords, picard_iters=picard_iters, scan_tile=scan_tile,
                 fused_time_loop=fused_time_loop, fused_window_len=fused_window_len))
+        if block_table is not None and cu_seqlens is None:
+            # paged h0 of a rectangular batch: the B rows the table names
+            h0 = gather_h0(h0, block_table, wx.shape[0], (4, int(cell.d_h)))
+            block_table = None
+        # packed streams run in the kernels themselves: heads cut the carry and
+        # read their h0 row (block_table[s] of a pool when given)
         r = cell.clipped_r()
-        states = ops.slstm_init_fused(wx, r, h0, picard_iters=int(picard_iters), eps=cell.eps)
+        states = ops.slstm_init_fused(wx, r, h0, cu_seqlens, block_table,
+                                      picard_iters=int(picard_iters), eps=cell.eps)
         return ops.newton_slstm_fused(
-            wx, r, h0, states, None,
+            wx, r, h0, states, block_table, cu_seqlens,
             max_iters=max_iters, omega=omega, eps=cell.eps, log_coords=log_coords,
             scan_tile=scan_tile, time_loop=fused_time_loop,
             window_len=0 if fused_window_len is None else int(fused_window_len),
@@ -192,12 +198,25 @@ def fused_newton(
     raise TypeError(_fused_error(cell, wx))
 
 
-def _fill_stats(cell, x, states, h0, config, *, iters, stats, history=(), known=None) -> None:
+def packed_in_kernel() -> bool:
+    """Packed diag-sLSTM streams run in the kernels (heads cut the carry);
+    ``PARARNN_AMD_PACKED=0`` pads them into length groups instead."""
+    return os.environ.get("PARARNN_AMD_PACKED", "1") != "0"
+
+
+def _prepend_any(states: Tensor, h0: Tensor | None, cu_seqlens: Tensor | None) -> Tensor:
+    if cu_seqlens is None:
+        return _prepend(states, h0)
+    return prepend_state_ragged(states, h0, cu_seqlens)
+
+
+def _fill_stats(cell, x, states, h0, config, *, iters, stats, history=(), known=None,
+                cu_seqlens=None) -> None:
     """Residual gate (newton/__init__.py:582-636): one extra cell step over T."""
     if stats is None and config.residual_fail is None:
         return
     if known is None:
-        pred = cell.step(_prepend(states, h0), x)
+        pred = cell.step(_prepend_any(states, h0, cu_seqlens), x)
         res = float((pred - states).detach().abs().amax())
     else:
         res = known
@@ -220,29 +239,37 @@ def _fill_stats(cell, x, states, h0, config, *, iters, stats, history=(), known=
         log.warning("newton_residual_high max_residual=%g iters=%d", res, iters)
 
 
-def _newton_solve(cell, x, config, *, h0, stats, wx=None) -> Tensor:
+def _newton_solve(cell, x, config, *, h0, stats, wx=None, cu_seqlens=None,
+                  block_table=None) -> Tensor:
     if config.chunk_len is not None:
         return _newton_chunked(cell, x, config, h0=h0, stats=stats)
     if wx is None:
         wx = cell.W_x(x)
+    gate_h0 = h0 if block_table is None else gather_h0(
+        h0, block_table, int(cu_seqlens.numel()) - 1, _state_tail(cell))
     if config.fused_early_exit and not torch.compiler.is_compiling():
-        states, iters, history = _fused_early_exit(cell, wx, config, h0=h0)
-        _fill_stats(cell, x, states, h0, config, iters=iters, stats=stats, history=history,
-                    known=history[-1] if history else float("nan"))
+        states, iters, history = _fused_early_exit(cell, wx, config, h0=h0,
+                                                   cu_seqlens=cu_seqlens,
+                                                   block_table=block_table)
+        _fill_stats(cell, x, states, gate_h0, config, iters=iters, stats=stats, history=history,
+                    known=history[-1] if history else float("nan"), cu_seqlens=cu_seqlens)
         return states
     states = fused_newton(
         cell, wx,
         max_iters=int(config.max_iters), omega=float(config.omega), h0=h0,
         log_coords=config.coords == "log", picard_iters=int(config.picard_iters or 0),
         scan_tile=config.scan_tile, fused_time_loop=config.fused_time_loop,
-        fused_window_len=config.fused_window_len,
+        fused_window_len=config.fused_window_len, cu_seqlens=cu_seqlens,
+        block_table=block_table,
     )
     if not torch.compiler.is_compiling():
-        _fill_stats(cell, x, states, h0, config, iters=int(config.max_iters), stats=stats)
+        _fill_stats(cell, x, states, gate_h0, config, iters=int(config.max_iters), stats=stats,
+                    cu_seqlens=cu_seqlens)
     return states
 
 
-def _fused_early_exit(cell, wx, config, *, h0) -> tuple[Tensor, int, list[float]]:
+def _fused_early_exit(cell, wx, config, *, h0, cu_seqlens=None,
+                      block_table=None) -> tuple[Tensor, int, list[float]]:
     """``NewtonConfig.fused_early_exit`` (newton/__init__.py:696-762, the early-exit
     branch of kernels/newton_slstm.py:2892-2922): the fused iterations one at a
     time on the fp32 work iterate; after each, the host reads max|F| of the
@@ -254,13 +281,16 @@ def _fused_early_exit(cell, wx, config, *, h0) -> tuple[Tensor, int, list[float]
     atol = float(config.residual_atol)
     r = cell.clipped_r()
     P = int(config.picard_iters or 0)
-    work = ops.slstm_init_fused(wx, r, h0, picard_iters=P, eps=cell.eps)
+    work = ops.slstm_init_fused(wx, r, h0, cu_seqlens, block_table, picard_iters=P, eps=cell.eps)
+    gate_h0 = h0 if block_table is None else gather_h0(
+        h0, block_table, int(cu_seqlens.numel()) - 1, _state_tail(cell))
     history: list[float] = []
     states = work
     for it in range(int(config.max_iters)):
-        work = ops.slstm_newton_step(wx, r, h0, work, omega=float(config.omega), eps=cell.eps)
+        work = ops.slstm_newton_step(wx, r, h0, work, omega=float(config.omega), eps=cell.eps,
+                                     cu_seqlens=cu_seqlens, block_table=block_table)
         states = work.to(wx.dtype)
-        pred = cell.step(_prepend(states, h0), None, wx=wx)
+        pred = cell.step(_prepend_any(states, gate_h0, cu_seqlens), None, wx=wx)
         res = float((pred - states).abs().amax())
         history.append(res)
         if res < atol:
@@ -298,18 +328,22 @@ def _picard_retry_needed(res: float, config: NewtonConfig) -> bool:
     return fail is not None and res > fail
 
 
-def _newton_forward(cell, x, config, *, h0, stats, wx=None) -> Tensor:
-    """The solve; ``wx`` (unchunked only) reuses a projection already computed."""
+def _newton_forward(cell, x, config, *, h0, stats, wx=None, cu_seqlens=None,
+                    block_table=None) -> Tensor:
+    """The solve; ``wx`` (unchunked only) reuses a projection already computed.
+    ``cu_seqlens`` / ``block_table``: a packed diag-sLSTM stream solved in the
+    kernels."""
     if config.chunk_len is not None:
         return _newton_chunked(cell, x, config, h0=h0, stats=stats)
+    packed = dict(cu_seqlens=cu_seqlens, block_table=block_table)
     if not (config.picard_adapt and isinstance(cell, ParaSLSTM)) or torch.compiler.is_compiling():
-        return _newton_solve(cell, x, config, h0=h0, stats=stats, wx=wx)
+        return _newton_solve(cell, x, config, h0=h0, stats=stats, wx=wx, **packed)
     # Adaptive Picard ladder (picard.py:105-158).
     cfg = config
     while True:
         st = stats if stats is not None else NewtonStats()
         states = _newton_solve(cell, x, replace(cfg, residual_fail=None), h0=h0, stats=st,
-                               wx=wx)
+                               wx=wx, **packed)
         res = st.max_residual
         nxt = slstm_picard_next(int(cfg.picard_iters or 0))
         if _picard_retry_needed(res, config) and nxt is not None:
@@ -320,7 +354,7 @@ def _newton_forward(cell, x, config, *, h0, stats, wx=None) -> Tensor:
         cap = config.residual_fail
         if cap is not None and (not math.isfinite(res) or res > cap):
             _fill_stats(cell, x, states, h0, config, iters=st.iters, stats=st,
-                        history=st.residual_history, known=res)
+                        history=st.residual_history, known=res, cu_seqlens=cu_seqlens)
         return states
 
 
@@ -362,6 +396,10 @@ def newton_apply(
             raise RuntimeError("block_table newton is inference-only")
     with _newton_precision_region(x.device):
         if cu_seqlens is not None:
+            if isinstance(cell, ParaSLSTM) and cell.mix == "diag" and packed_in_kernel():
+                return _newton_packed(cell, x, config, h0=h0, stats=stats,
+                                      cu_seqlens=cu_seqlens, block_table=block_table,
+                                      needs_grad=needs_grad)
             return _newton_ragged(cell, x, config, h0=h0, stats=stats, cu_seqlens=cu_seqlens,
                                   block_table=block_table, needs_grad=needs_grad)
         if block_table is not None:
@@ -403,6 +441,29 @@ def _check_ragged_args(x: Tensor, config: NewtonConfig) -> None:
         raise ValueError("chunk_len cannot be combined with cu_seqlens")
     if config.fused_time_loop:
         raise ValueError("fused_time_loop cannot be combined with cu_seqlens")
+
+
+def _newton_packed(cell, x, config, *, h0, stats, cu_seqlens, block_table, needs_grad):
+    """A packed diag-sLSTM stream in one solve: the kernels cut the carry at
+    every sequence head and read each head's h0 row themselves (block_table
+    rows of a pool when given), as the reference's packed semantics
+    (solvers/scan.py:206-216, layout.py:115-138); K, P, the Picard ladder and
+    the residual gate act on the packed stream (newton/__init__.py:327-355)."""
+    cs = validate_cu_seqlens(cu_seqlens, x.shape[1]).to(x.device)
+    n_seq = int(cs.numel()) - 1
+    if block_table is None and h0 is not None and h0.shape[0] != n_seq:
+        raise ValueError(f"h0 batch {h0.shape[0]} != n_seq {n_seq}")
+    if not needs_grad:
+        return _newton_forward(cell, x, config, h0=h0, stats=stats, cu_seqlens=cs,
+                               block_table=block_table)
+    has_h0 = h0 is not None
+    h0_leaf = h0 if has_h0 else x.new_zeros(())
+    _fwd_pack.clear()
+    _fwd_pack.update(cell=cell, config=config, stats=stats, has_h0=has_h0, cu_seqlens=cs)
+    try:
+        return _NewtonFixedPoint.apply(x, h0_leaf, *tuple(cell.parameters()))
+    finally:
+        _fwd_pack.clear()
 
 
 def _newton_ragged(cell, x, config, *, h0, stats, cu_seqlens, block_table, needs_grad):
@@ -470,6 +531,8 @@ class _NewtonFixedPoint(torch.autograd.Function):
         config = _fwd_pack["config"]
         has_h0 = bool(_fwd_pack["has_h0"])
         h0_fwd = h0_in if has_h0 else None
+        cs = _fwd_pack.get("cu_seqlens")
+        ctx.cu_seqlens = cs
         ctx.cell = cell
         ctx.has_h0 = has_h0
         ctx.recompute = bool(config.recompute)
@@ -482,7 +545,7 @@ class _NewtonFixedPoint(torch.autograd.Function):
             if config.chunk_len is None and not ctx.recompute:
                 wx = cell.W_x(x_in)
             states = _newton_forward(cell, x_in, config, h0=h0_fwd, stats=_fwd_pack["stats"],
-                                     wx=wx)
+                                     wx=wx, cu_seqlens=cs)
         if ctx.recompute:
             ctx.save_for_backward(x_in, h0_in)
         elif wx is not None:
@@ -502,7 +565,8 @@ class _NewtonFixedPoint(torch.autograd.Function):
             x_in, h0_in = ctx.saved_tensors
             h0_fwd = h0_in if ctx.has_h0 else None
             with torch.no_grad():
-                states = _newton_forward(ctx.cell, x_in, ctx.fwd_config, h0=h0_fwd, stats=None)
+                states = _newton_forward(ctx.cell, x_in, ctx.fwd_config, h0=h0_fwd, stats=None,
+                                         cu_seqlens=ctx.cu_seqlens)
         else:
             states, x_in, h0_in, *rest = ctx.saved_tensors
             wx = rest[0] if rest else None
@@ -516,7 +580,8 @@ class _NewtonFixedPoint(torch.autograd.Function):
                 )
             else:
                 grad_x, param_grads, grad_h0 = _eq26_vjp(
-                    ctx.cell, states, x_in, grad_states, h0=h0_fwd, wx=wx
+                    ctx.cell, states, x_in, grad_states, h0=h0_fwd, wx=wx,
+                    cu_seqlens=ctx.cu_seqlens
                 )
         if not x_in.requires_grad:
             grad_x = None
@@ -526,7 +591,8 @@ class _NewtonFixedPoint(torch.autograd.Function):
 
 
 def _eq26_vjp(cell: nn.Module, states: Tensor, x: Tensor, partial: Tensor, *,
-              h0: Tensor | None = None, wx: Tensor | None = None):
+              h0: Tensor | None = None, wx: Tensor | None = None,
+              cu_seqlens: Tensor | None = None):
     """``(grad_x, per-parameter grads, grad_h0)`` for diag ParaSLSTM and head ParaGRU.
 
     The reverse scan and the cell VJP run in one HIP op
@@ -541,10 +607,11 @@ def _eq26_vjp(cell: nn.Module, states: Tensor, x: Tensor, partial: Tensor, *,
     if isinstance(cell, ParaSLSTM) and cell.mix == "diag":
         r_mix = cell.clipped_r()
         g_wx, g_r, g_h0, g_b = ops.slstm_backward_fused(wx, r_mix, h0, states, partial,
-                                                       eps=cell.eps)
+                                                       cu_seqlens, eps=cell.eps)
         determinism.maybe_check_fused_vjp_once(
             (g_r,),
-            lambda: (ops.slstm_backward_fused(wx, r_mix, h0, states, partial, eps=cell.eps)[1],),
+            lambda: (ops.slstm_backward_fused(wx, r_mix, h0, states, partial, cu_seqlens,
+                                              eps=cell.eps)[1],),
             cell_name=type(cell).__name__, shape=states.shape)
         g_r = g_r.to(cell.R.dtype)
         if cap is not None:

@@ -140,9 +140,42 @@ def _slstm_h0(h0: Tensor | None, batch: int, d_h: int) -> Tensor | None:
     return h0.contiguous()
 
 
+def _packed_args(cu_seqlens: Tensor | None, block_table: Tensor | None, wx: Tensor,
+                 h0: Tensor | None, d_h: int):
+    """Device int32 ``cu_seqlens`` / ``block_table`` of a packed stream and the
+    checked ``h0`` (``(S, 4, d)`` per sequence, or a pool that ``block_table``
+    indexes), or ``(None, None, 0, h0)`` for a rectangular batch."""
+    if cu_seqlens is None:
+        return None, None, 0, h0
+    from pararnn_amd.ragged import validate_cu_seqlens
+
+    if wx.shape[0] != 1:
+        raise ValueError(f"cu_seqlens packs wx with batch=1, got batch={wx.shape[0]}")
+    cs = validate_cu_seqlens(cu_seqlens, wx.shape[1])
+    n_seq = int(cs.numel()) - 1
+    bt = None
+    if block_table is not None:
+        if h0 is None:
+            raise ValueError("block_table needs h0 as a pool (C, ...)")
+        bt = block_table.to(device=wx.device, dtype=torch.int32).contiguous()
+        if bt.dim() != 1 or int(bt.numel()) != n_seq:
+            raise ValueError(f"block_table B={int(bt.numel())} != {n_seq}")
+        if h0.shape[1:] != (4, d_h):
+            raise ValueError(f"pool h0 tail {tuple(h0.shape[1:])} != {(4, d_h)}")
+        mn, mx = int(bt.min()), int(bt.max())
+        if mn < 0 or mx >= int(h0.shape[0]):
+            raise ValueError(f"block_table slots [{mn}, {mx}] outside pool capacity "
+                             f"{int(h0.shape[0])}")
+    elif h0 is not None and h0.shape != (n_seq, 4, d_h):
+        raise ValueError(f"h0 shape {tuple(h0.shape)} != {(n_seq, 4, d_h)}")
+    cs32 = cs.to(device=wx.device, dtype=torch.int32).contiguous()
+    return cs32, bt, n_seq, None if h0 is None else h0.contiguous()
+
+
 @torch.library.custom_op("pararnn::slstm_init_fused", mutates_args=())
 def slstm_init_fused(
-    wx: Tensor, r: Tensor, h0: Tensor | None = None, *, picard_iters: int, eps: float
+    wx: Tensor, r: Tensor, h0: Tensor | None = None, cu_seqlens: Tensor | None = None,
+    block_table: Tensor | None = None, *, picard_iters: int, eps: float
 ) -> Tensor:
     """Zero-hidden frozen-gate scan plus ``picard_iters`` Picard passes on the GPU.
 
@@ -150,6 +183,10 @@ def slstm_init_fused(
     ``slstm_picard_init`` / ``slstm_zero_hidden_init`` (solvers/slstm_picard.py:143-181):
     states ``(B, T, 4, d_h)`` in ``wx``'s dtype; between passes the trajectory
     is held in that dtype and ``wx + R * h_prev`` is rounded after each op.
+    With ``cu_seqlens`` (``wx`` packed as ``(1, N, 4 d_h)``) every sequence
+    restarts from its own ``h0`` row (``block_table[s]`` of a pool when given)
+    inside the kernels, as the reference's ragged frozen-gate scan does
+    (slstm_picard.py:87-103).
     """
     batch, time, d_h = _slstm_shapes(wx, r)
     code = _validate("slstm_init_fused", wx, r, h0)
@@ -157,24 +194,35 @@ def slstm_init_fused(
         raise ValueError(f"n_picard must be >= 0, got {picard_iters!r}")
     wx = wx.contiguous()
     r = r.contiguous()
-    h0 = _slstm_h0(h0, batch, d_h)
+    cs32, bt, n_seq, h0 = _packed_args(cu_seqlens, block_table, wx, h0, d_h)
+    if cs32 is None:
+        h0 = _slstm_h0(h0, batch, d_h)
     out = wx.new_empty(batch, time, 4, d_h)
     lib = _lib.load()
     _lib.sync_deterministic(lib)
     with torch.cuda.device(wx.device):
-        nbytes = lib.prnn_slstm_init_workspace_size(batch, time, d_h, picard_iters, code)
-        ws, tag = _slstm_workspace(nbytes, wx.device)
-        rc = lib.prnn_slstm_init_ex(
-            _ptr(wx), _ptr(r), _ptr(h0), _ptr(out), batch, time, d_h, int(picard_iters),
-            float(eps), code, _ptr(ws), ws.numel(), tag, _stream(wx.device),
-        )
+        if cs32 is None:
+            nbytes = lib.prnn_slstm_init_workspace_size(batch, time, d_h, picard_iters, code)
+            ws, tag = _slstm_workspace(nbytes, wx.device)
+            rc = lib.prnn_slstm_init_ex(
+                _ptr(wx), _ptr(r), _ptr(h0), _ptr(out), batch, time, d_h, int(picard_iters),
+                float(eps), code, _ptr(ws), ws.numel(), tag, _stream(wx.device),
+            )
+        else:
+            nbytes = lib.prnn_slstm_init_packed_workspace_size(time, d_h, picard_iters, code)
+            ws, tag = _slstm_workspace(nbytes, wx.device)
+            rc = lib.prnn_slstm_init_packed(
+                _ptr(wx), _ptr(r), _ptr(h0), _ptr(out), time, d_h, int(picard_iters),
+                float(eps), code, _ptr(cs32), n_seq, _ptr(bt), _ptr(ws), ws.numel(), tag,
+                _stream(wx.device),
+            )
     _lib.check(rc, "slstm_init_fused")
     _check_lookback(ws, "slstm_init_fused")
     return out
 
 
 @slstm_init_fused.register_fake
-def _(wx, r, h0=None, *, picard_iters, eps):
+def _(wx, r, h0=None, cu_seqlens=None, block_table=None, *, picard_iters, eps):
     batch, time, _ = wx.shape
     return wx.new_empty(batch, time, 4, r.shape[-1])
 
@@ -186,6 +234,7 @@ def newton_slstm_fused(
     h0: Tensor | None = None,
     states: Tensor | None = None,
     block_table: Tensor | None = None,
+    cu_seqlens: Tensor | None = None,
     *,
     max_iters: int,
     omega: float,
@@ -197,10 +246,15 @@ def newton_slstm_fused(
 ) -> Tensor:
     """``max_iters`` fused Newton iterations for diag ParaSLSTM on the GPU.
 
-    Same schema as the reference op (kernels/custom_ops.py:486-516).  Work is
-    fp32 throughout; intermediate trajectories stay fp32 and the result is
-    rounded once to ``wx``'s dtype (kernels/newton_slstm.py:2780-2939).
-    ``states=None`` starts from the zero-hidden guess.
+    Same schema as the reference op (kernels/custom_ops.py:486-516), plus an
+    optional trailing ``cu_seqlens``.  Work is fp32 throughout; intermediate
+    trajectories stay fp32 and the result is rounded once to ``wx``'s dtype
+    (kernels/newton_slstm.py:2780-2939).  ``states=None`` starts from the
+    zero-hidden guess.  With ``cu_seqlens`` (``wx`` packed as ``(1, N, 4 d)``)
+    the kernels cut the carry at every sequence head (J = 0 there, the
+    sequence's ``h0`` row -- ``block_table[s]`` of a pool when given -- as
+    the previous state), the reference's packed semantics
+    (solvers/scan.py:206-216, layout.py:115-138), in one stream.
     """
     if log_coords:
         raise TypeError("newton_slstm_fused: log_coords is not provided by pararnn_amd")
@@ -209,17 +263,21 @@ def newton_slstm_fused(
     if time_loop or window_len:
         raise TypeError("newton_slstm_fused: fused_time_loop is not provided by pararnn_amd")
     batch, time, d_h = _slstm_shapes(wx, r)
-    if block_table is not None:
-        # paged h0: the pool rows the table names (kernels/_fused_common.py:106-139)
+    if block_table is not None and cu_seqlens is None:
+        # paged h0 of a rectangular batch: the pool rows the table names
+        # (kernels/_fused_common.py:106-139)
         from pararnn_amd.ragged import gather_h0
 
         h0 = gather_h0(h0, block_table, batch, (4, d_h))
+        block_table = None
     code = _validate("newton_slstm_fused", wx, r, h0)
     if max_iters < 0:
         raise ValueError(f"max_iters must be >= 0, got {max_iters!r}")
-    h0 = _slstm_h0(h0, batch, d_h)
+    cs32, bt, n_seq, h0 = _packed_args(cu_seqlens, block_table, wx, h0, d_h)
+    if cs32 is None:
+        h0 = _slstm_h0(h0, batch, d_h)
     if states is None:
-        states = slstm_init_fused(wx, r, h0, picard_iters=0, eps=eps)
+        states = slstm_init_fused(wx, r, h0, cs32, bt, picard_iters=0, eps=eps)
     else:
         if states.shape != (batch, time, 4, d_h):
             raise ValueError(f"states shape {tuple(states.shape)} != {(batch, time, 4, d_h)}")
@@ -231,20 +289,30 @@ def newton_slstm_fused(
     lib = _lib.load()
     _lib.sync_deterministic(lib)
     with torch.cuda.device(wx.device):
-        nbytes = lib.prnn_slstm_newton_workspace_size(batch, time, d_h, int(max_iters), code)
-        ws, tag = _slstm_workspace(nbytes, wx.device)
-        rc = lib.prnn_slstm_newton_ex(
-            _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), _ptr(out), batch, time, d_h,
-            int(max_iters), float(omega), float(eps), code, _ptr(ws), ws.numel(), tag,
-            _stream(wx.device),
-        )
+        if cs32 is None:
+            nbytes = lib.prnn_slstm_newton_workspace_size(batch, time, d_h, int(max_iters), code)
+            ws, tag = _slstm_workspace(nbytes, wx.device)
+            rc = lib.prnn_slstm_newton_ex(
+                _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), _ptr(out), batch, time, d_h,
+                int(max_iters), float(omega), float(eps), code, _ptr(ws), ws.numel(), tag,
+                _stream(wx.device),
+            )
+        else:
+            nbytes = lib.prnn_slstm_newton_packed_workspace_size(time, d_h, int(max_iters), code)
+            ws, tag = _slstm_workspace(nbytes, wx.device)
+            rc = lib.prnn_slstm_newton_packed(
+                _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), _ptr(out), time, d_h,
+                int(max_iters), float(omega), float(eps), code, _ptr(cs32), n_seq, _ptr(bt),
+                _ptr(ws), ws.numel(), tag, _stream(wx.device),
+            )
     _lib.check(rc, "newton_slstm_fused")
     _check_lookback(ws, "newton_slstm_fused")
     return out
 
 
 def slstm_newton_step(wx: Tensor, r: Tensor, h0: Tensor | None, states: Tensor, *,
-                      omega: float, eps: float) -> Tensor:
+                      omega: float, eps: float, cu_seqlens: Tensor | None = None,
+                      block_table: Tensor | None = None) -> Tensor:
     """One Newton iteration from ``states`` (``wx``'s dtype, or fp32 work)
     with an fp32 result: the per-iteration body of the fused op, for the
     host-checked early exit (``NewtonConfig.fused_early_exit``; reference
@@ -252,7 +320,9 @@ def slstm_newton_step(wx: Tensor, r: Tensor, h0: Tensor | None, states: Tensor, 
     synchronises with the host after every iteration."""
     batch, time, d_h = _slstm_shapes(wx, r)
     code = _validate("slstm_newton_step", wx, r, h0)
-    h0 = _slstm_h0(h0, batch, d_h)
+    cs32, bt, n_seq, h0 = _packed_args(cu_seqlens, block_table, wx, h0, d_h)
+    if cs32 is None:
+        h0 = _slstm_h0(h0, batch, d_h)
     if states.shape != (batch, time, 4, d_h):
         raise ValueError(f"states shape {tuple(states.shape)} != {(batch, time, 4, d_h)}")
     in_f32 = states.dtype == torch.float32
@@ -264,19 +334,29 @@ def slstm_newton_step(wx: Tensor, r: Tensor, h0: Tensor | None, states: Tensor, 
     lib = _lib.load()
     _lib.sync_deterministic(lib)
     with torch.cuda.device(wx.device):
-        nbytes = lib.prnn_slstm_newton_workspace_size(batch, time, d_h, 1, code)
-        ws, tag = _slstm_workspace(nbytes, wx.device)
-        rc = lib.prnn_slstm_newton_step(
-            _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), int(in_f32), _ptr(out), batch, time,
-            d_h, float(omega), float(eps), code, _ptr(ws), ws.numel(), tag, _stream(wx.device),
-        )
+        if cs32 is None:
+            nbytes = lib.prnn_slstm_newton_workspace_size(batch, time, d_h, 1, code)
+            ws, tag = _slstm_workspace(nbytes, wx.device)
+            rc = lib.prnn_slstm_newton_step(
+                _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), int(in_f32), _ptr(out), batch, time,
+                d_h, float(omega), float(eps), code, _ptr(ws), ws.numel(), tag,
+                _stream(wx.device),
+            )
+        else:
+            nbytes = lib.prnn_slstm_newton_packed_workspace_size(time, d_h, 1, code)
+            ws, tag = _slstm_workspace(nbytes, wx.device)
+            rc = lib.prnn_slstm_newton_step_packed(
+                _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), int(in_f32), _ptr(out), time, d_h,
+                float(omega), float(eps), code, _ptr(cs32), n_seq, _ptr(bt), _ptr(ws),
+                ws.numel(), tag, _stream(wx.device),
+            )
     _lib.check(rc, "slstm_newton_step")
     _check_lookback(ws, "slstm_newton_step")
     return out
 
 
 @newton_slstm_fused.register_fake
-def _(wx, r, h0=None, states=None, block_table=None, *, max_iters, omega, eps,
+def _(wx, r, h0=None, states=None, block_table=None, cu_seqlens=None, *, max_iters, omega, eps,
       log_coords=False, scan_tile="assoc", time_loop=False, window_len=0):
     if states is not None:
         return torch.empty_like(states)
@@ -286,7 +366,8 @@ def _(wx, r, h0=None, states=None, block_table=None, *, max_iters, omega, eps,
 
 @torch.library.custom_op("pararnn::slstm_backward_fused", mutates_args=())
 def slstm_backward_fused(
-    wx: Tensor, r: Tensor, h0: Tensor | None, states: Tensor, grad: Tensor, *, eps: float
+    wx: Tensor, r: Tensor, h0: Tensor | None, states: Tensor, grad: Tensor,
+    cu_seqlens: Tensor | None = None, *, eps: float
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Eq. 2.6 backward of diag ParaSLSTM at ``H* = states`` on the GPU.
 
@@ -297,6 +378,8 @@ def slstm_backward_fused(
     gradient, summed in the same pass).  The reference computes the same quantities with
     ``step_and_jacobian`` + ``reverse_scan_block4`` + ``slstm_recurrence_vjp``
     (solvers/newton/__init__.py:765-866, kernels/vjp_slstm.py:209-240).
+    With ``cu_seqlens`` (a packed stream, ``B = 1``) nothing flows across a
+    sequence head and ``g_h0`` is ``(S, 4, d_h)``, one row per sequence.
     """
     batch, time, d_h = _slstm_shapes(wx, r)
     code = _validate("slstm_backward_fused", wx, r, h0, states, grad)
@@ -304,33 +387,44 @@ def slstm_backward_fused(
         if t.shape != (batch, time, 4, d_h):
             raise ValueError(f"{name} shape {tuple(t.shape)} != {(batch, time, 4, d_h)}")
     wx, r, states, grad = wx.contiguous(), r.contiguous(), states.contiguous(), grad.contiguous()
-    h0 = _slstm_h0(h0, batch, d_h)
+    cs32, _, n_seq, h0 = _packed_args(cu_seqlens, None, wx, h0, d_h)
+    if cs32 is None:
+        h0 = _slstm_h0(h0, batch, d_h)
     g_wx = torch.empty_like(wx)
     g_r = torch.empty(4, d_h, dtype=torch.float32, device=wx.device)
-    g_h0 = torch.zeros(batch, 4, d_h, dtype=torch.float32, device=wx.device)
+    g_h0 = torch.zeros(n_seq if cs32 is not None else batch, 4, d_h, dtype=torch.float32,
+                       device=wx.device)
     g_b = torch.empty(4, d_h, dtype=torch.float32, device=wx.device)
     lib = _lib.load()
     _lib.sync_deterministic(lib)
     with torch.cuda.device(wx.device):
         nbytes = lib.prnn_slstm_backward_workspace_size(batch, time, d_h, code)
         ws, tag = _slstm_workspace(nbytes, wx.device)
-        rc = lib.prnn_slstm_backward_ex(
-            _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), _ptr(grad), _ptr(g_wx), _ptr(g_r),
-            _ptr(g_h0), _ptr(g_b), batch, time, d_h, float(eps), code, _ptr(ws), ws.numel(), tag,
-            _stream(wx.device),
-        )
+        if cs32 is None:
+            rc = lib.prnn_slstm_backward_ex(
+                _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), _ptr(grad), _ptr(g_wx), _ptr(g_r),
+                _ptr(g_h0), _ptr(g_b), batch, time, d_h, float(eps), code, _ptr(ws), ws.numel(),
+                tag, _stream(wx.device),
+            )
+        else:
+            rc = lib.prnn_slstm_backward_packed(
+                _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), _ptr(grad), _ptr(g_wx), _ptr(g_r),
+                _ptr(g_h0), _ptr(g_b), time, d_h, float(eps), code, _ptr(cs32), n_seq,
+                _ptr(ws), ws.numel(), tag, _stream(wx.device),
+            )
     _lib.check(rc, "slstm_backward_fused")
     _check_lookback(ws, "slstm_backward_fused")
     return g_wx, g_r, g_h0, g_b
 
 
 @slstm_backward_fused.register_fake
-def _(wx, r, h0, states, grad, *, eps):
+def _(wx, r, h0, states, grad, cu_seqlens=None, *, eps):
     batch, _, d_h = states.shape[0], states.shape[1], r.shape[-1]
+    rows = batch if cu_seqlens is None else cu_seqlens.shape[0] - 1
     return (
         torch.empty_like(wx),
         wx.new_empty(4, d_h, dtype=torch.float32),
-        wx.new_empty(batch, 4, d_h, dtype=torch.float32),
+        wx.new_empty(rows, 4, d_h, dtype=torch.float32),
         wx.new_empty(4, d_h, dtype=torch.float32),
     )
 

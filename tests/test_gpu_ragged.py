@@ -151,9 +151,10 @@ def _uneven(d_x, extra=(), seed=5):
 
 
 def test_slstm_ragged_length_groups(monkeypatch):
-    """Uneven lengths run as several padded groups: forward against the
-    per-sequence oracle, forward and every gradient against the single
-    padded rectangle (PARARNN_AMD_RAGGED_GROUPS=0)."""
+    """Uneven lengths: the packed stream solved in the kernels (default), and
+    with PARARNN_AMD_PACKED=0 as several padded length groups, against the
+    single padded rectangle (PARARNN_AMD_RAGGED_GROUPS=0): forward and every
+    gradient; the forward also against the per-sequence oracle."""
     from pararnn_amd import ParaSLSTM, newton_apply
 
     print("case slstm ragged length groups fp32 (3 groups, lengths 12..2500)", flush=True)
@@ -174,19 +175,23 @@ def test_slstm_ragged_length_groups(monkeypatch):
         out.update({n: p.grad.clone() for n, p in cell.named_parameters()})
         return out
 
+    packed = run()
+    monkeypatch.setenv("PARARNN_AMD_PACKED", "0")
     grouped = run()
     monkeypatch.setenv("PARARNN_AMD_RAGGED_GROUPS", "0")
     single = run()
-    for k in grouped:
-        e = ((grouped[k] - single[k]).abs().max() / single[k].abs().max()).item()
-        print(f"  {k}: grouped vs single rel diff {e:.2e}", flush=True)
-        assert e <= 1e-5, k
+    for name, got in (("grouped", grouped), ("packed", packed)):
+        for k in got:
+            e = ((got[k] - single[k]).abs().max() / single[k].abs().max()).item()
+            print(f"  {k}: {name} vs single rel diff {e:.2e}", flush=True)
+            assert e <= 1e-5, (name, k)
     p = O.SLSTMParams(cell.W_x.weight.detach().cpu(), cell.W_x.bias.detach().cpu(),
                       cell.R.detach().cpu())
     own = slstm_newton_ragged(p, x.cpu(), cs, max_iters=3, picard_iters=3, h0=h0.cpu())
-    e_own = ((grouped["H"].cpu() - own).abs() / (1 + own.abs())).max().item()
-    print(f"  rel err vs per-sequence oracle {e_own:.2e}", flush=True)
-    assert e_own <= 3e-5
+    for name, got in (("grouped", grouped), ("packed", packed)):
+        e_own = ((got["H"].cpu() - own).abs() / (1 + own.abs())).max().item()
+        print(f"  {name}: rel err vs per-sequence oracle {e_own:.2e}", flush=True)
+        assert e_own <= 3e-5
 
 
 def test_gru_head_ragged_length_groups(monkeypatch):
