@@ -138,19 +138,10 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
   // h0 row; nothing flows from a head to the step before it (nu = 0 there),
   // and the head's nu = J^T mu is that sequence's dL/dh0.
   Heads hd{0ull, 0};
-  float hst[4] = {0.f, 0.f, 0.f, 0.f};
-  if constexpr (PK) {
-    hd = find_heads(pk, t0, n_steps);
-    if (hd.mask) head_state(pk, h0, hd.seq(hd.first()), d, c0 + lane, live, hst);
-  }
+  if constexpr (PK) hd = find_heads(pk, t0, n_steps);
   auto prev_of = [&](int s, float p[4]) {
     if (PK && hd.at(s)) {
-      if (s == hd.first()) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) p[k] = hst[k];
-      } else {
-        head_state(pk, h0, hd.seq(s), d, c0 + lane, live, p);
-      }
+      head_state(pk, h0, hd.seq(s), d, c0 + lane, live, p);
     } else if (s == 0) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) p[k] = prev0[k];

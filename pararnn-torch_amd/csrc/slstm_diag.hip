@@ -1,1246 +1,13 @@
-// ParaSLSTM mix='diag' Newton + scan kernels for gfx950 (CDNA4).
-//
-// Two single-pass chunked scans over time, both with the same tile schedule:
-//
-//   tile  = (batch b, channel block of 64, time chunk of W*L steps)
-//   lane  = one channel; wave w = L consecutive steps of the chunk
-//
-// Pass 1 walks the lane's L steps serially from register-cached inputs and
-// folds them into the lane's segment aggregate; the W wave aggregates are
-// combined through LDS into the tile aggregate; wave 0 publishes it and runs a
-// decoupled look-back over earlier chunks of the same (b, channel block) to
-// get the carry into the tile; pass 2 replays the L steps from registers with
-// the true carry and streams the outputs.  Inputs are read from HBM once and
-// outputs written once per launch.
-//
-// (1) slstm_frozen_kernel: frozen-gate pass (zero-hidden or one Picard pass).
-//     Per step  m' = max(z_f + m, z_i),  f = e^{z_f + m - m'},  i = e^{z_i - m'},
-//     n' = f n + i,  c' = f c + i tanh z_z,  h = sigmoid(z_o) c' / (n' + eps)
-//     with pre = wx (+ R * h_prev of the previous pass).  The carry (m, n, c)
-//     composes through the stabilised monoid (F, M, N, C): F = sum z_f, M the
-//     max-plus aggregate, N / C the sums scaled by e^{-M}.
-//     Reference: solvers/slstm_picard.py:51-107, 143-181.
-// (2) slstm_newton_kernel: one Newton iteration.  Per step the cell value
-//     f(H_{t-1}, x_t), the 4x4 Jacobian J_t (12 structural non-zeros) and the
-//     residual F_t = f - H_t; the scan solves delta_t = J_t delta_{t-1} + F_t
-//     on the affine monoid (A, b) -> (J A, J b + F); H_t += omega delta_t.
-//     Reference: cells/para_slstm.py:347-446, solvers/scan.py:82-100,
-//     solvers/newton/__init__.py:516-543, kernels/newton_slstm.py:886-966.
-#include "slstm_scan.h"
+// ParaSLSTM mix='diag' host side: tile shapes, workspaces, launches of the
+// kernels in slstm_kernels.h for rectangular batches, and the C entry points
+// (packed streams launch through slstm_packed.hip).
+#include "slstm_kernels.h"
 
 #include <stdio.h>
 #include <stdlib.h>
 
 #include <mutex>
 #include <type_traits>
-
-namespace prnn {
-namespace slstm {
-
-// ---------------------------------------------------------------------------
-// (1) frozen-gate pass
-// ---------------------------------------------------------------------------
-
-struct FG {
-  float F, M, N, C;
-};
-
-__device__ __forceinline__ FG fg_identity() { return FG{0.f, -INFINITY, 0.f, 0.f}; }
-
-// Aggregate of segment x followed by segment y.
-__device__ __forceinline__ FG fg_compose(FG x, FG y) {
-  if (y.M == -INFINITY) return FG{x.F + y.F, x.M, x.N, x.C};
-  if (x.M == -INFINITY) return FG{x.F + y.F, y.M, y.N, y.C};
-  const float mx = y.F + x.M;
-  const float m = fmaxf(mx, y.M);
-  const float sx = fexp(mx - m), sy = fexp(y.M - m);
-  return FG{x.F + y.F, m, x.N * sx + y.N * sy, x.C * sx + y.C * sy};
-}
-
-// Carry (m, n, c) after applying aggregate y to carry (m, n, c).
-__device__ __forceinline__ void fg_apply(const FG& y, float& m, float& n, float& c) {
-  if (y.M == -INFINITY) return;
-  const float mc = y.F + m;
-  const float mn = fmaxf(mc, y.M);
-  const float sc = fexp(mc - mn), sy = fexp(y.M - mn);
-  n = n * sc + y.N * sy;
-  c = c * sc + y.C * sy;
-  m = mn;
-}
-
-// One frozen-gate step in place on (m, n, c); returns tanh-free readout pieces.
-// One of f, i is exactly e^0 = 1 (the larger exponent is the new stabiliser),
-// so a single exp of -|left - z_i| gives both, bit-identical to two exps.
-__device__ __forceinline__ void fg_step(float zi, float zf, float zz, float& m, float& n, float& c) {
-  const float left = zf + m;
-  const float mn = fmaxf(left, zi);
-  const float e = fexp(-fabsf(left - zi));
-  const bool lf = left >= zi;
-  const float f = lf ? 1.f : e;
-  const float i = lf ? e : 1.f;
-  const float z = ftanh(zz);
-  n = f * n + i;
-  c = f * c + i * z;
-  m = mn;
-}
-
-
-struct FrozenMonoid {
-  static constexpr int NI = 3;  // carry (m, n, c)
-  static constexpr int NA = 4;  // aggregate (F, M, N, C)
-  using Acc = FG;
-  static __device__ __forceinline__ void identity(Acc& a) { a = fg_identity(); }
-  static __device__ __forceinline__ void absorb(Acc& acc, const float a[NA]) {
-    acc = fg_compose(FG{a[0], a[1], a[2], a[3]}, acc);
-  }
-  static __device__ __forceinline__ void finish(const Acc& acc, const float v[NI], float out[NI]) {
-    float m = v[0], n = v[1], c = v[2];
-    fg_apply(acc, m, n, c);
-    out[0] = m;
-    out[1] = n;
-    out[2] = c;
-  }
-  static __device__ __forceinline__ void apply(const float a[NA], float v[NI]) {
-    fg_apply(FG{a[0], a[1], a[2], a[3]}, v[0], v[1], v[2]);
-  }
-};
-
-// Pre-activations of a tile's steps, held in registers between the two
-// passes.  In bf16 they are exact bf16 values (wx, or wx + R h_prev rounded as
-// the reference's two torch ops), packed two to a register.
-template <typename TX>
-struct PreStash;
-
-template <>
-struct PreStash<bf16> {
-  static constexpr int N = 2;  // registers per step: (z_i, z_f), (z_z, z_o)
-  template <bool HAS_H>
-  static __device__ __forceinline__ void make(const uint32_t x[4], const float r[4], float hp,
-                                              uint32_t w[N]) {
-    if (!HAS_H) {
-      w[0] = x[0] | (x[1] << 16);
-      w[1] = x[2] | (x[3] << 16);
-      return;
-    }
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      // round(R h) and round(wx + round(R h)), two gates per conversion.
-      const uint32_t q = pack_bf16x2(r[2 * k] * hp, r[2 * k + 1] * hp);
-      w[k] = pack_bf16x2(__uint_as_float(x[2 * k] << 16) + lo_bf16(q),
-                         __uint_as_float(x[2 * k + 1] << 16) + hi_bf16(q));
-    }
-  }
-  static __device__ __forceinline__ void get(const uint32_t w[N], float p[4]) {
-    p[0] = lo_bf16(w[0]);
-    p[1] = hi_bf16(w[0]);
-    p[2] = lo_bf16(w[1]);
-    p[3] = hi_bf16(w[1]);
-  }
-};
-
-template <>
-struct PreStash<float> {
-  static constexpr int N = 4;
-  template <bool HAS_H>
-  static __device__ __forceinline__ void make(const uint32_t x[4], const float r[4], float hp,
-                                              uint32_t w[N]) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const float xv = __uint_as_float(x[g]);
-      w[g] = __float_as_uint(HAS_H ? add_rn(xv, mul_rn(r[g], hp)) : xv);
-    }
-  }
-  static __device__ __forceinline__ void get(const uint32_t w[N], float p[4]) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) p[g] = __uint_as_float(w[g]);
-  }
-};
-
-// One frozen-gate pass over a tile of W waves x L steps x 64 channels.  Each
-// lane owns one channel; its L steps are read once (pass 1, which builds the
-// lane aggregate), kept in registers through the look-back, and replayed from
-// the true carry in pass 2, which writes the trajectory.
-template <typename TX, int L, int W, bool HAS_H, bool FULL_OUT, bool DET, bool PK>
-__global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
-    const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
-    const TX* __restrict__ hsrc, TX* __restrict__ out_full, TX* __restrict__ out_h, int B, int T,
-    int d, int n_cb, float eps, int* __restrict__ counter, unsigned long long* __restrict__ agg,
-    unsigned long long* __restrict__ incl, int epoch, Spin spin, Packed pk) {
-  constexpr int KP = 2;  // predecessors per wave per look-back round
-  using Stash = PreStash<TX>;
-  constexpr uint32_t SZ = sizeof(TX);
-  __shared__ float s_agg[W][4][kCB];
-  __shared__ float s_carry[W][3][kCB];
-  __shared__ LookbackShared<FrozenMonoid, W * KP> s_lb;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tile = take_ticket(counter);
-  const TileId id = decode_tile(tile, B, n_cb);
-  const int c0 = id.cb * kCB;
-  const bool live = c0 + lane < d;
-  const int t0 = id.chunk * (W * L) + wave * L;
-  const int n_steps = max(0, min(L, T - t0));
-  const size_t row4 = static_cast<size_t>(4) * d;
-  const size_t first = static_cast<size_t>(id.b) * T + t0;  // first (b, t) row of the wave
-  const uint32_t voff = live ? lane * SZ : kOOB;
-  const uint32_t slot = d * SZ;  // bytes between the slots of a (b, t, 4d) row
-  // Bytes from the wave's base to the end of its last live element.
-  const uint32_t span4 = n_steps > 0 ? ((n_steps - 1) * row4 + 3 * d + (d - c0)) * SZ : 0;
-  const uint32_t span1 = n_steps > 0 ? ((n_steps - 1) * static_cast<size_t>(d) + (d - c0)) * SZ : 0;
-
-  float r[4] = {0.f, 0.f, 0.f, 0.f};
-  float hp0 = 0.f;  // h_prev of the wave's first step
-  if (HAS_H && live) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) r[g] = ld(rmix + g * d + c0 + lane);
-    if (t0 > 0 && n_steps > 0)
-      hp0 = ld(hsrc + (first - 1) * d + c0 + lane);
-    else if (t0 == 0 && h0 != nullptr)
-      hp0 = ld(h0 + static_cast<size_t>(id.b) * row4 + 3 * d + c0 + lane);
-  }
-
-  // Packed sequences: heads among this wave's steps (see Packed); a head
-  // restarts the state from its sequence's initial one.
-  Heads hd{0ull, 0};
-  float hst[4] = {0.f, 0.f, 0.f, 0.f};
-  if constexpr (PK) {
-    hd = find_heads(pk, t0, n_steps);
-    if (hd.mask) head_state(pk, h0, hd.seq(hd.first()), d, c0 + lane, live, hst);
-  }
-  auto head_of = [&](int s, float st[4]) {
-    if (s == hd.first()) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) st[j] = hst[j];
-    } else {
-      head_state(pk, h0, hd.seq(s), d, c0 + lane, live, st);
-    }
-  };
-
-  // Pass 1: read the steps, stash the pre-activations, and fold the segment
-  // aggregate from the empty state (m = -inf, n = c = 0).
-  uint32_t stash[L][Stash::N];
-  FG a = fg_identity();
-  {
-    const rsrc_t rx = make_rsrc(wx + first * row4 + c0, span4);
-    const rsrc_t rh = make_rsrc(HAS_H ? hsrc + first * d + c0 : nullptr, HAS_H ? span1 : 0);
-    auto step = [&](int s, auto chk) {
-      constexpr bool CHECK = decltype(chk)::value;
-      const bool head = CHECK && hd.at(s);
-      float hs[4];
-      if (head) head_of(s, hs);
-      uint32_t x[4];
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        x[g] = ldb_bits(static_cast<TX*>(nullptr), rx, voff, s * row4 * SZ + g * slot);
-      float hp = hp0;
-      if (HAS_H && s > 0) hp = ldb<TX>(rh, voff, (s - 1) * d * SZ);
-      if (head) hp = hs[3];
-      Stash::template make<HAS_H>(x, r, hp, stash[s]);
-      float p[4];
-      Stash::get(stash[s], p);
-      if (head) a = FG{-INFINITY, hs[2], hs[1], hs[0]};
-      a.F += p[1];
-      fg_step(p[0], p[1], p[2], a.M, a.N, a.C);
-    };
-    // Whole segments run branch-free so the loads of many steps are in
-    // flight together; only the last segment of a sequence is guarded.
-    auto run = [&](auto chk) {
-      if (n_steps == L) {
-#pragma unroll
-        for (int s = 0; s < L; ++s) step(s, chk);
-      } else {
-#pragma unroll
-        for (int s = 0; s < L; ++s)
-          if (s < n_steps) step(s, chk);
-      }
-    };
-    if (PK && hd.mask)
-      run(std::true_type{});
-    else
-      run(std::false_type{});
-  }
-  s_agg[wave][0][lane] = a.F;
-  s_agg[wave][1][lane] = a.M;
-  s_agg[wave][2][lane] = a.N;
-  s_agg[wave][3][lane] = a.C;
-  __syncthreads();
-
-  float carry[3] = {0.f, 0.f, 0.f};  // (m, n, c) into the tile, wave 0
-  FG tile_agg = fg_identity();
-  if (wave == 0) {
-#pragma unroll
-    for (int w = 0; w < W; ++w)
-      tile_agg = fg_compose(
-          tile_agg, FG{s_agg[w][0][lane], s_agg[w][1][lane], s_agg[w][2][lane], s_agg[w][3][lane]});
-    if (id.chunk == 0) {
-      if (!PK && h0 != nullptr && live) {
-        const TX* hb = h0 + static_cast<size_t>(id.b) * row4 + c0 + lane;
-        carry[2] = ld(hb);
-        carry[1] = ld(hb + d);
-        carry[0] = ld(hb + 2 * d);
-      }
-    } else {
-      unsigned long long* ap = agg + (static_cast<size_t>(tile) * 4) * kCB + lane;
-      st_tagged(ap + 0 * kCB, tile_agg.F, epoch);
-      st_tagged(ap + 1 * kCB, tile_agg.M, epoch);
-      st_tagged(ap + 2 * kCB, tile_agg.N, epoch);
-      st_tagged(ap + 3 * kCB, tile_agg.C, epoch);
-    }
-  }
-  if (id.chunk > 0)
-    windowed_lookback<FrozenMonoid, W, KP, DET>(
-          id, B, n_cb, epoch, incl, agg, lane, wave, s_lb, carry, spin);
-  if (wave == 0) {
-    // Per-wave carries, then the tile's inclusive carry: the published
-    // aggregate applied to the carry in (what a successor's walk computes).
-    float m = carry[0], n = carry[1], c = carry[2];
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      s_carry[w][0][lane] = m;
-      s_carry[w][1][lane] = n;
-      s_carry[w][2][lane] = c;
-      fg_apply(FG{s_agg[w][0][lane], s_agg[w][1][lane], s_agg[w][2][lane], s_agg[w][3][lane]}, m,
-               n, c);
-    }
-    if (DET && id.chunk > 0) {
-      m = carry[0];
-      n = carry[1];
-      c = carry[2];
-      fg_apply(tile_agg, m, n, c);
-    }
-    unsigned long long* ip = incl + (static_cast<size_t>(tile) * 3) * kCB + lane;
-    st_tagged(ip, m, epoch);
-    st_tagged(ip + kCB, n, epoch);
-    st_tagged(ip + 2 * kCB, c, epoch);
-  }
-  __syncthreads();
-
-  // Pass 2: replay the stashed steps from the true carry and write the
-  // trajectory (dead lanes' stores fall outside the resources).
-  float m = s_carry[wave][0][lane], n = s_carry[wave][1][lane], c = s_carry[wave][2][lane];
-  const rsrc_t ro = FULL_OUT ? make_rsrc(out_full + first * row4 + c0, span4)
-                             : make_rsrc(out_h + first * d + c0, span1);
-  auto replay = [&](int s, auto chk) {
-    constexpr bool CHECK = decltype(chk)::value;
-    if (CHECK && hd.at(s)) {
-      float hs[4];
-      head_of(s, hs);
-      c = hs[0];
-      n = hs[1];
-      m = hs[2];
-    }
-    float p[4];
-    Stash::get(stash[s], p);
-    fg_step(p[0], p[1], p[2], m, n, c);
-    // h = sigmoid(z_o) c / (n + eps) with one reciprocal.
-    const float h = c * frcp((1.f + fexp(-p[3])) * (n + eps));
-    if (FULL_OUT) {
-      const uint32_t so = s * row4 * SZ;
-      stb<TX>(ro, voff, so, c);
-      stb<TX>(ro, voff, so + slot, n);
-      stb<TX>(ro, voff, so + 2 * slot, m);
-      stb<TX>(ro, voff, so + 3 * slot, h);
-    } else {
-      stb<TX>(ro, voff, s * d * SZ, h);
-    }
-  };
-  auto run2 = [&](auto chk) {
-    if (n_steps == L) {
-#pragma unroll
-      for (int s = 0; s < L; ++s) replay(s, chk);
-    } else {
-#pragma unroll
-      for (int s = 0; s < L; ++s)
-        if (s < n_steps) replay(s, chk);
-    }
-  };
-  if (PK && hd.mask)
-    run2(std::true_type{});
-  else
-    run2(std::false_type{});
-}
-
-// ---------------------------------------------------------------------------
-// (1b) all frozen-gate passes in one launch (bf16 storage)
-// ---------------------------------------------------------------------------
-//
-// Pass p of the Picard warm start freezes the gates at wx + R * h_{p-1}[t-1]
-// (h_{p-1} the readout of pass p - 1, rounded to bf16 as the reference keeps
-// it in the tensor dtype).  Each tile runs stage p = 0 .. P over its own
-// steps with wx, the stage's pre-activations and its h trajectory held in
-// registers; only the last stage writes the state.  Stage p of a tile needs
-//  * h_{p-1} at the step before the tile: the predecessor tile publishes the
-//    h of its last step after each stage (tagged word, stage-indexed);
-//  * the stage-p carry: a decoupled look-back on stage-indexed tagged words.
-// Both only ever wait on tiles with earlier tickets (already resident or
-// done), so every wave reaches the end.
-template <int L, int W, int WPE, bool DET, bool PK>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) void
-slstm_picard_fused_kernel(
-    const bf16* __restrict__ wx, const bf16* __restrict__ rmix, const bf16* __restrict__ h0,
-    bf16* __restrict__ out, int B, int T, int d, int n_cb, int n_tiles, int P, float eps,
-    int* __restrict__ counter, unsigned long long* __restrict__ agg,
-    unsigned long long* __restrict__ incl, unsigned long long* __restrict__ hlast, int tag_base,
-    Spin spin, Packed pk) {
-  static_assert(L % 2 == 0, "h is packed two steps to a register");
-  constexpr int KP = 2;
-  constexpr uint32_t SZ = 2;
-  __shared__ float s_agg[W][4][kCB];
-  __shared__ float s_carry[W][3][kCB];
-  __shared__ float s_hl[W][kCB];
-  __shared__ float s_tagg[4][kCB];  // the published tile aggregate (wave 0's lanes)
-  __shared__ LookbackShared<FrozenMonoid, W * KP> s_lb;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tile = take_ticket(counter);
-  const TileId id = decode_tile(tile, B, n_cb);
-  const int c0 = id.cb * kCB;
-  const bool live = c0 + lane < d;
-  const int t0 = id.chunk * (W * L) + wave * L;
-  const int n_steps = max(0, min(L, T - t0));
-  const size_t row4 = static_cast<size_t>(4) * d;
-  const size_t first = static_cast<size_t>(id.b) * T + t0;
-  const uint32_t voff = live ? lane * SZ : kOOB;
-  const uint32_t slot = d * SZ;
-  const uint32_t span4 = n_steps > 0 ? ((n_steps - 1) * row4 + 3 * d + (d - c0)) * SZ : 0;
-  const size_t stage_incl = static_cast<size_t>(n_tiles) * 3 * kCB;
-  const size_t stage_agg = static_cast<size_t>(n_tiles) * 4 * kCB;
-  const size_t stage_h = static_cast<size_t>(n_tiles) * kCB;
-
-  float r[4] = {0.f, 0.f, 0.f, 0.f};
-  float h0h = 0.f;  // h_prev at t = 0 in every pass
-  float c_init[3] = {0.f, 0.f, 0.f};  // (m, n, c) carry into time 0
-  if (live) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) r[g] = ld(rmix + g * d + c0 + lane);
-    if (h0 != nullptr) {
-      const bf16* hb = h0 + static_cast<size_t>(id.b) * row4 + c0 + lane;
-      c_init[2] = ld(hb);
-      c_init[1] = ld(hb + d);
-      c_init[0] = ld(hb + 2 * d);
-      h0h = ld(hb + 3 * d);
-    }
-  }
-
-  // Packed sequences: heads among this wave's steps and the initial state
-  // (c, n, m, h) of the first one's sequence (see Packed); a head restarts
-  // the frozen-gate state from it in every stage.
-  Heads hd{0ull, 0};
-  float hst[4] = {0.f, 0.f, 0.f, 0.f};
-  if constexpr (PK) {
-    c_init[0] = c_init[1] = c_init[2] = 0.f;
-    h0h = 0.f;
-    hd = find_heads(pk, t0, n_steps);
-    if (hd.mask) head_state(pk, h0, hd.seq(hd.first()), d, c0 + lane, live, hst);
-  }
-  auto head_of = [&](int s, float st[4]) {
-    if (s == hd.first()) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) st[j] = hst[j];
-    } else {
-      head_state(pk, h0, hd.seq(s), d, c0 + lane, live, st);
-    }
-  };
-
-  uint32_t xw[L][2], pre[L][2], hh[L / 2];
-  {
-    const rsrc_t rx = make_rsrc(wx + first * row4 + c0, span4);
-    auto load = [&](int s) {
-      uint32_t v[4];
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        v[g] = __builtin_amdgcn_raw_buffer_load_b16(rx, voff, s * row4 * SZ + g * slot, 0);
-      xw[s][0] = v[0] | (v[1] << 16);
-      xw[s][1] = v[2] | (v[3] << 16);
-    };
-    if (n_steps == L) {
-#pragma unroll
-      for (int s = 0; s < L; ++s) load(s);
-    } else {
-#pragma unroll
-      for (int s = 0; s < L; ++s)
-        if (s < n_steps) load(s);
-    }
-  }
-  const rsrc_t ro = make_rsrc(out + first * row4 + c0, span4);
-
-  // Stage P, which writes the state, is compiled separately from the others
-  // (no per-step branch between storing the state and keeping h).
-  auto stage = [&](const int p, auto last_c) __attribute__((always_inline)) {
-    constexpr bool last_stage = decltype(last_c)::value;
-    const bool first_stage = p == 0;
-    const int tag = tag_base + p + 1;
-    // Keep wx packed across stages: without this the compiler hoists the
-    // bf16 unpacking out of the stage loop and holds 4 floats per step.
-#pragma unroll
-    for (int s = 0; s < L; ++s) asm volatile("" : "+v"(xw[s][0]), "+v"(xw[s][1]));
-    // h_{p-1} at t0 - 1.
-    float hp0 = 0.f;
-    if (!first_stage) {
-      if (PK && hd.at(0)) {
-        hp0 = hst[3];
-      } else if (t0 == 0) {
-        hp0 = h0h;
-      } else if (wave > 0) {
-        hp0 = s_hl[wave - 1][lane];
-      } else {
-        const unsigned long long* hw =
-            hlast + (p - 1) * stage_h + (static_cast<size_t>(tile) - B * n_cb) * kCB + lane;
-        int spins = 0;
-        bool gave_up = false;
-        while (true) {
-          const bool ok = ld_tagged(hw, tag - 1, hp0);
-          if (__ballot(!ok) == 0ull) break;
-          if (++spins > 8) {
-            if (spins > spin.limit) {  // give up (see Spin)
-              spin_give_up(spin);
-              gave_up = true;
-              break;
-            }
-            __builtin_amdgcn_s_sleep(8);
-          } else {
-            __builtin_amdgcn_s_sleep(1);
-          }
-        }
-        if (gave_up) hp0 = __builtin_nanf("");
-      }
-    }
-
-    // Pass 1: this stage's pre-activations and the segment aggregate.
-    FG a = fg_identity();
-    auto step1 = [&](int s, auto chk) {
-      constexpr bool CHECK = decltype(chk)::value;
-      const bool head = CHECK && hd.at(s);
-      float hs[4];
-      if (head) head_of(s, hs);
-      if (first_stage) {
-        pre[s][0] = xw[s][0];
-        pre[s][1] = xw[s][1];
-      } else {
-        float hp =
-            s == 0 ? hp0 : ((s - 1) & 1 ? hi_bf16(hh[(s - 1) >> 1]) : lo_bf16(hh[(s - 1) >> 1]));
-        if (head) hp = hs[3];
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          // round(R h) and round(wx + round(R h)), two gates per conversion.
-          const uint32_t q = pack_bf16x2(r[2 * k] * hp, r[2 * k + 1] * hp);
-          pre[s][k] = pack_bf16x2(lo_bf16(xw[s][k]) + lo_bf16(q), hi_bf16(xw[s][k]) + hi_bf16(q));
-        }
-      }
-      const float zi = lo_bf16(pre[s][0]), zf = hi_bf16(pre[s][0]), zz = lo_bf16(pre[s][1]);
-      // a head: the segment so far no longer matters (F = -inf), the state
-      // restarts from the sequence's initial one
-      if (head) a = FG{-INFINITY, hs[2], hs[1], hs[0]};
-      a.F += zf;
-      fg_step(zi, zf, zz, a.M, a.N, a.C);
-    };
-    auto run1 = [&](auto chk) {
-      if (n_steps == L) {
-#pragma unroll
-        for (int s = 0; s < L; ++s) step1(s, chk);
-      } else {
-#pragma unroll
-        for (int s = 0; s < L; ++s)
-          if (s < n_steps) step1(s, chk);
-      }
-    };
-    if (PK && hd.mask)
-      run1(std::true_type{});
-    else
-      run1(std::false_type{});
-    s_agg[wave][0][lane] = a.F;
-    s_agg[wave][1][lane] = a.M;
-    s_agg[wave][2][lane] = a.N;
-    s_agg[wave][3][lane] = a.C;
-    // Hold pre packed through the look-back: pass 2 unpacks it again rather
-    // than the compiler keeping four floats per step alive.
-#pragma unroll
-    for (int s = 0; s < L; ++s) asm volatile("" : "+v"(pre[s][0]), "+v"(pre[s][1]));
-    __syncthreads();
-
-    unsigned long long* incl_p = incl + p * stage_incl;
-    unsigned long long* agg_p = agg + p * stage_agg;
-    float carry[3] = {0.f, 0.f, 0.f};
-    if (wave == 0) {
-      FG tile_agg = fg_identity();
-#pragma unroll
-      for (int w = 0; w < W; ++w)
-        tile_agg = fg_compose(tile_agg, FG{s_agg[w][0][lane], s_agg[w][1][lane],
-                                           s_agg[w][2][lane], s_agg[w][3][lane]});
-      if (id.chunk == 0) {
-        carry[0] = c_init[0];
-        carry[1] = c_init[1];
-        carry[2] = c_init[2];
-      } else {
-        unsigned long long* ap = agg_p + (static_cast<size_t>(tile) * 4) * kCB + lane;
-        st_tagged(ap + 0 * kCB, tile_agg.F, tag);
-        st_tagged(ap + 1 * kCB, tile_agg.M, tag);
-        st_tagged(ap + 2 * kCB, tile_agg.N, tag);
-        st_tagged(ap + 3 * kCB, tile_agg.C, tag);
-        if (DET) {
-          s_tagg[0][lane] = tile_agg.F;
-          s_tagg[1][lane] = tile_agg.M;
-          s_tagg[2][lane] = tile_agg.N;
-          s_tagg[3][lane] = tile_agg.C;
-        }
-      }
-    }
-    if (id.chunk > 0)
-      windowed_lookback<FrozenMonoid, W, KP, DET>(
-          id, B, n_cb, tag, incl_p, agg_p, lane, wave, s_lb, carry, spin);
-    if (wave == 0) {
-      float m = carry[0], n = carry[1], c = carry[2];
-#pragma unroll
-      for (int w = 0; w < W; ++w) {
-        s_carry[w][0][lane] = m;
-        s_carry[w][1][lane] = n;
-        s_carry[w][2][lane] = c;
-        fg_apply(FG{s_agg[w][0][lane], s_agg[w][1][lane], s_agg[w][2][lane], s_agg[w][3][lane]},
-                 m, n, c);
-      }
-      if (DET && id.chunk > 0) {
-        m = carry[0];
-        n = carry[1];
-        c = carry[2];
-        fg_apply(FG{s_tagg[0][lane], s_tagg[1][lane], s_tagg[2][lane], s_tagg[3][lane]}, m, n, c);
-      }
-      unsigned long long* ip = incl_p + (static_cast<size_t>(tile) * 3) * kCB + lane;
-      st_tagged(ip, m, tag);
-      st_tagged(ip + kCB, n, tag);
-      st_tagged(ip + 2 * kCB, c, tag);
-    }
-    __syncthreads();
-
-    // Pass 2: replay from the true carry; h (bf16) stays in registers, the
-    // last stage writes the state.
-    float m = s_carry[wave][0][lane], n = s_carry[wave][1][lane], c = s_carry[wave][2][lane];
-    float h_even = 0.f, h_last = 0.f;
-    auto step2 = [&](int s, auto chk) {
-      constexpr bool CHECK = decltype(chk)::value;
-      if (CHECK && hd.at(s)) {
-        float hs[4];
-        head_of(s, hs);
-        c = hs[0];
-        n = hs[1];
-        m = hs[2];
-      }
-      const float zi = lo_bf16(pre[s][0]), zf = hi_bf16(pre[s][0]);
-      const float zz = lo_bf16(pre[s][1]), zo = hi_bf16(pre[s][1]);
-      fg_step(zi, zf, zz, m, n, c);
-      const float h = c * frcp((1.f + fexp(-zo)) * (n + eps));
-      if constexpr (last_stage) {
-        const uint32_t so = s * row4 * SZ;
-        stb<bf16>(ro, voff, so, c);
-        stb<bf16>(ro, voff, so + slot, n);
-        stb<bf16>(ro, voff, so + 2 * slot, m);
-        stb<bf16>(ro, voff, so + 3 * slot, h);
-      } else if (s & 1) {
-        hh[s >> 1] = pack_bf16x2(h_even, h);
-        h_last = hi_bf16(hh[s >> 1]);
-      } else {
-        h_even = h;
-        hh[s >> 1] = pack_bf16x2(h, h);
-        h_last = lo_bf16(hh[s >> 1]);
-      }
-    };
-    auto run2 = [&](auto chk) {
-      if (n_steps == L) {
-#pragma unroll
-        for (int s = 0; s < L; ++s) step2(s, chk);
-      } else {
-#pragma unroll
-        for (int s = 0; s < L; ++s)
-          if (s < n_steps) step2(s, chk);
-      }
-    };
-    if (PK && hd.mask)
-      run2(std::true_type{});
-    else
-      run2(std::false_type{});
-    if constexpr (!last_stage) {
-      s_hl[wave][lane] = h_last;
-      if (wave == W - 1)
-        st_tagged(hlast + p * stage_h + static_cast<size_t>(tile) * kCB + lane, h_last, tag);
-    }
-    __syncthreads();
-  };
-  for (int p = 0; p < P; ++p) stage(p, std::false_type{});
-  stage(P, std::true_type{});
-}
-
-// ---------------------------------------------------------------------------
-// (2) Newton iteration
-// ---------------------------------------------------------------------------
-
-// One Newton iteration over a tile of W waves x L steps x 64 channels.  Pass 1
-// reads each step once (wx and the guess, kept in registers) and folds the
-// lane's affine aggregate x -> J x + F; pass 2 replays the steps from the true
-// carry, delta_t = J_t delta_{t-1} + F_t, and writes H + omega delta.
-template <typename TX, typename TIN, typename TOUT, int L, int W, bool DET, bool PK>
-__global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
-    const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
-    const TIN* __restrict__ hin, TOUT* __restrict__ hout, int B, int T, int d, int n_cb,
-    float omega, float eps, int* __restrict__ counter, unsigned long long* __restrict__ agg,
-    unsigned long long* __restrict__ incl, int epoch, Spin spin, Packed pk) {
-  // predecessors per wave per look-back round (the deterministic walk, which
-  // must find an inclusive carry inside its window, looks twice as far)
-  constexpr int KP = DET ? 2 : 1;
-  using XS = RowStash<TX>;
-  using HS = RowStash<TIN>;
-  __shared__ float s_agg[W][20][kCB];
-  __shared__ float s_carry[W][4][kCB];
-  __shared__ float s_tagg[20][kCB];  // the published tile aggregate (wave 0's lanes)
-  __shared__ LookbackShared<NewtonMonoid, W * KP> s_lb;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tile = take_ticket(counter);
-  const TileId id = decode_tile(tile, B, n_cb);
-  const int c0 = id.cb * kCB;
-  const bool live = c0 + lane < d;
-  const int t0 = id.chunk * (W * L) + wave * L;
-  const int n_steps = max(0, min(L, T - t0));
-  const size_t row4 = static_cast<size_t>(4) * d;
-  const size_t first = static_cast<size_t>(id.b) * T + t0;
-  // Per-slot byte offsets inside a (b, t, 4d) row for each storage type, and
-  // the bytes from the wave's base to its last live element.
-  const uint32_t vx = live ? lane * sizeof(TX) : kOOB;
-  const uint32_t vi = live ? lane * sizeof(TIN) : kOOB;
-  const uint32_t vo = live ? lane * sizeof(TOUT) : kOOB;
-  const size_t span = n_steps > 0 ? (n_steps - 1) * row4 + 3 * d + (d - c0) : 0;
-
-  float r[4] = {0.f, 0.f, 0.f, 0.f};
-  // Linearisation point H_{t0-1}: previous guess, h0 at t = 0, else zeros.
-  float prev0[4] = {0.f, 0.f, 0.f, 0.f};
-  if (live) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) r[g] = ld(rmix + g * d + c0 + lane);
-    if (t0 > 0 && n_steps > 0) {
-      const TIN* p = hin + (first - 1) * row4 + c0 + lane;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) prev0[k] = ld(p + k * d);
-    } else if (t0 == 0 && h0 != nullptr) {
-      const TX* p = h0 + static_cast<size_t>(id.b) * row4 + c0 + lane;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) prev0[k] = ld(p + k * d);
-    }
-  }
-
-  // Packed sequences: heads among this wave's steps (see Packed).
-  Heads hd{0ull, 0};
-  if constexpr (PK) {
-    hd = find_heads(pk, t0, n_steps);
-    if (hd.at(0)) head_state(pk, h0, hd.seq(0), d, c0 + lane, live, prev0);
-  }
-  auto head_prev = [&](int s, float p[4]) { head_state(pk, h0, hd.seq(s), d, c0 + lane, live, p); };
-
-  uint32_t xs[L][XS::N], hs[L][HS::N];
-  // Pass 1: lane segment aggregate (A, b) of the affine maps x -> J x + F.
-  Aff a;
-  aff_identity(a);
-  {
-    const rsrc_t rx = make_rsrc(wx + first * row4 + c0, span * sizeof(TX));
-    const rsrc_t ri = make_rsrc(hin + first * row4 + c0, span * sizeof(TIN));
-    float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
-    auto step = [&](int s, auto chk) {
-      constexpr bool CHECK = decltype(chk)::value;
-      const bool head = CHECK && hd.at(s);
-      XS::load(rx, vx, s * row4 * sizeof(TX), d * sizeof(TX), xs[s]);
-      HS::load(ri, vi, s * row4 * sizeof(TIN), d * sizeof(TIN), hs[s]);
-      if (head && s > 0) head_prev(s, prev);
-      float x[4], hv[4];
-      XS::get(xs[s], x);
-      HS::get(hs[s], hv);
-      CellJ J = cell_jac(prev, x, r, eps);
-      if (head) J.f = J.cm = J.ch = J.nm = J.nh = J.al = J.mh = J.inv = J.dn = J.g = 0.f;
-      const float F[4] = {J.pc - hv[0], J.pn - hv[1], J.pm - hv[2], J.ph - hv[3]};
-      jmv_affine(J, F, a.b);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float col[4] = {a.A[0][j], a.A[1][j], a.A[2][j], a.A[3][j]};
-        jmv(J, col);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) a.A[k][j] = col[k];
-      }
-#pragma unroll
-      for (int k = 0; k < 4; ++k) prev[k] = hv[k];
-    };
-    auto run = [&](auto chk) {
-      if (n_steps == L) {
-#pragma unroll
-        for (int s = 0; s < L; ++s) step(s, chk);
-      } else {
-#pragma unroll
-        for (int s = 0; s < L; ++s)
-          if (s < n_steps) step(s, chk);
-      }
-    };
-    if (PK && hd.mask)
-      run(std::true_type{});
-    else
-      run(std::false_type{});
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    s_agg[wave][16 + i][lane] = a.b[i];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) s_agg[wave][4 * i + j][lane] = a.A[i][j];
-  }
-  __syncthreads();
-
-  float carry[4] = {0.f, 0.f, 0.f, 0.f};  // delta into the tile (delta_{-1} = 0), wave 0
-  if (wave == 0 && id.chunk > 0) {
-    Aff tile_agg;
-    aff_identity(tile_agg);
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      Aff sw;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sw.b[i] = s_agg[w][16 + i][lane];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sw.A[i][j] = s_agg[w][4 * i + j][lane];
-      }
-      tile_agg = w == 0 ? sw : aff_compose(tile_agg, sw);
-    }
-    unsigned long long* ap = agg + (static_cast<size_t>(tile) * 20) * kCB + lane;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (DET) s_tagg[16 + i][lane] = tile_agg.b[i];
-      st_tagged(ap + (16 + i) * kCB, tile_agg.b[i], epoch);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (DET) s_tagg[4 * i + j][lane] = tile_agg.A[i][j];
-        st_tagged(ap + (4 * i + j) * kCB, tile_agg.A[i][j], epoch);
-      }
-    }
-  }
-  if (id.chunk > 0)
-    windowed_lookback<NewtonMonoid, W, KP, DET>(
-          id, B, n_cb, epoch, incl, agg, lane, wave, s_lb, carry, spin);
-  if (wave == 0) {
-    // Carry into each wave's segment, then the tile's outgoing carry (the
-    // published aggregate applied to the carry in, as a successor's walk
-    // would compute it).
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) s_carry[w][k][lane] = carry[k];
-      Aff sw;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sw.b[i] = s_agg[w][16 + i][lane];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sw.A[i][j] = s_agg[w][4 * i + j][lane];
-      }
-      aff_apply(sw, carry);
-    }
-    if (DET && id.chunk > 0) {
-      float a[20];
-#pragma unroll
-      for (int k = 0; k < 20; ++k) a[k] = s_tagg[k][lane];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) carry[k] = s_carry[0][k][lane];
-      NewtonMonoid::apply(a, carry);
-    }
-    unsigned long long* ip = incl + (static_cast<size_t>(tile) * 4) * kCB + lane;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) st_tagged(ip + k * kCB, carry[k], epoch);
-  }
-  __syncthreads();
-
-  // Pass 2: delta_t = J_t delta_{t-1} + F_t from the true carry; H += omega delta.
-  float dl[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) dl[k] = s_carry[wave][k][lane];
-  {
-    const rsrc_t ro = make_rsrc(hout + first * row4 + c0, span * sizeof(TOUT));
-    float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
-    auto replay = [&](int s, auto chk) {
-      constexpr bool CHECK = decltype(chk)::value;
-      if (CHECK && hd.at(s)) {
-        if (s > 0) head_prev(s, prev);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) dl[k] = 0.f;
-      }
-      float x[4], hv[4];
-      XS::get(xs[s], x);
-      HS::get(hs[s], hv);
-      float pv[4], jv[4];
-      cell_jvp(prev, x, r, eps, dl, pv, jv);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) dl[k] = jv[k] + (pv[k] - hv[k]);
-      const uint32_t so = s * row4 * sizeof(TOUT);
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        stb<TOUT>(ro, vo, so + k * d * sizeof(TOUT), hv[k] + omega * dl[k]);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) prev[k] = hv[k];
-    };
-    auto run = [&](auto chk) {
-      if (n_steps == L) {
-#pragma unroll
-        for (int s = 0; s < L; ++s) replay(s, chk);
-      } else {
-#pragma unroll
-        for (int s = 0; s < L; ++s)
-          if (s < n_steps) replay(s, chk);
-      }
-    };
-    if (PK && hd.mask)
-      run(std::true_type{});
-    else
-      run(std::false_type{});
-  }
-}
-
-
-// ---------------------------------------------------------------------------
-// (2b) all K Newton iterations in one launch
-// ---------------------------------------------------------------------------
-//
-// Each tile runs iterations k = 1 .. K over its own steps with wx and the fp32
-// iterate H^(k-1) held in registers; only the last iteration writes the state.
-// Iteration k of a tile needs
-//  * H^(k-1) at the step before the tile: the predecessor tile publishes the
-//    4 slots of its last step after each iteration (tagged words,
-//    iteration-indexed); waves of one tile hand it over through LDS;
-//  * the iteration-k carry: a decoupled look-back on iteration-indexed words.
-// Both only ever wait on tiles with earlier tickets, so every wave reaches the
-// end.  The arithmetic is that of K separate launches exchanging the fp32
-// iterate through memory.
-template <typename TX, int L, int W, int WPE, bool DET, bool PK>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) void
-slstm_newton_fused_kernel(
-    const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
-    const TX* __restrict__ guess, TX* __restrict__ out, int B, int T, int d, int n_cb,
-    int n_tiles, int K, float omega, float eps, int* __restrict__ counter,
-    unsigned long long* __restrict__ agg, unsigned long long* __restrict__ incl,
-    unsigned long long* __restrict__ hlast, int tag_base, Spin spin, Packed pk) {
-  // predecessors per wave per look-back round (the deterministic walk, which
-  // must find an inclusive carry inside its window, looks twice as far)
-  constexpr int KP = DET ? 2 : 1;
-  using XS = RowStash<TX>;
-  __shared__ float s_agg[W][20][kCB];
-  __shared__ float s_carry[W][4][kCB];
-  __shared__ float s_tagg[20][kCB];  // the published tile aggregate (wave 0's lanes)
-  __shared__ float s_hl[W][4][kCB];
-  __shared__ LookbackShared<NewtonMonoid, W * KP> s_lb;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tile = take_ticket(counter);
-  const TileId id = decode_tile(tile, B, n_cb);
-  const int c0 = id.cb * kCB;
-  const bool live = c0 + lane < d;
-  const int t0 = id.chunk * (W * L) + wave * L;
-  const int n_steps = max(0, min(L, T - t0));
-  const size_t row4 = static_cast<size_t>(4) * d;
-  const size_t first = static_cast<size_t>(id.b) * T + t0;
-  const uint32_t vx = live ? lane * sizeof(TX) : kOOB;
-  const size_t span = n_steps > 0 ? (n_steps - 1) * row4 + 3 * d + (d - c0) : 0;
-  const size_t stage_incl = static_cast<size_t>(n_tiles) * 4 * kCB;
-  const size_t stage_agg = static_cast<size_t>(n_tiles) * 20 * kCB;
-  const size_t stage_h = static_cast<size_t>(n_tiles) * 4 * kCB;
-
-  float r[4] = {0.f, 0.f, 0.f, 0.f};
-  float h0v[4] = {0.f, 0.f, 0.f, 0.f};   // linearisation point at t = 0, every iteration
-  float prevg[4] = {0.f, 0.f, 0.f, 0.f};  // the guess at t0 - 1 (iteration 1)
-  if (live) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) r[g] = ld(rmix + g * d + c0 + lane);
-    if (h0 != nullptr) {
-      const TX* p = h0 + static_cast<size_t>(id.b) * row4 + c0 + lane;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) h0v[k] = ld(p + k * d);
-    }
-    if (t0 > 0 && n_steps > 0) {
-      const TX* p = guess + (first - 1) * row4 + c0 + lane;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) prevg[k] = ld(p + k * d);
-    }
-  }
-  if (t0 == 0) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) prevg[k] = h0v[k];
-  }
-  // Packed sequences: the heads among this wave's steps, and the initial
-  // state of the first one's sequence (later heads of the wave load theirs
-  // when they come).
-  Heads hd{0ull, 0};
-  float hst[4] = {0.f, 0.f, 0.f, 0.f};
-  if constexpr (PK) {
-    hd = find_heads(pk, t0, n_steps);
-    if (hd.mask) head_state(pk, h0, hd.seq(hd.first()), d, c0 + lane, live, hst);
-  }
-  auto head_prev = [&](int s, float p[4]) {
-    if (s == hd.first()) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) p[j] = hst[j];
-    } else {
-      head_state(pk, h0, hd.seq(s), d, c0 + lane, live, p);
-    }
-  };
-
-  uint32_t xs[L][XS::N];
-  float hf[L][4];
-  {
-    const rsrc_t rx = make_rsrc(wx + first * row4 + c0, span * sizeof(TX));
-    const rsrc_t rg = make_rsrc(guess + first * row4 + c0, span * sizeof(TX));
-    auto load = [&](int s) {
-      uint32_t gw[XS::N];
-      XS::load(rx, vx, s * row4 * sizeof(TX), d * sizeof(TX), xs[s]);
-      XS::load(rg, vx, s * row4 * sizeof(TX), d * sizeof(TX), gw);
-      XS::get(gw, hf[s]);
-    };
-    if (n_steps == L) {
-#pragma unroll
-      for (int s = 0; s < L; ++s) load(s);
-    } else {
-#pragma unroll
-      for (int s = 0; s < L; ++s)
-        if (s < n_steps) load(s);
-    }
-  }
-  const rsrc_t ro = make_rsrc(out + first * row4 + c0, span * sizeof(TX));
-
-  // Iterations 1 .. K-1 keep the new iterate in registers; the last one,
-  // compiled separately, writes it (no per-step branch on the iteration).
-  auto iterate = [&](const int k, auto last_c) __attribute__((always_inline)) {
-    constexpr bool last_iter = decltype(last_c)::value;
-    const int tag = tag_base + k + 1;
-    // Keep wx packed across iterations (otherwise the unpacking is hoisted out
-    // of the loop and holds 4 floats per step).
-#pragma unroll
-    for (int s = 0; s < L; ++s)
-#pragma unroll
-      for (int q = 0; q < XS::N; ++q) asm volatile("" : "+v"(xs[s][q]));
-    // Linearisation point H^(k-1)_{t0-1}.
-    float prev0[4];
-    if (PK && hd.at(0)) {
-      head_prev(0, prev0);
-    } else if (k == 0 || t0 == 0) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) prev0[j] = prevg[j];
-      if (k > 0) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) prev0[j] = h0v[j];
-      }
-    } else if (wave > 0) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) prev0[j] = s_hl[wave - 1][j][lane];
-    } else {
-      const unsigned long long* hw =
-          hlast + (k - 1) * stage_h + (static_cast<size_t>(tile) - B * n_cb) * 4 * kCB + lane;
-      int spins = 0;
-      bool gave_up = false;
-      while (true) {
-        bool ok = true;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ok = ld_tagged(hw + j * kCB, tag - 1, prev0[j]) && ok;
-        if (__ballot(!ok) == 0ull) break;
-        if (++spins > 8) {
-          if (spins > spin.limit) {  // give up (see Spin)
-            spin_give_up(spin);
-            gave_up = true;
-            break;
-          }
-          __builtin_amdgcn_s_sleep(8);
-        } else {
-          __builtin_amdgcn_s_sleep(1);
-        }
-      }
-      if (gave_up) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) prev0[j] = __builtin_nanf("");
-      }
-    }
-
-    // Pass 1: lane segment aggregate (A, b) of the affine maps x -> J x + F.
-    Aff a;
-    aff_identity(a);
-    {
-      float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
-      auto step = [&](int s, auto chk) {
-        constexpr bool CHECK = decltype(chk)::value;
-        const bool head = CHECK && hd.at(s);
-        if (head && s > 0) head_prev(s, prev);
-        float x[4];
-        XS::get(xs[s], x);
-        CellJ J = cell_jac(prev, x, r, eps);
-        if (head) {
-          // the scan's map at a head is the constant F: no carry crosses it
-          J.f = J.cm = J.ch = J.nm = J.nh = J.al = J.mh = J.inv = J.dn = J.g = 0.f;
-        }
-        const float F[4] = {J.pc - hf[s][0], J.pn - hf[s][1], J.pm - hf[s][2],
-                            J.ph - hf[s][3]};
-        jmv_affine(J, F, a.b);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float col[4] = {a.A[0][j], a.A[1][j], a.A[2][j], a.A[3][j]};
-          jmv(J, col);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) a.A[i][j] = col[i];
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) prev[j] = hf[s][j];
-      };
-      auto run = [&](auto chk) {
-        if (n_steps == L) {
-#pragma unroll
-          for (int s = 0; s < L; ++s) step(s, chk);
-        } else {
-#pragma unroll
-          for (int s = 0; s < L; ++s)
-            if (s < n_steps) step(s, chk);
-        }
-      };
-      if (PK && hd.mask)
-        run(std::true_type{});
-      else
-        run(std::false_type{});
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      s_agg[wave][16 + i][lane] = a.b[i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) s_agg[wave][4 * i + j][lane] = a.A[i][j];
-    }
-    // Hold wx packed through the look-back: pass 2 unpacks it again.
-#pragma unroll
-    for (int s = 0; s < L; ++s)
-#pragma unroll
-      for (int q = 0; q < XS::N; ++q) asm volatile("" : "+v"(xs[s][q]));
-    __syncthreads();
-
-    unsigned long long* incl_k = incl + k * stage_incl;
-    unsigned long long* agg_k = agg + k * stage_agg;
-    float carry[4] = {0.f, 0.f, 0.f, 0.f};
-    if (wave == 0 && id.chunk > 0) {
-      Aff tile_agg;
-      aff_identity(tile_agg);
-#pragma unroll
-      for (int w = 0; w < W; ++w) {
-        Aff sw;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sw.b[i] = s_agg[w][16 + i][lane];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) sw.A[i][j] = s_agg[w][4 * i + j][lane];
-        }
-        tile_agg = w == 0 ? sw : aff_compose(tile_agg, sw);
-      }
-      unsigned long long* ap = agg_k + (static_cast<size_t>(tile) * 20) * kCB + lane;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (DET) s_tagg[16 + i][lane] = tile_agg.b[i];
-        st_tagged(ap + (16 + i) * kCB, tile_agg.b[i], tag);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (DET) s_tagg[4 * i + j][lane] = tile_agg.A[i][j];
-          st_tagged(ap + (4 * i + j) * kCB, tile_agg.A[i][j], tag);
-        }
-      }
-    }
-    if (id.chunk > 0)
-      windowed_lookback<NewtonMonoid, W, KP, DET>(
-          id, B, n_cb, tag, incl_k, agg_k, lane, wave, s_lb, carry, spin);
-    if (wave == 0) {
-      // Per-wave carries; the outgoing carry is the published aggregate
-      // applied to the carry in, as a successor's walk would compute it.
-#pragma unroll
-      for (int w = 0; w < W; ++w) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) s_carry[w][j][lane] = carry[j];
-        Aff sw;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sw.b[i] = s_agg[w][16 + i][lane];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) sw.A[i][j] = s_agg[w][4 * i + j][lane];
-        }
-        aff_apply(sw, carry);
-      }
-      if (DET && id.chunk > 0) {
-        float a[20];
-#pragma unroll
-        for (int k = 0; k < 20; ++k) a[k] = s_tagg[k][lane];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) carry[j] = s_carry[0][j][lane];
-        NewtonMonoid::apply(a, carry);
-      }
-      unsigned long long* ip = incl_k + (static_cast<size_t>(tile) * 4) * kCB + lane;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) st_tagged(ip + j * kCB, carry[j], tag);
-    }
-    __syncthreads();
-
-    // Pass 2: delta_t = J_t delta_{t-1} + F_t from the true carry; the new
-    // iterate H + omega delta stays in registers (written by the last one).
-    float dl[4], hl[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) dl[j] = s_carry[wave][j][lane];
-    {
-      float prev[4] = {prev0[0], prev0[1], prev0[2], prev0[3]};
-      auto replay = [&](int s, auto chk) {
-        constexpr bool CHECK = decltype(chk)::value;
-        if (CHECK && hd.at(s)) {
-          // a head: previous state h0 of its sequence, no incoming delta
-          if (s > 0) head_prev(s, prev);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) dl[j] = 0.f;
-        }
-        float x[4], hv[4];
-        XS::get(xs[s], x);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) hv[j] = hf[s][j];
-        float pv[4], jv[4];
-        cell_jvp(prev, x, r, eps, dl, pv, jv);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          dl[j] = jv[j] + (pv[j] - hv[j]);
-          hl[j] = hv[j] + omega * dl[j];
-          prev[j] = hv[j];
-        }
-        if constexpr (last_iter) {
-          const uint32_t so = s * row4 * sizeof(TX);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) stb<TX>(ro, vx, so + j * d * sizeof(TX), hl[j]);
-        } else {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) hf[s][j] = hl[j];
-        }
-      };
-      auto run = [&](auto chk) {
-        if (n_steps == L) {
-#pragma unroll
-          for (int s = 0; s < L; ++s) replay(s, chk);
-        } else {
-#pragma unroll
-          for (int s = 0; s < L; ++s)
-            if (s < n_steps) replay(s, chk);
-        }
-      };
-      if (PK && hd.mask)
-        run(std::true_type{});
-      else
-        run(std::false_type{});
-    }
-    if constexpr (!last_iter) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) s_hl[wave][j][lane] = hl[j];
-      if (wave == W - 1) {
-        unsigned long long* hw = hlast + k * stage_h + static_cast<size_t>(tile) * 4 * kCB + lane;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) st_tagged(hw + j * kCB, hl[j], tag);
-      }
-    }
-    __syncthreads();
-  };
-  for (int k = 0; k < K - 1; ++k) iterate(k, std::false_type{});
-  iterate(K - 1, std::true_type{});
-}
-
-}  // namespace slstm
-}  // namespace prnn
 
 // ===========================================================================
 // Host entry points
@@ -1254,13 +21,8 @@ namespace slstm {
 // always runs the default shapes (the only ones instantiated for it).
 // bf16 frozen tiles stash 2 registers per step, fp32 ones 4 (one fp32 shape).
 static const Shape kFrozenShapes[] = {{64, 4}, {32, 8}, {32, 4}, {64, 2}};
-constexpr Shape kFrozenDefault{64, 4};
-constexpr Shape kFrozenF32{32, 4};
 // Newton tiles stash wx and the guess: 4 to 6 registers per step in bf16, 8 in fp32.
 static const Shape kNewtonShapes[] = {{32, 8}, {32, 4}, {24, 4}, {16, 8}, {64, 4}};
-constexpr Shape kNewtonGuessDefault{32, 4};
-constexpr Shape kNewtonWorkDefault{24, 4};
-constexpr Shape kNewtonF32{16, 8};
 
 struct Tiles {
   Shape frozen;
@@ -1311,7 +73,6 @@ static bool picard_fused(int dtype) {
 // Shapes of the fused launch: wx, the stage's pre-activations and h stay in
 // registers (4.5 per step).  PRNN_SLSTM_PICARD_TILES="<L>x<W>" for tuning.
 static const Shape kPicardShapes[] = {{24, 4}, {16, 4}, {20, 4}, {32, 4}};
-constexpr Shape kPicardDefault{24, 4};
 
 static Shape picard_shape() {
   static const Shape s = [] {
@@ -1345,17 +106,13 @@ static InitWs carve_init(void* base, int B, int T, int d, int P, int dtype, size
   if (w.fused) {
     // Stage-indexed look-back words (a tile may run stages ahead of the
     // tiles that still read its earlier stages), cleared with the counters.
-    Geo g = geometry(B, T, d, picard_shape());
-    const Geo gd = geometry(B, T, d, kPicardDefault);
-    if (gd.n_tiles > g.n_tiles) g = gd;
+    const Geo g = geometry(B, T, d, packed ? kPicardPacked : picard_shape());
     w.lb = carve_lookback(cv, g, 3 * (P + 1), 4 * (P + 1));
     w.hlast = static_cast<unsigned long long*>(
         cv.take(sizeof(unsigned long long) * static_cast<size_t>(P) * kCB * g.n_tiles));
     w.lb.clear_words = (cv.used - (reinterpret_cast<char*>(w.lb.counters) - cv.base)) / sizeof(int);
   } else {
-    Geo g = geometry(B, T, d, frozen_shape(dtype));
-    const Geo gd = geometry(B, T, d, dtype == PRNN_BF16 ? kFrozenDefault : kFrozenF32);
-    if (gd.n_tiles > g.n_tiles) g = gd;
+    const Geo g = geometry(B, T, d, packed ? kFrozenPackedF32 : frozen_shape(dtype));
     w.lb = carve_lookback(cv, g, 3, 4);
     const size_t hb = static_cast<size_t>(B) * T * d * elem_size(dtype);
     w.hbuf[0] = P >= 1 ? cv.take(hb) : nullptr;
@@ -1381,8 +138,6 @@ static bool newton_fused(int K) {
 // and the fp32 iterate (4) stay in registers.
 // PRNN_SLSTM_NEWTON_FUSED_TILES="<L>x<W>" for tuning (bf16).
 static const Shape kNewtonFusedShapes[] = {{20, 4}, {16, 4}, {24, 4}, {16, 8}};
-constexpr Shape kNewtonFusedDefault{20, 4};
-constexpr Shape kNewtonFusedF32{16, 4};
 
 static Shape newton_fused_shape(int dtype) {
   static const Shape s = [] {
@@ -1417,7 +172,9 @@ static NewtonWs carve_newton(void* base, int B, int T, int d, int K, int dtype, 
   if (w.fused) {
     // Iteration-indexed look-back words (a tile may run iterations ahead of
     // the tiles that still read its earlier ones), cleared with the counters.
-    const Geo g = geometry(B, T, d, newton_fused_shape(dtype));
+    const Geo g = geometry(B, T, d,
+                           !packed ? newton_fused_shape(dtype)
+                           : dtype == PRNN_BF16 ? kNewtonFusedPacked : kNewtonFusedPackedF32);
     w.lb = carve_lookback(cv, g, 4 * K, 20 * K);
     w.hlast = static_cast<unsigned long long*>(
         cv.take(sizeof(unsigned long long) * static_cast<size_t>(K - 1) * 4 * kCB * g.n_tiles));
@@ -1429,8 +186,8 @@ static NewtonWs carve_newton(void* base, int B, int T, int d, int K, int dtype, 
   // largest tile count of the shapes a launch may take.
   const Geo g1 = geometry(B, T, d, newton_shape(dtype, false));
   const Geo g2 = geometry(B, T, d, newton_shape(dtype, true));
-  const Geo g3 = geometry(B, T, d, dtype == PRNN_BF16 ? kNewtonGuessDefault : kNewtonF32);
-  const Geo g4 = geometry(B, T, d, dtype == PRNN_BF16 ? kNewtonWorkDefault : kNewtonF32);
+  const Geo g3 = geometry(B, T, d, dtype == PRNN_BF16 ? kNewtonPackedGuess : kNewtonPackedF32);
+  const Geo g4 = geometry(B, T, d, dtype == PRNN_BF16 ? kNewtonPackedWork : kNewtonPackedF32);
   Geo g = g1.n_tiles >= g2.n_tiles ? g1 : g2;
   if (g3.n_tiles > g.n_tiles) g = g3;
   if (g4.n_tiles > g.n_tiles) g = g4;
@@ -1442,11 +199,12 @@ static NewtonWs carve_newton(void* base, int B, int T, int d, int K, int dtype, 
   return w;
 }
 
-template <typename TX, int L, int W, bool DET, bool PK = false>
+template <typename TX, int L, int W, bool DET>
 static void launch_frozen(bool has_h, bool full_out, const TX* wx, const TX* r, const TX* h0,
                           const TX* src, TX* out_full, TX* out_h, int B, int T, int d, float eps,
-                          const Lookback& lb, int epoch, hipStream_t stream,
-                          const Packed& pk = Packed{nullptr, nullptr, 0}) {
+                          const Lookback& lb, int epoch, hipStream_t stream) {
+  constexpr bool PK = false;
+  const Packed pk{nullptr, nullptr, 0};
   const Geo g = geometry(B, T, d, Shape{L, W});
   const dim3 grid(g.n_tiles), block(64 * W);
   int* ctr = lb.counters + epoch;
@@ -1471,13 +229,9 @@ static void frozen_pass(bool has_h, bool full_out, const TX* wx, const TX* r, co
                                        d, eps, lb, epoch, stream)
   if constexpr (sizeof(TX) == 4) {
     // packed streams: fp32 only (bf16 takes the single-launch warm start)
-    if (pk.cu != nullptr) {
-      if (deterministic())
-        return launch_frozen<TX, kFrozenF32.L, kFrozenF32.W, true, true>(
-            has_h, full_out, wx, r, h0, src, out_full, out_h, B, T, d, eps, lb, epoch, stream, pk);
-      return launch_frozen<TX, kFrozenF32.L, kFrozenF32.W, false, true>(
-          has_h, full_out, wx, r, h0, src, out_full, out_h, B, T, d, eps, lb, epoch, stream, pk);
-    }
+    if (pk.cu != nullptr)
+      return launch_frozen_packed(has_h, full_out, wx, r, h0, src, out_full, out_h, T, d, eps,
+                                  lb, epoch, stream, pk);
     if (deterministic()) PRNN_LAUNCH(kFrozenF32.L, kFrozenF32.W, true);
     PRNN_LAUNCH(kFrozenF32.L, kFrozenF32.W, false);
   } else {
@@ -1503,20 +257,17 @@ static int run_init(const TX* wx, const TX* r, const TX* h0, TX* states, int B, 
     if (w.fused) {
       const Shape sh = pk.cu != nullptr ? kPicardDefault : picard_shape();
       const Geo g = geometry(B, T, d, sh);
-#define PRNN_LAUNCH_P(LL, WW, WPE, DD, PP)                                                       \
-  slstm_picard_fused_kernel<LL, WW, WPE, DD, PP>                                                 \
+#define PRNN_LAUNCH(LL, WW, WPE, DD)                                                             \
+  slstm_picard_fused_kernel<LL, WW, WPE, DD, false>                                              \
       <<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>(                                           \
           wx, r, h0, states, B, T, d, g.n_cb, g.n_tiles, P, eps, w.lb.counters + 1, w.lb.agg,   \
-          w.lb.incl, w.hlast, w.lb.tag_base, w.lb.spin(), pk)
-#define PRNN_LAUNCH(LL, WW, WPE, DD) PRNN_LAUNCH_P(LL, WW, WPE, DD, false)
+          w.lb.incl, w.hlast, w.lb.tag_base, w.lb.spin(), Packed{nullptr, nullptr, 0})
 #define PRNN_SHAPE(LL, WW, WPE) \
   else if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, WPE, false);
       static_assert(kPicardDefault.L == 24 && kPicardDefault.W == 4, "default Picard shape");
       timing_begin(stream);
-      if (pk.cu != nullptr) {
-        if (deterministic()) PRNN_LAUNCH_P(24, 4, 3, true, true);
-        else PRNN_LAUNCH_P(24, 4, 3, false, true);
-      }
+      if (pk.cu != nullptr)
+        launch_picard_packed(wx, r, h0, states, T, d, P, eps, w.lb, w.hlast, stream, pk);
       else if (deterministic()) PRNN_LAUNCH(24, 4, 3, true);
       PRNN_SHAPE(24, 4, 3)
       PRNN_SHAPE(16, 4, 4)
@@ -1524,7 +275,6 @@ static int run_init(const TX* wx, const TX* r, const TX* h0, TX* states, int B, 
       PRNN_SHAPE(32, 4, 2)
 #undef PRNN_SHAPE
 #undef PRNN_LAUNCH
-#undef PRNN_LAUNCH_P
       timing_end(stream);
       PRNN_HIP(hipGetLastError());
       return PRNN_OK;
@@ -1583,26 +333,6 @@ static void launch_newton(const TX* wx, const TX* r, const TX* h0, const TIN* hi
 #undef PRNN_LAUNCH
 }
 
-// One Newton iteration on a packed stream (B = 1): default tile shapes.
-template <typename TX, typename TIN, typename TOUT>
-static void launch_newton_packed(const TX* wx, const TX* r, const TX* h0, const TIN* hin,
-                                 TOUT* hout, int T, int d, float omega, float eps,
-                                 const Lookback& lb, int epoch, hipStream_t stream,
-                                 const Packed& pk) {
-  constexpr Shape sh = sizeof(TX) == 4 ? kNewtonF32
-                       : sizeof(TIN) == 4 ? kNewtonWorkDefault : kNewtonGuessDefault;
-  const Geo g = geometry(1, T, d, sh);
-#define PRNN_LAUNCH(DD)                                                                     \
-  slstm_newton_kernel<TX, TIN, TOUT, sh.L, sh.W, DD, true>                                  \
-      <<<dim3(g.n_tiles), dim3(64 * sh.W), 0, stream>>>(                                    \
-          wx, r, h0, hin, hout, 1, T, d, g.n_cb, omega, eps, lb.counters + epoch, lb.agg, \
-          lb.incl, lb.tag_base + epoch, lb.spin(), pk)
-  if (deterministic())
-    PRNN_LAUNCH(true);
-  else
-    PRNN_LAUNCH(false);
-#undef PRNN_LAUNCH
-}
 
 template <typename TX>
 static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, TX* out, int B,
@@ -1618,26 +348,19 @@ static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, 
   if (w.fused) {
     const Shape sh = newton_fused_shape(sizeof(TX) == 2 ? PRNN_BF16 : PRNN_F32);
     const Geo g = geometry(B, T, d, sh);
-#define PRNN_LAUNCH_P(LL, WW, WPE, DD, PP)                                                       \
-  slstm_newton_fused_kernel<TX, LL, WW, WPE, DD, PP>                                             \
+#define PRNN_LAUNCH(LL, WW, WPE, DD)                                                             \
+  slstm_newton_fused_kernel<TX, LL, WW, WPE, DD, false>                                          \
       <<<dim3(g.n_tiles), dim3(64 * WW), 0, stream>>>(                                           \
           wx, r, h0, guess, out, B, T, d, g.n_cb, g.n_tiles, K, omega, eps, w.lb.counters + 1,   \
-          w.lb.agg, w.lb.incl, w.hlast, w.lb.tag_base, w.lb.spin(), pk)
-#define PRNN_LAUNCH(LL, WW, WPE, DD) PRNN_LAUNCH_P(LL, WW, WPE, DD, false)
+          w.lb.agg, w.lb.incl, w.hlast, w.lb.tag_base, w.lb.spin(), Packed{nullptr, nullptr, 0})
 #define PRNN_SHAPE(LL, WW, WPE) \
   else if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, WPE, false);
     static_assert(kNewtonFusedF32.L == 16 && kNewtonFusedF32.W == 4, "fp32 fused shape");
     static_assert(kNewtonFusedDefault.L == 20 && kNewtonFusedDefault.W == 4, "default shape");
     timing_begin(stream);
     if (pk.cu != nullptr) {
-      // packed sequences: default shapes only
-      if constexpr (sizeof(TX) == 4) {
-        if (deterministic()) PRNN_LAUNCH_P(16, 4, 2, true, true);
-        else PRNN_LAUNCH_P(16, 4, 2, false, true);
-      } else {
-        if (deterministic()) PRNN_LAUNCH_P(20, 4, 2, true, true);
-        else PRNN_LAUNCH_P(20, 4, 2, false, true);
-      }
+      launch_newton_fused_packed<TX>(wx, r, h0, guess, out, T, d, K, omega, eps, w.lb, w.hlast,
+                                     stream, pk);
     } else if constexpr (sizeof(TX) == 4) {
       if (deterministic()) PRNN_LAUNCH(16, 4, 2, true);
       PRNN_SHAPE(16, 4, 2)
@@ -1650,7 +373,6 @@ static int run_newton(const TX* wx, const TX* r, const TX* h0, const TX* guess, 
     }
 #undef PRNN_SHAPE
 #undef PRNN_LAUNCH
-#undef PRNN_LAUNCH_P
     timing_end(stream);
     PRNN_HIP(hipGetLastError());
     return PRNN_OK;
