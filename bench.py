@@ -223,8 +223,11 @@ def ragged_decode(torch, reps: int):
     """The packed-ragged and T=1 rows beside the metric (not bench lines of
     their own): ParaSLSTM diag d=1024 bf16, K=2, P=5.
     - ragged: one sequence of 65536 steps and 63 of 1024 packed into
-      (1, N, d), newton_apply end to end (GEMM included), with the length
-      groups and as one padded rectangle (PARARNN_AMD_RAGGED_GROUPS=0);
+      (1, N, d), newton_apply end to end (GEMM included): packed in-kernel
+      (the default: head flags cut the carry), by length groups
+      (PARARNN_AMD_PACKED=0) and as one padded rectangle (also
+      PARARNN_AMD_RAGGED_GROUPS=0); beside them one unbroken stream of the
+      same N tokens, the rate the packed path is held to;
     - decode: one step for 64 rows from a resident state and wx, eager and
       replayed from a captured HIP graph."""
     import os
@@ -241,20 +244,27 @@ def ragged_decode(torch, reps: int):
     x = torch.randn(1, n, D, generator=g, device=dev).to(torch.bfloat16)
     cfg = NewtonConfig(max_iters=K, picard_iters=P, residual_atol=None, residual_fail=None,
                        picard_adapt=False)
-    prev = os.environ.get("PARARNN_AMD_RAGGED_GROUPS")
+    keys = ("PARARNN_AMD_PACKED", "PARARNN_AMD_RAGGED_GROUPS")
+    prev = {k: os.environ.get(k) for k in keys}
     res = {}
     try:
         with torch.no_grad():
-            for mode, key in (("1", "grouped"), ("0", "one_rectangle")):
-                os.environ["PARARNN_AMD_RAGGED_GROUPS"] = mode
-                ms = _time(torch, lambda: newton_apply(cell, x, cfg, cu_seqlens=cs),
-                           reps if mode == "1" else 2, warm=1)
+            for packed, groups, key, nrep in (("1", "1", "packed", reps),
+                                              ("0", "1", "grouped", reps),
+                                              ("0", "0", "one_rectangle", 2)):
+                os.environ["PARARNN_AMD_PACKED"] = packed
+                os.environ["PARARNN_AMD_RAGGED_GROUPS"] = groups
+                ms = _time(torch, lambda: newton_apply(cell, x, cfg, cu_seqlens=cs), nrep, warm=1)
                 res[key] = {"ms": ms, "tokens_per_s": n / (ms * 1e-3)}
+            ms = _time(torch, lambda: newton_apply(cell, x, cfg), reps, warm=1)
+            res["same_tokens_one_stream"] = {"ms": ms, "tokens_per_s": n / (ms * 1e-3)}
     finally:
-        if prev is None:
-            os.environ.pop("PARARNN_AMD_RAGGED_GROUPS", None)
-        else:
-            os.environ["PARARNN_AMD_RAGGED_GROUPS"] = prev
+        for k, v in prev.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    res["packed_vs_one_stream"] = res["same_tokens_one_stream"]["ms"] / res["packed"]["ms"]
     ragged = {"workload": f"ParaSLSTM diag d=1024 bf16 K=2 P=5, cu_seqlens 1x65536 + 63x1024 "
                           f"(N={n}), newton_apply", **res}
 

@@ -1246,7 +1246,7 @@ constexpr Shape kNewtonFusedF32{16, 4};
 // the kernels free of register spills.
 constexpr Shape kPicardPacked{20, 4};
 constexpr Shape kFrozenPackedF32{32, 4};
-constexpr Shape kNewtonFusedPacked{16, 4};
+constexpr Shape kNewtonFusedPacked{20, 4};
 constexpr Shape kNewtonFusedPackedF32{12, 4};
 constexpr Shape kNewtonPackedGuess{16, 4};
 constexpr Shape kNewtonPackedWork{16, 4};

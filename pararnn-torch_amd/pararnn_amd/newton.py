@@ -449,7 +449,7 @@ def _newton_packed(cell, x, config, *, h0, stats, cu_seqlens, block_table, needs
     rows of a pool when given), as the reference's packed semantics
     (solvers/scan.py:206-216, layout.py:115-138); K, P, the Picard ladder and
     the residual gate act on the packed stream (newton/__init__.py:327-355)."""
-    cs = validate_cu_seqlens(cu_seqlens, x.shape[1]).to(x.device)
+    cs = validate_cu_seqlens(cu_seqlens, x.shape[1], x.device)
     n_seq = int(cs.numel()) - 1
     if block_table is None and h0 is not None and h0.shape[0] != n_seq:
         raise ValueError(f"h0 batch {h0.shape[0]} != n_seq {n_seq}")

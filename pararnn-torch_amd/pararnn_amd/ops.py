@@ -162,7 +162,8 @@ def _packed_args(cu_seqlens: Tensor | None, block_table: Tensor | None, wx: Tens
             raise ValueError(f"block_table B={int(bt.numel())} != {n_seq}")
         if h0.shape[1:] != (4, d_h):
             raise ValueError(f"pool h0 tail {tuple(h0.shape[1:])} != {(4, d_h)}")
-        mn, mx = int(bt.min()), int(bt.max())
+        host = bt.cpu()
+        mn, mx = int(host.min()), int(host.max())
         if mn < 0 or mx >= int(h0.shape[0]):
             raise ValueError(f"block_table slots [{mn}, {mx}] outside pool capacity "
                              f"{int(h0.shape[0])}")

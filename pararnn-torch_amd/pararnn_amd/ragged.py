@@ -3,12 +3,19 @@
 The reference packs S sequences into one stream ``(1, N, ...)`` with
 FlashAttention-style offsets ``cu_seqlens`` ``(S+1,)`` and drops the carry at
 each sequence head (J = 0 there, ``h0[s]`` as the previous state;
-``layout.py:93-138``, ``solvers/scan.py:206-216``).  Sequences never interact,
-so this build runs them as a padded rectangular batch ``(S, T_max, ...)``
-through the same fused kernels: every sequence starts from its own ``h0``
-exactly as at a head, positions past a sequence's end are computed and
-discarded (they come after it in time, so they cannot reach it), and the
-result is gathered back into the packed order.  Padding and gathering are
+``layout.py:93-138``, ``solvers/scan.py:206-216``).
+
+The diag-sLSTM kernels do exactly that on the packed stream itself (head
+flags inside the scans, ``block_table`` read by the kernels; see
+``ops.slstm_init_fused`` / ``ops.newton_slstm_fused``).  This module holds the
+host rules shared by every path (offset checks, the ragged prepend, the
+``block_table`` gather) and the padded route that the other cells take, and
+the diag sLSTM with ``PARARNN_AMD_PACKED=0``: sequences never interact, so
+they can run as a padded rectangular batch ``(S, T_max, ...)`` through the
+same fused kernels.  Every sequence then starts from its own ``h0`` exactly
+as at a head, positions past a sequence's end are computed and discarded
+(they come after it in time, so they cannot reach it), and the result is
+gathered back into the packed order.  Padding and gathering are
 differentiable index operations, so the eq. 2.6 backward runs unchanged (the
 upstream gradient at discarded positions is zero, so nothing flows from them).
 
@@ -24,23 +31,43 @@ group (at most ``log2(T_max / 256) + 2`` groups).
 from __future__ import annotations
 
 import os
+import weakref
 
 import torch
 from torch import Tensor
 
 
-def validate_cu_seqlens(cu_seqlens: Tensor, time: int) -> Tensor:
+# The last offsets that passed the checks: weak references to the tensor given
+# and to the int64 one returned, each with its version counter (bumped by every
+# in-place write), so the solve and the ops it calls check one stream once,
+# with one device-to-host copy.
+_checked: tuple[tuple[tuple[weakref.ref, int], ...], int] | None = None
+
+
+def _known(t: Tensor, time: int) -> bool:
+    c = _checked
+    return c is not None and c[1] == time and any(r() is t and v == t._version for r, v in c[0])
+
+
+def validate_cu_seqlens(cu_seqlens: Tensor, time: int,
+                        device: torch.device | None = None) -> Tensor:
     """``(S+1,)`` exclusive prefix with ``[0] = 0``, last = ``time``, strictly increasing
-    (layout.py:93-104)."""
+    (layout.py:93-104); returned as int64 on ``device`` (default: where it is)."""
+    global _checked
     if cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2:
         raise ValueError(f"cu_seqlens must be (S+1,), got {tuple(cu_seqlens.shape)}")
-    cs = cu_seqlens.to(dtype=torch.long)
-    if int(cs[0]) != 0:
-        raise ValueError(f"cu_seqlens[0] must be 0, got {int(cs[0])}")
-    if int(cs[-1]) != int(time):
-        raise ValueError(f"cu_seqlens[-1] must equal time={time}, got {int(cs[-1])}")
-    if torch.any(cs[1:] <= cs[:-1]):
+    cs = cu_seqlens.to(dtype=torch.long, device=device or cu_seqlens.device)
+    if _known(cu_seqlens, time) or _known(cs, time):
+        return cs
+    host = cs.cpu()
+    if int(host[0]) != 0:
+        raise ValueError(f"cu_seqlens[0] must be 0, got {int(host[0])}")
+    if int(host[-1]) != int(time):
+        raise ValueError(f"cu_seqlens[-1] must equal time={time}, got {int(host[-1])}")
+    if bool((host[1:] <= host[:-1]).any()):
         raise ValueError("cu_seqlens must be strictly increasing")
+    _checked = (tuple((weakref.ref(t), t._version) for t in {id(cu_seqlens): cu_seqlens,
+                                                             id(cs): cs}.values()), int(time))
     return cs
 
 

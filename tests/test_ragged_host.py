@@ -115,3 +115,19 @@ def test_ragged_plan_packed_order(lengths, monkeypatch):
     single = RaggedPlan(cs, torch.device("cpu"))
     assert single.n_groups == 1 and single.padded_steps == len(lengths) * max(lengths)
     assert torch.equal(single.run(packed.detach(), h0, _solve_marker), want)
+
+
+def test_validated_offsets_are_checked_again_after_a_write():
+    """The solve checks one stream once; an in-place write to the offsets (or
+    another length) makes the next call check them again."""
+    cs = torch.tensor([0, 3, 7], dtype=torch.int32)
+    out = validate_cu_seqlens(cs, 7)
+    assert out.dtype == torch.long and out.tolist() == [0, 3, 7]
+    assert validate_cu_seqlens(out, 7) is out
+    cs[1] = 9
+    with pytest.raises(ValueError, match="strictly increasing"):
+        validate_cu_seqlens(cs, 7)
+    cs[1] = 3
+    validate_cu_seqlens(cs, 7)
+    with pytest.raises(ValueError, match="must equal time"):
+        validate_cu_seqlens(cs, 8)
