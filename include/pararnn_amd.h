@@ -8,9 +8,10 @@
  * 256-byte aligned), and every entry point only enqueues work on `stream`.
  * Calls that share one workspace must not overlap in time.
  *
- * dtype codes: PRNN_F32 (float32) and PRNN_BF16 (bfloat16 storage).  All
- * arithmetic is fp32; bf16 tensors are widened on load and rounded (nearest
- * even) on store.
+ * dtype codes: PRNN_F32 (float32), PRNN_BF16 (bfloat16 storage) and PRNN_F16
+ * (float16 storage; kernels/precision.py:20-34 admits the same three).  All
+ * arithmetic is fp32; 16-bit tensors are widened on load and rounded (nearest
+ * even) on store, at the rounding points of the reference in that dtype.
  *
  * Return codes: PRNN_OK, or an error whose message prnn_last_error() returns
  * (thread-local).  The Python shim maps PRNN_ERR_VALUE -> ValueError,
@@ -53,7 +54,7 @@ extern "C" {
 
 #define PRNN_API __attribute__((visibility("default")))
 
-enum { PRNN_F32 = 0, PRNN_BF16 = 1 };
+enum { PRNN_F32 = 0, PRNN_BF16 = 1, PRNN_F16 = 2 };
 enum { PRNN_OK = 0, PRNN_ERR_VALUE = 1, PRNN_ERR_TYPE = 2, PRNN_ERR_RUNTIME = 3 };
 
 /* Library ABI version (bumped on any signature change). */

@@ -4,7 +4,7 @@
 // (or the pool slot block_table[b]), the recurrent parameters (clamped to
 // +-cap in-kernel, as the reference does so a captured graph allocates
 // nothing) and the step's wx, and write the next state row.  fp32 algebra,
-// bf16 widened on load and rounded on store.
+// 16-bit storage (bf16, fp16) widened on load and rounded on store.
 //
 //  slstm_decode_kernel     ParaSLSTM mix='diag': one thread per channel.
 //  gru_diag_decode_kernel  ParaGRU mix='diag': one thread per channel.
@@ -114,8 +114,7 @@ __global__ __launch_bounds__(64) void gru_head_decode_kernel(
 
 static int check(int B, int d, int dtype) {
   if (B < 1 || d < 1) return fail(PRNN_ERR_VALUE, "B and d must be >= 1, got B=%d d=%d", B, d);
-  if (dtype != PRNN_F32 && dtype != PRNN_BF16)
-    return fail(PRNN_ERR_TYPE, "dtype code %d is not float32 (0) or bfloat16 (1)", dtype);
+  if (check_dtype(dtype) != PRNN_OK) return PRNN_ERR_TYPE;
   if (B > 65535) return fail(PRNN_ERR_VALUE, "batch %d exceeds 65535", B);
   return PRNN_OK;
 }
@@ -135,14 +134,13 @@ extern "C" PRNN_API int prnn_slstm_decode(const void* state, const void* wx, con
     return fail(PRNN_ERR_VALUE, "state, wx, r and out must be non-null");
   const dim3 grid((d + 255) / 256, B);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == PRNN_F32)
-    decode::slstm_decode_kernel<float><<<grid, dim3(256), 0, s>>>(
-        static_cast<const float*>(state), static_cast<const float*>(wx),
-        static_cast<const float*>(r), static_cast<float*>(out), block_table, d, eps, cap, has_cap);
-  else
-    decode::slstm_decode_kernel<bf16><<<grid, dim3(256), 0, s>>>(
-        static_cast<const bf16*>(state), static_cast<const bf16*>(wx),
-        static_cast<const bf16*>(r), static_cast<bf16*>(out), block_table, d, eps, cap, has_cap);
+  with_storage(dtype, [&](auto tag) {
+    using TX = decltype(tag);
+    decode::slstm_decode_kernel<TX><<<grid, dim3(256), 0, s>>>(
+        static_cast<const TX*>(state), static_cast<const TX*>(wx), static_cast<const TX*>(r),
+        static_cast<TX*>(out), block_table, d, eps, cap, has_cap);
+    return PRNN_OK;
+  });
   PRNN_HIP(hipGetLastError());
   return PRNN_OK;
 }
@@ -161,30 +159,24 @@ extern "C" PRNN_API int prnn_gru_decode(const void* h, const void* wx, const voi
       return fail(PRNN_ERR_TYPE, "head decode needs d_head = 64, got d=%d n_heads=%d", d,
                   n_heads);
     const dim3 grid(n_heads, B);
-    if (dtype == PRNN_F32)
-      decode::gru_head_decode_kernel<float><<<grid, dim3(64), 0, s>>>(
-          static_cast<const float*>(h), static_cast<const float*>(wx),
-          static_cast<const float*>(a_z), static_cast<const float*>(a_r),
-          static_cast<const float*>(a_n), static_cast<float*>(out), block_table, n_heads, cap,
-          has_cap);
-    else
-      decode::gru_head_decode_kernel<bf16><<<grid, dim3(64), 0, s>>>(
-          static_cast<const bf16*>(h), static_cast<const bf16*>(wx),
-          static_cast<const bf16*>(a_z), static_cast<const bf16*>(a_r),
-          static_cast<const bf16*>(a_n), static_cast<bf16*>(out), block_table, n_heads, cap,
-          has_cap);
+    with_storage(dtype, [&](auto tag) {
+      using TX = decltype(tag);
+      decode::gru_head_decode_kernel<TX><<<grid, dim3(64), 0, s>>>(
+          static_cast<const TX*>(h), static_cast<const TX*>(wx), static_cast<const TX*>(a_z),
+          static_cast<const TX*>(a_r), static_cast<const TX*>(a_n), static_cast<TX*>(out),
+          block_table, n_heads, cap, has_cap);
+      return PRNN_OK;
+    });
   } else {
     const dim3 grid((d + 255) / 256, B);
-    if (dtype == PRNN_F32)
-      decode::gru_diag_decode_kernel<float><<<grid, dim3(256), 0, s>>>(
-          static_cast<const float*>(h), static_cast<const float*>(wx),
-          static_cast<const float*>(a_z), static_cast<const float*>(a_r),
-          static_cast<const float*>(a_n), static_cast<float*>(out), block_table, d, cap, has_cap);
-    else
-      decode::gru_diag_decode_kernel<bf16><<<grid, dim3(256), 0, s>>>(
-          static_cast<const bf16*>(h), static_cast<const bf16*>(wx),
-          static_cast<const bf16*>(a_z), static_cast<const bf16*>(a_r),
-          static_cast<const bf16*>(a_n), static_cast<bf16*>(out), block_table, d, cap, has_cap);
+    with_storage(dtype, [&](auto tag) {
+      using TX = decltype(tag);
+      decode::gru_diag_decode_kernel<TX><<<grid, dim3(256), 0, s>>>(
+          static_cast<const TX*>(h), static_cast<const TX*>(wx), static_cast<const TX*>(a_z),
+          static_cast<const TX*>(a_r), static_cast<const TX*>(a_n), static_cast<TX*>(out),
+          block_table, d, cap, has_cap);
+      return PRNN_OK;
+    });
   }
   PRNN_HIP(hipGetLastError());
   return PRNN_OK;

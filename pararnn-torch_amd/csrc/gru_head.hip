@@ -113,15 +113,15 @@ __device__ __forceinline__ Gates gates_step(float* s_h, float* s_u, float hp_j, 
   return g;
 }
 
-// 4 consecutive values of storage type T as floats / from floats (bf16: RNE).
+// 4 consecutive values of storage type T as floats / from floats (16-bit: RNE).
 template <typename T>
 __device__ __forceinline__ void st4(T* p, floatx4 v) {
   if constexpr (sizeof(T) == 4) {
     *reinterpret_cast<floatx4*>(p) = v;
   } else {
     uint2 w;
-    w.x = pack_bf16x2(v[0], v[1]);
-    w.y = pack_bf16x2(v[2], v[3]);
+    w.x = Narrow<T>::pack(v[0], v[1]);
+    w.y = Narrow<T>::pack(v[2], v[3]);
     *reinterpret_cast<uint2*>(p) = w;
   }
 }
@@ -132,7 +132,8 @@ __device__ __forceinline__ floatx4 ld4(const T* p) {
     return *reinterpret_cast<const floatx4*>(p);
   } else {
     const uint2 w = *reinterpret_cast<const uint2*>(p);
-    return floatx4{lo_bf16(w.x), hi_bf16(w.x), lo_bf16(w.y), hi_bf16(w.y)};
+    return floatx4{Narrow<T>::lo(w.x), Narrow<T>::hi(w.x), Narrow<T>::lo(w.y),
+                   Narrow<T>::hi(w.y)};
   }
 }
 
@@ -1695,8 +1696,7 @@ static int check(int B, int T, int H, int dh, int K, int dtype) {
     return fail(PRNN_ERR_VALUE, "B, T, n_heads must be >= 1, got B=%d T=%d n_heads=%d", B, T, H);
   if (dh != DH) return fail(PRNN_ERR_TYPE, "d_head must be %d, got %d", DH, dh);
   if (K < 0) return fail(PRNN_ERR_VALUE, "max_iters must be >= 0, got %d", K);
-  if (dtype != PRNN_F32 && dtype != PRNN_BF16)
-    return fail(PRNN_ERR_TYPE, "dtype code %d is not float32 (0) or bfloat16 (1)", dtype);
+  if (check_dtype(dtype) != PRNN_OK) return PRNN_ERR_TYPE;
   if (static_cast<long long>(B) * H * ((T + kChunk - 1) / kChunk) > (1ll << 30))
     return fail(PRNN_ERR_VALUE, "problem too large");
   return PRNN_OK;
@@ -1730,15 +1730,13 @@ extern "C" PRNN_API int prnn_gru_head_newton(const void* wx, const void* a_z, co
   if (workspace_bytes < need)
     return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == PRNN_F32)
-    return gru::run(static_cast<const float*>(wx), static_cast<const float*>(a_z),
-                    static_cast<const float*>(a_r), static_cast<const float*>(a_n),
-                    static_cast<const float*>(h0), static_cast<float*>(out), B, T, n_heads,
-                    max_iters, omega, w, s);
-  return gru::run(static_cast<const bf16*>(wx), static_cast<const bf16*>(a_z),
-                  static_cast<const bf16*>(a_r), static_cast<const bf16*>(a_n),
-                  static_cast<const bf16*>(h0), static_cast<bf16*>(out), B, T, n_heads,
-                  max_iters, omega, w, s);
+  return with_storage(dtype, [&](auto tag) {
+    using TX = decltype(tag);
+    return gru::run(static_cast<const TX*>(wx), static_cast<const TX*>(a_z),
+                    static_cast<const TX*>(a_r), static_cast<const TX*>(a_n),
+                    static_cast<const TX*>(h0), static_cast<TX*>(out), B, T, n_heads, max_iters,
+                    omega, w, s);
+  });
 }
 
 extern "C" PRNN_API size_t prnn_gru_head_backward_workspace_size(int B, int T, int n_heads,
@@ -1766,16 +1764,13 @@ extern "C" PRNN_API int prnn_gru_head_backward(const void* wx, const void* a_z, 
   if (workspace_bytes < need)
     return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == PRNN_F32)
-    return gru::run_bwd(static_cast<const float*>(wx), static_cast<const float*>(a_z),
-                        static_cast<const float*>(a_r), static_cast<const float*>(a_n),
-                        static_cast<const float*>(h0), static_cast<const float*>(states),
-                        static_cast<const float*>(grad), static_cast<float*>(g_wx), g_a, g_h0, B,
-                        T, n_heads, w, s);
-  return gru::run_bwd(static_cast<const bf16*>(wx), static_cast<const bf16*>(a_z),
-                      static_cast<const bf16*>(a_r), static_cast<const bf16*>(a_n),
-                      static_cast<const bf16*>(h0), static_cast<const bf16*>(states),
-                      static_cast<const bf16*>(grad), static_cast<bf16*>(g_wx), g_a, g_h0, B, T,
-                      n_heads, w, s);
+  return with_storage(dtype, [&](auto tag) {
+    using TX = decltype(tag);
+    return gru::run_bwd(static_cast<const TX*>(wx), static_cast<const TX*>(a_z),
+                        static_cast<const TX*>(a_r), static_cast<const TX*>(a_n),
+                        static_cast<const TX*>(h0), static_cast<const TX*>(states),
+                        static_cast<const TX*>(grad), static_cast<TX*>(g_wx), g_a, g_h0, B, T,
+                        n_heads, w, s);
+  });
 }
 

@@ -1,6 +1,7 @@
 // Shared device helpers for the pararnn_amd HIP kernels (gfx950 / CDNA4).
 //
-// * bf16 storage as raw 16-bit words with round-to-nearest-even conversion;
+// * bf16 and fp16 storage as raw 16-bit words with round-to-nearest-even
+//   conversion;
 // * transcendentals built on the hardware v_exp_f32 / v_rcp_f32 instructions;
 // * the decoupled look-back's tagged words (device-coherent atomics);
 // * buffer-resource loads / stores with wave-uniform offsets, and packed bf16.
@@ -14,10 +15,18 @@ namespace prnn {
 struct bf16 {
   uint16_t bits;
 };
+// IEEE binary16 storage (the algebra stays fp32; 65504 is the largest finite
+// value, so wider values round to +-inf as in the tensor dtype).
+struct f16 {
+  uint16_t bits;
+};
 
 __device__ __forceinline__ float to_f32(float v) { return v; }
 __device__ __forceinline__ float to_f32(bf16 v) {
   return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
+}
+__device__ __forceinline__ float to_f32(f16 v) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, v.bits));
 }
 
 template <typename T>
@@ -31,12 +40,22 @@ __device__ __forceinline__ bf16 from_f32<bf16>(float v) {
   return bf16{__builtin_bit_cast(uint16_t, h)};
 }
 
+template <>
+__device__ __forceinline__ f16 from_f32<f16>(float v) {
+  return f16{__builtin_bit_cast(uint16_t, static_cast<_Float16>(v))};
+}
+
 // Value after a round trip through storage type T (identity for fp32).
 template <typename T>
 __device__ __forceinline__ float round_to(float v) { return to_f32(from_f32<T>(v)); }
 template <>
 __device__ __forceinline__ float round_to<bf16>(float v) {
   return static_cast<float>(static_cast<__bf16>(v));
+}
+
+template <>
+__device__ __forceinline__ float round_to<f16>(float v) {
+  return static_cast<float>(static_cast<_Float16>(v));
 }
 
 template <typename T>
@@ -139,7 +158,13 @@ __device__ __forceinline__ uint32_t ldb_bits(bf16*, rsrc_t r, uint32_t voff, uin
 __device__ __forceinline__ uint32_t ldb_bits(float*, rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
 }
+__device__ __forceinline__ uint32_t ldb_bits(f16*, rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
 __device__ __forceinline__ float bits_to_f32(bf16*, uint32_t b) { return __uint_as_float(b << 16); }
+__device__ __forceinline__ float bits_to_f32(f16*, uint32_t b) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+}
 __device__ __forceinline__ float bits_to_f32(float*, uint32_t b) { return __uint_as_float(b); }
 
 template <typename T>
@@ -151,6 +176,10 @@ __device__ __forceinline__ void stb(rsrc_t r, uint32_t voff, uint32_t soff, floa
 template <>
 __device__ __forceinline__ void stb<bf16>(rsrc_t r, uint32_t voff, uint32_t soff, float v) {
   __builtin_amdgcn_raw_buffer_store_b16(from_f32<bf16>(v).bits, r, voff, soff, 0);
+}
+template <>
+__device__ __forceinline__ void stb<f16>(rsrc_t r, uint32_t voff, uint32_t soff, float v) {
+  __builtin_amdgcn_raw_buffer_store_b16(from_f32<f16>(v).bits, r, voff, soff, 0);
 }
 template <>
 __device__ __forceinline__ void stb<float>(rsrc_t r, uint32_t voff, uint32_t soff, float v) {
@@ -166,5 +195,42 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 __device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2_t{lo, hi}, f16x2_t));
+}
+__device__ __forceinline__ float lo_f16(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w)));
+}
+__device__ __forceinline__ float hi_f16(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+}
+
+// Two values of a 16-bit storage type in one register (low | high << 16):
+// pack rounds two floats (RNE), lo / hi read one back exactly, and val reads
+// one zero-extended raw storage word.
+template <typename T>
+struct Narrow;
+
+template <>
+struct Narrow<bf16> {
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
+    return pack_bf16x2(lo, hi);
+  }
+  static __device__ __forceinline__ float lo(uint32_t w) { return lo_bf16(w); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return hi_bf16(w); }
+  static __device__ __forceinline__ float val(uint32_t bits) { return __uint_as_float(bits << 16); }
+};
+
+template <>
+struct Narrow<f16> {
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
+    return pack_f16x2(lo, hi);
+  }
+  static __device__ __forceinline__ float lo(uint32_t w) { return lo_f16(w); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return hi_f16(w); }
+  static __device__ __forceinline__ float val(uint32_t bits) { return lo_f16(bits); }
+};
 
 }  // namespace prnn

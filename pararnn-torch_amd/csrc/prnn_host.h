@@ -9,6 +9,7 @@
 #include <stdio.h>
 
 #include "pararnn_amd.h"
+#include "prnn_common.h"
 
 namespace prnn {
 
@@ -21,6 +22,22 @@ inline int fail(int code, const char* fmt, ...) {
   vsnprintf(last_error_buffer(), 512, fmt, ap);
   va_end(ap);
   return code;
+}
+
+// f(TX{}) with TX the storage type of a checked dtype code.
+template <typename F>
+inline int with_storage(int dtype, F&& f) {
+  if (dtype == PRNN_F32) return f(float{});
+  if (dtype == PRNN_F16) return f(f16{});
+  return f(bf16{});
+}
+
+// The dtype check every entry point runs.
+inline int check_dtype(int dtype) {
+  if (dtype != PRNN_F32 && dtype != PRNN_BF16 && dtype != PRNN_F16)
+    return fail(PRNN_ERR_TYPE, "dtype code %d is not float32 (0), bfloat16 (1) or float16 (2)",
+                dtype);
+  return PRNN_OK;
 }
 
 inline int hip_fail(hipError_t e, const char* what) {

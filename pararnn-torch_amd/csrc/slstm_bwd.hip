@@ -408,8 +408,9 @@ static Shape bwd_shape(int dtype) {
     }
     return r;
   }();
-  if (dtype != PRNN_BF16) return kBwdF32;
-  return deterministic() ? kBwdDefault : s;
+  if (!narrow(dtype)) return kBwdF32;
+  // fp16 storage is compiled in the default shape only
+  return deterministic() || dtype == PRNN_F16 ? kBwdDefault : s;
 }
 
 struct BwdWs {
@@ -420,7 +421,7 @@ struct BwdWs {
 static BwdWs carve_bwd(void* base, int B, int T, int d, int dtype, size_t* total) {
   // the packed launch takes the default shape: size for both
   Geo g = geometry(B, T, d, bwd_shape(dtype));
-  const Geo gd = geometry(B, T, d, dtype == PRNN_BF16 ? kBwdDefault : kBwdF32);
+  const Geo gd = geometry(B, T, d, narrow(dtype) ? kBwdDefault : kBwdF32);
   if (gd.n_tiles > g.n_tiles) g = gd;
   Carver cv(base);
   BwdWs w;
@@ -468,10 +469,11 @@ static int run_bwd(const TX* wx, const TX* r, const TX* h0, const TX* states, co
     else
       PRNN_LAUNCH(kBwdF32.L, kBwdF32.W, false);
   } else {
-    sh = bwd_shape(PRNN_BF16);
+    sh = bwd_shape(dtype_code<TX>());
 #define PRNN_SHAPE(LL, WW) \
   else if (sh.L == LL && sh.W == WW) PRNN_LAUNCH(LL, WW, false);
     if (deterministic()) PRNN_LAUNCH(kBwdDefault.L, kBwdDefault.W, true);
+    else if constexpr (std::is_same<TX, f16>::value) PRNN_LAUNCH(kBwdDefault.L, kBwdDefault.W, false);
     PRNN_SHAPE(16, 8)
     PRNN_SHAPE(16, 4)
     PRNN_SHAPE(24, 4)
@@ -521,15 +523,13 @@ int backward_call(const void* wx, const void* r, const void* h0, const void* sta
     return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
   w.lb.tag_base = tag_base;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == PRNN_F32)
-    return slstm::run_bwd(static_cast<const float*>(wx), static_cast<const float*>(r),
-                          static_cast<const float*>(h0), static_cast<const float*>(states),
-                          static_cast<const float*>(grad), static_cast<float*>(gwx), gr, gh0, gb,
-                          B, T, d, eps, w, s, pk);
-  return slstm::run_bwd(static_cast<const bf16*>(wx), static_cast<const bf16*>(r),
-                        static_cast<const bf16*>(h0), static_cast<const bf16*>(states),
-                        static_cast<const bf16*>(grad), static_cast<bf16*>(gwx), gr, gh0, gb, B, T,
-                        d, eps, w, s, pk);
+  return with_storage(dtype, [&](auto tag) {
+    using TX = decltype(tag);
+    return slstm::run_bwd(static_cast<const TX*>(wx), static_cast<const TX*>(r),
+                          static_cast<const TX*>(h0), static_cast<const TX*>(states),
+                          static_cast<const TX*>(grad), static_cast<TX*>(gwx), gr, gh0, gb, B, T,
+                          d, eps, w, s, pk);
+  });
 }
 
 }  // namespace

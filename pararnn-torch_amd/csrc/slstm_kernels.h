@@ -109,13 +109,12 @@ struct FrozenMonoid {
 };
 
 // Pre-activations of a tile's steps, held in registers between the two
-// passes.  In bf16 they are exact bf16 values (wx, or wx + R h_prev rounded as
-// the reference's two torch ops), packed two to a register.
+// passes.  With 16-bit storage they are exact values of the storage type (wx,
+// or wx + R h_prev rounded as the reference's two torch ops), packed two to a
+// register.
 template <typename TX>
-struct PreStash;
-
-template <>
-struct PreStash<bf16> {
+struct PreStash {
+  using NT = Narrow<TX>;
   static constexpr int N = 2;  // registers per step: (z_i, z_f), (z_z, z_o)
   template <bool HAS_H>
   static __device__ __forceinline__ void make(const uint32_t x[4], const float r[4], float hp,
@@ -128,16 +127,15 @@ struct PreStash<bf16> {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       // round(R h) and round(wx + round(R h)), two gates per conversion.
-      const uint32_t q = pack_bf16x2(r[2 * k] * hp, r[2 * k + 1] * hp);
-      w[k] = pack_bf16x2(__uint_as_float(x[2 * k] << 16) + lo_bf16(q),
-                         __uint_as_float(x[2 * k + 1] << 16) + hi_bf16(q));
+      const uint32_t q = NT::pack(r[2 * k] * hp, r[2 * k + 1] * hp);
+      w[k] = NT::pack(NT::val(x[2 * k]) + NT::lo(q), NT::val(x[2 * k + 1]) + NT::hi(q));
     }
   }
   static __device__ __forceinline__ void get(const uint32_t w[N], float p[4]) {
-    p[0] = lo_bf16(w[0]);
-    p[1] = hi_bf16(w[0]);
-    p[2] = lo_bf16(w[1]);
-    p[3] = hi_bf16(w[1]);
+    p[0] = NT::lo(w[0]);
+    p[1] = NT::hi(w[0]);
+    p[2] = NT::lo(w[1]);
+    p[3] = NT::hi(w[1]);
   }
 };
 
@@ -353,11 +351,11 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// (1b) all frozen-gate passes in one launch (bf16 storage)
+// (1b) all frozen-gate passes in one launch (16-bit storage: bf16 or fp16)
 // ---------------------------------------------------------------------------
 //
 // Pass p of the Picard warm start freezes the gates at wx + R * h_{p-1}[t-1]
-// (h_{p-1} the readout of pass p - 1, rounded to bf16 as the reference keeps
+// (h_{p-1} the readout of pass p - 1, rounded to the storage type as the reference keeps
 // it in the tensor dtype).  Each tile runs stage p = 0 .. P over its own
 // steps with wx, the stage's pre-activations and its h trajectory held in
 // registers; only the last stage writes the state.  Stage p of a tile needs
@@ -366,15 +364,17 @@ __global__ __launch_bounds__(64 * W) void slstm_frozen_kernel(
 //  * the stage-p carry: a decoupled look-back on stage-indexed tagged words.
 // Both only ever wait on tiles with earlier tickets (already resident or
 // done), so every wave reaches the end.
-template <int L, int W, int WPE, bool DET, bool PK>
+template <typename TN, int L, int W, int WPE, bool DET, bool PK>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) void
 slstm_picard_fused_kernel(
-    const bf16* __restrict__ wx, const bf16* __restrict__ rmix, const bf16* __restrict__ h0,
-    bf16* __restrict__ out, int B, int T, int d, int n_cb, int n_tiles, int P, float eps,
+    const TN* __restrict__ wx, const TN* __restrict__ rmix, const TN* __restrict__ h0,
+    TN* __restrict__ out, int B, int T, int d, int n_cb, int n_tiles, int P, float eps,
     int* __restrict__ counter, unsigned long long* __restrict__ agg,
     unsigned long long* __restrict__ incl, unsigned long long* __restrict__ hlast, int tag_base,
     Spin spin, Packed pk) {
   static_assert(L % 2 == 0, "h is packed two steps to a register");
+  static_assert(sizeof(TN) == 2, "16-bit storage");
+  using NT = Narrow<TN>;
   constexpr int KP = 2;
   constexpr uint32_t SZ = 2;
   __shared__ float s_agg[W][4][kCB];
@@ -406,7 +406,7 @@ slstm_picard_fused_kernel(
 #pragma unroll
     for (int g = 0; g < 4; ++g) r[g] = ld(rmix + g * d + c0 + lane);
     if (h0 != nullptr) {
-      const bf16* hb = h0 + static_cast<size_t>(id.b) * row4 + c0 + lane;
+      const TN* hb = h0 + static_cast<size_t>(id.b) * row4 + c0 + lane;
       c_init[2] = ld(hb);
       c_init[1] = ld(hb + d);
       c_init[0] = ld(hb + 2 * d);
@@ -459,7 +459,7 @@ slstm_picard_fused_kernel(
     const bool first_stage = p == 0;
     const int tag = tag_base + p + 1;
     // Keep wx packed across stages: without this the compiler hoists the
-    // bf16 unpacking out of the stage loop and holds 4 floats per step.
+    // 16-bit unpacking out of the stage loop and holds 4 floats per step.
 #pragma unroll
     for (int s = 0; s < L; ++s) asm volatile("" : "+v"(xw[s][0]), "+v"(xw[s][1]));
     // h_{p-1} at t0 - 1.
@@ -506,16 +506,16 @@ slstm_picard_fused_kernel(
         pre[s][1] = xw[s][1];
       } else {
         float hp =
-            s == 0 ? hp0 : ((s - 1) & 1 ? hi_bf16(hh[(s - 1) >> 1]) : lo_bf16(hh[(s - 1) >> 1]));
+            s == 0 ? hp0 : ((s - 1) & 1 ? NT::hi(hh[(s - 1) >> 1]) : NT::lo(hh[(s - 1) >> 1]));
         if (head) hp = head_h(s);
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
           // round(R h) and round(wx + round(R h)), two gates per conversion.
-          const uint32_t q = pack_bf16x2(r[2 * k] * hp, r[2 * k + 1] * hp);
-          pre[s][k] = pack_bf16x2(lo_bf16(xw[s][k]) + lo_bf16(q), hi_bf16(xw[s][k]) + hi_bf16(q));
+          const uint32_t q = NT::pack(r[2 * k] * hp, r[2 * k + 1] * hp);
+          pre[s][k] = NT::pack(NT::lo(xw[s][k]) + NT::lo(q), NT::hi(xw[s][k]) + NT::hi(q));
         }
       }
-      const float zi = lo_bf16(pre[s][0]), zf = hi_bf16(pre[s][0]), zz = lo_bf16(pre[s][1]);
+      const float zi = NT::lo(pre[s][0]), zf = NT::hi(pre[s][0]), zz = NT::lo(pre[s][1]);
       // a head: the segment so far no longer matters (F = -inf), the state
       // restarts from the sequence's initial one
       if (head) {
@@ -603,7 +603,7 @@ slstm_picard_fused_kernel(
     }
     __syncthreads();
 
-    // Pass 2: replay from the true carry; h (bf16) stays in registers, the
+    // Pass 2: replay from the true carry; h (storage type) stays in registers, the
     // last stage writes the state.
     float m = s_carry[wave][0][lane], n = s_carry[wave][1][lane], c = s_carry[wave][2][lane];
     float h_even = 0.f, h_last = 0.f;
@@ -616,23 +616,23 @@ slstm_picard_fused_kernel(
         n = hs[1];
         m = hs[2];
       }
-      const float zi = lo_bf16(pre[s][0]), zf = hi_bf16(pre[s][0]);
-      const float zz = lo_bf16(pre[s][1]), zo = hi_bf16(pre[s][1]);
+      const float zi = NT::lo(pre[s][0]), zf = NT::hi(pre[s][0]);
+      const float zz = NT::lo(pre[s][1]), zo = NT::hi(pre[s][1]);
       fg_step(zi, zf, zz, m, n, c);
       const float h = c * frcp((1.f + fexp(-zo)) * (n + eps));
       if constexpr (last_stage) {
         const uint32_t so = s * row4 * SZ;
-        stb<bf16>(ro, voff, so, c);
-        stb<bf16>(ro, voff, so + slot, n);
-        stb<bf16>(ro, voff, so + 2 * slot, m);
-        stb<bf16>(ro, voff, so + 3 * slot, h);
+        stb<TN>(ro, voff, so, c);
+        stb<TN>(ro, voff, so + slot, n);
+        stb<TN>(ro, voff, so + 2 * slot, m);
+        stb<TN>(ro, voff, so + 3 * slot, h);
       } else if (s & 1) {
-        hh[s >> 1] = pack_bf16x2(h_even, h);
-        h_last = hi_bf16(hh[s >> 1]);
+        hh[s >> 1] = NT::pack(h_even, h);
+        h_last = NT::hi(hh[s >> 1]);
       } else {
         h_even = h;
-        hh[s >> 1] = pack_bf16x2(h, h);
-        h_last = lo_bf16(hh[s >> 1]);
+        hh[s >> 1] = NT::pack(h, h);
+        h_last = NT::lo(hh[s >> 1]);
       }
     };
     auto run2 = [&](auto chk) {
@@ -1254,7 +1254,8 @@ constexpr Shape kNewtonPackedF32{8, 8};
 
 // Packed-stream launches (B = 1, default shapes), compiled in their own
 // translation unit (slstm_packed.hip).
-void launch_picard_packed(const bf16* wx, const bf16* r, const bf16* h0, bf16* out, int T, int d,
+template <typename TN>
+void launch_picard_packed(const TN* wx, const TN* r, const TN* h0, TN* out, int T, int d,
                           int P, float eps, const Lookback& lb, unsigned long long* hlast,
                           hipStream_t stream, const Packed& pk);
 void launch_frozen_packed(bool has_h, bool full_out, const float* wx, const float* r,

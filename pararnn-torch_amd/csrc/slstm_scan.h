@@ -18,6 +18,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 namespace prnn {
 namespace slstm {
 
@@ -520,12 +522,9 @@ struct NewtonMonoid {
 };
 
 // Raw storage words of a tile's steps, held in registers between the two
-// passes: bf16 values packed two to a register, fp32 values one each.
+// passes: 16-bit values packed two to a register, fp32 values one each.
 template <typename T>
-struct RowStash;
-
-template <>
-struct RowStash<bf16> {
+struct RowStash {
   static constexpr int N = 2;
   // Slot g of the row at byte offset soff (+ g * slot bytes, wave-uniform).
   static __device__ __forceinline__ void load(rsrc_t rs, uint32_t voff, uint32_t soff,
@@ -538,10 +537,10 @@ struct RowStash<bf16> {
     w[1] = v[2] | (v[3] << 16);
   }
   static __device__ __forceinline__ void get(const uint32_t w[N], float p[4]) {
-    p[0] = lo_bf16(w[0]);
-    p[1] = hi_bf16(w[0]);
-    p[2] = lo_bf16(w[1]);
-    p[3] = hi_bf16(w[1]);
+    p[0] = Narrow<T>::lo(w[0]);
+    p[1] = Narrow<T>::hi(w[0]);
+    p[2] = Narrow<T>::lo(w[1]);
+    p[3] = Narrow<T>::hi(w[1]);
   }
 };
 
@@ -585,15 +584,20 @@ static Geo geometry(int B, int T, int d, Shape sh) {
   return g;
 }
 
-static size_t elem_size(int dtype) { return dtype == PRNN_BF16 ? 2 : 4; }
+// bf16 and fp16 storage: 16-bit words, fp32 algebra, the same kernels.
+static bool narrow(int dtype) { return dtype != PRNN_F32; }
+static size_t elem_size(int dtype) { return narrow(dtype) ? 2 : 4; }
+template <typename TX>
+constexpr int dtype_code() {
+  return sizeof(TX) == 4 ? PRNN_F32 : std::is_same<TX, f16>::value ? PRNN_F16 : PRNN_BF16;
+}
 
 static int check_dims(int B, int T, int d, int dtype) {
   if (B < 1 || T < 1 || d < 1)
     return fail(PRNN_ERR_VALUE, "B, T, d must be >= 1, got B=%d T=%d d=%d", B, T, d);
   // A wave addresses its steps with 32-bit buffer offsets.
   if (d >= (1 << 20)) return fail(PRNN_ERR_VALUE, "d must be < 2^20, got %d", d);
-  if (dtype != PRNN_F32 && dtype != PRNN_BF16)
-    return fail(PRNN_ERR_TYPE, "dtype code %d is not float32 (0) or bfloat16 (1)", dtype);
+  if (check_dtype(dtype) != PRNN_OK) return PRNN_ERR_TYPE;
   const long long tiles = static_cast<long long>(B) * ((d + kCB - 1) / kCB) * T;
   if (tiles > (1ll << 30))
     return fail(PRNN_ERR_VALUE, "problem too large: B*T*ceil(d/64) = %lld", tiles);

@@ -15,6 +15,7 @@ from pararnn_amd._build import LIB_PATH
 
 PRNN_F32 = 0
 PRNN_BF16 = 1
+PRNN_F16 = 2
 PRNN_OK = 0
 PRNN_ERR_VALUE = 1
 PRNN_ERR_TYPE = 2

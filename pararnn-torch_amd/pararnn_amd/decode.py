@@ -26,7 +26,8 @@ from pararnn_amd.ops import _ptr, _stream, _validate
 
 def can_decode_step(cell: nn.Module, ref: Tensor) -> bool:
     """Whether ``decode_step`` runs the HIP kernel for ``cell`` on ``ref``'s device/dtype."""
-    if ref.device.type != "cuda" or ref.dtype not in (torch.float32, torch.bfloat16):
+    if ref.device.type != "cuda" or ref.dtype not in (torch.float32, torch.bfloat16,
+                                                      torch.float16):
         return False
     if isinstance(cell, ParaSLSTM):
         return cell.mix == "diag"

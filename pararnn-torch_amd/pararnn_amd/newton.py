@@ -79,7 +79,7 @@ def auto_newton_iters(cell: nn.Module, seq_len: int, *, schedule=None) -> int:
 
 
 def _fusable(cell: nn.Module, x: Tensor) -> bool:
-    if x.device.type != "cuda" or x.dtype not in (torch.float32, torch.bfloat16):
+    if x.device.type != "cuda" or x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
         return False
     if isinstance(cell, ParaSLSTM):
         return cell.mix == "diag"
@@ -91,7 +91,7 @@ def _fusable(cell: nn.Module, x: Tensor) -> bool:
 def _fused_error(cell: nn.Module, x: Tensor) -> str:
     return (
         "scan_backend='fused' in pararnn_amd needs ParaSLSTM(mix='diag') or "
-        "ParaGRU(mix='head', d_head <= 64) on a ROCm GPU in float32/bfloat16 "
+        "ParaGRU(mix='head', d_head <= 64) on a ROCm GPU in float32/bfloat16/float16 "
         f"(got {type(cell).__name__}(mix={getattr(cell, 'mix', None)!r}) "
         f"{x.dtype} on {x.device})"
     )

@@ -24,12 +24,13 @@ from torch import Tensor
 from pararnn_amd import _lib
 from pararnn_amd.head_blocks import HeadBlocks
 
-_DTYPES = {torch.float32: _lib.PRNN_F32, torch.bfloat16: _lib.PRNN_BF16}
+_DTYPES = {torch.float32: _lib.PRNN_F32, torch.bfloat16: _lib.PRNN_BF16,
+           torch.float16: _lib.PRNN_F16}
 
 
 def _validate(name: str, *tensors: Tensor | None) -> int:
     """Device/dtype rules of the reference's ``validate_cuda_tensors``
-    (kernels/precision.py:40-68): one GPU device, one dtype, float32/bfloat16."""
+    (kernels/precision.py:40-68): one GPU device, one dtype, float32/bfloat16/float16."""
     ts = [t for t in tensors if t is not None]
     ref = ts[0]
     for t in ts:
@@ -40,7 +41,7 @@ def _validate(name: str, *tensors: Tensor | None) -> int:
         if t.dtype != ref.dtype:
             raise TypeError(f"{name}: dtype mismatch {t.dtype} vs {ref.dtype}")
     if ref.dtype not in _DTYPES:
-        raise TypeError(f"{name} supports float32/bfloat16, got {ref.dtype}")
+        raise TypeError(f"{name} supports float32/bfloat16/float16, got {ref.dtype}")
     return _DTYPES[ref.dtype]
 
 

@@ -8,7 +8,7 @@ script therefore imports the reference ONCE, in the build container (never on
 the GPU box), and stores small safetensors fixtures next to itself.  The
 fixtures are data only: inputs, weights and the reference's outputs.
 
-Run:  PYTHONPATH=/root/reference/src python tests/golden/make_golden.py
+Run:  PYTHONPATH=/root/reference/src python tests/golden/make_golden.py [case ...]
 
 Reference call sites exercised (paths relative to the reference's src/pararnn):
   solvers/newton/__init__.py:212 newton_apply   (scan_backend='eager')
@@ -361,46 +361,80 @@ def auto_picard_table():
     return {str(t): slstm_auto_picard(t) for t in (1, 64, 65, 2048, 2049, 16384, 131072)}
 
 
-def main() -> int:
-    torch.set_num_threads(8)
-    parts_case()
+CASES = {
+    "parts": parts_case,
     # BASELINE config 1, the reference's CPU-runnable parity case.
-    slstm_case("slstm_cfg1_fp32", d_in=64, d=64, B=2, T=1024, K=2, P=3,
-               dtype=torch.float32, seed=0, keep_wx=False)
-    slstm_case("slstm_h0_fp32", d_in=24, d=32, B=2, T=200, K=3, P=1,
-               dtype=torch.float32, seed=5, with_h0=True)
-    slstm_case("slstm_bf16", d_in=64, d=64, B=2, T=512, K=2, P=3,
-               dtype=torch.bfloat16, seed=1)
-    slstm_case("slstm_long_fp32", d_in=16, d=16, B=1, T=4096, K=2, P=5,
-               dtype=torch.float32, seed=2, x_std=0.5)
-    gru_head_case("gru_head_fp32", d_in=64, n_heads=2, d_head=64, B=2, T=256, K=3,
-                  dtype=torch.float32, seed=3)
-    gru_head_case("gru_head_h0_fp32", d_in=32, n_heads=2, d_head=64, B=1, T=96, K=3,
-                  dtype=torch.float32, seed=4, with_h0=True)
-    gru_head_case("gru_head_bf16", d_in=64, n_heads=2, d_head=64, B=1, T=128, K=3,
-                  dtype=torch.bfloat16, seed=6)
-    bwd_parts_case()
-    slstm_bwd_case("slstm_bwd_fp32", d_in=24, d=32, B=2, T=256, K=3, P=3,
-                   dtype=torch.float32, seed=7, with_h0=True)
-    slstm_bwd_case("slstm_bwd_bf16", d_in=32, d=32, B=2, T=256, K=2, P=3,
-                   dtype=torch.bfloat16, seed=8)
-    ragged_case("slstm_ragged_fp32", "slstm", d_in=12, d=16, lengths=(37, 100, 64), K=2, P=3,
-                seed=11)
-    ragged_case("gru_head_ragged_fp32", "gru_head", d_in=16, d=128, lengths=(20, 45, 7), K=3,
-                P=None, seed=12, n_heads=2)
-    gru_head_bwd_case("gru_head_bwd_fp32", d_in=16, d=128, n_heads=2, B=2, T=80, K=3,
-                      dtype=torch.float32, seed=31, with_h0=True)
-    gru_head_bwd_case("gru_head_bwd_bf16", d_in=16, d=128, n_heads=2, B=2, T=64, K=3,
-                      dtype=torch.bfloat16, seed=32)
-    gru_head_bwd_parts_case()
-    para_rnn_case("para_rnn_slstm_fp32", "slstm", d_in=12, d=32, layers=2, B=2, T=60, K=3, P=3,
-                  seed=41)
-    para_rnn_case("para_rnn_gru_head_fp32", "gru_head", d_in=12, d=128, layers=2, B=2, T=50, K=3,
-                  P=None, seed=42, n_heads=2)
-    with open(os.path.join(HERE, "auto_picard.json"), "w") as f:
-        json.dump(auto_picard_table(), f, indent=1)
+    "slstm_cfg1_fp32": lambda: slstm_case(
+        "slstm_cfg1_fp32", d_in=64, d=64, B=2, T=1024, K=2, P=3, dtype=torch.float32, seed=0,
+        keep_wx=False),
+    "slstm_h0_fp32": lambda: slstm_case(
+        "slstm_h0_fp32", d_in=24, d=32, B=2, T=200, K=3, P=1, dtype=torch.float32, seed=5,
+        with_h0=True),
+    "slstm_bf16": lambda: slstm_case(
+        "slstm_bf16", d_in=64, d=64, B=2, T=512, K=2, P=3, dtype=torch.bfloat16, seed=1),
+    "slstm_fp16": lambda: slstm_case(
+        "slstm_fp16", d_in=64, d=64, B=2, T=512, K=2, P=3, dtype=torch.float16, seed=13,
+        with_h0=True),
+    "slstm_long_fp32": lambda: slstm_case(
+        "slstm_long_fp32", d_in=16, d=16, B=1, T=4096, K=2, P=5, dtype=torch.float32, seed=2,
+        x_std=0.5),
+    "gru_head_fp32": lambda: gru_head_case(
+        "gru_head_fp32", d_in=64, n_heads=2, d_head=64, B=2, T=256, K=3, dtype=torch.float32,
+        seed=3),
+    "gru_head_h0_fp32": lambda: gru_head_case(
+        "gru_head_h0_fp32", d_in=32, n_heads=2, d_head=64, B=1, T=96, K=3, dtype=torch.float32,
+        seed=4, with_h0=True),
+    "gru_head_bf16": lambda: gru_head_case(
+        "gru_head_bf16", d_in=64, n_heads=2, d_head=64, B=1, T=128, K=3, dtype=torch.bfloat16,
+        seed=6),
+    "gru_head_fp16": lambda: gru_head_case(
+        "gru_head_fp16", d_in=64, n_heads=2, d_head=64, B=2, T=128, K=3, dtype=torch.float16,
+        seed=14, with_h0=True),
+    "bwd_parts": bwd_parts_case,
+    "slstm_bwd_fp32": lambda: slstm_bwd_case(
+        "slstm_bwd_fp32", d_in=24, d=32, B=2, T=256, K=3, P=3, dtype=torch.float32, seed=7,
+        with_h0=True),
+    "slstm_bwd_bf16": lambda: slstm_bwd_case(
+        "slstm_bwd_bf16", d_in=32, d=32, B=2, T=256, K=2, P=3, dtype=torch.bfloat16, seed=8),
+    "slstm_bwd_fp16": lambda: slstm_bwd_case(
+        "slstm_bwd_fp16", d_in=32, d=32, B=2, T=256, K=2, P=3, dtype=torch.float16, seed=15),
+    "slstm_ragged_fp32": lambda: ragged_case(
+        "slstm_ragged_fp32", "slstm", d_in=12, d=16, lengths=(37, 100, 64), K=2, P=3, seed=11),
+    "gru_head_ragged_fp32": lambda: ragged_case(
+        "gru_head_ragged_fp32", "gru_head", d_in=16, d=128, lengths=(20, 45, 7), K=3, P=None,
+        seed=12, n_heads=2),
+    "gru_head_bwd_fp32": lambda: gru_head_bwd_case(
+        "gru_head_bwd_fp32", d_in=16, d=128, n_heads=2, B=2, T=80, K=3, dtype=torch.float32,
+        seed=31, with_h0=True),
+    "gru_head_bwd_bf16": lambda: gru_head_bwd_case(
+        "gru_head_bwd_bf16", d_in=16, d=128, n_heads=2, B=2, T=64, K=3, dtype=torch.bfloat16,
+        seed=32),
+    "gru_head_bwd_fp16": lambda: gru_head_bwd_case(
+        "gru_head_bwd_fp16", d_in=16, d=128, n_heads=2, B=2, T=64, K=3, dtype=torch.float16,
+        seed=33),
+    "gru_head_bwd_parts": gru_head_bwd_parts_case,
+    "para_rnn_slstm_fp32": lambda: para_rnn_case(
+        "para_rnn_slstm_fp32", "slstm", d_in=12, d=32, layers=2, B=2, T=60, K=3, P=3, seed=41),
+    "para_rnn_gru_head_fp32": lambda: para_rnn_case(
+        "para_rnn_gru_head_fp32", "gru_head", d_in=12, d=128, layers=2, B=2, T=50, K=3, P=None,
+        seed=42, n_heads=2),
+}
+
+
+def main(argv: list[str]) -> int:
+    """Write every fixture, or only the cases named on the command line."""
+    torch.set_num_threads(8)
+    names = argv or list(CASES)
+    unknown = [n for n in names if n not in CASES]
+    if unknown:
+        raise SystemExit(f"unknown cases {unknown}; known: {sorted(CASES)}")
+    for n in names:
+        CASES[n]()
+    if not argv:
+        with open(os.path.join(HERE, "auto_picard.json"), "w") as f:
+            json.dump(auto_picard_table(), f, indent=1)
     return 0
 
 
 if __name__ == "__main__":
-    sys.exit(main())
+    sys.exit(main(sys.argv[1:]))

@@ -35,7 +35,7 @@ def _ref_slstm(cell, state, wx):
     return O.slstm_step(p, state.float().cpu(), wx.float().cpu()).to(state.dtype)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("B,d", [(1, 1), (3, 70), (8, 1024)])
 def test_slstm_decode_matches_oracle(dtype, B, d):
     from pararnn_amd import decode_step
@@ -50,9 +50,10 @@ def test_slstm_decode_matches_oracle(dtype, B, d):
     ref = _ref_slstm(cell, state, wx)
     if dtype == torch.float32:
         assert torch.allclose(out, ref, rtol=2e-6, atol=2e-6)
-    else:  # same fp32 algebra, one rounding: at most one bf16 ulp apart
+    else:  # same fp32 algebra, one rounding: at most one ulp of the dtype apart
         diff = (out.float() - ref.float()).abs()
-        ulp = ref.float().abs() * 2 ** -7 + 1e-30
+        fi = torch.finfo(dtype)
+        ulp = ref.float().abs() * fi.eps + fi.smallest_normal * fi.eps
         assert bool((diff <= ulp).all()), diff.max()
 
 
@@ -102,7 +103,7 @@ def test_slstm_decode_from_x_and_sequential_t1():
 
 
 @pytest.mark.parametrize("mix", ["diag", "head"])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_gru_decode_matches_float64(mix, dtype):
     from pararnn_amd import ParaGRU, decode_step
 
@@ -134,7 +135,7 @@ def test_gru_decode_matches_float64(mix, dtype):
         r = torch.sigmoid(mixv(hv, A[1]) + rx)
         n = torch.tanh(mixv(hv * r.reshape(B, 2, 64), A[2]) + nx)
     ref = (1 - z) * h64 + z * n
-    tol = 2e-6 if dtype == torch.float32 else 2 ** -8
+    tol = {torch.float32: 2e-6, torch.bfloat16: 2 ** -8, torch.float16: 2 ** -11}[dtype]
     err = ((out.double() - ref).abs() / (1 + ref.abs())).max().item()
     print(f"  rel err {err:.2e}", flush=True)
     assert err <= tol

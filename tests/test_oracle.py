@@ -9,8 +9,9 @@ from conftest import load_golden
 import oracle as O
 from oracle.slstm import prepend
 
-SLSTM_CASES = ["slstm_cfg1_fp32", "slstm_h0_fp32", "slstm_bf16", "slstm_long_fp32"]
-GRU_CASES = ["gru_head_fp32", "gru_head_h0_fp32", "gru_head_bf16"]
+SLSTM_CASES = [
+    "slstm_cfg1_fp32", "slstm_h0_fp32", "slstm_bf16", "slstm_fp16", "slstm_long_fp32"]
+GRU_CASES = ["gru_head_fp32", "gru_head_h0_fp32", "gru_head_bf16", "gru_head_fp16"]
 
 
 def _slstm_params(t):

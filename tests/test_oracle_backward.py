@@ -67,7 +67,7 @@ def test_backward_matches_autograd_through_sequential_float64(with_h0):
     assert (R.abs() > 0.5).any() and (out["R"][R.abs() > 0.5] == 0).all()
 
 
-@pytest.mark.parametrize("name", ["slstm_bwd_fp32", "slstm_bwd_bf16"])
+@pytest.mark.parametrize("name", ["slstm_bwd_fp32", "slstm_bwd_bf16", "slstm_bwd_fp16"])
 def test_backward_matches_reference(name):
     t, m = load_golden(name)
     dtype = getattr(torch, m["dtype"])
@@ -185,7 +185,8 @@ def test_gru_head_backward_matches_autograd_float64(cap):
         assert (A[0].abs() > cap).any() and (out["A_z"][A[0].abs() > cap] == 0).all()
 
 
-@pytest.mark.parametrize("name", ["gru_head_bwd_fp32", "gru_head_bwd_bf16"])
+@pytest.mark.parametrize("name", [
+    "gru_head_bwd_fp32", "gru_head_bwd_bf16", "gru_head_bwd_fp16"])
 def test_gru_head_backward_matches_reference(name):
     from oracle.backward import gru_head_backward
     from oracle.gru_head import gru_head_newton
