@@ -417,18 +417,12 @@ slstm_picard_fused_kernel(
   // Packed sequences: heads among this wave's steps and the initial state
   // (c, n, m, h) of the first one's sequence (see Packed); a head restarts
   // the frozen-gate state from it in every stage.
-  Heads hd{0ull, 0};
+  Heads hd_all{0ull, 0};
   if constexpr (PK) {
     c_init[0] = c_init[1] = c_init[2] = 0.f;
     h0h = 0.f;
-    hd = find_heads(pk, t0, n_steps);
+    hd_all = find_heads(pk, t0, n_steps);
   }
-  auto head_of = [&](int s, float st[4]) { head_state(pk, h0, hd.seq(s), d, c0 + lane, live, st); };
-  auto head_h = [&](int s) {
-    float st[4];
-    head_of(s, st);
-    return st[3];
-  };
 
   uint32_t xw[L][2], pre[L][2], hh[L / 2];
   {
@@ -457,6 +451,35 @@ slstm_picard_fused_kernel(
   auto stage = [&](const int p, auto last_c) __attribute__((always_inline)) {
     constexpr bool last_stage = decltype(last_c)::value;
     const bool first_stage = p == 0;
+    // Packed streams: the head flags and the step count re-enter each stage
+    // through an opaque copy, so what the steps derive from them (flags,
+    // sequence numbers, rows, step guards) is computed per stage where it is
+    // used instead of being hoisted out of the stage loop into scalar
+    // registers for all L steps at once; and the steps run one guarded,
+    // head-checked loop (a single copy of the unrolled stage body).
+    Heads hd = hd_all;
+    if constexpr (PK) {
+      uint32_t lo = static_cast<uint32_t>(hd.mask), hi = static_cast<uint32_t>(hd.mask >> 32);
+      int q0 = hd.seq0;
+      asm volatile("" : "+v"(lo), "+v"(hi), "+v"(q0));
+      lo = __builtin_amdgcn_readfirstlane(lo);
+      hi = __builtin_amdgcn_readfirstlane(hi);
+      hd.seq0 = __builtin_amdgcn_readfirstlane(q0);
+      hd.mask = (static_cast<uint64_t>(hi) << 32) | lo;
+    }
+    int ns = n_steps;
+    if constexpr (PK) {
+      asm volatile("" : "+v"(ns));
+      ns = __builtin_amdgcn_readfirstlane(ns);
+    }
+    auto head_of = [&](int s, float st[4]) {
+      head_state(pk, h0, hd.seq(s), d, c0 + lane, live, st);
+    };
+    auto head_h = [&](int s) {
+      float st[4];
+      head_of(s, st);
+      return st[3];
+    };
     const int tag = tag_base + p + 1;
     // Keep wx packed across stages: without this the compiler hoists the
     // 16-bit unpacking out of the stage loop and holds 4 floats per step.
@@ -527,16 +550,16 @@ slstm_picard_fused_kernel(
       fg_step(zi, zf, zz, a.M, a.N, a.C);
     };
     auto run1 = [&](auto chk) {
-      if (n_steps == L) {
+      if (!PK && ns == L) {
 #pragma unroll
         for (int s = 0; s < L; ++s) step1(s, chk);
       } else {
 #pragma unroll
         for (int s = 0; s < L; ++s)
-          if (s < n_steps) step1(s, chk);
+          if (s < ns) step1(s, chk);
       }
     };
-    if (PK && hd.mask)
+    if constexpr (PK)
       run1(std::true_type{});
     else
       run1(std::false_type{});
@@ -636,16 +659,16 @@ slstm_picard_fused_kernel(
       }
     };
     auto run2 = [&](auto chk) {
-      if (n_steps == L) {
+      if (!PK && ns == L) {
 #pragma unroll
         for (int s = 0; s < L; ++s) step2(s, chk);
       } else {
 #pragma unroll
         for (int s = 0; s < L; ++s)
-          if (s < n_steps) step2(s, chk);
+          if (s < ns) step2(s, chk);
       }
     };
-    if (PK && hd.mask)
+    if constexpr (PK)
       run2(std::true_type{});
     else
       run2(std::false_type{});
@@ -957,9 +980,8 @@ slstm_newton_fused_kernel(
   // Packed sequences: the heads among this wave's steps, and the initial
   // state of the first one's sequence (later heads of the wave load theirs
   // when they come).
-  Heads hd{0ull, 0};
-  if constexpr (PK) hd = find_heads(pk, t0, n_steps);
-  auto head_prev = [&](int s, float p[4]) { head_state(pk, h0, hd.seq(s), d, c0 + lane, live, p); };
+  Heads hd_all{0ull, 0};
+  if constexpr (PK) hd_all = find_heads(pk, t0, n_steps);
 
   uint32_t xs[L][XS::N];
   float hf[L][4];
@@ -986,6 +1008,25 @@ slstm_newton_fused_kernel(
   // Iterations 1 .. K-1 keep the new iterate in registers; the last one,
   // compiled separately, writes it (no per-step branch on the iteration).
   auto iterate = [&](const int k, auto last_c) __attribute__((always_inline)) {
+    // Packed streams: the head flags and the step count re-enter each
+    // iteration through an opaque copy (what the steps derive from them is
+    // computed where it is used, not hoisted out of the iteration loop into
+    // scalar registers for all L steps), and the steps run one guarded,
+    // head-checked loop (a single copy of the unrolled iteration body).
+    Heads hd = hd_all;
+    int ns = n_steps;
+    if constexpr (PK) {
+      uint32_t lo = static_cast<uint32_t>(hd.mask), hi = static_cast<uint32_t>(hd.mask >> 32);
+      int q0 = hd.seq0;
+      asm volatile("" : "+v"(lo), "+v"(hi), "+v"(q0), "+v"(ns));
+      hd.mask = (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(hi)) << 32) |
+                __builtin_amdgcn_readfirstlane(lo);
+      hd.seq0 = __builtin_amdgcn_readfirstlane(q0);
+      ns = __builtin_amdgcn_readfirstlane(ns);
+    }
+    auto head_prev = [&](int s, float p[4]) {
+      head_state(pk, h0, hd.seq(s), d, c0 + lane, live, p);
+    };
     constexpr bool last_iter = decltype(last_c)::value;
     const int tag = tag_base + k + 1;
     // Keep wx packed across iterations (otherwise the unpacking is hoisted out
@@ -1071,16 +1112,16 @@ slstm_newton_fused_kernel(
         for (int j = 0; j < 4; ++j) prev[j] = hf[s][j];
       };
       auto run = [&](auto chk) {
-        if (n_steps == L) {
+        if (!PK && ns == L) {
 #pragma unroll
           for (int s = 0; s < L; ++s) step(s, chk);
         } else {
 #pragma unroll
           for (int s = 0; s < L; ++s)
-            if (s < n_steps) step(s, chk);
+            if (s < ns) step(s, chk);
         }
       };
-      if (PK && hd.mask)
+      if constexpr (PK)
         run(std::true_type{});
       else
         run(std::false_type{});
@@ -1197,16 +1238,16 @@ slstm_newton_fused_kernel(
         }
       };
       auto run = [&](auto chk) {
-        if (n_steps == L) {
+        if (!PK && ns == L) {
 #pragma unroll
           for (int s = 0; s < L; ++s) replay(s, chk);
         } else {
 #pragma unroll
           for (int s = 0; s < L; ++s)
-            if (s < n_steps) replay(s, chk);
+            if (s < ns) replay(s, chk);
         }
       };
-      if (PK && hd.mask)
+      if constexpr (PK)
         run(std::true_type{});
       else
         run(std::false_type{});
@@ -1241,10 +1282,10 @@ constexpr Shape kPicardDefault{24, 4};
 constexpr Shape kNewtonFusedDefault{20, 4};
 constexpr Shape kNewtonFusedF32{16, 4};
 
-// Packed streams: a few registers more per wave (the head checks and the
-// loads of head states), so shorter tiles than the rectangular defaults keep
-// the kernels free of register spills.
-constexpr Shape kPicardPacked{20, 4};
+// Packed streams: the fused warm start and Newton launches take the
+// rectangular tile lengths (their packed bodies are one guarded, head-checked
+// loop: no spills); the single-iteration launches run shorter tiles.
+constexpr Shape kPicardPacked{24, 4};
 constexpr Shape kFrozenPackedF32{32, 4};
 constexpr Shape kNewtonFusedPacked{20, 4};
 constexpr Shape kNewtonFusedPackedF32{12, 4};
