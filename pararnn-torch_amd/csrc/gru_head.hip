@@ -509,7 +509,13 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
       const float d1v[4] = {d1.x, d1.y, d1.z, d1.w}, d2v[4] = {d2.x, d2.y, d2.z, d2.w};
       const float d3v[4] = {d3.x, d3.y, d3.z, d3.w};
 #pragma unroll
-      for (int v = 0; v < 4; ++v) P[rt][v] = d1v[v] * P[rt][v] + d2v[v] * X1[rt][v] + d3v[v] * X3[rt][v];
+      for (int v = 0; v < 4; ++v) {
+        // in place: P <- d1 P, then two fused multiply-adds into P (no copy
+        // of the new Phi back into Phi's registers)
+        float t = d1v[v] * P[rt][v];
+        t = __builtin_fmaf(d2v[v], X1[rt][v], t);
+        P[rt][v] = __builtin_fmaf(d3v[v], X3[rt][v], t);
+      }
     }
   }
   float* po = phi_out + static_cast<size_t>(blockIdx.x) * DH * DH;

@@ -135,3 +135,38 @@ def test_full_size_cfg4_head_slice_vs_oracle():
     err = (got - ref).abs().max().item()
     print(f"cfg4 slice max|gpu-oracle| {err:.2e}", flush=True)
     assert err <= 1e-5
+
+
+def test_full_size_cfg4_bf16_head_slice_vs_fused_semantics():
+    """BASELINE config 4 shape in bf16 (H=8, d_head=64, B=4, T=32768, K=3), the
+    timed bf16 leg: one (batch, head) sequence of the GPU solve against the
+    oracle's fused-op semantics (fp32 algebra on the bf16 operands, one rounding
+    of the result; kernels/newton_gru_head.py:460-567) over the full T.  This
+    also bounds the bf16 chunk transfer matrices at full length."""
+    from pararnn_amd import ParaGRU, fused_newton
+
+    print("case full-size cfg4 bf16 slice", flush=True)
+    torch.manual_seed(0)
+    H, B, T = 8, 4, 32768
+    cell = ParaGRU(512, 512, mix="head", n_heads=H).to(DEV, torch.bfloat16)
+    g = torch.Generator(device=DEV).manual_seed(2)
+    x = torch.randn(B, T, 512, generator=g, device=DEV).to(torch.bfloat16)
+    b_s, h_s = 1, 6
+    with torch.no_grad():
+        wx = cell.W_x(x)
+        out = fused_newton(cell, wx, max_iters=3, omega=1.0, h0=None)
+        assert torch.isfinite(out).all()
+        got = out[b_s, :, 64 * h_s:64 * (h_s + 1)].float().cpu()
+        cols = torch.cat([torch.arange(64 * h_s, 64 * (h_s + 1)) + gi * 512 for gi in range(3)])
+        wx_s = wx[b_s:b_s + 1, :, cols.to(DEV)].cpu()
+        p = O.GRUHeadParams(torch.zeros(192, 1), torch.zeros(192),
+                            *(getattr(cell, k).detach()[h_s:h_s + 1].cpu()
+                              for k in ("A_z", "A_r", "A_n")))
+    ref = O.gru_head_newton(p, None, max_iters=3, wx=wx_s, work="fused")[0].float()
+    diff = (got - ref).abs()
+    rel_max = (diff.max() / ref.abs().max()).item()
+    rel_norm = ((got - ref).norm() / ref.norm()).item()
+    ulp_frac = (diff > ref.abs() * 2 ** -8).double().mean().item()
+    print(f"cfg4 bf16 slice: max rel {rel_max:.2e}, norm rel {rel_norm:.2e}, "
+          f"fraction more than one bf16 ulp apart {ulp_frac:.2e}", flush=True)
+    assert rel_max <= 2e-2 and rel_norm <= 5e-3
