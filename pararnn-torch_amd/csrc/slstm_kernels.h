@@ -71,20 +71,24 @@ __device__ __forceinline__ void fg_apply(const FG& y, float& m, float& n, float&
   m = mn;
 }
 
-// One frozen-gate step in place on (m, n, c); returns tanh-free readout pieces.
+// One frozen-gate step in place on (m, n, c), given z = tanh(z_z).
 // One of f, i is exactly e^0 = 1 (the larger exponent is the new stabiliser),
 // so a single exp of -|left - z_i| gives both, bit-identical to two exps.
-__device__ __forceinline__ void fg_step(float zi, float zf, float zz, float& m, float& n, float& c) {
+__device__ __forceinline__ void fg_step_z(float zi, float zf, float z, float& m, float& n,
+                                          float& c) {
   const float left = zf + m;
   const float mn = fmaxf(left, zi);
   const float e = fexp(-fabsf(left - zi));
   const bool lf = left >= zi;
   const float f = lf ? 1.f : e;
   const float i = lf ? e : 1.f;
-  const float z = ftanh(zz);
   n = f * n + i;
   c = f * c + i * z;
   m = mn;
+}
+
+__device__ __forceinline__ void fg_step(float zi, float zf, float zz, float& m, float& n, float& c) {
+  fg_step_z(zi, zf, ftanh(zz), m, n, c);
 }
 
 
@@ -381,6 +385,9 @@ slstm_picard_fused_kernel(
   __shared__ float s_carry[W][3][kCB];
   __shared__ float s_hl[W][kCB];
   __shared__ float s_tagg[4][kCB];  // the published tile aggregate (wave 0's lanes)
+  // tanh(z_z) of the stage's steps: pass 1 evaluates it, pass 2 reads it back
+  // (it does not depend on the carry; a transcendental pair per step saved)
+  __shared__ float s_z[W][L][kCB];
   __shared__ LookbackShared<FrozenMonoid, W * KP> s_lb;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -547,7 +554,9 @@ slstm_picard_fused_kernel(
         a = FG{-INFINITY, hs[2], hs[1], hs[0]};
       }
       a.F += zf;
-      fg_step(zi, zf, zz, a.M, a.N, a.C);
+      const float z = ftanh(zz);
+      s_z[wave][s][lane] = z;
+      fg_step_z(zi, zf, z, a.M, a.N, a.C);
     };
     auto run1 = [&](auto chk) {
       if (!PK && ns == L) {
@@ -640,8 +649,8 @@ slstm_picard_fused_kernel(
         m = hs[2];
       }
       const float zi = NT::lo(pre[s][0]), zf = NT::hi(pre[s][0]);
-      const float zz = NT::lo(pre[s][1]), zo = NT::hi(pre[s][1]);
-      fg_step(zi, zf, zz, m, n, c);
+      const float zo = NT::hi(pre[s][1]);
+      fg_step_z(zi, zf, s_z[wave][s][lane], m, n, c);
       const float h = c * frcp((1.f + fexp(-zo)) * (n + eps));
       if constexpr (last_stage) {
         const uint32_t so = s * row4 * SZ;
@@ -939,6 +948,9 @@ slstm_newton_fused_kernel(
   __shared__ float s_carry[W][4][kCB];
   __shared__ float s_tagg[20][kCB];  // the published tile aggregate (wave 0's lanes)
   __shared__ float s_hl[W][4][kCB];
+  // z = tanh(z_z) of the iteration's steps: pass 1 evaluates it at the
+  // linearisation point, pass 2 (same point) reads it back
+  __shared__ float s_z[W][L][kCB];
   __shared__ LookbackShared<NewtonMonoid, W * KP> s_lb;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1087,7 +1099,9 @@ slstm_newton_fused_kernel(
         if (head && s > 0) head_prev(s, prev);
         float x[4];
         XS::get(xs[s], x);
-        const CellJ J = cell_jac(prev, x, r, eps);
+        const float zc = cell_z(prev, x, r);
+        s_z[wave][s][lane] = zc;
+        const CellJ J = cell_jac_z(prev, x, r, eps, zc);
         const float F[4] = {J.pc - hf[s][0], J.pn - hf[s][1], J.pm - hf[s][2],
                             J.ph - hf[s][3]};
         jmv_affine(J, F, a.b);
@@ -1221,7 +1235,7 @@ slstm_newton_fused_kernel(
 #pragma unroll
         for (int j = 0; j < 4; ++j) hv[j] = hf[s][j];
         float pv[4], jv[4];
-        cell_jvp(prev, x, r, eps, dl, pv, jv);
+        cell_jvp_z(prev, x, r, eps, s_z[wave][s][lane], dl, pv, jv);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           dl[j] = jv[j] + (pv[j] - hv[j]);

@@ -326,8 +326,15 @@ struct CellJ {
   float f, cm, ch, nm, nh, al, mh, inv, dn, g;
 };
 
-__device__ __forceinline__ CellJ cell_jac(const float prev[4], const float x[4], const float r[4],
-                                          float eps) {
+// The cell's z = tanh(z_z) at this step (it depends only on x and h).
+__device__ __forceinline__ float cell_z(const float prev[4], const float x[4], const float r[4]) {
+  return ftanh5(x[2] + r[2] * prev[3]);
+}
+
+// cell_jac with z = cell_z(prev, x, r) given (GIVEN_Z) or evaluated here.
+template <bool GIVEN_Z>
+__device__ __forceinline__ CellJ cell_jac_impl(const float prev[4], const float x[4],
+                                               const float r[4], float eps, float zg) {
   const float c = prev[0], n = prev[1], m = prev[2], h = prev[3];
   const float zi = x[0] + r[0] * h;
   const float zf = x[1] + r[1] * h;
@@ -341,7 +348,7 @@ __device__ __forceinline__ CellJ cell_jac(const float prev[4], const float x[4],
   const bool lf = left >= zi;
   const float f = lf ? 1.f : e;
   const float i = lf ? e : 1.f;
-  const float z = ftanh5(zz);
+  const float z = GIVEN_Z ? zg : ftanh5(zz);
   const float nn = f * n + i;
   const float cn = f * c + i * z;
   const float o = fsigmoid(zo);
@@ -372,11 +379,23 @@ __device__ __forceinline__ CellJ cell_jac(const float prev[4], const float x[4],
   return J;
 }
 
+__device__ __forceinline__ CellJ cell_jac(const float prev[4], const float x[4], const float r[4],
+                                          float eps) {
+  return cell_jac_impl<false>(prev, x, r, eps, 0.f);
+}
+__device__ __forceinline__ CellJ cell_jac_z(const float prev[4], const float x[4],
+                                            const float r[4], float eps, float z) {
+  return cell_jac_impl<true>(prev, x, r, eps, z);
+}
+
 // Cell value p = f(prev, x) and the directional derivative jv = J v along
 // v, without forming J (a forward-mode pass through the cell, about half the
 // arithmetic of building the 12 entries and multiplying).
-__device__ __forceinline__ void cell_jvp(const float prev[4], const float x[4], const float r[4],
-                                         float eps, const float v[4], float p[4], float jv[4]) {
+// cell_jvp with z = cell_z(prev, x, r) given (GIVEN_Z) or evaluated here.
+template <bool GIVEN_Z>
+__device__ __forceinline__ void cell_jvp_impl(const float prev[4], const float x[4],
+                                              const float r[4], float eps, float zg,
+                                              const float v[4], float p[4], float jv[4]) {
   const float c = prev[0], n = prev[1], m = prev[2], h = prev[3];
   const float zi = x[0] + r[0] * h;
   const float zf = x[1] + r[1] * h;
@@ -389,7 +408,7 @@ __device__ __forceinline__ void cell_jvp(const float prev[4], const float x[4], 
   const bool lf = left >= zi;
   const float f = lf ? 1.f : e;
   const float i = lf ? e : 1.f;
-  const float z = ftanh5(zz);
+  const float z = GIVEN_Z ? zg : ftanh5(zz);
   const float nn = f * n + i;
   const float cn = f * c + i * z;
   const float o = fsigmoid(zo);
@@ -413,6 +432,16 @@ __device__ __forceinline__ void cell_jvp(const float prev[4], const float x[4], 
   jv[1] = dnn;
   jv[2] = dmn;
   jv[3] = dso * u + o * inv_den * (dcn - u * dnn);
+}
+
+__device__ __forceinline__ void cell_jvp(const float prev[4], const float x[4], const float r[4],
+                                         float eps, const float v[4], float p[4], float jv[4]) {
+  cell_jvp_impl<false>(prev, x, r, eps, 0.f, v, p, jv);
+}
+__device__ __forceinline__ void cell_jvp_z(const float prev[4], const float x[4],
+                                           const float r[4], float eps, float z, const float v[4],
+                                           float p[4], float jv[4]) {
+  cell_jvp_impl<true>(prev, x, r, eps, z, v, p, jv);
 }
 
 // v <- J v
