@@ -447,8 +447,14 @@ slstm_picard_fused_kernel(
       for (int s = 0; s < L; ++s) load(s);
     } else {
 #pragma unroll
-      for (int s = 0; s < L; ++s)
-        if (s < n_steps) load(s);
+      for (int s = 0; s < L; ++s) {
+        if (s < n_steps) {
+          load(s);
+        } else {
+          // steps past the end run unguarded in packed streams: defined zeros
+          xw[s][0] = xw[s][1] = 0u;
+        }
+      }
     }
   }
   const rsrc_t ro = make_rsrc(out + first * row4 + c0, span4);
@@ -458,12 +464,15 @@ slstm_picard_fused_kernel(
   auto stage = [&](const int p, auto last_c) __attribute__((always_inline)) {
     constexpr bool last_stage = decltype(last_c)::value;
     const bool first_stage = p == 0;
-    // Packed streams: the head flags and the step count re-enter each stage
-    // through an opaque copy, so what the steps derive from them (flags,
-    // sequence numbers, rows, step guards) is computed per stage where it is
-    // used instead of being hoisted out of the stage loop into scalar
-    // registers for all L steps at once; and the steps run one guarded,
-    // head-checked loop (a single copy of the unrolled stage body).
+    // Packed streams: the head flags re-enter each stage through an opaque
+    // copy, so what the steps derive from them (flags, sequence numbers,
+    // rows) is computed per stage where it is used instead of being hoisted
+    // out of the stage loop into scalar registers for all L steps at once;
+    // and the steps run one unguarded, head-checked loop (a single copy of
+    // the unrolled stage body).  Only the stream's last tile has steps past
+    // the end: they read zeros, their stores fall outside the output's
+    // buffer range (dropped), and no tile follows the last one, so nothing
+    // reads what they produce.
     Heads hd = hd_all;
     if constexpr (PK) {
       uint32_t lo = static_cast<uint32_t>(hd.mask), hi = static_cast<uint32_t>(hd.mask >> 32);
@@ -559,7 +568,7 @@ slstm_picard_fused_kernel(
       fg_step_z(zi, zf, z, a.M, a.N, a.C);
     };
     auto run1 = [&](auto chk) {
-      if (!PK && ns == L) {
+      if (PK || ns == L) {
 #pragma unroll
         for (int s = 0; s < L; ++s) step1(s, chk);
       } else {
@@ -668,7 +677,7 @@ slstm_picard_fused_kernel(
       }
     };
     auto run2 = [&](auto chk) {
-      if (!PK && ns == L) {
+      if (PK || ns == L) {
 #pragma unroll
         for (int s = 0; s < L; ++s) step2(s, chk);
       } else {
@@ -1011,8 +1020,17 @@ slstm_newton_fused_kernel(
       for (int s = 0; s < L; ++s) load(s);
     } else {
 #pragma unroll
-      for (int s = 0; s < L; ++s)
-        if (s < n_steps) load(s);
+      for (int s = 0; s < L; ++s) {
+        if (s < n_steps) {
+          load(s);
+        } else {
+          // steps past the end run unguarded in packed streams: defined zeros
+#pragma unroll
+          for (int q = 0; q < XS::N; ++q) xs[s][q] = 0u;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) hf[s][j] = 0.f;
+        }
+      }
     }
   }
   const rsrc_t ro = make_rsrc(out + first * row4 + c0, span * sizeof(TX));
@@ -1020,11 +1038,12 @@ slstm_newton_fused_kernel(
   // Iterations 1 .. K-1 keep the new iterate in registers; the last one,
   // compiled separately, writes it (no per-step branch on the iteration).
   auto iterate = [&](const int k, auto last_c) __attribute__((always_inline)) {
-    // Packed streams: the head flags and the step count re-enter each
-    // iteration through an opaque copy (what the steps derive from them is
-    // computed where it is used, not hoisted out of the iteration loop into
-    // scalar registers for all L steps), and the steps run one guarded,
-    // head-checked loop (a single copy of the unrolled iteration body).
+    // Packed streams: the head flags re-enter each iteration through an
+    // opaque copy (what the steps derive from them is computed where it is
+    // used, not hoisted out of the iteration loop into scalar registers for
+    // all L steps), and the steps run one unguarded, head-checked loop (a
+    // single copy of the unrolled iteration body; steps past the end of the
+    // stream's last tile are harmless, as in the warm start).
     Heads hd = hd_all;
     int ns = n_steps;
     if constexpr (PK) {
@@ -1126,7 +1145,7 @@ slstm_newton_fused_kernel(
         for (int j = 0; j < 4; ++j) prev[j] = hf[s][j];
       };
       auto run = [&](auto chk) {
-        if (!PK && ns == L) {
+        if (PK || ns == L) {
 #pragma unroll
           for (int s = 0; s < L; ++s) step(s, chk);
         } else {
@@ -1252,7 +1271,7 @@ slstm_newton_fused_kernel(
         }
       };
       auto run = [&](auto chk) {
-        if (!PK && ns == L) {
+        if (PK || ns == L) {
 #pragma unroll
           for (int s = 0; s < L; ++s) replay(s, chk);
         } else {
