@@ -280,6 +280,38 @@ PRNN_API int prnn_gru_head_backward(const void* wx, const void* a_z, const void*
                                     int T, int n_heads, int d_head, int dtype, void* workspace,
                                     size_t workspace_bytes, void* stream);
 
+/* Head GRU on a packed stream: wx (1, T, 3d) holds n_seq sequences, sequence
+ * q on steps [cu_seqlens[q], cu_seqlens[q+1]) (int32 device array, n_seq + 1
+ * entries, 0 = cu_seqlens[0] < ... < cu_seqlens[n_seq] = T).  At a sequence's
+ * first step the carry is cut (the reference's packed semantics:
+ * solvers/scan.py:206-216, layout.py:93-138; its fused head op,
+ * kernels/custom_ops.py:311-358, takes rectangular batches only) and the
+ * previous state is h0 row block_table[q] (row q when block_table is NULL;
+ * zeros when h0 is NULL).  out: (1, T, d).  The library builds the stream's
+ * head table in the workspace. */
+PRNN_API size_t prnn_gru_head_newton_packed_workspace_size(int T, int n_heads, int d_head,
+                                                           int max_iters, int dtype);
+PRNN_API int prnn_gru_head_newton_packed(const void* wx, const void* a_z, const void* a_r,
+                                         const void* a_n, const void* h0, void* out, int T,
+                                         int n_heads, int d_head, int max_iters, float omega,
+                                         int dtype, const int* cu_seqlens, int n_seq,
+                                         const int* block_table, void* workspace,
+                                         size_t workspace_bytes, void* stream);
+
+/* Eq. 2.6 backward of a packed head-GRU stream (cu_seqlens as above):
+ * nothing flows from a sequence's first step to the step before it, and
+ * g_h0 (n_seq, d) fp32 (or NULL; written only when h0 is non-NULL) receives
+ * J_head^T mu_head per sequence. */
+PRNN_API size_t prnn_gru_head_backward_packed_workspace_size(int T, int n_heads, int d_head,
+                                                             int dtype);
+PRNN_API int prnn_gru_head_backward_packed(const void* wx, const void* a_z, const void* a_r,
+                                           const void* a_n, const void* h0, const void* states,
+                                           const void* grad, void* g_wx, float* g_a,
+                                           float* g_h0, int T, int n_heads, int d_head,
+                                           int dtype, const int* cu_seqlens, int n_seq,
+                                           void* workspace, size_t workspace_bytes,
+                                           void* stream);
+
 /* ---- T = 1 decode (serving loop) -----------------------------------------
  * One recurrent step.  state / out: (rows, 4, d) sLSTM or (rows, d) GRU;
  * wx: (B, 4d) / (B, 3d) for this step.  block_table: NULL (row b of state is

@@ -66,6 +66,32 @@ __device__ __forceinline__ size_t h_at(int b, int t, int T, int d, int head, int
   return (static_cast<size_t>(b) * T + t) * d + head * DH + j;
 }
 
+// Packed streams (cu_seqlens): one batch row (B = 1) of T steps holding n_seq
+// sequences, sequence q on steps [cu[q], cu[q+1]); hq[t] = q at a sequence's
+// first step (a head), -1 elsewhere.  A head's previous state is row tbl[q]
+// of h0 (row q without a table) or zero without h0, and the Jacobian there is
+// zero: no carry crosses a head (reference solvers/scan.py:206-216,
+// layout.py:115-138).  The PK = false instantiations ignore it: each batch
+// row is one sequence starting at t = 0 from h0 row b.
+struct GPk {
+  const int* cu;
+  const int* hq;
+  const int* tbl;
+  int n_seq;
+};
+
+// Row of h0 that step t starts from, or -1 when its previous state is step
+// t - 1's.
+template <bool PK>
+__device__ __forceinline__ int start_row(const GPk& pk, int b, int t) {
+  if constexpr (PK) {
+    const int q = pk.hq[t];
+    return q < 0 ? -1 : (pk.tbl != nullptr ? pk.tbl[q] : q);
+  } else {
+    return t == 0 ? b : -1;
+  }
+}
+
 // Column j of a head's (in, out) matrix, i.e. A[i][j] for i = 0..63.
 template <typename TX>
 __device__ __forceinline__ void load_col(const TX* A, int head, int j, float col[DH]) {
@@ -144,18 +170,21 @@ __device__ __forceinline__ floatx4 ld4(const T* p) {
 // h0 needs the mat-vecs (gru_init_kernel, one wave per sequence and block of
 // `steps` steps).
 // ---------------------------------------------------------------------------
-template <typename TX, typename TOUT>
+template <typename TX, typename TOUT, bool PK>
 __global__ __launch_bounds__(256) void gru_init_elem_kernel(const TX* __restrict__ wx,
                                                             const TX* __restrict__ h0,
                                                             TOUT* __restrict__ out, int B, int T,
-                                                            int d) {
+                                                            int d, GPk pk) {
   const int q4 = d / 4;
   const size_t n = static_cast<size_t>(B) * T * q4;
   const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
   for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
     const size_t bt = i / q4;
     const int c = static_cast<int>(i % q4) * 4;
-    if (h0 != nullptr && bt % T == 0) continue;  // t = 0 with h0: gru_init_kernel
+    // a first step with h0: gru_init_kernel
+    if (h0 != nullptr &&
+        start_row<PK>(pk, static_cast<int>(bt / T), static_cast<int>(bt % T)) >= 0)
+      continue;
     const TX* row = wx + bt * 3 * d + c;
     const floatx4 zx = ld4(row), nx = ld4(row + 2 * static_cast<size_t>(d));
     floatx4 h;
@@ -166,31 +195,33 @@ __global__ __launch_bounds__(256) void gru_init_elem_kernel(const TX* __restrict
 }
 
 
-template <typename TX, typename TOUT>
+// PK: one block per (packed sequence q, head): the sequence's first step.
+template <typename TX, typename TOUT, bool PK>
 __global__ __launch_bounds__(64) void gru_init_kernel(const TX* __restrict__ wx,
                                                      const TX* __restrict__ a_z,
                                                      const TX* __restrict__ a_r,
                                                      const TX* __restrict__ a_n,
                                                      const TX* __restrict__ h0,
                                                      TOUT* __restrict__ out, int B, int T, int H,
-                                                     int steps, int n_blk) {
+                                                     int steps, int n_blk, GPk pk) {
   __shared__ float s_h[DH], s_u[DH];
   const int j = threadIdx.x;
   const int d = H * DH;
   const int seq = blockIdx.x / n_blk, blk = blockIdx.x % n_blk;
-  const int b = seq / H, head = seq % H;
-  const int t0 = blk * steps, t1 = min(T, t0 + steps);
+  const int b = PK ? 0 : seq / H, head = seq % H;
+  const int t0 = PK ? pk.cu[seq / H] : blk * steps, t1 = min(T, t0 + steps);
   for (int t = t0; t < t1; ++t) {
     const float zx = ld(wx + wx_at(b, t, T, d, 0, head, j));
     const float rx = ld(wx + wx_at(b, t, T, d, 1, head, j));
     const float nx = ld(wx + wx_at(b, t, T, d, 2, head, j));
     Gates g;
-    if (t == 0 && h0 != nullptr) {
+    const int hr = start_row<PK>(pk, b, t);
+    if (hr >= 0 && h0 != nullptr) {
       float az[DH], ar[DH], an[DH];
       load_col(a_z, head, j, az);
       load_col(a_r, head, j, ar);
       load_col(a_n, head, j, an);
-      const float hp = ld(h0 + static_cast<size_t>(b) * d + head * DH + j);
+      const float hp = ld(h0 + static_cast<size_t>(hr) * d + head * DH + j);
       s_h[j] = hp;
       __builtin_amdgcn_wave_barrier();
       g = gates_step(s_h, s_u, hp, zx, rx, nx, az, ar, an, false);
@@ -294,12 +325,12 @@ __global__ __launch_bounds__(64) void gru_pack_at_kernel(const TX* __restrict__ 
   }
 }
 
-template <typename TX, typename TH, bool TRANS>
+template <typename TX, typename TH, bool TRANS, bool PK>
 __global__ __launch_bounds__(256) void gru_phi_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ a_z, const TX* __restrict__ a_r,
     const TX* __restrict__ a_n, const TX* __restrict__ h0, const TH* __restrict__ hin, int B,
     int T, int H, int n_chunks, float* __restrict__ phi_out, float* __restrict__ gates_out,
-    const u32x4* __restrict__ at_packed, const floatx4* __restrict__ b_packed) {
+    const u32x4* __restrict__ at_packed, const floatx4* __restrict__ b_packed, GPk pk) {
   __shared__ PhiShared sh;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int li = lane & 15, g = lane >> 4;
@@ -312,16 +343,19 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
 
   // ---- inputs of the chunk into LDS (zero rows past the end); unrolled so
   // every load of the chunk is in flight at once ----
+  bool head_here = false;  // PK: a head among this thread's steps
 #pragma unroll
   for (int idx = threadIdx.x; idx < kChunk * DH / 4; idx += 256) {
     const int s = idx / (DH / 4), j = 4 * (idx % (DH / 4));
     const int t = t0 + s;
     floatx4 hp = {0.f, 0.f, 0.f, 0.f}, zx = hp, rx = hp, nx = hp;
     if (s < len) {
-      if (t > 0)
+      const int hr = start_row<PK>(pk, b, t);
+      if (PK) head_here |= hr >= 0;
+      if (hr < 0)
         hp = ld4(hin + h_at(b, t - 1, T, d, head, j));
       else if (h0 != nullptr)
-        hp = ld4(h0 + static_cast<size_t>(b) * d + head * DH + j);
+        hp = ld4(h0 + static_cast<size_t>(hr) * d + head * DH + j);
       zx = ld4(wx + wx_at(b, t, T, d, 0, head, j));
       rx = ld4(wx + wx_at(b, t, T, d, 1, head, j));
       nx = ld4(wx + wx_at(b, t, T, d, 2, head, j));
@@ -448,11 +482,13 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
   __syncthreads();
 
   // Phi = I on this wave's columns: lane holds Phi[16 rt + 4 g + v][col].
+  // PK: a chunk holding a head has Phi = 0 (the Jacobian at the head is zero).
+  const bool cut = PK && __syncthreads_or(head_here);
   float P[4][4];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) P[rt][v] = (16 * rt + 4 * g + v == col) ? 1.f : 0.f;
+    for (int v = 0; v < 4; ++v) P[rt][v] = (!cut && 16 * rt + 4 * g + v == col) ? 1.f : 0.f;
 
   // B operand of a product from D-layout values: slots of step ks are rows
   // 16 (2 ks) + 4 g + (0..3) then 16 (2 ks + 1) + 4 g + (0..3).
@@ -477,7 +513,7 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
     }
   };
 
-  for (int s = 0; s < len; ++s) {
+  for (int s = 0; s < (cut ? 0 : len); ++s) {
     const float* rsc = &sh.rs[s][0][4 * g];
     bf16x8 bp[2];
     to_b(P, bp);
@@ -745,12 +781,12 @@ __global__ __launch_bounds__(64 * PARTS) void gru_carry_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kPair = 2;
 
-template <typename TX, typename TOUT, bool LOCAL>
+template <typename TX, typename TOUT, bool LOCAL, bool PK>
 __global__ __launch_bounds__(256) void gru_replay_kernel(
     const TX* __restrict__ a_z, const TX* __restrict__ a_r, const TX* __restrict__ a_n,
     const TX* __restrict__ h0, const float* __restrict__ hin, const float* __restrict__ gates,
     const float* __restrict__ carry_in, TOUT* __restrict__ hout, float* __restrict__ e_out,
-    int B, int T, int H, int n_chunks, float omega) {
+    int B, int T, int H, int n_chunks, float omega, GPk pk) {
   __shared__ float s_v[4][kPair][2][DH];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n_pairs = (n_chunks + kPair - 1) / kPair;
@@ -767,6 +803,7 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
 
   struct In {
     float hp, z, r, n, ht;
+    bool head;  // PK: a sequence's first step (no carry reaches it)
   };
   int t0[kPair], len[kPair];
   float dl[kPair];
@@ -782,13 +819,15 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
     gt[k] = gates + id * kChunk * 3 * DH + lane;
   }
   auto load_in = [&](int k, int s) {
-    In v{0.f, 0.f, 0.f, 0.f, 0.f};
+    In v{0.f, 0.f, 0.f, 0.f, 0.f, false};
     if (s < len[k]) {
       const int t = t0[k] + s;
-      if (t > 0)
+      const int hr = start_row<PK>(pk, b, t);
+      v.head = PK && hr >= 0;
+      if (hr < 0)
         v.hp = hin[h_at(b, t - 1, T, d, head, lane)];
       else if (h0 != nullptr)
-        v.hp = ld(h0 + static_cast<size_t>(b) * d + head * DH + lane);
+        v.hp = ld(h0 + static_cast<size_t>(hr) * d + head * DH + lane);
       v.z = gt[k][(s * 3) * DH];
       v.r = gt[k][(s * 3 + 1) * DH];
       v.n = gt[k][(s * 3 + 2) * DH];
@@ -802,6 +841,11 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
 #pragma unroll
     for (int k = 0; k < kPair; ++k) cur[k] = load_in(k, s);
     // J delta = (1-z) delta + d2 (delta @ A_z) + d3 ((r delta + d5 (delta @ A_r)) @ A_n)
+    if constexpr (PK) {
+#pragma unroll
+      for (int k = 0; k < kPair; ++k)
+        if (cur[k].head) dl[k] = 0.f;  // no carry crosses a head
+    }
 #pragma unroll
     for (int k = 0; k < kPair; ++k) s_v[wave][k][0][lane] = dl[k];
     __builtin_amdgcn_wave_barrier();
@@ -855,12 +899,12 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kRCols = 16;  // chunks per wave (the MFMA N dimension)
 
-template <typename TX, typename TOUT, bool LOCAL>
+template <typename TX, typename TOUT, bool LOCAL, bool PK>
 __global__ __launch_bounds__(256) void gru_replay_mfma_kernel(
     const TX* __restrict__ a_z, const TX* __restrict__ a_r, const TX* __restrict__ a_n,
     const TX* __restrict__ h0, const float* __restrict__ hin, const float* __restrict__ gates,
     const float* __restrict__ carry_in, TOUT* __restrict__ hout, float* __restrict__ e_out,
-    int B, int T, int H, int n_chunks, float omega) {
+    int B, int T, int H, int n_chunks, float omega, GPk pk) {
   // [matrix][output tile][contraction tile][lane] -> the 4 A operands v = 0..3
   __shared__ floatx4 sA[3][4][4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -895,24 +939,36 @@ __global__ __launch_bounds__(256) void gru_replay_mfma_kernel(
   const int steps = min(kChunk, T - c_first * kChunk);  // the wave's longest chunk
   struct In {
     floatx4 hp[4], ht[4], gz[4], gr[4], gn[4];
+    bool head;  // PK: this lane's chunk starts a sequence at this step
   };
   // Step s's inputs (zeros past the chunk's end); loaded one step ahead.  h at
   // t - 1 is the previous step's h at t except at the chunk's first step.
   auto load_in = [&](int s, In& v, const floatx4* h_prev) {
     const bool act = s < len;
     const int t = t0 + s;
+    int hr = -1;
+    if constexpr (PK) hr = act ? start_row<PK>(pk, b, t) : -1;
+    v.head = hr >= 0;
 #pragma unroll
     for (int to = 0; to < 4; ++to) {
       const floatx4 zero{0.f, 0.f, 0.f, 0.f};
       v.hp[to] = v.ht[to] = v.gz[to] = v.gr[to] = v.gn[to] = zero;
       if (act) {
         const int j = 16 * to + 4 * g;
-        if (h_prev != nullptr)
+        if (!PK) {
+          if (h_prev != nullptr)
+            v.hp[to] = h_prev[to];
+          else if (t > 0)
+            v.hp[to] = *reinterpret_cast<const floatx4*>(hin + h_at(b, t - 1, T, d, head, j));
+          else if (h0 != nullptr)
+            v.hp[to] = ld4(h0 + static_cast<size_t>(b) * d + head * DH + j);
+        } else if (hr >= 0) {
+          if (h0 != nullptr) v.hp[to] = ld4(h0 + static_cast<size_t>(hr) * d + head * DH + j);
+        } else if (h_prev != nullptr) {
           v.hp[to] = h_prev[to];
-        else if (t > 0)
+        } else {
           v.hp[to] = *reinterpret_cast<const floatx4*>(hin + h_at(b, t - 1, T, d, head, j));
-        else if (h0 != nullptr)
-          v.hp[to] = ld4(h0 + static_cast<size_t>(b) * d + head * DH + j);
+        }
         v.ht[to] = *reinterpret_cast<const floatx4*>(hin + h_at(b, t, T, d, head, j));
         v.gz[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3) * DH + 16 * to);
         v.gr[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3 + 1) * DH + 16 * to);
@@ -928,6 +984,13 @@ __global__ __launch_bounds__(256) void gru_replay_mfma_kernel(
     const In cur = nx;
     if (s + 1 < steps) load_in(s + 1, nx, cur.ht);
     const floatx4 *hp = cur.hp, *ht = cur.ht, *gz = cur.gz, *gr = cur.gr, *gn = cur.gn;
+    if constexpr (PK) {
+      // no carry crosses a head: this lane's column of delta restarts at zero
+      if (cur.head) {
+#pragma unroll
+        for (int to = 0; to < 4; ++to) dl[to] = floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
     // J delta = (1-z) delta + d2 (delta @ A_z) + d3 ((r delta + d5 (delta @ A_r)) @ A_n)
     floatx4 yz[4], yr[4], yn[4], vv[4];
 #pragma unroll
@@ -1030,12 +1093,14 @@ __device__ __forceinline__ void load_row(const TX* A, int head, int i, float row
 // Per step: mu = g + nu;  d_zpre = mu (n - h) z(1-z);  d_npre = mu z (1-n^2);
 // d_u = A_n d_npre;  d_rpre = d_u h r(1-r);
 // nu <- (1-z) mu + A_z d_zpre + r d_u + A_r d_rpre.
-template <typename TX>
+// PK: at a head nu is that sequence's grad h0 (row q of g_h0), and nothing
+// flows to the step before it.
+template <typename TX, bool PK>
 __global__ __launch_bounds__(256) void gru_rev_kernel(
     const TX* __restrict__ a_z, const TX* __restrict__ a_r, const TX* __restrict__ a_n,
     const TX* __restrict__ h0, const TX* __restrict__ states, const TX* __restrict__ grad,
     const float* __restrict__ gates, const float* __restrict__ carry_in, TX* __restrict__ g_wx,
-    float* __restrict__ g_h0, int B, int T, int H, int n_chunks) {
+    float* __restrict__ g_h0, int B, int T, int H, int n_chunks, GPk pk) {
   __shared__ float s_v[4][3][DH];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int task = blockIdx.x * 4 + wave;
@@ -1056,16 +1121,19 @@ __global__ __launch_bounds__(256) void gru_rev_kernel(
 
   struct In {
     float hp, g, z, r, n;
+    int q;  // PK: the sequence this step starts, -1 elsewhere
   };
   const float* gt = gates + static_cast<size_t>(task) * kChunk * 3 * DH + lane;
   auto load_in = [&](int s) {
-    In v{0.f, 0.f, 0.f, 0.f, 0.f};
+    In v{0.f, 0.f, 0.f, 0.f, 0.f, -1};
     if (s >= 0) {
       const int t = t0 + s;
-      if (t > 0)
+      const int hr = start_row<PK>(pk, b, t);
+      if (PK && hr >= 0) v.q = pk.hq[t];
+      if (hr < 0)
         v.hp = ld(states + h_at(b, t - 1, T, d, head, lane));
       else if (h0 != nullptr)
-        v.hp = ld(h0 + static_cast<size_t>(b) * d + head * DH + lane);
+        v.hp = ld(h0 + static_cast<size_t>(hr) * d + head * DH + lane);
       v.g = ld(grad + h_at(b, t, T, d, head, lane));
       v.z = gt[(s * 3) * DH];
       v.r = gt[(s * 3 + 1) * DH];
@@ -1096,23 +1164,27 @@ __global__ __launch_bounds__(256) void gru_rev_kernel(
       st(g_wx + wx_at(b, t, T, d, 1, head, lane), d_rpre);
       st(g_wx + wx_at(b, t, T, d, 2, head, lane), d_npre);
     }
+    if (PK && cur.q >= 0) {
+      if (g_h0 != nullptr) g_h0[static_cast<size_t>(cur.q) * d + head * DH + lane] = nu;
+      nu = 0.f;
+    }
     __builtin_amdgcn_wave_barrier();
     cur = nx1;
     nx1 = nx2;
   }
-  if (c == 0 && g_h0 != nullptr)
+  if (!PK && c == 0 && g_h0 != nullptr)
     g_h0[static_cast<size_t>(b) * d + head * DH + lane] = nu;
 }
 
 // Local reverse walk: nu from a zero carry over each chunk, two consecutive
 // chunks of a sequence per wave side by side (lane i keeps row i of A_z, A_r,
 // A_n); the chunk's final nu is its local solution e.
-template <typename TX>
+template <typename TX, bool PK>
 __global__ __launch_bounds__(256) void gru_rev_local_kernel(
     const TX* __restrict__ a_z, const TX* __restrict__ a_r, const TX* __restrict__ a_n,
     const TX* __restrict__ h0, const TX* __restrict__ states, const TX* __restrict__ grad,
     const float* __restrict__ gates, float* __restrict__ e_out, int B, int T, int H,
-    int n_chunks) {
+    int n_chunks, GPk pk) {
   constexpr int NP = kPair;
   __shared__ float s_v[4][NP][3][DH];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1129,6 +1201,7 @@ __global__ __launch_bounds__(256) void gru_rev_local_kernel(
 
   struct In {
     float hp, g, z, r, n;
+    bool head;  // PK: a sequence's first step (nothing flows before it)
   };
   int t0[NP], len[NP];
   float nu[NP];
@@ -1145,13 +1218,15 @@ __global__ __launch_bounds__(256) void gru_rev_local_kernel(
   }
   // Steps past a chunk's end read zeros, and a zero step leaves nu unchanged.
   auto load_in = [&](int k, int s) {
-    In v{0.f, 0.f, 0.f, 0.f, 0.f};
+    In v{0.f, 0.f, 0.f, 0.f, 0.f, false};
     if (s < len[k]) {
       const int t = t0[k] + s;
-      if (t > 0)
+      const int hr = start_row<PK>(pk, b, t);
+      v.head = PK && hr >= 0;
+      if (hr < 0)
         v.hp = ld(states + h_at(b, t - 1, T, d, head, lane));
       else if (h0 != nullptr)
-        v.hp = ld(h0 + static_cast<size_t>(b) * d + head * DH + lane);
+        v.hp = ld(h0 + static_cast<size_t>(hr) * d + head * DH + lane);
       v.g = ld(grad + h_at(b, t, T, d, head, lane));
       v.z = gt[k][(s * 3) * DH];
       v.r = gt[k][(s * 3 + 1) * DH];
@@ -1187,6 +1262,7 @@ __global__ __launch_bounds__(256) void gru_rev_local_kernel(
     for (int k = 0; k < NP; ++k) {
       const float t_r = vec_col(s_v[wave][k][2], ar);
       nu[k] = (1.f - cur[k].z) * mu[k] + t_z[k] + cur[k].r * d_u[k] + t_r;
+      if (PK && cur[k].head) nu[k] = 0.f;  // nothing flows before a head
     }
     __builtin_amdgcn_wave_barrier();
   }
@@ -1203,12 +1279,15 @@ __global__ __launch_bounds__(256) void gru_rev_local_kernel(
 // unchanged.  LOCAL: nu from zero, writing each chunk's final nu (e);
 // otherwise from the chunk's carry, writing the pre-activation gradients
 // g_wx and, for chunk 0, grad h0 = nu_0.
-template <typename TX, bool LOCAL>
+// PK: at a head (per column) nu is that sequence's grad h0 (written by the
+// final walk) and restarts at zero for the steps before it.
+template <typename TX, bool LOCAL, bool PK>
 __global__ __launch_bounds__(256) void gru_rev_mfma_kernel(
     const TX* __restrict__ a_z, const TX* __restrict__ a_r, const TX* __restrict__ a_n,
     const TX* __restrict__ h0, const TX* __restrict__ states, const TX* __restrict__ grad,
     const float* __restrict__ gates, const float* __restrict__ carry_in, TX* __restrict__ g_wx,
-    float* __restrict__ g_h0, float* __restrict__ e_out, int B, int T, int H, int n_chunks) {
+    float* __restrict__ g_h0, float* __restrict__ e_out, int B, int T, int H, int n_chunks,
+    GPk pk) {
   __shared__ floatx4 sA[3][4][4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n_grp = (n_chunks + 4 * kRCols - 1) / (4 * kRCols);
@@ -1242,20 +1321,23 @@ __global__ __launch_bounds__(256) void gru_rev_mfma_kernel(
   const int steps = min(kChunk, T - c_first * kChunk);  // the wave's longest chunk
   struct In {
     floatx4 hp[4], gr_[4], z[4], r[4], nn[4];
+    int q;  // PK: the sequence this lane's step starts, -1 elsewhere
   };
   auto load_in = [&](int s, In& v) {
     const bool act = s >= 0 && s < len;
     const int t = t0 + s;
+    const int hr = act ? start_row<PK>(pk, b, t) : -1;
+    v.q = (PK && hr >= 0) ? pk.hq[t] : -1;
 #pragma unroll
     for (int to = 0; to < 4; ++to) {
       const floatx4 zero{0.f, 0.f, 0.f, 0.f};
       v.hp[to] = v.gr_[to] = v.z[to] = v.r[to] = v.nn[to] = zero;
       if (act) {
         const int j = 16 * to + 4 * g;
-        if (t > 0)
+        if (hr < 0)
           v.hp[to] = ld4(states + h_at(b, t - 1, T, d, head, j));
         else if (h0 != nullptr)
-          v.hp[to] = ld4(h0 + static_cast<size_t>(b) * d + head * DH + j);
+          v.hp[to] = ld4(h0 + static_cast<size_t>(hr) * d + head * DH + j);
         v.gr_[to] = ld4(grad + h_at(b, t, T, d, head, j));
         v.z[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3) * DH + 16 * to);
         v.r[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3 + 1) * DH + 16 * to);
@@ -1337,6 +1419,17 @@ __global__ __launch_bounds__(256) void gru_rev_mfma_kernel(
         st4(g_wx + wx_at(b, t, T, d, 2, head, j), dn[to]);
       }
     }
+    if constexpr (PK) {
+      if (cur.q >= 0) {
+#pragma unroll
+        for (int to = 0; to < 4; ++to) {
+          if (!LOCAL && g_h0 != nullptr)
+            *reinterpret_cast<floatx4*>(g_h0 + static_cast<size_t>(cur.q) * d + head * DH +
+                                        16 * to + 4 * g) = nu[to];
+          nu[to] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    }
   }
   if (valid) {
 #pragma unroll
@@ -1344,7 +1437,7 @@ __global__ __launch_bounds__(256) void gru_rev_mfma_kernel(
       const int j = 16 * to + 4 * g;
       if (LOCAL)
         *reinterpret_cast<floatx4*>(e_out + id * DH + j) = nu[to];
-      else if (c == 0 && g_h0 != nullptr)
+      else if (!PK && c == 0 && g_h0 != nullptr)
         *reinterpret_cast<floatx4*>(g_h0 + static_cast<size_t>(b) * d + head * DH + j) = nu[to];
     }
   }
@@ -1359,11 +1452,11 @@ __global__ __launch_bounds__(256) void gru_rev_mfma_kernel(
 constexpr int kGaRows = 16;
 constexpr int kGaPad = 80;  // fp32 LDS row stride (the 4 lane groups land on distinct banks)
 
-template <typename TX>
+template <typename TX, bool PK>
 __global__ __launch_bounds__(256) void gru_ga_kernel(
     const TX* __restrict__ h0, const TX* __restrict__ states, const float* __restrict__ gates,
     const TX* __restrict__ g_wx, int B, int T, int H, int n_chunks, int n_split, int rows_per,
-    float* __restrict__ part) {
+    float* __restrict__ part, GPk pk) {
   __shared__ float sx[2][kGaRows][kGaPad], sy[3][kGaRows][kGaPad];
   const int split = blockIdx.x % n_split;
   const int head = blockIdx.x / n_split;
@@ -1392,10 +1485,11 @@ __global__ __launch_bounds__(256) void gru_ga_kernel(
     const long long k = k0 + sr;
     if (k < r1) {
       const int b = static_cast<int>(k / T), t = static_cast<int>(k % T);
-      if (t > 0)
+      const int hr = start_row<PK>(pk, b, t);
+      if (hr < 0)
         st.hv = ld4(states + h_at(b, t - 1, T, d, head, sj));
       else if (h0 != nullptr)
-        st.hv = ld4(h0 + static_cast<size_t>(b) * d + head * DH + sj);
+        st.hv = ld4(h0 + static_cast<size_t>(hr) * d + head * DH + sj);
       const size_t task = static_cast<size_t>(b * H + head) * n_chunks + t / kChunk;
       const floatx4 rv =
           *reinterpret_cast<const floatx4*>(gates + ((task * kChunk + t % kChunk) * 3 + 1) * DH + sj);
@@ -1509,6 +1603,7 @@ struct Ws {
   u32x4* at;     // packed bf16 A^T operands of the chunk kernel
   floatx4* atb;  // packed fp32 B operands of its gate GEMMs
   CarryWs cs;
+  int* hq;  // packed streams: the head table (see GPk)
 };
 
 static u32x4* carve_at(Carver& cv, int H) {
@@ -1518,10 +1613,11 @@ static floatx4* carve_atb(Carver& cv, int H) {
   return static_cast<floatx4*>(cv.take(sizeof(floatx4) * static_cast<size_t>(H) * 4 * 3 * 4 * 64));
 }
 
-static Ws carve(void* base, int B, int T, int H, int K, size_t* total) {
+static Ws carve(void* base, int B, int T, int H, int K, size_t* total, bool packed = false) {
   const int n_seq = B * H, n_chunks = (T + kChunk - 1) / kChunk;
   Carver cv(base);
   Ws w;
+  w.hq = packed ? static_cast<int*>(cv.take(sizeof(int) * static_cast<size_t>(T))) : nullptr;
   w.phi = static_cast<float*>(cv.take(sizeof(float) * static_cast<size_t>(n_seq) * n_chunks * DH * DH));
   w.e = static_cast<float*>(cv.take(sizeof(float) * static_cast<size_t>(n_seq) * n_chunks * DH));
   w.carry = static_cast<float*>(cv.take(sizeof(float) * static_cast<size_t>(n_seq) * n_chunks * DH));
@@ -1549,66 +1645,84 @@ static bool walks_mfma(const char* env, int n_seq, int n_chunks) {
   return n_seq * ((n_chunks + kRCols - 1) / kRCols) >= kReplayMfmaMinWaves;
 }
 
-template <typename TX, typename TOUT, bool LOCAL>
+template <typename TX, typename TOUT, bool LOCAL, bool PK>
 static void launch_replay(const TX* az, const TX* ar, const TX* an, const TX* h0,
                           const float* hin, const float* gates, const float* carry, TOUT* out,
                           float* e, int B, int T, int H, int n_chunks, float omega,
-                          hipStream_t stream) {
+                          hipStream_t stream, const GPk& pk) {
   const int n_seq = B * H;
   if (walks_mfma("PRNN_GRU_REPLAY_MFMA", n_seq, n_chunks)) {
     const int n_grp = (n_chunks + 4 * kRCols - 1) / (4 * kRCols);
-    gru_replay_mfma_kernel<TX, TOUT, LOCAL><<<dim3(n_seq * n_grp), dim3(256), 0, stream>>>(
-        az, ar, an, h0, hin, gates, carry, out, e, B, T, H, n_chunks, omega);
+    gru_replay_mfma_kernel<TX, TOUT, LOCAL, PK><<<dim3(n_seq * n_grp), dim3(256), 0, stream>>>(
+        az, ar, an, h0, hin, gates, carry, out, e, B, T, H, n_chunks, omega, pk);
   } else {
     const int blocks = (n_seq * ((n_chunks + kPair - 1) / kPair) + 3) / 4;
-    gru_replay_kernel<TX, TOUT, LOCAL><<<dim3(blocks), dim3(256), 0, stream>>>(
-        az, ar, an, h0, hin, gates, carry, out, e, B, T, H, n_chunks, omega);
+    gru_replay_kernel<TX, TOUT, LOCAL, PK><<<dim3(blocks), dim3(256), 0, stream>>>(
+        az, ar, an, h0, hin, gates, carry, out, e, B, T, H, n_chunks, omega, pk);
   }
+}
+
+// The head table of a packed stream: hq[t] = q where t = cu[q], -1 elsewhere.
+__global__ __launch_bounds__(256) void gru_heads_kernel(const int* __restrict__ cu, int n_seq,
+                                                        int T, int* __restrict__ hq) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= T) return;
+  int lo = 0, hi = n_seq;  // largest q in [0, n_seq) with cu[q] <= t
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (cu[mid] <= t)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  hq[t] = cu[lo] == t ? lo : -1;
 }
 
 // The initial guess into `out`: every step elementwise, then the t = 0 rows
 // from h0 (one step per sequence) when h0 is given.
-template <typename TX, typename TOUT>
+template <typename TX, typename TOUT, bool PK>
 static void launch_init(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX* h0,
-                        TOUT* out, int B, int T, int H, hipStream_t stream) {
+                        TOUT* out, int B, int T, int H, hipStream_t stream, const GPk& pk) {
   const int d = H * DH;
   const size_t n = static_cast<size_t>(B) * T * (d / 4);
   const unsigned blocks = static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 8192));
-  gru_init_elem_kernel<TX, TOUT><<<dim3(blocks), dim3(256), 0, stream>>>(wx, h0, out, B, T, d);
-  if (h0 != nullptr)  // one block of one step per sequence: t = 0 only
-    gru_init_kernel<TX, TOUT><<<dim3(B * H), dim3(64), 0, stream>>>(wx, az, ar, an, h0, out, B,
-                                                                     T, H, 1, 1);
+  gru_init_elem_kernel<TX, TOUT, PK><<<dim3(blocks), dim3(256), 0, stream>>>(wx, h0, out, B, T,
+                                                                           d, pk);
+  if (h0 != nullptr)  // one block of one step per sequence and head: its first step
+    gru_init_kernel<TX, TOUT, PK><<<dim3((PK ? pk.n_seq : B) * H), dim3(64), 0, stream>>>(
+        wx, az, ar, an, h0, out, B, T, H, 1, 1, pk);
 }
 
-template <typename TX>
+template <typename TX, bool PK>
 static int run(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX* h0, TX* out,
-               int B, int T, int H, int K, float omega, const Ws& w, hipStream_t stream) {
+               int B, int T, int H, int K, float omega, const Ws& w, hipStream_t stream,
+               const GPk& pk) {
   const int n_seq = B * H, n_chunks = (T + kChunk - 1) / kChunk;
   if (K == 0) {
-    launch_init<TX, TX>(wx, az, ar, an, h0, out, B, T, H, stream);
+    launch_init<TX, TX, PK>(wx, az, ar, an, h0, out, B, T, H, stream, pk);
     PRNN_HIP(hipGetLastError());
     return PRNN_OK;
   }
-  launch_init<TX, float>(wx, az, ar, an, h0, w.work[0], B, T, H, stream);
+  launch_init<TX, float, PK>(wx, az, ar, an, h0, w.work[0], B, T, H, stream, pk);
   gru_pack_at_kernel<TX><<<dim3(H), dim3(64), 0, stream>>>(az, ar, an, w.at, w.atb);
   PRNN_HIP(hipGetLastError());
   for (int k = 1; k <= K; ++k) {
     const float* hin = w.work[(k - 1) & 1];
-    gru_phi_kernel<TX, float, false><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
-        wx, az, ar, an, h0, hin, B, T, H, n_chunks, w.phi, w.gates, w.at, w.atb);
+    gru_phi_kernel<TX, float, false, PK><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
+        wx, az, ar, an, h0, hin, B, T, H, n_chunks, w.phi, w.gates, w.at, w.atb, pk);
     PRNN_HIP(hipGetLastError());
-    launch_replay<TX, float, true>(az, ar, an, h0, hin, w.gates, nullptr,
-                                   static_cast<float*>(nullptr), w.e, B, T, H, n_chunks, omega,
-                                   stream);
+    launch_replay<TX, float, true, PK>(az, ar, an, h0, hin, w.gates, nullptr,
+                                       static_cast<float*>(nullptr), w.e, B, T, H, n_chunks,
+                                       omega, stream, pk);
     PRNN_HIP(hipGetLastError());
     carry_scan<false>(w.phi, w.e, w.carry, n_seq, n_chunks, w.cs, stream);
     PRNN_HIP(hipGetLastError());
     if (k == K)
-      launch_replay<TX, TX, false>(az, ar, an, h0, hin, w.gates, w.carry, out, nullptr, B, T, H,
-                                   n_chunks, omega, stream);
+      launch_replay<TX, TX, false, PK>(az, ar, an, h0, hin, w.gates, w.carry, out, nullptr, B,
+                                       T, H, n_chunks, omega, stream, pk);
     else
-      launch_replay<TX, float, false>(az, ar, an, h0, hin, w.gates, w.carry, w.work[k & 1],
-                                      nullptr, B, T, H, n_chunks, omega, stream);
+      launch_replay<TX, float, false, PK>(az, ar, an, h0, hin, w.gates, w.carry, w.work[k & 1],
+                                          nullptr, B, T, H, n_chunks, omega, stream, pk);
     PRNN_HIP(hipGetLastError());
   }
   return PRNN_OK;
@@ -1625,6 +1739,7 @@ struct BwdWs {
   u32x4* at;
   floatx4* atb;
   CarryWs cs;
+  int* hq;  // packed streams: the head table (see GPk)
 };
 
 static void ga_split(int B, int T, int H, int* n_split, int* rows_per) {
@@ -1638,7 +1753,7 @@ static void ga_split(int B, int T, int H, int* n_split, int* rows_per) {
   *n_split = static_cast<int>((n_rows + rp - 1) / rp);
 }
 
-static BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
+static BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total, bool packed = false) {
   const int n_seq = B * H, n_chunks = (T + kChunk - 1) / kChunk;
   Carver cv(base);
   BwdWs w;
@@ -1652,44 +1767,45 @@ static BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   w.cs = carve_carry(cv, n_seq, n_chunks);
   w.at = carve_at(cv, H);
   w.atb = carve_atb(cv, H);
+  w.hq = packed ? static_cast<int*>(cv.take(sizeof(int) * static_cast<size_t>(T))) : nullptr;
   *total = cv.used;
   return w;
 }
 
-template <typename TX>
+template <typename TX, bool PK>
 static int run_bwd(const TX* wx, const TX* az, const TX* ar, const TX* an, const TX* h0,
                    const TX* states, const TX* grad, TX* g_wx, float* g_a, float* g_h0, int B,
-                   int T, int H, const BwdWs& w, hipStream_t stream) {
+                   int T, int H, const BwdWs& w, hipStream_t stream, const GPk& pk) {
   const int n_seq = B * H, n_chunks = (T + kChunk - 1) / kChunk;
   const int rev_blocks_local = (n_seq * ((n_chunks + kPair - 1) / kPair) + 3) / 4;
   const int rev_blocks = (n_seq * n_chunks + 3) / 4;
   const bool mfma_walks = walks_mfma("PRNN_GRU_REV_MFMA", n_seq, n_chunks);
   const int mfma_blocks = n_seq * ((n_chunks + 4 * kRCols - 1) / (4 * kRCols));
   gru_pack_at_kernel<TX><<<dim3(H), dim3(64), 0, stream>>>(az, ar, an, w.at, w.atb);
-  gru_phi_kernel<TX, TX, true><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
-      wx, az, ar, an, h0, states, B, T, H, n_chunks, w.phi, w.gates, w.at, w.atb);
+  gru_phi_kernel<TX, TX, true, PK><<<dim3(n_seq * n_chunks), dim3(256), 0, stream>>>(
+      wx, az, ar, an, h0, states, B, T, H, n_chunks, w.phi, w.gates, w.at, w.atb, pk);
   PRNN_HIP(hipGetLastError());
   if (mfma_walks)
-    gru_rev_mfma_kernel<TX, true><<<dim3(mfma_blocks), dim3(256), 0, stream>>>(
+    gru_rev_mfma_kernel<TX, true, PK><<<dim3(mfma_blocks), dim3(256), 0, stream>>>(
         az, ar, an, h0, states, grad, w.gates, nullptr, nullptr, nullptr, w.e, B, T, H,
-        n_chunks);
+        n_chunks, pk);
   else
-    gru_rev_local_kernel<TX><<<dim3(rev_blocks_local), dim3(256), 0, stream>>>(
-        az, ar, an, h0, states, grad, w.gates, w.e, B, T, H, n_chunks);
+    gru_rev_local_kernel<TX, PK><<<dim3(rev_blocks_local), dim3(256), 0, stream>>>(
+        az, ar, an, h0, states, grad, w.gates, w.e, B, T, H, n_chunks, pk);
   PRNN_HIP(hipGetLastError());
   carry_scan<true>(w.phi, w.e, w.carry, n_seq, n_chunks, w.cs, stream);
   PRNN_HIP(hipGetLastError());
   if (mfma_walks)
-    gru_rev_mfma_kernel<TX, false><<<dim3(mfma_blocks), dim3(256), 0, stream>>>(
+    gru_rev_mfma_kernel<TX, false, PK><<<dim3(mfma_blocks), dim3(256), 0, stream>>>(
         az, ar, an, h0, states, grad, w.gates, w.carry, g_wx, h0 != nullptr ? g_h0 : nullptr,
-        nullptr, B, T, H, n_chunks);
+        nullptr, B, T, H, n_chunks, pk);
   else
-    gru_rev_kernel<TX><<<dim3(rev_blocks), dim3(256), 0, stream>>>(
+    gru_rev_kernel<TX, PK><<<dim3(rev_blocks), dim3(256), 0, stream>>>(
         az, ar, an, h0, states, grad, w.gates, w.carry, g_wx, h0 != nullptr ? g_h0 : nullptr,
-        B, T, H, n_chunks);
+        B, T, H, n_chunks, pk);
   PRNN_HIP(hipGetLastError());
-  gru_ga_kernel<TX><<<dim3(w.n_split * H), dim3(256), 0, stream>>>(
-      h0, states, w.gates, g_wx, B, T, H, n_chunks, w.n_split, w.rows_per, w.part);
+  gru_ga_kernel<TX, PK><<<dim3(w.n_split * H), dim3(256), 0, stream>>>(
+      h0, states, w.gates, g_wx, B, T, H, n_chunks, w.n_split, w.rows_per, w.part, pk);
   PRNN_HIP(hipGetLastError());
   gru_ga_reduce_kernel<<<dim3((3 * H * DH * DH + 255) / 256), dim3(256), 0, stream>>>(
       w.part, H, w.n_split, g_a);
@@ -1713,6 +1829,89 @@ static int check(int B, int T, int H, int dh, int K, int dtype) {
 
 using namespace prnn;
 
+namespace {
+
+int head_newton_call(const void* wx, const void* a_z, const void* a_r, const void* a_n,
+                     const void* h0, void* out, int B, int T, int n_heads, int d_head,
+                     int max_iters, float omega, int dtype, void* workspace,
+                     size_t workspace_bytes, void* stream, const int* cu, int n_seq,
+                     const int* tbl) {
+  int rc = gru::check(B, T, n_heads, d_head, max_iters, dtype);
+  if (rc != PRNN_OK) return rc;
+  if (!wx || !a_z || !a_r || !a_n || !out || !workspace)
+    return fail(PRNN_ERR_VALUE, "wx, a_z, a_r, a_n, out and workspace must be non-null");
+  const bool packed = cu != nullptr;
+  if (packed && (n_seq < 1 || n_seq > T))
+    return fail(PRNN_ERR_VALUE, "n_seq must be in [1, T], got %d", n_seq);
+  size_t need = 0;
+  const gru::Ws w = gru::carve(workspace, B, T, n_heads, max_iters, &need, packed);
+  if (workspace_bytes < need)
+    return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const gru::GPk pk{cu, w.hq, tbl, n_seq};
+  if (packed) {
+    gru::gru_heads_kernel<<<dim3((T + 255) / 256), dim3(256), 0, s>>>(cu, n_seq, T, w.hq);
+    PRNN_HIP(hipGetLastError());
+  }
+  return with_storage(dtype, [&](auto tag) {
+    using TX = decltype(tag);
+    const TX* wx_ = static_cast<const TX*>(wx);
+    const TX* az = static_cast<const TX*>(a_z);
+    const TX* ar = static_cast<const TX*>(a_r);
+    const TX* an = static_cast<const TX*>(a_n);
+    const TX* h0_ = static_cast<const TX*>(h0);
+    TX* out_ = static_cast<TX*>(out);
+    if (packed)
+      return gru::run<TX, true>(wx_, az, ar, an, h0_, out_, B, T, n_heads, max_iters, omega, w,
+                                s, pk);
+    return gru::run<TX, false>(wx_, az, ar, an, h0_, out_, B, T, n_heads, max_iters, omega, w,
+                               s, pk);
+  });
+}
+
+int head_backward_call(const void* wx, const void* a_z, const void* a_r, const void* a_n,
+                       const void* h0, const void* states, const void* grad, void* g_wx,
+                       float* g_a, float* g_h0, int B, int T, int n_heads, int d_head, int dtype,
+                       void* workspace, size_t workspace_bytes, void* stream, const int* cu,
+                       int n_seq) {
+  int rc = gru::check(B, T, n_heads, d_head, 0, dtype);
+  if (rc != PRNN_OK) return rc;
+  if (!wx || !a_z || !a_r || !a_n || !states || !grad || !g_wx || !g_a || !workspace)
+    return fail(PRNN_ERR_VALUE,
+                "wx, a_z, a_r, a_n, states, grad, g_wx, g_a and workspace must be non-null");
+  const bool packed = cu != nullptr;
+  if (packed && (n_seq < 1 || n_seq > T))
+    return fail(PRNN_ERR_VALUE, "n_seq must be in [1, T], got %d", n_seq);
+  size_t need = 0;
+  const gru::BwdWs w = gru::carve_bwd(workspace, B, T, n_heads, &need, packed);
+  if (workspace_bytes < need)
+    return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const gru::GPk pk{cu, w.hq, nullptr, n_seq};
+  if (packed) {
+    gru::gru_heads_kernel<<<dim3((T + 255) / 256), dim3(256), 0, s>>>(cu, n_seq, T, w.hq);
+    PRNN_HIP(hipGetLastError());
+  }
+  return with_storage(dtype, [&](auto tag) {
+    using TX = decltype(tag);
+    const TX* wx_ = static_cast<const TX*>(wx);
+    const TX* az = static_cast<const TX*>(a_z);
+    const TX* ar = static_cast<const TX*>(a_r);
+    const TX* an = static_cast<const TX*>(a_n);
+    const TX* h0_ = static_cast<const TX*>(h0);
+    const TX* st_ = static_cast<const TX*>(states);
+    const TX* gr_ = static_cast<const TX*>(grad);
+    TX* gwx = static_cast<TX*>(g_wx);
+    if (packed)
+      return gru::run_bwd<TX, true>(wx_, az, ar, an, h0_, st_, gr_, gwx, g_a, g_h0, B, T,
+                                    n_heads, w, s, pk);
+    return gru::run_bwd<TX, false>(wx_, az, ar, an, h0_, st_, gr_, gwx, g_a, g_h0, B, T, n_heads,
+                                   w, s, pk);
+  });
+}
+
+}  // namespace
+
 extern "C" PRNN_API size_t prnn_gru_head_newton_workspace_size(int B, int T, int n_heads,
                                                                int d_head, int max_iters,
                                                                int dtype) {
@@ -1727,22 +1926,31 @@ extern "C" PRNN_API int prnn_gru_head_newton(const void* wx, const void* a_z, co
                                              int T, int n_heads, int d_head, int max_iters,
                                              float omega, int dtype, void* workspace,
                                              size_t workspace_bytes, void* stream) {
-  int rc = gru::check(B, T, n_heads, d_head, max_iters, dtype);
-  if (rc != PRNN_OK) return rc;
-  if (!wx || !a_z || !a_r || !a_n || !out || !workspace)
-    return fail(PRNN_ERR_VALUE, "wx, a_z, a_r, a_n, out and workspace must be non-null");
-  size_t need = 0;
-  const gru::Ws w = gru::carve(workspace, B, T, n_heads, max_iters, &need);
-  if (workspace_bytes < need)
-    return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  return with_storage(dtype, [&](auto tag) {
-    using TX = decltype(tag);
-    return gru::run(static_cast<const TX*>(wx), static_cast<const TX*>(a_z),
-                    static_cast<const TX*>(a_r), static_cast<const TX*>(a_n),
-                    static_cast<const TX*>(h0), static_cast<TX*>(out), B, T, n_heads, max_iters,
-                    omega, w, s);
-  });
+  return head_newton_call(wx, a_z, a_r, a_n, h0, out, B, T, n_heads, d_head, max_iters, omega,
+                          dtype, workspace, workspace_bytes, stream, nullptr, 0, nullptr);
+}
+
+extern "C" PRNN_API size_t prnn_gru_head_newton_packed_workspace_size(int T, int n_heads,
+                                                                      int d_head, int max_iters,
+                                                                      int dtype) {
+  if (gru::check(1, T, n_heads, d_head, max_iters, dtype) != PRNN_OK) return 0;
+  size_t total = 0;
+  gru::carve(nullptr, 1, T, n_heads, max_iters, &total, true);
+  return total;
+}
+
+extern "C" PRNN_API int prnn_gru_head_newton_packed(const void* wx, const void* a_z,
+                                                    const void* a_r, const void* a_n,
+                                                    const void* h0, void* out, int T,
+                                                    int n_heads, int d_head, int max_iters,
+                                                    float omega, int dtype,
+                                                    const int* cu_seqlens, int n_seq,
+                                                    const int* block_table, void* workspace,
+                                                    size_t workspace_bytes, void* stream) {
+  if (!cu_seqlens) return fail(PRNN_ERR_VALUE, "cu_seqlens must be non-null");
+  return head_newton_call(wx, a_z, a_r, a_n, h0, out, 1, T, n_heads, d_head, max_iters, omega,
+                          dtype, workspace, workspace_bytes, stream, cu_seqlens, n_seq,
+                          block_table);
 }
 
 extern "C" PRNN_API size_t prnn_gru_head_backward_workspace_size(int B, int T, int n_heads,
@@ -1760,23 +1968,28 @@ extern "C" PRNN_API int prnn_gru_head_backward(const void* wx, const void* a_z, 
                                                int n_heads, int d_head, int dtype,
                                                void* workspace, size_t workspace_bytes,
                                                void* stream) {
-  int rc = gru::check(B, T, n_heads, d_head, 0, dtype);
-  if (rc != PRNN_OK) return rc;
-  if (!wx || !a_z || !a_r || !a_n || !states || !grad || !g_wx || !g_a || !workspace)
-    return fail(PRNN_ERR_VALUE,
-                "wx, a_z, a_r, a_n, states, grad, g_wx, g_a and workspace must be non-null");
-  size_t need = 0;
-  const gru::BwdWs w = gru::carve_bwd(workspace, B, T, n_heads, &need);
-  if (workspace_bytes < need)
-    return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  return with_storage(dtype, [&](auto tag) {
-    using TX = decltype(tag);
-    return gru::run_bwd(static_cast<const TX*>(wx), static_cast<const TX*>(a_z),
-                        static_cast<const TX*>(a_r), static_cast<const TX*>(a_n),
-                        static_cast<const TX*>(h0), static_cast<const TX*>(states),
-                        static_cast<const TX*>(grad), static_cast<TX*>(g_wx), g_a, g_h0, B, T,
-                        n_heads, w, s);
-  });
+  return head_backward_call(wx, a_z, a_r, a_n, h0, states, grad, g_wx, g_a, g_h0, B, T, n_heads,
+                            d_head, dtype, workspace, workspace_bytes, stream, nullptr, 0);
 }
 
+extern "C" PRNN_API size_t prnn_gru_head_backward_packed_workspace_size(int T, int n_heads,
+                                                                        int d_head, int dtype) {
+  if (gru::check(1, T, n_heads, d_head, 0, dtype) != PRNN_OK) return 0;
+  size_t total = 0;
+  gru::carve_bwd(nullptr, 1, T, n_heads, &total, true);
+  return total;
+}
+
+extern "C" PRNN_API int prnn_gru_head_backward_packed(const void* wx, const void* a_z,
+                                                      const void* a_r, const void* a_n,
+                                                      const void* h0, const void* states,
+                                                      const void* grad, void* g_wx, float* g_a,
+                                                      float* g_h0, int T, int n_heads,
+                                                      int d_head, int dtype,
+                                                      const int* cu_seqlens, int n_seq,
+                                                      void* workspace, size_t workspace_bytes,
+                                                      void* stream) {
+  if (!cu_seqlens) return fail(PRNN_ERR_VALUE, "cu_seqlens must be non-null");
+  return head_backward_call(wx, a_z, a_r, a_n, h0, states, grad, g_wx, g_a, g_h0, 1, T, n_heads,
+                            d_head, dtype, workspace, workspace_bytes, stream, cu_seqlens, n_seq);
+}

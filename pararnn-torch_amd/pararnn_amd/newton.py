@@ -36,6 +36,7 @@ from pararnn_amd.cells import SLSTM_HIDDEN, ParaGRU, ParaSLSTM
 from pararnn_amd.ragged import (
     RaggedPlan,
     gather_h0,
+    packed_in_kernel,
     prepend_state_ragged,
     validate_cu_seqlens,
 )
@@ -164,7 +165,9 @@ def fused_newton(
         if fused_time_loop:
             raise TypeError("fused_time_loop is ParaSLSTM only")
         if block_table is not None:
-            raise TypeError("block_table fused Newton supports ParaSLSTM mix='diag' only")
+            # paged h0: the rows the table names (one per sequence, or batch row)
+            rows = wx.shape[0] if cu_seqlens is None else int(cu_seqlens.numel()) - 1
+            h0 = gather_h0(h0, block_table, rows, (int(cell.d_h),))
         a_z, a_r, a_n = cell.clipped_a_head()
         return ops.newton_gru_head_fused(
             wx, a_z, a_r, a_n, h0, cu_seqlens, max_iters=max_iters, omega=omega
@@ -196,12 +199,6 @@ def fused_newton(
             window_len=0 if fused_window_len is None else int(fused_window_len),
         )
     raise TypeError(_fused_error(cell, wx))
-
-
-def packed_in_kernel() -> bool:
-    """Packed diag-sLSTM streams run in the kernels (heads cut the carry);
-    ``PARARNN_AMD_PACKED=0`` pads them into length groups instead."""
-    return os.environ.get("PARARNN_AMD_PACKED", "1") != "0"
 
 
 def _prepend_any(states: Tensor, h0: Tensor | None, cu_seqlens: Tensor | None) -> Tensor:
@@ -396,7 +393,7 @@ def newton_apply(
             raise RuntimeError("block_table newton is inference-only")
     with _newton_precision_region(x.device):
         if cu_seqlens is not None:
-            if isinstance(cell, ParaSLSTM) and cell.mix == "diag" and packed_in_kernel():
+            if _packable(cell) and packed_in_kernel():
                 return _newton_packed(cell, x, config, h0=h0, stats=stats,
                                       cu_seqlens=cu_seqlens, block_table=block_table,
                                       needs_grad=needs_grad)
@@ -443,10 +440,17 @@ def _check_ragged_args(x: Tensor, config: NewtonConfig) -> None:
         raise ValueError("fused_time_loop cannot be combined with cu_seqlens")
 
 
+def _packable(cell: nn.Module) -> bool:
+    """Cells whose kernels solve packed streams in place."""
+    return (isinstance(cell, ParaSLSTM) and cell.mix == "diag") or (
+        isinstance(cell, ParaGRU) and cell.mix == "head")
+
+
 def _newton_packed(cell, x, config, *, h0, stats, cu_seqlens, block_table, needs_grad):
-    """A packed diag-sLSTM stream in one solve: the kernels cut the carry at
-    every sequence head and read each head's h0 row themselves (block_table
-    rows of a pool when given), as the reference's packed semantics
+    """A packed stream in one solve (diag sLSTM, head GRU): the kernels cut the
+    carry at every sequence head and read each head's h0 row themselves
+    (block_table rows of a pool when given: in the sLSTM kernels, gathered
+    first for the head GRU), as the reference's packed semantics
     (solvers/scan.py:206-216, layout.py:115-138); K, P, the Picard ladder and
     the residual gate act on the packed stream (newton/__init__.py:327-355)."""
     cs = validate_cu_seqlens(cu_seqlens, x.shape[1], x.device)
@@ -619,10 +623,12 @@ def _eq26_vjp(cell: nn.Module, states: Tensor, x: Tensor, partial: Tensor, *,
         by_name = {"R": g_r, "W_x.bias": g_b.reshape(-1).to(cell.W_x.bias.dtype)}
     elif isinstance(cell, ParaGRU) and cell.mix == "head":
         a_z, a_r, a_n = cell.clipped_a_head()
-        g_wx, g_a, g_h0 = ops.gru_head_backward_fused(wx, a_z, a_r, a_n, h0, states, partial)
+        g_wx, g_a, g_h0 = ops.gru_head_backward_fused(wx, a_z, a_r, a_n, h0, states, partial,
+                                                      cu_seqlens)
         determinism.maybe_check_fused_vjp_once(
             (g_a,),
-            lambda: (ops.gru_head_backward_fused(wx, a_z, a_r, a_n, h0, states, partial)[1],),
+            lambda: (ops.gru_head_backward_fused(wx, a_z, a_r, a_n, h0, states, partial,
+                                                 cu_seqlens)[1],),
             cell_name=type(cell).__name__, shape=states.shape)
         by_name = {}
         for i, name in enumerate(("A_z", "A_r", "A_n")):

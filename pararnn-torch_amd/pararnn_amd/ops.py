@@ -452,6 +452,11 @@ def newton_gru_head_fused(
 
     Initial guess ``f(h_prev0, x_t)`` (zeros except ``h0`` at t = 0), then
     ``max_iters`` Newton iterations, all in fp32; result in ``wx``'s dtype.
+    ``cu_seqlens`` packs ``S`` sequences into ``wx`` ``(1, N, 3 d_h)`` with
+    ``h0`` ``(S, d_h)``: the kernels cut the carry at every head (the
+    reference's packed semantics, solvers/scan.py:206-216; its fused op takes
+    rectangular batches only), or with ``PARARNN_AMD_PACKED=0`` the sequences
+    run as padded length groups.
     """
     if a_z.dim() != 3 or a_z.shape[-1] != a_z.shape[-2]:
         raise ValueError(f"a_z needs (H,d,d), got {tuple(a_z.shape)}")
@@ -464,27 +469,31 @@ def newton_gru_head_fused(
     if d_head > 64:
         raise TypeError(f"newton_gru_head_fused: pararnn_amd provides d_head <= 64, got {d_head}")
     if cu_seqlens is not None:
-        # Packed sequences run as a padded batch, each from its own h0.
-        from pararnn_amd.ragged import RaggedPlan, validate_cu_seqlens
+        from pararnn_amd.ragged import RaggedPlan, packed_in_kernel, validate_cu_seqlens
 
         if wx.shape[0] != 1:
             raise ValueError(f"cu_seqlens packs wx with batch=1, got batch={wx.shape[0]}")
-        cs = validate_cu_seqlens(cu_seqlens, wx.shape[1])
+        cs = validate_cu_seqlens(cu_seqlens, wx.shape[1], wx.device)
+        n_seq = int(cs.numel()) - 1
+        if h0 is not None and h0.shape != (n_seq, d_h):
+            raise ValueError(f"h0 shape {tuple(h0.shape)} != {(n_seq, d_h)}")
+        if packed_in_kernel():
+            return _gru_head_dense(wx, a_z, a_r, a_n, h0, max_iters, omega, cs)
         plan = RaggedPlan(cs, wx.device)
-        if h0 is not None and h0.shape != (plan.n_seq, d_h):
-            raise ValueError(f"h0 shape {tuple(h0.shape)} != {(plan.n_seq, d_h)}")
         return plan.run(wx, h0, lambda w, h: _gru_head_dense(w, a_z, a_r, a_n, h, max_iters,
                                                               omega))
     return _gru_head_dense(wx, a_z, a_r, a_n, h0, max_iters, omega)
 
 
-def _gru_head_dense(wx, a_z, a_r, a_n, h0, max_iters, omega):
+def _gru_head_dense(wx, a_z, a_r, a_n, h0, max_iters, omega, cs=None):
+    """A rectangular batch, or (``cs``: checked int64 offsets) one packed stream."""
     n_heads, d_head, _ = a_z.shape
     d_h = n_heads * d_head
     batch, time, _ = wx.shape
     code = _validate("newton_gru_head_fused", wx, a_z, a_r, a_n, h0)
-    if h0 is not None and h0.shape != (batch, d_h):
-        raise ValueError(f"h0 shape {tuple(h0.shape)} != {(batch, d_h)}")
+    rows = batch if cs is None else int(cs.numel()) - 1
+    if h0 is not None and h0.shape != (rows, d_h):
+        raise ValueError(f"h0 shape {tuple(h0.shape)} != {(rows, d_h)}")
     if max_iters < 0:
         raise ValueError(f"max_iters must be >= 0, got {max_iters!r}")
     # heads narrower than 64 run as block-diagonal 64 x 64 blocks
@@ -495,14 +504,25 @@ def _gru_head_dense(wx, a_z, a_r, a_n, h0, max_iters, omega):
     out = wx.new_empty(batch, time, hb.d_pad)
     lib = _lib.load()
     with torch.cuda.device(wx.device):
-        nbytes = lib.prnn_gru_head_newton_workspace_size(batch, time, hb.n_blocks, 64,
-                                                         int(max_iters), code)
-        ws = _workspace(nbytes, wx.device)
-        rc = lib.prnn_gru_head_newton(
-            _ptr(wx), _ptr(a_z), _ptr(a_r), _ptr(a_n), _ptr(h0), _ptr(out), batch, time,
-            hb.n_blocks, 64, int(max_iters), float(omega), code, _ptr(ws), ws.numel(),
-            _stream(wx.device),
-        )
+        if cs is None:
+            nbytes = lib.prnn_gru_head_newton_workspace_size(batch, time, hb.n_blocks, 64,
+                                                             int(max_iters), code)
+            ws = _workspace(nbytes, wx.device)
+            rc = lib.prnn_gru_head_newton(
+                _ptr(wx), _ptr(a_z), _ptr(a_r), _ptr(a_n), _ptr(h0), _ptr(out), batch, time,
+                hb.n_blocks, 64, int(max_iters), float(omega), code, _ptr(ws), ws.numel(),
+                _stream(wx.device),
+            )
+        else:
+            cs32 = cs.to(device=wx.device, dtype=torch.int32).contiguous()
+            nbytes = lib.prnn_gru_head_newton_packed_workspace_size(time, hb.n_blocks, 64,
+                                                                    int(max_iters), code)
+            ws = _workspace(nbytes, wx.device)
+            rc = lib.prnn_gru_head_newton_packed(
+                _ptr(wx), _ptr(a_z), _ptr(a_r), _ptr(a_n), _ptr(h0), _ptr(out), time,
+                hb.n_blocks, 64, int(max_iters), float(omega), code, _ptr(cs32),
+                int(cs32.numel()) - 1, None, _ptr(ws), ws.numel(), _stream(wx.device),
+            )
     _lib.check(rc, "newton_gru_head_fused")
     return hb.from_blocks(out)
 
@@ -516,7 +536,7 @@ def _(wx, a_z, a_r, a_n, h0=None, cu_seqlens=None, *, max_iters, omega):
 @torch.library.custom_op("pararnn::gru_head_backward_fused", mutates_args=())
 def gru_head_backward_fused(
     wx: Tensor, a_z: Tensor, a_r: Tensor, a_n: Tensor, h0: Tensor | None, states: Tensor,
-    grad: Tensor,
+    grad: Tensor, cu_seqlens: Tensor | None = None,
 ) -> tuple[Tensor, Tensor, Tensor]:
     """Eq. 2.6 backward of ``ParaGRU(mix='head')`` at ``H* = states`` on the GPU.
 
@@ -526,6 +546,8 @@ def gru_head_backward_fused(
     None).  The reference computes these with ``reverse_factor_scan_gru_head``,
     ``gru_head_t0_vjp`` and ``gru_head_recurrence_vjp``
     (solvers/newton/__init__.py:798-817, kernels/vjp_gru.py:656).
+    ``cu_seqlens``: one packed stream ``(1, N, ...)`` of ``S`` sequences
+    (nothing flows across a head; ``h0`` and ``g_h0`` are ``(S, d_h)``).
     """
     if a_z.dim() != 3 or a_z.shape[-1] != a_z.shape[-2]:
         raise ValueError(f"a_z needs (H,d,d), got {tuple(a_z.shape)}")
@@ -542,8 +564,17 @@ def gru_head_backward_fused(
     for name, t in (("states", states), ("grad", grad)):
         if t.shape != (batch, time, d_h):
             raise ValueError(f"{name} shape {tuple(t.shape)} != {(batch, time, d_h)}")
-    if h0 is not None and h0.shape != (batch, d_h):
-        raise ValueError(f"h0 shape {tuple(h0.shape)} != {(batch, d_h)}")
+    cs32 = None
+    rows = batch
+    if cu_seqlens is not None:
+        from pararnn_amd.ragged import validate_cu_seqlens
+
+        if batch != 1:
+            raise ValueError(f"cu_seqlens packs wx with batch=1, got batch={batch}")
+        cs32 = validate_cu_seqlens(cu_seqlens, time, wx.device).to(torch.int32).contiguous()
+        rows = int(cs32.numel()) - 1
+    if h0 is not None and h0.shape != (rows, d_h):
+        raise ValueError(f"h0 shape {tuple(h0.shape)} != {(rows, d_h)}")
     # heads narrower than 64 run as block-diagonal 64 x 64 blocks
     hb = HeadBlocks(n_heads, d_head, wx.device)
     wx = hb.to_blocks(wx, 3).contiguous()
@@ -553,25 +584,37 @@ def gru_head_backward_fused(
     h0 = None if h0 is None else hb.to_blocks(h0).contiguous()
     g_wx = torch.empty_like(wx)
     g_a = torch.empty(3, hb.n_blocks, 64, 64, dtype=torch.float32, device=wx.device)
-    g_h0 = torch.zeros(batch, hb.d_pad, dtype=torch.float32, device=wx.device)
+    g_h0 = torch.zeros(rows, hb.d_pad, dtype=torch.float32, device=wx.device)
     lib = _lib.load()
     with torch.cuda.device(wx.device):
-        nbytes = lib.prnn_gru_head_backward_workspace_size(batch, time, hb.n_blocks, 64, code)
-        ws = _workspace(nbytes, wx.device)
-        rc = lib.prnn_gru_head_backward(
-            _ptr(wx), _ptr(a_z), _ptr(a_r), _ptr(a_n), _ptr(h0), _ptr(states), _ptr(grad),
-            _ptr(g_wx), _ptr(g_a), _ptr(g_h0), batch, time, hb.n_blocks, 64, code, _ptr(ws),
-            ws.numel(), _stream(wx.device),
-        )
+        if cs32 is None:
+            nbytes = lib.prnn_gru_head_backward_workspace_size(batch, time, hb.n_blocks, 64,
+                                                               code)
+            ws = _workspace(nbytes, wx.device)
+            rc = lib.prnn_gru_head_backward(
+                _ptr(wx), _ptr(a_z), _ptr(a_r), _ptr(a_n), _ptr(h0), _ptr(states), _ptr(grad),
+                _ptr(g_wx), _ptr(g_a), _ptr(g_h0), batch, time, hb.n_blocks, 64, code,
+                _ptr(ws), ws.numel(), _stream(wx.device),
+            )
+        else:
+            nbytes = lib.prnn_gru_head_backward_packed_workspace_size(time, hb.n_blocks, 64,
+                                                                      code)
+            ws = _workspace(nbytes, wx.device)
+            rc = lib.prnn_gru_head_backward_packed(
+                _ptr(wx), _ptr(a_z), _ptr(a_r), _ptr(a_n), _ptr(h0), _ptr(states), _ptr(grad),
+                _ptr(g_wx), _ptr(g_a), _ptr(g_h0), time, hb.n_blocks, 64, code, _ptr(cs32),
+                rows, _ptr(ws), ws.numel(), _stream(wx.device),
+            )
     _lib.check(rc, "gru_head_backward_fused")
     return hb.from_blocks(g_wx, 3), hb.head_grads(g_a), hb.from_blocks(g_h0)
 
 
 @gru_head_backward_fused.register_fake
-def _(wx, a_z, a_r, a_n, h0, states, grad):
+def _(wx, a_z, a_r, a_n, h0, states, grad, cu_seqlens=None):
     n_heads, d_head, _ = a_z.shape
+    rows = states.shape[0] if cu_seqlens is None else cu_seqlens.shape[0] - 1
     return (
         torch.empty_like(wx),
         wx.new_empty(3, n_heads, d_head, d_head, dtype=torch.float32),
-        wx.new_empty(states.shape[0], n_heads * d_head, dtype=torch.float32),
+        wx.new_empty(rows, n_heads * d_head, dtype=torch.float32),
     )

@@ -49,6 +49,12 @@ def _known(t: Tensor, time: int) -> bool:
     return c is not None and c[1] == time and any(r() is t and v == t._version for r, v in c[0])
 
 
+def packed_in_kernel() -> bool:
+    """Packed streams run in the kernels (heads cut the carry; diag sLSTM and
+    head GRU); ``PARARNN_AMD_PACKED=0`` pads them into length groups instead."""
+    return os.environ.get("PARARNN_AMD_PACKED", "1") != "0"
+
+
 def validate_cu_seqlens(cu_seqlens: Tensor, time: int,
                         device: torch.device | None = None) -> Tensor:
     """``(S+1,)`` exclusive prefix with ``[0] = 0``, last = ``time``, strictly increasing

@@ -195,19 +195,45 @@ def test_slstm_ragged_length_groups(monkeypatch):
 
 
 def test_gru_head_ragged_length_groups(monkeypatch):
+    """Head GRU, uneven lengths: the packed stream in the kernels (default),
+    padded length groups (PARARNN_AMD_PACKED=0) and one padded rectangle
+    (also PARARNN_AMD_RAGGED_GROUPS=0): forward and every gradient, and the
+    forward against the per-sequence oracle."""
+    from oracle.ragged import gru_head_newton_ragged
+
     from pararnn_amd import ParaGRU, newton_apply
 
     print("case gru head ragged length groups fp32 (3 groups, lengths 12..2500)", flush=True)
     torch.manual_seed(7)
     cell = ParaGRU(16, 128, mix="head", n_heads=2).to(DEV)
     lengths, cs, x, (h0,) = _uneven(16, extra=((128,),))
-    x, h0, csd = x.to(DEV), (0.3 * h0).to(DEV), cs.to(DEV)
-    with torch.no_grad():
-        a = newton_apply(cell, x, _cfg(3), h0=h0, cu_seqlens=csd)
-        monkeypatch.setenv("PARARNN_AMD_RAGGED_GROUPS", "0")
-        b = newton_apply(cell, x, _cfg(3), h0=h0, cu_seqlens=csd)
-    err = (a - b).abs().max().item()
-    print(f"  max|grouped - single| {err:.2e}", flush=True)
+    up = torch.randn(1, x.shape[1], 128, generator=torch.Generator().manual_seed(8))
+    x, h0, csd, up = x.to(DEV), (0.3 * h0).to(DEV), cs.to(DEV), up.to(DEV)
+
+    def run():
+        cell.zero_grad(set_to_none=True)
+        xx, hh = x.clone().requires_grad_(True), h0.clone().requires_grad_(True)
+        H = newton_apply(cell, xx, _cfg(3), h0=hh, cu_seqlens=csd)
+        (H * up).sum().backward()
+        out = {"H": H.detach(), "x": xx.grad, "h0": hh.grad}
+        out.update({n: p.grad.clone() for n, p in cell.named_parameters()})
+        return out
+
+    packed = run()
+    monkeypatch.setenv("PARARNN_AMD_PACKED", "0")
+    grouped = run()
+    monkeypatch.setenv("PARARNN_AMD_RAGGED_GROUPS", "0")
+    single = run()
+    for name, got in (("grouped", grouped), ("packed", packed)):
+        for k in got:
+            e = ((got[k] - single[k]).abs().max() / single[k].abs().max()).item()
+            print(f"  {k}: {name} vs single rel diff {e:.2e}", flush=True)
+            assert e <= 1e-5, (name, k)
+    p = O.GRUHeadParams(cell.W_x.weight.detach().cpu(), cell.W_x.bias.detach().cpu(),
+                        *(a.detach().cpu() for a in cell.clipped_a_head()))
+    own = gru_head_newton_ragged(p, x.cpu(), cs, max_iters=3, h0=h0.cpu())
+    err = (packed["H"].cpu() - own).abs().max().item()
+    print(f"  packed: max|gpu - per-sequence oracle| {err:.2e}", flush=True)
     assert err <= 1e-5
 
 
