@@ -219,6 +219,42 @@ def slstm_cfg2(torch, reps: int):
     }
 
 
+def _ragged_head(torch, lengths, reps: int):
+    """The same packed lengths through ParaGRU(mix='head') (H=8, d_head=64,
+    fp32, K=3, the config-4 cell): packed in the kernels, by length groups
+    (PARARNN_AMD_PACKED=0), and one unbroken stream of the same tokens."""
+    import os
+
+    from pararnn_amd import NewtonConfig, ParaGRU, newton_apply
+
+    dev = "cuda:0"
+    torch.manual_seed(1)
+    cell = ParaGRU(512, 512, mix="head", n_heads=8).to(dev)
+    cs = torch.tensor([0] + list(lengths)).cumsum(0).to(dev)
+    n = int(cs[-1])
+    g = torch.Generator(device=dev).manual_seed(4)
+    x = torch.randn(1, n, 512, generator=g, device=dev)
+    cfg = NewtonConfig(max_iters=3, residual_atol=None, residual_fail=None)
+    prev = os.environ.get("PARARNN_AMD_PACKED")
+    res = {"workload": f"ParaGRU head H=8 d_head=64 fp32 K=3, same cu_seqlens (N={n}), "
+                       "newton_apply"}
+    try:
+        with torch.no_grad():
+            for packed, key in (("1", "packed"), ("0", "grouped")):
+                os.environ["PARARNN_AMD_PACKED"] = packed
+                ms = _time(torch, lambda: newton_apply(cell, x, cfg, cu_seqlens=cs), reps, warm=1)
+                res[key] = {"ms": ms, "tokens_per_s": n / (ms * 1e-3)}
+            ms = _time(torch, lambda: newton_apply(cell, x, cfg), reps, warm=1)
+            res["same_tokens_one_stream"] = {"ms": ms, "tokens_per_s": n / (ms * 1e-3)}
+    finally:
+        if prev is None:
+            os.environ.pop("PARARNN_AMD_PACKED", None)
+        else:
+            os.environ["PARARNN_AMD_PACKED"] = prev
+    res["packed_vs_one_stream"] = res["same_tokens_one_stream"]["ms"] / res["packed"]["ms"]
+    return res
+
+
 def ragged_decode(torch, reps: int):
     """The packed-ragged and T=1 rows beside the metric (not bench lines of
     their own): ParaSLSTM diag d=1024 bf16, K=2, P=5.
@@ -265,6 +301,7 @@ def ragged_decode(torch, reps: int):
             else:
                 os.environ[k] = v
     res["packed_vs_one_stream"] = res["same_tokens_one_stream"]["ms"] / res["packed"]["ms"]
+    res["head_gru"] = _ragged_head(torch, lengths, reps)
     ragged = {"workload": f"ParaSLSTM diag d=1024 bf16 K=2 P=5, cu_seqlens 1x65536 + 63x1024 "
                           f"(N={n}), newton_apply", **res}
 
