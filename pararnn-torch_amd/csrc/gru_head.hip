@@ -513,46 +513,76 @@ __global__ __launch_bounds__(256) void gru_phi_kernel(
     }
   };
 
+  // One step, in three MFMA groups of 8, each interleaved with VALU work
+  // that does not wait on it (one MFMA, then the VALU that fits in its
+  // execution), so the matrix pipe and the vector ALU overlap inside the wave:
+  //   A_r^T P  with  Y = r P,  P <- d1 P
+  //   A_z^T P  with  Y += d5 (A_r^T P), Y -> bf16
+  //   A_n^T Y  with  P += d2 (A_z^T P)
+  // then P += d3 (A_n^T Y) and P -> bf16 for the next step.  The sums are the
+  // same fused multiply-adds in the same order as J Phi written out.
+  bf16x8 bp[2];
+  to_b(P, bp);
   for (int s = 0; s < (cut ? 0 : len); ++s) {
     const float* rsc = &sh.rs[s][0][4 * g];
-    bf16x8 bp[2];
-    to_b(P, bp);
-    // Y = r P + d5 (A_r^T P), the operand of the A_n product.
-    float X[4][4];
-    product(atr, bp, X);
-    __builtin_amdgcn_sched_barrier(0);
-    float Y[4][4];
+    float rv[4][4], d1v[4][4], d2v[4][4], d3v[4][4], d5v[4][4];
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
-      const float4 r4 = *reinterpret_cast<const float4*>(rsc + 3 * DH + 16 * rt);
-      const float4 d5 = *reinterpret_cast<const float4*>(rsc + 4 * DH + 16 * rt);
-      const float rv[4] = {r4.x, r4.y, r4.z, r4.w}, d5v[4] = {d5.x, d5.y, d5.z, d5.w};
-#pragma unroll
-      for (int v = 0; v < 4; ++v) Y[rt][v] = rv[v] * P[rt][v] + d5v[v] * X[rt][v];
+      const float4 q0 = *reinterpret_cast<const float4*>(rsc + 0 * DH + 16 * rt);
+      const float4 q1 = *reinterpret_cast<const float4*>(rsc + 1 * DH + 16 * rt);
+      const float4 q2 = *reinterpret_cast<const float4*>(rsc + 2 * DH + 16 * rt);
+      const float4 q3 = *reinterpret_cast<const float4*>(rsc + 3 * DH + 16 * rt);
+      const float4 q4 = *reinterpret_cast<const float4*>(rsc + 4 * DH + 16 * rt);
+      d1v[rt][0] = q0.x; d1v[rt][1] = q0.y; d1v[rt][2] = q0.z; d1v[rt][3] = q0.w;
+      d2v[rt][0] = q1.x; d2v[rt][1] = q1.y; d2v[rt][2] = q1.z; d2v[rt][3] = q1.w;
+      d3v[rt][0] = q2.x; d3v[rt][1] = q2.y; d3v[rt][2] = q2.z; d3v[rt][3] = q2.w;
+      rv[rt][0] = q3.x; rv[rt][1] = q3.y; rv[rt][2] = q3.z; rv[rt][3] = q3.w;
+      d5v[rt][0] = q4.x; d5v[rt][1] = q4.y; d5v[rt][2] = q4.z; d5v[rt][3] = q4.w;
     }
-    bf16x8 by[2];
-    to_b(Y, by);
-    // A_z^T P and A_n^T Y issued together; P <- d1 P + d2 (A_z^T P) + d3 (A_n^T Y).
-    float X1[4][4], X3[4][4];
-    product(atz, bp, X1);
-    product(atn, by, X3);
-    __builtin_amdgcn_sched_barrier(0);
+    float X[4][4], X1[4][4], X3[4][4], Y[4][4];
+    product(atr, bp, X);
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-      const float4 d1 = *reinterpret_cast<const float4*>(rsc + 0 * DH + 16 * rt);
-      const float4 d2 = *reinterpret_cast<const float4*>(rsc + 1 * DH + 16 * rt);
-      const float4 d3 = *reinterpret_cast<const float4*>(rsc + 2 * DH + 16 * rt);
-      const float d1v[4] = {d1.x, d1.y, d1.z, d1.w}, d2v[4] = {d2.x, d2.y, d2.z, d2.w};
-      const float d3v[4] = {d3.x, d3.y, d3.z, d3.w};
+    for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        // in place: P <- d1 P, then two fused multiply-adds into P (no copy
-        // of the new Phi back into Phi's registers)
-        float t = d1v[v] * P[rt][v];
-        t = __builtin_fmaf(d2v[v], X1[rt][v], t);
-        P[rt][v] = __builtin_fmaf(d3v[v], X3[rt][v], t);
+        Y[rt][v] = rv[rt][v] * P[rt][v];
+        P[rt][v] = d1v[rt][v] * P[rt][v];
       }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
     }
+    __builtin_amdgcn_sched_barrier(0);
+    product(atz, bp, X1);
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) Y[rt][v] = __builtin_fmaf(d5v[rt][v], X[rt][v], Y[rt][v]);
+    bf16x8 by[2];
+    to_b(Y, by);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    product(atn, by, X3);
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) P[rt][v] = __builtin_fmaf(d2v[rt][v], X1[rt][v], P[rt][v]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) P[rt][v] = __builtin_fmaf(d3v[rt][v], X3[rt][v], P[rt][v]);
+    to_b(P, bp);
   }
   float* po = phi_out + static_cast<size_t>(blockIdx.x) * DH * DH;
   if (TRANS) {
