@@ -949,9 +949,11 @@ slstm_newton_fused_kernel(
     int n_tiles, int K, float omega, float eps, int* __restrict__ counter,
     unsigned long long* __restrict__ agg, unsigned long long* __restrict__ incl,
     unsigned long long* __restrict__ hlast, int tag_base, Spin spin, Packed pk) {
-  // predecessors per wave per look-back round (the deterministic walk, which
-  // must find an inclusive carry inside its window, looks twice as far)
-  constexpr int KP = DET ? 2 : 1;
+  // predecessors per wave per look-back round, in both modes: a window of 8
+  // (20 KB more LDS) would leave one block per CU beside the tanh cache.  The
+  // deterministic walk waits for an inclusive carry inside its window; its
+  // result does not depend on the window.
+  constexpr int KP = 1;
   using XS = RowStash<TX>;
   __shared__ float s_agg[W][20][kCB];
   __shared__ float s_carry[W][4][kCB];
