@@ -138,7 +138,20 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
   // h0 row; nothing flows from a head to the step before it (nu = 0 there),
   // and the head's nu = J^T mu is that sequence's dL/dh0.
   Heads hd{0ull, 0};
-  if constexpr (PK) hd = find_heads(pk, t0, n_steps);
+  int ns = n_steps;
+  if constexpr (PK) {
+    hd = find_heads(pk, t0, n_steps);
+    // The head flags and the step count pass through an opaque copy: what the
+    // steps derive from them is computed where it is used, not hoisted out of
+    // the unrolled loops into scalar registers for all L steps.
+    uint32_t lo = static_cast<uint32_t>(hd.mask), hi = static_cast<uint32_t>(hd.mask >> 32);
+    int q0 = hd.seq0;
+    asm volatile("" : "+v"(lo), "+v"(hi), "+v"(q0), "+v"(ns));
+    hd.mask = (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(hi)) << 32) |
+              __builtin_amdgcn_readfirstlane(lo);
+    hd.seq0 = __builtin_amdgcn_readfirstlane(q0);
+    ns = __builtin_amdgcn_readfirstlane(ns);
+  }
   auto prev_of = [&](int s, float p[4]) {
     if (PK && hd.at(s)) {
       head_state(pk, h0, hd.seq(s), d, c0 + lane, live, p);
@@ -186,17 +199,20 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
         }
       }
     };
+    // Packed streams: one head-checked copy of the loop (steps past the end
+    // of the stream stay guarded: this scan composes from the last step
+    // down, so they would come first).
     auto run = [&](auto chk) {
-      if (n_steps == L) {
+      if (!PK && n_steps == L) {
 #pragma unroll
         for (int s = L - 1; s >= 0; --s) step(s, chk);
       } else {
 #pragma unroll
         for (int s = L - 1; s >= 0; --s)
-          if (s < n_steps) step(s, chk);
+          if (s < ns) step(s, chk);
       }
     };
-    if (PK && hd.mask)
+    if constexpr (PK)
       run(std::true_type{});
     else
       run(std::false_type{});
@@ -304,16 +320,16 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
       }
     };
     auto run = [&](auto chk) {
-      if (n_steps == L) {
+      if (!PK && n_steps == L) {
 #pragma unroll
         for (int s = L - 1; s >= 0; --s) replay(s, chk);
       } else {
 #pragma unroll
         for (int s = L - 1; s >= 0; --s)
-          if (s < n_steps) replay(s, chk);
+          if (s < ns) replay(s, chk);
       }
     };
-    if (PK && hd.mask)
+    if constexpr (PK)
       run(std::true_type{});
     else
       run(std::false_type{});
