@@ -129,16 +129,18 @@ static InitWs carve_init(void* base, int B, int T, int d, int P, int dtype, size
   return w;
 }
 
-// K >= 2 Newton iterations in one launch (the fp32 iterate stays in
-// registers); a single iteration keeps its own launch, which holds the guess
-// packed and runs at higher occupancy.  PRNN_SLSTM_NEWTON_FUSED=0 selects one
-// launch per iteration throughout.
+// All K Newton iterations in one launch (the fp32 iterate stays in
+// registers), K = 1 included: the per-iteration kernel, which holds the guess
+// packed, measured no faster for a single iteration (and 1.8x slower on packed
+// streams, where its head handling leaves one wave per SIMD).
+// PRNN_SLSTM_NEWTON_FUSED=0 selects one launch per iteration throughout; the
+// residual-gated early-exit path always runs one launch per iteration.
 static bool newton_fused(int K) {
   static const bool on = [] {
     const char* e = getenv("PRNN_SLSTM_NEWTON_FUSED");
     return !(e && atoi(e) == 0);
   }();
-  return on && K >= 2;
+  return on && K >= 1;
 }
 
 // Shapes of the fused launch: wx (2 registers per step in bf16, 4 in fp32)
@@ -172,8 +174,8 @@ static NewtonWs carve_newton(void* base, int B, int T, int d, int K, int dtype, 
                              bool packed = false) {
   Carver cv(base);
   NewtonWs w;
-  // packed streams always take the single-launch path for K >= 2
-  w.fused = packed ? K >= 2 : newton_fused(K);
+  // packed streams always take the single-launch path
+  w.fused = packed ? K >= 1 : newton_fused(K);
   w.work[0] = w.work[1] = nullptr;
   w.hlast = nullptr;
   if (w.fused) {

@@ -1310,7 +1310,7 @@ slstm_newton_fused_kernel(
 // ---------------------------------------------------------------------------
 constexpr Shape kFrozenDefault{64, 4};
 constexpr Shape kFrozenF32{32, 4};
-constexpr Shape kNewtonGuessDefault{32, 4};
+constexpr Shape kNewtonGuessDefault{24, 4};
 constexpr Shape kNewtonWorkDefault{24, 4};
 constexpr Shape kNewtonF32{16, 8};
 constexpr Shape kPicardDefault{24, 4};
