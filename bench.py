@@ -499,6 +499,7 @@ def main() -> int:
     ach_newton = newton_bytes / (ms_newton * 1e-3) / 1e9
     newton_share = ms_n2 / ms
     init_share = ms_initP / ms
+    newton_traffic = _traffic_from_profile("slstm_newton_cfg3.md")
     out = {
         "metric": "Newton+scan fwd tokens/sec + % HBM roofline, ParaSLSTM diag d=1024 T=131072",
         "value": tokens / (ms * 1e-3),
@@ -525,7 +526,14 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": ach_newton / HBM_PEAK_GBS,
-            "traffic": _traffic_from_profile("slstm_newton_cfg3.md"),
+            "traffic": newton_traffic,
+            # HBM counters cannot be read from inside this process: the bytes
+            # come from rocprofv3 --pmc runs of this same bench (calibrated
+            # against a plain copy), committed with their commands
+            "traffic_source": "profiles/slstm_newton_cfg3.md (rocprofv3 FETCH_SIZE / WRITE_SIZE "
+                              "per dispatch, copy-calibrated)",
+            "traffic_GBps": (None if newton_traffic is None
+                             else newton_traffic / (ms_newton * 1e-3) / 1e9),
             "algorithmic_bytes_per_launch": newton_bytes,
             "avg_launch_ms": ms_newton,
             "avg_op_ms": ms_n2,
