@@ -642,38 +642,71 @@ __global__ __launch_bounds__(256) void gru_group_kernel(const float* __restrict_
   auto chunk_of = [&](int w) { return REV ? n_chunks - 1 - w : w; };
   // thread t stages elements 4 t .. 4 t + 3 of rows r = (t / 16) + 16 q
   const int r0 = threadIdx.x / 16, c4 = 4 * (threadIdx.x % 16);
-  float4 nxt[4];
-  auto fetch = [&](int w) {
+  // Chunk matrices are fetched kAhead products ahead into a ring of register
+  // slots (the loop is unrolled over the group, so every slot index is a
+  // constant): the fetch latency is many products long under load, and one
+  // matrix in flight per block left the kernel latency-bound.
+  constexpr int kAhead = 3;
+  float4 nxt[kAhead][4];
+  auto fetch = [&](int slot, int w) {
     const float* src = P + static_cast<size_t>(chunk_of(min(w, w_end - 1))) * DH * DH;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) nxt[q] = *reinterpret_cast<const float4*>(src + (r0 + 16 * q) * DH + c4);
-  };
-  auto stage = [&](float (*dst)[kSPad]) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) *reinterpret_cast<float4*>(&dst[r0 + 16 * q][c4]) = nxt[q];
+    for (int q = 0; q < 4; ++q)
+      nxt[slot][q] = *reinterpret_cast<const float4*>(src + (r0 + 16 * q) * DH + c4);
   };
   // M = S_first, ell = e_first
-  fetch(w_begin);
+  {
+    const float* src = P + static_cast<size_t>(chunk_of(w_begin)) * DH * DH;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) *reinterpret_cast<float4*>(&sM[r0 + 16 * q][c4]) = nxt[q];
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<float4*>(&sM[r0 + 16 * q][c4]) =
+          *reinterpret_cast<const float4*>(src + (r0 + 16 * q) * DH + c4);
+  }
   if (threadIdx.x < DH) sL[0][threadIdx.x] = E[static_cast<size_t>(chunk_of(w_begin)) * DH + threadIdx.x];
   int cur = 0;
   floatx4 acc[4];
-  // The next chunk's matrix is fetched one product ahead (its loads are in
-  // flight during the current product).
-  if (w_begin + 1 < w_end) fetch(w_begin + 1);
-  for (int w = w_begin + 1; w < w_end; ++w) {
+  // This lane's row of e for every chunk of the group, loaded up front: a load
+  // inside the loop would make its wait (memory counters retire in order)
+  // also wait for the chunk matrices fetched ahead of it.
+  const int erow = 16 * wave + (lane >> 2);
+  float ev[kGroup];
+#pragma unroll
+  for (int i = 1; i < kGroup; ++i)
+    ev[i] = E[static_cast<size_t>(chunk_of(min(w_begin + i, w_end - 1))) * DH + erow];
+#pragma unroll
+  for (int k = 0; k < kAhead; ++k) fetch(k, w_begin + 1 + k);  // clamped past the end
+  // Branch-free over the whole group: past the group's end (a short last
+  // group) the product runs with S = I and e = 0, which leaves M and ell as
+  // they are.
+#pragma unroll
+  for (int i = 1; i < kGroup; ++i) {
+    const int w = w_begin + i;
+    const bool past = w >= w_end;
+    const int slot = (i - 1) % kAhead;
     __syncthreads();  // the previous product's reads of sS / sM are done
-    stage(sS);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = r0 + 16 * q;
+      float4 v = nxt[slot][q];
+      if (past) {
+        v.x = row == c4 ? 1.f : 0.f;
+        v.y = row == c4 + 1 ? 1.f : 0.f;
+        v.z = row == c4 + 2 ? 1.f : 0.f;
+        v.w = row == c4 + 3 ? 1.f : 0.f;
+      }
+      *reinterpret_cast<float4*>(&sS[row][c4]) = v;
+    }
     __syncthreads();
-    fetch(w + 1);  // clamped to the group's last chunk past the end
+    fetch(slot, w + kAhead);  // clamped to the group's last chunk past the end
+    // keep the fetch here: it is consumed kAhead products later
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) acc[rt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < DH / 4; ++ks) {
-      const float b = sM[4 * ks + g][16 * wave + li];
+      const float bb = sM[4 * ks + g][16 * wave + li];
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt) acc[rt] = mfma_f32(sS[16 * rt + li][4 * ks + g], b, acc[rt]);
+      for (int rt = 0; rt < 4; ++rt) acc[rt] = mfma_f32(sS[16 * rt + li][4 * ks + g], bb, acc[rt]);
     }
     {
       // ell <- S ell + e: row 16 wave + lane / 4, quarter lane % 4 of its terms
@@ -687,7 +720,7 @@ __global__ __launch_bounds__(256) void gru_group_kernel(const float* __restrict_
       }
       v += dpp_f<0xB1>(v);  // quad_perm [1,0,3,2]
       v += dpp_f<0x4E>(v);  // quad_perm [2,3,0,1]
-      if ((lane & 3) == 0) sL[cur ^ 1][row] = v + E[static_cast<size_t>(chunk_of(w)) * DH + row];
+      if ((lane & 3) == 0) sL[cur ^ 1][row] = v + (past ? 0.f : ev[i]);
     }
     cur ^= 1;
     __syncthreads();  // every read of sM is done
