@@ -31,6 +31,7 @@
 #include "prnn_host.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace prnn {
 namespace gru {
@@ -158,6 +159,25 @@ __device__ __forceinline__ floatx4 ld4(const T* p) {
     return *reinterpret_cast<const floatx4*>(p);
   } else {
     const uint2 w = *reinterpret_cast<const uint2*>(p);
+    return floatx4{Narrow<T>::lo(w.x), Narrow<T>::hi(w.x), Narrow<T>::lo(w.y),
+                   Narrow<T>::hi(w.y)};
+  }
+}
+
+// Four values as loaded (fp32, or 16-bit storage packed two to a register),
+// for loads issued ahead of their use: unpacking right after the load would
+// wait for it there.
+template <typename T>
+using Raw4 = typename std::conditional<sizeof(T) == 4, floatx4, uint2>::type;
+template <typename T>
+__device__ __forceinline__ Raw4<T> ldr4(const T* p) {
+  return *reinterpret_cast<const Raw4<T>*>(p);
+}
+template <typename T>
+__device__ __forceinline__ floatx4 unpack4(const Raw4<T>& w) {
+  if constexpr (sizeof(T) == 4) {
+    return w;
+  } else {
     return floatx4{Narrow<T>::lo(w.x), Narrow<T>::hi(w.x), Narrow<T>::lo(w.y),
                    Narrow<T>::hi(w.y)};
   }
@@ -1383,7 +1403,8 @@ __global__ __launch_bounds__(256) void gru_rev_mfma_kernel(
   }
   const int steps = min(kChunk, T - c_first * kChunk);  // the wave's longest chunk
   struct In {
-    floatx4 hp[4], gr_[4], z[4], r[4], nn[4];
+    Raw4<TX> hp[4], gr_[4];  // as loaded (unpacked where the step uses them)
+    floatx4 z[4], r[4], nn[4];
     int q;  // PK: the sequence this lane's step starts, -1 elsewhere
   };
   auto load_in = [&](int s, In& v) {
@@ -1394,14 +1415,15 @@ __global__ __launch_bounds__(256) void gru_rev_mfma_kernel(
 #pragma unroll
     for (int to = 0; to < 4; ++to) {
       const floatx4 zero{0.f, 0.f, 0.f, 0.f};
-      v.hp[to] = v.gr_[to] = v.z[to] = v.r[to] = v.nn[to] = zero;
+      v.hp[to] = v.gr_[to] = Raw4<TX>{};
+      v.z[to] = v.r[to] = v.nn[to] = zero;
       if (act) {
         const int j = 16 * to + 4 * g;
         if (hr < 0)
-          v.hp[to] = ld4(states + h_at(b, t - 1, T, d, head, j));
+          v.hp[to] = ldr4(states + h_at(b, t - 1, T, d, head, j));
         else if (h0 != nullptr)
-          v.hp[to] = ld4(h0 + static_cast<size_t>(hr) * d + head * DH + j);
-        v.gr_[to] = ld4(grad + h_at(b, t, T, d, head, j));
+          v.hp[to] = ldr4(h0 + static_cast<size_t>(hr) * d + head * DH + j);
+        v.gr_[to] = ldr4(grad + h_at(b, t, T, d, head, j));
         v.z[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3) * DH + 16 * to);
         v.r[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3 + 1) * DH + 16 * to);
         v.nn[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3 + 2) * DH + 16 * to);
@@ -1415,6 +1437,12 @@ __global__ __launch_bounds__(256) void gru_rev_mfma_kernel(
     const int t = t0 + s;
     const In cur = nx;
     if (s > 0) load_in(s - 1, nx);
+    floatx4 hpv[4], grv[4];
+#pragma unroll
+    for (int to = 0; to < 4; ++to) {
+      hpv[to] = unpack4<TX>(cur.hp[to]);
+      grv[to] = unpack4<TX>(cur.gr_[to]);
+    }
     // mu = g + nu;  d_zpre = mu (n - h) z(1-z);  d_npre = mu z (1-n^2)
     floatx4 mu[4], dz[4], dn[4], dr[4], tz[4], du[4], tr[4];
 #pragma unroll
@@ -1422,8 +1450,8 @@ __global__ __launch_bounds__(256) void gru_rev_mfma_kernel(
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const float z = cur.z[to][v], nv = cur.nn[to][v];
-        mu[to][v] = cur.gr_[to][v] + nu[to][v];
-        dz[to][v] = mu[to][v] * (nv - cur.hp[to][v]) * (z * (1.f - z));
+        mu[to][v] = grv[to][v] + nu[to][v];
+        dz[to][v] = mu[to][v] * (nv - hpv[to][v]) * (z * (1.f - z));
         dn[to][v] = mu[to][v] * z * (1.f - nv * nv);
       }
 #pragma unroll
@@ -1452,7 +1480,7 @@ __global__ __launch_bounds__(256) void gru_rev_mfma_kernel(
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const float r = cur.r[to][v];
-        dr[to][v] = du[to][v] * cur.hp[to][v] * r * (1.f - r);
+        dr[to][v] = du[to][v] * hpv[to][v] * r * (1.f - r);
       }
 #pragma unroll
     for (int tc = 0; tc < 4; ++tc) {
