@@ -1568,38 +1568,41 @@ __global__ __launch_bounds__(256) void gru_ga_kernel(
   static_assert(kGaRows * DH == 4 * 256, "one float4 per thread and array");
   const int sr = threadIdx.x / 16, sj = 4 * (threadIdx.x % 16);
   struct Stage {
-    floatx4 hv, rv, y0, y1, y2;  // h_{t-1}, r_t (h r is formed when staged), dL/dwx
+    Raw4<TX> hv, y0, y1, y2;  // h_{t-1} and dL/dwx as loaded (unpacked when staged)
+    floatx4 rv;               // r_t (h r is formed when staged)
   };
   auto load_rows = [&](long long k0, Stage& st) {
     const floatx4 zero{0.f, 0.f, 0.f, 0.f};
-    st.hv = st.rv = st.y0 = st.y1 = st.y2 = zero;
+    st.hv = st.y0 = st.y1 = st.y2 = Raw4<TX>{};
+    st.rv = zero;
     const long long k = k0 + sr;
     if (k < r1) {
       const int b = static_cast<int>(k / T), t = static_cast<int>(k % T);
       const int hr = start_row<PK>(pk, b, t);
       if (hr < 0)
-        st.hv = ld4(states + h_at(b, t - 1, T, d, head, sj));
+        st.hv = ldr4(states + h_at(b, t - 1, T, d, head, sj));
       else if (h0 != nullptr)
-        st.hv = ld4(h0 + static_cast<size_t>(hr) * d + head * DH + sj);
+        st.hv = ldr4(h0 + static_cast<size_t>(hr) * d + head * DH + sj);
       const size_t task = static_cast<size_t>(b * H + head) * n_chunks + t / kChunk;
       // r stays as loaded: multiplying here would wait for these loads at
       // once instead of while the current block's products run
       st.rv =
           *reinterpret_cast<const floatx4*>(gates + ((task * kChunk + t % kChunk) * 3 + 1) * DH + sj);
-      st.y0 = ld4(g_wx + wx_at(b, t, T, d, 0, head, sj));
-      st.y1 = ld4(g_wx + wx_at(b, t, T, d, 1, head, sj));
-      st.y2 = ld4(g_wx + wx_at(b, t, T, d, 2, head, sj));
+      st.y0 = ldr4(g_wx + wx_at(b, t, T, d, 0, head, sj));
+      st.y1 = ldr4(g_wx + wx_at(b, t, T, d, 1, head, sj));
+      st.y2 = ldr4(g_wx + wx_at(b, t, T, d, 2, head, sj));
     }
   };
   Stage nx;
   load_rows(r0, nx);
   for (long long k0 = r0; k0 < r1; k0 += kGaRows) {
     __syncthreads();  // the previous block's products are done with sx / sy
-    *reinterpret_cast<floatx4*>(&sx[0][sr][sj]) = nx.hv;
-    *reinterpret_cast<floatx4*>(&sx[1][sr][sj]) = nx.hv * nx.rv;
-    *reinterpret_cast<floatx4*>(&sy[0][sr][sj]) = nx.y0;
-    *reinterpret_cast<floatx4*>(&sy[1][sr][sj]) = nx.y1;
-    *reinterpret_cast<floatx4*>(&sy[2][sr][sj]) = nx.y2;
+    const floatx4 hv = unpack4<TX>(nx.hv);
+    *reinterpret_cast<floatx4*>(&sx[0][sr][sj]) = hv;
+    *reinterpret_cast<floatx4*>(&sx[1][sr][sj]) = hv * nx.rv;
+    *reinterpret_cast<floatx4*>(&sy[0][sr][sj]) = unpack4<TX>(nx.y0);
+    *reinterpret_cast<floatx4*>(&sy[1][sr][sj]) = unpack4<TX>(nx.y1);
+    *reinterpret_cast<floatx4*>(&sy[2][sr][sj]) = unpack4<TX>(nx.y2);
     __syncthreads();
     if (k0 + kGaRows < r1) load_rows(k0 + kGaRows, nx);
 #pragma unroll
