@@ -1021,55 +1021,67 @@ __global__ __launch_bounds__(256) void gru_replay_mfma_kernel(
   }
   const int steps = min(kChunk, T - c_first * kChunk);  // the wave's longest chunk
   struct In {
-    floatx4 hp[4], ht[4], gz[4], gr[4], gn[4];
-    bool head;  // PK: this lane's chunk starts a sequence at this step
+    floatx4 ht[4], gz[4], gr[4], gn[4];
+    int hr;  // PK: the h0 row of the sequence this lane's chunk starts at this step, else -1
   };
-  // Step s's inputs (zeros past the chunk's end); loaded one step ahead.  h at
-  // t - 1 is the previous step's h at t except at the chunk's first step.
-  auto load_in = [&](int s, In& v, const floatx4* h_prev) {
+  // Step s's inputs (zeros past the chunk's end); loaded one step ahead.
+  auto load_in = [&](int s, In& v) {
     const bool act = s < len;
     const int t = t0 + s;
-    int hr = -1;
-    if constexpr (PK) hr = act ? start_row<PK>(pk, b, t) : -1;
-    v.head = hr >= 0;
+    v.hr = -1;
+    if constexpr (PK) v.hr = act ? start_row<PK>(pk, b, t) : -1;
 #pragma unroll
     for (int to = 0; to < 4; ++to) {
       const floatx4 zero{0.f, 0.f, 0.f, 0.f};
-      v.hp[to] = v.ht[to] = v.gz[to] = v.gr[to] = v.gn[to] = zero;
+      v.ht[to] = v.gz[to] = v.gr[to] = v.gn[to] = zero;
       if (act) {
-        const int j = 16 * to + 4 * g;
-        if (!PK) {
-          if (h_prev != nullptr)
-            v.hp[to] = h_prev[to];
-          else if (t > 0)
-            v.hp[to] = *reinterpret_cast<const floatx4*>(hin + h_at(b, t - 1, T, d, head, j));
-          else if (h0 != nullptr)
-            v.hp[to] = ld4(h0 + static_cast<size_t>(b) * d + head * DH + j);
-        } else if (hr >= 0) {
-          if (h0 != nullptr) v.hp[to] = ld4(h0 + static_cast<size_t>(hr) * d + head * DH + j);
-        } else if (h_prev != nullptr) {
-          v.hp[to] = h_prev[to];
-        } else {
-          v.hp[to] = *reinterpret_cast<const floatx4*>(hin + h_at(b, t - 1, T, d, head, j));
-        }
-        v.ht[to] = *reinterpret_cast<const floatx4*>(hin + h_at(b, t, T, d, head, j));
+        v.ht[to] = *reinterpret_cast<const floatx4*>(hin + h_at(b, t, T, d, head, 16 * to + 4 * g));
         v.gz[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3) * DH + 16 * to);
         v.gr[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3 + 1) * DH + 16 * to);
         v.gn[to] = *reinterpret_cast<const floatx4*>(gt + (s * 3 + 2) * DH + 16 * to);
       }
     }
   };
+  // h at t - 1 of the current step: the previous step's h at t, except at the
+  // chunk's first step (below) and at a head (its sequence's h0 row, loaded
+  // where it is used).  One copy of it rather than one per prefetched step
+  // keeps the kernel at two waves per SIMD.
+  floatx4 hprev[4];
+#pragma unroll
+  for (int to = 0; to < 4; ++to) {
+    const int j = 16 * to + 4 * g;
+    hprev[to] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (len > 0) {
+      if (t0 > 0)
+        hprev[to] = *reinterpret_cast<const floatx4*>(hin + h_at(b, t0 - 1, T, d, head, j));
+      else if (!PK && h0 != nullptr)
+        hprev[to] = ld4(h0 + static_cast<size_t>(b) * d + head * DH + j);
+    }
+  }
   In nx;
-  load_in(0, nx, nullptr);
+  load_in(0, nx);
   for (int s = 0; s < steps; ++s) {
     const bool act = s < len;
     const int t = t0 + s;
     const In cur = nx;
-    if (s + 1 < steps) load_in(s + 1, nx, cur.ht);
-    const floatx4 *hp = cur.hp, *ht = cur.ht, *gz = cur.gz, *gr = cur.gr, *gn = cur.gn;
+    if (s + 1 < steps) load_in(s + 1, nx);
+    floatx4 hpv[4];
+#pragma unroll
+    for (int to = 0; to < 4; ++to) hpv[to] = hprev[to];
+    if constexpr (PK) {
+      if (cur.hr >= 0) {
+#pragma unroll
+        for (int to = 0; to < 4; ++to) {
+          hpv[to] = floatx4{0.f, 0.f, 0.f, 0.f};
+          if (h0 != nullptr)
+            hpv[to] = ld4(h0 + static_cast<size_t>(cur.hr) * d + head * DH + 16 * to + 4 * g);
+        }
+      }
+    }
+    const floatx4 *hp = hpv, *ht = cur.ht, *gz = cur.gz, *gr = cur.gr, *gn = cur.gn;
     if constexpr (PK) {
       // no carry crosses a head: this lane's column of delta restarts at zero
-      if (cur.head) {
+      if (cur.hr >= 0) {
 #pragma unroll
         for (int to = 0; to < 4; ++to) dl[to] = floatx4{0.f, 0.f, 0.f, 0.f};
       }
@@ -1133,6 +1145,8 @@ __global__ __launch_bounds__(256) void gru_replay_mfma_kernel(
         if (!LOCAL) st4(hout + h_at(b, t, T, d, head, 16 * to + 4 * g), o);
       }
     }
+#pragma unroll
+    for (int to = 0; to < 4; ++to) hprev[to] = cur.ht[to];
   }
   if (LOCAL && valid) {
 #pragma unroll
