@@ -136,13 +136,21 @@ def test_slstm_ops_deterministic_repeat(deterministic):
     wx = (0.5 * torch.randn(B, T, 4 * d, generator=g)).to(DEV, torch.bfloat16)
     r = (0.3 * torch.rand(4, d, generator=g) - 0.15).to(DEV, torch.bfloat16)
     grad = torch.randn(B, T, 4, d, generator=g).to(DEV, torch.bfloat16)
+    # a packed stream of the same tokens (several sequences) and K = 1, which
+    # also takes the single fused launch
+    cs = torch.tensor([0, 5000, 5001, 17000, 32768], device=DEV)
     outs = []
     for _ in range(4):
         guess = ops.slstm_init_fused(wx, r, None, picard_iters=5, eps=1e-6)
         H = ops.newton_slstm_fused(wx, r, None, guess, max_iters=2, omega=1.0, eps=1e-6)
+        H1 = ops.newton_slstm_fused(wx, r, None, guess, max_iters=1, omega=1.0, eps=1e-6)
         g_wx, g_r, g_h0, g_b = ops.slstm_backward_fused(wx, r, None, H, grad, eps=1e-6)
+        pg = ops.slstm_init_fused(wx, r, None, cs, picard_iters=5, eps=1e-6)
+        pH = ops.newton_slstm_fused(wx, r, None, pg, None, cs, max_iters=2, omega=1.0, eps=1e-6)
+        pH1 = ops.newton_slstm_fused(wx, r, None, pg, None, cs, max_iters=1, omega=1.0, eps=1e-6)
         torch.cuda.synchronize()
-        outs.append({"guess": guess, "H": H, "g_wx": g_wx, "g_r": g_r, "g_b": g_b})
+        outs.append({"guess": guess, "H": H, "H1": H1, "g_wx": g_wx, "g_r": g_r, "g_b": g_b,
+                     "packed_guess": pg, "packed_H": pH, "packed_H1": pH1})
     for o in outs[1:]:
         eq = _bitequal(outs[0], o)
         assert all(eq.values()), eq
