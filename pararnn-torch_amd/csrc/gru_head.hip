@@ -863,21 +863,22 @@ __global__ __launch_bounds__(64 * PARTS) void gru_carry_kernel(
 // otherwise from the chunk's carry, writing H + omega delta.
 // ---------------------------------------------------------------------------
 constexpr int kPair = 2;
+constexpr int kSimds = 1024;  // 256 CUs x 4 SIMDs
 
-template <typename TX, typename TOUT, bool LOCAL, bool PK>
+template <typename TX, typename TOUT, bool LOCAL, bool PK, int NP>
 __global__ __launch_bounds__(256) void gru_replay_kernel(
     const TX* __restrict__ a_z, const TX* __restrict__ a_r, const TX* __restrict__ a_n,
     const TX* __restrict__ h0, const float* __restrict__ hin, const float* __restrict__ gates,
     const float* __restrict__ carry_in, TOUT* __restrict__ hout, float* __restrict__ e_out,
     int B, int T, int H, int n_chunks, float omega, GPk pk) {
-  __shared__ float s_v[4][kPair][2][DH];
+  __shared__ float s_v[4][NP][2][DH];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n_pairs = (n_chunks + kPair - 1) / kPair;
+  const int n_pairs = (n_chunks + NP - 1) / NP;
   const int task = blockIdx.x * 4 + wave;
   const int n_seq = B * H;
   if (task >= n_seq * n_pairs) return;  // whole wave exits together
   const int d = H * DH;
-  const int seq = task / n_pairs, c0 = (task % n_pairs) * kPair;
+  const int seq = task / n_pairs, c0 = (task % n_pairs) * NP;
   const int b = seq / H, head = seq % H;
   float az[DH], ar[DH], an[DH];
   load_col(a_z, head, lane, az);
@@ -888,11 +889,11 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
     float hp, z, r, n, ht;
     bool head;  // PK: a sequence's first step (no carry reaches it)
   };
-  int t0[kPair], len[kPair];
-  float dl[kPair];
-  const float* gt[kPair];
+  int t0[NP], len[NP];
+  float dl[NP];
+  const float* gt[NP];
 #pragma unroll
-  for (int k = 0; k < kPair; ++k) {
+  for (int k = 0; k < NP; ++k) {
     const int c = c0 + k;
     const bool valid = c < n_chunks;
     t0[k] = c * kChunk;
@@ -920,34 +921,34 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
   };
   // Chunk 0 of the pair is the longest (only a sequence's last chunk is short).
   for (int s = 0; s < len[0]; ++s) {
-    In cur[kPair];
+    In cur[NP];
 #pragma unroll
-    for (int k = 0; k < kPair; ++k) cur[k] = load_in(k, s);
+    for (int k = 0; k < NP; ++k) cur[k] = load_in(k, s);
     // J delta = (1-z) delta + d2 (delta @ A_z) + d3 ((r delta + d5 (delta @ A_r)) @ A_n)
     if constexpr (PK) {
 #pragma unroll
-      for (int k = 0; k < kPair; ++k)
+      for (int k = 0; k < NP; ++k)
         if (cur[k].head) dl[k] = 0.f;  // no carry crosses a head
     }
 #pragma unroll
-    for (int k = 0; k < kPair; ++k) s_v[wave][k][0][lane] = dl[k];
+    for (int k = 0; k < NP; ++k) s_v[wave][k][0][lane] = dl[k];
     __builtin_amdgcn_wave_barrier();
-    float yz[kPair], yr[kPair], yn[kPair];
+    float yz[NP], yr[NP], yn[NP];
 #pragma unroll
-    for (int k = 0; k < kPair; ++k) {
+    for (int k = 0; k < NP; ++k) {
       yz[k] = vec_col(s_v[wave][k][0], az);
       yr[k] = vec_col(s_v[wave][k][0], ar);
     }
 #pragma unroll
-    for (int k = 0; k < kPair; ++k) {
+    for (int k = 0; k < NP; ++k) {
       const float d5 = cur[k].hp * cur[k].r * (1.f - cur[k].r);
       s_v[wave][k][1][lane] = cur[k].r * dl[k] + d5 * yr[k];
     }
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int k = 0; k < kPair; ++k) yn[k] = vec_col(s_v[wave][k][1], an);
+    for (int k = 0; k < NP; ++k) yn[k] = vec_col(s_v[wave][k][1], an);
 #pragma unroll
-    for (int k = 0; k < kPair; ++k) {
+    for (int k = 0; k < NP; ++k) {
       const In& v = cur[k];
       const float d2 = (v.n - v.hp) * v.z * (1.f - v.z);
       const float d3 = v.z * (1.f - v.n * v.n);
@@ -960,7 +961,7 @@ __global__ __launch_bounds__(256) void gru_replay_kernel(
   }
   if (LOCAL) {
 #pragma unroll
-    for (int k = 0; k < kPair; ++k)
+    for (int k = 0; k < NP; ++k)
       if (len[k] > 0) e_out[(static_cast<size_t>(seq) * n_chunks + c0 + k) * DH + lane] = dl[k];
   }
 }
@@ -1765,9 +1766,18 @@ static void launch_replay(const TX* az, const TX* ar, const TX* an, const TX* h0
     gru_replay_mfma_kernel<TX, TOUT, LOCAL, PK><<<dim3(n_seq * n_grp), dim3(256), 0, stream>>>(
         az, ar, an, h0, hin, gates, carry, out, e, B, T, H, n_chunks, omega, pk);
   } else {
-    const int blocks = (n_seq * ((n_chunks + kPair - 1) / kPair) + 3) / 4;
-    gru_replay_kernel<TX, TOUT, LOCAL, PK><<<dim3(blocks), dim3(256), 0, stream>>>(
-        az, ar, an, h0, hin, gates, carry, out, e, B, T, H, n_chunks, omega, pk);
+    // kPair chunks per wave give each wave two independent serial walks, but
+    // when that leaves SIMDs without a wave (short or few sequences: the
+    // reference's B=1, T=4096 shape) one chunk per wave fills them instead
+    if (n_seq * ((n_chunks + kPair - 1) / kPair) < kSimds) {
+      const int blocks = (n_seq * n_chunks + 3) / 4;
+      gru_replay_kernel<TX, TOUT, LOCAL, PK, 1><<<dim3(blocks), dim3(256), 0, stream>>>(
+          az, ar, an, h0, hin, gates, carry, out, e, B, T, H, n_chunks, omega, pk);
+    } else {
+      const int blocks = (n_seq * ((n_chunks + kPair - 1) / kPair) + 3) / 4;
+      gru_replay_kernel<TX, TOUT, LOCAL, PK, kPair><<<dim3(blocks), dim3(256), 0, stream>>>(
+          az, ar, an, h0, hin, gates, carry, out, e, B, T, H, n_chunks, omega, pk);
+    }
   }
 }
 
