@@ -1274,16 +1274,15 @@ __global__ __launch_bounds__(256) void gru_rev_kernel(
     g_h0[static_cast<size_t>(b) * d + head * DH + lane] = nu;
 }
 
-// Local reverse walk: nu from a zero carry over each chunk, two consecutive
+// Local reverse walk: nu from a zero carry over each chunk, NP consecutive
 // chunks of a sequence per wave side by side (lane i keeps row i of A_z, A_r,
 // A_n); the chunk's final nu is its local solution e.
-template <typename TX, bool PK>
+template <typename TX, bool PK, int NP>
 __global__ __launch_bounds__(256) void gru_rev_local_kernel(
     const TX* __restrict__ a_z, const TX* __restrict__ a_r, const TX* __restrict__ a_n,
     const TX* __restrict__ h0, const TX* __restrict__ states, const TX* __restrict__ grad,
     const float* __restrict__ gates, float* __restrict__ e_out, int B, int T, int H,
     int n_chunks, GPk pk) {
-  constexpr int NP = kPair;
   __shared__ float s_v[4][NP][3][DH];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n_pairs = (n_chunks + NP - 1) / NP;
@@ -1908,8 +1907,11 @@ static int run_bwd(const TX* wx, const TX* az, const TX* ar, const TX* an, const
     gru_rev_mfma_kernel<TX, true, PK><<<dim3(mfma_blocks), dim3(256), 0, stream>>>(
         az, ar, an, h0, states, grad, w.gates, nullptr, nullptr, nullptr, w.e, B, T, H,
         n_chunks, pk);
+  else if (n_seq * ((n_chunks + kPair - 1) / kPair) < kSimds)  // as in launch_replay
+    gru_rev_local_kernel<TX, PK, 1><<<dim3(rev_blocks), dim3(256), 0, stream>>>(
+        az, ar, an, h0, states, grad, w.gates, w.e, B, T, H, n_chunks, pk);
   else
-    gru_rev_local_kernel<TX, PK><<<dim3(rev_blocks_local), dim3(256), 0, stream>>>(
+    gru_rev_local_kernel<TX, PK, kPair><<<dim3(rev_blocks_local), dim3(256), 0, stream>>>(
         az, ar, an, h0, states, grad, w.gates, w.e, B, T, H, n_chunks, pk);
   PRNN_HIP(hipGetLastError());
   carry_scan<true>(w.phi, w.e, w.carry, n_seq, n_chunks, w.cs, stream);
