@@ -1642,18 +1642,27 @@ __global__ __launch_bounds__(256) void gru_ga_kernel(
   }
 }
 
-// g_a[gate][head] = sum over splits in index order.
+// g_a[gate][head] = sum over the splits.  Each block takes 64 elements; its
+// four waves sum every fourth split (wave q: splits q, q + 4, ...) and the four
+// partial sums are added in wave order, so the order is fixed (deterministic)
+// and four times as many loads are in flight as with one thread per element.
 __global__ __launch_bounds__(256) void gru_ga_reduce_kernel(const float* __restrict__ part,
                                                            int H, int n_split,
                                                            float* __restrict__ g_a) {
-  const int e = blockIdx.x * 256 + threadIdx.x;  // over 3 H 64 64
-  if (e >= 3 * H * DH * DH) return;
-  const int mat = e / (DH * DH), ij = e % (DH * DH);
-  const int gate = mat / H, head = mat % H;
-  const float* p = part + (static_cast<size_t>(head * 3 + gate) * n_split) * DH * DH + ij;
+  __shared__ float s_part[4][64];
+  const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int e = blockIdx.x * 64 + lane;  // over 3 H 64 64
   float acc = 0.f;
-  for (int sp = 0; sp < n_split; ++sp) acc += p[static_cast<size_t>(sp) * DH * DH];
-  g_a[e] = acc;
+  if (e < 3 * H * DH * DH) {
+    const int mat = e / (DH * DH), ij = e % (DH * DH);
+    const int gate = mat / H, head = mat % H;
+    const float* p = part + (static_cast<size_t>(head * 3 + gate) * n_split) * DH * DH + ij;
+    for (int sp = q; sp < n_split; sp += 4) acc += p[static_cast<size_t>(sp) * DH * DH];
+  }
+  s_part[q][lane] = acc;
+  __syncthreads();
+  if (q == 0 && e < 3 * H * DH * DH)
+    g_a[e] = ((s_part[0][lane] + s_part[1][lane]) + s_part[2][lane]) + s_part[3][lane];
 }
 
 
@@ -1928,7 +1937,7 @@ static int run_bwd(const TX* wx, const TX* az, const TX* ar, const TX* an, const
   gru_ga_kernel<TX, PK><<<dim3(w.n_split * H), dim3(256), 0, stream>>>(
       h0, states, w.gates, g_wx, B, T, H, n_chunks, w.n_split, w.rows_per, w.part, pk);
   PRNN_HIP(hipGetLastError());
-  gru_ga_reduce_kernel<<<dim3((3 * H * DH * DH + 255) / 256), dim3(256), 0, stream>>>(
+  gru_ga_reduce_kernel<<<dim3((3 * H * DH * DH + 63) / 64), dim3(256), 0, stream>>>(
       w.part, H, w.n_split, g_a);
   PRNN_HIP(hipGetLastError());
   return PRNN_OK;
