@@ -3,8 +3,9 @@
 Workload (the one the metric names): ParaSLSTM mix='diag',
 d=1024, B=1, T=131072, bf16, K=2 Newton iterations, P=5 Picard passes,
 x ~ N(0, 0.5) seeded, default seeded init.  A step is one solve on one batch
-with ``wx = W_x(x)`` already resident in HBM: the zero-hidden pass, P Picard
-passes and K Newton iterations (8 kernel launches plus two status clears).
+with ``wx = W_x(x)`` already resident in HBM: the zero-hidden pass and the P
+Picard passes (one launch), then the K Newton iterations (one launch), each
+after a small clear of its status words.
 The W_x GEMM and the end-to-end ``newton_apply`` (GEMM + solve) are timed
 separately and reported as extra fields, as are BASELINE config 2 (the same
 step at B=8, T=16384, ``slstm_cfg2``), config 5 (one training step: forward
