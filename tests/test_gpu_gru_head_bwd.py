@@ -247,3 +247,33 @@ def test_recompute_chunk_len_and_packed_sequences():
     assert _rel(xp.grad[0, :150].cpu(), xs[0].grad[0].cpu()) <= 1e-5
     assert _rel(xp.grad[0, 150:].cpu(), xs[1].grad[0].cpu()) <= 1e-5
     assert _rel(hp.grad.cpu(), hs.grad.cpu()) <= 1e-5
+
+
+def test_per_lane_walks_at_full_length_match_matrix_core_walks(monkeypatch):
+    """At a size with more than a thousand chunk pairs the per-lane reverse
+    walks take two chunks per wave (the other branch of their launch); their
+    results against the matrix-core walks on the same inputs (fp32, the same
+    arithmetic summed in a different order)."""
+    from pararnn_amd import ops
+
+    print("case full-length per-lane walks (two chunks per wave) vs matrix-core walks", flush=True)
+    torch.manual_seed(5)
+    B, T, H, din = 1, 32768, 8, 16
+    d = 64 * H
+    g = torch.Generator().manual_seed(6)
+    p = GRUHeadParams(torch.randn(3 * d, din, generator=g) * 0.2,
+                      torch.randn(3 * d, generator=g) * 0.1,
+                      *(torch.randn(H, 64, 64, generator=g) * 0.1 for _ in range(3)))
+    x = torch.randn(B, T, din, generator=g)
+    wx = p.wx(x).to(DEV)
+    states = torch.tanh(torch.randn(B, T, d, generator=g)).to(DEV)
+    grad = torch.randn(B, T, d, generator=g).to(DEV)
+    a = [t.to(DEV) for t in p.mats()]
+    res = {}
+    for walks in ("0", "1"):
+        monkeypatch.setenv("PRNN_GRU_REV_MFMA", walks)
+        res[walks] = ops.gru_head_backward_fused(wx, *a, None, states, grad)
+    for i, k in enumerate(("g_wx", "g_a")):
+        e = _rel(res["0"][i].cpu(), res["1"][i].cpu())
+        print(f"  {k}: rel diff {e:.2e}", flush=True)
+        assert e <= 1e-5, k
