@@ -160,7 +160,10 @@ PRNN_API int prnn_gru_head_newton(const void* wx, const void* a_z, const void* a
  * when h0 is NULL -- and no carry crosses it.  The kernels read cu_seqlens
  * and block_table themselves: no padding, no gather, one launch set for the
  * whole stream.  Workspace from the *_packed_workspace_size calls; tag_base
- * as for the _ex calls.  The caller checks cu_seqlens (the kernels trust it). */
+ * as for the _ex calls.  The caller checks cu_seqlens (the kernels trust it):
+ * it must rise strictly, since an empty sequence would make the kernels
+ * assign every later step to the wrong sequence (wrong h0 and g_h0 rows).
+ * The library itself rejects n_seq outside [1, T] with PRNN_ERR_VALUE. */
 PRNN_API size_t prnn_slstm_init_packed_workspace_size(int T, int d, int picard_iters, int dtype);
 PRNN_API int prnn_slstm_init_packed(const void* wx, const void* r, const void* h0, void* states,
                                     int T, int d, int picard_iters, float eps, int dtype,
@@ -179,6 +182,28 @@ PRNN_API int prnn_slstm_newton_step_packed(const void* wx, const void* r, const 
                                            const int* cu_seqlens, int n_seq,
                                            const int* block_table, void* workspace,
                                            size_t workspace_bytes, int tag_base, void* stream);
+
+/* One Newton iteration with the reference's eager rounding (replaces the
+ * loop body of solvers/newton/__init__.py:516-543 for scan_backend='eager':
+ * step_and_jacobian in the tensor dtype, cells/para_slstm.py:241-281 and
+ * :378-446, the fp32 block-4 scan of solvers/scan.py:82-100 and 229-246, and
+ * the rounded update).  `in` is the current iterate and `out` receives the
+ * next one, both (B, T, 4, d) in `dtype`: every cell and Jacobian op rounds to
+ * `dtype` as the eager tensor op does, the residual is rounded, the scan runs
+ * in fp32, delta is rounded, then in + omega * delta is rounded.  `out` must
+ * not alias `in`.  Workspace: prnn_slstm_newton_workspace_size (packed:
+ * prnn_slstm_newton_packed_workspace_size) with max_iters = 1; tag_base as
+ * for the _ex calls; cu_seqlens / n_seq / block_table as for the packed
+ * calls above. */
+PRNN_API int prnn_slstm_newton_eager(const void* wx, const void* r, const void* h0,
+                                     const void* in, void* out, int B, int T, int d, float omega,
+                                     float eps, int dtype, void* workspace,
+                                     size_t workspace_bytes, int tag_base, void* stream);
+PRNN_API int prnn_slstm_newton_eager_packed(const void* wx, const void* r, const void* h0,
+                                            const void* in, void* out, int T, int d, float omega,
+                                            float eps, int dtype, const int* cu_seqlens,
+                                            int n_seq, const int* block_table, void* workspace,
+                                            size_t workspace_bytes, int tag_base, void* stream);
 
 /* Eq. 2.6 backward at the solved trajectory `states` = H* (B, T, 4, d) with
  * upstream gradient `grad` = dL/dH (B, T, 4, d):

@@ -1968,11 +1968,11 @@ int head_newton_call(const void* wx, const void* a_z, const void* a_r, const voi
                      const int* tbl) {
   int rc = gru::check(B, T, n_heads, d_head, max_iters, dtype);
   if (rc != PRNN_OK) return rc;
-  if (!wx || !a_z || !a_r || !a_n || !out || !workspace)
-    return fail(PRNN_ERR_VALUE, "wx, a_z, a_r, a_n, out and workspace must be non-null");
   const bool packed = cu != nullptr;
   if (packed && (n_seq < 1 || n_seq > T))
     return fail(PRNN_ERR_VALUE, "n_seq must be in [1, T], got %d", n_seq);
+  if (!wx || !a_z || !a_r || !a_n || !out || !workspace)
+    return fail(PRNN_ERR_VALUE, "wx, a_z, a_r, a_n, out and workspace must be non-null");
   size_t need = 0;
   const gru::Ws w = gru::carve(workspace, B, T, n_heads, max_iters, &need, packed);
   if (workspace_bytes < need)
@@ -2006,12 +2006,12 @@ int head_backward_call(const void* wx, const void* a_z, const void* a_r, const v
                        int n_seq) {
   int rc = gru::check(B, T, n_heads, d_head, 0, dtype);
   if (rc != PRNN_OK) return rc;
-  if (!wx || !a_z || !a_r || !a_n || !states || !grad || !g_wx || !g_a || !workspace)
-    return fail(PRNN_ERR_VALUE,
-                "wx, a_z, a_r, a_n, states, grad, g_wx, g_a and workspace must be non-null");
   const bool packed = cu != nullptr;
   if (packed && (n_seq < 1 || n_seq > T))
     return fail(PRNN_ERR_VALUE, "n_seq must be in [1, T], got %d", n_seq);
+  if (!wx || !a_z || !a_r || !a_n || !states || !grad || !g_wx || !g_a || !workspace)
+    return fail(PRNN_ERR_VALUE,
+                "wx, a_z, a_r, a_n, states, grad, g_wx, g_a and workspace must be non-null");
   size_t need = 0;
   const gru::BwdWs w = gru::carve_bwd(workspace, B, T, n_heads, &need, packed);
   if (workspace_bytes < need)

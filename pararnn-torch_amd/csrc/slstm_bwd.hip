@@ -529,8 +529,10 @@ int backward_call(const void* wx, const void* r, const void* h0, const void* sta
   if (rc != PRNN_OK) return rc;
   rc = slstm::check_tag_base(tag_base);
   if (rc != PRNN_OK) return rc;
-  if (pk.cu != nullptr && pk.n_seq < 1)
-    return fail(PRNN_ERR_VALUE, "n_seq must be >= 1, got %d", pk.n_seq);
+  if (pk.cu != nullptr && B != 1)
+    return fail(PRNN_ERR_VALUE, "a packed stream has B = 1, got B = %d", B);
+  if (pk.cu != nullptr && (pk.n_seq < 1 || pk.n_seq > T))
+    return fail(PRNN_ERR_VALUE, "n_seq must be in [1, T], got %d (T = %d)", pk.n_seq, T);
   if (!wx || !r || !states || !grad || !gwx || !gr || !workspace)
     return fail(PRNN_ERR_VALUE, "wx, r, states, grad, g_wx, g_r and workspace must be non-null");
   size_t need = 0;

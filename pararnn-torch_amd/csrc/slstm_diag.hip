@@ -16,12 +16,6 @@ extern "C" PRNN_API size_t prnn_slstm_init_workspace_size(int B, int T, int d, i
 
 namespace {
 
-int check_packed(const slstm::Packed& pk) {
-  if (pk.cu == nullptr) return PRNN_OK;
-  if (pk.n_seq < 1) return fail(PRNN_ERR_VALUE, "n_seq must be >= 1, got %d", pk.n_seq);
-  return PRNN_OK;
-}
-
 int init_call(const void* wx, const void* r, const void* h0, void* states, int B, int T, int d,
               int picard_iters, float eps, int dtype, void* workspace, size_t workspace_bytes,
               int tag_base, void* stream, const slstm::Packed& pk) {
@@ -29,7 +23,7 @@ int init_call(const void* wx, const void* r, const void* h0, void* states, int B
   if (rc != PRNN_OK) return rc;
   rc = slstm::check_tag_base(tag_base);
   if (rc != PRNN_OK) return rc;
-  rc = check_packed(pk);
+  rc = slstm::check_packed(pk, B, T);
   if (rc != PRNN_OK) return rc;
   if (picard_iters < 0 || picard_iters > slstm::kMaxStages - 2)
     return fail(PRNN_ERR_VALUE, "picard_iters must be in [0, %d], got %d",
@@ -64,7 +58,7 @@ int newton_call(const void* wx, const void* r, const void* h0, const void* state
   if (rc != PRNN_OK) return rc;
   rc = slstm::check_tag_base(tag_base);
   if (rc != PRNN_OK) return rc;
-  rc = check_packed(pk);
+  rc = slstm::check_packed(pk, B, T);
   if (rc != PRNN_OK) return rc;
   if (max_iters < 0 || max_iters > slstm::kMaxStages - 1)
     return fail(PRNN_ERR_VALUE, "max_iters must be in [0, %d], got %d", slstm::kMaxStages - 1,
@@ -190,7 +184,7 @@ int step_call(const void* wx, const void* r, const void* h0, const void* in, int
   if (rc != PRNN_OK) return rc;
   rc = slstm::check_tag_base(tag_base);
   if (rc != PRNN_OK) return rc;
-  rc = check_packed(pk);
+  rc = slstm::check_packed(pk, B, T);
   if (rc != PRNN_OK) return rc;
   if (!wx || !r || !in || !out || !workspace)
     return fail(PRNN_ERR_VALUE, "wx, r, in, out and workspace must be non-null");

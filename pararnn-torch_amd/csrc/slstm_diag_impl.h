@@ -435,5 +435,18 @@ void launch_newton_step_f16(bool in_f32, const f16* wx, const f16* r, const f16*
                             const void* in, float* out, int B, int T, int d, float omega,
                             float eps, const Lookback& lb, hipStream_t stream);
 
+// A packed stream is one batch row of T steps holding n_seq non-empty
+// sequences: cu_seqlens must rise strictly from 0 to T (the kernels locate
+// heads by a binary search and a per-wave bit mask, which an empty sequence
+// would make ambiguous).  The device cannot check the offsets without a host
+// copy, so only what the sizes imply is rejected here.
+static int check_packed(const slstm::Packed& pk, int B, int T) {
+  if (pk.cu == nullptr) return PRNN_OK;
+  if (B != 1) return fail(PRNN_ERR_VALUE, "a packed stream has B = 1, got B = %d", B);
+  if (pk.n_seq < 1 || pk.n_seq > T)
+    return fail(PRNN_ERR_VALUE, "n_seq must be in [1, T], got %d (T = %d)", pk.n_seq, T);
+  return PRNN_OK;
+}
+
 }  // namespace slstm
 }  // namespace prnn

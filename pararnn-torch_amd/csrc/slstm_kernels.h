@@ -709,7 +709,15 @@ slstm_picard_fused_kernel(
 // reads each step once (wx and the guess, kept in registers) and folds the
 // lane's affine aggregate x -> J x + F; pass 2 replays the steps from the true
 // carry, delta_t = J_t delta_{t-1} + F_t, and writes H + omega delta.
-template <typename TX, typename TIN, typename TOUT, int L, int W, bool DET, bool PK>
+//
+// EAGER (scan_backend='eager'): the step's cell and Jacobian round like the
+// reference's eager tensor ops in the storage dtype TX (cell_jac_eager), the
+// residual F = pred - H is rounded to TX, the scan runs in fp32 on those
+// values, and the update rounds delta to TX before H + omega delta is rounded
+// again (solvers/newton/__init__.py:516-543).  Pass 2 re-forms J instead of
+// the forward-mode replay so that it applies exactly the rounded entries.
+template <typename TX, typename TIN, typename TOUT, int L, int W, bool DET, bool PK,
+          bool EAGER = false>
 __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ rmix, const TX* __restrict__ h0,
     const TIN* __restrict__ hin, TOUT* __restrict__ hout, int B, int T, int d, int n_cb,
@@ -783,16 +791,32 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
       float x[4], hv[4];
       XS::get(xs[s], x);
       HS::get(hs[s], hv);
-      CellJ J = cell_jac(prev, x, r, eps);
-      if (head) J.f = J.cm = J.ch = J.nm = J.nh = J.al = J.mh = J.inv = J.dn = J.g = 0.f;
-      const float F[4] = {J.pc - hv[0], J.pn - hv[1], J.pm - hv[2], J.ph - hv[3]};
-      jmv_affine(J, F, a.b);
+      if constexpr (EAGER) {
+        CellJE J = cell_jac_eager<TX>(prev, x, r, eps);
+        if (head)
+          J.f = J.cm = J.ch = J.nm = J.nh = J.al = J.mh = J.hc = J.hn = J.hm = J.hh = 0.f;
+        const float F[4] = {round_to<TX>(J.pc - hv[0]), round_to<TX>(J.pn - hv[1]),
+                            round_to<TX>(J.pm - hv[2]), round_to<TX>(J.ph - hv[3])};
+        jmv_affine_e(J, F, a.b);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float col[4] = {a.A[0][j], a.A[1][j], a.A[2][j], a.A[3][j]};
-        jmv(J, col);
+        for (int j = 0; j < 4; ++j) {
+          float col[4] = {a.A[0][j], a.A[1][j], a.A[2][j], a.A[3][j]};
+          jmv_e(J, col);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) a.A[k][j] = col[k];
+          for (int k = 0; k < 4; ++k) a.A[k][j] = col[k];
+        }
+      } else {
+        CellJ J = cell_jac(prev, x, r, eps);
+        if (head) J.f = J.cm = J.ch = J.nm = J.nh = J.al = J.mh = J.inv = J.dn = J.g = 0.f;
+        const float F[4] = {J.pc - hv[0], J.pn - hv[1], J.pm - hv[2], J.ph - hv[3]};
+        jmv_affine(J, F, a.b);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float col[4] = {a.A[0][j], a.A[1][j], a.A[2][j], a.A[3][j]};
+          jmv(J, col);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) a.A[k][j] = col[k];
+        }
       }
 #pragma unroll
       for (int k = 0; k < 4; ++k) prev[k] = hv[k];
@@ -898,14 +922,25 @@ __global__ __launch_bounds__(64 * W) void slstm_newton_kernel(
       float x[4], hv[4];
       XS::get(xs[s], x);
       HS::get(hs[s], hv);
-      float pv[4], jv[4];
-      cell_jvp(prev, x, r, eps, dl, pv, jv);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) dl[k] = jv[k] + (pv[k] - hv[k]);
       const uint32_t so = s * row4 * sizeof(TOUT);
+      if constexpr (EAGER) {
+        CellJE J = cell_jac_eager<TX>(prev, x, r, eps);
+        const float F[4] = {round_to<TX>(J.pc - hv[0]), round_to<TX>(J.pn - hv[1]),
+                            round_to<TX>(J.pm - hv[2]), round_to<TX>(J.ph - hv[3])};
+        jmv_affine_e(J, F, dl);
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        stb<TOUT>(ro, vo, so + k * d * sizeof(TOUT), hv[k] + omega * dl[k]);
+        for (int k = 0; k < 4; ++k)
+          stb<TOUT>(ro, vo, so + k * d * sizeof(TOUT),
+                    add_rn(hv[k], mul_rn(omega, round_to<TX>(dl[k]))));
+      } else {
+        float pv[4], jv[4];
+        cell_jvp(prev, x, r, eps, dl, pv, jv);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) dl[k] = jv[k] + (pv[k] - hv[k]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          stb<TOUT>(ro, vo, so + k * d * sizeof(TOUT), hv[k] + omega * dl[k]);
+      }
 #pragma unroll
       for (int k = 0; k < 4; ++k) prev[k] = hv[k];
     };

@@ -464,6 +464,87 @@ __device__ __forceinline__ void jmv_affine(const CellJ& J, const float F[4], flo
   v[3] = J.inv * tc + J.dn * tn + J.g * h + F[3];
 }
 
+// ---- eager-rounding cell (scan_backend='eager' with 16-bit storage) -------
+// The reference's eager Newton step evaluates the cell and its Jacobian as a
+// chain of tensor ops in the storage dtype S, each rounding its result to S
+// (cells/para_slstm.py:241-281 for the cell, :378-446 for the Jacobian,
+// :530-534 for the max subgradient), then scans the S-valued J and residual
+// in fp32 (solvers/scan.py:229-246).  CellJE restates that op chain: every
+// intermediate is rounded where the eager op rounds it, in the same operand
+// order, with no contraction into FMAs.  Transcendentals use the accurate
+// library functions: the eager ops round a correctly evaluated fp32 result.
+// The h row is dense (hc, hn, hm, hh), as the eager Jacobian forms it.
+struct CellJE {
+  float pc, pn, pm, ph;                      // f(prev, x), S-valued
+  float f, cm, ch, nm, nh, al, mh;           // c, n, m rows
+  float hc, hn, hm, hh;                      // h row
+};
+
+template <typename S>
+__device__ __forceinline__ CellJE cell_jac_eager(const float prev[4], const float x[4],
+                                                 const float r[4], float eps) {
+#pragma clang fp contract(off)
+  auto R = [](float v) { return round_to<S>(v); };
+  const float c = prev[0], n = prev[1], m = prev[2], h = prev[3];
+  // pre = wx + r * h (two ops)
+  const float zi = R(x[0] + R(r[0] * h));
+  const float zf = R(x[1] + R(r[1] * h));
+  const float zz = R(x[2] + R(r[2] * h));
+  const float zo = R(x[3] + R(r[3] * h));
+  const float left = R(zf + m);
+  const float mn = fmaxf(left, zi);
+  const float al = left > zi ? 1.f : (left == zi ? 0.5f : 0.f);
+  const float ig = R(expf(R(zi - mn)));
+  const float fg = R(expf(R(left - mn)));
+  const float z = R(tanhf(zz));
+  const float nn = R(R(fg * n) + ig);
+  const float cn = R(R(fg * c) + R(ig * z));
+  const float o = R(1.f / (1.f + expf(-zo)));
+  const float den = R(nn + eps);
+  const float u = R(cn / den);
+  CellJE J;
+  J.pc = cn;
+  J.pn = nn;
+  J.pm = mn;
+  J.ph = R(o * u);
+  const float be = 1.f - al;
+  const float dm_dh = R(R(al * r[1]) + R(be * r[0]));
+  const float di_dm = R(-ig * al);
+  const float df_dm = R(fg * be);
+  const float di_dh = R(ig * R(r[0] - dm_dh));
+  const float df_dh = R(fg * R(r[1] - dm_dh));
+  const float dz_dh = R(R(1.f - R(z * z)) * r[2]);
+  const float do_dh = R(R(o * R(1.f - o)) * r[3]);
+  J.f = fg;
+  J.al = al;
+  J.mh = dm_dh;
+  J.cm = R(R(df_dm * c) + R(di_dm * z));
+  J.ch = R(R(R(df_dh * c) + R(di_dh * z)) + R(ig * dz_dh));
+  J.nm = R(R(df_dm * n) + di_dm);
+  J.nh = R(R(df_dh * n) + di_dh);
+  const float inv = R(o / den);
+  const float dn = R(R(-o * cn) / R(den * den));
+  J.hc = R(inv * fg);
+  J.hn = R(dn * fg);
+  J.hm = R(R(inv * J.cm) + R(dn * J.nm));
+  J.hh = R(R(R(inv * J.ch) + R(dn * J.nh)) + R(u * do_dh));
+  return J;
+}
+
+// v <- J v + F with the dense h row (fp32, as the eager scan composes).
+__device__ __forceinline__ void jmv_affine_e(const CellJE& J, const float F[4], float v[4]) {
+  const float c = v[0], n = v[1], m = v[2], h = v[3];
+  v[0] = J.f * c + J.cm * m + J.ch * h + F[0];
+  v[1] = J.f * n + J.nm * m + J.nh * h + F[1];
+  v[2] = J.al * m + J.mh * h + F[2];
+  v[3] = J.hc * c + J.hn * n + J.hm * m + J.hh * h + F[3];
+}
+
+__device__ __forceinline__ void jmv_e(const CellJE& J, float v[4]) {
+  const float zero[4] = {0.f, 0.f, 0.f, 0.f};
+  jmv_affine_e(J, zero, v);
+}
+
 // 4x4 affine element (A, b): x -> A x + b
 struct Aff {
   float A[4][4];

@@ -67,6 +67,10 @@ SIGNATURES: dict[str, tuple] = {
         _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _I, _P]),
     "prnn_slstm_newton_step": (
         _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _F, _F, _I, _P, _S, _I, _P]),
+    "prnn_slstm_newton_eager": (
+        _I, [_P, _P, _P, _P, _P, _I, _I, _I, _F, _F, _I, _P, _S, _I, _P]),
+    "prnn_slstm_newton_eager_packed": (
+        _I, [_P, _P, _P, _P, _P, _I, _I, _F, _F, _I, _P, _I, _P, _P, _S, _I, _P]),
     "prnn_slstm_init_packed_workspace_size": (_S, [_I, _I, _I, _I]),
     "prnn_slstm_init_packed": (
         _I, [_P, _P, _P, _P, _I, _I, _I, _F, _I, _P, _I, _P, _P, _S, _I, _P]),

@@ -10,13 +10,15 @@ Control flow follows the reference (``solvers/newton/__init__.py:212-324,
   residual exceeds ``picard_retry_atol``;
 * ``scan_backend`` 'auto' / 'fused' select the HIP kernels for
   ``ParaSLSTM(mix='diag')`` and ``ParaGRU(mix='head')`` on a ROCm device;
+  'eager' runs the reference's eager loop on the GPU (the sLSTM iterations in
+  a kernel that rounds like the eager tensor ops);
 * after the solve the residual gate re-evaluates ``max |F|`` with the cell's
   torch ``step`` and raises :class:`NewtonDivergenceError` above
   ``residual_fail``.
 
 The Newton solve itself never runs on the CPU: inputs on another device, or
-backends this build does not provide ('eager', 'triton',
-'context_parallel'), raise instead of falling back.
+backends this build does not provide ('triton', 'context_parallel'), raise
+instead of falling back.
 """
 
 from __future__ import annotations
@@ -91,7 +93,7 @@ def _fusable(cell: nn.Module, x: Tensor) -> bool:
 
 def _fused_error(cell: nn.Module, x: Tensor) -> str:
     return (
-        "scan_backend='fused' in pararnn_amd needs ParaSLSTM(mix='diag') or "
+        "pararnn_amd's Newton solve ('fused' / 'auto' / 'eager') needs ParaSLSTM(mix='diag') or "
         "ParaGRU(mix='head', d_head <= 64) on a ROCm GPU in float32/bfloat16/float16 "
         f"(got {type(cell).__name__}(mix={getattr(cell, 'mix', None)!r}) "
         f"{x.dtype} on {x.device})"
@@ -118,13 +120,15 @@ def _resolve_backend(cell: nn.Module, x: Tensor, config: NewtonConfig) -> Newton
     requested = config.scan_backend
     if config.coords == "log":
         raise TypeError("NewtonConfig(coords='log') is not provided by pararnn_amd")
-    if requested in ("eager", "triton", "context_parallel"):
+    if requested in ("triton", "context_parallel"):
         raise NotImplementedError(
             f"scan_backend={requested!r} is not provided by pararnn_amd; its Newton solve "
-            "runs the fused HIP kernels ('fused' / 'auto')"
+            "runs the HIP kernels ('fused' / 'auto', or 'eager' for the eager rounding)"
         )
     if not _fusable(cell, x):
         raise TypeError(_fused_error(cell, x))
+    if requested == "eager":
+        return config
     return replace(config, scan_backend="fused")
 
 
@@ -244,6 +248,13 @@ def _newton_solve(cell, x, config, *, h0, stats, wx=None, cu_seqlens=None,
         wx = cell.W_x(x)
     gate_h0 = h0 if block_table is None else gather_h0(
         h0, block_table, int(cu_seqlens.numel()) - 1, _state_tail(cell))
+    if config.scan_backend == "eager":
+        states, iters, history, last, current = _newton_eager(cell, wx, config, h0=h0,
+                                                              cu_seqlens=cu_seqlens)
+        if not torch.compiler.is_compiling():
+            _fill_stats(cell, x, states, h0, config, iters=iters, stats=stats, history=history,
+                        known=last if current else None, cu_seqlens=cu_seqlens)
+        return states
     if config.fused_early_exit and not torch.compiler.is_compiling():
         states, iters, history = _fused_early_exit(cell, wx, config, h0=h0,
                                                    cu_seqlens=cu_seqlens,
@@ -293,6 +304,56 @@ def _fused_early_exit(cell, wx, config, *, h0, cu_seqlens=None,
         if res < atol:
             return states, it + 1, history
     return states, int(config.max_iters), history
+
+
+def _newton_eager(cell, wx, config, *, h0, cu_seqlens=None):
+    """``scan_backend='eager'``: the reference's eager Newton loop
+    (newton/__init__.py:467-549) on the GPU.  Returns ``(states, iterations,
+    residual history, last residual, whether it is the residual of states)``.
+
+    ParaSLSTM diag: the Picard guess (the same warm start as the fused path:
+    the reference's eager and fused paths share it, picard.py:161-186), then
+    one launch per iteration whose cell, Jacobian, residual, delta and update
+    round in the tensor dtype where the eager tensor ops round
+    (``prnn_slstm_newton_eager``).  ParaGRU head: the fused kernels (fp32 work
+    on the tensor dtype), since its eager and fused semantics agree to within
+    the bf16 tolerance.  With ``residual_atol`` set (and not compiling) the
+    host reads max|F| of the current iterate before each update and stops
+    below it, as the eager loop does; that iteration counts."""
+    atol = config.residual_atol if not torch.compiler.is_compiling() else None
+    K = int(config.max_iters)
+    omega = float(config.omega)
+    history: list[float] = []
+
+    def residual(states: Tensor) -> float:
+        pred = cell.step(_prepend_any(states, h0, cu_seqlens), None, wx=wx)
+        return float((pred - states).abs().amax())
+
+    if isinstance(cell, ParaSLSTM):
+        r = cell.clipped_r()
+        states = ops.slstm_init_fused(wx, r, h0, cu_seqlens, None,
+                                      picard_iters=int(config.picard_iters or 0), eps=cell.eps)
+        for it in range(K):
+            if atol is not None:
+                history.append(residual(states))
+                if history[-1] < atol:
+                    return states, it + 1, history, history[-1], True
+            states = ops.slstm_newton_eager(wx, r, h0, states, omega=omega, eps=cell.eps,
+                                            cu_seqlens=cu_seqlens)
+        return states, K, history, (history[-1] if history else float("nan")), False
+
+    def solve(k: int) -> Tensor:
+        return fused_newton(cell, wx, max_iters=k, omega=omega, h0=h0, cu_seqlens=cu_seqlens)
+
+    if atol is None:
+        return solve(K), K, history, float("nan"), False
+    # the iterate before update `it` is the K = it fused solve
+    for it in range(K):
+        states = solve(it)
+        history.append(residual(states))
+        if history[-1] < atol:
+            return states, it + 1, history, history[-1], True
+    return solve(K), K, history, history[-1] if history else float("nan"), False
 
 
 def _newton_chunked(cell, x, config, *, h0, stats) -> Tensor:
@@ -387,6 +448,9 @@ def newton_apply(
         or any(p.requires_grad for p in params)
     )
     if block_table is not None:
+        if config.scan_backend != "fused":
+            raise ValueError("block_table newton needs scan_backend='fused' (or auto on a ROCm "
+                             "GPU)")
         if config.chunk_len is not None:
             raise ValueError("block_table cannot be combined with chunk_len")
         if needs_grad:
@@ -481,11 +545,16 @@ def _newton_ragged(cell, x, config, *, h0, stats, cu_seqlens, block_table, needs
         h0 = gather_h0(h0, block_table, n_seq, _state_tail(cell))
     elif h0 is not None and h0.shape[0] != n_seq:
         raise ValueError(f"h0 batch {h0.shape[0]} != n_seq {n_seq}")
+    if config.fused_early_exit:
+        if not (isinstance(cell, ParaSLSTM) and cell.mix == "diag"):
+            raise TypeError("fused_early_exit is mix='diag' only; ParaGRU(mix='head') uses "
+                            "fixed K")
+        # an exit decided per length group would not be the packed stream's
+        raise ValueError("fused_early_exit with cu_seqlens runs in the packed kernels; it is "
+                         "not available with PARARNN_AMD_PACKED=0 (length groups)")
     plan = RaggedPlan(cs, x.device)
     ladder = bool(config.picard_adapt) and isinstance(cell, ParaSLSTM)
-    # The length groups run the full K: an early exit decided per group would
-    # not be the packed stream's (fused_early_exit is ignored with cu_seqlens).
-    inner = replace(config, picard_adapt=False, residual_fail=None, fused_early_exit=False)
+    inner = replace(config, picard_adapt=False, residual_fail=None)
     hist = []
     while True:
         if needs_grad:

@@ -357,6 +357,47 @@ def slstm_newton_step(wx: Tensor, r: Tensor, h0: Tensor | None, states: Tensor, 
     return out
 
 
+def slstm_newton_eager(wx: Tensor, r: Tensor, h0: Tensor | None, states: Tensor, *,
+                       omega: float, eps: float, cu_seqlens: Tensor | None = None,
+                       block_table: Tensor | None = None) -> Tensor:
+    """One Newton iteration with the reference's eager rounding
+    (``scan_backend='eager'``, solvers/newton/__init__.py:516-543): the cell and
+    its Jacobian rounded op by op in ``wx``'s dtype, the residual rounded, an
+    fp32 scan, the rounded delta and the rounded update.  ``states`` and the
+    result are in ``wx``'s dtype.  Not a registered op: the eager loop runs
+    one launch per iteration from the host."""
+    batch, time, d_h = _slstm_shapes(wx, r)
+    code = _validate("slstm_newton_eager", wx, r, h0, states)
+    cs32, bt, n_seq, h0 = _packed_args(cu_seqlens, block_table, wx, h0, d_h)
+    if cs32 is None:
+        h0 = _slstm_h0(h0, batch, d_h)
+    if states.shape != (batch, time, 4, d_h):
+        raise ValueError(f"states shape {tuple(states.shape)} != {(batch, time, 4, d_h)}")
+    wx, r, states = wx.contiguous(), r.contiguous(), states.contiguous()
+    out = torch.empty_like(states)
+    lib = _lib.load()
+    _lib.sync_deterministic(lib)
+    with torch.cuda.device(wx.device):
+        if cs32 is None:
+            nbytes = lib.prnn_slstm_newton_workspace_size(batch, time, d_h, 1, code)
+            ws, tag = _slstm_workspace(nbytes, wx.device)
+            rc = lib.prnn_slstm_newton_eager(
+                _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), _ptr(out), batch, time, d_h,
+                float(omega), float(eps), code, _ptr(ws), ws.numel(), tag, _stream(wx.device),
+            )
+        else:
+            nbytes = lib.prnn_slstm_newton_packed_workspace_size(time, d_h, 1, code)
+            ws, tag = _slstm_workspace(nbytes, wx.device)
+            rc = lib.prnn_slstm_newton_eager_packed(
+                _ptr(wx), _ptr(r), _ptr(h0), _ptr(states), _ptr(out), time, d_h, float(omega),
+                float(eps), code, _ptr(cs32), n_seq, _ptr(bt), _ptr(ws), ws.numel(), tag,
+                _stream(wx.device),
+            )
+    _lib.check(rc, "slstm_newton_eager")
+    _check_lookback(ws, "slstm_newton_eager")
+    return out
+
+
 @newton_slstm_fused.register_fake
 def _(wx, r, h0=None, states=None, block_table=None, cu_seqlens=None, *, max_iters, omega, eps,
       log_coords=False, scan_tile="assoc", time_loop=False, window_len=0):

@@ -82,8 +82,12 @@ def test_cpu_input_fails_loudly():
             newton_apply(cell, x, NewtonConfig(scan_backend="fused"))
         with pytest.raises(TypeError, match="ROCm GPU"):
             newton_apply(cell, x)
-        with pytest.raises(NotImplementedError):
+        # the eager loop runs on the GPU too: a CPU tensor is refused, not
+        # solved by torch ops
+        with pytest.raises(TypeError, match="ROCm GPU"):
             newton_apply(cell, x, NewtonConfig(scan_backend="eager"))
+        with pytest.raises(NotImplementedError):
+            newton_apply(cell, x, NewtonConfig(scan_backend="triton"))
 
 
 def test_unsupported_cells_and_knobs():

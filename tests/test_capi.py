@@ -89,3 +89,31 @@ def test_host_only_calls():
     rc = lib.prnn_slstm_backward_ex(None, None, None, None, None, None, None, None, None, 1, 1, 1,
                                     1e-6, 0, None, 0, 5, None)
     assert rc == _lib.PRNN_ERR_VALUE and b"non-null" in lib.prnn_last_error()
+
+
+def test_packed_entry_points_reject_bad_sequence_counts():
+    """n_seq outside [1, T] cannot describe strictly rising offsets of a
+    T-step stream: every packed entry point rejects it before any device
+    work (cu_seqlens is never read, so a dummy address is enough)."""
+    from pararnn_amd import _lib
+
+    if not os.path.exists(_lib.lib_path()):
+        pytest.skip("library not built")
+    lib = _lib.load()
+    cu = 64  # never dereferenced: the size check fails first
+    for n_seq in (0, 11):
+        rc = lib.prnn_slstm_init_packed(None, None, None, None, 10, 4, 1, 1e-6, 0, cu, n_seq,
+                                        None, None, 0, 0, None)
+        assert rc == _lib.PRNN_ERR_VALUE and b"n_seq" in lib.prnn_last_error()
+        rc = lib.prnn_slstm_newton_packed(None, None, None, None, None, 10, 4, 2, 1.0, 1e-6, 0,
+                                          cu, n_seq, None, None, 0, 0, None)
+        assert rc == _lib.PRNN_ERR_VALUE and b"n_seq" in lib.prnn_last_error()
+        rc = lib.prnn_slstm_newton_step_packed(None, None, None, None, 0, None, 10, 4, 1.0, 1e-6,
+                                               0, cu, n_seq, None, None, 0, 0, None)
+        assert rc == _lib.PRNN_ERR_VALUE and b"n_seq" in lib.prnn_last_error()
+        rc = lib.prnn_slstm_backward_packed(None, None, None, None, None, None, None, None, None,
+                                            10, 4, 1e-6, 0, cu, n_seq, None, 0, 0, None)
+        assert rc == _lib.PRNN_ERR_VALUE and b"n_seq" in lib.prnn_last_error()
+        rc = lib.prnn_gru_head_newton_packed(None, None, None, None, None, None, 10, 1, 64, 2,
+                                             1.0, 0, cu, n_seq, None, None, 0, None)
+        assert rc == _lib.PRNN_ERR_VALUE and b"n_seq" in lib.prnn_last_error()
