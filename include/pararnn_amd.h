@@ -305,6 +305,35 @@ PRNN_API int prnn_gru_head_backward(const void* wx, const void* a_z, const void*
                                     int T, int n_heads, int d_head, int dtype, void* workspace,
                                     size_t workspace_bytes, void* stream);
 
+/* Wide heads, 64 < d_head <= 128 (replaces the reference's streamed head
+ * tier, kernels/newton_gru_head.py:121-150 and its _newton_head_stream_a_kernel
+ * at :765-960, one program per (b, head) walking T).  The host computes the
+ * gates of every step at the current iterate -- z, r, n (B, T, d) fp32 from
+ * hp, the previous state of every step (h0's row at a sequence start) --
+ * with GEMMs over all rows; these walk time, one workgroup per (sequence,
+ * head), A_* (n_heads, d_head, d_head) in `dtype`, fp32 work.
+ *
+ * prnn_gru_wide_walk: one Newton iteration's linear solve and update,
+ *   delta_t = J_t delta_{t-1} + lerp(hp_t, n_t, z_t) - hin_t,
+ *   out_t = hin_t + omega delta_t
+ * (out fp32 when out_f32, which may alias hin; else `dtype`).
+ * prnn_gru_wide_reverse: the eq. 2.6 adjoint at H* (hp from H*), grad =
+ * dL/dH (fp32 when grad_f32, else `dtype`): g_wx (B, T, 3d) fp32 receives the
+ * pre-activation gradients (z, r, n blocks), g_h0 (rows, d) fp32 (or NULL)
+ * J^T mu at each sequence's first step.
+ * cu_seqlens / n_seq: a packed stream (B = 1) walked per sequence, or NULL. */
+PRNN_API int prnn_gru_wide_walk(const float* z, const float* r, const float* n, const float* hp,
+                                const float* hin, const void* a_z, const void* a_r,
+                                const void* a_n, void* out, int out_f32, int B, int T,
+                                int n_heads, int d_head, float omega, int dtype,
+                                const int* cu_seqlens, int n_seq, void* stream);
+PRNN_API int prnn_gru_wide_reverse(const float* z, const float* r, const float* n,
+                                   const float* hp, const void* grad, int grad_f32,
+                                   const void* a_z, const void* a_r, const void* a_n,
+                                   float* g_wx, float* g_h0, int B, int T, int n_heads,
+                                   int d_head, int dtype, const int* cu_seqlens, int n_seq,
+                                   void* stream);
+
 /* Head GRU on a packed stream: wx (1, T, 3d) holds n_seq sequences, sequence
  * q on steps [cu_seqlens[q], cu_seqlens[q+1]) (int32 device array, n_seq + 1
  * entries, 0 = cu_seqlens[0] < ... < cu_seqlens[n_seq] = T).  At a sequence's

@@ -87,6 +87,10 @@ SIGNATURES: dict[str, tuple] = {
     "prnn_gru_head_backward_packed_workspace_size": (_S, [_I, _I, _I, _I]),
     "prnn_gru_head_backward_packed": (
         _I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _S, _P]),
+    "prnn_gru_wide_walk": (
+        _I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _P, _I, _P]),
+    "prnn_gru_wide_reverse": (
+        _I, [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P]),
     "prnn_slstm_decode": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _F, _I, _I, _P]),
     "prnn_gru_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _I, _I, _P]),
 }

@@ -18,7 +18,13 @@ have zero inputs, zero weights and zero initial state, so they stay at zero
 (z = r = 1/2, n = 0 gives h' = h / 2) and never touch a real channel.
 
 The reference handles ``d_head <= 64`` with a masked ``BLOCK_D`` tile
-(kernels/newton_gru_head.py:121-136); ``d_head > 64`` is not provided here.
+(kernels/newton_gru_head.py:121-136).  Heads of 64 < d_head <= 128 take the
+wide tier instead (``ops._gru_head_wide``), not these blocks.
+
+Caveat of sharing a block: the matrix-core products multiply the zero
+off-diagonal entries too, so a non-finite value in one narrow head's state
+or gradient (inf * 0 = NaN) reaches the other heads of its block, where the
+reference's masked tile keeps heads apart.  Finite inputs are unaffected.
 """
 
 from __future__ import annotations

@@ -87,14 +87,14 @@ def _fusable(cell: nn.Module, x: Tensor) -> bool:
     if isinstance(cell, ParaSLSTM):
         return cell.mix == "diag"
     if isinstance(cell, ParaGRU):
-        return cell.mix == "head" and cell.d_head <= 64
+        return cell.mix == "head" and cell.d_head <= 128
     return False
 
 
 def _fused_error(cell: nn.Module, x: Tensor) -> str:
     return (
         "pararnn_amd's Newton solve ('fused' / 'auto' / 'eager') needs ParaSLSTM(mix='diag') or "
-        "ParaGRU(mix='head', d_head <= 64) on a ROCm GPU in float32/bfloat16/float16 "
+        "ParaGRU(mix='head', d_head <= 128) on a ROCm GPU in float32/bfloat16/float16 "
         f"(got {type(cell).__name__}(mix={getattr(cell, 'mix', None)!r}) "
         f"{x.dtype} on {x.device})"
     )

@@ -507,8 +507,9 @@ def newton_gru_head_fused(
     d_h = n_heads * d_head
     if wx.dim() != 3 or wx.shape[-1] != 3 * d_h:
         raise ValueError(f"wx last dim {wx.shape[-1]} != 3 * d_h={3 * d_h}")
-    if d_head > 64:
-        raise TypeError(f"newton_gru_head_fused: pararnn_amd provides d_head <= 64, got {d_head}")
+    if d_head > WIDE_MAX:
+        raise TypeError(f"newton_gru_head_fused: pararnn_amd provides d_head <= {WIDE_MAX}, "
+                        f"got {d_head}")
     if cu_seqlens is not None:
         from pararnn_amd.ragged import RaggedPlan, packed_in_kernel, validate_cu_seqlens
 
@@ -537,6 +538,8 @@ def _gru_head_dense(wx, a_z, a_r, a_n, h0, max_iters, omega, cs=None):
         raise ValueError(f"h0 shape {tuple(h0.shape)} != {(rows, d_h)}")
     if max_iters < 0:
         raise ValueError(f"max_iters must be >= 0, got {max_iters!r}")
+    if d_head > 64:
+        return _gru_head_wide(wx, a_z, a_r, a_n, h0, int(max_iters), float(omega), code, cs)
     # heads narrower than 64 run as block-diagonal 64 x 64 blocks
     hb = HeadBlocks(n_heads, d_head, wx.device)
     wx = hb.to_blocks(wx, 3).contiguous()
@@ -595,8 +598,9 @@ def gru_head_backward_fused(
     n_heads, d_head, _ = a_z.shape
     if a_r.shape != a_z.shape or a_n.shape != a_z.shape:
         raise ValueError("a_z, a_r, a_n shape mismatch")
-    if d_head > 64:
-        raise TypeError(f"gru_head_backward_fused: pararnn_amd provides d_head <= 64, got {d_head}")
+    if d_head > WIDE_MAX:
+        raise TypeError(f"gru_head_backward_fused: pararnn_amd provides d_head <= {WIDE_MAX}, "
+                        f"got {d_head}")
     d_h = n_heads * d_head
     if wx.dim() != 3 or wx.shape[-1] != 3 * d_h:
         raise ValueError(f"wx last dim {wx.shape[-1]} != 3 * d_h={3 * d_h}")
@@ -616,6 +620,8 @@ def gru_head_backward_fused(
         rows = int(cs32.numel()) - 1
     if h0 is not None and h0.shape != (rows, d_h):
         raise ValueError(f"h0 shape {tuple(h0.shape)} != {(rows, d_h)}")
+    if d_head > 64:
+        return _gru_head_wide_backward(wx, a_z, a_r, a_n, h0, states, grad, code, cs32)
     # heads narrower than 64 run as block-diagonal 64 x 64 blocks
     hb = HeadBlocks(n_heads, d_head, wx.device)
     wx = hb.to_blocks(wx, 3).contiguous()
@@ -659,3 +665,120 @@ def _(wx, a_z, a_r, a_n, h0, states, grad, cu_seqlens=None):
         wx.new_empty(3, n_heads, d_head, d_head, dtype=torch.float32),
         wx.new_empty(rows, n_heads * d_head, dtype=torch.float32),
     )
+
+
+# ---------------------------------------------------------------------------
+# Wide heads, 64 < d_head <= 128 (the tier of the reference's streamed head
+# kernel, kernels/newton_gru_head.py:121-150, 900-960)
+# ---------------------------------------------------------------------------
+
+WIDE_MAX = 128
+
+
+def _wide_prev(states: Tensor, h0: Tensor | None, cs: Tensor | None) -> Tensor:
+    """Previous state at every step (fp32): h0's row (zeros without h0) at each
+    sequence's first step."""
+    if cs is not None:
+        from pararnn_amd.ragged import prepend_state_ragged
+
+        return prepend_state_ragged(states, h0, cs)
+    out = states.new_empty(states.shape)
+    out[:, 1:] = states[:, :-1]
+    out[:, 0] = 0 if h0 is None else h0
+    return out
+
+
+def _wide_gates(wx32: Tensor, hp: Tensor, a: tuple[Tensor, Tensor, Tensor]):
+    """Gates ``z, r, n`` (fp32 ``(B, T, d)``) of every step from its previous
+    state ``hp``: ``sigmoid(wx_z + h A_z)``, ``sigmoid(wx_r + h A_r)``,
+    ``tanh(wx_n + (h r) A_n)`` per head (cells/para_gru.py:414-467).  The
+    three products are GEMMs over all B*T rows; nothing here depends on the
+    Newton walk, so it runs as wide parallel work before it."""
+    batch, time, three_d = wx32.shape
+    n_heads, d_head, _ = a[0].shape
+    rows = batch * time
+    hv = hp.reshape(rows, n_heads, d_head).transpose(0, 1)  # (H, rows, dh)
+    x = wx32.reshape(rows, 3, n_heads, d_head)
+
+    def mix(v: Tensor, m: Tensor) -> Tensor:  # (H, rows, dh) @ (H, dh, dh) -> (rows, H, dh)
+        return torch.bmm(v, m).transpose(0, 1)
+
+    z = torch.sigmoid(mix(hv, a[0]) + x[:, 0])
+    r = torch.sigmoid(mix(hv, a[1]) + x[:, 1])
+    n = torch.tanh(mix(hv * r.transpose(0, 1), a[2]) + x[:, 2])
+    shape = (batch, time, n_heads * d_head)
+    return z.reshape(shape), r.reshape(shape), n.reshape(shape)
+
+
+def _gru_head_wide(wx, a_z, a_r, a_n, h0, max_iters, omega, code, cs=None):
+    """Forward of the wide tier: the initial guess ``f(h_prev0, x)``, then per
+    Newton iteration the gates at the iterate (GEMMs) and one HIP walk per
+    (sequence, head) for ``delta`` and the update (``prnn_gru_wide_walk``).
+    fp32 work; the result in ``wx``'s dtype."""
+    n_heads, d_head, _ = a_z.shape
+    batch, time, _ = wx.shape
+    d_h = n_heads * d_head
+    wx32 = wx.float()
+    a32 = tuple(t.float().contiguous() for t in (a_z, a_r, a_n))
+    h0_32 = None if h0 is None else h0.float()
+    zeros = wx32.new_zeros(batch, time, d_h)
+    hp0 = _wide_prev(zeros, h0_32, cs)
+    z, _, n = _wide_gates(wx32, hp0, a32)
+    states = torch.lerp(hp0, n, z)
+    if max_iters == 0:
+        return states.to(wx.dtype)
+    a_k = tuple(t.contiguous() for t in (a_z, a_r, a_n))
+    cs32 = None if cs is None else cs.to(device=wx.device, dtype=torch.int32).contiguous()
+    n_seq = 0 if cs32 is None else int(cs32.numel()) - 1
+    lib = _lib.load()
+    out = None
+    for it in range(max_iters):
+        hp = _wide_prev(states, h0_32, cs).contiguous()
+        z, r, n = (t.contiguous() for t in _wide_gates(wx32, hp, a32))
+        last = it == max_iters - 1
+        narrow = last and wx.dtype != torch.float32
+        out = wx.new_empty(batch, time, d_h) if narrow else states
+        with torch.cuda.device(wx.device):
+            rc = lib.prnn_gru_wide_walk(
+                _ptr(z), _ptr(r), _ptr(n), _ptr(hp), _ptr(states), _ptr(a_k[0]), _ptr(a_k[1]),
+                _ptr(a_k[2]), _ptr(out), int(not narrow), batch, time, n_heads, d_head,
+                float(omega), code, _ptr(cs32), n_seq, _stream(wx.device),
+            )
+        _lib.check(rc, "newton_gru_head_fused (wide heads)")
+        states = out
+    return out if out.dtype == wx.dtype else out.to(wx.dtype)
+
+
+def _gru_head_wide_backward(wx, a_z, a_r, a_n, h0, states, grad, code, cs32=None):
+    """Eq. 2.6 backward of the wide tier at ``H* = states``: the gates at H*
+    (GEMMs), one HIP adjoint walk per (sequence, head)
+    (``prnn_gru_wide_reverse``: dL/dwx and dL/dh0), then dL/dA as GEMMs over
+    the B*T rows, ``sum_t X_t^T D_t`` with X = h_prev (z, r) or h_prev r (n)."""
+    n_heads, d_head, _ = a_z.shape
+    batch, time, _ = wx.shape
+    d_h = n_heads * d_head
+    cs = None if cs32 is None else cs32.long()
+    rows = batch if cs32 is None else int(cs32.numel()) - 1
+    wx32 = wx.float()
+    a32 = tuple(t.float().contiguous() for t in (a_z, a_r, a_n))
+    hp = _wide_prev(states.float(), None if h0 is None else h0.float(), cs).contiguous()
+    z, r, n = (t.contiguous() for t in _wide_gates(wx32, hp, a32))
+    a_k = tuple(t.contiguous() for t in (a_z, a_r, a_n))
+    grad = grad.contiguous()
+    g_wx = torch.empty(batch, time, 3 * d_h, dtype=torch.float32, device=wx.device)
+    g_h0 = torch.zeros(rows, d_h, dtype=torch.float32, device=wx.device)
+    lib = _lib.load()
+    with torch.cuda.device(wx.device):
+        rc = lib.prnn_gru_wide_reverse(
+            _ptr(z), _ptr(r), _ptr(n), _ptr(hp), _ptr(grad), int(grad.dtype == torch.float32),
+            _ptr(a_k[0]), _ptr(a_k[1]), _ptr(a_k[2]), _ptr(g_wx), _ptr(g_h0), batch, time,
+            n_heads, d_head, code, _ptr(cs32), 0 if cs32 is None else rows, _stream(wx.device),
+        )
+    _lib.check(rc, "gru_head_backward_fused (wide heads)")
+    n_rows = batch * time
+    dpre = g_wx.view(n_rows, 3, n_heads, d_head).permute(1, 2, 0, 3)  # (3, H, rows, dh)
+    xs = hp.view(n_rows, n_heads, d_head).transpose(0, 1)  # (H, rows, dh)
+    xr = (hp * r).view(n_rows, n_heads, d_head).transpose(0, 1)
+    g_a = torch.stack([torch.bmm(x.transpose(1, 2), dpre[g])
+                       for g, x in enumerate((xs, xs, xr))])
+    return g_wx.to(wx.dtype), g_a, g_h0
