@@ -402,6 +402,48 @@ def head_cfg4(torch, reps: int):
     return out
 
 
+def extra_paths(torch, reps: int):
+    """Two paths beside the metric, timed end to end through newton_apply:
+    - eager: scan_backend='eager' at config 2's shape (d=1024, B=8, T=16384,
+      bf16, K=2, P=5): the warm start and one eager-rounding launch per
+      Newton iteration;
+    - wide heads: ParaGRU(mix='head') with d_head=128 (H=4, d=512), B=4,
+      T=8192, fp32, K=3 -- forward solve and the eq. 2.6 backward op (the
+      tier whose Newton solve walks time per (sequence, head))."""
+    from pararnn_amd import NewtonConfig, ParaGRU, ParaSLSTM, newton_apply, ops
+
+    dev = "cuda:0"
+    out = {}
+    torch.manual_seed(0)
+    cell = ParaSLSTM(D, D).to(dev, torch.bfloat16)
+    g = torch.Generator(device=dev).manual_seed(1)
+    x = torch.randn(8, 16384, D, generator=g, device=dev).to(torch.bfloat16)
+    cfg = NewtonConfig(max_iters=K, picard_iters=P, residual_atol=None, residual_fail=None,
+                       picard_adapt=False, scan_backend="eager")
+    with torch.no_grad():
+        ms = _time(torch, lambda: newton_apply(cell, x, cfg), reps, warm=1)
+    out["eager_cfg2"] = {"workload": "ParaSLSTM diag d=1024 B=8 T=16384 bf16 K=2 P=5, "
+                                     "scan_backend='eager', newton_apply",
+                         "ms": ms, "tokens_per_s": 8 * 16384 / (ms * 1e-3)}
+    del x
+    b, t, H, dh = 4, 8192, 4, 128
+    torch.manual_seed(0)
+    gcell = ParaGRU(512, 512, mix="head", n_heads=H).to(dev)
+    xg = torch.randn(b, t, 512, generator=g, device=dev)
+    up = torch.randn(b, t, 512, generator=g, device=dev)
+    gcfg = NewtonConfig(max_iters=3, residual_atol=None, residual_fail=None)
+    with torch.no_grad():
+        ms_f = _time(torch, lambda: newton_apply(gcell, xg, gcfg), 2, warm=1)
+        Hs = newton_apply(gcell, xg, gcfg)
+        wx = gcell.W_x(xg)
+        a = gcell.clipped_a_head()
+        ms_b = _time(torch, lambda: ops.gru_head_backward_fused(wx, *a, None, Hs, up), 2, warm=1)
+    out["head_wide"] = {"workload": f"ParaGRU head H={H} d_head={dh} d=512 B={b} T={t} fp32 K=3",
+                        "fwd_ms": ms_f, "fwd_tokens_per_s": b * t / (ms_f * 1e-3),
+                        "bwd_op_ms": ms_b}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -413,6 +455,8 @@ def main() -> int:
     ap.add_argument("--no-head", action="store_true", help="skip the config 4 head-GRU lines")
     ap.add_argument("--no-ragged", action="store_true",
                     help="skip the ragged cu_seqlens and T=1 decode lines")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the eager-backend and wide-head lines")
     ap.add_argument("--head-only", action="store_true",
                     help="only the config 4 head-GRU lines (for profiling that path)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -613,6 +657,8 @@ def main() -> int:
         out["head_cfg4"] = head_cfg4(torch, 3)
     if not args.no_ragged:
         out["ragged"], out["decode_t1"] = ragged_decode(torch, 5)
+    if not args.no_extra:
+        out.update(extra_paths(torch, 3))
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(torch, args.cpu_sample)
         out["gpu_over_cpu"] = out["value"] / out["cpu_baseline"]["value"]
