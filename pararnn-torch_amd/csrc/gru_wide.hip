@@ -3,7 +3,7 @@
 // workgroup per (sequence, head).
 //
 // This is the tier of the reference's streamed head kernel
-// (kernels/newton_gru_head.py:900-960, _newton_head_stream_a_kernel: one
+// (kernels/newton_gru_head.py:765-960, _newton_head_stream_a_kernel: one
 // program per (b, head), a serial walk over T per Newton iteration, A_* read
 // in fp32).  Here the parts of an iteration that do not depend on the walk
 // run beforehand as wide parallel work (the gates z, r, n at the iterate:
@@ -59,6 +59,29 @@ __device__ __forceinline__ void load_quarter(const TX* A, int dh, int c, int q, 
   }
 }
 
+// One step's per-channel inputs, loaded two steps ahead of their use: a walk
+// step is short, so a load issued at the step that needs it would wait for
+// the full memory latency every step.
+struct StepIn {
+  float z, r, n, hp, x;  // x: the iterate (forward) or dL/dH (adjoint)
+};
+
+template <typename TG>
+__device__ __forceinline__ StepIn load_step(const float* __restrict__ z, const float* __restrict__ r,
+                                            const float* __restrict__ n,
+                                            const float* __restrict__ hp, const TG* __restrict__ x,
+                                            size_t at, bool ok) {
+  StepIn v{0.f, 0.f, 0.f, 0.f, 0.f};
+  if (ok) {
+    v.z = z[at];
+    v.r = r[at];
+    v.n = n[at];
+    v.hp = hp[at];
+    v.x = ld(x + at);
+  }
+  return v;
+}
+
 __device__ __forceinline__ float dot_quarter(const float a[kK], const float* __restrict__ v) {
   float acc = 0.f;
 #pragma unroll
@@ -101,16 +124,17 @@ __global__ __launch_bounds__(kThreads) void gruw_walk_kernel(
   if (q == 0) s_d[c] = 0.f;
   float delta = 0.f;
   __syncthreads();
+  const size_t base = static_cast<size_t>(sp.row) * T * d + col;
+  StepIn p0 = load_step(z, r, n, hp, hin, base + static_cast<size_t>(sp.t0) * d,
+                        live && sp.t0 < sp.t1);
+  StepIn p1 = load_step(z, r, n, hp, hin, base + static_cast<size_t>(sp.t0 + 1) * d,
+                        live && sp.t0 + 1 < sp.t1);
   for (int t = sp.t0; t < sp.t1; ++t) {
-    const size_t at = (static_cast<size_t>(sp.row) * T + t) * d + col;
-    float zt = 0.f, rt = 0.f, nt = 0.f, ht = 0.f, hv = 0.f;
-    if (live) {
-      zt = z[at];
-      rt = r[at];
-      nt = n[at];
-      ht = hp[at];
-      hv = hin[at];
-    }
+    const size_t at = base + static_cast<size_t>(t) * d;
+    const StepIn cur = p0;
+    p0 = p1;
+    p1 = load_step(z, r, n, hp, hin, at + 2 * static_cast<size_t>(d), live && t + 2 < sp.t1);
+    const float zt = cur.z, rt = cur.r, nt = cur.n, ht = cur.hp, hv = cur.x;
     // stage 1: A_r^T delta and A_z^T delta, this quarter of k
     s_p[0][q][c] = dot_quarter(ar, s_d + q * kK);
     s_p[1][q][c] = dot_quarter(az, s_d + q * kK);
@@ -166,16 +190,17 @@ __global__ __launch_bounds__(kThreads) void gruw_reverse_kernel(
   const bool live = c < dh;
   const size_t col = static_cast<size_t>(head) * dh + c;
   float nu = 0.f;
+  const size_t base = static_cast<size_t>(sp.row) * T * d + col;
+  StepIn p0 = load_step(z, r, n, hp, grad, base + static_cast<size_t>(sp.t1 - 1) * d,
+                        live && sp.t1 - 1 >= sp.t0);
+  StepIn p1 = load_step(z, r, n, hp, grad, base + static_cast<size_t>(sp.t1 - 2) * d,
+                        live && sp.t1 - 2 >= sp.t0);
   for (int t = sp.t1 - 1; t >= sp.t0; --t) {
-    const size_t at = (static_cast<size_t>(sp.row) * T + t) * d + col;
-    float zt = 0.f, rt = 0.f, nt = 0.f, ht = 0.f, g = 0.f;
-    if (live) {
-      zt = z[at];
-      rt = r[at];
-      nt = n[at];
-      ht = hp[at];
-      g = ld(grad + at);
-    }
+    const size_t at = base + static_cast<size_t>(t) * d;
+    const StepIn cur = p0;
+    p0 = p1;
+    p1 = load_step(z, r, n, hp, grad, at - 2 * static_cast<size_t>(d), live && t - 2 >= sp.t0);
+    const float zt = cur.z, rt = cur.r, nt = cur.n, ht = cur.hp, g = cur.x;
     const float mu = g + nu;
     const float dz = mu * (nt - ht) * zt * (1.f - zt);
     const float dn = mu * zt * (1.f - nt * nt);
