@@ -295,3 +295,37 @@ def test_block_table_needs_fused():
         with torch.no_grad():
             newton_apply(cell, x, _cfg(2, 1), h0=pool,
                          block_table=torch.tensor([0, 2], dtype=torch.int32, device=DEV))
+
+
+def test_fp16_packed_stream_with_early_stop():
+    """fp16 storage, a packed stream with per-sequence h0, and the residual-gated
+    early stop: the count and the result agree with the fixed-K eager loop at
+    that count, and each sequence stays close to being solved alone."""
+    from pararnn_amd import NewtonStats, ParaSLSTM, newton_apply
+
+    print("case eager fp16 packed early stop", flush=True)
+    torch.manual_seed(8)
+    lengths = [100, 1, 260, 33]
+    cs = torch.tensor([0] + lengths).cumsum(0).to(torch.int32).to(DEV)
+    d = 70
+    cell = ParaSLSTM(6, d).to(DEV, torch.float16)
+    x = torch.randn(1, int(cs[-1]), 6, device=DEV).to(torch.float16)
+    h0 = torch.randn(len(lengths), 4, d, device=DEV) * 0.5
+    h0[:, 1] = h0[:, 1].abs() + 0.5
+    h0 = h0.to(torch.float16)
+    st = NewtonStats()
+    with torch.no_grad():
+        # zero-hidden guess (P = 0), so the stop takes a few iterations
+        out = newton_apply(cell, x, _cfg(8, 0, residual_atol=5e-2), h0=h0, cu_seqlens=cs,
+                           stats=st)
+        same = newton_apply(cell, x, _cfg(st.iters - 1, 0), h0=h0, cu_seqlens=cs)
+        alone = torch.cat([newton_apply(cell, x[:, a:b], _cfg(st.iters - 1, 0), h0=h0[s:s + 1])
+                           for s, (a, b) in enumerate(zip(cs[:-1].tolist(), cs[1:].tolist()))],
+                          dim=1)
+    print(f"  iters {st.iters}, history {['%.1e' % v for v in st.residual_history]}", flush=True)
+    assert st.iters >= 2 and len(st.residual_history) == st.iters
+    assert st.residual_history[-1] < 5e-2 <= min(st.residual_history[:-1])
+    d_same = ((out.float() - same.float()).norm() / same.float().norm()).item()
+    d_alone = ((out.float() - alone.float()).norm() / alone.float().norm()).item()
+    print(f"  vs fixed K: {d_same:.2e}; vs each sequence alone: {d_alone:.2e}", flush=True)
+    assert d_same <= 1e-3 and d_alone <= 1e-2

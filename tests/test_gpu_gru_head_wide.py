@@ -218,3 +218,29 @@ def test_wider_than_128_is_refused():
     with pytest.raises(TypeError, match="128"):
         with torch.no_grad():
             newton_apply(cell, torch.randn(1, 5, 4, device=DEV), _cfg(2))
+
+
+def test_stacked_layers_and_verify_agreement():
+    """A two-layer ParaRNN of wide heads: train() (Newton per layer) against
+    eval() (sequential unroll per layer), and verify_agreement's verdict at
+    its default tolerance."""
+    from pararnn_amd import NewtonConfig, ParaGRU, ParaRNN, verify_agreement
+
+    print("case wide heads ParaRNN 2 layers", flush=True)
+    torch.manual_seed(3)
+    cell = ParaGRU(16, 192, mix="head", n_heads=2)
+    cfg = NewtonConfig(max_iters=6, residual_atol=None, residual_fail=None)
+    model = ParaRNN(cell, num_layers=2, config=cfg).to(DEV)
+    x = torch.randn(2, 300, 16, device=DEV)
+    with torch.no_grad():
+        model.train()
+        y = model(x)
+        model.eval()
+        ys = model(x)
+    err = (y - ys).abs().max().item()
+    print(f"  max|train - eval| {err:.2e}", flush=True)
+    assert err <= 1e-5
+    rep = verify_agreement(cell.to(DEV), torch.randn(2, 300, 16, device=DEV),
+                           config=NewtonConfig(max_iters=6))
+    print(f"  verify_agreement max_abs {rep.max_abs:.2e} ok={rep.ok}", flush=True)
+    assert rep.ok
