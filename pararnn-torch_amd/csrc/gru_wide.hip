@@ -14,11 +14,14 @@
 // cells/para_gru.py:385-412), three 128-wide mat-vecs.
 //
 // Workgroup: 512 lanes = 128 channels x 4 quarters of the contraction index.
-// Lane (c, q) keeps 32 entries of each A in registers -- column c (forward:
-// A^T products) or row c (adjoint: A products) over k in [32 q, 32 q + 32) --
-// and the quarters' partial sums meet in LDS in a fixed order (the result
-// does not depend on scheduling).  fp32 throughout; lanes c >= d_head and
-// entries k >= d_head hold zeros.
+// Lane l of wave w is channel c = 16 w + l % 16, quarter q = l / 16: it keeps
+// 32 entries of each A in registers -- column c (forward: A^T products) or
+// row c (adjoint: A products) over k in [32 q, 32 q + 32) -- and the four
+// quarters of a channel sit in one wave, so their partial sums meet through
+// two butterfly shuffles, every quarter holding the same sum.  A step then
+// needs LDS and a barrier only to broadcast the two vectors the next
+// products read: two barriers per step.  fp32 throughout; lanes c >= d_head
+// and entries k >= d_head hold zeros.
 #include "prnn_common.h"
 #include "pararnn_amd.h"
 #include "prnn_host.h"
@@ -59,40 +62,72 @@ __device__ __forceinline__ void load_quarter(const TX* A, int dh, int c, int q, 
   }
 }
 
-// One step's per-channel inputs, loaded two steps ahead of their use: a walk
-// step is short, so a load issued at the step that needs it would wait for
-// the full memory latency every step.
-struct StepIn {
-  float z, r, n, hp, x;  // x: the iterate (forward) or dL/dH (adjoint)
+// A step's per-channel inputs (z, r, n, the previous state, and the iterate
+// or dL/dH) are staged through LDS kS steps at a time: while a block of kS
+// steps is walked from LDS, every lane holds its share of the next block's
+// loads in registers and writes them to the other LDS buffer at the end of
+// the block.  A walk step is short, so loads issued per step would expose
+// the memory latency every step; here it overlaps kS steps of work.
+constexpr int kS = 16;                     // steps per staged block
+constexpr int kIn = 5;                     // inputs per step and channel
+constexpr int kPer = kIn * kS * DW / kThreads;  // staged values per lane (20)
+
+struct Staged {
+  float v[kPer];
 };
 
+// Lane `tid` loads values j = 0 .. kPer-1 of the block whose steps are
+// t_first + dir * s (s < kS): input j / 4, step s = tid / DW + 4 (j % 4),
+// channel tid % DW (clamped into the head and the sequence: the values
+// outside are never used).
 template <typename TG>
-__device__ __forceinline__ StepIn load_step(const float* __restrict__ z, const float* __restrict__ r,
-                                            const float* __restrict__ n,
-                                            const float* __restrict__ hp, const TG* __restrict__ x,
-                                            size_t at, bool ok) {
-  StepIn v{0.f, 0.f, 0.f, 0.f, 0.f};
-  if (ok) {
-    v.z = z[at];
-    v.r = r[at];
-    v.n = n[at];
-    v.hp = hp[at];
-    v.x = ld(x + at);
+__device__ __forceinline__ Staged load_block(const float* __restrict__ z,
+                                             const float* __restrict__ r,
+                                             const float* __restrict__ n,
+                                             const float* __restrict__ hp,
+                                             const TG* __restrict__ x, size_t row_base, int d,
+                                             int head, int dh, int t_first, int dir, int t_lo,
+                                             int t_hi) {
+  const int cc = min(static_cast<int>(threadIdx.x) & (DW - 1), dh - 1);
+  const size_t colb = row_base + static_cast<size_t>(head) * dh + cc;
+  Staged st;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int s = static_cast<int>(threadIdx.x) / DW + 4 * (j % 4);
+    const int t = min(max(t_first + dir * s, t_lo), t_hi);
+    const size_t at = colb + static_cast<size_t>(t) * d;
+    const int a = j / 4;
+    st.v[j] = a == 0 ? z[at] : a == 1 ? r[at] : a == 2 ? n[at] : a == 3 ? hp[at] : ld(x + at);
   }
-  return v;
+  return st;
 }
 
-__device__ __forceinline__ float dot_quarter(const float a[kK], const float* __restrict__ v) {
-  float acc = 0.f;
+__device__ __forceinline__ void store_block(float (*buf)[kS][DW], const Staged& st, int dh) {
+  const int cc = static_cast<int>(threadIdx.x) & (DW - 1);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int s = static_cast<int>(threadIdx.x) / DW + 4 * (j % 4);
+    buf[j / 4][s][cc] = cc < dh ? st.v[j] : 0.f;  // dead channels read zeros
+  }
+}
+
+// sum_k a[k] v[k] over this lane's quarter, four independent chains (a long
+// dependent FMA chain would set the step's latency), then over the channel's
+// four quarters (lanes l, l ^ 16, l ^ 32, l ^ 48 of the wave).
+__device__ __forceinline__ float dot_channel(const float a[kK], const float* __restrict__ v) {
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int kk = 0; kk < kK; kk += 4) {
     const float4 x = *reinterpret_cast<const float4*>(v + kk);
-    acc = fmaf(a[kk], x.x, acc);
-    acc = fmaf(a[kk + 1], x.y, acc);
-    acc = fmaf(a[kk + 2], x.z, acc);
-    acc = fmaf(a[kk + 3], x.w, acc);
+    acc[0] = fmaf(a[kk], x.x, acc[0]);
+    acc[1] = fmaf(a[kk + 1], x.y, acc[1]);
+    acc[2] = fmaf(a[kk + 2], x.z, acc[2]);
+    acc[3] = fmaf(a[kk + 3], x.w, acc[3]);
   }
-  return acc;
+  float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  s += __shfl_xor(s, 16);
+  s += __shfl_xor(s, 32);
+  return s;
 }
 
 // Forward walk of one Newton iteration: delta_t = J_t delta_{t-1} + F_t with
@@ -109,8 +144,9 @@ __global__ __launch_bounds__(kThreads) void gruw_walk_kernel(
     int H, int dh, float omega, const int* __restrict__ cu) {
   __shared__ __attribute__((aligned(16))) float s_d[DW];
   __shared__ __attribute__((aligned(16))) float s_w[DW];
-  __shared__ float s_p[3][kQ][DW];
-  const int c = threadIdx.x & (DW - 1), q = threadIdx.x / DW;
+  __shared__ float s_in[2][kIn][kS][DW];
+  const int lane = threadIdx.x & 63;
+  const int c = (threadIdx.x >> 6) * 16 + (lane & 15), q = lane >> 4;
   const int head = blockIdx.x % H;
   const Span sp = span_of(blockIdx.x / H, T, cu);
   const size_t hoff = static_cast<size_t>(head) * dh * dh;
@@ -123,41 +159,47 @@ __global__ __launch_bounds__(kThreads) void gruw_walk_kernel(
   const size_t col = static_cast<size_t>(head) * dh + c;
   if (q == 0) s_d[c] = 0.f;
   float delta = 0.f;
+  if (sp.t0 >= sp.t1) return;
+  const size_t row_base = static_cast<size_t>(sp.row) * T * d;
+  const rsrc_t ro = make_rsrc(out + row_base,
+                              static_cast<uint32_t>(static_cast<size_t>(T) * d * sizeof(TOUT)));
+  const uint32_t vo = (live && q == 0) ? static_cast<uint32_t>(col * sizeof(TOUT)) : kOOB;
+  store_block(s_in[0], load_block(z, r, n, hp, hin, row_base, d, head, dh, sp.t0, 1, sp.t0,
+                                  sp.t1 - 1), dh);
   __syncthreads();
-  const size_t base = static_cast<size_t>(sp.row) * T * d + col;
-  StepIn p0 = load_step(z, r, n, hp, hin, base + static_cast<size_t>(sp.t0) * d,
-                        live && sp.t0 < sp.t1);
-  StepIn p1 = load_step(z, r, n, hp, hin, base + static_cast<size_t>(sp.t0 + 1) * d,
-                        live && sp.t0 + 1 < sp.t1);
-  for (int t = sp.t0; t < sp.t1; ++t) {
-    const size_t at = base + static_cast<size_t>(t) * d;
-    const StepIn cur = p0;
-    p0 = p1;
-    p1 = load_step(z, r, n, hp, hin, at + 2 * static_cast<size_t>(d), live && t + 2 < sp.t1);
-    const float zt = cur.z, rt = cur.r, nt = cur.n, ht = cur.hp, hv = cur.x;
-    // stage 1: A_r^T delta and A_z^T delta, this quarter of k
-    s_p[0][q][c] = dot_quarter(ar, s_d + q * kK);
-    s_p[1][q][c] = dot_quarter(az, s_d + q * kK);
-    __syncthreads();
-    const float sr = ((s_p[0][0][c] + s_p[0][1][c]) + s_p[0][2][c]) + s_p[0][3][c];
-    const float sz = ((s_p[1][0][c] + s_p[1][1][c]) + s_p[1][2][c]) + s_p[1][3][c];
-    const float d5 = ht * rt * (1.f - rt);
-    if (q == 0) s_w[c] = rt * delta + d5 * sr;
-    __syncthreads();
-    // stage 2: A_n^T (r delta + d5 A_r^T delta)
-    s_p[2][q][c] = dot_quarter(an, s_w + q * kK);
-    __syncthreads();
-    const float sn = ((s_p[2][0][c] + s_p[2][1][c]) + s_p[2][2][c]) + s_p[2][3][c];
-    const float d2 = (nt - ht) * zt * (1.f - zt);
-    const float d3 = zt * (1.f - nt * nt);
-    const float f = lerp_t(ht, nt, zt) - hv;
-    delta = (1.f - zt) * delta + d2 * sz + d3 * sn + f;
-    if (!live) delta = 0.f;
-    if (q == 0) {
-      s_d[c] = delta;
-      if (live) st(out + at, hv + omega * delta);
+  int buf = 0;
+  for (int tb = sp.t0; tb < sp.t1; tb += kS) {
+    const bool more = tb + kS < sp.t1;
+    Staged next;
+    if (more)
+      next = load_block(z, r, n, hp, hin, row_base, d, head, dh, tb + kS, 1, sp.t0, sp.t1 - 1);
+    const int ns = min(kS, sp.t1 - tb);
+    for (int s = 0; s < ns; ++s) {
+      const int t = tb + s;
+      const float zt = s_in[buf][0][s][c], rt = s_in[buf][1][s][c], nt = s_in[buf][2][s][c];
+      const float ht = s_in[buf][3][s][c], hv = s_in[buf][4][s][c];
+      // A_r^T delta and A_z^T delta (delta_{t-1} broadcast in s_d)
+      const float sr = dot_channel(ar, s_d + q * kK);
+      const float sz = dot_channel(az, s_d + q * kK);
+      const float d5 = ht * rt * (1.f - rt);
+      if (q == 0) s_w[c] = rt * delta + d5 * sr;
+      __syncthreads();
+      // A_n^T (r delta + d5 A_r^T delta)
+      const float sn = dot_channel(an, s_w + q * kK);
+      const float d2 = (nt - ht) * zt * (1.f - zt);
+      const float d3 = zt * (1.f - nt * nt);
+      const float f = lerp_t(ht, nt, zt) - hv;
+      delta = (1.f - zt) * delta + d2 * sz + d3 * sn + f;
+      if (q == 0) s_d[c] = delta;
+      // a buffer store, dropped for lanes with the out-of-range offset
+      stb<TOUT>(ro, vo, static_cast<uint32_t>(t) * (d * sizeof(TOUT)), hv + omega * delta);
+      __syncthreads();
     }
-    __syncthreads();
+    if (more) {
+      store_block(s_in[buf ^ 1], next, dh);
+      __syncthreads();
+    }
+    buf ^= 1;
   }
 }
 
@@ -177,8 +219,9 @@ __global__ __launch_bounds__(kThreads) void gruw_reverse_kernel(
   __shared__ __attribute__((aligned(16))) float s_dz[DW];
   __shared__ __attribute__((aligned(16))) float s_dn[DW];
   __shared__ __attribute__((aligned(16))) float s_dr[DW];
-  __shared__ float s_p[3][kQ][DW];
-  const int c = threadIdx.x & (DW - 1), q = threadIdx.x / DW;
+  __shared__ float s_in[2][kIn][kS][DW];
+  const int lane = threadIdx.x & 63;
+  const int c = (threadIdx.x >> 6) * 16 + (lane & 15), q = lane >> 4;
   const int head = blockIdx.x % H;
   const Span sp = span_of(blockIdx.x / H, T, cu);
   const size_t hoff = static_cast<size_t>(head) * dh * dh;
@@ -190,45 +233,56 @@ __global__ __launch_bounds__(kThreads) void gruw_reverse_kernel(
   const bool live = c < dh;
   const size_t col = static_cast<size_t>(head) * dh + c;
   float nu = 0.f;
-  const size_t base = static_cast<size_t>(sp.row) * T * d + col;
-  StepIn p0 = load_step(z, r, n, hp, grad, base + static_cast<size_t>(sp.t1 - 1) * d,
-                        live && sp.t1 - 1 >= sp.t0);
-  StepIn p1 = load_step(z, r, n, hp, grad, base + static_cast<size_t>(sp.t1 - 2) * d,
-                        live && sp.t1 - 2 >= sp.t0);
-  for (int t = sp.t1 - 1; t >= sp.t0; --t) {
-    const size_t at = base + static_cast<size_t>(t) * d;
-    const StepIn cur = p0;
-    p0 = p1;
-    p1 = load_step(z, r, n, hp, grad, at - 2 * static_cast<size_t>(d), live && t - 2 >= sp.t0);
-    const float zt = cur.z, rt = cur.r, nt = cur.n, ht = cur.hp, g = cur.x;
-    const float mu = g + nu;
-    const float dz = mu * (nt - ht) * zt * (1.f - zt);
-    const float dn = mu * zt * (1.f - nt * nt);
-    if (q == 0) {
-      s_dz[c] = dz;
-      s_dn[c] = dn;
+  if (sp.t0 >= sp.t1) return;
+  const size_t row_base = static_cast<size_t>(sp.row) * T * d;
+  const rsrc_t rg = make_rsrc(g_wx + row_base * 3,
+                              static_cast<uint32_t>(static_cast<size_t>(T) * 3 * d * sizeof(float)));
+  const uint32_t vg = (live && q == 0) ? static_cast<uint32_t>(col * sizeof(float)) : kOOB;
+  store_block(s_in[0], load_block(z, r, n, hp, grad, row_base, d, head, dh, sp.t1 - 1, -1,
+                                  sp.t0, sp.t1 - 1), dh);
+  __syncthreads();
+  int buf = 0;
+  for (int tb = sp.t1 - 1; tb >= sp.t0; tb -= kS) {
+    const bool more = tb - kS >= sp.t0;
+    Staged next;
+    if (more)
+      next = load_block(z, r, n, hp, grad, row_base, d, head, dh, tb - kS, -1, sp.t0, sp.t1 - 1);
+    const int ns = min(kS, tb - sp.t0 + 1);
+    for (int s = 0; s < ns; ++s) {
+      const int t = tb - s;
+      const float zt = s_in[buf][0][s][c], rt = s_in[buf][1][s][c], nt = s_in[buf][2][s][c];
+      const float ht = s_in[buf][3][s][c], g = s_in[buf][4][s][c];
+      const float mu = g + nu;
+      const float dz = mu * (nt - ht) * zt * (1.f - zt);
+      const float dn = mu * zt * (1.f - nt * nt);
+      if (q == 0) {
+        s_dz[c] = dz;
+        s_dn[c] = dn;
+      }
+      __syncthreads();
+      const float du = dot_channel(an, s_dn + q * kK);
+      const float azdz = dot_channel(az, s_dz + q * kK);
+      const float dr = du * ht * rt * (1.f - rt);
+      if (q == 0) s_dr[c] = dr;
+      __syncthreads();
+      const float ardr = dot_channel(ar, s_dr + q * kK);
+      nu = (1.f - zt) * mu + azdz + rt * du + ardr;
+      // buffer stores, dropped for the other lanes
+      const uint32_t so = static_cast<uint32_t>(t) * (3 * d * sizeof(float));
+      stb<float>(rg, vg, so, dz);
+      stb<float>(rg, vg, so + d * sizeof(float), dr);
+      stb<float>(rg, vg, so + 2 * d * sizeof(float), dn);
     }
-    __syncthreads();
-    s_p[0][q][c] = dot_quarter(an, s_dn + q * kK);
-    s_p[1][q][c] = dot_quarter(az, s_dz + q * kK);
-    __syncthreads();
-    const float du = ((s_p[0][0][c] + s_p[0][1][c]) + s_p[0][2][c]) + s_p[0][3][c];
-    const float azdz = ((s_p[1][0][c] + s_p[1][1][c]) + s_p[1][2][c]) + s_p[1][3][c];
-    const float dr = du * ht * rt * (1.f - rt);
-    if (q == 0) s_dr[c] = dr;
-    __syncthreads();
-    s_p[2][q][c] = dot_quarter(ar, s_dr + q * kK);
-    __syncthreads();
-    const float ardr = ((s_p[2][0][c] + s_p[2][1][c]) + s_p[2][2][c]) + s_p[2][3][c];
-    nu = (1.f - zt) * mu + azdz + rt * du + ardr;
-    if (q == 0 && live) {
-      float* gw = g_wx + (static_cast<size_t>(sp.row) * T + t) * 3 * d + col;
-      gw[0] = dz;
-      gw[d] = dr;
-      gw[2 * static_cast<size_t>(d)] = dn;
-      if (t == sp.t0 && g_h0 != nullptr) g_h0[static_cast<size_t>(sp.seq) * d + col] = nu;
+    // (the other staging buffer was last read a block ago, before this
+    // block's barriers)
+    if (more) {
+      store_block(s_in[buf ^ 1], next, dh);
+      __syncthreads();
     }
+    buf ^= 1;
   }
+  // nu at the sequence's first step: dL/dh0 of its row
+  if (q == 0 && live && g_h0 != nullptr) g_h0[static_cast<size_t>(sp.seq) * d + col] = nu;
 }
 
 static int check(int B, int T, int H, int dh, int dtype, const int* cu, int n_seq) {
@@ -236,6 +290,9 @@ static int check(int B, int T, int H, int dh, int dtype, const int* cu, int n_se
     return fail(PRNN_ERR_VALUE, "B, T, n_heads must be >= 1, got B=%d T=%d n_heads=%d", B, T, H);
   if (dh < 1 || dh > DW) return fail(PRNN_ERR_TYPE, "d_head must be in [1, %d], got %d", DW, dh);
   if (check_dtype(dtype) != PRNN_OK) return PRNN_ERR_TYPE;
+  // one batch row's outputs are addressed with 32-bit buffer offsets
+  if (static_cast<long long>(T) * 3 * H * dh * sizeof(float) >= (1ll << 32))
+    return fail(PRNN_ERR_VALUE, "a batch row of T * 3 * d fp32 values must stay below 4 GiB");
   if (cu != nullptr && (B != 1 || n_seq < 1 || n_seq > T))
     return fail(PRNN_ERR_VALUE, "a packed stream has B = 1 and n_seq in [1, T], got B=%d n_seq=%d",
                 B, n_seq);
