@@ -14,11 +14,11 @@
 // cells/para_gru.py:385-412), three 128-wide mat-vecs.
 //
 // Workgroup: 512 lanes = 128 channels x 4 quarters of the contraction index.
-// Lane l of wave w is channel c = 16 w + l % 16, quarter q = l / 16: it keeps
+// Lane l of wave w is channel c = 16 w + l / 4, quarter q = l % 4: it keeps
 // 32 entries of each A in registers -- column c (forward: A^T products) or
 // row c (adjoint: A products) over k in [32 q, 32 q + 32) -- and the four
-// quarters of a channel sit in one wave, so their partial sums meet through
-// two butterfly shuffles, every quarter holding the same sum.  A step then
+// quarters of a channel are one quad of lanes, so their partial sums meet
+// through two DPP moves, every quarter holding the same sum.  A step then
 // needs LDS and a barrier only to broadcast the two vectors the next
 // products read: two barriers per step.  fp32 throughout; lanes c >= d_head
 // and entries k >= d_head hold zeros.
@@ -33,6 +33,11 @@ constexpr int DW = 128;       // widest head
 constexpr int kQ = 4;         // quarters of the contraction index
 constexpr int kK = DW / kQ;   // entries per lane and matrix
 constexpr int kThreads = DW * kQ;
+// A broadcast vector sits in LDS as kQ segments of kK entries, each padded
+// to kP so that the four segments a quad reads at once start in different
+// banks.
+constexpr int kP = kK + 4;
+__device__ __forceinline__ int slot(int c) { return (c / kK) * kP + c % kK; }
 
 // torch.lerp(start, end, weight) for fp32 (the cell's update).
 __device__ __forceinline__ float lerp_t(float s, float e, float w) {
@@ -113,7 +118,7 @@ __device__ __forceinline__ void store_block(float (*buf)[kS][DW], const Staged& 
 
 // sum_k a[k] v[k] over this lane's quarter, four independent chains (a long
 // dependent FMA chain would set the step's latency), then over the channel's
-// four quarters (lanes l, l ^ 16, l ^ 32, l ^ 48 of the wave).
+// four quarters (the lanes of a quad).
 __device__ __forceinline__ float dot_channel(const float a[kK], const float* __restrict__ v) {
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -125,8 +130,11 @@ __device__ __forceinline__ float dot_channel(const float a[kK], const float* __r
     acc[3] = fmaf(a[kk + 3], x.w, acc[3]);
   }
   float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-  s += __shfl_xor(s, 16);
-  s += __shfl_xor(s, 32);
+  // quad_perm [1,0,3,2] then [2,3,0,1]: row-local DPP moves
+  s += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, s), 0xB1, 0xF,
+                                                          0xF, false));
+  s += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, s), 0x4E, 0xF,
+                                                          0xF, false));
   return s;
 }
 
@@ -142,11 +150,12 @@ __global__ __launch_bounds__(kThreads) void gruw_walk_kernel(
     const float* __restrict__ hp, const float* __restrict__ hin, const TX* __restrict__ a_z,
     const TX* __restrict__ a_r, const TX* __restrict__ a_n, TOUT* __restrict__ out, int T,
     int H, int dh, float omega, const int* __restrict__ cu) {
-  __shared__ __attribute__((aligned(16))) float s_d[DW];
-  __shared__ __attribute__((aligned(16))) float s_w[DW];
+  __shared__ __attribute__((aligned(16))) float s_d[kQ * kP];
+  __shared__ __attribute__((aligned(16))) float s_w[kQ * kP];
   __shared__ float s_in[2][kIn][kS][DW];
   const int lane = threadIdx.x & 63;
-  const int c = (threadIdx.x >> 6) * 16 + (lane & 15), q = lane >> 4;
+  const int c = (threadIdx.x >> 6) * 16 + (lane >> 2), q = lane & 3;
+  const int sc = slot(c);
   const int head = blockIdx.x % H;
   const Span sp = span_of(blockIdx.x / H, T, cu);
   const size_t hoff = static_cast<size_t>(head) * dh * dh;
@@ -157,7 +166,7 @@ __global__ __launch_bounds__(kThreads) void gruw_walk_kernel(
   const int d = H * dh;
   const bool live = c < dh;
   const size_t col = static_cast<size_t>(head) * dh + c;
-  if (q == 0) s_d[c] = 0.f;
+  if (q == 0) s_d[sc] = 0.f;
   float delta = 0.f;
   if (sp.t0 >= sp.t1) return;
   const size_t row_base = static_cast<size_t>(sp.row) * T * d;
@@ -179,18 +188,18 @@ __global__ __launch_bounds__(kThreads) void gruw_walk_kernel(
       const float zt = s_in[buf][0][s][c], rt = s_in[buf][1][s][c], nt = s_in[buf][2][s][c];
       const float ht = s_in[buf][3][s][c], hv = s_in[buf][4][s][c];
       // A_r^T delta and A_z^T delta (delta_{t-1} broadcast in s_d)
-      const float sr = dot_channel(ar, s_d + q * kK);
-      const float sz = dot_channel(az, s_d + q * kK);
+      const float sr = dot_channel(ar, s_d + q * kP);
+      const float sz = dot_channel(az, s_d + q * kP);
       const float d5 = ht * rt * (1.f - rt);
-      if (q == 0) s_w[c] = rt * delta + d5 * sr;
+      if (q == 0) s_w[sc] = rt * delta + d5 * sr;
       __syncthreads();
       // A_n^T (r delta + d5 A_r^T delta)
-      const float sn = dot_channel(an, s_w + q * kK);
+      const float sn = dot_channel(an, s_w + q * kP);
       const float d2 = (nt - ht) * zt * (1.f - zt);
       const float d3 = zt * (1.f - nt * nt);
       const float f = lerp_t(ht, nt, zt) - hv;
       delta = (1.f - zt) * delta + d2 * sz + d3 * sn + f;
-      if (q == 0) s_d[c] = delta;
+      if (q == 0) s_d[sc] = delta;
       // a buffer store, dropped for lanes with the out-of-range offset
       stb<TOUT>(ro, vo, static_cast<uint32_t>(t) * (d * sizeof(TOUT)), hv + omega * delta);
       __syncthreads();
@@ -216,12 +225,13 @@ __global__ __launch_bounds__(kThreads) void gruw_reverse_kernel(
     const float* __restrict__ hp, const TG* __restrict__ grad, const TX* __restrict__ a_z,
     const TX* __restrict__ a_r, const TX* __restrict__ a_n, float* __restrict__ g_wx,
     float* __restrict__ g_h0, int T, int H, int dh, const int* __restrict__ cu) {
-  __shared__ __attribute__((aligned(16))) float s_dz[DW];
-  __shared__ __attribute__((aligned(16))) float s_dn[DW];
-  __shared__ __attribute__((aligned(16))) float s_dr[DW];
+  __shared__ __attribute__((aligned(16))) float s_dz[kQ * kP];
+  __shared__ __attribute__((aligned(16))) float s_dn[kQ * kP];
+  __shared__ __attribute__((aligned(16))) float s_dr[kQ * kP];
   __shared__ float s_in[2][kIn][kS][DW];
   const int lane = threadIdx.x & 63;
-  const int c = (threadIdx.x >> 6) * 16 + (lane & 15), q = lane >> 4;
+  const int c = (threadIdx.x >> 6) * 16 + (lane >> 2), q = lane & 3;
+  const int sc = slot(c);
   const int head = blockIdx.x % H;
   const Span sp = span_of(blockIdx.x / H, T, cu);
   const size_t hoff = static_cast<size_t>(head) * dh * dh;
@@ -256,16 +266,16 @@ __global__ __launch_bounds__(kThreads) void gruw_reverse_kernel(
       const float dz = mu * (nt - ht) * zt * (1.f - zt);
       const float dn = mu * zt * (1.f - nt * nt);
       if (q == 0) {
-        s_dz[c] = dz;
-        s_dn[c] = dn;
+        s_dz[sc] = dz;
+        s_dn[sc] = dn;
       }
       __syncthreads();
-      const float du = dot_channel(an, s_dn + q * kK);
-      const float azdz = dot_channel(az, s_dz + q * kK);
+      const float du = dot_channel(an, s_dn + q * kP);
+      const float azdz = dot_channel(az, s_dz + q * kP);
       const float dr = du * ht * rt * (1.f - rt);
-      if (q == 0) s_dr[c] = dr;
+      if (q == 0) s_dr[sc] = dr;
       __syncthreads();
-      const float ardr = dot_channel(ar, s_dr + q * kK);
+      const float ardr = dot_channel(ar, s_dr + q * kP);
       nu = (1.f - zt) * mu + azdz + rt * du + ardr;
       // buffer stores, dropped for the other lanes
       const uint32_t so = static_cast<uint32_t>(t) * (3 * d * sizeof(float));
