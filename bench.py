@@ -9,10 +9,21 @@ after a small clear of its status words.
 The W_x GEMM and the end-to-end ``newton_apply`` (GEMM + solve) are timed
 separately and reported as extra fields, as are BASELINE config 2 (the same
 step at B=8, T=16384, ``slstm_cfg2``), config 5 (one training step: forward
-solve + eq. 2.6 backward, ``train_cfg5``) and config 4 (head GRU forward,
-backward and training step, ``head_cfg4``).
+solve + eq. 2.6 backward, ``train_cfg5``), config 4 (head GRU forward,
+backward and training step, ``head_cfg4``), packed ``cu_seqlens`` streams
+(``ragged``), T=1 decode (``decode_t1``), ``scan_backend='eager'`` at config 2
+(``eager_cfg2``) and heads with d_head=128 (``head_wide``).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Timing: W untimed warmup steps, then K steps each bracketed by HIP events on
+the launch stream (synchronised before and after the timed region); ``value``
+and ``ms_per_step`` use the fastest step, ``ms_per_step_mean`` the mean.
+``roofline`` / ``roofline_init`` give, per launch, the algorithmic-model
+fraction, the compulsory-byte fraction and the counter-traffic fraction (the
+traffic from the committed rocprofv3 summaries); ``pinned_solve`` reports the
+residual and non-finite fractions of the solve that is timed.
+``cpu_baseline`` times the oracle (the CPU restatement) on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra ...]
 Prints one JSON line.
 """
 
