@@ -181,9 +181,17 @@ static NewtonWs carve_newton(void* base, int B, int T, int d, int K, int dtype, 
   if (w.fused) {
     // Iteration-indexed look-back words (a tile may run iterations ahead of
     // the tiles that still read its earlier ones), cleared with the counters.
-    const Geo g = geometry(B, T, d,
-                           !packed ? newton_fused_shape(dtype)
-                           : narrow(dtype) ? kNewtonFusedPacked : kNewtonFusedPackedF32);
+    Geo g = geometry(B, T, d,
+                     !packed ? newton_fused_shape(dtype)
+                     : narrow(dtype) ? kNewtonFusedPacked : kNewtonFusedPackedF32);
+    if (K == 1) {
+      // a one-iteration workspace also serves the eager launch, whose tiles
+      // may be shorter (more of them)
+      const Geo ge = geometry(B, T, d,
+                              !packed ? (narrow(dtype) ? kNewtonEager : kNewtonEagerF32)
+                              : narrow(dtype) ? kNewtonEagerPacked : kNewtonEagerPackedF32);
+      if (ge.n_tiles > g.n_tiles) g = ge;
+    }
     w.lb = carve_lookback(cv, g, 4 * K, 20 * K);
     w.hlast = static_cast<unsigned long long*>(
         cv.take(sizeof(unsigned long long) * static_cast<size_t>(K - 1) * 4 * kCB * g.n_tiles));
@@ -200,6 +208,10 @@ static NewtonWs carve_newton(void* base, int B, int T, int d, int K, int dtype, 
   Geo g = g1.n_tiles >= g2.n_tiles ? g1 : g2;
   if (g3.n_tiles > g.n_tiles) g = g3;
   if (g4.n_tiles > g.n_tiles) g = g4;
+  if (K == 1) {
+    const Geo ge = geometry(B, T, d, narrow(dtype) ? kNewtonEager : kNewtonEagerF32);
+    if (ge.n_tiles > g.n_tiles) g = ge;
+  }
   w.lb = carve_lookback(cv, g, 4, 20);
   const size_t wb = static_cast<size_t>(B) * T * 4 * d * sizeof(float);
   w.work[0] = K >= 2 ? static_cast<float*>(cv.take(wb)) : nullptr;

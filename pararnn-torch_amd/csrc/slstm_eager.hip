@@ -11,11 +11,10 @@ using namespace prnn;
 namespace prnn {
 namespace slstm {
 
-// Tile shapes: those of the per-iteration kernel for the same storage.
 template <typename TX, bool PK>
 constexpr Shape eager_shape() {
-  if constexpr (PK) return sizeof(TX) == 4 ? kNewtonPackedF32 : kNewtonPackedGuess;
-  return sizeof(TX) == 4 ? kNewtonF32 : kNewtonGuessDefault;
+  if constexpr (PK) return sizeof(TX) == 4 ? kNewtonEagerPackedF32 : kNewtonEagerPacked;
+  return sizeof(TX) == 4 ? kNewtonEagerF32 : kNewtonEager;
 }
 
 template <typename TX, bool PK>

@@ -1367,6 +1367,17 @@ constexpr Shape kNewtonPackedGuess{16, 4};
 constexpr Shape kNewtonPackedWork{16, 4};
 constexpr Shape kNewtonPackedF32{8, 8};
 
+// scan_backend='eager' iterations (slstm_newton_kernel<EAGER>, one launch per
+// iteration): the op-by-op rounding keeps more values live per step than the
+// fused arithmetic, so 16-bit storage takes shorter tiles.  bf16 at d=1024,
+// B=8, T=16384: 12x4 (~170 VGPRs) runs an iteration in 3.0 ms against 4.6 ms
+// for 24x4 (291 VGPRs, one wave per SIMD); packed streams 8x4 (~228 VGPRs)
+// 3.9 ms against 4.6 ms for 16x4 (437 VGPRs).
+constexpr Shape kNewtonEager{12, 4};
+constexpr Shape kNewtonEagerF32{16, 8};
+constexpr Shape kNewtonEagerPacked{8, 4};
+constexpr Shape kNewtonEagerPackedF32{8, 8};
+
 // Packed-stream launches (B = 1, default shapes), compiled in their own
 // translation unit (slstm_packed.hip).
 template <typename TN>
