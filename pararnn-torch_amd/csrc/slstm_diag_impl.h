@@ -185,12 +185,18 @@ static NewtonWs carve_newton(void* base, int B, int T, int d, int K, int dtype, 
                      !packed ? newton_fused_shape(dtype)
                      : narrow(dtype) ? kNewtonFusedPacked : kNewtonFusedPackedF32);
     if (K == 1) {
-      // a one-iteration workspace also serves the eager launch, whose tiles
-      // may be shorter (more of them)
-      const Geo ge = geometry(B, T, d,
-                              !packed ? (narrow(dtype) ? kNewtonEager : kNewtonEagerF32)
-                              : narrow(dtype) ? kNewtonEagerPacked : kNewtonEagerPackedF32);
-      if (ge.n_tiles > g.n_tiles) g = ge;
+      // A one-iteration workspace also serves the single-iteration launches
+      // (the residual-gated step and the eager iteration), whose tiles may be
+      // shorter: size the words for the largest tile count.
+      const Shape one[3] = {
+          !packed ? newton_shape(dtype, false) : narrow(dtype) ? kNewtonPackedGuess : kNewtonPackedF32,
+          !packed ? newton_shape(dtype, true) : narrow(dtype) ? kNewtonPackedWork : kNewtonPackedF32,
+          !packed ? (narrow(dtype) ? kNewtonEager : kNewtonEagerF32)
+          : narrow(dtype) ? kNewtonEagerPacked : kNewtonEagerPackedF32};
+      for (const Shape& sh : one) {
+        const Geo gs = geometry(B, T, d, sh);
+        if (gs.n_tiles > g.n_tiles) g = gs;
+      }
     }
     w.lb = carve_lookback(cv, g, 4 * K, 20 * K);
     w.hlast = static_cast<unsigned long long*>(

@@ -117,3 +117,26 @@ def test_packed_entry_points_reject_bad_sequence_counts():
         rc = lib.prnn_gru_head_newton_packed(None, None, None, None, None, None, 10, 1, 64, 2,
                                              1.0, 0, cu, n_seq, None, None, 0, None)
         assert rc == _lib.PRNN_ERR_VALUE and b"n_seq" in lib.prnn_last_error()
+
+
+def test_one_iteration_workspace_covers_the_short_tiles():
+    """A max_iters = 1 workspace also serves the single-iteration launches (the
+    residual-gated step and the eager iteration), whose tiles can be shorter
+    than the fused launch's: its look-back words (4 inclusive + 20 aggregate
+    8-byte words per channel and tile) must cover the shortest 16-bit tiles of
+    those launches, 32 steps on packed streams (8 x 4 waves) and 48 steps on
+    rectangular batches (12 x 4)."""
+    from pararnn_amd import _lib
+
+    if not os.path.exists(_lib.lib_path()):
+        pytest.skip("library not built (run __graft_entry__.build())")
+    lib = _lib.load()
+    bf16 = 1
+
+    def words(T, d, steps):
+        return 24 * 8 * 64 * (-(-T // steps) * -(-d // 64))
+
+    for T, d in ((131072, 1024), (4099, 192), (64, 64)):
+        assert lib.prnn_slstm_newton_packed_workspace_size(T, d, 1, bf16) >= words(T, d, 32)
+        assert lib.prnn_slstm_newton_workspace_size(1, T, d, 1, bf16) >= words(T, d, 48)
+        assert lib.prnn_slstm_newton_workspace_size(4, T, d, 1, bf16) >= 4 * words(T, d, 48)
