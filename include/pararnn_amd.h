@@ -334,6 +334,27 @@ PRNN_API int prnn_gru_wide_reverse(const float* z, const float* r, const float* 
                                    int d_head, int dtype, const int* cu_seqlens, int n_seq,
                                    void* stream);
 
+/* All max_iters Newton iterations of the wide tier in one launch, without the
+ * host's gate GEMMs: iteration k's workgroup per (sequence, head) evaluates
+ * the gates at the previous iterate inside its walk and runs a block or two
+ * of steps behind iteration k - 1, whose iterate it reads from the workspace
+ * as tagged words (same replaced reference tier as above; its program per
+ * (b, head) runs the iterations one after another).  wx (B, T, 3d) and A_*
+ * in `dtype`; h0 (rows, d) fp32 or NULL; guess (B, T, d) fp32, the initial
+ * iterate; out (B, T, d) in `dtype` receives the last iterate and must not
+ * alias guess.  Workspace: prnn_gru_wide_newton_workspace_size; tag_base as
+ * for the sLSTM _ex calls (0: the call clears the whole workspace), and the
+ * status word of a wait that gave up reads with prnn_slstm_lookback_status.
+ * max_iters in [1, PRNN_TAG_SPAN]. */
+PRNN_API size_t prnn_gru_wide_newton_workspace_size(int B, int T, int n_heads, int d_head,
+                                                    int max_iters);
+PRNN_API int prnn_gru_wide_newton(const void* wx, const void* a_z, const void* a_r,
+                                  const void* a_n, const float* h0, const float* guess,
+                                  void* out, int B, int T, int n_heads, int d_head,
+                                  int max_iters, float omega, int dtype, const int* cu_seqlens,
+                                  int n_seq, void* workspace, size_t workspace_bytes,
+                                  int tag_base, void* stream);
+
 /* Head GRU on a packed stream: wx (1, T, 3d) holds n_seq sequences, sequence
  * q on steps [cu_seqlens[q], cu_seqlens[q+1]) (int32 device array, n_seq + 1
  * entries, 0 = cu_seqlens[0] < ... < cu_seqlens[n_seq] = T).  At a sequence's

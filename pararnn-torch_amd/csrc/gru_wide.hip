@@ -295,6 +295,231 @@ __global__ __launch_bounds__(kThreads) void gruw_reverse_kernel(
   if (q == 0 && live && g_h0 != nullptr) g_h0[static_cast<size_t>(sp.seq) * d + col] = nu;
 }
 
+// ---------------------------------------------------------------------------
+// All K Newton iterations in one launch.  Iteration k's walk needs only the
+// previous iterate H_{k-1} at steps t-1 and t, so the K walks of a (sequence,
+// head) run together, iteration k a block or two of steps behind iteration
+// k - 1: K x (sequences x heads) workgroups, each evaluating its own gates at
+// H_{k-1} inside the walk (h A_z, h A_r and (h r) A_n beside the three
+// Jacobian products) instead of as GEMMs between launches.
+//   H_{k-1} (k >= 1) passes through the workspace as tagged words
+// {value, tag}, written step by step by iteration k - 1 and read with a tag
+// check, so no flag or fence orders them (the device-coherent words of the
+// sLSTM look-back); iteration 0 reads the initial guess, the last iteration
+// writes `out`.  Workgroups take their (k, sequence, head) from a ticket in
+// start order, k-major, so the iteration a workgroup waits on is running or
+// done.  A wait that outlasts the spin limit gives up -- the value reads as
+// NaN and the call's status word is set -- so every workgroup ends.
+// Bounded waits: `limit` polling rounds, then the wait gives up and ORs 1
+// into *status (the word after PRNN_TAG_SPAN ticket counters, where
+// prnn_slstm_lookback_status reads it).
+struct WaitLimit {
+  int* status;
+  int limit;
+};
+
+constexpr int kXP = 3 * kS * DW / kThreads;  // staged wx values per lane (12)
+constexpr int kSP = kS * DW / kThreads;      // staged iterate values per lane (4)
+
+struct StagedN {
+  float x[kXP];  // wx, gate j / 4, step tid / DW + 4 (j % 4)
+  float v[kSP];  // H_{k-1}, step tid / DW + 4 j
+  bool ok[kSP];  // the tagged word carried this call's tag
+};
+
+// Where a step's iterate comes from: the initial guess (plain fp32) or the
+// tagged words of the previous iteration.
+struct IterSrc {
+  const float* plain;
+  const unsigned long long* words;
+  int tag;
+};
+
+__device__ __forceinline__ size_t wide_at(size_t row_base, int t, int d, size_t col) {
+  return row_base + static_cast<size_t>(t) * d + col;
+}
+
+template <typename TX>
+__device__ __forceinline__ void load_block_n(StagedN& st, const TX* __restrict__ wx,
+                                             const IterSrc& src, size_t row_base, int d,
+                                             int head, int dh, int t_first, int t_lo,
+                                             int t_hi) {
+  const int cc = min(static_cast<int>(threadIdx.x) & (DW - 1), dh - 1);
+  const size_t col = static_cast<size_t>(head) * dh + cc;
+#pragma unroll
+  for (int j = 0; j < kXP; ++j) {
+    const int s = static_cast<int>(threadIdx.x) / DW + 4 * (j % 4);
+    const int t = min(max(t_first + s, t_lo), t_hi);
+    st.x[j] = ld(wx + 3 * wide_at(row_base, t, d, 0) + static_cast<size_t>(j / 4) * d + col);
+  }
+#pragma unroll
+  for (int j = 0; j < kSP; ++j) {
+    const int s = static_cast<int>(threadIdx.x) / DW + 4 * j;
+    const size_t at = wide_at(row_base, min(max(t_first + s, t_lo), t_hi), d, col);
+    if (src.words != nullptr) {
+      st.ok[j] = ld_tagged(src.words + at, src.tag, st.v[j]);
+    } else {
+      st.v[j] = src.plain[at];
+      st.ok[j] = true;
+    }
+  }
+}
+
+// Polls the staged tagged words that were not yet written.  Bounded: after
+// `limit` rounds the lane gives up (NaN for what is missing, status word set)
+// and, through `gave_up`, waits no more for the rest of its walk.
+static_assert(kSP == 4, "await_block_n tests four staged words");
+__device__ __forceinline__ void await_block_n(StagedN& st, const IterSrc& src, size_t row_base,
+                                              int d, int head, int dh, int t_first, int t_lo,
+                                              int t_hi, const WaitLimit& spin, bool& gave_up) {
+  if (src.words == nullptr) return;
+  const int cc = min(static_cast<int>(threadIdx.x) & (DW - 1), dh - 1);
+  const size_t col = static_cast<size_t>(head) * dh + cc;
+  int rounds = 0;
+  bool pending = !(st.ok[0] && st.ok[1] && st.ok[2] && st.ok[3]);
+  while (pending) {
+    if (gave_up || ++rounds > spin.limit) {
+#pragma unroll
+      for (int j = 0; j < kSP; ++j)
+        if (!st.ok[j]) st.v[j] = __builtin_nanf("");
+      if (!gave_up)
+        __hip_atomic_fetch_or(spin.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      gave_up = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(2);
+    pending = false;
+#pragma unroll
+    for (int j = 0; j < kSP; ++j) {
+      if (!st.ok[j]) {
+        const int s = static_cast<int>(threadIdx.x) / DW + 4 * j;
+        const size_t at = wide_at(row_base, min(max(t_first + s, t_lo), t_hi), d, col);
+        st.ok[j] = ld_tagged(src.words + at, src.tag, st.v[j]);
+        pending |= !st.ok[j];
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ void store_block_n(float (*x)[kS][DW], float (*v)[kQ * kP],
+                                              const StagedN& st, int dh) {
+  const int cc = static_cast<int>(threadIdx.x) & (DW - 1);
+  const bool live = cc < dh;
+#pragma unroll
+  for (int j = 0; j < kXP; ++j)
+    x[j / 4][static_cast<int>(threadIdx.x) / DW + 4 * (j % 4)][cc] = live ? st.x[j] : 0.f;
+#pragma unroll
+  for (int j = 0; j < kSP; ++j)
+    v[static_cast<int>(threadIdx.x) / DW + 4 * j][slot(cc)] = live ? st.v[j] : 0.f;
+}
+
+template <typename TX>
+__global__ __launch_bounds__(kThreads) void gruw_newton_kernel(
+    const TX* __restrict__ wx, const TX* __restrict__ a_z, const TX* __restrict__ a_r,
+    const TX* __restrict__ a_n, const float* __restrict__ h0, const float* __restrict__ guess,
+    unsigned long long* __restrict__ iters, TX* __restrict__ out, int B, int T, int H, int dh,
+    int n_rows, int K, float omega, const int* __restrict__ cu, int* __restrict__ ticket,
+    int tag_base, WaitLimit spin) {
+  __shared__ float s_x[2][3][kS][DW];
+  __shared__ __attribute__((aligned(16))) float s_v[2][kS][kQ * kP];
+  __shared__ __attribute__((aligned(16))) float s_first[kQ * kP];
+  __shared__ __attribute__((aligned(16))) float s_d[kQ * kP];
+  __shared__ __attribute__((aligned(16))) float s_w[kQ * kP];
+  __shared__ __attribute__((aligned(16))) float s_hr[kQ * kP];
+  __shared__ int s_ticket;
+  if (threadIdx.x == 0)
+    s_ticket = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const int units = n_rows * H;
+  const int k = s_ticket / units, unit = s_ticket % units;
+  const int lane = threadIdx.x & 63;
+  const int c = (threadIdx.x >> 6) * 16 + (lane >> 2), q = lane & 3;
+  const int sc = slot(c);
+  const int head = unit % H;
+  const Span sp = span_of(unit / H, T, cu);
+  const size_t hoff = static_cast<size_t>(head) * dh * dh;
+  float az[kK], ar[kK], an[kK];
+  load_quarter<TX, true>(a_z + hoff, dh, c, q, az);
+  load_quarter<TX, true>(a_r + hoff, dh, c, q, ar);
+  load_quarter<TX, true>(a_n + hoff, dh, c, q, an);
+  const int d = H * dh;
+  const bool live = c < dh;
+  const size_t col = static_cast<size_t>(head) * dh + c;
+  const size_t btd = static_cast<size_t>(B) * T * d;
+  // the sequence's initial state (h0 row or zeros) and delta_{t0-1} = 0
+  if (q == 0) {
+    s_first[sc] = (live && h0 != nullptr) ? h0[static_cast<size_t>(sp.seq) * d + col] : 0.f;
+    s_d[sc] = 0.f;
+  }
+  if (sp.t0 >= sp.t1) return;
+  const IterSrc src{guess, k == 0 ? nullptr : iters + (k - 1) * btd, tag_base + k};
+  const bool last = k == K - 1;
+  unsigned long long* dst = last ? nullptr : iters + k * btd;
+  const int dst_tag = tag_base + 1 + k;
+  const size_t row_base = static_cast<size_t>(sp.row) * T * d;
+  const rsrc_t ro = make_rsrc(out + row_base,
+                              static_cast<uint32_t>(static_cast<size_t>(T) * d * sizeof(TX)));
+  const uint32_t vo = (last && live && q == 0) ? static_cast<uint32_t>(col * sizeof(TX)) : kOOB;
+  float delta = 0.f;
+  bool gave_up = false;
+  {
+    StagedN st;
+    load_block_n(st, wx, src, row_base, d, head, dh, sp.t0, sp.t0, sp.t1 - 1);
+    await_block_n(st, src, row_base, d, head, dh, sp.t0, sp.t0, sp.t1 - 1, spin, gave_up);
+    store_block_n(s_x[0], s_v[0], st, dh);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (int tb = sp.t0; tb < sp.t1; tb += kS) {
+    const bool more = tb + kS < sp.t1;
+    StagedN next;
+    if (more) load_block_n(next, wx, src, row_base, d, head, dh, tb + kS, sp.t0, sp.t1 - 1);
+    const int ns = min(kS, sp.t1 - tb);
+    for (int s = 0; s < ns; ++s) {
+      const int t = tb + s;
+      // previous state (all channels): the sequence's initial state, the
+      // other buffer's last row, or this block's previous row
+      const float* hrow = s > 0 ? s_v[buf][s - 1] : tb == sp.t0 ? s_first : s_v[buf ^ 1][kS - 1];
+      const float hp = hrow[sc], hin = s_v[buf][s][sc];
+      const float xz = s_x[buf][0][s][c], xr = s_x[buf][1][s][c], xn = s_x[buf][2][s][c];
+      // gates' h A_z, h A_r and the Jacobian's A_r^T delta, A_z^T delta
+      const float hz = dot_channel(az, hrow + q * kP);
+      const float hr = dot_channel(ar, hrow + q * kP);
+      const float sr = dot_channel(ar, s_d + q * kP);
+      const float sz = dot_channel(az, s_d + q * kP);
+      const float z = fsigmoid(xz + hz), r = fsigmoid(xr + hr);
+      const float d5 = hp * r * (1.f - r);
+      if (q == 0) {
+        s_w[sc] = r * delta + d5 * sr;
+        s_hr[sc] = hp * r;
+      }
+      __syncthreads();
+      // (h r) A_n for the gate n, A_n^T (r delta + d5 A_r^T delta)
+      const float un = dot_channel(an, s_hr + q * kP);
+      const float sn = dot_channel(an, s_w + q * kP);
+      const float n = ftanh(xn + un);
+      const float d2 = (n - hp) * z * (1.f - z);
+      const float d3 = z * (1.f - n * n);
+      const float f = lerp_t(hp, n, z) - hin;
+      delta = (1.f - z) * delta + d2 * sz + d3 * sn + f;
+      const float h_new = hin + omega * delta;
+      if (q == 0) s_d[sc] = delta;
+      if (dst != nullptr) {
+        if (live && q == 0) st_tagged(dst + wide_at(row_base, t, d, col), h_new, dst_tag);
+      } else {
+        stb<TX>(ro, vo, static_cast<uint32_t>(t) * (d * sizeof(TX)), h_new);
+      }
+      __syncthreads();
+    }
+    if (more) {
+      await_block_n(next, src, row_base, d, head, dh, tb + kS, sp.t0, sp.t1 - 1, spin, gave_up);
+      store_block_n(s_x[buf ^ 1], s_v[buf ^ 1], next, dh);
+      __syncthreads();
+    }
+    buf ^= 1;
+  }
+}
+
 static int check(int B, int T, int H, int dh, int dtype, const int* cu, int n_seq) {
   if (B < 1 || T < 1 || H < 1)
     return fail(PRNN_ERR_VALUE, "B, T, n_heads must be >= 1, got B=%d T=%d n_heads=%d", B, T, H);
@@ -307,6 +532,26 @@ static int check(int B, int T, int H, int dh, int dtype, const int* cu, int n_se
     return fail(PRNN_ERR_VALUE, "a packed stream has B = 1 and n_seq in [1, T], got B=%d n_seq=%d",
                 B, n_seq);
   return PRNN_OK;
+}
+
+// Workspace of the one-launch Newton solve: PRNN_TAG_SPAN ticket counters
+// (the first is used) and the status word, then the tagged iterates
+// H_0 .. H_{K-2}, (B, T, d) 64-bit words each.
+struct NewtonWs {
+  int* counters;
+  unsigned long long* iters;
+  size_t clear_words;  // 32-bit words from `counters` to the end
+};
+
+static NewtonWs carve_newton(void* base, int B, int T, int d, int K, size_t* total) {
+  Carver cv(base);
+  NewtonWs w;
+  w.counters = static_cast<int*>(cv.take(sizeof(int) * (PRNN_TAG_SPAN + 1)));
+  w.iters = static_cast<unsigned long long*>(cv.take(
+      sizeof(unsigned long long) * static_cast<size_t>(K > 1 ? K - 1 : 0) * B * T * d));
+  w.clear_words = cv.used / sizeof(int);
+  *total = cv.used;
+  return w;
 }
 
 }  // namespace gruw
@@ -374,6 +619,60 @@ extern "C" PRNN_API int prnn_gru_wide_reverse(const float* z, const float* r, co
           d_head, cu_seqlens);
     return PRNN_OK;
   });
+  PRNN_HIP(hipGetLastError());
+  return PRNN_OK;
+}
+
+extern "C" PRNN_API size_t prnn_gru_wide_newton_workspace_size(int B, int T, int n_heads,
+                                                              int d_head, int max_iters) {
+  if (B < 1 || T < 1 || n_heads < 1 || d_head < 1 || max_iters < 1) return 0;
+  size_t total = 0;
+  gruw::carve_newton(nullptr, B, T, n_heads * d_head, max_iters, &total);
+  return total;
+}
+
+extern "C" PRNN_API int prnn_gru_wide_newton(const void* wx, const void* a_z, const void* a_r,
+                                             const void* a_n, const float* h0,
+                                             const float* guess, void* out, int B, int T,
+                                             int n_heads, int d_head, int max_iters, float omega,
+                                             int dtype, const int* cu_seqlens, int n_seq,
+                                             void* workspace, size_t workspace_bytes,
+                                             int tag_base, void* stream) {
+  int rc = gruw::check(B, T, n_heads, d_head, dtype, cu_seqlens, n_seq);
+  if (rc != PRNN_OK) return rc;
+  if (max_iters < 1 || max_iters > PRNN_TAG_SPAN)
+    return fail(PRNN_ERR_VALUE, "max_iters must be in [1, %d], got %d", PRNN_TAG_SPAN, max_iters);
+  if (tag_base < 0 || tag_base > PRNN_TAG_BASE_MAX)
+    return fail(PRNN_ERR_VALUE, "tag_base must be in [0, %d], got %d", PRNN_TAG_BASE_MAX,
+                tag_base);
+  if (!wx || !a_z || !a_r || !a_n || !guess || !out || !workspace)
+    return fail(PRNN_ERR_VALUE, "wx, a_z, a_r, a_n, guess, out and workspace must be non-null");
+  if (static_cast<const void*>(guess) == out)
+    return fail(PRNN_ERR_VALUE, "out must not alias guess");
+  const int d = n_heads * d_head;
+  size_t need = 0;
+  const gruw::NewtonWs w = gruw::carve_newton(workspace, B, T, d, max_iters, &need);
+  if (workspace_bytes < need)
+    return fail(PRNN_ERR_VALUE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // tag_base > 0: every word holds a tag below tag_base + 1, only the
+  // counters need zeroing (as for the sLSTM workspaces)
+  rc = clear_words(w.counters, tag_base > 0 ? PRNN_TAG_SPAN + 1 : w.clear_words, s);
+  if (rc != PRNN_OK) return rc;
+  const int rows = cu_seqlens ? n_seq : B;
+  const gruw::WaitLimit lim{w.counters + PRNN_TAG_SPAN, spin_limit()};
+  timing_begin(s);
+  with_storage(dtype, [&](auto tag) {
+    using TX = decltype(tag);
+    gruw::gruw_newton_kernel<TX>
+        <<<dim3(max_iters * rows * n_heads), dim3(gruw::kThreads), 0, s>>>(
+            static_cast<const TX*>(wx), static_cast<const TX*>(a_z),
+            static_cast<const TX*>(a_r), static_cast<const TX*>(a_n), h0, guess, w.iters,
+            static_cast<TX*>(out), B, T, n_heads, d_head, rows, max_iters, omega, cu_seqlens,
+            w.counters, tag_base, lim);
+    return PRNN_OK;
+  });
+  timing_end(s);
   PRNN_HIP(hipGetLastError());
   return PRNN_OK;
 }

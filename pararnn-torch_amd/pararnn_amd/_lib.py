@@ -91,6 +91,9 @@ SIGNATURES: dict[str, tuple] = {
         _I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _P, _I, _P]),
     "prnn_gru_wide_reverse": (
         _I, [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P]),
+    "prnn_gru_wide_newton_workspace_size": (_S, [_I, _I, _I, _I, _I]),
+    "prnn_gru_wide_newton": (
+        _I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _P, _I, _P, _S, _I, _P]),
     "prnn_slstm_decode": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _F, _I, _I, _P]),
     "prnn_gru_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _I, _I, _P]),
 }

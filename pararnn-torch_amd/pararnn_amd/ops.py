@@ -711,10 +711,14 @@ def _wide_gates(wx32: Tensor, hp: Tensor, a: tuple[Tensor, Tensor, Tensor]):
 
 
 def _gru_head_wide(wx, a_z, a_r, a_n, h0, max_iters, omega, code, cs=None):
-    """Forward of the wide tier: the initial guess ``f(h_prev0, x)``, then per
-    Newton iteration the gates at the iterate (GEMMs) and one HIP walk per
-    (sequence, head) for ``delta`` and the update (``prnn_gru_wide_walk``).
-    fp32 work; the result in ``wx``'s dtype."""
+    """Forward of the wide tier: the initial guess ``f(h_prev0, x)``, then the
+    Newton iterations.  K >= 2: one launch (``prnn_gru_wide_newton``) whose
+    walks, one per (iteration, sequence, head), evaluate the gates in the walk
+    and run the iterations a block or two of steps apart
+    (``PARARNN_AMD_WIDE_FUSED=0``: one launch per iteration, as for K = 1).
+    K = 1: the gates at the guess (GEMMs) and one HIP walk per (sequence,
+    head) for ``delta`` and the update (``prnn_gru_wide_walk``).  fp32 work;
+    the result in ``wx``'s dtype."""
     n_heads, d_head, _ = a_z.shape
     batch, time, _ = wx.shape
     d_h = n_heads * d_head
@@ -731,6 +735,23 @@ def _gru_head_wide(wx, a_z, a_r, a_n, h0, max_iters, omega, code, cs=None):
     cs32 = None if cs is None else cs.to(device=wx.device, dtype=torch.int32).contiguous()
     n_seq = 0 if cs32 is None else int(cs32.numel()) - 1
     lib = _lib.load()
+    if max_iters >= 2 and os.environ.get("PARARNN_AMD_WIDE_FUSED", "1") != "0":
+        # all iterations in one launch, each a block or two behind the last
+        out = wx.new_empty(batch, time, d_h)
+        nbytes = lib.prnn_gru_wide_newton_workspace_size(batch, time, n_heads, d_head, max_iters)
+        ws, tag = _slstm_workspace(nbytes, wx.device)
+        h0_c = None if h0_32 is None else h0_32.contiguous()
+        wx_c = wx.contiguous()
+        guess = states.contiguous()
+        with torch.cuda.device(wx.device):
+            rc = lib.prnn_gru_wide_newton(
+                _ptr(wx_c), _ptr(a_k[0]), _ptr(a_k[1]), _ptr(a_k[2]), _ptr(h0_c), _ptr(guess),
+                _ptr(out), batch, time, n_heads, d_head, max_iters, float(omega), code,
+                _ptr(cs32), n_seq, _ptr(ws), ws.numel(), tag, _stream(wx.device),
+            )
+        _lib.check(rc, "newton_gru_head_fused (wide heads)")
+        _check_lookback(ws, "newton_gru_head_fused (wide heads)")
+        return out
     out = None
     for it in range(max_iters):
         hp = _wide_prev(states, h0_32, cs).contiguous()

@@ -244,3 +244,37 @@ def test_stacked_layers_and_verify_agreement():
                            config=NewtonConfig(max_iters=6))
     print(f"  verify_agreement max_abs {rep.max_abs:.2e} ok={rep.ok}", flush=True)
     assert rep.ok
+
+
+@pytest.mark.parametrize("packed", [False, True])
+@pytest.mark.parametrize("K", [2, 5])
+def test_one_launch_matches_launch_per_iteration(packed, K, monkeypatch):
+    """K >= 2 runs all iterations in one launch (gates evaluated in the walks,
+    iteration k a block or two behind k - 1, iterates passed as tagged words);
+    PARARNN_AMD_WIDE_FUSED=0 runs one walk per iteration after host GEMMs for
+    the gates.  Same algebra, gates summed in another order: they agree to
+    float32 rounding, and no wait gives up (PARARNN_AMD_CHECK_STATUS=1)."""
+    from pararnn_amd import newton_apply
+
+    print(f"case wide heads one launch vs per iteration packed={packed} K={K}", flush=True)
+    cell, _ = _make(2, 128, 11 + K)
+    cell = cell.to(DEV)
+    g = torch.Generator().manual_seed(K)
+    if packed:
+        lengths = [700, 3, 129, 1200, 17]
+        cs = torch.tensor([0] + lengths).cumsum(0).to(DEV)
+        x = torch.randn(1, int(cs[-1]), 12, generator=g).to(DEV)
+        h0 = (torch.randn(len(lengths), 256, generator=g) * 0.5).to(DEV)
+        kw = {"cu_seqlens": cs}
+    else:
+        x = torch.randn(3, 1500, 12, generator=g).to(DEV)
+        h0 = (torch.randn(3, 256, generator=g) * 0.5).to(DEV)
+        kw = {}
+    monkeypatch.setenv("PARARNN_AMD_CHECK_STATUS", "1")
+    with torch.no_grad():
+        one = newton_apply(cell, x, _cfg(K), h0=h0, **kw)
+        monkeypatch.setenv("PARARNN_AMD_WIDE_FUSED", "0")
+        per = newton_apply(cell, x, _cfg(K), h0=h0, **kw)
+    err = (one - per).abs().max().item()
+    print(f"  max|one launch - per iteration| {err:.2e}", flush=True)
+    assert torch.isfinite(one).all() and err <= 1e-5
