@@ -1,6 +1,8 @@
 // ParaGRU mix='head' with wide heads (64 < d_head <= 128): the Newton
 // iteration's linear solve and the eq. 2.6 adjoint as walks over time, one
-// workgroup per (sequence, head).
+// workgroup per (sequence, head) -- and, for K >= 2 iterations, one launch
+// whose K walks per (sequence, head) run a block or two of steps apart
+// (gruw_newton_kernel, further down).
 //
 // This is the tier of the reference's streamed head kernel
 // (kernels/newton_gru_head.py:765-960, _newton_head_stream_a_kernel: one
