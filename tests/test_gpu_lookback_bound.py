@@ -66,3 +66,41 @@ def test_give_up_is_reported_and_kernels_end(monkeypatch):
     print("  after restoring the budget: bit-equal to the first solve "
           f"{torch.equal(again, ref)}", flush=True)
     assert torch.equal(again, ref)
+
+
+def test_wide_head_one_launch_give_up(monkeypatch):
+    """The one-launch wide-head Newton solve waits for the previous iteration's
+    tagged words; with a one-round budget the waiting walks give up, the
+    launch ends, the status word reports it, and afterwards the default
+    budget reproduces the first solve bit for bit."""
+    from pararnn_amd import NewtonConfig, ParaGRU, _lib, newton_apply
+
+    lib = _lib.load()
+    torch.manual_seed(0)
+    cell = ParaGRU(16, 256, mix="head", n_heads=2).to(DEV)
+    g = torch.Generator(device=DEV).manual_seed(2)
+    x = torch.randn(2, 3000, 16, generator=g, device=DEV)
+    cfg = NewtonConfig(max_iters=3, residual_atol=None, residual_fail=None)
+    print("case wide one-launch give-up: spin limit 1, B=2, T=3000, d_head=128, K=3", flush=True)
+    with torch.no_grad():
+        ref = newton_apply(cell, x, cfg)
+    assert torch.isfinite(ref).all()
+    monkeypatch.setenv("PARARNN_AMD_CHECK_STATUS", "1")
+    raised = 0
+    lib.prnn_set_spin_limit(1)
+    try:
+        for _ in range(4):
+            try:
+                with torch.no_grad():
+                    newton_apply(cell, x, cfg)
+            except RuntimeError as e:
+                assert "gave up" in str(e)
+                raised += 1
+    finally:
+        lib.prnn_set_spin_limit(0)
+    torch.cuda.synchronize()
+    print(f"  launches that reported a give-up: {raised} of 4", flush=True)
+    assert raised >= 1
+    with torch.no_grad():
+        again = newton_apply(cell, x, cfg)
+    assert torch.equal(again, ref)
