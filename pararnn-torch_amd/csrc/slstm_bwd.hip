@@ -212,10 +212,16 @@ __global__ __launch_bounds__(64 * W) void slstm_reverse_kernel(
           if (s < ns) step(s, chk);
       }
     };
-    if constexpr (PK)
-      run(std::true_type{});
-    else
+    // a wave whose steps hold no head skips the per-step checks here (pass 2
+    // keeps the one checked copy)
+    if constexpr (PK) {
+      if (hd.mask == 0ull)
+        run(std::false_type{});
+      else
+        run(std::true_type{});
+    } else {
       run(std::false_type{});
+    }
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
