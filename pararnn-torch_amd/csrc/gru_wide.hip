@@ -312,6 +312,7 @@ __global__ __launch_bounds__(kThreads) void gruw_reverse_kernel(
 // start order, k-major, so the iteration a workgroup waits on is running or
 // done.  A wait that outlasts the spin limit gives up -- the value reads as
 // NaN and the call's status word is set -- so every workgroup ends.
+
 // Bounded waits: `limit` polling rounds, then the wait gives up and ORs 1
 // into *status (the word after PRNN_TAG_SPAN ticket counters, where
 // prnn_slstm_lookback_status reads it).
