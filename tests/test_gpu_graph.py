@@ -69,3 +69,29 @@ def test_gru_head_solve_graph_replay_bit_equal():
             graph.replay()
             torch.cuda.synchronize()
             assert torch.equal(out, eager), i
+
+
+def test_wide_head_one_launch_graph_replay_bit_equal():
+    """d_head = 128, K = 3: the one-launch wide solve (ticket counters and the
+    tagged iterates cleared by a fill kernel inside the graph) replays bit
+    for bit."""
+    from pararnn_amd import ParaGRU, fused_newton
+
+    print("case graph: wide heads fp32 K=3 one launch, 4 replays, bit-equal", flush=True)
+    torch.manual_seed(4)
+    cell = ParaGRU(32, 256, mix="head", n_heads=2).to(DEV)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    x = torch.randn(2, 1500, 32, generator=g, device=DEV)
+    h0 = torch.randn(2, 256, generator=g, device=DEV) * 0.5
+    with torch.no_grad():
+        wx = cell.W_x(x)
+        run = lambda: fused_newton(cell, wx, max_iters=3, omega=1.0, h0=h0)
+        eager = run().clone()
+        graph, out = _capture(run)
+        for i in range(4):
+            out.zero_()
+            _ = run()
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), i
