@@ -281,3 +281,25 @@ def test_one_launch_matches_launch_per_iteration(packed, K, monkeypatch):
     err = (one - per).abs().max().item()
     print(f"  max|one launch - per iteration| {err:.2e}", flush=True)
     assert torch.isfinite(one).all() and err <= 1e-5
+
+
+def test_one_launch_more_workgroups_than_fit_at_once(monkeypatch):
+    """K x B x H = 3 x 64 x 8 = 1536 one-launch workgroups, more than the GPU
+    holds at once: the ticket order (iteration-major) lets every waiting walk
+    find its predecessor running or done, so the solve completes without a
+    wait giving up, equal to one launch per iteration."""
+    from pararnn_amd import NewtonConfig, ParaGRU, newton_apply
+
+    print("case wide heads one launch, 1536 workgroups (B=64, H=8, K=3)", flush=True)
+    torch.manual_seed(21)
+    cell = ParaGRU(16, 1024, mix="head", n_heads=8).to(DEV)
+    x = torch.randn(64, 96, 16, device=DEV)
+    cfg = NewtonConfig(max_iters=3, residual_atol=None, residual_fail=None)
+    monkeypatch.setenv("PARARNN_AMD_CHECK_STATUS", "1")
+    with torch.no_grad():
+        one = newton_apply(cell, x, cfg)
+        monkeypatch.setenv("PARARNN_AMD_WIDE_FUSED", "0")
+        per = newton_apply(cell, x, cfg)
+    err = (one - per).abs().max().item()
+    print(f"  max|one launch - per iteration| {err:.2e}", flush=True)
+    assert err <= 1e-5
