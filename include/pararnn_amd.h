@@ -57,7 +57,7 @@ extern "C" {
 enum { PRNN_F32 = 0, PRNN_BF16 = 1, PRNN_F16 = 2 };
 enum { PRNN_OK = 0, PRNN_ERR_VALUE = 1, PRNN_ERR_TYPE = 2, PRNN_ERR_RUNTIME = 3 };
 
-/* Library ABI version (bumped on any signature change). */
+/* Library ABI version (bumped on any signature change or added entry point). */
 PRNN_API int prnn_abi_version(void);
 /* Message of the last failing call on this thread ("" if none). */
 PRNN_API const char* prnn_last_error(void);

@@ -20,7 +20,7 @@ PRNN_OK = 0
 PRNN_ERR_VALUE = 1
 PRNN_ERR_TYPE = 2
 PRNN_ERR_RUNTIME = 3
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # name -> (restype, argtypes); mirrors include/pararnn_amd.h
 _P = ctypes.c_void_p
