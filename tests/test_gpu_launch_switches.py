@@ -54,6 +54,6 @@ def test_per_launch_fallbacks_match_single_launch(tmp_path, dtype):
     assert fused.shape == split.shape and torch.isfinite(fused).all()
     rel = ((fused.float() - split.float()).abs() / (1 + fused.float().abs())).max().item()
     print(f"  max rel diff {rel:.2e}", flush=True)
-    # bf16: a few storage ulps (the passes round h to bf16 at other points of
-    # the scan association)
+    # bf16: a few storage ulps (fp32 scans associated differently, then
+    # rounded to bf16)
     assert rel <= (1e-5 if dtype == "torch.float32" else 2 ** -6)
