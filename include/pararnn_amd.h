@@ -307,11 +307,11 @@ PRNN_API int prnn_gru_head_backward(const void* wx, const void* a_z, const void*
 
 /* Wide heads, 64 < d_head <= 128 (replaces the reference's streamed head
  * tier, kernels/newton_gru_head.py:121-150 and its _newton_head_stream_a_kernel
- * at :765-960, one program per (b, head) walking T).  The host computes the
- * gates of every step at the current iterate -- z, r, n (B, T, d) fp32 from
- * hp, the previous state of every step (h0's row at a sequence start) --
- * with GEMMs over all rows; these walk time, one workgroup per (sequence,
- * head), A_* (n_heads, d_head, d_head) in `dtype`, fp32 work.
+ * at :765-960, one program per (b, head) walking T).  The gates of every
+ * step at the current iterate -- z, r, n (B, T, d) fp32 from hp, the previous
+ * state of every step (h0's row at a sequence start) -- come first, for all
+ * rows at once (prnn_gru_wide_gates below); these walk time, one workgroup
+ * per (sequence, head), A_* (n_heads, d_head, d_head) in `dtype`, fp32 work.
  *
  * prnn_gru_wide_walk: one Newton iteration's linear solve and update,
  *   delta_t = J_t delta_{t-1} + lerp(hp_t, n_t, z_t) - hin_t,
@@ -333,6 +333,16 @@ PRNN_API int prnn_gru_wide_reverse(const float* z, const float* r, const float* 
                                    float* g_wx, float* g_h0, int B, int T, int n_heads,
                                    int d_head, int dtype, const int* cu_seqlens, int n_seq,
                                    void* stream);
+
+/* The gates of every row (b, t) of the wide tier at its previous state:
+ * z = sigmoid(wx_z + hp A_z), r = sigmoid(wx_r + hp A_r),
+ * n = tanh(wx_n + (hp r) A_n) per head (the cell of cells/para_gru.py:443-467
+ * that the reference's streamed kernel evaluates inside its walk).  wx
+ * (rows, 3d) and A_* in `dtype`, hp (rows, d) fp32 (h0's row, or zeros, at a
+ * sequence's first step), z, r, n (rows, d) fp32. */
+PRNN_API int prnn_gru_wide_gates(const void* wx, const float* hp, const void* a_z,
+                                 const void* a_r, const void* a_n, float* z, float* r, float* n,
+                                 int rows, int n_heads, int d_head, int dtype, void* stream);
 
 /* All max_iters Newton iterations of the wide tier in one launch, without the
  * host's gate GEMMs: iteration k's workgroup per (sequence, head) evaluates

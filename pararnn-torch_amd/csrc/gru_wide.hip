@@ -8,22 +8,21 @@
 // (kernels/newton_gru_head.py:765-960, _newton_head_stream_a_kernel: one
 // program per (b, head), a serial walk over T per Newton iteration, A_* read
 // in fp32).  Here the parts of an iteration that do not depend on the walk
-// run beforehand as wide parallel work (the gates z, r, n at the iterate:
-// three GEMMs over all B*T rows and elementwise ops, issued by the host), so a
-// walk step is only the Jacobian applied to the previous delta,
+// run beforehand as wide parallel work (the gates z, r, n at the iterate for
+// all B*T rows, gruw_gates_kernel), so a walk step is only the Jacobian
+// applied to the previous delta,
 //     J delta = (1-z) delta + d2 (A_z^T delta) + d3 A_n^T (r delta + d5 (A_r^T delta))
 // with d2 = (n-h) z(1-z), d3 = z(1-n^2), d5 = h r(1-r) (reference
 // cells/para_gru.py:385-412), three 128-wide mat-vecs.
 //
-// Workgroup: 512 lanes = 128 channels x 4 quarters of the contraction index.
-// Lane l of wave w is channel c = 16 w + l / 4, quarter q = l % 4: it keeps
-// 32 entries of each A in registers -- column c (forward: A^T products) or
-// row c (adjoint: A products) over k in [32 q, 32 q + 32) -- and the four
-// quarters of a channel are one quad of lanes, so their partial sums meet
-// through two DPP moves, every quarter holding the same sum.  A step then
-// needs LDS and a barrier only to broadcast the two vectors the next
-// products read: two barriers per step.  fp32 throughout; lanes c >= d_head
-// and entries k >= d_head hold zeros.
+// Workgroup: 512 lanes = 64 channel pairs x 8 parts of the contraction index
+// (see Role): a lane keeps 16 entries of each A for both channels of its pair
+// in registers -- columns (forward: A^T products) or rows (adjoint: A
+// products) -- and the eight parts of a pair are eight neighbouring lanes, so
+// their partial sums meet through three DPP moves.  A step then needs LDS
+// and a barrier only to broadcast the two vectors the next products read:
+// two barriers per step.  fp32 throughout; channels >= d_head and entries
+// k >= d_head hold zeros.
 #include "prnn_common.h"
 #include "pararnn_amd.h"
 #include "prnn_host.h"
@@ -32,14 +31,14 @@ namespace prnn {
 namespace gruw {
 
 constexpr int DW = 128;       // widest head
-constexpr int kQ = 4;         // quarters of the contraction index
-constexpr int kK = DW / kQ;   // entries per lane and matrix
-constexpr int kThreads = DW * kQ;
-// A broadcast vector sits in LDS as kQ segments of kK entries, each padded
-// to kP so that the four segments a quad reads at once start in different
-// banks.
-constexpr int kP = kK + 4;
-__device__ __forceinline__ int slot(int c) { return (c / kK) * kP + c % kK; }
+constexpr int kParts = 8;     // parts of the contraction index
+constexpr int kKP = DW / kParts;  // contraction entries per lane (16)
+constexpr int kK = 2 * kKP;   // entries per lane and matrix: two channels (32)
+constexpr int kThreads = DW / 2 * kParts;
+// A broadcast vector sits in LDS in two halves of 64 entries, the second
+// shifted by four words (bank spread of the segments one wave reads).
+constexpr int kVec = DW + 4;
+__device__ __forceinline__ int slot(int c) { return c + (c >> 6) * 4; }
 
 // torch.lerp(start, end, weight) for fp32 (the cell's update).
 __device__ __forceinline__ float lerp_t(float s, float e, float w) {
@@ -56,17 +55,42 @@ __device__ __forceinline__ Span span_of(int s, int T, const int* cu) {
   return Span{0, cu[s], cu[s + 1], s};
 }
 
-// Entries k in [32 q, 32 q + 32) of column c (COL) or row c of a head's A
-// ((in, out) layout, d_head x d_head), zero outside the head.
+// Lane roles.  Lane l of wave w holds the channel pair 2 p, 2 p + 1 with
+// p = 8 w + l / 8, and the contraction entries k in [16 j, 16 j + 16) with
+// j = l % 8: its products read 16 entries of the broadcast vector and feed
+// two channels (half the LDS reads per multiply-add of one channel per
+// lane: the walks are bound by the LDS read rate).  After the reduction the
+// lanes j < 4 hold channel 2 p and the lanes j >= 4 channel 2 p + 1; j = 0
+// and j = 4 write it.
+struct Role {
+  int pair, part, c;
+  bool wr;
+};
+__device__ __forceinline__ Role role() {
+  const int lane = threadIdx.x & 63;
+  Role o;
+  o.part = lane & (kParts - 1);
+  o.pair = (threadIdx.x >> 6) * 8 + (lane >> 3);
+  o.c = 2 * o.pair + (o.part >> 2);
+  o.wr = (o.part & 3) == 0;
+  return o;
+}
+
+// Entries k in [16 j, 16 j + 16) of columns (COL) or rows 2 p, 2 p + 1 of a
+// head's A ((in, out) layout, d_head x d_head), zero outside the head:
+// a[2 kk + i] = A[k][2 p + i] (COL) or A[2 p + i][k].
 template <typename TX, bool COL>
-__device__ __forceinline__ void load_quarter(const TX* A, int dh, int c, int q, float a[kK]) {
+__device__ __forceinline__ void load_pair(const TX* A, int dh, const Role& ro, float a[kK]) {
 #pragma unroll
-  for (int kk = 0; kk < kK; ++kk) {
-    const int k = q * kK + kk;
-    const bool in = c < dh && k < dh;
-    a[kk] = in ? ld(A + (COL ? static_cast<size_t>(k) * dh + c : static_cast<size_t>(c) * dh + k))
-               : 0.f;
-  }
+  for (int kk = 0; kk < kKP; ++kk)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int k = ro.part * kKP + kk, ch = 2 * ro.pair + i;
+      const bool in = ch < dh && k < dh;
+      a[2 * kk + i] =
+          in ? ld(A + (COL ? static_cast<size_t>(k) * dh + ch : static_cast<size_t>(ch) * dh + k))
+             : 0.f;
+    }
 }
 
 // A step's per-channel inputs (z, r, n, the previous state, and the iterate
@@ -118,26 +142,42 @@ __device__ __forceinline__ void store_block(float (*buf)[kS][DW], const Staged& 
   }
 }
 
-// sum_k a[k] v[k] over this lane's quarter, four independent chains (a long
-// dependent FMA chain would set the step's latency), then over the channel's
-// four quarters (the lanes of a quad).
-__device__ __forceinline__ float dot_channel(const float a[kK], const float* __restrict__ v) {
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// sum_k A v for this lane's channel: the lane's 16 entries for both of its
+// pair's channels (two chains each), the sums over the eight parts of the
+// pair (quad_perm [1,0,3,2] and [2,3,0,1] within each quad for both
+// channels, then row_half_mirror between the two quads, which exchanges the
+// channel the other quad keeps).  Every lane of a channel ends with the same
+// sum.
+__device__ __forceinline__ float dot_pair(const float a[kK], const float* __restrict__ v,
+                                          const Role& ro) {
+  const float* seg = v + slot(ro.part * kKP);
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int kk = 0; kk < kK; kk += 4) {
-    const float4 x = *reinterpret_cast<const float4*>(v + kk);
-    acc[0] = fmaf(a[kk], x.x, acc[0]);
-    acc[1] = fmaf(a[kk + 1], x.y, acc[1]);
-    acc[2] = fmaf(a[kk + 2], x.z, acc[2]);
-    acc[3] = fmaf(a[kk + 3], x.w, acc[3]);
+  for (int kk = 0; kk < kKP; kk += 4) {
+    const float4 x = *reinterpret_cast<const float4*>(seg + kk);
+    acc[0] = fmaf(a[2 * kk], x.x, acc[0]);
+    acc[1] = fmaf(a[2 * kk + 1], x.x, acc[1]);
+    acc[2] = fmaf(a[2 * kk + 2], x.y, acc[2]);
+    acc[3] = fmaf(a[2 * kk + 3], x.y, acc[3]);
+    acc[0] = fmaf(a[2 * kk + 4], x.z, acc[0]);
+    acc[1] = fmaf(a[2 * kk + 5], x.z, acc[1]);
+    acc[2] = fmaf(a[2 * kk + 6], x.w, acc[2]);
+    acc[3] = fmaf(a[2 * kk + 7], x.w, acc[3]);
   }
-  float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-  // quad_perm [1,0,3,2] then [2,3,0,1]: row-local DPP moves
-  s += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, s), 0xB1, 0xF,
-                                                          0xF, false));
-  s += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, s), 0x4E, 0xF,
-                                                          0xF, false));
-  return s;
+  float s0 = acc[0] + acc[2], s1 = acc[1] + acc[3];
+  s0 += dppf<0xB1>(s0);
+  s1 += dppf<0xB1>(s1);
+  s0 += dppf<0x4E>(s0);
+  s1 += dppf<0x4E>(s1);
+  const bool second = ro.part >= 4;
+  const float keep = second ? s1 : s0, send = second ? s0 : s1;
+  return keep + dppf<0x141>(send);
 }
 
 // Forward walk of one Newton iteration: delta_t = J_t delta_{t-1} + F_t with
@@ -152,29 +192,29 @@ __global__ __launch_bounds__(kThreads) void gruw_walk_kernel(
     const float* __restrict__ hp, const float* __restrict__ hin, const TX* __restrict__ a_z,
     const TX* __restrict__ a_r, const TX* __restrict__ a_n, TOUT* __restrict__ out, int T,
     int H, int dh, float omega, const int* __restrict__ cu) {
-  __shared__ __attribute__((aligned(16))) float s_d[kQ * kP];
-  __shared__ __attribute__((aligned(16))) float s_w[kQ * kP];
+  __shared__ __attribute__((aligned(16))) float s_d[kVec];
+  __shared__ __attribute__((aligned(16))) float s_w[kVec];
   __shared__ float s_in[2][kIn][kS][DW];
-  const int lane = threadIdx.x & 63;
-  const int c = (threadIdx.x >> 6) * 16 + (lane >> 2), q = lane & 3;
+  const Role rl = role();
+  const int c = rl.c;
   const int sc = slot(c);
   const int head = blockIdx.x % H;
   const Span sp = span_of(blockIdx.x / H, T, cu);
   const size_t hoff = static_cast<size_t>(head) * dh * dh;
   float az[kK], ar[kK], an[kK];
-  load_quarter<TX, true>(a_z + hoff, dh, c, q, az);
-  load_quarter<TX, true>(a_r + hoff, dh, c, q, ar);
-  load_quarter<TX, true>(a_n + hoff, dh, c, q, an);
+  load_pair<TX, true>(a_z + hoff, dh, rl, az);
+  load_pair<TX, true>(a_r + hoff, dh, rl, ar);
+  load_pair<TX, true>(a_n + hoff, dh, rl, an);
   const int d = H * dh;
   const bool live = c < dh;
   const size_t col = static_cast<size_t>(head) * dh + c;
-  if (q == 0) s_d[sc] = 0.f;
+  if (rl.wr) s_d[sc] = 0.f;
   float delta = 0.f;
   if (sp.t0 >= sp.t1) return;
   const size_t row_base = static_cast<size_t>(sp.row) * T * d;
   const rsrc_t ro = make_rsrc(out + row_base,
                               static_cast<uint32_t>(static_cast<size_t>(T) * d * sizeof(TOUT)));
-  const uint32_t vo = (live && q == 0) ? static_cast<uint32_t>(col * sizeof(TOUT)) : kOOB;
+  const uint32_t vo = (live && rl.wr) ? static_cast<uint32_t>(col * sizeof(TOUT)) : kOOB;
   store_block(s_in[0], load_block(z, r, n, hp, hin, row_base, d, head, dh, sp.t0, 1, sp.t0,
                                   sp.t1 - 1), dh);
   __syncthreads();
@@ -190,18 +230,18 @@ __global__ __launch_bounds__(kThreads) void gruw_walk_kernel(
       const float zt = s_in[buf][0][s][c], rt = s_in[buf][1][s][c], nt = s_in[buf][2][s][c];
       const float ht = s_in[buf][3][s][c], hv = s_in[buf][4][s][c];
       // A_r^T delta and A_z^T delta (delta_{t-1} broadcast in s_d)
-      const float sr = dot_channel(ar, s_d + q * kP);
-      const float sz = dot_channel(az, s_d + q * kP);
+      const float sr = dot_pair(ar, s_d, rl);
+      const float sz = dot_pair(az, s_d, rl);
       const float d5 = ht * rt * (1.f - rt);
-      if (q == 0) s_w[sc] = rt * delta + d5 * sr;
+      if (rl.wr) s_w[sc] = rt * delta + d5 * sr;
       __syncthreads();
       // A_n^T (r delta + d5 A_r^T delta)
-      const float sn = dot_channel(an, s_w + q * kP);
+      const float sn = dot_pair(an, s_w, rl);
       const float d2 = (nt - ht) * zt * (1.f - zt);
       const float d3 = zt * (1.f - nt * nt);
       const float f = lerp_t(ht, nt, zt) - hv;
       delta = (1.f - zt) * delta + d2 * sz + d3 * sn + f;
-      if (q == 0) s_d[sc] = delta;
+      if (rl.wr) s_d[sc] = delta;
       // a buffer store, dropped for lanes with the out-of-range offset
       stb<TOUT>(ro, vo, static_cast<uint32_t>(t) * (d * sizeof(TOUT)), hv + omega * delta);
       __syncthreads();
@@ -209,6 +249,105 @@ __global__ __launch_bounds__(kThreads) void gruw_walk_kernel(
     if (more) {
       store_block(s_in[buf ^ 1], next, dh);
       __syncthreads();
+    }
+    buf ^= 1;
+  }
+}
+
+// Gates z, r, n of every row (b, t) at its previous state hp: z =
+// sigmoid(wx_z + hp A_z), r = sigmoid(wx_r + hp A_r), n = tanh(wx_n + (hp r)
+// A_n), per head (reference cells/para_gru.py:443-467).  Rows are independent
+// (no walk): workgroup (head, block of rows) stages kS rows of hp and wx at a
+// time, forms h A_z and h A_r for all of them, then, after one barrier for
+// the (hp r) rows, (hp r) A_n.  A column quarter of each A stays in registers
+// as in the walks.  z, r, n fp32 (rows, d).
+template <typename TX>
+__global__ __launch_bounds__(kThreads) void gruw_gates_kernel(
+    const TX* __restrict__ wx, const float* __restrict__ hp, const TX* __restrict__ a_z,
+    const TX* __restrict__ a_r, const TX* __restrict__ a_n, float* __restrict__ z,
+    float* __restrict__ r, float* __restrict__ n, int rows, int rows_per_block, int H, int dh) {
+  __shared__ __attribute__((aligned(16))) float s_h[2][kS][kVec];
+  __shared__ __attribute__((aligned(16))) float s_hr[kS][kVec];
+  __shared__ float s_x[2][3][kS][DW];
+  const Role rl = role();
+  const int c = rl.c;
+  const int sc = slot(c);
+  const int head = blockIdx.x % H;
+  const int r0 = (blockIdx.x / H) * rows_per_block;
+  const int r1 = min(rows, r0 + rows_per_block);
+  if (r0 >= r1) return;
+  const size_t hoff = static_cast<size_t>(head) * dh * dh;
+  float az[kK], ar[kK], an[kK];
+  load_pair<TX, true>(a_z + hoff, dh, rl, az);
+  load_pair<TX, true>(a_r + hoff, dh, rl, ar);
+  load_pair<TX, true>(a_n + hoff, dh, rl, an);
+  const int d = H * dh;
+  const bool live = c < dh;
+  const size_t col = static_cast<size_t>(head) * dh + c;
+  // Staging: lane tid holds channel tid % DW of rows tid / DW + 4 j of the
+  // next block in registers while the current one is computed from LDS.
+  const int cc = static_cast<int>(threadIdx.x) & (DW - 1);
+  const bool live_cc = cc < dh;
+  const size_t col_cc = static_cast<size_t>(head) * dh + min(cc, dh - 1);
+  constexpr int kJ = kS * DW / kThreads;  // rows per lane and block (4)
+  float nh[kJ], nx[3][kJ];
+  auto fetch = [&](int rb) {
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+      const int s = static_cast<int>(threadIdx.x) / DW + 4 * j;
+      const size_t row = static_cast<size_t>(min(rb + s, r1 - 1));
+      nh[j] = hp[row * d + col_cc];
+#pragma unroll
+      for (int g = 0; g < 3; ++g) nx[g][j] = ld(wx + row * 3 * d + g * d + col_cc);
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+      const int s = static_cast<int>(threadIdx.x) / DW + 4 * j;
+      s_h[buf][s][slot(cc)] = live_cc ? nh[j] : 0.f;
+#pragma unroll
+      for (int g = 0; g < 3; ++g) s_x[buf][g][s][cc] = live_cc ? nx[g][j] : 0.f;
+    }
+  };
+  fetch(r0);
+  int buf = 0;
+  for (int rb = r0; rb < r1; rb += kS) {
+    stash(buf);
+    __syncthreads();
+    if (rb + kS < r1) fetch(rb + kS);
+    const int ns = min(kS, r1 - rb);
+    auto gates_zr = [&](int s) {
+      const float hz = dot_pair(az, s_h[buf][s], rl);
+      const float hr = dot_pair(ar, s_h[buf][s], rl);
+      const float zv = fsigmoid(s_x[buf][0][s][c] + hz);
+      const float rv = fsigmoid(s_x[buf][1][s][c] + hr);
+      if (rl.wr) {
+        s_hr[s][sc] = s_h[buf][s][sc] * rv;
+        if (live) {
+          const size_t at = static_cast<size_t>(rb + s) * d + col;
+          z[at] = zv;
+          r[at] = rv;
+        }
+      }
+    };
+    auto gate_n = [&](int s) {
+      const float un = dot_pair(an, s_hr[s], rl);
+      const float nv = ftanh(s_x[buf][2][s][c] + un);
+      if (rl.wr && live) n[static_cast<size_t>(rb + s) * d + col] = nv;
+    };
+    if (ns == kS) {
+#pragma unroll
+      for (int s = 0; s < kS; ++s) gates_zr(s);
+    } else {
+      for (int s = 0; s < ns; ++s) gates_zr(s);
+    }
+    __syncthreads();
+    if (ns == kS) {
+#pragma unroll
+      for (int s = 0; s < kS; ++s) gate_n(s);
+    } else {
+      for (int s = 0; s < ns; ++s) gate_n(s);
     }
     buf ^= 1;
   }
@@ -227,20 +366,20 @@ __global__ __launch_bounds__(kThreads) void gruw_reverse_kernel(
     const float* __restrict__ hp, const TG* __restrict__ grad, const TX* __restrict__ a_z,
     const TX* __restrict__ a_r, const TX* __restrict__ a_n, float* __restrict__ g_wx,
     float* __restrict__ g_h0, int T, int H, int dh, const int* __restrict__ cu) {
-  __shared__ __attribute__((aligned(16))) float s_dz[kQ * kP];
-  __shared__ __attribute__((aligned(16))) float s_dn[kQ * kP];
-  __shared__ __attribute__((aligned(16))) float s_dr[kQ * kP];
+  __shared__ __attribute__((aligned(16))) float s_dz[kVec];
+  __shared__ __attribute__((aligned(16))) float s_dn[kVec];
+  __shared__ __attribute__((aligned(16))) float s_dr[kVec];
   __shared__ float s_in[2][kIn][kS][DW];
-  const int lane = threadIdx.x & 63;
-  const int c = (threadIdx.x >> 6) * 16 + (lane >> 2), q = lane & 3;
+  const Role rl = role();
+  const int c = rl.c;
   const int sc = slot(c);
   const int head = blockIdx.x % H;
   const Span sp = span_of(blockIdx.x / H, T, cu);
   const size_t hoff = static_cast<size_t>(head) * dh * dh;
   float az[kK], ar[kK], an[kK];
-  load_quarter<TX, false>(a_z + hoff, dh, c, q, az);
-  load_quarter<TX, false>(a_r + hoff, dh, c, q, ar);
-  load_quarter<TX, false>(a_n + hoff, dh, c, q, an);
+  load_pair<TX, false>(a_z + hoff, dh, rl, az);
+  load_pair<TX, false>(a_r + hoff, dh, rl, ar);
+  load_pair<TX, false>(a_n + hoff, dh, rl, an);
   const int d = H * dh;
   const bool live = c < dh;
   const size_t col = static_cast<size_t>(head) * dh + c;
@@ -249,7 +388,7 @@ __global__ __launch_bounds__(kThreads) void gruw_reverse_kernel(
   const size_t row_base = static_cast<size_t>(sp.row) * T * d;
   const rsrc_t rg = make_rsrc(g_wx + row_base * 3,
                               static_cast<uint32_t>(static_cast<size_t>(T) * 3 * d * sizeof(float)));
-  const uint32_t vg = (live && q == 0) ? static_cast<uint32_t>(col * sizeof(float)) : kOOB;
+  const uint32_t vg = (live && rl.wr) ? static_cast<uint32_t>(col * sizeof(float)) : kOOB;
   store_block(s_in[0], load_block(z, r, n, hp, grad, row_base, d, head, dh, sp.t1 - 1, -1,
                                   sp.t0, sp.t1 - 1), dh);
   __syncthreads();
@@ -267,17 +406,17 @@ __global__ __launch_bounds__(kThreads) void gruw_reverse_kernel(
       const float mu = g + nu;
       const float dz = mu * (nt - ht) * zt * (1.f - zt);
       const float dn = mu * zt * (1.f - nt * nt);
-      if (q == 0) {
+      if (rl.wr) {
         s_dz[sc] = dz;
         s_dn[sc] = dn;
       }
       __syncthreads();
-      const float du = dot_channel(an, s_dn + q * kP);
-      const float azdz = dot_channel(az, s_dz + q * kP);
+      const float du = dot_pair(an, s_dn, rl);
+      const float azdz = dot_pair(az, s_dz, rl);
       const float dr = du * ht * rt * (1.f - rt);
-      if (q == 0) s_dr[sc] = dr;
+      if (rl.wr) s_dr[sc] = dr;
       __syncthreads();
-      const float ardr = dot_channel(ar, s_dr + q * kP);
+      const float ardr = dot_pair(ar, s_dr, rl);
       nu = (1.f - zt) * mu + azdz + rt * du + ardr;
       // buffer stores, dropped for the other lanes
       const uint32_t so = static_cast<uint32_t>(t) * (3 * d * sizeof(float));
@@ -294,7 +433,7 @@ __global__ __launch_bounds__(kThreads) void gruw_reverse_kernel(
     buf ^= 1;
   }
   // nu at the sequence's first step: dL/dh0 of its row
-  if (q == 0 && live && g_h0 != nullptr) g_h0[static_cast<size_t>(sp.seq) * d + col] = nu;
+  if (rl.wr && live && g_h0 != nullptr) g_h0[static_cast<size_t>(sp.seq) * d + col] = nu;
 }
 
 // ---------------------------------------------------------------------------
@@ -404,7 +543,7 @@ __device__ __forceinline__ void await_block_n(StagedN& st, const IterSrc& src, s
   }
 }
 
-__device__ __forceinline__ void store_block_n(float (*x)[kS][DW], float (*v)[kQ * kP],
+__device__ __forceinline__ void store_block_n(float (*x)[kS][DW], float (*v)[kVec],
                                               const StagedN& st, int dh) {
   const int cc = static_cast<int>(threadIdx.x) & (DW - 1);
   const bool live = cc < dh;
@@ -424,33 +563,33 @@ __global__ __launch_bounds__(kThreads) void gruw_newton_kernel(
     int n_rows, int K, float omega, const int* __restrict__ cu, int* __restrict__ ticket,
     int tag_base, WaitLimit spin) {
   __shared__ float s_x[2][3][kS][DW];
-  __shared__ __attribute__((aligned(16))) float s_v[2][kS][kQ * kP];
-  __shared__ __attribute__((aligned(16))) float s_first[kQ * kP];
-  __shared__ __attribute__((aligned(16))) float s_d[kQ * kP];
-  __shared__ __attribute__((aligned(16))) float s_w[kQ * kP];
-  __shared__ __attribute__((aligned(16))) float s_hr[kQ * kP];
+  __shared__ __attribute__((aligned(16))) float s_v[2][kS][kVec];
+  __shared__ __attribute__((aligned(16))) float s_first[kVec];
+  __shared__ __attribute__((aligned(16))) float s_d[kVec];
+  __shared__ __attribute__((aligned(16))) float s_w[kVec];
+  __shared__ __attribute__((aligned(16))) float s_hr[kVec];
   __shared__ int s_ticket;
   if (threadIdx.x == 0)
     s_ticket = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   const int units = n_rows * H;
   const int k = s_ticket / units, unit = s_ticket % units;
-  const int lane = threadIdx.x & 63;
-  const int c = (threadIdx.x >> 6) * 16 + (lane >> 2), q = lane & 3;
+  const Role rl = role();
+  const int c = rl.c;
   const int sc = slot(c);
   const int head = unit % H;
   const Span sp = span_of(unit / H, T, cu);
   const size_t hoff = static_cast<size_t>(head) * dh * dh;
   float az[kK], ar[kK], an[kK];
-  load_quarter<TX, true>(a_z + hoff, dh, c, q, az);
-  load_quarter<TX, true>(a_r + hoff, dh, c, q, ar);
-  load_quarter<TX, true>(a_n + hoff, dh, c, q, an);
+  load_pair<TX, true>(a_z + hoff, dh, rl, az);
+  load_pair<TX, true>(a_r + hoff, dh, rl, ar);
+  load_pair<TX, true>(a_n + hoff, dh, rl, an);
   const int d = H * dh;
   const bool live = c < dh;
   const size_t col = static_cast<size_t>(head) * dh + c;
   const size_t btd = static_cast<size_t>(B) * T * d;
   // the sequence's initial state (h0 row or zeros) and delta_{t0-1} = 0
-  if (q == 0) {
+  if (rl.wr) {
     s_first[sc] = (live && h0 != nullptr) ? h0[static_cast<size_t>(sp.seq) * d + col] : 0.f;
     s_d[sc] = 0.f;
   }
@@ -462,7 +601,7 @@ __global__ __launch_bounds__(kThreads) void gruw_newton_kernel(
   const size_t row_base = static_cast<size_t>(sp.row) * T * d;
   const rsrc_t ro = make_rsrc(out + row_base,
                               static_cast<uint32_t>(static_cast<size_t>(T) * d * sizeof(TX)));
-  const uint32_t vo = (last && live && q == 0) ? static_cast<uint32_t>(col * sizeof(TX)) : kOOB;
+  const uint32_t vo = (last && live && rl.wr) ? static_cast<uint32_t>(col * sizeof(TX)) : kOOB;
   float delta = 0.f;
   bool gave_up = false;
   {
@@ -486,29 +625,29 @@ __global__ __launch_bounds__(kThreads) void gruw_newton_kernel(
       const float hp = hrow[sc], hin = s_v[buf][s][sc];
       const float xz = s_x[buf][0][s][c], xr = s_x[buf][1][s][c], xn = s_x[buf][2][s][c];
       // gates' h A_z, h A_r and the Jacobian's A_r^T delta, A_z^T delta
-      const float hz = dot_channel(az, hrow + q * kP);
-      const float hr = dot_channel(ar, hrow + q * kP);
-      const float sr = dot_channel(ar, s_d + q * kP);
-      const float sz = dot_channel(az, s_d + q * kP);
+      const float hz = dot_pair(az, hrow, rl);
+      const float hr = dot_pair(ar, hrow, rl);
+      const float sr = dot_pair(ar, s_d, rl);
+      const float sz = dot_pair(az, s_d, rl);
       const float z = fsigmoid(xz + hz), r = fsigmoid(xr + hr);
       const float d5 = hp * r * (1.f - r);
-      if (q == 0) {
+      if (rl.wr) {
         s_w[sc] = r * delta + d5 * sr;
         s_hr[sc] = hp * r;
       }
       __syncthreads();
       // (h r) A_n for the gate n, A_n^T (r delta + d5 A_r^T delta)
-      const float un = dot_channel(an, s_hr + q * kP);
-      const float sn = dot_channel(an, s_w + q * kP);
+      const float un = dot_pair(an, s_hr, rl);
+      const float sn = dot_pair(an, s_w, rl);
       const float n = ftanh(xn + un);
       const float d2 = (n - hp) * z * (1.f - z);
       const float d3 = z * (1.f - n * n);
       const float f = lerp_t(hp, n, z) - hin;
       delta = (1.f - z) * delta + d2 * sz + d3 * sn + f;
       const float h_new = hin + omega * delta;
-      if (q == 0) s_d[sc] = delta;
+      if (rl.wr) s_d[sc] = delta;
       if (dst != nullptr) {
-        if (live && q == 0) st_tagged(dst + wide_at(row_base, t, d, col), h_new, dst_tag);
+        if (live && rl.wr) st_tagged(dst + wide_at(row_base, t, d, col), h_new, dst_tag);
       } else {
         stb<TX>(ro, vo, static_cast<uint32_t>(t) * (d * sizeof(TX)), h_new);
       }
@@ -676,6 +815,35 @@ extern "C" PRNN_API int prnn_gru_wide_newton(const void* wx, const void* a_z, co
     return PRNN_OK;
   });
   timing_end(s);
+  PRNN_HIP(hipGetLastError());
+  return PRNN_OK;
+}
+
+extern "C" PRNN_API int prnn_gru_wide_gates(const void* wx, const float* hp, const void* a_z,
+                                            const void* a_r, const void* a_n, float* z, float* r,
+                                            float* n, int rows, int n_heads, int d_head,
+                                            int dtype, void* stream) {
+  if (rows < 1 || n_heads < 1)
+    return fail(PRNN_ERR_VALUE, "rows and n_heads must be >= 1, got rows=%d n_heads=%d", rows,
+                n_heads);
+  if (d_head < 1 || d_head > gruw::DW)
+    return fail(PRNN_ERR_TYPE, "d_head must be in [1, %d], got %d", gruw::DW, d_head);
+  if (check_dtype(dtype) != PRNN_OK) return PRNN_ERR_TYPE;
+  if (!wx || !hp || !a_z || !a_r || !a_n || !z || !r || !n)
+    return fail(PRNN_ERR_VALUE, "wx, hp, a_z, a_r, a_n, z, r and n must be non-null");
+  // about four workgroups per CU over all heads, whole staging blocks each
+  const int target = (1024 + n_heads - 1) / n_heads;
+  int per = (rows + target - 1) / target;
+  per = ((per + gruw::kS - 1) / gruw::kS) * gruw::kS;
+  const int blocks = (rows + per - 1) / per;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  with_storage(dtype, [&](auto tag) {
+    using TX = decltype(tag);
+    gruw::gruw_gates_kernel<TX><<<dim3(blocks * n_heads), dim3(gruw::kThreads), 0, s>>>(
+        static_cast<const TX*>(wx), hp, static_cast<const TX*>(a_z), static_cast<const TX*>(a_r),
+        static_cast<const TX*>(a_n), z, r, n, rows, per, n_heads, d_head);
+    return PRNN_OK;
+  });
   PRNN_HIP(hipGetLastError());
   return PRNN_OK;
 }

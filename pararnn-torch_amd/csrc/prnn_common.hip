@@ -65,7 +65,7 @@ int clear_words(int* p, size_t n, hipStream_t stream) {
 
 }  // namespace prnn
 
-extern "C" PRNN_API int prnn_abi_version(void) { return 9; }
+extern "C" PRNN_API int prnn_abi_version(void) { return 10; }
 
 extern "C" PRNN_API const char* prnn_last_error(void) { return prnn::last_error_buffer(); }
 

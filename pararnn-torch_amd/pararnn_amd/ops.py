@@ -688,26 +688,25 @@ def _wide_prev(states: Tensor, h0: Tensor | None, cs: Tensor | None) -> Tensor:
     return out
 
 
-def _wide_gates(wx32: Tensor, hp: Tensor, a: tuple[Tensor, Tensor, Tensor]):
+def _wide_gates(wx: Tensor, hp: Tensor, a: tuple[Tensor, Tensor, Tensor], code: int):
     """Gates ``z, r, n`` (fp32 ``(B, T, d)``) of every step from its previous
-    state ``hp``: ``sigmoid(wx_z + h A_z)``, ``sigmoid(wx_r + h A_r)``,
-    ``tanh(wx_n + (h r) A_n)`` per head (cells/para_gru.py:414-467).  The
-    three products are GEMMs over all B*T rows; nothing here depends on the
+    state ``hp`` (fp32): ``sigmoid(wx_z + h A_z)``, ``sigmoid(wx_r + h A_r)``,
+    ``tanh(wx_n + (h r) A_n)`` per head (cells/para_gru.py:414-467), in one
+    HIP launch over all B*T rows (``prnn_gru_wide_gates``; ``wx`` and ``a`` in
+    the storage dtype ``code``, contiguous).  Nothing here depends on the
     Newton walk, so it runs as wide parallel work before it."""
-    batch, time, three_d = wx32.shape
+    batch, time, _ = wx.shape
     n_heads, d_head, _ = a[0].shape
-    rows = batch * time
-    hv = hp.reshape(rows, n_heads, d_head).transpose(0, 1)  # (H, rows, dh)
-    x = wx32.reshape(rows, 3, n_heads, d_head)
-
-    def mix(v: Tensor, m: Tensor) -> Tensor:  # (H, rows, dh) @ (H, dh, dh) -> (rows, H, dh)
-        return torch.bmm(v, m).transpose(0, 1)
-
-    z = torch.sigmoid(mix(hv, a[0]) + x[:, 0])
-    r = torch.sigmoid(mix(hv, a[1]) + x[:, 1])
-    n = torch.tanh(mix(hv * r.transpose(0, 1), a[2]) + x[:, 2])
     shape = (batch, time, n_heads * d_head)
-    return z.reshape(shape), r.reshape(shape), n.reshape(shape)
+    z, r, n = (torch.empty(shape, dtype=torch.float32, device=wx.device) for _ in range(3))
+    lib = _lib.load()
+    with torch.cuda.device(wx.device):
+        rc = lib.prnn_gru_wide_gates(
+            _ptr(wx), _ptr(hp), _ptr(a[0]), _ptr(a[1]), _ptr(a[2]), _ptr(z), _ptr(r), _ptr(n),
+            batch * time, n_heads, d_head, code, _stream(wx.device),
+        )
+    _lib.check(rc, "gru head gates (wide heads)")
+    return z, r, n
 
 
 def _gru_head_wide(wx, a_z, a_r, a_n, h0, max_iters, omega, code, cs=None):
@@ -716,22 +715,21 @@ def _gru_head_wide(wx, a_z, a_r, a_n, h0, max_iters, omega, code, cs=None):
     walks, one per (iteration, sequence, head), evaluate the gates in the walk
     and run the iterations a block or two of steps apart
     (``PARARNN_AMD_WIDE_FUSED=0``: one launch per iteration, as for K = 1).
-    K = 1: the gates at the guess (GEMMs) and one HIP walk per (sequence,
-    head) for ``delta`` and the update (``prnn_gru_wide_walk``).  fp32 work;
+    K = 1: the gates at the guess (``prnn_gru_wide_gates``) and one HIP walk
+    per (sequence, head) for ``delta`` and the update (``prnn_gru_wide_walk``).  fp32 work;
     the result in ``wx``'s dtype."""
     n_heads, d_head, _ = a_z.shape
     batch, time, _ = wx.shape
     d_h = n_heads * d_head
-    wx32 = wx.float()
-    a32 = tuple(t.float().contiguous() for t in (a_z, a_r, a_n))
+    wx_c = wx.contiguous()
+    a_k = tuple(t.contiguous() for t in (a_z, a_r, a_n))
     h0_32 = None if h0 is None else h0.float()
-    zeros = wx32.new_zeros(batch, time, d_h)
-    hp0 = _wide_prev(zeros, h0_32, cs)
-    z, _, n = _wide_gates(wx32, hp0, a32)
+    zeros = wx.new_zeros(batch, time, d_h, dtype=torch.float32)
+    hp0 = _wide_prev(zeros, h0_32, cs).contiguous()
+    z, _, n = _wide_gates(wx_c, hp0, a_k, code)
     states = torch.lerp(hp0, n, z)
     if max_iters == 0:
         return states.to(wx.dtype)
-    a_k = tuple(t.contiguous() for t in (a_z, a_r, a_n))
     cs32 = None if cs is None else cs.to(device=wx.device, dtype=torch.int32).contiguous()
     n_seq = 0 if cs32 is None else int(cs32.numel()) - 1
     lib = _lib.load()
@@ -741,7 +739,6 @@ def _gru_head_wide(wx, a_z, a_r, a_n, h0, max_iters, omega, code, cs=None):
         nbytes = lib.prnn_gru_wide_newton_workspace_size(batch, time, n_heads, d_head, max_iters)
         ws, tag = _slstm_workspace(nbytes, wx.device)
         h0_c = None if h0_32 is None else h0_32.contiguous()
-        wx_c = wx.contiguous()
         guess = states.contiguous()
         with torch.cuda.device(wx.device):
             rc = lib.prnn_gru_wide_newton(
@@ -755,7 +752,7 @@ def _gru_head_wide(wx, a_z, a_r, a_n, h0, max_iters, omega, code, cs=None):
     out = None
     for it in range(max_iters):
         hp = _wide_prev(states, h0_32, cs).contiguous()
-        z, r, n = (t.contiguous() for t in _wide_gates(wx32, hp, a32))
+        z, r, n = _wide_gates(wx_c, hp, a_k, code)
         last = it == max_iters - 1
         narrow = last and wx.dtype != torch.float32
         out = wx.new_empty(batch, time, d_h) if narrow else states
@@ -772,7 +769,7 @@ def _gru_head_wide(wx, a_z, a_r, a_n, h0, max_iters, omega, code, cs=None):
 
 def _gru_head_wide_backward(wx, a_z, a_r, a_n, h0, states, grad, code, cs32=None):
     """Eq. 2.6 backward of the wide tier at ``H* = states``: the gates at H*
-    (GEMMs), one HIP adjoint walk per (sequence, head)
+    (``prnn_gru_wide_gates``), one HIP adjoint walk per (sequence, head)
     (``prnn_gru_wide_reverse``: dL/dwx and dL/dh0), then dL/dA as GEMMs over
     the B*T rows, ``sum_t X_t^T D_t`` with X = h_prev (z, r) or h_prev r (n)."""
     n_heads, d_head, _ = a_z.shape
@@ -780,11 +777,9 @@ def _gru_head_wide_backward(wx, a_z, a_r, a_n, h0, states, grad, code, cs32=None
     d_h = n_heads * d_head
     cs = None if cs32 is None else cs32.long()
     rows = batch if cs32 is None else int(cs32.numel()) - 1
-    wx32 = wx.float()
-    a32 = tuple(t.float().contiguous() for t in (a_z, a_r, a_n))
-    hp = _wide_prev(states.float(), None if h0 is None else h0.float(), cs).contiguous()
-    z, r, n = (t.contiguous() for t in _wide_gates(wx32, hp, a32))
     a_k = tuple(t.contiguous() for t in (a_z, a_r, a_n))
+    hp = _wide_prev(states.float(), None if h0 is None else h0.float(), cs).contiguous()
+    z, r, n = _wide_gates(wx.contiguous(), hp, a_k, code)
     grad = grad.contiguous()
     g_wx = torch.empty(batch, time, 3 * d_h, dtype=torch.float32, device=wx.device)
     g_h0 = torch.zeros(rows, d_h, dtype=torch.float32, device=wx.device)

@@ -303,3 +303,34 @@ def test_one_launch_more_workgroups_than_fit_at_once(monkeypatch):
     err = (one - per).abs().max().item()
     print(f"  max|one launch - per iteration| {err:.2e}", flush=True)
     assert err <= 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gates_kernel_matches_the_oracle_cell(dtype):
+    """prnn_gru_wide_gates against the oracle's head cell (reference
+    cells/para_gru.py:414-467) at the same previous states, with h0 rows at
+    the sequence starts, d_head = 96 (dead lanes) and a row count that is not
+    a multiple of the staging block."""
+    from oracle.gru_head import _acts
+    from pararnn_amd import ops
+
+    print(f"case wide heads gates kernel {dtype}", flush=True)
+    g = torch.Generator().manual_seed(0)
+    H, dh, B, T = 2, 96, 3, 37
+    d = H * dh
+    p = O.GRUHeadParams(torch.randn(3 * d, 5, generator=g), torch.randn(3 * d, generator=g),
+                        *(torch.randn(H, dh, dh, generator=g) * 0.1 for _ in range(3)))
+    wx = torch.randn(B, T, 3 * d, generator=g).to(dtype)
+    states = torch.randn(B, T, d, generator=g)
+    h0 = torch.randn(B, d, generator=g)
+    mats = tuple(m.to(dtype) for m in p.mats())
+    hp = ops._wide_prev(states, h0, None)
+    code = {torch.float32: 0, torch.bfloat16: 1}[dtype]
+    z, r, n = ops._wide_gates(wx.to(DEV), hp.to(DEV).contiguous(),
+                              tuple(m.to(DEV).contiguous() for m in mats), code)
+    p32 = O.GRUHeadParams(p.W, p.b, *(m.float() for m in mats))
+    a = _acts(p32, hp, wx.float())
+    for name, got, want in (("z", z, a["z"]), ("r", r, a["r"]), ("n", n, a["n"])):
+        err = (got.cpu() - want.reshape(B, T, d)).abs().max().item()
+        print(f"  {name}: max|gpu - oracle| {err:.2e}", flush=True)
+        assert err <= 2e-6

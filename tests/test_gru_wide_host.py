@@ -1,33 +1,8 @@
 """Host-side pieces of the wide-head GRU tier (64 < d_head <= 128) that run
-without a GPU: the gates the host computes before each HIP walk, against the
-oracle's head cell (reference cells/para_gru.py:414-467), and the
-previous-state layout with and without packed sequences."""
+without a GPU: the previous-state layout with and without packed sequences,
+and the argument checks of the one-launch entry point."""
 
 import torch
-
-import oracle as O
-from oracle.gru_head import _acts
-
-
-def test_wide_gates_match_the_oracle_cell():
-    from pararnn_amd.ops import _wide_gates, _wide_prev
-
-    g = torch.Generator().manual_seed(0)
-    H, dh, B, T = 2, 96, 2, 17
-    d = H * dh
-    p = O.GRUHeadParams(torch.randn(3 * d, 5, generator=g), torch.randn(3 * d, generator=g),
-                        *(torch.randn(H, dh, dh, generator=g) * 0.1 for _ in range(3)))
-    wx = torch.randn(B, T, 3 * d, generator=g)
-    states = torch.randn(B, T, d, generator=g)
-    h0 = torch.randn(B, d, generator=g)
-    hp = _wide_prev(states, h0, None)
-    assert torch.equal(hp[:, 0], h0) and torch.equal(hp[:, 1:], states[:, :-1])
-    z, r, n = _wide_gates(wx, hp, p.mats())
-    a = _acts(p, hp, wx)
-    for got, want in ((z, a["z"]), (r, a["r"]), (n, a["n"])):
-        assert (got - want.reshape(B, T, d)).abs().max().item() <= 1e-6
-    new = torch.lerp(hp, n, z)
-    assert (new - a["new"]).abs().max().item() <= 1e-6
 
 
 def test_wide_prev_of_a_packed_stream():
@@ -69,4 +44,24 @@ def test_one_launch_newton_entry_refuses_bad_arguments():
 
     for rc in (call(K=0), call(K=65), call(out=fake), call(guess=None),
                call(ws_bytes=need - 1), call(dh_=129)):
+        assert rc != 0
+
+
+def test_gates_entry_refuses_bad_arguments():
+    """prnn_gru_wide_gates checks sizes, dtype and pointers before launching."""
+    import ctypes
+    import os
+
+    import pytest
+    from pararnn_amd import _lib
+
+    if not os.path.exists(_lib.lib_path()):
+        pytest.skip("library not built (run __graft_entry__.build())")
+    lib = _lib.load()
+    p = ctypes.c_void_p(4096)
+
+    def call(rows=10, H=2, dh=96, dtype=0, z=p):
+        return lib.prnn_gru_wide_gates(p, p, p, p, p, z, p, p, rows, H, dh, dtype, None)
+
+    for rc in (call(rows=0), call(H=0), call(dh=0), call(dh=129), call(dtype=7), call(z=None)):
         assert rc != 0
