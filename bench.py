@@ -542,16 +542,16 @@ def main() -> int:
                                                                   eps=cell.eps), reps)
         ms_newton = _time_kernel(torch, lambda: newton_slstm_fused(
             wx, r, None, init, max_iters=2, omega=1.0, eps=cell.eps), reps)
-        ms_gemm = _time(torch, lambda: cell.W_x(x), reps)
+        ms_gemm = _time(torch, lambda: cell.W_x(x), 2 * reps, warm=3)
         cfg = NewtonConfig(max_iters=K, picard_iters=P, residual_atol=None, residual_fail=None,
                            picard_adapt=False)
-        ms_e2e = _time(torch, lambda: newton_apply(cell, x, cfg), max(3, reps // 2), warm=1)
+        ms_e2e = _time(torch, lambda: newton_apply(cell, x, cfg), 2 * reps, warm=3)
         # The same with the residual gate on (one extra cell pass and its
         # reduction), and the literal NewtonConfig(max_iters=2) once: what the
         # default auto-P, Picard adapt and the residual gate resolve to.
         cfg_gate = NewtonConfig(max_iters=K, picard_iters=P, residual_atol=1e-5,
                                 residual_fail=None, picard_adapt=False)
-        ms_gate = _time(torch, lambda: newton_apply(cell, x, cfg_gate), max(3, reps // 2), warm=1)
+        ms_gate = _time(torch, lambda: newton_apply(cell, x, cfg_gate), 2 * reps, warm=3)
         pinned = _pinned_report(torch, cell, wx, step())
         literal = _literal_config(torch, cell, x)
 
