@@ -345,11 +345,11 @@ PRNN_API int prnn_gru_wide_gates(const void* wx, const float* hp, const void* a_
                                  int rows, int n_heads, int d_head, int dtype, void* stream);
 
 /* All max_iters Newton iterations of the wide tier in one launch, without the
- * host's gate GEMMs: iteration k's workgroup per (sequence, head) evaluates
- * the gates at the previous iterate inside its walk and runs a block or two
- * of steps behind iteration k - 1, whose iterate it reads from the workspace
- * as tagged words (same replaced reference tier as above; its program per
- * (b, head) runs the iterations one after another).  wx (B, T, 3d) and A_*
+ * host's gate GEMMs: per iteration k and (sequence, head), gate workgroups
+ * evaluate the gates at the previous iterate and a walk consumes them, a few
+ * blocks of steps behind iteration k - 1; the iterate and the gates pass
+ * through the workspace as tagged words (same replaced reference tier as
+ * above; its program per (b, head) runs the iterations one after another).  wx (B, T, 3d) and A_*
  * in `dtype`; h0 (rows, d) fp32 or NULL; guess (B, T, d) fp32, the initial
  * iterate; out (B, T, d) in `dtype` receives the last iterate and must not
  * alias guess.  Workspace: prnn_gru_wide_newton_workspace_size; tag_base as

@@ -1,8 +1,8 @@
 // ParaGRU mix='head' with wide heads (64 < d_head <= 128): the Newton
 // iteration's linear solve and the eq. 2.6 adjoint as walks over time, one
 // workgroup per (sequence, head) -- and, for K >= 2 iterations, one launch
-// whose K walks per (sequence, head) run a block or two of steps apart
-// (gruw_newton_kernel, further down).
+// whose K walks per (sequence, head) run a few blocks of steps apart, each
+// fed by a workgroup evaluating its gates (gruw_newton_kernel, further down).
 //
 // This is the tier of the reference's streamed head kernel
 // (kernels/newton_gru_head.py:765-960, _newton_head_stream_a_kernel: one
@@ -23,6 +23,8 @@
 // and a barrier only to broadcast the two vectors the next products read:
 // two barriers per step.  fp32 throughout; channels >= d_head and entries
 // k >= d_head hold zeros.
+#include <type_traits>
+
 #include "prnn_common.h"
 #include "pararnn_amd.h"
 #include "prnn_host.h"
@@ -437,20 +439,26 @@ __global__ __launch_bounds__(kThreads) void gruw_reverse_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// All K Newton iterations in one launch.  Iteration k's walk needs only the
-// previous iterate H_{k-1} at steps t-1 and t, so the K walks of a (sequence,
-// head) run together, iteration k a block or two of steps behind iteration
-// k - 1: K x (sequences x heads) workgroups, each evaluating its own gates at
-// H_{k-1} inside the walk (h A_z, h A_r and (h r) A_n beside the three
-// Jacobian products) instead of as GEMMs between launches.
-//   H_{k-1} (k >= 1) passes through the workspace as tagged words
-// {value, tag}, written step by step by iteration k - 1 and read with a tag
-// check, so no flag or fence orders them (the device-coherent words of the
-// sLSTM look-back); iteration 0 reads the initial guess, the last iteration
-// writes `out`.  Workgroups take their (k, sequence, head) from a ticket in
-// start order, k-major, so the iteration a workgroup waits on is running or
-// done.  A wait that outlasts the spin limit gives up -- the value reads as
-// NaN and the call's status word is set -- so every workgroup ends.
+// All K Newton iterations in one launch.  Iteration k needs only the previous
+// iterate H_{k-1} (at steps t-1 and t), so the iterations of a (sequence,
+// head) run together, iteration k a few blocks of steps behind iteration
+// k - 1, with two workgroups per (iteration, sequence, head):
+//  * a gate workgroup evaluates the gates z, r, n of iteration k at H_{k-1}
+//    (h A_z, h A_r, then (h r) A_n, a block of steps per barrier as in
+//    gruw_gates_kernel) as soon as H_{k-1} reaches them;
+//  * a walk workgroup runs the linear solve of iteration k on those gates
+//    (the three Jacobian products per step, as in gruw_walk_kernel).
+// The gate products do not depend on the walk, so they run on other CUs and
+// leave the walk's per-step critical path with the Jacobian alone.
+//   H_{k-1} (k >= 1) and the gates pass through the workspace as tagged
+// words {value, tag}, written step by step and read with a tag check, so no
+// flag or fence orders them (the device-coherent words of the sLSTM
+// look-back); iteration 0 reads the initial guess, the last iteration writes
+// `out`.  Workgroups take their (k, role, sequence, head) from a ticket in
+// start order -- iteration-major, gates before walks -- so whatever a
+// workgroup waits on belongs to a running or finished workgroup.  A wait that
+// outlasts the spin limit gives up -- the value reads as NaN and the call's
+// status word is set -- so every workgroup ends.
 
 // Bounded waits: `limit` polling rounds, then the wait gives up and ORs 1
 // into *status (the word after PRNN_TAG_SPAN ticket counters, where
@@ -460,205 +468,430 @@ struct WaitLimit {
   int limit;
 };
 
-constexpr int kXP = 3 * kS * DW / kThreads;  // staged wx values per lane (12)
-constexpr int kSP = kS * DW / kThreads;      // staged iterate values per lane (4)
+// Steps per staged block of the one-launch solve: half the walks' kS, so
+// that the raw tagged words a lane prefetches for the next block (three
+// gates and the iterate per step) fit beside the three A's in registers.
+constexpr int kSN = 8;
+constexpr int kRows = kThreads / DW;                  // steps one load pass covers (4)
+constexpr int kXP = 3 * kSN * DW / kThreads;  // staged gate or wx values per lane (6)
+constexpr int kSP = kSN * DW / kThreads;      // staged iterate values per lane (2)
 
+// A staged value: plain fp32 (wx converted, the initial guess) or a raw
+// tagged word.  Tagged words are kept as loaded and tested only when the
+// block is consumed: testing them at the load would make every load of the
+// block wait for its round trip in turn.
+template <bool TAGGED>
+using Raw = typename std::conditional<TAGGED, unsigned long long, float>::type;
+
+// Staged inputs of one block: x (wx for the gate workgroups, the gates z, r,
+// n for the walks; gate j / kSP, step tid / DW + kRows (j % kSP)) and the
+// iterate H_{k-1} (step tid / DW + kRows j, shifted by vshift).
+template <bool XT, bool VT>
 struct StagedN {
-  float x[kXP];  // wx, gate j / 4, step tid / DW + 4 (j % 4)
-  float v[kSP];  // H_{k-1}, step tid / DW + 4 j
-  bool ok[kSP];  // the tagged word carried this call's tag
+  Raw<XT> x[kXP];
+  Raw<VT> v[kSP];
 };
 
-// Where a step's iterate comes from: the initial guess (plain fp32) or the
-// tagged words of the previous iteration.
-struct IterSrc {
-  const float* plain;
-  const unsigned long long* words;
-  int tag;
+// Sources: the gate words of this iteration (gate g at g * plane) or wx;
+// the previous iteration's words or the initial guess.
+template <typename TX>
+struct NewtonSrc {
+  const TX* wx;
+  const unsigned long long* gwords;
+  size_t plane;
+  int gtag;
+  const float* guess;
+  const unsigned long long* hwords;
+  int htag;
 };
 
 __device__ __forceinline__ size_t wide_at(size_t row_base, int t, int d, size_t col) {
   return row_base + static_cast<size_t>(t) * d + col;
 }
 
-template <typename TX>
-__device__ __forceinline__ void load_block_n(StagedN& st, const TX* __restrict__ wx,
-                                             const IterSrc& src, size_t row_base, int d,
-                                             int head, int dh, int t_first, int t_lo,
-                                             int t_hi) {
-  const int cc = min(static_cast<int>(threadIdx.x) & (DW - 1), dh - 1);
-  const size_t col = static_cast<size_t>(head) * dh + cc;
+__device__ __forceinline__ unsigned long long ld_word(const unsigned long long* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Where lane tid's staged values of the block at t_first live (steps clamped
+// into [t_lo, t_hi]; clamped values are never used).
+struct BlockAt {
+  size_t row_base;
+  int d;
+  size_t col;
+  int t_first, vshift, t_lo, t_hi;
+  __device__ __forceinline__ size_t x_at(int j) const {
+    const int s = static_cast<int>(threadIdx.x) / DW + kRows * (j % kSP);
+    return wide_at(row_base, min(max(t_first + s, t_lo), t_hi), d, col);
+  }
+  __device__ __forceinline__ size_t v_at(int j) const {
+    const int s = static_cast<int>(threadIdx.x) / DW + kRows * j;
+    return wide_at(row_base, min(max(t_first + s + vshift, t_lo), t_hi), d, col);
+  }
+};
+
+template <bool XT, bool VT, typename TX>
+__device__ __forceinline__ void load_block_n(StagedN<XT, VT>& st, const NewtonSrc<TX>& src,
+                                             const BlockAt& at, int d) {
 #pragma unroll
   for (int j = 0; j < kXP; ++j) {
-    const int s = static_cast<int>(threadIdx.x) / DW + 4 * (j % 4);
-    const int t = min(max(t_first + s, t_lo), t_hi);
-    st.x[j] = ld(wx + 3 * wide_at(row_base, t, d, 0) + static_cast<size_t>(j / 4) * d + col);
+    if constexpr (XT) {
+      st.x[j] = ld_word(src.gwords + (j / kSP) * src.plane + at.x_at(j));
+    } else {
+      // wx rows hold the three gates' blocks of d one after the other
+      const size_t a = at.x_at(j);
+      const size_t row = (a - at.col) / d;
+      st.x[j] = ld(src.wx + row * 3 * d + static_cast<size_t>(j / kSP) * d + at.col);
+    }
   }
 #pragma unroll
   for (int j = 0; j < kSP; ++j) {
-    const int s = static_cast<int>(threadIdx.x) / DW + 4 * j;
-    const size_t at = wide_at(row_base, min(max(t_first + s, t_lo), t_hi), d, col);
-    if (src.words != nullptr) {
-      st.ok[j] = ld_tagged(src.words + at, src.tag, st.v[j]);
-    } else {
-      st.v[j] = src.plain[at];
-      st.ok[j] = true;
-    }
+    if constexpr (VT)
+      st.v[j] = ld_word(src.hwords + at.v_at(j));
+    else
+      st.v[j] = src.guess[at.v_at(j)];
   }
 }
 
-// Polls the staged tagged words that were not yet written.  Bounded: after
-// `limit` rounds the lane gives up (NaN for what is missing, status word set)
-// and, through `gave_up`, waits no more for the rest of its walk.
-static_assert(kSP == 4, "await_block_n tests four staged words");
-__device__ __forceinline__ void await_block_n(StagedN& st, const IterSrc& src, size_t row_base,
-                                              int d, int head, int dh, int t_first, int t_lo,
-                                              int t_hi, const WaitLimit& spin, bool& gave_up) {
-  if (src.words == nullptr) return;
-  const int cc = min(static_cast<int>(threadIdx.x) & (DW - 1), dh - 1);
-  const size_t col = static_cast<size_t>(head) * dh + cc;
-  int rounds = 0;
-  bool pending = !(st.ok[0] && st.ok[1] && st.ok[2] && st.ok[3]);
-  while (pending) {
-    if (gave_up || ++rounds > spin.limit) {
+__device__ __forceinline__ bool word_ok(unsigned long long w, int tag) {
+  return static_cast<int>(w >> 32) == tag;
+}
+__device__ __forceinline__ float word_val(unsigned long long w) {
+  return __uint_as_float(static_cast<uint32_t>(w));
+}
+
+// Waits until every staged tagged word carries this call's tag, reloading
+// the ones that do not.  Bounded: after `limit` rounds the lane gives up
+// (NaN for what is missing, status word set) and, through `gave_up`, waits
+// no more for the rest of its walk.
+template <bool XT, bool VT, typename TX>
+__device__ __forceinline__ void await_block_n(StagedN<XT, VT>& st, const NewtonSrc<TX>& src,
+                                              const BlockAt& at_in, const WaitLimit& spin,
+                                              bool& gave_up) {
+  if constexpr (XT || VT) {
+    // The reload addresses are recomputed from an opaque copy of the block's
+    // first step: otherwise the compiler keeps the load's 16 addresses live
+    // through the whole block (and spills).
+    BlockAt at = at_in;
+    asm volatile("" : "+s"(at.t_first));
+    auto missing = [&]() {
+      bool m = false;
+      if constexpr (XT) {
 #pragma unroll
-      for (int j = 0; j < kSP; ++j)
-        if (!st.ok[j]) st.v[j] = __builtin_nanf("");
-      if (!gave_up)
-        __hip_atomic_fetch_or(spin.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      gave_up = true;
-      break;
-    }
-    __builtin_amdgcn_s_sleep(2);
-    pending = false;
+        for (int j = 0; j < kXP; ++j) m |= !word_ok(st.x[j], src.gtag);
+      }
+      if constexpr (VT) {
 #pragma unroll
-    for (int j = 0; j < kSP; ++j) {
-      if (!st.ok[j]) {
-        const int s = static_cast<int>(threadIdx.x) / DW + 4 * j;
-        const size_t at = wide_at(row_base, min(max(t_first + s, t_lo), t_hi), d, col);
-        st.ok[j] = ld_tagged(src.words + at, src.tag, st.v[j]);
-        pending |= !st.ok[j];
+        for (int j = 0; j < kSP; ++j) m |= !word_ok(st.v[j], src.htag);
+      }
+      return m;
+    };
+    int rounds = 0;
+    while (missing()) {
+      if (gave_up || ++rounds > spin.limit) {
+        const unsigned long long nan_w = 0x7fc00000ull;
+        if constexpr (XT) {
+#pragma unroll
+          for (int j = 0; j < kXP; ++j)
+            if (!word_ok(st.x[j], src.gtag))
+              st.x[j] = (static_cast<unsigned long long>(static_cast<uint32_t>(src.gtag)) << 32) |
+                        nan_w;
+        }
+        if constexpr (VT) {
+#pragma unroll
+          for (int j = 0; j < kSP; ++j)
+            if (!word_ok(st.v[j], src.htag))
+              st.v[j] = (static_cast<unsigned long long>(static_cast<uint32_t>(src.htag)) << 32) |
+                        nan_w;
+        }
+        if (!gave_up)
+          __hip_atomic_fetch_or(spin.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        gave_up = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+      if constexpr (XT) {
+#pragma unroll
+        for (int j = 0; j < kXP; ++j)
+          if (!word_ok(st.x[j], src.gtag))
+            st.x[j] = ld_word(src.gwords + (j / kSP) * src.plane + at.x_at(j));
+      }
+      if constexpr (VT) {
+#pragma unroll
+        for (int j = 0; j < kSP; ++j)
+          if (!word_ok(st.v[j], src.htag)) st.v[j] = ld_word(src.hwords + at.v_at(j));
       }
     }
   }
 }
 
-__device__ __forceinline__ void store_block_n(float (*x)[kS][DW], float (*v)[kVec],
-                                              const StagedN& st, int dh) {
+template <bool XT, bool VT>
+__device__ __forceinline__ void store_block_n(float (*x)[kSN][DW], float (*v)[kVec],
+                                              const StagedN<XT, VT>& st, int dh) {
   const int cc = static_cast<int>(threadIdx.x) & (DW - 1);
   const bool live = cc < dh;
 #pragma unroll
-  for (int j = 0; j < kXP; ++j)
-    x[j / 4][static_cast<int>(threadIdx.x) / DW + 4 * (j % 4)][cc] = live ? st.x[j] : 0.f;
+  for (int j = 0; j < kXP; ++j) {
+    float val;
+    if constexpr (XT)
+      val = word_val(st.x[j]);
+    else
+      val = st.x[j];
+    x[j / kSP][static_cast<int>(threadIdx.x) / DW + kRows * (j % kSP)][cc] = live ? val : 0.f;
+  }
 #pragma unroll
-  for (int j = 0; j < kSP; ++j)
-    v[static_cast<int>(threadIdx.x) / DW + 4 * j][slot(cc)] = live ? st.v[j] : 0.f;
+  for (int j = 0; j < kSP; ++j) {
+    float val;
+    if constexpr (VT)
+      val = word_val(st.v[j]);
+    else
+      val = st.v[j];
+    v[static_cast<int>(threadIdx.x) / DW + kRows * j][slot(cc)] = live ? val : 0.f;
+  }
+}
+
+// Gate workgroups per walk: one evaluates a block's gates more slowly than
+// the walk consumes them, so each walk is fed by two taking alternate blocks.
+constexpr int kGateWGs = 2;
+
+struct NewtonShared {
+  float x[2][3][kSN][DW];                               // wx (gates) or z, r, n (walks)
+  __attribute__((aligned(16))) float v[2][kSN][kVec];   // H_{k-1}
+  __attribute__((aligned(16))) float first[kVec];      // the sequence's initial state
+  __attribute__((aligned(16))) float d[kVec];          // walks: delta_{t-1}
+  __attribute__((aligned(16))) float w[kVec];          // walks: r delta + d5 A_r^T delta
+  __attribute__((aligned(16))) float hr[kSN][kVec];     // gates: (h r) rows of a block
+};
+
+// What both roles of a workgroup share.
+struct NewtonCtx {
+  Role rl;
+  int c, sc, head, d, dh, k, K, T;
+  bool live;
+  size_t col, btd, row_base;
+  Span sp;
+};
+
+// Gate workgroup `part` of iteration k: blocks part, part + kGateWGs, ... of
+// the span.  Step t of a block needs H_{k-1} at t - 1 (the sequence's
+// initial state at its first step), staged as the block's rows (vshift -1).
+//   z = sigmoid(wx_z + h A_z), r = sigmoid(wx_r + h A_r) for the block's
+// steps, then n = tanh(wx_n + (h r) A_n) after one barrier (reference
+// cells/para_gru.py:443-467), each written as a tagged word.
+template <bool VT, typename TX>
+__device__ __forceinline__ void newton_gates(NewtonShared& sh, const NewtonCtx& cx,
+                                             const NewtonSrc<TX>& src, int part,
+                                             const float az[kK], const float ar[kK],
+                                             const float an[kK],
+                                             unsigned long long* __restrict__ gk, int gtag,
+                                             const WaitLimit& spin) {
+  const Span& sp = cx.sp;
+  const Role& rl = cx.rl;
+  const int c = cx.c, sc = cx.sc;
+  int tb = sp.t0 + part * kSN;
+  if (tb >= sp.t1) return;
+  const int cc = min(static_cast<int>(threadIdx.x) & (DW - 1), cx.dh - 1);
+  const size_t ccol = static_cast<size_t>(cx.head) * cx.dh + cc;
+  auto at_of = [&](int t_first) {
+    return BlockAt{cx.row_base, cx.d, ccol, t_first, -1, sp.t0, sp.t1 - 1};
+  };
+  bool gave_up = false;
+  {
+    StagedN<false, VT> st;
+    load_block_n(st, src, at_of(tb), cx.d);
+    await_block_n(st, src, at_of(tb), spin, gave_up);
+    store_block_n(sh.x[0], sh.v[0], st, cx.dh);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (; tb < sp.t1; tb += kGateWGs * kSN) {
+    const int tn = tb + kGateWGs * kSN;
+    const bool more = tn < sp.t1;
+    StagedN<false, VT> next;
+    if (more) load_block_n(next, src, at_of(tn), cx.d);
+    const int ns = min(kSN, sp.t1 - tb);
+    auto gates_zr = [&](int s) {
+      const float* hrow = tb + s == sp.t0 ? sh.first : sh.v[buf][s];
+      const float hz = dot_pair(az, hrow, rl);
+      const float hr = dot_pair(ar, hrow, rl);
+      const float z = fsigmoid(sh.x[buf][0][s][c] + hz);
+      const float r = fsigmoid(sh.x[buf][1][s][c] + hr);
+      if (rl.wr) {
+        sh.hr[s][sc] = hrow[sc] * r;
+        if (cx.live) {
+          const size_t a = wide_at(cx.row_base, tb + s, cx.d, cx.col);
+          st_tagged(gk + a, z, gtag);
+          st_tagged(gk + cx.btd + a, r, gtag);
+        }
+      }
+    };
+    auto gate_n = [&](int s) {
+      const float un = dot_pair(an, sh.hr[s], rl);
+      const float n = ftanh(sh.x[buf][2][s][c] + un);
+      if (rl.wr && cx.live)
+        st_tagged(gk + 2 * cx.btd + wide_at(cx.row_base, tb + s, cx.d, cx.col), n, gtag);
+    };
+    if (ns == kSN) {
+#pragma unroll
+      for (int s = 0; s < kSN; ++s) gates_zr(s);
+    } else {
+      for (int s = 0; s < ns; ++s) gates_zr(s);
+    }
+    __syncthreads();
+    if (ns == kSN) {
+#pragma unroll
+      for (int s = 0; s < kSN; ++s) gate_n(s);
+    } else {
+      for (int s = 0; s < ns; ++s) gate_n(s);
+    }
+    if (more) {
+      await_block_n(next, src, at_of(tn), spin, gave_up);
+      store_block_n(sh.x[buf ^ 1], sh.v[buf ^ 1], next, cx.dh);
+    }
+    // (h r) rows and the staging buffers are rewritten after this
+    __syncthreads();
+    buf ^= 1;
+  }
+}
+
+// Walk of iteration k: delta_t = J_t delta_{t-1} + F_t, F_t = lerp(h, n, z) -
+// H_t, then H_t + omega delta_t (the gates and H_{k-1} from the staged
+// blocks); iterations before the last write tagged words, the last `out`.
+template <bool VT, typename TX>
+__device__ __forceinline__ void newton_walk(NewtonShared& sh, const NewtonCtx& cx,
+                                            const NewtonSrc<TX>& src, const float az[kK],
+                                            const float ar[kK], const float an[kK],
+                                            unsigned long long* __restrict__ iters,
+                                            TX* __restrict__ out, float omega, int tag_base,
+                                            const WaitLimit& spin) {
+  const Span& sp = cx.sp;
+  const Role& rl = cx.rl;
+  const int c = cx.c, sc = cx.sc;
+  const int cc = min(static_cast<int>(threadIdx.x) & (DW - 1), cx.dh - 1);
+  const size_t ccol = static_cast<size_t>(cx.head) * cx.dh + cc;
+  auto at_of = [&](int t_first) {
+    return BlockAt{cx.row_base, cx.d, ccol, t_first, 0, sp.t0, sp.t1 - 1};
+  };
+  bool gave_up = false;
+  {
+    StagedN<true, VT> st;
+    load_block_n(st, src, at_of(sp.t0), cx.d);
+    await_block_n(st, src, at_of(sp.t0), spin, gave_up);
+    store_block_n(sh.x[0], sh.v[0], st, cx.dh);
+  }
+  __syncthreads();
+  const bool last = cx.k == cx.K - 1;
+  unsigned long long* dst = last ? nullptr : iters + cx.k * cx.btd;
+  const int dst_tag = tag_base + 1 + cx.k;
+  const rsrc_t ro = make_rsrc(out + cx.row_base,
+                              static_cast<uint32_t>(static_cast<size_t>(cx.T) * cx.d * sizeof(TX)));
+  const uint32_t vo =
+      (last && cx.live && rl.wr) ? static_cast<uint32_t>(cx.col * sizeof(TX)) : kOOB;
+  float delta = 0.f;
+  int buf = 0;
+  for (int tb = sp.t0; tb < sp.t1; tb += kSN) {
+    const bool more = tb + kSN < sp.t1;
+    StagedN<true, VT> next;
+    if (more) load_block_n(next, src, at_of(tb + kSN), cx.d);
+    const int ns = min(kSN, sp.t1 - tb);
+    for (int s = 0; s < ns; ++s) {
+      const int t = tb + s;
+      // previous state (the sequence's initial state, the other buffer's
+      // last row, or this block's previous row) and the iterate at t
+      const float* hrow = s > 0 ? sh.v[buf][s - 1] : tb == sp.t0 ? sh.first : sh.v[buf ^ 1][kSN - 1];
+      const float hp = hrow[sc];
+      const float hin = sh.v[buf][s][sc];
+      const float z = sh.x[buf][0][s][c], r = sh.x[buf][1][s][c], n = sh.x[buf][2][s][c];
+      // A_r^T delta and A_z^T delta (delta_{t-1} broadcast in sh.d)
+      const float sr = dot_pair(ar, sh.d, rl);
+      const float sz = dot_pair(az, sh.d, rl);
+      const float d5 = hp * r * (1.f - r);
+      if (rl.wr) sh.w[sc] = r * delta + d5 * sr;
+      __syncthreads();
+      // A_n^T (r delta + d5 A_r^T delta)
+      const float sn = dot_pair(an, sh.w, rl);
+      const float d2 = (n - hp) * z * (1.f - z);
+      const float d3 = z * (1.f - n * n);
+      const float f = lerp_t(hp, n, z) - hin;
+      delta = (1.f - z) * delta + d2 * sz + d3 * sn + f;
+      const float h_new = hin + omega * delta;
+      if (rl.wr) sh.d[sc] = delta;
+      if (dst != nullptr) {
+        if (cx.live && rl.wr) st_tagged(dst + wide_at(cx.row_base, t, cx.d, cx.col), h_new, dst_tag);
+      } else {
+        stb<TX>(ro, vo, static_cast<uint32_t>(t) * (cx.d * sizeof(TX)), h_new);
+      }
+      __syncthreads();
+    }
+    if (more) {
+      await_block_n(next, src, at_of(tb + kSN), spin, gave_up);
+      store_block_n(sh.x[buf ^ 1], sh.v[buf ^ 1], next, cx.dh);
+      __syncthreads();
+    }
+    buf ^= 1;
+  }
 }
 
 template <typename TX>
 __global__ __launch_bounds__(kThreads) void gruw_newton_kernel(
     const TX* __restrict__ wx, const TX* __restrict__ a_z, const TX* __restrict__ a_r,
     const TX* __restrict__ a_n, const float* __restrict__ h0, const float* __restrict__ guess,
-    unsigned long long* __restrict__ iters, TX* __restrict__ out, int B, int T, int H, int dh,
-    int n_rows, int K, float omega, const int* __restrict__ cu, int* __restrict__ ticket,
-    int tag_base, WaitLimit spin) {
-  __shared__ float s_x[2][3][kS][DW];
-  __shared__ __attribute__((aligned(16))) float s_v[2][kS][kVec];
-  __shared__ __attribute__((aligned(16))) float s_first[kVec];
-  __shared__ __attribute__((aligned(16))) float s_d[kVec];
-  __shared__ __attribute__((aligned(16))) float s_w[kVec];
-  __shared__ __attribute__((aligned(16))) float s_hr[kVec];
+    unsigned long long* __restrict__ iters, unsigned long long* __restrict__ gates,
+    TX* __restrict__ out, int B, int T, int H, int dh, int n_rows, int K, float omega,
+    const int* __restrict__ cu, int* __restrict__ ticket, int tag_base, WaitLimit spin) {
+  __shared__ NewtonShared sh;
   __shared__ int s_ticket;
   if (threadIdx.x == 0)
     s_ticket = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
+  // per iteration: kGateWGs gate workgroups per (sequence, head), then the walks
   const int units = n_rows * H;
-  const int k = s_ticket / units, unit = s_ticket % units;
-  const Role rl = role();
-  const int c = rl.c;
-  const int sc = slot(c);
-  const int head = unit % H;
-  const Span sp = span_of(unit / H, T, cu);
-  const size_t hoff = static_cast<size_t>(head) * dh * dh;
+  const int per_iter = (kGateWGs + 1) * units;
+  const int k = s_ticket / per_iter, q = s_ticket % per_iter;
+  const bool gate_role = q < kGateWGs * units;
+  const int part = q / units;
+  const int unit = q % units;
+  NewtonCtx cx;
+  cx.rl = role();
+  cx.c = cx.rl.c;
+  cx.sc = slot(cx.c);
+  cx.head = unit % H;
+  cx.sp = span_of(unit / H, T, cu);
+  cx.d = H * dh;
+  cx.dh = dh;
+  cx.k = k;
+  cx.K = K;
+  cx.T = T;
+  cx.live = cx.c < dh;
+  cx.col = static_cast<size_t>(cx.head) * dh + cx.c;
+  cx.btd = static_cast<size_t>(B) * T * cx.d;
+  cx.row_base = static_cast<size_t>(cx.sp.row) * T * cx.d;
+  const size_t hoff = static_cast<size_t>(cx.head) * dh * dh;
   float az[kK], ar[kK], an[kK];
-  load_pair<TX, true>(a_z + hoff, dh, rl, az);
-  load_pair<TX, true>(a_r + hoff, dh, rl, ar);
-  load_pair<TX, true>(a_n + hoff, dh, rl, an);
-  const int d = H * dh;
-  const bool live = c < dh;
-  const size_t col = static_cast<size_t>(head) * dh + c;
-  const size_t btd = static_cast<size_t>(B) * T * d;
+  load_pair<TX, true>(a_z + hoff, dh, cx.rl, az);
+  load_pair<TX, true>(a_r + hoff, dh, cx.rl, ar);
+  load_pair<TX, true>(a_n + hoff, dh, cx.rl, an);
   // the sequence's initial state (h0 row or zeros) and delta_{t0-1} = 0
-  if (rl.wr) {
-    s_first[sc] = (live && h0 != nullptr) ? h0[static_cast<size_t>(sp.seq) * d + col] : 0.f;
-    s_d[sc] = 0.f;
+  if (cx.rl.wr) {
+    sh.first[cx.sc] =
+        (cx.live && h0 != nullptr) ? h0[static_cast<size_t>(cx.sp.seq) * cx.d + cx.col] : 0.f;
+    sh.d[cx.sc] = 0.f;
   }
-  if (sp.t0 >= sp.t1) return;
-  const IterSrc src{guess, k == 0 ? nullptr : iters + (k - 1) * btd, tag_base + k};
-  const bool last = k == K - 1;
-  unsigned long long* dst = last ? nullptr : iters + k * btd;
-  const int dst_tag = tag_base + 1 + k;
-  const size_t row_base = static_cast<size_t>(sp.row) * T * d;
-  const rsrc_t ro = make_rsrc(out + row_base,
-                              static_cast<uint32_t>(static_cast<size_t>(T) * d * sizeof(TX)));
-  const uint32_t vo = (last && live && rl.wr) ? static_cast<uint32_t>(col * sizeof(TX)) : kOOB;
-  float delta = 0.f;
-  bool gave_up = false;
-  {
-    StagedN st;
-    load_block_n(st, wx, src, row_base, d, head, dh, sp.t0, sp.t0, sp.t1 - 1);
-    await_block_n(st, src, row_base, d, head, dh, sp.t0, sp.t0, sp.t1 - 1, spin, gave_up);
-    store_block_n(s_x[0], s_v[0], st, dh);
-  }
-  __syncthreads();
-  int buf = 0;
-  for (int tb = sp.t0; tb < sp.t1; tb += kS) {
-    const bool more = tb + kS < sp.t1;
-    StagedN next;
-    if (more) load_block_n(next, wx, src, row_base, d, head, dh, tb + kS, sp.t0, sp.t1 - 1);
-    const int ns = min(kS, sp.t1 - tb);
-    for (int s = 0; s < ns; ++s) {
-      const int t = tb + s;
-      // previous state (all channels): the sequence's initial state, the
-      // other buffer's last row, or this block's previous row
-      const float* hrow = s > 0 ? s_v[buf][s - 1] : tb == sp.t0 ? s_first : s_v[buf ^ 1][kS - 1];
-      const float hp = hrow[sc], hin = s_v[buf][s][sc];
-      const float xz = s_x[buf][0][s][c], xr = s_x[buf][1][s][c], xn = s_x[buf][2][s][c];
-      // gates' h A_z, h A_r and the Jacobian's A_r^T delta, A_z^T delta
-      const float hz = dot_pair(az, hrow, rl);
-      const float hr = dot_pair(ar, hrow, rl);
-      const float sr = dot_pair(ar, s_d, rl);
-      const float sz = dot_pair(az, s_d, rl);
-      const float z = fsigmoid(xz + hz), r = fsigmoid(xr + hr);
-      const float d5 = hp * r * (1.f - r);
-      if (rl.wr) {
-        s_w[sc] = r * delta + d5 * sr;
-        s_hr[sc] = hp * r;
-      }
-      __syncthreads();
-      // (h r) A_n for the gate n, A_n^T (r delta + d5 A_r^T delta)
-      const float un = dot_pair(an, s_hr, rl);
-      const float sn = dot_pair(an, s_w, rl);
-      const float n = ftanh(xn + un);
-      const float d2 = (n - hp) * z * (1.f - z);
-      const float d3 = z * (1.f - n * n);
-      const float f = lerp_t(hp, n, z) - hin;
-      delta = (1.f - z) * delta + d2 * sz + d3 * sn + f;
-      const float h_new = hin + omega * delta;
-      if (rl.wr) s_d[sc] = delta;
-      if (dst != nullptr) {
-        if (live && rl.wr) st_tagged(dst + wide_at(row_base, t, d, col), h_new, dst_tag);
-      } else {
-        stb<TX>(ro, vo, static_cast<uint32_t>(t) * (d * sizeof(TX)), h_new);
-      }
-      __syncthreads();
-    }
-    if (more) {
-      await_block_n(next, src, row_base, d, head, dh, tb + kS, sp.t0, sp.t1 - 1, spin, gave_up);
-      store_block_n(s_x[buf ^ 1], s_v[buf ^ 1], next, dh);
-      __syncthreads();
-    }
-    buf ^= 1;
+  if (cx.sp.t0 >= cx.sp.t1) return;
+  unsigned long long* gk = gates + static_cast<size_t>(k) * 3 * cx.btd;
+  const NewtonSrc<TX> src{wx,    gk,    cx.btd, tag_base + 1 + k, guess,
+                          k == 0 ? nullptr : iters + (k - 1) * cx.btd, tag_base + k};
+  // iteration 0 reads the plain initial guess, later ones the tagged iterate
+  if (gate_role) {
+    if (k == 0)
+      newton_gates<false>(sh, cx, src, part, az, ar, an, gk, tag_base + 1 + k, spin);
+    else
+      newton_gates<true>(sh, cx, src, part, az, ar, an, gk, tag_base + 1 + k, spin);
+  } else {
+    if (k == 0)
+      newton_walk<false>(sh, cx, src, az, ar, an, iters, out, omega, tag_base, spin);
+    else
+      newton_walk<true>(sh, cx, src, az, ar, an, iters, out, omega, tag_base, spin);
   }
 }
 
@@ -678,19 +911,24 @@ static int check(int B, int T, int H, int dh, int dtype, const int* cu, int n_se
 
 // Workspace of the one-launch Newton solve: PRNN_TAG_SPAN ticket counters
 // (the first is used) and the status word, then the tagged iterates
-// H_0 .. H_{K-2}, (B, T, d) 64-bit words each.
+// H_0 .. H_{K-2} and the tagged gates z, r, n of iterations 0 .. K-1,
+// (B, T, d) 64-bit words each.
 struct NewtonWs {
   int* counters;
   unsigned long long* iters;
+  unsigned long long* gates;
   size_t clear_words;  // 32-bit words from `counters` to the end
 };
 
 static NewtonWs carve_newton(void* base, int B, int T, int d, int K, size_t* total) {
   Carver cv(base);
   NewtonWs w;
+  const size_t plane = static_cast<size_t>(B) * T * d;
   w.counters = static_cast<int*>(cv.take(sizeof(int) * (PRNN_TAG_SPAN + 1)));
-  w.iters = static_cast<unsigned long long*>(cv.take(
-      sizeof(unsigned long long) * static_cast<size_t>(K > 1 ? K - 1 : 0) * B * T * d));
+  w.iters = static_cast<unsigned long long*>(
+      cv.take(sizeof(unsigned long long) * static_cast<size_t>(K > 1 ? K - 1 : 0) * plane));
+  w.gates = static_cast<unsigned long long*>(
+      cv.take(sizeof(unsigned long long) * 3 * static_cast<size_t>(K) * plane));
   w.clear_words = cv.used / sizeof(int);
   *total = cv.used;
   return w;
@@ -803,15 +1041,17 @@ extern "C" PRNN_API int prnn_gru_wide_newton(const void* wx, const void* a_z, co
   if (rc != PRNN_OK) return rc;
   const int rows = cu_seqlens ? n_seq : B;
   const gruw::WaitLimit lim{w.counters + PRNN_TAG_SPAN, spin_limit()};
+  // per iteration and (sequence, head): kGateWGs gate workgroups and a walk
+  const int grid = (gruw::kGateWGs + 1) * max_iters * rows * n_heads;
   timing_begin(s);
   with_storage(dtype, [&](auto tag) {
     using TX = decltype(tag);
     gruw::gruw_newton_kernel<TX>
-        <<<dim3(max_iters * rows * n_heads), dim3(gruw::kThreads), 0, s>>>(
+        <<<dim3(grid), dim3(gruw::kThreads), 0, s>>>(
             static_cast<const TX*>(wx), static_cast<const TX*>(a_z),
             static_cast<const TX*>(a_r), static_cast<const TX*>(a_n), h0, guess, w.iters,
-            static_cast<TX*>(out), B, T, n_heads, d_head, rows, max_iters, omega, cu_seqlens,
-            w.counters, tag_base, lim);
+            w.gates, static_cast<TX*>(out), B, T, n_heads, d_head, rows, max_iters, omega,
+            cu_seqlens, w.counters, tag_base, lim);
     return PRNN_OK;
   });
   timing_end(s);

@@ -711,9 +711,9 @@ def _wide_gates(wx: Tensor, hp: Tensor, a: tuple[Tensor, Tensor, Tensor], code: 
 
 def _gru_head_wide(wx, a_z, a_r, a_n, h0, max_iters, omega, code, cs=None):
     """Forward of the wide tier: the initial guess ``f(h_prev0, x)``, then the
-    Newton iterations.  K >= 2: one launch (``prnn_gru_wide_newton``) whose
-    walks, one per (iteration, sequence, head), evaluate the gates in the walk
-    and run the iterations a block or two of steps apart
+    Newton iterations.  K >= 2: one launch (``prnn_gru_wide_newton``) in which,
+    per (iteration, sequence, head), gate workgroups feed a walk, the
+    iterations a few blocks of steps apart
     (``PARARNN_AMD_WIDE_FUSED=0``: one launch per iteration, as for K = 1).
     K = 1: the gates at the guess (``prnn_gru_wide_gates``) and one HIP walk
     per (sequence, head) for ``delta`` and the update (``prnn_gru_wide_walk``).  fp32 work;
@@ -734,7 +734,7 @@ def _gru_head_wide(wx, a_z, a_r, a_n, h0, max_iters, omega, code, cs=None):
     n_seq = 0 if cs32 is None else int(cs32.numel()) - 1
     lib = _lib.load()
     if max_iters >= 2 and os.environ.get("PARARNN_AMD_WIDE_FUSED", "1") != "0":
-        # all iterations in one launch, each a block or two behind the last
+        # all iterations in one launch, each a few blocks behind the last
         out = wx.new_empty(batch, time, d_h)
         nbytes = lib.prnn_gru_wide_newton_workspace_size(batch, time, n_heads, d_head, max_iters)
         ws, tag = _slstm_workspace(nbytes, wx.device)

@@ -252,11 +252,11 @@ def test_stacked_layers_and_verify_agreement():
 @pytest.mark.parametrize("packed", [False, True])
 @pytest.mark.parametrize("K", [2, 5])
 def test_one_launch_matches_launch_per_iteration(packed, K, monkeypatch):
-    """K >= 2 runs all iterations in one launch (gates evaluated in the walks,
-    iteration k a block or two behind k - 1, iterates passed as tagged words);
-    PARARNN_AMD_WIDE_FUSED=0 runs one walk per iteration after host GEMMs for
-    the gates.  Same algebra, gates summed in another order: they agree to
-    float32 rounding, and no wait gives up (PARARNN_AMD_CHECK_STATUS=1)."""
+    """K >= 2 runs all iterations in one launch (gate workgroups feeding the
+    walks, iteration k a few blocks behind k - 1, gates and iterates passed
+    as tagged words); PARARNN_AMD_WIDE_FUSED=0 runs the gates kernel and one
+    walk per iteration.  The same arithmetic: they agree to float32 rounding,
+    and no wait gives up (PARARNN_AMD_CHECK_STATUS=1)."""
     from pararnn_amd import newton_apply
 
     print(f"case wide heads one launch vs per iteration packed={packed} K={K}", flush=True)
@@ -284,13 +284,15 @@ def test_one_launch_matches_launch_per_iteration(packed, K, monkeypatch):
 
 
 def test_one_launch_more_workgroups_than_fit_at_once(monkeypatch):
-    """K x B x H = 3 x 64 x 8 = 1536 one-launch workgroups, more than the GPU
-    holds at once: the ticket order (iteration-major) lets every waiting walk
-    find its predecessor running or done, so the solve completes without a
-    wait giving up, equal to one launch per iteration."""
+    """K x B x H = 3 x 64 x 8 = 1536 (iteration, sequence, head) triples,
+    three workgroups each (two gate workgroups and a walk): 4608 one-launch
+    workgroups, more than the GPU holds at once.  The ticket order
+    (iteration-major, gates before walks) lets every waiting workgroup find
+    what it waits on running or done, so the solve completes without a wait
+    giving up, equal to one launch per iteration."""
     from pararnn_amd import NewtonConfig, ParaGRU, newton_apply
 
-    print("case wide heads one launch, 1536 workgroups (B=64, H=8, K=3)", flush=True)
+    print("case wide heads one launch, 4608 workgroups (B=64, H=8, K=3)", flush=True)
     torch.manual_seed(21)
     cell = ParaGRU(16, 1024, mix="head", n_heads=8).to(DEV)
     x = torch.randn(64, 96, 16, device=DEV)
