@@ -468,13 +468,14 @@ struct WaitLimit {
   int limit;
 };
 
-// Steps per staged block of the one-launch solve: half the walks' kS, so
-// that the raw tagged words a lane prefetches for the next block (three
-// gates and the iterate per step) fit beside the three A's in registers.
-constexpr int kSN = 8;
-constexpr int kRows = kThreads / DW;                  // steps one load pass covers (4)
-constexpr int kXP = 3 * kSN * DW / kThreads;  // staged gate or wx values per lane (6)
-constexpr int kSP = kSN * DW / kThreads;      // staged iterate values per lane (2)
+// Steps per staged block of the one-launch solve (the raw tagged words a
+// lane prefetches for the next block, three gates and the iterate per step,
+// sit beside the three A's in registers: 8-step blocks ran 6.67 ms at the
+// bench's wide shape, 16-step blocks 6.40 ms).
+constexpr int kSN = 16;
+constexpr int kRows = kThreads / DW;          // steps one load pass covers (4)
+constexpr int kXP = 3 * kSN * DW / kThreads;  // staged gate or wx values per lane (12)
+constexpr int kSP = kSN * DW / kThreads;      // staged iterate values per lane (4)
 
 // A staged value: plain fp32 (wx converted, the initial guess) or a raw
 // tagged word.  Tagged words are kept as loaded and tested only when the
@@ -610,16 +611,15 @@ __device__ __forceinline__ void await_block_n(StagedN<XT, VT>& st, const NewtonS
         break;
       }
       __builtin_amdgcn_s_sleep(2);
+      // reload the whole block (the words already there read the same)
       if constexpr (XT) {
 #pragma unroll
         for (int j = 0; j < kXP; ++j)
-          if (!word_ok(st.x[j], src.gtag))
-            st.x[j] = ld_word(src.gwords + (j / kSP) * src.plane + at.x_at(j));
+          st.x[j] = ld_word(src.gwords + (j / kSP) * src.plane + at.x_at(j));
       }
       if constexpr (VT) {
 #pragma unroll
-        for (int j = 0; j < kSP; ++j)
-          if (!word_ok(st.v[j], src.htag)) st.v[j] = ld_word(src.hwords + at.v_at(j));
+        for (int j = 0; j < kSP; ++j) st.v[j] = ld_word(src.hwords + at.v_at(j));
       }
     }
   }
@@ -788,6 +788,9 @@ __device__ __forceinline__ void newton_walk(NewtonShared& sh, const NewtonCtx& c
   const uint32_t vo =
       (last && cx.live && rl.wr) ? static_cast<uint32_t>(cx.col * sizeof(TX)) : kOOB;
   float delta = 0.f;
+  // this lane's word of the iterate at the current step (iterations before the last)
+  unsigned long long* dst_t =
+      dst == nullptr ? nullptr : dst + wide_at(cx.row_base, sp.t0, cx.d, cx.col);
   int buf = 0;
   for (int tb = sp.t0; tb < sp.t1; tb += kSN) {
     const bool more = tb + kSN < sp.t1;
@@ -817,7 +820,8 @@ __device__ __forceinline__ void newton_walk(NewtonShared& sh, const NewtonCtx& c
       const float h_new = hin + omega * delta;
       if (rl.wr) sh.d[sc] = delta;
       if (dst != nullptr) {
-        if (cx.live && rl.wr) st_tagged(dst + wide_at(cx.row_base, t, cx.d, cx.col), h_new, dst_tag);
+        if (cx.live && rl.wr) st_tagged(dst_t, h_new, dst_tag);
+        dst_t += cx.d;
       } else {
         stb<TX>(ro, vo, static_cast<uint32_t>(t) * (cx.d * sizeof(TX)), h_new);
       }
