@@ -442,10 +442,11 @@ __global__ __launch_bounds__(kThreads) void gruw_reverse_kernel(
 // All K Newton iterations in one launch.  Iteration k needs only the previous
 // iterate H_{k-1} (at steps t-1 and t), so the iterations of a (sequence,
 // head) run together, iteration k a few blocks of steps behind iteration
-// k - 1, with two workgroups per (iteration, sequence, head):
-//  * a gate workgroup evaluates the gates z, r, n of iteration k at H_{k-1}
+// k - 1, with kGateWGs + 1 workgroups per (iteration, sequence, head):
+//  * gate workgroups evaluate the gates z, r, n of iteration k at H_{k-1}
 //    (h A_z, h A_r, then (h r) A_n, a block of steps per barrier as in
-//    gruw_gates_kernel) as soon as H_{k-1} reaches them;
+//    gruw_gates_kernel; alternate blocks each) as soon as H_{k-1} reaches
+//    them;
 //  * a walk workgroup runs the linear solve of iteration k on those gates
 //    (the three Jacobian products per step, as in gruw_walk_kernel).
 // The gate products do not depend on the walk, so they run on other CUs and
@@ -521,9 +522,12 @@ struct BlockAt {
   int d;
   size_t col;
   int t_first, vshift, t_lo, t_hi;
-  __device__ __forceinline__ size_t x_at(int j) const {
+  __device__ __forceinline__ int x_step(int j) const {
     const int s = static_cast<int>(threadIdx.x) / DW + kRows * (j % kSP);
-    return wide_at(row_base, min(max(t_first + s, t_lo), t_hi), d, col);
+    return min(max(t_first + s, t_lo), t_hi);
+  }
+  __device__ __forceinline__ size_t x_at(int j) const {
+    return wide_at(row_base, x_step(j), d, col);
   }
   __device__ __forceinline__ size_t v_at(int j) const {
     const int s = static_cast<int>(threadIdx.x) / DW + kRows * j;
@@ -540,9 +544,8 @@ __device__ __forceinline__ void load_block_n(StagedN<XT, VT>& st, const NewtonSr
       st.x[j] = ld_word(src.gwords + (j / kSP) * src.plane + at.x_at(j));
     } else {
       // wx rows hold the three gates' blocks of d one after the other
-      const size_t a = at.x_at(j);
-      const size_t row = (a - at.col) / d;
-      st.x[j] = ld(src.wx + row * 3 * d + static_cast<size_t>(j / kSP) * d + at.col);
+      st.x[j] = ld(src.wx + 3 * wide_at(at.row_base, at.x_step(j), d, 0) +
+                   static_cast<size_t>(j / kSP) * d + at.col);
     }
   }
 #pragma unroll
