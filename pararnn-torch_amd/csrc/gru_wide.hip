@@ -885,7 +885,11 @@ __global__ __launch_bounds__(kThreads) void gruw_newton_kernel(
     sh.d[cx.sc] = 0.f;
   }
   if (cx.sp.t0 >= cx.sp.t1) return;
-  unsigned long long* gk = gates + static_cast<size_t>(k) * 3 * cx.btd;
+  // Iterations k and k + 2 share gate words: the gate workgroups of k + 2
+  // reach block b only after the iterate of k + 1 covers it, i.e. after the
+  // walk of k has finished block b and so read its gates for the last time
+  // (distinct tags keep the two iterations' words apart).
+  unsigned long long* gk = gates + static_cast<size_t>(k % 2) * 3 * cx.btd;
   const NewtonSrc<TX> src{wx,    gk,    cx.btd, tag_base + 1 + k, guess,
                           k == 0 ? nullptr : iters + (k - 1) * cx.btd, tag_base + k};
   // iteration 0 reads the plain initial guess, later ones the tagged iterate
@@ -918,8 +922,8 @@ static int check(int B, int T, int H, int dh, int dtype, const int* cu, int n_se
 
 // Workspace of the one-launch Newton solve: PRNN_TAG_SPAN ticket counters
 // (the first is used) and the status word, then the tagged iterates
-// H_0 .. H_{K-2} and the tagged gates z, r, n of iterations 0 .. K-1,
-// (B, T, d) 64-bit words each.
+// H_0 .. H_{K-2} and the tagged gates z, r, n of two iterations (even and
+// odd k), (B, T, d) 64-bit words each.
 struct NewtonWs {
   int* counters;
   unsigned long long* iters;
@@ -935,7 +939,7 @@ static NewtonWs carve_newton(void* base, int B, int T, int d, int K, size_t* tot
   w.iters = static_cast<unsigned long long*>(
       cv.take(sizeof(unsigned long long) * static_cast<size_t>(K > 1 ? K - 1 : 0) * plane));
   w.gates = static_cast<unsigned long long*>(
-      cv.take(sizeof(unsigned long long) * 3 * static_cast<size_t>(K) * plane));
+      cv.take(sizeof(unsigned long long) * 3 * static_cast<size_t>(K > 1 ? 2 : 1) * plane));
   w.clear_words = cv.used / sizeof(int);
   *total = cv.used;
   return w;

@@ -709,15 +709,24 @@ def _wide_gates(wx: Tensor, hp: Tensor, a: tuple[Tensor, Tensor, Tensor], code: 
     return z, r, n
 
 
+def _wide_workspace_cap(dev: torch.device) -> int:
+    """Largest one-launch workspace the wide tier takes (a quarter of the
+    device's memory: 8 bytes per element for each of K - 1 iterates and six
+    gate planes); larger solves run one launch per iteration instead, whose
+    buffers are a few fp32 copies of the states."""
+    return torch.cuda.get_device_properties(dev).total_memory // 4
+
+
 def _gru_head_wide(wx, a_z, a_r, a_n, h0, max_iters, omega, code, cs=None):
     """Forward of the wide tier: the initial guess ``f(h_prev0, x)``, then the
     Newton iterations.  K >= 2: one launch (``prnn_gru_wide_newton``) in which,
     per (iteration, sequence, head), gate workgroups feed a walk, the
     iterations a few blocks of steps apart
     (``PARARNN_AMD_WIDE_FUSED=0``: one launch per iteration, as for K = 1).
-    K = 1: the gates at the guess (``prnn_gru_wide_gates``) and one HIP walk
-    per (sequence, head) for ``delta`` and the update (``prnn_gru_wide_walk``).  fp32 work;
-    the result in ``wx``'s dtype."""
+    K = 1 (and solves whose one-launch workspace exceeds ``_wide_workspace_cap``):
+    the gates at the iterate (``prnn_gru_wide_gates``) and one HIP walk per
+    (sequence, head) for ``delta`` and the update (``prnn_gru_wide_walk``), per
+    iteration.  fp32 work; the result in ``wx``'s dtype."""
     n_heads, d_head, _ = a_z.shape
     batch, time, _ = wx.shape
     d_h = n_heads * d_head
@@ -733,10 +742,11 @@ def _gru_head_wide(wx, a_z, a_r, a_n, h0, max_iters, omega, code, cs=None):
     cs32 = None if cs is None else cs.to(device=wx.device, dtype=torch.int32).contiguous()
     n_seq = 0 if cs32 is None else int(cs32.numel()) - 1
     lib = _lib.load()
-    if max_iters >= 2 and os.environ.get("PARARNN_AMD_WIDE_FUSED", "1") != "0":
+    nbytes = lib.prnn_gru_wide_newton_workspace_size(batch, time, n_heads, d_head, max_iters)
+    if (max_iters >= 2 and os.environ.get("PARARNN_AMD_WIDE_FUSED", "1") != "0"
+            and nbytes <= _wide_workspace_cap(wx.device)):
         # all iterations in one launch, each a few blocks behind the last
         out = wx.new_empty(batch, time, d_h)
-        nbytes = lib.prnn_gru_wide_newton_workspace_size(batch, time, n_heads, d_head, max_iters)
         ws, tag = _slstm_workspace(nbytes, wx.device)
         h0_c = None if h0_32 is None else h0_32.contiguous()
         guess = states.contiguous()

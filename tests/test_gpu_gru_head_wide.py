@@ -307,6 +307,23 @@ def test_one_launch_more_workgroups_than_fit_at_once(monkeypatch):
     assert err <= 1e-5
 
 
+def test_one_launch_workspace_cap_falls_back(monkeypatch):
+    """A solve whose one-launch workspace exceeds the cap (here: any) runs one
+    launch per iteration: the same result as PARARNN_AMD_WIDE_FUSED=0."""
+    from pararnn_amd import newton_apply, ops
+
+    print("case wide heads one-launch workspace cap", flush=True)
+    cell, _ = _make(2, 96, 5)
+    cell = cell.to(DEV)
+    x = torch.randn(2, 300, 12, generator=torch.Generator().manual_seed(3)).to(DEV)
+    with torch.no_grad():
+        monkeypatch.setattr(ops, "_wide_workspace_cap", lambda dev: 0)
+        capped = newton_apply(cell, x, _cfg(3))
+        monkeypatch.setenv("PARARNN_AMD_WIDE_FUSED", "0")
+        per = newton_apply(cell, x, _cfg(3))
+    assert torch.isfinite(capped).all() and torch.equal(capped, per)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_gates_kernel_matches_the_oracle_cell(dtype):
     """prnn_gru_wide_gates against the oracle's head cell (reference
