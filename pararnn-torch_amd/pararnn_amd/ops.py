@@ -709,6 +709,31 @@ def _wide_gates(wx: Tensor, hp: Tensor, a: tuple[Tensor, Tensor, Tensor], code: 
     return z, r, n
 
 
+def _wide_guess(wx: Tensor, a: tuple[Tensor, Tensor, Tensor], h0: Tensor | None,
+                cs: Tensor | None, code: int) -> Tensor:
+    """The initial guess ``f(h_prev0, x)`` (fp32), ``h_prev0 = 0`` except h0's
+    row at each sequence's first step (reference solvers/newton/__init__.py:
+    925-940).  With a zero previous state the cell is elementwise, ``lerp(0,
+    tanh(wx_n), sigmoid(wx_z))``; only the first steps with h0 need the gate
+    mat-vecs (``prnn_gru_wide_gates`` on those rows alone)."""
+    batch, time, three_d = wx.shape
+    d_h = three_d // 3
+    z = torch.sigmoid(wx[..., :d_h].float())
+    n = torch.tanh(wx[..., 2 * d_h:].float())
+    states = torch.lerp(torch.zeros_like(n), n, z)
+    if h0 is not None:
+        if cs is None:
+            bi = torch.arange(batch, device=wx.device)
+            ti = torch.zeros(batch, dtype=torch.long, device=wx.device)
+        else:
+            ti = cs[:-1].to(device=wx.device, dtype=torch.long)
+            bi = torch.zeros_like(ti)
+        hp = h0.unsqueeze(0).contiguous()
+        zs, _, ns = _wide_gates(wx[bi, ti].unsqueeze(0).contiguous(), hp, a, code)
+        states[bi, ti] = torch.lerp(hp, ns, zs)[0]
+    return states
+
+
 def _wide_workspace_cap(dev: torch.device) -> int:
     """Largest one-launch workspace the wide tier takes (a quarter of the
     device's memory: 8 bytes per element for each of K - 1 iterates and six
@@ -733,10 +758,7 @@ def _gru_head_wide(wx, a_z, a_r, a_n, h0, max_iters, omega, code, cs=None):
     wx_c = wx.contiguous()
     a_k = tuple(t.contiguous() for t in (a_z, a_r, a_n))
     h0_32 = None if h0 is None else h0.float()
-    zeros = wx.new_zeros(batch, time, d_h, dtype=torch.float32)
-    hp0 = _wide_prev(zeros, h0_32, cs).contiguous()
-    z, _, n = _wide_gates(wx_c, hp0, a_k, code)
-    states = torch.lerp(hp0, n, z)
+    states = _wide_guess(wx_c, a_k, h0_32, cs, code)
     if max_iters == 0:
         return states.to(wx.dtype)
     cs32 = None if cs is None else cs.to(device=wx.device, dtype=torch.int32).contiguous()
