@@ -354,9 +354,10 @@ PRNN_API int prnn_gru_wide_gates(const void* wx, const float* hp, const void* a_
  * (B, T, d) fp32, the initial iterate; out (B, T, d) in `dtype` receives the
  * last iterate and must not alias guess.  Workspace:
  * prnn_gru_wide_newton_workspace_size, 8 bytes per element of (B, T, d) for
- * each of max_iters - 1 iterates and six gate planes; tag_base as for the
- * sLSTM _ex calls (0: the call clears the whole workspace), and the status
- * word of a wait that gave up reads with prnn_slstm_lookback_status.
+ * each of max_iters - 1 iterates and six gate planes (three for max_iters
+ * 1); tag_base as for the sLSTM _ex calls (0: the call clears the whole
+ * workspace), and the status word of a wait that gave up reads with
+ * prnn_slstm_lookback_status.
  * max_iters in [1, PRNN_TAG_SPAN]. */
 PRNN_API size_t prnn_gru_wide_newton_workspace_size(int B, int T, int n_heads, int d_head,
                                                     int max_iters);
