@@ -151,7 +151,8 @@ __device__ __forceinline__ float dppf(float v) {
 }
 
 // sum_k A v for this lane's channel: the lane's 16 entries for both of its
-// pair's channels (two chains each), the sums over the eight parts of the
+// pair's channels (one chain each: two chains per channel and the adds that
+// join them ran 2-3% slower), the sums over the eight parts of the
 // pair (quad_perm [1,0,3,2] and [2,3,0,1] within each quad for both
 // channels, then row_half_mirror between the two quads, which exchanges the
 // channel the other quad keeps).  Every lane of a channel ends with the same
@@ -159,20 +160,19 @@ __device__ __forceinline__ float dppf(float v) {
 __device__ __forceinline__ float dot_pair(const float a[kK], const float* __restrict__ v,
                                           const Role& ro) {
   const float* seg = v + slot(ro.part * kKP);
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float s0 = 0.f, s1 = 0.f;
 #pragma unroll
   for (int kk = 0; kk < kKP; kk += 4) {
     const float4 x = *reinterpret_cast<const float4*>(seg + kk);
-    acc[0] = fmaf(a[2 * kk], x.x, acc[0]);
-    acc[1] = fmaf(a[2 * kk + 1], x.x, acc[1]);
-    acc[2] = fmaf(a[2 * kk + 2], x.y, acc[2]);
-    acc[3] = fmaf(a[2 * kk + 3], x.y, acc[3]);
-    acc[0] = fmaf(a[2 * kk + 4], x.z, acc[0]);
-    acc[1] = fmaf(a[2 * kk + 5], x.z, acc[1]);
-    acc[2] = fmaf(a[2 * kk + 6], x.w, acc[2]);
-    acc[3] = fmaf(a[2 * kk + 7], x.w, acc[3]);
+    s0 = fmaf(a[2 * kk], x.x, s0);
+    s1 = fmaf(a[2 * kk + 1], x.x, s1);
+    s0 = fmaf(a[2 * kk + 2], x.y, s0);
+    s1 = fmaf(a[2 * kk + 3], x.y, s1);
+    s0 = fmaf(a[2 * kk + 4], x.z, s0);
+    s1 = fmaf(a[2 * kk + 5], x.z, s1);
+    s0 = fmaf(a[2 * kk + 6], x.w, s0);
+    s1 = fmaf(a[2 * kk + 7], x.w, s1);
   }
-  float s0 = acc[0] + acc[2], s1 = acc[1] + acc[3];
   s0 += dppf<0xB1>(s0);
   s1 += dppf<0xB1>(s1);
   s0 += dppf<0x4E>(s0);
