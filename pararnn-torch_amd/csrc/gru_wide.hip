@@ -144,10 +144,14 @@ __device__ __forceinline__ void store_block(float (*buf)[kS][DW], const Staged& 
   }
 }
 
+// A lane's value from the lane the DPP control names (every lane has a
+// source for the controls used here).  Written as an update with old = 0 and
+// bound_ctrl so that the compiler folds the move into the add that consumes
+// it (v_add_f32 with a DPP operand): one instruction per reduction step.
 template <int CTRL>
 __device__ __forceinline__ float dppf(float v) {
-  return __builtin_bit_cast(float,
-                            __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 
 // sum_k A v for this lane's channel: the lane's 16 entries for both of its
