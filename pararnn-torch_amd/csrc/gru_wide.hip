@@ -79,15 +79,16 @@ __device__ __forceinline__ Role role() {
 }
 
 // Entries k in [16 j, 16 j + 16) of columns (COL) or rows 2 p, 2 p + 1 of a
-// head's A ((in, out) layout, d_head x d_head), zero outside the head:
-// a[2 kk + i] = A[k][2 p + i] (COL) or A[2 p + i][k].
+// head's A ((in, out) layout, d_head x d_head), zero outside the head, the
+// lane's own channel c first: a[2 kk + i] = A[k][ch_i] (COL) or A[ch_i][k]
+// with ch_0 = c and ch_1 the other channel of the pair.
 template <typename TX, bool COL>
 __device__ __forceinline__ void load_pair(const TX* A, int dh, const Role& ro, float a[kK]) {
 #pragma unroll
   for (int kk = 0; kk < kKP; ++kk)
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int k = ro.part * kKP + kk, ch = 2 * ro.pair + i;
+      const int k = ro.part * kKP + kk, ch = ro.c ^ i;
       const bool in = ch < dh && k < dh;
       a[2 * kk + i] =
           in ? ld(A + (COL ? static_cast<size_t>(k) * dh + ch : static_cast<size_t>(ch) * dh + k))
@@ -158,9 +159,9 @@ __device__ __forceinline__ float dppf(float v) {
 // pair's channels (one chain each: two chains per channel and the adds that
 // join them ran 2-3% slower), the sums over the eight parts of the
 // pair (quad_perm [1,0,3,2] and [2,3,0,1] within each quad for both
-// channels, then row_half_mirror between the two quads, which exchanges the
-// channel the other quad keeps).  Every lane of a channel ends with the same
-// sum.
+// channels, then row_half_mirror between the two quads: each quad sends the
+// sum of the channel it does not keep, which the other quad keeps).  Every
+// lane of a channel ends with the same sum.
 __device__ __forceinline__ float dot_pair(const float a[kK], const float* __restrict__ v,
                                           const Role& ro) {
   const float* seg = v + slot(ro.part * kKP);
@@ -181,9 +182,7 @@ __device__ __forceinline__ float dot_pair(const float a[kK], const float* __rest
   s1 += dppf<0xB1>(s1);
   s0 += dppf<0x4E>(s0);
   s1 += dppf<0x4E>(s1);
-  const bool second = ro.part >= 4;
-  const float keep = second ? s1 : s0, send = second ? s0 : s1;
-  return keep + dppf<0x141>(send);
+  return s0 + dppf<0x141>(s1);
 }
 
 // Forward walk of one Newton iteration: delta_t = J_t delta_{t-1} + F_t with
