@@ -32,6 +32,8 @@
 namespace prnn {
 namespace gruw {
 
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
 constexpr int DW = 128;       // widest head
 constexpr int kParts = 8;     // parts of the contraction index
 constexpr int kKP = DW / kParts;  // contraction entries per lane (16)
@@ -262,99 +264,132 @@ __global__ __launch_bounds__(kThreads) void gruw_walk_kernel(
 // Gates z, r, n of every row (b, t) at its previous state hp: z =
 // sigmoid(wx_z + hp A_z), r = sigmoid(wx_r + hp A_r), n = tanh(wx_n + (hp r)
 // A_n), per head (reference cells/para_gru.py:443-467).  Rows are independent
-// (no walk): workgroup (head, block of rows) stages kS rows of hp and wx at a
-// time, forms h A_z and h A_r for all of them, then, after one barrier for
-// the (hp r) rows, (hp r) A_n.  A column quarter of each A stays in registers
-// as in the walks.  z, r, n fp32 (rows, d).
+// (no walk), so the products are fp32 GEMMs on the matrix cores
+// (v_mfma_f32_16x16x4f32): workgroup (head, block of rows) takes 16 rows at
+// a time, wave w the 16 output channels 16 w .. 16 w + 15.  The contraction
+// index is permuted so that lane (n, g) = (l % 16, l / 16) supplies entries k
+// = 32 g + j (j = 0 .. 31) of row n of hp (eight 16-byte LDS reads) and holds
+// column 16 w + n of each A at the same k in registers.  h A_z and h A_r for
+// the 16 rows, then, after one barrier for the (hp r) rows, (hp r) A_n.  z, r,
+// n fp32 (rows, d).
+constexpr int kGRows = 16;          // rows per MFMA tile
+constexpr int kGPad = DW + 4;       // LDS row stride of the staged rows
+__device__ __forceinline__ floatx4 mfma_f32(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 template <typename TX>
 __global__ __launch_bounds__(kThreads) void gruw_gates_kernel(
     const TX* __restrict__ wx, const float* __restrict__ hp, const TX* __restrict__ a_z,
     const TX* __restrict__ a_r, const TX* __restrict__ a_n, float* __restrict__ z,
     float* __restrict__ r, float* __restrict__ n, int rows, int rows_per_block, int H, int dh) {
-  __shared__ __attribute__((aligned(16))) float s_h[2][kS][kVec];
-  __shared__ __attribute__((aligned(16))) float s_hr[kS][kVec];
-  __shared__ float s_x[2][3][kS][DW];
-  const Role rl = role();
-  const int c = rl.c;
-  const int sc = slot(c);
+  __shared__ __attribute__((aligned(16))) float s_h[kGRows][kGPad];
+  __shared__ __attribute__((aligned(16))) float s_hr[kGRows][kGPad];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = lane & 15, g = lane >> 4;
   const int head = blockIdx.x % H;
   const int r0 = (blockIdx.x / H) * rows_per_block;
   const int r1 = min(rows, r0 + rows_per_block);
   if (r0 >= r1) return;
-  const size_t hoff = static_cast<size_t>(head) * dh * dh;
-  float az[kK], ar[kK], an[kK];
-  load_pair<TX, true>(a_z + hoff, dh, rl, az);
-  load_pair<TX, true>(a_r + hoff, dh, rl, ar);
-  load_pair<TX, true>(a_n + hoff, dh, rl, an);
   const int d = H * dh;
-  const bool live = c < dh;
-  const size_t col = static_cast<size_t>(head) * dh + c;
-  // Staging: lane tid holds channel tid % DW of rows tid / DW + 4 j of the
-  // next block in registers while the current one is computed from LDS.
-  const int cc = static_cast<int>(threadIdx.x) & (DW - 1);
-  const bool live_cc = cc < dh;
-  const size_t col_cc = static_cast<size_t>(head) * dh + min(cc, dh - 1);
-  constexpr int kJ = kS * DW / kThreads;  // rows per lane and block (4)
-  float nh[kJ], nx[3][kJ];
+  const int col = 16 * wave + li;  // this lane's output channel within the head
+  const bool live = col < dh;
+  // B operands: A[32 g + j][col] (zero outside the head)
+  float bz[32], br[32], bn[32];
+  {
+    const size_t hoff = static_cast<size_t>(head) * dh * dh;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const int k = 32 * g + j;
+      const bool in = live && k < dh;
+      const size_t at = hoff + static_cast<size_t>(k) * dh + col;
+      bz[j] = in ? ld(a_z + at) : 0.f;
+      br[j] = in ? ld(a_r + at) : 0.f;
+      bn[j] = in ? ld(a_n + at) : 0.f;
+    }
+  }
+  const size_t ccol = static_cast<size_t>(head) * dh + min(col, dh - 1);
+  // Staging of hp rows: thread tid holds channel tid % DW of rows tid / DW + 4 q.
+  const int sc = static_cast<int>(threadIdx.x) & (DW - 1);
+  const bool live_sc = sc < dh;
+  const size_t scol = static_cast<size_t>(head) * dh + min(sc, dh - 1);
+  constexpr int kQ = kGRows * DW / kThreads;  // 4
+  float nh[kQ], nx[3][4];
   auto fetch = [&](int rb) {
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-      const int s = static_cast<int>(threadIdx.x) / DW + 4 * j;
-      const size_t row = static_cast<size_t>(min(rb + s, r1 - 1));
-      nh[j] = hp[row * d + col_cc];
-#pragma unroll
-      for (int g = 0; g < 3; ++g) nx[g][j] = ld(wx + row * 3 * d + g * d + col_cc);
+    for (int q = 0; q < kQ; ++q) {
+      const int row = min(rb + static_cast<int>(threadIdx.x) / DW + 4 * q, r1 - 1);
+      nh[q] = hp[static_cast<size_t>(row) * d + scol];
     }
-  };
-  auto stash = [&](int buf) {
+    // wx at this lane's output positions: rows 4 g + v, channel col
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-      const int s = static_cast<int>(threadIdx.x) / DW + 4 * j;
-      s_h[buf][s][slot(cc)] = live_cc ? nh[j] : 0.f;
+    for (int v = 0; v < 4; ++v) {
+      const size_t row = static_cast<size_t>(min(rb + 4 * g + v, r1 - 1));
 #pragma unroll
-      for (int g = 0; g < 3; ++g) s_x[buf][g][s][cc] = live_cc ? nx[g][j] : 0.f;
+      for (int gt = 0; gt < 3; ++gt) nx[gt][v] = ld(wx + row * 3 * d + gt * d + ccol);
     }
   };
   fetch(r0);
-  int buf = 0;
-  for (int rb = r0; rb < r1; rb += kS) {
-    stash(buf);
+  for (int rb = r0; rb < r1; rb += kGRows) {
+    float cx[3][4];
+#pragma unroll
+    for (int q = 0; q < kQ; ++q)
+      s_h[static_cast<int>(threadIdx.x) / DW + 4 * q][sc] = live_sc ? nh[q] : 0.f;
+#pragma unroll
+    for (int gt = 0; gt < 3; ++gt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) cx[gt][v] = nx[gt][v];
     __syncthreads();
-    if (rb + kS < r1) fetch(rb + kS);
-    const int ns = min(kS, r1 - rb);
-    auto gates_zr = [&](int s) {
-      const float hz = dot_pair(az, s_h[buf][s], rl);
-      const float hr = dot_pair(ar, s_h[buf][s], rl);
-      const float zv = fsigmoid(s_x[buf][0][s][c] + hz);
-      const float rv = fsigmoid(s_x[buf][1][s][c] + hr);
-      if (rl.wr) {
-        s_hr[s][sc] = s_h[buf][s][sc] * rv;
-        if (live) {
-          const size_t at = static_cast<size_t>(rb + s) * d + col;
-          z[at] = zv;
-          r[at] = rv;
-        }
+    if (rb + kGRows < r1) fetch(rb + kGRows);
+    // A operands: entries 32 g .. 32 g + 31 of row li
+    float av[32];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float4 f = *reinterpret_cast<const float4*>(&s_h[li][32 * g + 4 * q]);
+      av[4 * q] = f.x;
+      av[4 * q + 1] = f.y;
+      av[4 * q + 2] = f.z;
+      av[4 * q + 3] = f.w;
+    }
+    floatx4 accz = {0.f, 0.f, 0.f, 0.f}, accr = accz;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      accz = mfma_f32(av[j], bz[j], accz);
+      accr = mfma_f32(av[j], br[j], accr);
+    }
+    // D layout: rows 4 g + v, channel col
+    float zv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      zv[v] = fsigmoid(cx[0][v] + accz[v]);
+      const float rv = fsigmoid(cx[1][v] + accr[v]);
+      s_hr[4 * g + v][col] = s_h[4 * g + v][col] * rv;
+      const int row = rb + 4 * g + v;
+      if (live && row < r1) {
+        const size_t at = static_cast<size_t>(row) * d + ccol;
+        z[at] = zv[v];
+        r[at] = rv;
       }
-    };
-    auto gate_n = [&](int s) {
-      const float un = dot_pair(an, s_hr[s], rl);
-      const float nv = ftanh(s_x[buf][2][s][c] + un);
-      if (rl.wr && live) n[static_cast<size_t>(rb + s) * d + col] = nv;
-    };
-    if (ns == kS) {
-#pragma unroll
-      for (int s = 0; s < kS; ++s) gates_zr(s);
-    } else {
-      for (int s = 0; s < ns; ++s) gates_zr(s);
     }
     __syncthreads();
-    if (ns == kS) {
 #pragma unroll
-      for (int s = 0; s < kS; ++s) gate_n(s);
-    } else {
-      for (int s = 0; s < ns; ++s) gate_n(s);
+    for (int q = 0; q < 8; ++q) {
+      const float4 f = *reinterpret_cast<const float4*>(&s_hr[li][32 * g + 4 * q]);
+      av[4 * q] = f.x;
+      av[4 * q + 1] = f.y;
+      av[4 * q + 2] = f.z;
+      av[4 * q + 3] = f.w;
     }
-    buf ^= 1;
+    floatx4 accn = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 32; ++j) accn = mfma_f32(av[j], bn[j], accn);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = rb + 4 * g + v;
+      if (live && row < r1) n[static_cast<size_t>(row) * d + ccol] = ftanh(cx[2][v] + accn[v]);
+    }
+    // s_h and s_hr are rewritten for the next rows after this
+    __syncthreads();
   }
 }
 
@@ -807,7 +842,8 @@ __device__ __forceinline__ void newton_walk(NewtonShared& sh, const NewtonCtx& c
       const int t = tb + s;
       // previous state (the sequence's initial state, the other buffer's
       // last row, or this block's previous row) and the iterate at t
-      const float* hrow = s > 0 ? sh.v[buf][s - 1] : tb == sp.t0 ? sh.first : sh.v[buf ^ 1][kSN - 1];
+      const float* hrow =
+          s > 0 ? sh.v[buf][s - 1] : tb == sp.t0 ? sh.first : sh.v[buf ^ 1][kSN - 1];
       const float hp = hrow[sc];
       const float hin = sh.v[buf][s][sc];
       const float z = sh.x[buf][0][s][c], r = sh.x[buf][1][s][c], n = sh.x[buf][2][s][c];
