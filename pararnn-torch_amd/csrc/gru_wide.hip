@@ -482,9 +482,8 @@ __global__ __launch_bounds__(kThreads) void gruw_reverse_kernel(
 // head) run together, iteration k a few blocks of steps behind iteration
 // k - 1, with kGateWGs + 1 workgroups per (iteration, sequence, head):
 //  * gate workgroups evaluate the gates z, r, n of iteration k at H_{k-1}
-//    (h A_z, h A_r, then (h r) A_n, a block of steps per barrier as in
-//    gruw_gates_kernel; alternate blocks each) as soon as H_{k-1} reaches
-//    them;
+//    (h A_z, h A_r, then (h r) A_n, a block of steps per barrier; every
+//    kGateWGs-th block each) as soon as H_{k-1} reaches them;
 //  * a walk workgroup runs the linear solve of iteration k on those gates
 //    (the three Jacobian products per step, as in gruw_walk_kernel).
 // The gate products do not depend on the walk, so they run on other CUs and
@@ -691,9 +690,9 @@ __device__ __forceinline__ void store_block_n(float (*x)[kSN][DW], float (*v)[kV
   }
 }
 
-// Gate workgroups per walk: one evaluates a block's gates more slowly than
-// the walk consumes them, so each walk is fed by two taking alternate blocks.
-constexpr int kGateWGs = 2;
+// Gate workgroups per walk (each takes every kGateWGs-th block).  One keeps
+// up with its walk: with two or three the solve ran 1-2% slower.
+constexpr int kGateWGs = 1;
 
 struct NewtonShared {
   float x[2][3][kSN][DW];                               // wx (gates) or z, r, n (walks)

@@ -285,14 +285,14 @@ def test_one_launch_matches_launch_per_iteration(packed, K, monkeypatch):
 
 def test_one_launch_more_workgroups_than_fit_at_once(monkeypatch):
     """K x B x H = 3 x 64 x 8 = 1536 (iteration, sequence, head) triples,
-    three workgroups each (two gate workgroups and a walk): 4608 one-launch
-    workgroups, more than the GPU holds at once.  The ticket order
+    a gate workgroup and a walk each: 3072 one-launch workgroups, more than
+    the GPU holds at once.  The ticket order
     (iteration-major, gates before walks) lets every waiting workgroup find
     what it waits on running or done, so the solve completes without a wait
     giving up, equal to one launch per iteration."""
     from pararnn_amd import NewtonConfig, ParaGRU, newton_apply
 
-    print("case wide heads one launch, 4608 workgroups (B=64, H=8, K=3)", flush=True)
+    print("case wide heads one launch, 3072 workgroups (B=64, H=8, K=3)", flush=True)
     torch.manual_seed(21)
     cell = ParaGRU(16, 1024, mix="head", n_heads=8).to(DEV)
     x = torch.randn(64, 96, 16, device=DEV)
