@@ -50,6 +50,13 @@ def _flags() -> list[str]:
     ]
 
 
+# Per-file compiler options on top of _flags(): the wide-head adjoint walk runs
+# ~8% faster under the iterative ILP scheduler, the forward walks slower.
+_FILE_FLAGS = {
+    "gru_wide_rev.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+}
+
+
 def sources() -> list[str]:
     return sorted(
         os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip")
@@ -65,7 +72,7 @@ def build(verbose: bool = False) -> str:
 
     def compile_one(src: str) -> str:
         obj = os.path.join(obj_dir, os.path.basename(src) + ".o")
-        cmd = [hipcc, *_flags(), "-c", src, "-o", obj]
+        cmd = [hipcc, *_flags(), *_FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         res = subprocess.run(cmd, capture_output=True, text=True)
