@@ -54,11 +54,13 @@ def _flags() -> list[str]:
 # other files were unchanged or slower with them):
 #  * the wide-head adjoint walk runs ~8% faster under the iterative ILP
 #    scheduler (the forward walks slower);
-#  * the rectangular sLSTM kernels with the scheduler's AMDGPU register
-#    pressure trackers: the fused Newton launch 1.87 -> 1.80 ms at config 3.
+#  * the sLSTM kernels with the scheduler's AMDGPU register pressure
+#    trackers: the fused Newton launch 1.87 -> 1.80 ms at config 3, the
+#    packed-stream line ~1.5% faster.
 _FILE_FLAGS = {
     "gru_wide_rev.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
     "slstm_diag.hip": ["-mllvm", "-amdgpu-use-amdgpu-trackers=1"],
+    "slstm_packed.hip": ["-mllvm", "-amdgpu-use-amdgpu-trackers=1"],
 }
 
 
